@@ -1,0 +1,177 @@
+/*
+ * seeai_hip.h -- the C ABI of the SeeAI gfx950 executor (libseeai_hip.so).
+ *
+ * The reference executor has no C ABI: its seam is the C++ class
+ * ExecutorBackend (runtime/executor/backend.h:82-166) with the CPU backend
+ * (runtime/executor/cpu_backend.cc) and a Metal backend behind it.  This
+ * header is the thin C layer a HIP ExecutorBackend sits on: plain pointers
+ * and sizes, no C++ or torch types, one status code per call.
+ *
+ *   status  0 ok
+ *           1 refused: a non-finite gradient norm (kNonFiniteNormRefusal) or
+ *             a clip threshold that is not a finite positive float
+ *             (kClipThresholdRefusal); seeai_last_error() holds the
+ *             reference's exact words (runtime/executor/backend.h:65-80)
+ *           2 invalid argument (unknown opcode, shape the kernel refuses)
+ *           3 HIP runtime error
+ *
+ * Threading: a context is single-threaded; all its work is enqueued on one
+ * HIP stream in call order (the reference's one-engine-thread contract,
+ * backend.h:82-166 and update_engine.cc:325-364).
+ *
+ * Pointers named `d_*` are device pointers; the others are host pointers.
+ */
+#ifndef SEEAI_HIP_H_
+#define SEEAI_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SEEAI_OK 0
+#define SEEAI_REFUSED 1
+#define SEEAI_INVALID 2
+#define SEEAI_HIP_ERROR 3
+
+typedef struct seeai_ctx seeai_ctx;
+
+/* Per-range optimizer scalars: StepParams (runtime/executor/backend.h:56-63). */
+typedef struct seeai_step_params {
+  float lr;
+  float beta1;
+  float beta2;
+  float eps;
+  float weight_decay;
+  uint32_t reserved;
+  uint64_t step; /* 1-indexed AdamW timestep */
+} seeai_step_params;
+
+/* --- Context: the backend object (CreateBackend, backend.cc:26-60) ------- */
+int seeai_create(int device, seeai_ctx** out);
+void seeai_destroy(seeai_ctx* ctx);
+/* The message of the last non-zero status (never NULL). */
+const char* seeai_last_error(const seeai_ctx* ctx);
+/* Enqueue on `hip_stream` (a hipStream_t at default priority; NULL is the
+ * null stream) instead of the context's own stream, which seeai_get_stream
+ * returns right after seeai_create. */
+int seeai_set_stream(seeai_ctx* ctx, void* hip_stream);
+void* seeai_get_stream(seeai_ctx* ctx);
+/* Whether kFlagRelaxed (instruction.h:356-384) is taken as a permission
+ * (default 1): relaxed tiled attention runs the bf16 MFMA kernels. */
+int seeai_set_relaxed(seeai_ctx* ctx, int allow);
+/* ExecutorBackend::relaxed_executions (backend.h:149-162). */
+uint64_t seeai_relaxed_executions(const seeai_ctx* ctx);
+
+/* --- Binding: ExecutorBackend::Bind / BindSource (backend.h:99-109) ------ */
+/* Allocates the device arena (zeroed, arena_bytes rounded up to 16 KiB,
+ * kArenaAlignment backend.h:51) and uploads the rodata image.  A failed
+ * bind keeps the previous binding. */
+int seeai_bind(seeai_ctx* ctx, uint64_t arena_bytes, const void* rodata,
+               uint64_t rodata_bytes);
+int seeai_bind_source(seeai_ctx* ctx, const void* data, uint64_t bytes);
+/* Host <-> arena copies for the engine's host-sync points: the I/O slots
+ * and the loss slot (update_engine.cc:853-856), eval probabilities (:535),
+ * the persistent segment (:763) and merge deltas (:1051-1060).
+ * Stream-ordered; seeai_download returns with the bytes on the host. */
+int seeai_upload(seeai_ctx* ctx, uint64_t arena_offset, const void* src,
+                 uint64_t bytes);
+int seeai_download(seeai_ctx* ctx, uint64_t arena_offset, void* dst,
+                   uint64_t bytes);
+/* The device arena's base (for callers that place tensors themselves). */
+void* seeai_arena(seeai_ctx* ctx);
+uint64_t seeai_arena_bytes(const seeai_ctx* ctx);
+
+/* --- Execution: ExecutorBackend::Execute / Flush (backend.h:122-147) ----- */
+/* Enqueues one validated 64-byte UpdateInstruction (instruction.h:438-447)
+ * against the bound arena / rodata / source. */
+int seeai_execute(seeai_ctx* ctx, const void* instruction,
+                  const seeai_step_params* params);
+/* Runs `count` consecutive instructions (ExecuteRange's loop,
+ * update_engine.cc:345-351); stops at the first non-zero status and
+ * reports its index in *failed_at. */
+int seeai_execute_range(seeai_ctx* ctx, const void* instructions,
+                        uint64_t count, const seeai_step_params* params,
+                        uint64_t* failed_at);
+/* Waits for the stream; reports a refusal raised on the device since the
+ * last flush (non-finite clip norm: nothing it guarded was written). */
+int seeai_flush(seeai_ctx* ctx);
+
+/* --- Op-family entry points on caller-owned device memory --------------- */
+/* GemmNN / NT / TN / AccNN (runtime/executor/gemm.cc:582-624).
+ * layout 0 NN (A[M,K], B[K,N]), 1 NT (B[N,K]), 2 TN (A[K,M]);
+ * act 0 none 1 relu 2 gelu 3 silu; d_bias [N] or NULL; d_addend [M,N] or
+ * NULL; accumulate = 1 is GemmAccNN (C += alpha A@B). */
+int seeai_gemm_f32(seeai_ctx* ctx, int layout, const float* d_A,
+                   const float* d_B, float* d_C, uint64_t M, uint64_t N,
+                   uint64_t K, const float* d_bias, int act,
+                   const float* d_addend, float alpha, int accumulate);
+/* GemmNNQ8 / GemmNTQ8 (gemm.cc:626-674): nt 0 -> B int8 [K,N], 1 -> [N,K];
+ * d_col_scale (kFlagQ8ColScale): NN per output column [N], NT per
+ * reduction index [K]; NULL uses the per-tensor `scale`. */
+int seeai_gemm_q8(seeai_ctx* ctx, int nt, const float* d_A,
+                  const int8_t* d_B, float* d_C, uint64_t M, uint64_t N,
+                  uint64_t K, float scale, const float* d_col_scale, int act);
+/* GemmNNBF16 / GemmNTBF16 (gemm.cc:676-699). */
+int seeai_gemm_bf16w(seeai_ctx* ctx, int nt, const float* d_A,
+                     const uint16_t* d_B, float* d_C, uint64_t M, uint64_t N,
+                     uint64_t K, const float* d_bias, int act);
+
+/* W8A8 -- no reference counterpart (the reference's int8 GEMMs widen int8
+ * weights into f32 arithmetic); the quantizer rule is the reference's int8
+ * packer's (compiler/backend/allocation/arena_binder.cc:129-177). */
+/* Per-row symmetric int8 of X [rows, cols]: d_scale[rows], d_Q [rows, cols]. */
+int seeai_w8a8_quantize_rows(seeai_ctx* ctx, const float* d_X, int8_t* d_Q,
+                             float* d_scale, uint64_t rows, uint64_t cols);
+/* Per-output-column int8 of W [K, N], packed K-contiguous: d_Qt [N, K]. */
+int seeai_w8a8_pack_weights(seeai_ctx* ctx, const float* d_W, int8_t* d_Qt,
+                            float* d_scale, uint64_t K, uint64_t N);
+/* C[m,n] = (f32(sum_k QA[m,k] QWt[n,k]) * sa[m]) * sw[n]; the int32
+ * accumulators also land in d_acc [M,N] when it is not NULL. */
+int seeai_w8a8_gemm(seeai_ctx* ctx, const int8_t* d_QA, const float* d_sa,
+                    const int8_t* d_QWt, const float* d_sw, float* d_C,
+                    int32_t* d_acc, uint64_t M, uint64_t N, uint64_t K);
+
+/* Tiled attention (kAttnFwdTiled..kAttnDVTiled, attention.cc:448-590):
+ * q, k, v, o, dout [B*S, H*d]; stats [B*H*S, 4]; d_starts [B*S] or NULL.
+ * dtype 0 = f32 (exact family), 1 = bf16 MFMA (relaxed family). */
+int seeai_attn_fwd(seeai_ctx* ctx, int dtype, const float* d_q,
+                   const float* d_k, const float* d_v, float* d_o,
+                   float* d_stats, uint64_t B, uint64_t S, uint64_t H,
+                   uint64_t d, const int32_t* d_starts);
+int seeai_attn_dq(seeai_ctx* ctx, int dtype, const float* d_q,
+                  const float* d_k, const float* d_v, const float* d_dout,
+                  float* d_stats, float* d_dq, uint64_t B, uint64_t S,
+                  uint64_t H, uint64_t d);
+int seeai_attn_dk(seeai_ctx* ctx, int dtype, const float* d_q,
+                  const float* d_k, const float* d_v, const float* d_dout,
+                  const float* d_stats, float* d_dk, uint64_t B, uint64_t S,
+                  uint64_t H, uint64_t d);
+int seeai_attn_dv(seeai_ctx* ctx, int dtype, const float* d_q,
+                  const float* d_k, const float* d_dout, const float* d_stats,
+                  float* d_dv, uint64_t B, uint64_t S, uint64_t H,
+                  uint64_t d);
+
+/* SoftmaxXEntFwd / Bwd and the masked pair (loss.cc:35-126). */
+int seeai_xent_fwd(seeai_ctx* ctx, const float* d_logits,
+                   const int32_t* d_labels, float* d_loss, float* d_probs,
+                   uint64_t N, uint64_t C, int masked);
+int seeai_xent_bwd(seeai_ctx* ctx, const float* d_probs,
+                   const int32_t* d_labels, const float* d_seed,
+                   float* d_dlogits, uint64_t N, uint64_t C, int masked);
+/* AdamWStep with the fused clip (optimizer.cc:104-132); a refused step is
+ * reported by the next seeai_flush. */
+int seeai_adamw_step(seeai_ctx* ctx, float* d_p, const float* d_g,
+                     float* d_m, float* d_v, uint64_t n,
+                     const seeai_step_params* params, float clip_norm);
+/* The eval argmax, first maximum wins (update_engine.cc:537-565). */
+int seeai_argmax_rows(seeai_ctx* ctx, const float* d_probs, uint64_t rows,
+                      uint64_t cols, int32_t* d_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SEEAI_HIP_H_ */

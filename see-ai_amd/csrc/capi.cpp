@@ -1,0 +1,824 @@
+// capi.cpp -- the C ABI of the gfx950 executor: the context (device, stream,
+// device arena / rodata / source images, scratch, refusal word) and the
+// instruction dispatcher.
+//
+// seeai_execute decodes each 64-byte UpdateInstruction exactly as the
+// reference CPU backend decodes it (runtime/executor/cpu_backend.cc:260-646:
+// operand slots, packed dim words, flag bits, the imm word) and enqueues the
+// matching HIP kernels; nothing here computes on the host except the
+// per-step scalars the reference also hoists (AdamW's bias corrections,
+// RoPE's frequency step), evaluated with the reference's expressions.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/seeai_hip.h"
+#include "common.h"
+
+using namespace seeai;
+
+namespace {
+
+// runtime/executor/backend.h:65-80 -- the reference's shared verdicts.
+const char* const kNonFiniteNormRefusal =
+    "gradient norm is not finite \xe2\x80\x94 the step was refused with the parameters "
+    "and optimizer state untouched";
+const char* const kClipThresholdRefusal =
+    "clip threshold is not a finite positive float \xe2\x80\x94 the instruction was "
+    "refused with the gradient untouched";
+
+// source/plan/instruction.h:25-42 -- reference encoding.
+constexpr uint64_t kRodataBit = 1ULL << 63;
+constexpr uint64_t kSourceBit = 1ULL << 62;
+constexpr uint64_t kNullRef = ~0ULL;
+constexpr uint64_t kArenaAlignment = 16384;  // backend.h:51
+
+// instruction.h:311-382 -- flag bits.
+constexpr uint16_t kFlagEpilogueBias = 1u << 0;
+constexpr uint16_t kFlagGemmAddend = 1u << 3;
+constexpr uint16_t kFlagQ8ColScale = 1u << 4;
+constexpr uint16_t kFlagRelaxed = 1u << 5;
+
+#pragma pack(push, 1)
+struct Instruction {  // instruction.h:438-447
+  uint16_t opcode;
+  uint16_t flags;
+  uint32_t imm;
+  uint64_t in[4];
+  uint64_t out[3];
+};
+#pragma pack(pop)
+static_assert(sizeof(Instruction) == 64, "UpdateInstruction is one 64-byte word");
+
+float BitsToF32(uint64_t w) {
+  const uint32_t u = static_cast<uint32_t>(w);
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+constexpr size_t kSmallBytes = 4096;              // refusal word + scale slot
+constexpr size_t kInitialScratch = 1u << 20;      // grown on demand
+
+}  // namespace
+
+struct seeai_ctx {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  uint8_t* arena = nullptr;
+  uint64_t arena_bytes = 0;
+  uint8_t* rodata = nullptr;
+  uint64_t rodata_bytes = 0;
+  uint8_t* source = nullptr;
+  uint64_t source_bytes = 0;
+  uint8_t* small = nullptr;  // [0] refusal word, [64] scale slot
+  int* host_flag = nullptr;  // pinned
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  int allow_relaxed = 1;
+  uint64_t relaxed = 0;
+  std::string err;
+
+  int* flag() { return reinterpret_cast<int*>(small); }
+  float* scale_slot() { return reinterpret_cast<float*>(small + 64); }
+};
+
+namespace {
+
+int Fail(seeai_ctx* c, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (c) c->err = buf;
+  return code;
+}
+
+int Hip(seeai_ctx* c, hipError_t e, const char* what) {
+  if (e == hipSuccess) return SEEAI_OK;
+  return Fail(c, SEEAI_HIP_ERROR, "hip: %s: %s", what, hipGetErrorString(e));
+}
+
+#define SEEAI_TRY(ctx, expr, what)                         \
+  do {                                                     \
+    const int seeai_rc_ = Hip((ctx), (expr), (what));      \
+    if (seeai_rc_ != SEEAI_OK) return seeai_rc_;           \
+  } while (0)
+
+// Scratch for reductions; grown (after draining the stream) when an op
+// needs more than it holds.
+int Scratch(seeai_ctx* c, size_t bytes, void** out) {
+  if (bytes > c->scratch_bytes) {
+    SEEAI_TRY(c, hipStreamSynchronize(c->stream), "scratch drain");
+    if (c->scratch) SEEAI_TRY(c, hipFree(c->scratch), "scratch free");
+    c->scratch = nullptr;
+    c->scratch_bytes = 0;
+    size_t want = kInitialScratch;
+    while (want < bytes) want *= 2;
+    SEEAI_TRY(c, hipMalloc(&c->scratch, want), "scratch alloc");
+    c->scratch_bytes = want;
+  }
+  *out = c->scratch;
+  return SEEAI_OK;
+}
+
+struct Ptrs {
+  seeai_ctx* c;
+  uint8_t* at(uint64_t ref) const {
+    const uint64_t off = ref & ~(kRodataBit | kSourceBit);
+    if (ref & kRodataBit) return c->rodata + off;
+    if ((ref & (kRodataBit | kSourceBit)) == kSourceBit) return c->source + off;
+    return c->arena + off;
+  }
+  float* f(uint64_t ref) const { return reinterpret_cast<float*>(at(ref)); }
+  const float* fo(uint64_t ref) const { return ref == kNullRef ? nullptr : f(ref); }
+  int32_t* i32(uint64_t ref) const { return reinterpret_cast<int32_t*>(at(ref)); }
+};
+
+int AdamWLaunch(seeai_ctx* c, float* p, const float* g, float* m, float* v, uint64_t n,
+                const seeai_step_params& P, float clip) {
+  // optimizer.cc:115-118, evaluated on the host with the reference's powf.
+  const float inv_bc1 = 1.0f / (1.0f - std::pow(P.beta1, static_cast<float>(P.step)));
+  const float inv_bc2 = 1.0f / (1.0f - std::pow(P.beta2, static_cast<float>(P.step)));
+  const float* scale = nullptr;
+  if (clip > 0.0f) {
+    void* ws;
+    if (int rc = Scratch(c, 8 * 1024, &ws)) return rc;
+    SEEAI_TRY(c, LaunchClipFactor(g, n, clip, c->scale_slot(), c->flag(), ws, c->stream),
+              "adamw clip");
+    scale = c->scale_slot();
+  }
+  SEEAI_TRY(c,
+            LaunchAdamW(p, g, m, v, n, P.lr, P.beta1, P.beta2, P.eps, P.weight_decay, inv_bc1,
+                        inv_bc2, scale, c->flag(), c->stream),
+            "adamw");
+  return SEEAI_OK;
+}
+
+int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P) {
+  if (!c->arena) return Fail(c, SEEAI_INVALID, "execute: no arena is bound");
+  const Ptrs R{c};
+  hipStream_t s = c->stream;
+  const int act = (ins.flags >> 1) & 3;
+  const float alpha = ins.imm == 0 ? 1.0f : BitsToF32(ins.imm);
+  const float norm_eps = ins.imm == 0 ? 1e-5f : BitsToF32(ins.imm);
+  const uint64_t hi0 = ins.out[0] >> 32, lo0 = ins.out[0] & 0xFFFFFFFFu;
+  switch (ins.opcode) {
+    case 0:  // kNop
+      return SEEAI_OK;
+    case 1:    // kGemmNN
+    case 2:    // kGemmNT
+    case 3: {  // kGemmTN
+      GemmArgs a{};
+      a.layout = ins.opcode - 1;
+      a.b_kind = 0;
+      a.A = R.f(ins.in[0]);
+      a.B = R.f(ins.in[1]);
+      a.C = R.f(ins.in[2]);
+      a.M = ins.out[0];
+      a.N = ins.out[1];
+      a.K = ins.out[2];
+      // instruction.h:384-404: NN / TN fold alpha into A, NT onto the dot.
+      a.alpha_a = ins.opcode == 2 ? 1.0f : alpha;
+      a.alpha_dot = ins.opcode == 2 ? alpha : 1.0f;
+      a.addend = (ins.flags & kFlagGemmAddend) ? R.f(ins.in[3]) : nullptr;
+      a.bias = (ins.opcode == 1 && (ins.flags & kFlagEpilogueBias)) ? R.f(ins.in[3]) : nullptr;
+      a.act = ins.opcode == 1 ? act : 0;
+      SEEAI_TRY(c, LaunchGemm(a, s), "gemm");
+      return SEEAI_OK;
+    }
+    case 4: {  // kGemmAccNN: C += alpha A@B, alpha bits in in[3]
+      GemmArgs a{};
+      a.layout = 0;
+      a.A = R.f(ins.in[0]);
+      a.B = R.f(ins.in[1]);
+      a.C = R.f(ins.in[2]);
+      a.M = ins.out[0];
+      a.N = ins.out[1];
+      a.K = ins.out[2];
+      a.alpha_a = BitsToF32(ins.in[3]);
+      a.alpha_dot = 1.0f;
+      a.accumulate = 1;
+      SEEAI_TRY(c, LaunchGemm(a, s), "gemm.acc_nn");
+      return SEEAI_OK;
+    }
+    case 29:    // kGemmNNQ8
+    case 30: {  // kGemmNTQ8
+      const bool nt = ins.opcode == 30;
+      const bool cs = (ins.flags & kFlagQ8ColScale) != 0;
+      GemmArgs a{};
+      a.layout = nt ? 1 : 0;
+      a.b_kind = 1;
+      a.A = R.f(ins.in[0]);
+      a.B = R.at(ins.in[1]);
+      a.C = R.f(ins.in[2]);
+      a.M = ins.out[0];
+      a.N = ins.out[1];
+      a.K = ins.out[2];
+      const float scale = cs ? 1.0f : BitsToF32(ins.in[3]);
+      // gemm.cc:626-674: NN per-tensor scale folds into A, a column scale
+      // joins the widening; NT per-tensor scale multiplies the dot, a
+      // k-scale multiplies A's elements.
+      a.alpha_a = nt ? 1.0f : scale;
+      a.alpha_dot = nt ? scale : 1.0f;
+      if (cs) {
+        if (nt)
+          a.a_k_scale = R.f(ins.in[3]);
+        else
+          a.b_col_scale = R.f(ins.in[3]);
+      }
+      a.act = nt ? 0 : act;
+      SEEAI_TRY(c, LaunchGemm(a, s), "gemm.q8");
+      return SEEAI_OK;
+    }
+    case 43:    // kGemmNNBF16
+    case 44: {  // kGemmNTBF16
+      const bool nt = ins.opcode == 44;
+      GemmArgs a{};
+      a.layout = nt ? 1 : 0;
+      a.b_kind = 2;
+      a.A = R.f(ins.in[0]);
+      a.B = R.at(ins.in[1]);
+      a.C = R.f(ins.in[2]);
+      a.M = ins.out[0];
+      a.N = ins.out[1];
+      a.K = ins.out[2];
+      a.alpha_a = 1.0f;
+      a.alpha_dot = 1.0f;
+      a.bias = (!nt && (ins.flags & kFlagEpilogueBias)) ? R.f(ins.in[3]) : nullptr;
+      a.act = nt ? 0 : act;
+      SEEAI_TRY(c, LaunchGemm(a, s), "gemm.bf16");
+      return SEEAI_OK;
+    }
+    case 5:
+      SEEAI_TRY(c, LaunchAddEW(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s), "add");
+      return SEEAI_OK;
+    case 21:
+      SEEAI_TRY(c, LaunchMulEW(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s), "mul");
+      return SEEAI_OK;
+    case 6:
+      SEEAI_TRY(c,
+                LaunchAddBias(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0],
+                              ins.out[1], s),
+                "add.bias");
+      return SEEAI_OK;
+    case 7:   // ReluFwd
+    case 22:  // GeluFwd
+    case 24:  // SiluFwd
+      SEEAI_TRY(c,
+                LaunchUnary(ins.opcode == 7 ? 1 : ins.opcode == 22 ? 2 : 3, R.f(ins.in[0]),
+                            R.f(ins.in[1]), ins.out[0], 1.0f, s),
+                "act.fwd");
+      return SEEAI_OK;
+    case 8:   // ReluBwd
+    case 23:  // GeluBwd
+    case 25:  // SiluBwd
+      SEEAI_TRY(c,
+                LaunchBinaryBwd(ins.opcode == 8 ? 1 : ins.opcode == 23 ? 2 : 3, R.f(ins.in[0]),
+                                R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s),
+                "act.bwd");
+      return SEEAI_OK;
+    case 9:  // kScale
+      SEEAI_TRY(c,
+                LaunchUnary(4, R.f(ins.in[0]), R.f(ins.in[1]), ins.out[0], BitsToF32(ins.in[2]), s),
+                "scale");
+      return SEEAI_OK;
+    case 10:
+      SEEAI_TRY(c, LaunchReduceRows(R.f(ins.in[0]), R.f(ins.in[1]), ins.out[0], ins.out[1], s),
+                "reduce_rows");
+      return SEEAI_OK;
+    case 11:
+    case 51: {  // SoftmaxXEntFwd (+masked)
+      void* ws;
+      if (int rc = Scratch(c, 8 * ins.out[0] + 64, &ws)) return rc;
+      SEEAI_TRY(c,
+                LaunchXEntFwd(R.f(ins.in[0]), R.i32(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                              ins.out[0], ins.out[1], ins.opcode == 51, ws, s),
+                "softmax_xent.fwd");
+      return SEEAI_OK;
+    }
+    case 12:
+    case 52: {  // SoftmaxXEntBwd (+masked)
+      void* ws;
+      if (int rc = Scratch(c, 64, &ws)) return rc;
+      SEEAI_TRY(c,
+                LaunchXEntBwd(R.f(ins.in[0]), R.i32(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                              ins.out[0], ins.out[1], ins.opcode == 52, ws, s),
+                "softmax_xent.bwd");
+      return SEEAI_OK;
+    }
+    case 17: {  // kSgdStep
+      const float clip = BitsToF32(ins.out[1]);
+      const float* scale = nullptr;
+      if (clip > 0.0f) {
+        void* ws;
+        if (int rc = Scratch(c, 8 * 1024, &ws)) return rc;
+        SEEAI_TRY(c,
+                  LaunchClipFactor(R.f(ins.in[1]), ins.out[0], clip, c->scale_slot(), c->flag(),
+                                   ws, s),
+                  "sgd clip");
+        scale = c->scale_slot();
+      }
+      SEEAI_TRY(c,
+                LaunchSgd(R.f(ins.in[0]), R.f(ins.in[1]), ins.out[0], P.lr, P.weight_decay, scale,
+                          c->flag(), s),
+                "sgd");
+      return SEEAI_OK;
+    }
+    case 18:  // kAdamWStep (+ fused clip in out[1])
+      return AdamWLaunch(c, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                         ins.out[0], P, BitsToF32(ins.out[1]));
+    case 28: {  // kClipNorm
+      const float cap = BitsToF32(ins.in[1]);
+      if (!std::isfinite(cap) || !(cap > 0.0f)) return Fail(c, SEEAI_REFUSED, "%s", kClipThresholdRefusal);
+      void* ws;
+      if (int rc = Scratch(c, 8 * 1024, &ws)) return rc;
+      SEEAI_TRY(c, LaunchClipFactor(R.f(ins.in[0]), ins.out[0], cap, c->scale_slot(), c->flag(), ws, s),
+                "clip");
+      SEEAI_TRY(c, LaunchScaleByFactor(R.f(ins.in[0]), ins.out[0], c->scale_slot(), c->flag(), s),
+                "clip scale");
+      return SEEAI_OK;
+    }
+    case 53: {  // kSqNormAccum
+      void* ws;
+      if (int rc = Scratch(c, 8 * 1024, &ws)) return rc;
+      SEEAI_TRY(c, LaunchSqNormAccum(R.f(ins.in[0]), ins.out[0], R.f(ins.in[1]), ws, s), "sqnorm");
+      return SEEAI_OK;
+    }
+    case 54: {  // kClipGlobal
+      const float cap = BitsToF32(ins.in[2]);
+      if (!std::isfinite(cap) || !(cap > 0.0f)) return Fail(c, SEEAI_REFUSED, "%s", kClipThresholdRefusal);
+      SEEAI_TRY(c, LaunchGlobalClipFactor(R.f(ins.in[1]), cap, c->scale_slot(), c->flag(), s),
+                "clip.global");
+      SEEAI_TRY(c, LaunchScaleByFactor(R.f(ins.in[0]), ins.out[0], c->scale_slot(), c->flag(), s),
+                "clip.global scale");
+      return SEEAI_OK;
+    }
+    case 19:
+      SEEAI_TRY(c, LaunchFill(R.f(ins.in[0]), BitsToF32(ins.in[1]), ins.out[0], s), "fill");
+      return SEEAI_OK;
+    case 20:
+      SEEAI_TRY(c, LaunchCopy(R.f(ins.in[0]), R.f(ins.in[1]), ins.out[0], s), "copy");
+      return SEEAI_OK;
+    case 42:
+      SEEAI_TRY(c, LaunchAccumulate(R.f(ins.in[0]), R.f(ins.in[1]), ins.out[0], s), "accumulate");
+      return SEEAI_OK;
+    case 26:
+      SEEAI_TRY(c,
+                LaunchLayerNormFwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                                   R.f(ins.out[1]), R.f(ins.out[2]), hi0, lo0, norm_eps, s),
+                "layernorm.fwd");
+      return SEEAI_OK;
+    case 27:
+      SEEAI_TRY(c,
+                LaunchLayerNormBwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.out[0]),
+                                   R.f(ins.out[1]), R.f(ins.in[3]), ins.out[2] >> 32,
+                                   ins.out[2] & 0xFFFFFFFFu, s),
+                "layernorm.bwd");
+      return SEEAI_OK;
+    case 31:
+      SEEAI_TRY(c,
+                LaunchRmsNormFwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                                 hi0, lo0, norm_eps, s),
+                "rmsnorm.fwd");
+      return SEEAI_OK;
+    case 32:
+      SEEAI_TRY(c,
+                LaunchRmsNormBwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.out[0]),
+                                 R.f(ins.in[3]), ins.out[1] >> 32, ins.out[1] & 0xFFFFFFFFu, s),
+                "rmsnorm.bwd");
+      return SEEAI_OK;
+    case 33:
+    case 34: {  // RopeFwd / RopeBwd (v12 table in in[2])
+      const uint64_t d = ins.out[1] & 0xFFFFFFFFu;
+      const float base = BitsToF32(ins.out[2]);
+      const float step = std::pow(base, -2.0f / static_cast<float>(d));  // attention.cc:123
+      SEEAI_TRY(c,
+                LaunchRope(R.f(ins.in[0]), R.f(ins.in[1]), hi0, lo0, ins.out[1] >> 32, d, step,
+                           R.fo(ins.in[2]), ins.opcode == 34, s),
+                "rope");
+      return SEEAI_OK;
+    }
+    case 45: {  // RopeTable
+      const float step = std::pow(BitsToF32(ins.out[1]), -2.0f / static_cast<float>(lo0));
+      SEEAI_TRY(c, LaunchRopeTable(R.f(ins.in[0]), hi0, lo0, step, s), "rope.table");
+      return SEEAI_OK;
+    }
+    case 46: {  // FusedMap
+      SEEAI_TRY(c,
+                LaunchFusedMap(R.f(ins.in[0]), R.fo(ins.in[1]), R.fo(ins.in[2]), R.f(ins.in[3]),
+                               ins.out[0], ins.out[1], BitsToF32(ins.out[2]),
+                               BitsToF32(ins.out[2] >> 32), s),
+                "fused_map");
+      return SEEAI_OK;
+    }
+    case 41:
+      SEEAI_TRY(c,
+                LaunchEmbed(R.i32(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0],
+                            ins.out[1] & 0xFFFFFFFFu, s),
+                "embed");
+      return SEEAI_OK;
+    case 55:
+      SEEAI_TRY(c,
+                LaunchSegmentStarts(R.i32(ins.in[0]), R.i32(ins.in[1]), hi0, lo0,
+                                    static_cast<int32_t>(ins.out[1]), s),
+                "segment_starts");
+      return SEEAI_OK;
+    case 35:
+    case 56: {  // AttnFwd (+Seg): cached family
+      uint64_t B, S, H, d;
+      const int32_t* starts = nullptr;
+      if (ins.opcode == 35) {
+        B = ins.out[1] >> 32, S = ins.out[1] & 0xFFFFFFFFu, H = ins.out[2] >> 32,
+        d = ins.out[2] & 0xFFFFFFFFu;
+      } else {
+        const uint64_t g = ins.out[1];
+        B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
+        starts = R.i32(ins.out[2]);
+      }
+      SEEAI_TRY(c,
+                LaunchAttnFwdCached(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                                    R.f(ins.out[0]), B, S, H, d, starts, s),
+                "attn.fwd");
+      return SEEAI_OK;
+    }
+    case 36:
+      SEEAI_TRY(c,
+                LaunchAttnDP(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), hi0, lo0,
+                             ins.out[1] >> 32, ins.out[1] & 0xFFFFFFFFu, s),
+                "attn.dp");
+      return SEEAI_OK;
+    case 37:
+      SEEAI_TRY(c,
+                LaunchAttnDV(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), hi0, lo0,
+                             ins.out[1] >> 32, ins.out[1] & 0xFFFFFFFFu, s),
+                "attn.dv");
+      return SEEAI_OK;
+    case 38:
+      SEEAI_TRY(c,
+                LaunchSoftmaxRowsBwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), hi0, lo0, s),
+                "softmax_rows.bwd");
+      return SEEAI_OK;
+    case 39:
+      SEEAI_TRY(c,
+                LaunchAttnDQ(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), hi0, lo0,
+                             ins.out[1] >> 32, ins.out[1] & 0xFFFFFFFFu, s),
+                "attn.dq");
+      return SEEAI_OK;
+    case 40:
+      SEEAI_TRY(c,
+                LaunchAttnDK(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), hi0, lo0,
+                             ins.out[1] >> 32, ins.out[1] & 0xFFFFFFFFu, s),
+                "attn.dk");
+      return SEEAI_OK;
+    case 47:
+    case 57: {  // AttnFwdTiled (+Seg)
+      uint64_t B, S, H, d;
+      const int32_t* starts = nullptr;
+      if (ins.opcode == 47) {
+        B = ins.out[1] >> 32, S = ins.out[1] & 0xFFFFFFFFu, H = ins.out[2] >> 32,
+        d = ins.out[2] & 0xFFFFFFFFu;
+      } else {
+        const uint64_t g = ins.out[1];
+        B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
+        starts = R.i32(ins.out[2]);
+      }
+      const int dt = (ins.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
+      c->relaxed += dt;
+      SEEAI_TRY(c,
+                LaunchAttnFwdTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]),
+                                   R.f(ins.in[3]), R.f(ins.out[0]), B, S, H, d, starts, s),
+                "attn.fwd_tiled");
+      return SEEAI_OK;
+    }
+    case 48:
+    case 49:
+    case 50: {  // AttnDQTiled / DKTiled / DVTiled
+      const uint64_t g = ins.out[2];
+      const uint64_t B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
+      const int dt = (ins.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
+      c->relaxed += dt;
+      hipError_t e;
+      if (ins.opcode == 48)
+        e = LaunchAttnDQTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                              R.f(ins.out[0]), R.f(ins.out[1]), B, S, H, d, s);
+      else if (ins.opcode == 49)
+        e = LaunchAttnDKTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                              R.f(ins.out[0]), R.f(ins.out[1]), B, S, H, d, s);
+      else
+        e = LaunchAttnDVTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[3]), R.f(ins.out[0]),
+                              R.f(ins.out[1]), B, S, H, d, s);
+      SEEAI_TRY(c, e, "attn.bwd_tiled");
+      return SEEAI_OK;
+    }
+    default:
+      // kMseFwd/Bwd (13/14) and kKLDistillFwd/Bwd (15/16) are outside this
+      // executor's hot path.
+      return Fail(c, SEEAI_INVALID, "execute: opcode %u is not supported by the gfx950 executor",
+                  static_cast<unsigned>(ins.opcode));
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int seeai_create(int device, seeai_ctx** out) {
+  if (!out) return SEEAI_INVALID;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) return SEEAI_HIP_ERROR;
+  auto* c = new seeai_ctx();
+  c->device = device;
+  int rc = Hip(c, hipSetDevice(device), "set device");
+  if (rc == SEEAI_OK) rc = Hip(c, hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "stream");
+  if (rc == SEEAI_OK) rc = Hip(c, hipMalloc(&c->small, kSmallBytes), "small alloc");
+  if (rc == SEEAI_OK) rc = Hip(c, hipMemset(c->small, 0, kSmallBytes), "small clear");
+  if (rc == SEEAI_OK) rc = Hip(c, hipHostMalloc(reinterpret_cast<void**>(&c->host_flag), 64), "pinned");
+  if (rc != SEEAI_OK) {
+    seeai_destroy(c);
+    return rc;
+  }
+  c->stream = c->own_stream;
+  *out = c;
+  return SEEAI_OK;
+}
+
+void seeai_destroy(seeai_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  if (c->arena) (void)hipFree(c->arena);
+  if (c->rodata) (void)hipFree(c->rodata);
+  if (c->source) (void)hipFree(c->source);
+  if (c->scratch) (void)hipFree(c->scratch);
+  if (c->small) (void)hipFree(c->small);
+  if (c->host_flag) (void)hipHostFree(c->host_flag);
+  if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+  delete c;
+}
+
+const char* seeai_last_error(const seeai_ctx* c) { return c ? c->err.c_str() : "no context"; }
+
+int seeai_set_stream(seeai_ctx* c, void* stream) {
+  if (!c) return SEEAI_INVALID;
+  c->stream = static_cast<hipStream_t>(stream);
+  return SEEAI_OK;
+}
+void* seeai_get_stream(seeai_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
+int seeai_set_relaxed(seeai_ctx* c, int allow) {
+  if (!c) return SEEAI_INVALID;
+  c->allow_relaxed = allow ? 1 : 0;
+  return SEEAI_OK;
+}
+uint64_t seeai_relaxed_executions(const seeai_ctx* c) { return c ? c->relaxed : 0; }
+
+int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t rodata_bytes) {
+  if (!c) return SEEAI_INVALID;
+  const uint64_t bytes = (arena_bytes + kArenaAlignment - 1) / kArenaAlignment * kArenaAlignment;
+  uint8_t* arena = nullptr;
+  uint8_t* ro = nullptr;
+  // Build the new binding completely before replacing the old one, so a
+  // refused bind leaves the previous binding executable (backend.h:89-98).
+  hipError_t e = hipMalloc(&arena, bytes ? bytes : kArenaAlignment);
+  if (e == hipSuccess) e = hipMemsetAsync(arena, 0, bytes ? bytes : kArenaAlignment, c->stream);
+  if (e == hipSuccess && rodata_bytes) e = hipMalloc(&ro, rodata_bytes);
+  if (e == hipSuccess && rodata_bytes)
+    e = hipMemcpyAsync(ro, rodata, rodata_bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    if (arena) (void)hipFree(arena);
+    if (ro) (void)hipFree(ro);
+    return Hip(c, e, "bind");
+  }
+  if (c->arena) (void)hipFree(c->arena);
+  if (c->rodata) (void)hipFree(c->rodata);
+  c->arena = arena;
+  c->arena_bytes = bytes;
+  c->rodata = ro;
+  c->rodata_bytes = rodata_bytes;
+  return SEEAI_OK;
+}
+
+int seeai_bind_source(seeai_ctx* c, const void* data, uint64_t bytes) {
+  if (!c) return SEEAI_INVALID;
+  SEEAI_TRY(c, hipStreamSynchronize(c->stream), "bind_source drain");
+  if (c->source) (void)hipFree(c->source);
+  c->source = nullptr;
+  c->source_bytes = 0;
+  if (!data || !bytes) return SEEAI_OK;
+  SEEAI_TRY(c, hipMalloc(&c->source, bytes), "bind_source alloc");
+  SEEAI_TRY(c, hipMemcpy(c->source, data, bytes, hipMemcpyHostToDevice), "bind_source copy");
+  c->source_bytes = bytes;
+  return SEEAI_OK;
+}
+
+int seeai_upload(seeai_ctx* c, uint64_t off, const void* src, uint64_t bytes) {
+  if (!c || !c->arena || off + bytes > c->arena_bytes) return Fail(c, SEEAI_INVALID, "upload: extent outside the arena");
+  if (!bytes) return SEEAI_OK;
+  SEEAI_TRY(c, hipMemcpyAsync(c->arena + off, src, bytes, hipMemcpyHostToDevice, c->stream), "upload");
+  // The source buffer is the caller's pageable memory: complete the copy
+  // before returning so the caller may reuse it at once.
+  SEEAI_TRY(c, hipStreamSynchronize(c->stream), "upload sync");
+  return SEEAI_OK;
+}
+
+int seeai_download(seeai_ctx* c, uint64_t off, void* dst, uint64_t bytes) {
+  if (!c || !c->arena || off + bytes > c->arena_bytes) return Fail(c, SEEAI_INVALID, "download: extent outside the arena");
+  if (!bytes) return SEEAI_OK;
+  SEEAI_TRY(c, hipMemcpyAsync(dst, c->arena + off, bytes, hipMemcpyDeviceToHost, c->stream), "download");
+  SEEAI_TRY(c, hipStreamSynchronize(c->stream), "download sync");
+  return SEEAI_OK;
+}
+
+void* seeai_arena(seeai_ctx* c) { return c ? c->arena : nullptr; }
+uint64_t seeai_arena_bytes(const seeai_ctx* c) { return c ? c->arena_bytes : 0; }
+
+int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params* params) {
+  if (!c || !instruction) return SEEAI_INVALID;
+  Instruction ins;
+  std::memcpy(&ins, instruction, sizeof ins);
+  seeai_step_params P{};
+  if (params) P = *params;
+  return ExecuteOne(c, ins, P);
+}
+
+int seeai_execute_range(seeai_ctx* c, const void* instructions, uint64_t count,
+                        const seeai_step_params* params, uint64_t* failed_at) {
+  if (!c || (!instructions && count)) return SEEAI_INVALID;
+  const auto* base = static_cast<const uint8_t*>(instructions);
+  for (uint64_t i = 0; i < count; ++i) {
+    if (int rc = seeai_execute(c, base + i * 64, params)) {
+      if (failed_at) *failed_at = i;
+      return rc;
+    }
+  }
+  return SEEAI_OK;
+}
+
+int seeai_flush(seeai_ctx* c) {
+  if (!c) return SEEAI_INVALID;
+  SEEAI_TRY(c, hipMemcpyAsync(c->host_flag, c->flag(), sizeof(int), hipMemcpyDeviceToHost, c->stream),
+            "flush flag");
+  SEEAI_TRY(c, hipStreamSynchronize(c->stream), "flush");
+  if (*c->host_flag) {
+    SEEAI_TRY(c, hipMemsetAsync(c->flag(), 0, sizeof(int), c->stream), "flush reset");
+    SEEAI_TRY(c, hipStreamSynchronize(c->stream), "flush reset sync");
+    return Fail(c, SEEAI_REFUSED, "%s", kNonFiniteNormRefusal);
+  }
+  return SEEAI_OK;
+}
+
+int seeai_gemm_f32(seeai_ctx* c, int layout, const float* A, const float* B, float* C, uint64_t M,
+                   uint64_t N, uint64_t K, const float* bias, int act, const float* addend,
+                   float alpha, int accumulate) {
+  if (!c || layout < 0 || layout > 2 || act < 0 || act > 3) return Fail(c, SEEAI_INVALID, "gemm_f32: bad layout/act");
+  GemmArgs a{};
+  a.layout = layout;
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.alpha_a = layout == 1 ? 1.0f : alpha;
+  a.alpha_dot = layout == 1 ? alpha : 1.0f;
+  a.addend = addend;
+  a.bias = bias;
+  a.act = act;
+  a.accumulate = accumulate;
+  SEEAI_TRY(c, LaunchGemm(a, c->stream), "gemm_f32");
+  return SEEAI_OK;
+}
+
+int seeai_gemm_q8(seeai_ctx* c, int nt, const float* A, const int8_t* B, float* C, uint64_t M,
+                  uint64_t N, uint64_t K, float scale, const float* col_scale, int act) {
+  if (!c || act < 0 || act > 3 || (nt && act)) return Fail(c, SEEAI_INVALID, "gemm_q8: bad act");
+  GemmArgs a{};
+  a.layout = nt ? 1 : 0;
+  a.b_kind = 1;
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  const float sc = col_scale ? 1.0f : scale;
+  a.alpha_a = nt ? 1.0f : sc;
+  a.alpha_dot = nt ? sc : 1.0f;
+  if (col_scale) {
+    if (nt)
+      a.a_k_scale = col_scale;
+    else
+      a.b_col_scale = col_scale;
+  }
+  a.act = act;
+  SEEAI_TRY(c, LaunchGemm(a, c->stream), "gemm_q8");
+  return SEEAI_OK;
+}
+
+int seeai_gemm_bf16w(seeai_ctx* c, int nt, const float* A, const uint16_t* B, float* C, uint64_t M,
+                     uint64_t N, uint64_t K, const float* bias, int act) {
+  if (!c || act < 0 || act > 3 || (nt && (act || bias))) return Fail(c, SEEAI_INVALID, "gemm_bf16w: NT takes no epilogue");
+  GemmArgs a{};
+  a.layout = nt ? 1 : 0;
+  a.b_kind = 2;
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.alpha_a = 1.0f;
+  a.alpha_dot = 1.0f;
+  a.bias = bias;
+  a.act = act;
+  SEEAI_TRY(c, LaunchGemm(a, c->stream), "gemm_bf16w");
+  return SEEAI_OK;
+}
+
+int seeai_w8a8_quantize_rows(seeai_ctx* c, const float* X, int8_t* Q, float* scale, uint64_t rows,
+                             uint64_t cols) {
+  if (!c) return SEEAI_INVALID;
+  SEEAI_TRY(c, LaunchQuantizeRows(X, Q, scale, rows, cols, c->stream), "quantize_rows");
+  return SEEAI_OK;
+}
+
+int seeai_w8a8_pack_weights(seeai_ctx* c, const float* W, int8_t* Qt, float* scale, uint64_t K,
+                            uint64_t N) {
+  if (!c) return SEEAI_INVALID;
+  SEEAI_TRY(c, LaunchPackWeightsI8(W, Qt, scale, K, N, c->stream), "pack_weights");
+  return SEEAI_OK;
+}
+
+int seeai_w8a8_gemm(seeai_ctx* c, const int8_t* QA, const float* sa, const int8_t* QWt,
+                    const float* sw, float* C, int32_t* acc, uint64_t M, uint64_t N, uint64_t K) {
+  if (!c) return SEEAI_INVALID;
+  if (K > 133144) return Fail(c, SEEAI_INVALID, "w8a8_gemm: K = %llu could overflow the int32 accumulator",
+                             static_cast<unsigned long long>(K));
+  SEEAI_TRY(c, LaunchGemmW8A8(QA, sa, QWt, sw, C, acc, M, N, K, c->stream), "w8a8_gemm");
+  return SEEAI_OK;
+}
+
+int seeai_attn_fwd(seeai_ctx* c, int dtype, const float* q, const float* k, const float* v, float* o,
+                   float* stats, uint64_t B, uint64_t S, uint64_t H, uint64_t d,
+                   const int32_t* starts) {
+  if (!c || dtype < 0 || dtype > 1) return Fail(c, SEEAI_INVALID, "attn_fwd: dtype is 0 or 1");
+  SEEAI_TRY(c, LaunchAttnFwdTiled(dtype, q, k, v, o, stats, B, S, H, d, starts, c->stream), "attn_fwd");
+  return SEEAI_OK;
+}
+int seeai_attn_dq(seeai_ctx* c, int dtype, const float* q, const float* k, const float* v,
+                  const float* dout, float* stats, float* dq, uint64_t B, uint64_t S, uint64_t H,
+                  uint64_t d) {
+  if (!c || dtype < 0 || dtype > 1) return Fail(c, SEEAI_INVALID, "attn_dq: dtype is 0 or 1");
+  SEEAI_TRY(c, LaunchAttnDQTiled(dtype, q, k, v, dout, stats, dq, B, S, H, d, c->stream), "attn_dq");
+  return SEEAI_OK;
+}
+int seeai_attn_dk(seeai_ctx* c, int dtype, const float* q, const float* k, const float* v,
+                  const float* dout, const float* stats, float* dk, uint64_t B, uint64_t S,
+                  uint64_t H, uint64_t d) {
+  if (!c || dtype < 0 || dtype > 1) return Fail(c, SEEAI_INVALID, "attn_dk: dtype is 0 or 1");
+  SEEAI_TRY(c, LaunchAttnDKTiled(dtype, q, k, v, dout, stats, dk, B, S, H, d, c->stream), "attn_dk");
+  return SEEAI_OK;
+}
+int seeai_attn_dv(seeai_ctx* c, int dtype, const float* q, const float* k, const float* dout,
+                  const float* stats, float* dv, uint64_t B, uint64_t S, uint64_t H, uint64_t d) {
+  if (!c || dtype < 0 || dtype > 1) return Fail(c, SEEAI_INVALID, "attn_dv: dtype is 0 or 1");
+  SEEAI_TRY(c, LaunchAttnDVTiled(dtype, q, k, dout, stats, dv, B, S, H, d, c->stream), "attn_dv");
+  return SEEAI_OK;
+}
+
+int seeai_xent_fwd(seeai_ctx* c, const float* logits, const int32_t* labels, float* loss,
+                   float* probs, uint64_t N, uint64_t C, int masked) {
+  if (!c) return SEEAI_INVALID;
+  void* ws;
+  if (int rc = Scratch(c, 8 * N + 64, &ws)) return rc;
+  SEEAI_TRY(c, LaunchXEntFwd(logits, labels, loss, probs, N, C, masked, ws, c->stream), "xent_fwd");
+  return SEEAI_OK;
+}
+int seeai_xent_bwd(seeai_ctx* c, const float* probs, const int32_t* labels, const float* seed,
+                   float* dlogits, uint64_t N, uint64_t C, int masked) {
+  if (!c) return SEEAI_INVALID;
+  void* ws;
+  if (int rc = Scratch(c, 64, &ws)) return rc;
+  SEEAI_TRY(c, LaunchXEntBwd(probs, labels, seed, dlogits, N, C, masked, ws, c->stream), "xent_bwd");
+  return SEEAI_OK;
+}
+int seeai_adamw_step(seeai_ctx* c, float* p, const float* g, float* m, float* v, uint64_t n,
+                     const seeai_step_params* params, float clip_norm) {
+  if (!c || !params) return SEEAI_INVALID;
+  return AdamWLaunch(c, p, g, m, v, n, *params, clip_norm);
+}
+int seeai_argmax_rows(seeai_ctx* c, const float* probs, uint64_t rows, uint64_t cols, int32_t* out) {
+  if (!c) return SEEAI_INVALID;
+  SEEAI_TRY(c, LaunchArgmaxRows(probs, rows, cols, out, c->stream), "argmax");
+  return SEEAI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,249 @@
+// common.h -- shared device helpers and the internal launcher interface of
+// the SeeAI gfx950 executor.  Every kernel family (.hip file) exposes its
+// launchers through the declarations at the bottom; capi.cpp (the C-ABI and
+// the instruction dispatcher) is the only caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace seeai {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+// The fused-epilogue activations (instruction.h:384-396, the expressions of
+// kernel_policy.h:122-136).  Built with -ffp-contract=off, so every product
+// and sum rounds where the reference's x86-64 build rounds it.
+__device__ __forceinline__ float SigmoidExpr(float x) {
+  return 1.0f / (1.0f + expf(-x));
+}
+__device__ __forceinline__ float ReluExpr(float x) { return x > 0.0f ? x : 0.0f; }
+__device__ __forceinline__ float GeluExpr(float x) {
+  const float kC = 0.7978845608028654f, kA = 0.044715f;
+  const float t = tanhf(kC * (x + kA * x * x * x));
+  return 0.5f * x * (1.0f + t);
+}
+__device__ __forceinline__ float SiluExpr(float x) { return x * SigmoidExpr(x); }
+__device__ __forceinline__ float ActExpr(int act, float v) {
+  switch (act) {
+    case 1: return ReluExpr(v);
+    case 2: return GeluExpr(v);
+    case 3: return SiluExpr(v);
+    default: return v;
+  }
+}
+
+// Wave-wide butterfly sums: a fixed pairing of lanes, so the result is a
+// pure function of the 64 inputs (bitwise reproducible run to run).
+__device__ __forceinline__ double WaveSumD(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float WaveSumF(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float WaveMaxF(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Block-wide sum of one double per thread through LDS, combined in wave
+// order: fixed association for a fixed block size.
+template <int kThreads>
+__device__ __forceinline__ double BlockSumD(double v, double* lds) {
+  v = WaveSumD(v);
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  if (l == 0) lds[w] = v;
+  __syncthreads();
+  double s = 0.0;
+  if (threadIdx.x == 0) {
+    for (int i = 0; i < kThreads / kWave; ++i) s += lds[i];
+    lds[0] = s;
+  }
+  __syncthreads();
+  s = lds[0];
+  __syncthreads();
+  return s;
+}
+template <int kThreads>
+__device__ __forceinline__ float BlockMaxF(float v, float* lds) {
+  v = WaveMaxF(v);
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  if (l == 0) lds[w] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = lds[0];
+    for (int i = 1; i < kThreads / kWave; ++i) s = fmaxf(s, lds[i]);
+    lds[0] = s;
+  }
+  __syncthreads();
+  const float r = lds[0];
+  __syncthreads();
+  return r;
+}
+template <int kThreads>
+__device__ __forceinline__ float BlockSumF(float v, float* lds) {
+  v = WaveSumF(v);
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  if (l == 0) lds[w] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int i = 0; i < kThreads / kWave; ++i) s += lds[i];
+    lds[0] = s;
+  }
+  __syncthreads();
+  const float r = lds[0];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ float Bf16ToF32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+// Round-to-nearest-even narrowing (source/plan/bf16.h:18-24).
+__device__ __forceinline__ uint16_t F32ToBf16(float f) {
+  const uint32_t bits = __float_as_uint(f);
+  if ((bits & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((bits >> 16) | 0x0040u);
+  const uint32_t bias = 0x7FFFu + ((bits >> 16) & 1u);
+  return static_cast<uint16_t>((bits + bias) >> 16);
+}
+
+inline unsigned GridFor(size_t n, unsigned threads, unsigned cap = 65536u) {
+  size_t g = (n + threads - 1) / threads;
+  if (g == 0) g = 1;
+  return static_cast<unsigned>(g < cap ? g : cap);
+}
+
+// ---------------------------------------------------------------------------
+// Launchers (host side).  All take the stream last; all return hipError_t.
+// Pointers are device pointers.  The workspace (`ws`) pointers are scratch
+// device memory the caller owns; each launcher documents the bytes it needs.
+// ---------------------------------------------------------------------------
+
+// Elementwise family (k_elementwise.hip).
+hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hipStream_t s);
+hipError_t LaunchMulEW(const float* x, const float* y, float* out, size_t n, hipStream_t s);
+hipError_t LaunchAddBias(const float* x, const float* b, float* out, size_t rows, size_t cols,
+                         hipStream_t s);
+hipError_t LaunchUnary(int kind, const float* x, float* out, size_t n, float alpha, hipStream_t s);
+hipError_t LaunchBinaryBwd(int kind, const float* dy, const float* x, float* dx, size_t n,
+                           hipStream_t s);
+hipError_t LaunchReduceRows(const float* dy, float* db, size_t rows, size_t cols, hipStream_t s);
+hipError_t LaunchFill(float* dst, float value, size_t n, hipStream_t s);
+hipError_t LaunchCopy(const float* src, float* dst, size_t n, hipStream_t s);
+hipError_t LaunchAccumulate(float* dst, const float* src, size_t n, hipStream_t s);
+hipError_t LaunchEmbed(const int32_t* tokens, const float* table, float* out, size_t rows,
+                       size_t dim, hipStream_t s);
+hipError_t LaunchFusedMap(const float* x, const float* o1, const float* o2, float* out, size_t n,
+                          uint64_t stages, float imm0, float imm1, hipStream_t s);
+hipError_t LaunchLayerNormFwd(const float* x, const float* g, const float* b, float* y,
+                              float* mean, float* rstd, size_t rows, size_t cols, float eps,
+                              hipStream_t s);
+hipError_t LaunchLayerNormBwd(const float* dy, const float* x, const float* g,
+                              const float* mean, const float* rstd, float* dx, size_t rows,
+                              size_t cols, hipStream_t s);
+hipError_t LaunchRmsNormFwd(const float* x, const float* g, float* y, float* rstd, size_t rows,
+                            size_t cols, float eps, hipStream_t s);
+hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, const float* rstd,
+                            float* dx, size_t rows, size_t cols, hipStream_t s);
+hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
+                      float step, const float* table, int backward, hipStream_t s);
+hipError_t LaunchRopeTable(float* table, size_t S, size_t d, float step, hipStream_t s);
+hipError_t LaunchSegmentStarts(const int32_t* tokens, int32_t* starts, size_t B, size_t S,
+                               int32_t eos, hipStream_t s);
+hipError_t LaunchArgmaxRows(const float* probs, size_t rows, size_t cols, int32_t* out,
+                            hipStream_t s);
+
+// Loss family (k_loss.hip).  ws: 8 * rows bytes.
+hipError_t LaunchXEntFwd(const float* logits, const int32_t* labels, float* loss, float* probs,
+                         size_t N, size_t C, int masked, void* ws, hipStream_t s);
+hipError_t LaunchXEntBwd(const float* probs, const int32_t* labels, const float* seed,
+                         float* dlogits, size_t N, size_t C, int masked, void* ws,
+                         hipStream_t s);
+
+// Optimizer family (k_optim.hip).  `flag` is the device refusal word that
+// every parameter-writing kernel honours; `scale` a device float slot.
+// ws for the norm: 8 * 1024 bytes.
+hipError_t LaunchClipFactor(const float* g, size_t n, float max_norm, float* scale, int* flag,
+                            void* ws, hipStream_t s);
+hipError_t LaunchSqNormAccum(const float* g, size_t n, float* acc, void* ws, hipStream_t s);
+hipError_t LaunchGlobalClipFactor(const float* acc, float max_norm, float* scale, int* flag,
+                                  hipStream_t s);
+hipError_t LaunchScaleByFactor(float* g, size_t n, const float* scale, const int* flag,
+                               hipStream_t s);
+hipError_t LaunchAdamW(float* p, const float* g, float* m, float* v, size_t n, float lr,
+                       float beta1, float beta2, float eps, float wd, float inv_bc1,
+                       float inv_bc2, const float* scale, const int* flag, hipStream_t s);
+hipError_t LaunchSgd(float* p, const float* g, size_t n, float lr, float wd, const float* scale,
+                     const int* flag, hipStream_t s);
+
+// fp32-output GEMM family on MFMA (k_gemm_f32.hip).
+struct GemmArgs {
+  int layout;          // 0 NN (A[M,K], B[K,N]), 1 NT (B[N,K]), 2 TN (A[K,M])
+  int b_kind;          // 0 f32, 1 int8, 2 bf16
+  const float* A;
+  const void* B;
+  float* C;
+  size_t M, N, K;
+  float alpha_a;       // multiplies A's elements as they enter (NN / TN alpha, q8 scale)
+  float alpha_dot;     // multiplies the finished dot (NT alpha, NT q8 scale)
+  const float* b_col_scale;  // NN q8: widened weight * scale[n]
+  const float* a_k_scale;    // NT q8: A[m,k] * scale[k]
+  const float* addend;       // C = D + dot
+  const float* bias;         // epilogue bias [N]
+  int act;                   // epilogue activation
+  int accumulate;            // C += (GemmAccNN)
+  int relaxed;               // bf16 MFMA over bf16-rounded A (kFlagRelaxed)
+};
+hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s);
+
+// W8A8 (k_gemm_i8.hip).
+hipError_t LaunchQuantizeRows(const float* X, int8_t* Q, float* scale, size_t rows, size_t cols,
+                              hipStream_t s);
+hipError_t LaunchPackWeightsI8(const float* W, int8_t* Qt, float* scale, size_t K, size_t N,
+                               hipStream_t s);
+hipError_t LaunchGemmW8A8(const int8_t* QA, const float* sa, const int8_t* QWt, const float* sw,
+                          float* C, int32_t* acc, size_t M, size_t N, size_t K, hipStream_t s);
+
+// Attention (k_attention.hip).  dtype 0 = f32 exact family, 1 = bf16 MFMA.
+hipError_t LaunchAttnFwdTiled(int dtype, const float* q, const float* k, const float* v, float* o,
+                              float* stats, size_t B, size_t S, size_t H, size_t d,
+                              const int32_t* starts, hipStream_t s);
+hipError_t LaunchAttnDQTiled(int dtype, const float* q, const float* k, const float* v,
+                             const float* dout, float* stats, float* dq, size_t B, size_t S,
+                             size_t H, size_t d, hipStream_t s);
+hipError_t LaunchAttnDKTiled(int dtype, const float* q, const float* k, const float* v,
+                             const float* dout, const float* stats, float* dk, size_t B,
+                             size_t S, size_t H, size_t d, hipStream_t s);
+hipError_t LaunchAttnDVTiled(int dtype, const float* q, const float* k, const float* dout,
+                             const float* stats, float* dv, size_t B, size_t S, size_t H,
+                             size_t d, hipStream_t s);
+hipError_t LaunchAttnFwdCached(const float* q, const float* k, const float* v, float* o,
+                               float* probs, size_t B, size_t S, size_t H, size_t d,
+                               const int32_t* starts, hipStream_t s);
+hipError_t LaunchAttnDP(const float* dout, const float* v, float* dp, size_t B, size_t S,
+                        size_t H, size_t d, hipStream_t s);
+hipError_t LaunchAttnDV(const float* probs, const float* dout, float* dv, size_t B, size_t S,
+                        size_t H, size_t d, hipStream_t s);
+hipError_t LaunchSoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t rows,
+                                size_t cols, hipStream_t s);
+hipError_t LaunchAttnDQ(const float* ds, const float* k, float* dq, size_t B, size_t S, size_t H,
+                        size_t d, hipStream_t s);
+hipError_t LaunchAttnDK(const float* ds, const float* q, float* dk, size_t B, size_t S, size_t H,
+                        size_t d, hipStream_t s);
+
+}  // namespace seeai

@@ -1,0 +1,438 @@
+// k_elementwise.hip -- the HBM-bound plan-completeness family on gfx950:
+// pointwise arithmetic and activations, the bias broadcast, the column
+// reduction, fused elementwise chains, the embedding gather, LayerNorm,
+// RMSNorm, RoPE and the eval argmax.
+//
+// Pointwise kernels are one element per lane over a grid-stride loop with
+// 16-byte loads where the tensor allows; every element has one writer, so
+// results never depend on the grid.  Row kernels (norms, argmax) give one
+// 256-lane workgroup to a row and reduce in a fixed butterfly + wave order.
+// Every expression is the reference's own (built -ffp-contract=off), so the
+// arithmetic kernels reproduce the reference's bits wherever no libm call
+// is involved.
+#include "common.h"
+
+namespace seeai {
+namespace {
+
+constexpr int kThreads = 256;
+
+template <typename F>
+__global__ void __launch_bounds__(kThreads) MapKernel(size_t n, F f) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
+    f(i);
+}
+
+template <typename F>
+hipError_t Map(size_t n, hipStream_t s, F f) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(MapKernel<F>, dim3(GridFor(n, kThreads, 8192)), dim3(kThreads), 0, s, n, f);
+  return hipGetLastError();
+}
+
+// elementwise.cc:16-27 / 38-48 as 4-wide vectors when n and the pointers
+// allow (the same per-element expression; vectors only widen the access).
+__global__ void __launch_bounds__(kThreads)
+AddEW4(const float4* __restrict__ x, const float4* __restrict__ y, float4* __restrict__ o, size_t n4) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
+    const float4 a = x[i], b = y[i];
+    o[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+  }
+}
+
+inline bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// kFusedMap (elementwise.cc:56-149, instruction.h:270-297).
+struct FusedProgram {
+  uint8_t stage[4];
+  int count;
+};
+
+__global__ void __launch_bounds__(kThreads)
+FusedMapKernel(const float* __restrict__ x, const float* __restrict__ o1,
+               const float* __restrict__ o2, float* __restrict__ out, size_t n,
+               FusedProgram prog, float imm0, float imm1) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
+    float run = x[i];
+    for (int s = 0; s < prog.count; ++s) {
+      const uint8_t st = prog.stage[s];
+      const int arg = (st >> 4) & 3;
+      const bool right = (st & 0x80) != 0;
+      const float* other = arg == 1 ? o1 : o2;
+      switch (st & 0x0F) {
+        case 1: run = right ? other[i] + run : run + other[i]; break;
+        case 2: run = right ? other[i] * run : run * other[i]; break;
+        case 3: run = (arg == 0 ? imm0 : imm1) * run; break;
+        case 4: run = ReluExpr(run); break;
+        case 5: run = GeluExpr(run); break;
+        case 6: run = SiluExpr(run); break;
+        default: break;
+      }
+    }
+    out[i] = run;
+  }
+}
+
+// ReduceRows (elementwise.cc:160-187): one lane per column walking the rows
+// in order -- the reference's per-column association exactly.
+__global__ void __launch_bounds__(kThreads)
+ReduceRowsKernel(const float* __restrict__ dy, float* __restrict__ db, size_t rows, size_t cols) {
+  const size_t c = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (c >= cols) return;
+  float acc = 0.0f;
+  for (size_t r = 0; r < rows; ++r) acc += dy[r * cols + c];
+  db[c] = acc;
+}
+
+// EmbedFwd (elementwise.cc:151-158): one workgroup per token row.
+__global__ void __launch_bounds__(kThreads)
+EmbedKernel(const int32_t* __restrict__ tokens, const float* __restrict__ table,
+            float* __restrict__ out, size_t dim) {
+  const size_t r = blockIdx.x;
+  const float* src = table + static_cast<size_t>(tokens[r]) * dim;
+  float* dst = out + r * dim;
+  for (size_t c = threadIdx.x; c < dim; c += kThreads) dst[c] = src[c];
+}
+
+// LayerNorm forward (normalization.cc:17-45): double row sums, f32 stats.
+__global__ void __launch_bounds__(kThreads)
+LayerNormFwdKernel(const float* __restrict__ x, const float* __restrict__ g,
+                   const float* __restrict__ b, float* __restrict__ y, float* __restrict__ mean,
+                   float* __restrict__ rstd, size_t cols, float eps) {
+  __shared__ double red[kThreads / kWave];
+  const size_t r = blockIdx.x;
+  const float* xr = x + r * cols;
+  double sum = 0.0;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads) sum += xr[c];
+  sum = BlockSumD<kThreads>(sum, red);
+  const float mu = static_cast<float>(sum / static_cast<double>(cols));
+  double var = 0.0;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads) {
+    const double d = static_cast<double>(xr[c]) - mu;
+    var += d * d;
+  }
+  var = BlockSumD<kThreads>(var, red);
+  const float rs = 1.0f / sqrtf(static_cast<float>(var / static_cast<double>(cols)) + eps);
+  if (threadIdx.x == 0) {
+    mean[r] = mu;
+    rstd[r] = rs;
+  }
+  float* yr = y + r * cols;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads) yr[c] = (xr[c] - mu) * rs * g[c] + b[c];
+}
+
+// LayerNorm backward (normalization.cc:47-78).
+__global__ void __launch_bounds__(kThreads)
+LayerNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
+                   const float* __restrict__ g, const float* __restrict__ mean,
+                   const float* __restrict__ rstd, float* __restrict__ dx, size_t cols) {
+  __shared__ double red[kThreads / kWave];
+  const size_t r = blockIdx.x;
+  const float* dyr = dy + r * cols;
+  const float* xr = x + r * cols;
+  const float mu = mean[r], rs = rstd[r];
+  double sg = 0.0, sgx = 0.0;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float xhat = (xr[c] - mu) * rs;
+    const float gg = dyr[c] * g[c];
+    sg += gg;
+    sgx += static_cast<double>(gg) * xhat;
+  }
+  sg = BlockSumD<kThreads>(sg, red);
+  sgx = BlockSumD<kThreads>(sgx, red);
+  const float inv_d = 1.0f / static_cast<float>(cols);
+  const float mg = static_cast<float>(sg) * inv_d;
+  const float mgx = static_cast<float>(sgx) * inv_d;
+  float* dxr = dx + r * cols;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float xhat = (xr[c] - mu) * rs;
+    const float gg = dyr[c] * g[c];
+    dxr[c] = rs * (gg - mg - xhat * mgx);
+  }
+}
+
+// RMSNorm forward / backward (normalization.cc:80-113).
+__global__ void __launch_bounds__(kThreads)
+RmsNormFwdKernel(const float* __restrict__ x, const float* __restrict__ g, float* __restrict__ y,
+                 float* __restrict__ rstd, size_t cols, float eps) {
+  __shared__ double red[kThreads / kWave];
+  const size_t r = blockIdx.x;
+  const float* xr = x + r * cols;
+  double ss = 0.0;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads) ss += static_cast<double>(xr[c]) * xr[c];
+  ss = BlockSumD<kThreads>(ss, red);
+  const float rs = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + eps);
+  if (threadIdx.x == 0) rstd[r] = rs;
+  float* yr = y + r * cols;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads) yr[c] = xr[c] * rs * g[c];
+}
+
+__global__ void __launch_bounds__(kThreads)
+RmsNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
+                 const float* __restrict__ g, const float* __restrict__ rstd,
+                 float* __restrict__ dx, size_t cols) {
+  __shared__ double red[kThreads / kWave];
+  const size_t r = blockIdx.x;
+  const float* dyr = dy + r * cols;
+  const float* xr = x + r * cols;
+  const float rs = rstd[r];
+  double sgx = 0.0;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads)
+    sgx += static_cast<double>(dyr[c] * g[c]) * xr[c];
+  sgx = BlockSumD<kThreads>(sgx, red);
+  const float inv_d = 1.0f / static_cast<float>(cols);
+  const float mgx = static_cast<float>(sgx) * inv_d;
+  float* dxr = dx + r * cols;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads)
+    dxr[c] = rs * (dyr[c] * g[c] - xr[c] * rs * rs * mgx);
+}
+
+// RoPE (attention.cc:103-174): one lane per (b, s, h) head segment, walking
+// the pairs in order with the reference's frequency recurrence, so every
+// angle is the reference's float; cos/sin are the device's.
+__global__ void __launch_bounds__(kThreads)
+RopeKernel(const float* __restrict__ x, float* __restrict__ y, size_t B, size_t S, size_t H,
+           size_t d, float step, const float* __restrict__ table, int backward) {
+  const size_t u = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (u >= B * S * H) return;
+  const size_t D = H * d, half = d / 2;
+  const size_t s = (u / H) % S;
+  const float* xr = x + (u / H) * D + (u % H) * d;
+  float* yr = y + (u / H) * D + (u % H) * d;
+  const float* row = table ? table + s * half * 2 : nullptr;
+  float freq = 1.0f;
+  for (size_t c = 0; c + 1 < d; c += 2) {
+    float cs, sn;
+    if (row) {
+      cs = row[c];
+      sn = row[c + 1];
+    } else {
+      const float theta = static_cast<float>(s) * freq;
+      cs = cosf(theta);
+      sn = sinf(theta);
+      freq *= step;
+    }
+    const float a = xr[c], b2 = xr[c + 1];
+    if (backward) {
+      yr[c] = a * cs + b2 * sn;
+      yr[c + 1] = -a * sn + b2 * cs;
+    } else {
+      yr[c] = a * cs - b2 * sn;
+      yr[c + 1] = a * sn + b2 * cs;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+RopeTableKernel(float* __restrict__ table, size_t S, size_t d, float step) {
+  const size_t s = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (s >= S) return;
+  const size_t half = d / 2;
+  float* row = table + s * half * 2;
+  float freq = 1.0f;
+  for (size_t c = 0; c < half; ++c) {
+    const float theta = static_cast<float>(s) * freq;
+    row[2 * c] = cosf(theta);
+    row[2 * c + 1] = sinf(theta);
+    freq *= step;
+  }
+}
+
+// SegmentStarts (attention.cc:176-185): a sequential scan per window.
+__global__ void SegmentStartsKernel(const int32_t* __restrict__ tokens, int32_t* __restrict__ starts,
+                                    size_t B, size_t S, int32_t eos) {
+  const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  int32_t start = 0;
+  for (size_t t = 0; t < S; ++t) {
+    starts[b * S + t] = start;
+    if (tokens[b * S + t] == eos) start = static_cast<int32_t>(t + 1);
+  }
+}
+
+// Eval argmax (update_engine.cc:552-560): the first maximum wins; a NaN
+// never wins, and a NaN in column 0 keeps index 0 (no comparison beats it).
+__global__ void __launch_bounds__(kThreads)
+ArgmaxKernel(const float* __restrict__ probs, size_t cols, int32_t* __restrict__ out) {
+  __shared__ float bv[kThreads];
+  __shared__ int bi[kThreads];
+  const float* row = probs + static_cast<size_t>(blockIdx.x) * cols;
+  float best = -INFINITY;
+  int idx = -1;
+  for (size_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float v = row[c];
+    if (v == v && (idx < 0 || v > best)) {
+      best = v;
+      idx = static_cast<int>(c);
+    }
+  }
+  bv[threadIdx.x] = best;
+  bi[threadIdx.x] = idx;
+  __syncthreads();
+  for (int o = kThreads / 2; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      const float v2 = bv[threadIdx.x + o];
+      const int i2 = bi[threadIdx.x + o];
+      const int i1 = bi[threadIdx.x];
+      if (i2 >= 0 && (i1 < 0 || v2 > bv[threadIdx.x] || (v2 == bv[threadIdx.x] && i2 < i1))) {
+        bv[threadIdx.x] = v2;
+        bi[threadIdx.x] = i2;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float v0 = row[0];
+    out[blockIdx.x] = (v0 != v0 || bi[0] < 0) ? 0 : bi[0];
+  }
+}
+
+}  // namespace
+
+hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hipStream_t s) {
+  if (n % 4 == 0 && Aligned16(x) && Aligned16(y) && Aligned16(out)) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(AddEW4, dim3(GridFor(n / 4, kThreads, 8192)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const float4*>(x), reinterpret_cast<const float4*>(y),
+                       reinterpret_cast<float4*>(out), n / 4);
+    return hipGetLastError();
+  }
+  return Map(n, s, [=] __device__(size_t i) { out[i] = x[i] + y[i]; });
+}
+hipError_t LaunchMulEW(const float* x, const float* y, float* out, size_t n, hipStream_t s) {
+  return Map(n, s, [=] __device__(size_t i) { out[i] = x[i] * y[i]; });
+}
+hipError_t LaunchAddBias(const float* x, const float* b, float* out, size_t rows, size_t cols,
+                         hipStream_t s) {
+  return Map(rows * cols, s, [=] __device__(size_t i) { out[i] = x[i] + b[i % cols]; });
+}
+// kind: 1 relu, 2 gelu, 3 silu, 4 scale (out = alpha * x).
+hipError_t LaunchUnary(int kind, const float* x, float* out, size_t n, float alpha, hipStream_t s) {
+  switch (kind) {
+    case 1: return Map(n, s, [=] __device__(size_t i) { out[i] = ReluExpr(x[i]); });
+    case 2: return Map(n, s, [=] __device__(size_t i) { out[i] = GeluExpr(x[i]); });
+    case 3: return Map(n, s, [=] __device__(size_t i) { out[i] = SiluExpr(x[i]); });
+    default: return Map(n, s, [=] __device__(size_t i) { out[i] = alpha * x[i]; });
+  }
+}
+// kind: 1 relu, 2 gelu, 3 silu backward (activation.cc:28-75).
+hipError_t LaunchBinaryBwd(int kind, const float* dy, const float* x, float* dx, size_t n,
+                           hipStream_t s) {
+  switch (kind) {
+    case 1:
+      return Map(n, s, [=] __device__(size_t i) { dx[i] = x[i] > 0.0f ? dy[i] : 0.0f; });
+    case 2:
+      return Map(n, s, [=] __device__(size_t i) {
+        const float kC = 0.7978845608028654f, kA = 0.044715f;
+        const float v = x[i];
+        const float u = kC * (v + kA * v * v * v);
+        const float t = tanhf(u);
+        const float omt2 = 1.0f - t * t;
+        const float tail = omt2 == 0.0f ? 0.0f : 0.5f * v * omt2 * (kC * (1.0f + 3.0f * kA * v * v));
+        dx[i] = dy[i] * (0.5f * (1.0f + t) + tail);
+      });
+    default:
+      return Map(n, s, [=] __device__(size_t i) {
+        const float sg = SigmoidExpr(x[i]);
+        dx[i] = dy[i] * (sg * (1.0f + x[i] * (1.0f - sg)));
+      });
+  }
+}
+hipError_t LaunchReduceRows(const float* dy, float* db, size_t rows, size_t cols, hipStream_t s) {
+  if (cols == 0) return hipSuccess;
+  hipLaunchKernelGGL(ReduceRowsKernel, dim3(GridFor(cols, kThreads)), dim3(kThreads), 0, s, dy, db,
+                     rows, cols);
+  return hipGetLastError();
+}
+hipError_t LaunchFill(float* dst, float value, size_t n, hipStream_t s) {
+  return Map(n, s, [=] __device__(size_t i) { dst[i] = value; });
+}
+hipError_t LaunchCopy(const float* src, float* dst, size_t n, hipStream_t s) {
+  return Map(n, s, [=] __device__(size_t i) { dst[i] = src[i]; });
+}
+hipError_t LaunchAccumulate(float* dst, const float* src, size_t n, hipStream_t s) {
+  return Map(n, s, [=] __device__(size_t i) { dst[i] += src[i]; });
+}
+hipError_t LaunchEmbed(const int32_t* tokens, const float* table, float* out, size_t rows,
+                       size_t dim, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(EmbedKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, tokens,
+                     table, out, dim);
+  return hipGetLastError();
+}
+hipError_t LaunchFusedMap(const float* x, const float* o1, const float* o2, float* out, size_t n,
+                          uint64_t stages, float imm0, float imm1, hipStream_t s) {
+  FusedProgram p{};
+  p.count = 0;
+  for (; p.count < 4; ++p.count) {
+    p.stage[p.count] = static_cast<uint8_t>(stages >> (8 * p.count));
+    if ((p.stage[p.count] & 0x0F) == 0) break;
+  }
+  if (p.count == 0 || n == 0) return hipSuccess;
+  hipLaunchKernelGGL(FusedMapKernel, dim3(GridFor(n, kThreads, 8192)), dim3(kThreads), 0, s, x, o1,
+                     o2, out, n, p, imm0, imm1);
+  return hipGetLastError();
+}
+hipError_t LaunchLayerNormFwd(const float* x, const float* g, const float* b, float* y,
+                              float* mean, float* rstd, size_t rows, size_t cols, float eps,
+                              hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(LayerNormFwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s,
+                     x, g, b, y, mean, rstd, cols, eps);
+  return hipGetLastError();
+}
+hipError_t LaunchLayerNormBwd(const float* dy, const float* x, const float* g,
+                              const float* mean, const float* rstd, float* dx, size_t rows,
+                              size_t cols, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(LayerNormBwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s,
+                     dy, x, g, mean, rstd, dx, cols);
+  return hipGetLastError();
+}
+hipError_t LaunchRmsNormFwd(const float* x, const float* g, float* y, float* rstd, size_t rows,
+                            size_t cols, float eps, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(RmsNormFwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, x,
+                     g, y, rstd, cols, eps);
+  return hipGetLastError();
+}
+hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, const float* rstd,
+                            float* dx, size_t rows, size_t cols, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(RmsNormBwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, dy,
+                     x, g, rstd, dx, cols);
+  return hipGetLastError();
+}
+hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
+                      float step, const float* table, int backward, hipStream_t s) {
+  const size_t n = B * S * H;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(RopeKernel, dim3(GridFor(n, kThreads)), dim3(kThreads), 0, s, x, y, B, S, H,
+                     d, step, table, backward);
+  return hipGetLastError();
+}
+hipError_t LaunchRopeTable(float* table, size_t S, size_t d, float step, hipStream_t s) {
+  if (S == 0) return hipSuccess;
+  hipLaunchKernelGGL(RopeTableKernel, dim3(GridFor(S, kThreads)), dim3(kThreads), 0, s, table, S,
+                     d, step);
+  return hipGetLastError();
+}
+hipError_t LaunchSegmentStarts(const int32_t* tokens, int32_t* starts, size_t B, size_t S,
+                               int32_t eos, hipStream_t s) {
+  if (B == 0) return hipSuccess;
+  hipLaunchKernelGGL(SegmentStartsKernel, dim3(GridFor(B, 64)), dim3(64), 0, s, tokens, starts, B,
+                     S, eos);
+  return hipGetLastError();
+}
+hipError_t LaunchArgmaxRows(const float* probs, size_t rows, size_t cols, int32_t* out,
+                            hipStream_t s) {
+  if (rows == 0 || cols == 0) return hipSuccess;
+  hipLaunchKernelGGL(ArgmaxKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, probs,
+                     cols, out);
+  return hipGetLastError();
+}
+
+}  // namespace seeai

@@ -1,0 +1,355 @@
+// k_gemm_i8.hip -- the W8A8 GEMM on CDNA4 int8 MFMA: per-row symmetric
+// int8 activations x per-output-channel symmetric int8 weights, int32
+// accumulation, f32 dequant C[m,n] = (f32(acc) * sa[m]) * sw[n].
+//
+// The reference has no such kernel (its q8 GEMM widens int8 weights into f32
+// arithmetic); the quantizer follows the reference's int8 weight packer
+// (compiler/backend/allocation/arena_binder.cc:129-177): scale = max|x|/127,
+// an all-zero vector takes 1, a subnormal quotient FLT_MIN, levels
+// clamp(round(x / scale), -127, 127) by a true division, ties away from zero.
+// int8 x int8 products summed in int32 are exact (|sum| <= 127^2 K < 2^31 for
+// K <= 133,144), so every accumulation order gives the same bits.
+//
+// Layout: activations QA [M, K] row-major, weights packed once into
+// QWt [N, K] (K contiguous: both MFMA operands then read 16 contiguous
+// bytes per lane).
+//
+// Large M: a 256 x 256 tile per 256-lane workgroup, four waves in 2 x 2,
+// each a 128 x 128 block of v_mfma_i32_32x32x32_i8 tiles (16 accumulators
+// of 16 int32 -- the compiler places them in AGPRs); K walks BK bytes at a
+// time through padded LDS rows (a 16-byte pad per row: the 16-byte lane
+// reads of a wave fall in distinct banks), the next K tile prefetched into
+// registers while the current one multiplies.
+// Small M (decode-like, M <= 64): one 16-column slice of C per workgroup,
+// its four waves each reducing a quarter of K on v_mfma_i32_16x16x64_i8
+// straight from global memory (each weight byte is read once), then summed
+// through LDS -- the weight stream is the whole cost, spread over N/16
+// workgroups.
+#include <cfloat>
+#include <cstdlib>
+
+#include "common.h"
+
+namespace seeai {
+namespace {
+
+// --- quantizers --------------------------------------------------------------
+
+__device__ __forceinline__ float QuantScale(float max_abs) {
+  if (max_abs == 0.0f) return 1.0f;
+  const float s = __fdiv_rn(max_abs, 127.0f);
+  return s > FLT_MIN ? s : FLT_MIN;
+}
+__device__ __forceinline__ int8_t QuantLevel(float x, float scale) {
+  float r = roundf(__fdiv_rn(x, scale));
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return static_cast<int8_t>(r);
+}
+
+constexpr int kQThreads = 256;
+
+__global__ void __launch_bounds__(kQThreads)
+QuantizeRowsKernel(const float* __restrict__ X, int8_t* __restrict__ Q, float* __restrict__ scale,
+                   size_t cols) {
+  __shared__ float red[kQThreads / kWave];
+  const size_t r = blockIdx.x;
+  const float* x = X + r * cols;
+  int8_t* q = Q + r * cols;
+  const bool vec = (cols % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(q) & 3) == 0);
+  float mx = 0.0f;
+  if (vec) {
+    for (size_t c = threadIdx.x * 4; c < cols; c += kQThreads * 4) {
+      const float4 v = *reinterpret_cast<const float4*>(x + c);
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+  } else {
+    for (size_t c = threadIdx.x; c < cols; c += kQThreads) mx = fmaxf(mx, fabsf(x[c]));
+  }
+  mx = BlockMaxF<kQThreads>(mx, red);
+  const float s = QuantScale(mx);
+  if (threadIdx.x == 0) scale[r] = s;
+  if (vec) {
+    for (size_t c = threadIdx.x * 4; c < cols; c += kQThreads * 4) {
+      const float4 v = *reinterpret_cast<const float4*>(x + c);
+      const uint32_t packed = static_cast<uint8_t>(QuantLevel(v.x, s)) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.y, s))) << 8) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.z, s))) << 16) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.w, s))) << 24);
+      *reinterpret_cast<uint32_t*>(q + c) = packed;
+    }
+  } else {
+    for (size_t c = threadIdx.x; c < cols; c += kQThreads) q[c] = QuantLevel(x[c], s);
+  }
+}
+
+// Column max-abs of W [K, N]: one lane per column, coalesced across lanes.
+__global__ void __launch_bounds__(kQThreads)
+ColumnScaleKernel(const float* __restrict__ W, float* __restrict__ scale, size_t K, size_t N) {
+  const size_t n = static_cast<size_t>(blockIdx.x) * kQThreads + threadIdx.x;
+  if (n >= N) return;
+  float mx = 0.0f;
+  for (size_t k = 0; k < K; ++k) mx = fmaxf(mx, fabsf(W[k * N + n]));
+  scale[n] = QuantScale(mx);
+}
+
+// Quantize and transpose W [K, N] -> Qt [N, K] through a 32 x 32 LDS tile.
+__global__ void __launch_bounds__(kQThreads)
+PackTransposeKernel(const float* __restrict__ W, const float* __restrict__ scale,
+                    int8_t* __restrict__ Qt, size_t K, size_t N) {
+  __shared__ int8_t tile[32][33];
+  const size_t k0 = static_cast<size_t>(blockIdx.y) * 32, n0 = static_cast<size_t>(blockIdx.x) * 32;
+  const int tx = threadIdx.x % 32, ty = threadIdx.x / 32;  // 32 x 8
+  for (int r = ty; r < 32; r += 8) {
+    const size_t k = k0 + r, n = n0 + tx;
+    tile[r][tx] = (k < K && n < N) ? QuantLevel(W[k * N + n], scale[n]) : 0;
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const size_t n = n0 + r, k = k0 + tx;
+    if (n < N && k < K) Qt[n * K + k] = tile[tx][r];
+  }
+}
+
+// --- the large-M GEMM ----------------------------------------------------------
+
+constexpr int kThreads = 256;
+
+template <int BM, int BN, int BK>
+__global__ void __launch_bounds__(kThreads)
+GemmI8TileKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
+                 const int8_t* __restrict__ QW, const float* __restrict__ sw,
+                 float* __restrict__ C, int32_t* __restrict__ acc_out, int M, int N, int K) {
+  constexpr int LDK = BK + 16;                 // padded LDS row stride (bytes)
+  constexpr int WM = BM / 2, WN = BN / 2;      // per-wave block
+  constexpr int TM = WM / 32, TN = WN / 32;    // 32 x 32 MFMA tiles per wave
+  constexpr int kChunksRow = BK / 16;          // 16-byte chunks per tile row
+  constexpr int NA = BM * kChunksRow / kThreads;
+  constexpr int NB = BN * kChunksRow / kThreads;
+  __shared__ __attribute__((aligned(16))) int8_t As[BM * LDK];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[BN * LDK];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int wm = (wave / 2) * WM, wn = (wave % 2) * WN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+  v16i acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  v4i ra[NA], rb[NB];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int e = 0; e < NA; ++e) {
+      const int c = tid + e * kThreads;
+      const int row = c / kChunksRow, kc = c % kChunksRow;
+      const int m = m0 + row, k = k0 + kc * 16;
+      ra[e] = (m < M && k < K) ? *reinterpret_cast<const v4i*>(QA + static_cast<size_t>(m) * K + k)
+                               : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int e = 0; e < NB; ++e) {
+      const int c = tid + e * kThreads;
+      const int row = c / kChunksRow, kc = c % kChunksRow;
+      const int n = n0 + row, k = k0 + kc * 16;
+      rb[e] = (n < N && k < K) ? *reinterpret_cast<const v4i*>(QW + static_cast<size_t>(n) * K + k)
+                               : v4i{0, 0, 0, 0};
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int e = 0; e < NA; ++e) {
+      const int c = tid + e * kThreads;
+      *reinterpret_cast<v4i*>(As + (c / kChunksRow) * LDK + (c % kChunksRow) * 16) = ra[e];
+    }
+#pragma unroll
+    for (int e = 0; e < NB; ++e) {
+      const int c = tid + e * kThreads;
+      *reinterpret_cast<v4i*>(Bs + (c / kChunksRow) * LDK + (c % kChunksRow) * 16) = rb[e];
+    }
+  };
+
+  load(0);
+  for (int k0 = 0; k0 < K; k0 += BK) {
+    __syncthreads();
+    store();
+    __syncthreads();
+    if (k0 + BK < K) load(k0 + BK);
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 32) {
+      v4i af[TM], bf[TN];
+      const int koff = ks + (lane / 32) * 16;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const v4i*>(As + (wm + i * 32 + lane % 32) * LDK + koff);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const v4i*>(Bs + (wn + j * 32 + lane % 32) * LDK + koff);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Lane holds column (lane % 32) and rows 8*(r/4) + 4*(lane/32) + r%4.
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn + j * 32 + lane % 32;
+      if (n >= N) continue;
+      const float swn = sw[n];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+        if (m >= M) continue;
+        const size_t o = static_cast<size_t>(m) * N + n;
+        const int32_t v = acc[i][j][r];
+        if (acc_out) acc_out[o] = v;
+        C[o] = (static_cast<float>(v) * sa[m]) * swn;
+      }
+    }
+}
+
+// --- the small-M GEMM (decode-like) ---------------------------------------------
+
+template <int MT>  // 16-row MFMA tiles covering M <= 16 * MT
+__global__ void __launch_bounds__(kThreads)
+GemmI8SkinnyKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
+                   const int8_t* __restrict__ QW, const float* __restrict__ sw,
+                   float* __restrict__ C, int32_t* __restrict__ acc_out, int M, int N, int K) {
+  __shared__ v4i part[4][MT][kWave];
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int n0 = blockIdx.x * 16;
+  const int kq = K / 4;  // each wave reduces one contiguous quarter of K
+  const int kb = wave * kq, ke = kb + kq;
+  const int col = n0 + lane % 16;
+  const int kl = (lane / 16) * 16;
+  const int8_t* wrow = QW + static_cast<size_t>(col < N ? col : 0) * K;
+  v4i acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = v4i{0, 0, 0, 0};
+#pragma unroll 4
+  for (int k = kb; k < ke; k += 64) {
+    const v4i b = col < N ? *reinterpret_cast<const v4i*>(wrow + k + kl) : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = t * 16 + lane % 16;
+      const v4i a = m < M ? *reinterpret_cast<const v4i*>(QA + static_cast<size_t>(m) * K + k + kl)
+                          : v4i{0, 0, 0, 0};
+      acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) part[wave][t][lane] = acc[t];
+  __syncthreads();
+  if (wave != 0) return;
+  // Integer sums: exact in any order; wave order for good measure.
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    v4i s = part[0][t][lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) s += part[w][t][lane];
+    if (col >= N) continue;
+    const float swn = sw[col];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = t * 16 + (lane / 16) * 4 + r;  // lane holds rows 4*(lane/16)+r
+      if (m >= M) continue;
+      const size_t o = static_cast<size_t>(m) * N + col;
+      if (acc_out) acc_out[o] = s[r];
+      C[o] = (static_cast<float>(s[r]) * sa[m]) * swn;
+    }
+  }
+}
+
+// --- any shape: one lane per output, for K not a multiple of the vector ------
+
+__global__ void __launch_bounds__(kThreads)
+GemmI8NaiveKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
+                  const int8_t* __restrict__ QW, const float* __restrict__ sw,
+                  float* __restrict__ C, int32_t* __restrict__ acc_out, size_t M, size_t N,
+                  size_t K) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= M * N) return;
+  const size_t m = i / N, n = i % N;
+  int32_t s = 0;
+  for (size_t k = 0; k < K; ++k)
+    s += static_cast<int32_t>(QA[m * K + k]) * static_cast<int32_t>(QW[n * K + k]);
+  if (acc_out) acc_out[i] = s;
+  C[i] = (static_cast<float>(s) * sa[m]) * sw[n];
+}
+
+inline bool Aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace
+
+hipError_t LaunchQuantizeRows(const float* X, int8_t* Q, float* scale, size_t rows, size_t cols,
+                              hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(QuantizeRowsKernel, dim3(static_cast<unsigned>(rows)), dim3(kQThreads), 0, s,
+                     X, Q, scale, cols);
+  return hipGetLastError();
+}
+
+hipError_t LaunchPackWeightsI8(const float* W, int8_t* Qt, float* scale, size_t K, size_t N,
+                               hipStream_t s) {
+  if (N == 0) return hipSuccess;
+  hipLaunchKernelGGL(ColumnScaleKernel, dim3(GridFor(N, kQThreads)), dim3(kQThreads), 0, s, W,
+                     scale, K, N);
+  if (K == 0) return hipGetLastError();
+  hipLaunchKernelGGL(PackTransposeKernel,
+                     dim3(static_cast<unsigned>((N + 31) / 32), static_cast<unsigned>((K + 31) / 32)),
+                     dim3(kQThreads), 0, s, W, scale, Qt, K, N);
+  return hipGetLastError();
+}
+
+hipError_t LaunchGemmW8A8(const int8_t* QA, const float* sa, const int8_t* QWt, const float* sw,
+                          float* C, int32_t* acc, size_t M, size_t N, size_t K, hipStream_t s) {
+  if (M == 0 || N == 0) return hipSuccess;
+  const bool vec_ok = K % 16 == 0 && Aligned(QA, 16) && Aligned(QWt, 16) && M < (1u << 30) &&
+                      N < (1u << 30) && K < (1u << 30) && M * K < (1ull << 31) &&
+                      N * K < (1ull << 31);
+  if (vec_ok && M <= 64 && K % 256 == 0) {
+    const dim3 grid(static_cast<unsigned>((N + 15) / 16));
+    if (M <= 32)
+      hipLaunchKernelGGL(GemmI8SkinnyKernel<2>, grid, dim3(kThreads), 0, s, QA, sa, QWt, sw, C, acc,
+                         static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+    else
+      hipLaunchKernelGGL(GemmI8SkinnyKernel<4>, grid, dim3(kThreads), 0, s, QA, sa, QWt, sw, C, acc,
+                         static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+    return hipGetLastError();
+  }
+  if (vec_ok) {
+    // Tile geometry: 256 x 256 once the grid still fills the chip, else
+    // 128 x 128.  SEEAI_I8_TILE=128|256 overrides (measurement sweeps).
+    static const int forced = [] {
+      const char* e = std::getenv("SEEAI_I8_TILE");
+      return e ? std::atoi(e) : 0;
+    }();
+    const bool big = forced ? forced == 256 : (M >= 2048 && N >= 2048);
+    if (big) {
+      const dim3 grid(static_cast<unsigned>((N + 255) / 256), static_cast<unsigned>((M + 255) / 256));
+      hipLaunchKernelGGL((GemmI8TileKernel<256, 256, 64>), grid, dim3(kThreads), 0, s, QA, sa, QWt,
+                         sw, C, acc, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+    } else {
+      const dim3 grid(static_cast<unsigned>((N + 127) / 128), static_cast<unsigned>((M + 127) / 128));
+      hipLaunchKernelGGL((GemmI8TileKernel<128, 128, 128>), grid, dim3(kThreads), 0, s, QA, sa, QWt,
+                         sw, C, acc, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+    }
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(GemmI8NaiveKernel, dim3(GridFor(M * N, kThreads, 1u << 30)), dim3(kThreads), 0,
+                     s, QA, sa, QWt, sw, C, acc, M, N, K);
+  return hipGetLastError();
+}
+
+}  // namespace seeai

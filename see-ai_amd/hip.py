@@ -1,0 +1,229 @@
+"""ctypes binding of libseeai_hip.so (include/seeai_hip.h) and the Python
+mirror of the reference's executor seam.
+
+``HipBackend`` mirrors ``seeml::update_rt::ExecutorBackend``
+(runtime/executor/backend.h:82-166) for the gfx950 executor: ``name``,
+``device``, ``Bind``, ``BindSource``, ``Configure``, ``Execute``,
+``BeginRange`` / ``EndRange``, ``Flush``, ``relaxed_executions`` -- plus the
+host-sync verbs a discrete GPU needs (``Upload`` / ``Download``).  Failures
+raise ``BackendError`` carrying the library's message, which for a refused
+optimizer step is the reference's own verdict string (backend.h:65-80).
+
+The library is required: importing this module on a machine where it has
+not been built raises ``ImportError`` -- there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import struct
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libseeai_hip.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is not built: run __graft_entry__.build() (hipcc, gfx950)")
+
+_lib = C.CDLL(LIB_PATH)
+
+_P = C.c_void_p
+_U64 = C.c_uint64
+_I = C.c_int
+_F = C.c_float
+
+OK, REFUSED, INVALID, HIP_ERROR = 0, 1, 2, 3
+
+# The reference's shared refusal strings (runtime/executor/backend.h:65-80).
+NON_FINITE_NORM_REFUSAL = (
+    "gradient norm is not finite — the step was refused with the parameters "
+    "and optimizer state untouched")
+CLIP_THRESHOLD_REFUSAL = (
+    "clip threshold is not a finite positive float — the instruction was "
+    "refused with the gradient untouched")
+
+
+class StepParams(C.Structure):
+    """StepParams (runtime/executor/backend.h:56-63)."""
+    _fields_ = [("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float),
+                ("eps", C.c_float), ("weight_decay", C.c_float),
+                ("reserved", C.c_uint32), ("step", C.c_uint64)]
+
+
+# Every exported symbol with its ctypes signature: the header, one to one.
+EXPORTS = {
+    "seeai_create": (_I, [_I, C.POINTER(_P)]),
+    "seeai_destroy": (None, [_P]),
+    "seeai_last_error": (C.c_char_p, [_P]),
+    "seeai_set_stream": (_I, [_P, _P]),
+    "seeai_get_stream": (_P, [_P]),
+    "seeai_set_relaxed": (_I, [_P, _I]),
+    "seeai_relaxed_executions": (_U64, [_P]),
+    "seeai_bind": (_I, [_P, _U64, _P, _U64]),
+    "seeai_bind_source": (_I, [_P, _P, _U64]),
+    "seeai_upload": (_I, [_P, _U64, _P, _U64]),
+    "seeai_download": (_I, [_P, _U64, _P, _U64]),
+    "seeai_arena": (_P, [_P]),
+    "seeai_arena_bytes": (_U64, [_P]),
+    "seeai_execute": (_I, [_P, _P, _P]),
+    "seeai_execute_range": (_I, [_P, _P, _U64, _P, C.POINTER(_U64)]),
+    "seeai_flush": (_I, [_P]),
+    "seeai_gemm_f32": (_I, [_P, _I, _P, _P, _P, _U64, _U64, _U64, _P, _I, _P, _F, _I]),
+    "seeai_gemm_q8": (_I, [_P, _I, _P, _P, _P, _U64, _U64, _U64, _F, _P, _I]),
+    "seeai_gemm_bf16w": (_I, [_P, _I, _P, _P, _P, _U64, _U64, _U64, _P, _I]),
+    "seeai_w8a8_quantize_rows": (_I, [_P, _P, _P, _P, _U64, _U64]),
+    "seeai_w8a8_pack_weights": (_I, [_P, _P, _P, _P, _U64, _U64]),
+    "seeai_w8a8_gemm": (_I, [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64]),
+    "seeai_attn_fwd": (_I, [_P, _I, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64, _P]),
+    "seeai_attn_dq": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
+    "seeai_attn_dk": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
+    "seeai_attn_dv": (_I, [_P, _I, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
+    "seeai_xent_fwd": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _I]),
+    "seeai_xent_bwd": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _I]),
+    "seeai_adamw_step": (_I, [_P, _P, _P, _P, _P, _U64, C.POINTER(StepParams), _F]),
+    "seeai_argmax_rows": (_I, [_P, _P, _U64, _U64, _P]),
+}
+for _name, (_res, _args) in EXPORTS.items():
+    _fn = getattr(_lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+class BackendError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+def lib():
+    return _lib
+
+
+def ptr(t) -> int | None:
+    """Device address of a torch tensor (or None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+class Context:
+    """One seeai_ctx: a device, a stream, scratch and (optionally) an arena."""
+
+    def __init__(self, device: int = 0):
+        h = _P()
+        rc = _lib.seeai_create(device, C.byref(h))
+        if rc != OK:
+            raise BackendError(rc, f"seeai_create failed with status {rc}")
+        self.h = h
+        self.device_index = device
+
+    def close(self):
+        if self.h:
+            _lib.seeai_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 -- interpreter shutdown
+            pass
+
+    def check(self, rc: int):
+        if rc != OK:
+            raise BackendError(rc, _lib.seeai_last_error(self.h).decode("utf-8", "replace"))
+
+    def call(self, name: str, *args):
+        self.check(getattr(_lib, name)(self.h, *args))
+
+    def use_torch_stream(self):
+        """Enqueue on torch's current stream (0 is the null stream) so torch's
+        copies and the library's kernels are ordered."""
+        import torch
+        handle = torch.cuda.current_stream().cuda_stream
+        self.check(_lib.seeai_set_stream(self.h, _P(handle) if handle else None))
+
+
+class HipBackend:
+    """The gfx950 ExecutorBackend (runtime/executor/backend.h:82-166)."""
+
+    def __init__(self, device: int = 0):
+        self.ctx = Context(device)
+        self._params = StepParams(0.0, 0.9, 0.999, 1e-8, 0.0, 0, 0)
+
+    # backend.h:84-85
+    def name(self) -> str:
+        return "hip"
+
+    def device(self) -> str:
+        return f"AMD gfx950 device {self.ctx.device_index}"
+
+    # backend.h:99-109
+    def Bind(self, arena: bytes | bytearray | None, arena_bytes: int, rodata: bytes,
+             rodata_bytes: int | None = None):
+        ro = bytes(rodata) if rodata is not None else b""
+        n = len(ro) if rodata_bytes is None else rodata_bytes
+        buf = C.create_string_buffer(ro, max(n, 1))
+        self.ctx.call("seeai_bind", _U64(arena_bytes), buf, _U64(n))
+        if arena is not None and len(arena):
+            self.Upload(0, bytes(arena))
+
+    def BindSource(self, data: bytes | None):
+        if not data:
+            self.ctx.call("seeai_bind_source", None, _U64(0))
+            return
+        buf = C.create_string_buffer(bytes(data), len(data))
+        self.ctx.call("seeai_bind_source", buf, _U64(len(data)))
+
+    def Configure(self, policy=None):  # backend.h:117 -- the GPU keeps its own tiles
+        return None
+
+    def Execute(self, instruction: bytes, params: StepParams | None = None):
+        assert len(instruction) == 64
+        buf = C.create_string_buffer(bytes(instruction), 64)
+        self.ctx.call("seeai_execute", buf, C.byref(params or self._params))
+
+    def ExecuteRange(self, program: bytes, params: StepParams | None = None):
+        n = len(program) // 64
+        buf = C.create_string_buffer(bytes(program), max(len(program), 1))
+        failed = _U64(0)
+        rc = _lib.seeai_execute_range(self.ctx.h, buf, _U64(n), C.byref(params or self._params),
+                                      C.byref(failed))
+        if rc != OK:
+            raise BackendError(rc, f"backend 'hip' failed at instruction {failed.value}: "
+                               + _lib.seeai_last_error(self.ctx.h).decode("utf-8", "replace"))
+
+    def BeginRange(self, program, begin, end):  # backend.h:139
+        return None
+
+    def EndRange(self):
+        return None
+
+    def Flush(self):
+        self.ctx.call("seeai_flush")
+
+    def relaxed_executions(self) -> int:
+        return int(_lib.seeai_relaxed_executions(self.ctx.h))
+
+    def SetRelaxed(self, allow: bool):
+        self.ctx.call("seeai_set_relaxed", int(bool(allow)))
+
+    # host-sync verbs
+    def Upload(self, offset: int, data: bytes):
+        buf = C.create_string_buffer(bytes(data), max(len(data), 1))
+        self.ctx.call("seeai_upload", _U64(offset), buf, _U64(len(data)))
+
+    def Download(self, offset: int, nbytes: int) -> bytes:
+        buf = C.create_string_buffer(max(nbytes, 1))
+        self.ctx.call("seeai_download", _U64(offset), buf, _U64(nbytes))
+        return buf.raw[:nbytes]
+
+    def arena_ptr(self) -> int:
+        return _lib.seeai_arena(self.ctx.h)
+
+
+def pack_instruction(opcode: int, flags: int = 0, imm: int = 0, ins=(), outs=()) -> bytes:
+    """One 64-byte UpdateInstruction (source/plan/instruction.h:438-447)."""
+    null = 0xFFFFFFFFFFFFFFFF
+    i4 = list(ins) + [null] * (4 - len(ins))
+    o3 = list(outs) + [0] * (3 - len(outs))
+    return struct.pack("<HHI4Q3Q", opcode, flags, imm, *i4, *o3)

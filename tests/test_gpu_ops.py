@@ -1,0 +1,434 @@
+"""GPU parity: every opcode of the hot path, executed through the C ABI
+(seeai_execute on a bound device arena), against the oracle's instruction
+interpreter (oracle.c's restatement of cpu_backend.cc:260-646) on identical
+arena bytes.
+
+Bars: bit-exact where the kernel's arithmetic is the
+reference's expression on the reference's operands (integer, copy, add,
+bias, ReLU, the AdamW update, argmax); otherwise per-tensor
+max|a-b|/max|b| <= 1e-5 for f32 and <= 2e-2 for the bf16 (relaxed) family.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.arena import NULL, Arena, f32_bits
+from tests.conftest import bits_equal, maxrel
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+TOL_BF16 = 2e-2
+PARAMS = (1e-3, 0.9, 0.999, 1e-8, 0.01, 3)  # lr, beta1, beta2, eps, wd, step
+
+# The reference's ragged GEMM shapes (kernels_test.cc:1777-1782) plus the
+# config-1 shapes (32x512x256, 32x256x512, LoRA rank 8).
+GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 257, 63),
+               (131, 517, 203), (8, 1100, 300), (2, 700, 900), (257, 33, 64), (66, 131, 65),
+               (32, 512, 256), (32, 8, 256), (32, 512, 8), (8, 256, 32), (512, 8, 32)]
+
+
+@pytest.fixture(scope="module")
+def backend(hip):
+    return hip.HipBackend(0)
+
+
+def execute(hip, orc, backend, ar: Arena, program, params=PARAMS, expect_cpu=0):
+    arena, ro = ar.images()
+    cpu = arena.copy()
+    for ins in program:
+        rc = orc.execute(ins, cpu, ro, params)
+        assert rc == expect_cpu, f"oracle status {rc}"
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    sp = hip.StepParams(*params[:5], 0, params[5])
+    for ins in program:
+        backend.Execute(ins, sp)
+    backend.Flush()
+    gpu = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    return cpu, gpu
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# --- GEMM family -------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_gemm_f32_family(hip, orc, backend, M, N, K):
+    r = rng(M * 7919 + N * 31 + K)
+    A = r.standard_normal((M, K)).astype(np.float32)
+    At = r.standard_normal((K, M)).astype(np.float32)
+    B = r.standard_normal((K, N)).astype(np.float32)
+    Bt = r.standard_normal((N, K)).astype(np.float32)
+    D = r.standard_normal((M, N)).astype(np.float32)
+    bias = r.standard_normal(N).astype(np.float32)
+    ar = Arena()
+    a, at, b, bt = ar.add("A", A), ar.add("At", At), ar.add("B", B), ar.add("Bt", Bt)
+    d, bi = ar.add("D", D), ar.add("bias", bias)
+    outs = {n: ar.empty(n, (M, N)) for n in
+            ["nn", "nn_relu", "nn_gelu_b", "nn_silu_b", "nn_add", "nt", "nt_add", "tn", "tn_add"]}
+    acc = ar.add("acc", D.copy())
+    from tests.plan_ops import ins
+    prog = [
+        ins(1, [a, b, outs["nn"]], [M, N, K]),
+        ins(1, [a, b, outs["nn_relu"]], [M, N, K], flags=1 << 1),
+        ins(1, [a, b, outs["nn_gelu_b"], bi], [M, N, K], flags=1 | (2 << 1)),
+        ins(1, [a, b, outs["nn_silu_b"], bi], [M, N, K], flags=1 | (3 << 1)),
+        ins(1, [a, b, outs["nn_add"], d], [M, N, K], flags=1 << 3, imm=f32_bits(2.0)),
+        ins(2, [a, bt, outs["nt"]], [M, N, K], imm=f32_bits(0.37)),
+        ins(2, [a, bt, outs["nt_add"], d], [M, N, K], flags=1 << 3, imm=f32_bits(2.0)),
+        ins(3, [at, b, outs["tn"]], [M, N, K], imm=f32_bits(1.7)),
+        ins(3, [at, b, outs["tn_add"], d], [M, N, K], flags=1 << 3),
+        ins(4, [a, b, acc, f32_bits(2.0)], [M, N, K]),
+    ]
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    for name in list(outs) + ["acc"]:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= TOL, f"{name} {M}x{N}x{K}: max-rel {e:.3g}"
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 5, 7), (67, 129, 66), (131, 517, 203), (32, 512, 256),
+                                   (2, 700, 900)])
+def test_gemm_narrow_weights(hip, orc, backend, M, N, K):
+    r = rng(M + 100 * N + K)
+    A = r.standard_normal((M, K)).astype(np.float32)
+    Wq = r.integers(-127, 128, (K, N)).astype(np.int8)
+    Wqt = r.integers(-127, 128, (N, K)).astype(np.int8)
+    cs = r.uniform(1e-3, 5e-2, N).astype(np.float32)
+    ks = r.uniform(1e-3, 5e-2, K).astype(np.float32)
+    Wh = (r.standard_normal((K, N)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    Wht = (r.standard_normal((N, K)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    bias = r.standard_normal(N).astype(np.float32)
+    ar = Arena()
+    a, bi = ar.add("A", A), ar.add("bias", bias)
+    wq, wqt = ar.add("Wq", Wq, rodata=True), ar.add("Wqt", Wqt, rodata=True)
+    csr, ksr = ar.add("cs", cs, rodata=True), ar.add("ks", ks, rodata=True)
+    wh, wht = ar.add("Wh", Wh, rodata=True), ar.add("Wht", Wht, rodata=True)
+    names = ["q8", "q8cs", "q8nt", "q8ntks", "bf", "bfnt"]
+    o = {n: ar.empty(n, (M, N)) for n in names}
+    from tests.plan_ops import ins
+    prog = [
+        ins(29, [a, wq, o["q8"], f32_bits(0.013)], [M, N, K], flags=1 << 1),
+        ins(29, [a, wq, o["q8cs"], csr], [M, N, K], flags=(1 << 4) | (3 << 1)),
+        ins(30, [a, wqt, o["q8nt"], f32_bits(0.021)], [M, N, K]),
+        ins(30, [a, wqt, o["q8ntks"], ksr], [M, N, K], flags=1 << 4),
+        ins(43, [a, wh, o["bf"], bi], [M, N, K], flags=1 | (2 << 1)),
+        ins(44, [a, wht, o["bfnt"]], [M, N, K]),
+    ]
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    for name in names:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= TOL, f"{name} {M}x{N}x{K}: max-rel {e:.3g}"
+
+
+# --- elementwise / activation / normalization -------------------------------------
+
+def test_elementwise_family(hip, orc, backend):
+    from tests.plan_ops import ins
+    r = rng(5)
+    n, rows, cols = 50021, 37, 301
+    x = (r.standard_normal(n) * 4).astype(np.float32)
+    y = r.standard_normal(n).astype(np.float32)
+    X = r.standard_normal((rows, cols)).astype(np.float32)
+    bvec = r.standard_normal(cols).astype(np.float32)
+    toks = r.integers(0, 50, 77).astype(np.int32)
+    table = r.standard_normal((50, 33)).astype(np.float32)
+    ar = Arena()
+    rx, ry, rX, rb = ar.add("x", x), ar.add("y", y), ar.add("X", X), ar.add("b", bvec)
+    rt, rtab = ar.add("toks", toks), ar.add("table", table, rodata=True)
+    acc = ar.add("acc", y.copy())
+    exact = {"add": (5, [rx, ry]), "mul": (21, [rx, ry]), "relu": (7, [rx]),
+             "relu_b": (8, [ry, rx])}
+    approx = {"gelu": (22, [rx]), "gelu_b": (23, [ry, rx]), "silu": (24, [rx]),
+              "silu_b": (25, [ry, rx])}
+    prog, outs = [], {}
+    for name, (op, srcs) in {**exact, **approx}.items():
+        outs[name] = ar.empty(name, (n,))
+        prog.append(ins(op, srcs + [outs[name]], [n]))
+    outs["scale"] = ar.empty("scale", (n,))
+    prog.append(ins(9, [rx, outs["scale"], f32_bits(0.3)], [n]))
+    outs["bias"] = ar.empty("bias", (rows, cols))
+    prog.append(ins(6, [rX, rb, outs["bias"]], [rows, cols]))
+    outs["rr"] = ar.empty("rr", (cols,))
+    prog.append(ins(10, [rX, outs["rr"]], [rows, cols]))
+    outs["fill"] = ar.empty("fill", (n,))
+    prog.append(ins(19, [outs["fill"], f32_bits(-2.5)], [n]))
+    outs["copy"] = ar.empty("copy", (n,))
+    prog.append(ins(20, [rx, outs["copy"]], [n]))
+    prog.append(ins(42, [acc, rx], [n]))
+    outs["embed"] = ar.empty("embed", (77, 33))
+    prog.append(ins(41, [rt, rtab, outs["embed"]], [77, (50 << 32) | 33]))
+    # FusedMap chains (instruction.h:270-297): relu; add(slot1); gelu(add(x, y));
+    # silu(scale1(y * run)).
+    for k, (stages, o1, o2) in enumerate([(0x04, NULL, NULL), (0x11, ry, NULL),
+                                          ((0x05 << 8) | 0x11, ry, NULL),
+                                          ((0x06 << 16) | (0x13 << 8) | 0x92, ry, rx)]):
+        nm = f"fm{k}"
+        outs[nm] = ar.empty(nm, (n,))
+        prog.append(ins(46, [rx, o1, o2, outs[nm]],
+                        [n, stages, f32_bits(0.25) | (f32_bits(3.0) << 32)]))
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    for name in list(exact) + ["scale", "bias", "rr", "fill", "copy", "acc", "embed", "fm0",
+                               "fm1"]:
+        assert bits_equal(ar.get(gpu, name), ar.get(cpu, name)), name
+    for name in list(approx) + ["fm2", "fm3"]:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= TOL, f"{name}: {e:.3g}"
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (37, 300), (64, 768), (9, 2048)])
+def test_norms(hip, orc, backend, rows, cols):
+    from tests.plan_ops import ins
+    r = rng(rows * cols)
+    X = (r.standard_normal((rows, cols)) * 2 + 0.5).astype(np.float32)
+    dY = r.standard_normal((rows, cols)).astype(np.float32)
+    g = r.standard_normal(cols).astype(np.float32)
+    b = r.standard_normal(cols).astype(np.float32)
+    ar = Arena()
+    rx, rdy, rg, rb = ar.add("x", X), ar.add("dy", dY), ar.add("g", g), ar.add("b", b)
+    y, mean, rstd = ar.empty("y", X.shape), ar.empty("mean", (rows,)), ar.empty("rstd", (rows,))
+    dx = ar.empty("dx", X.shape)
+    ry, rrs, rdx = ar.empty("ry", X.shape), ar.empty("rrs", (rows,)), ar.empty("rdx", X.shape)
+    rc = (rows << 32) | cols
+    prog = [ins(26, [rx, rg, rb, y], [rc, mean, rstd]),
+            ins(27, [rdy, rx, rg, dx], [mean, rstd, rc]),
+            ins(31, [rx, rg, ry, rrs], [rc], imm=f32_bits(1e-6)),
+            ins(32, [rdy, rx, rg, rdx], [rrs, rc])]
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    for name in ["y", "mean", "rstd", "dx", "ry", "rrs", "rdx"]:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= TOL, f"{name}: {e:.3g}"
+
+
+def test_rope(hip, orc, backend):
+    from tests.plan_ops import ins
+    B, S, H, d = 2, 33, 3, 16
+    r = rng(9)
+    x = r.standard_normal((B * S, H * d)).astype(np.float32)
+    ar = Arena()
+    rx = ar.add("x", x)
+    tab = ar.empty("tab", (S, d // 2, 2))
+    outs = {k: ar.empty(k, x.shape) for k in ["f", "b", "ft", "bt"]}
+    base = f32_bits(10000.0)
+    g0, g1 = (B << 32) | S, (H << 32) | d
+    prog = [ins(45, [tab], [(S << 32) | d, base]),
+            ins(33, [rx, outs["f"], NULL], [g0, g1, base]),
+            ins(34, [rx, outs["b"], NULL], [g0, g1, base]),
+            ins(33, [rx, outs["ft"], tab], [g0, g1, base]),
+            ins(34, [rx, outs["bt"], tab], [g0, g1, base])]
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    for name in ["tab", "f", "b", "ft", "bt"]:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= TOL, f"{name}: {e:.3g}"
+
+
+# --- losses ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,C", [(1, 1), (2, 4), (32, 256), (300, 1000), (64, 32000),
+                                 (4, 40000)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_xent(hip, orc, backend, N, C, masked):
+    from tests.plan_ops import ins
+    r = rng(N * C + masked)
+    logits = (r.standard_normal((N, C)) * 3).astype(np.float32)
+    labels = r.integers(0, C, N).astype(np.int32)
+    if masked:
+        labels[::3] = -1
+    ar = Arena()
+    rl, ry = ar.add("logits", logits), ar.add("labels", labels)
+    loss, probs = ar.empty("loss", (1,)), ar.empty("probs", (N, C))
+    seed, dl = ar.add("seed", np.array([1.0], np.float32)), ar.empty("dl", (N, C))
+    fwd, bwd = (51, 52) if masked else (11, 12)
+    prog = [ins(fwd, [rl, ry, loss, probs], [N, C]), ins(bwd, [probs, ry, seed, dl], [N, C])]
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    for name in ["loss", "probs", "dl"]:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= TOL, f"{name}: {e:.3g}"
+
+
+# --- optimizer -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 2048, 100003])
+def test_adamw_is_bit_exact(hip, orc, backend, n):
+    from tests.plan_ops import ins
+    r = rng(n)
+    p = r.standard_normal(n).astype(np.float32)
+    g = (r.standard_normal(n) * 1e-2).astype(np.float32)
+    m = (r.standard_normal(n) * 1e-3).astype(np.float32)
+    v = np.abs(r.standard_normal(n) * 1e-5).astype(np.float32)
+    ar = Arena()
+    rp, rg, rm, rv = ar.add("p", p), ar.add("g", g), ar.add("m", m), ar.add("v", v)
+    cpu, gpu = execute(hip, orc, backend, ar, [ins(18, [rp, rg, rm, rv], [n, 0])])
+    for name in ["p", "m", "v"]:
+        assert bits_equal(ar.get(gpu, name), ar.get(cpu, name)), name
+
+
+def test_adamw_fused_clip_and_global_clip(hip, orc, backend):
+    from tests.plan_ops import ins
+    r = rng(77)
+    n = 70001
+    p, g = r.standard_normal(n).astype(np.float32), r.standard_normal(n).astype(np.float32)
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    g2 = r.standard_normal(5000).astype(np.float32)
+    ar = Arena()
+    rp, rg, rm, rv = ar.add("p", p), ar.add("g", g), ar.add("m", m), ar.add("v", v)
+    rg2, racc = ar.add("g2", g2), ar.add("acc", np.zeros(1, np.float32))
+    rg3 = ar.add("g3", g2.copy())
+    prog = [ins(18, [rp, rg, rm, rv], [n, f32_bits(1.0)]),      # fused clip
+            ins(53, [rg2, racc], [5000]), ins(53, [rg, racc], [n]),
+            ins(54, [rg2, racc, f32_bits(0.5)], [5000]),
+            ins(28, [rg3, f32_bits(2.0)], [5000])]
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    for name in ["p", "m", "v", "acc", "g2", "g3"]:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= 1e-6, f"{name}: {e:.3g}"
+
+
+def test_non_finite_norm_is_refused_untouched(hip, orc, backend):
+    from tests.plan_ops import ins
+    n = 1000
+    p = np.ones(n, np.float32)
+    g = np.ones(n, np.float32)
+    g[17] = np.nan
+    ar = Arena()
+    rp, rg = ar.add("p", p), ar.add("g", g)
+    rm, rv = ar.add("m", np.zeros(n, np.float32)), ar.add("v", np.zeros(n, np.float32))
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.Execute(ins(18, [rp, rg, rm, rv], [n, f32_bits(1.0)]), hip.StepParams(1e-3, 0.9, 0.999, 1e-8, 0.0, 0, 1))
+    with pytest.raises(hip.BackendError) as err:
+        backend.Flush()
+    assert str(err.value) == hip.NON_FINITE_NORM_REFUSAL
+    out = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert bits_equal(ar.get(out, "p"), p) and not ar.get(out, "m").any()
+    backend.Flush()  # the verdict is reported once
+
+
+def test_bad_clip_threshold_is_refused(hip, backend):
+    from tests.plan_ops import ins
+    ar = Arena()
+    rg = ar.add("g", np.ones(10, np.float32))
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    with pytest.raises(hip.BackendError) as err:
+        backend.Execute(ins(28, [rg, f32_bits(float("inf"))], [10]))
+    assert str(err.value) == hip.CLIP_THRESHOLD_REFUSAL
+
+
+# --- attention ---------------------------------------------------------------------------------
+
+ATTN_SHAPES = [(1, 1, 1, 64), (2, 67, 2, 64), (1, 130, 3, 128), (2, 33, 2, 16), (1, 9, 2, 4)]
+
+
+@pytest.mark.parametrize("B,S,H,d", ATTN_SHAPES)
+@pytest.mark.parametrize("seg", [False, True])
+@pytest.mark.parametrize("relaxed", [False, True])
+def test_attention_tiled(hip, orc, backend, B, S, H, d, seg, relaxed):
+    from tests.plan_ops import ins
+    r = rng(B * 1000 + S * 10 + H + d + 7 * seg)
+    shape = (B * S, H * d)
+    q, k, v, do = (r.standard_normal(shape).astype(np.float32) for _ in range(4))
+    ar = Arena()
+    rq, rk, rv, rdo = ar.add("q", q), ar.add("k", k), ar.add("v", v), ar.add("do", do)
+    o, st = ar.empty("o", shape), ar.empty("stats", (B * H * S, 4))
+    dq, dk, dv = ar.empty("dq", shape), ar.empty("dk", shape), ar.empty("dv", shape)
+    flags = (1 << 5) if relaxed else 0
+    prog = []
+    if seg:
+        toks = r.integers(0, 4, B * S).astype(np.int32)
+        rt, rs = ar.add("toks", toks), ar.empty("starts", (B * S,), np.int32)
+        prog.append(ins(55, [rt, rs], [(B << 32) | S, 3]))
+        geo = (B << 48) | (S << 32) | (H << 16) | d
+        prog.append(ins(57, [rq, rk, rv, o], [st, geo, rs], flags=flags))
+    else:
+        prog.append(ins(47, [rq, rk, rv, o], [st, (B << 32) | S, (H << 32) | d], flags=flags))
+    geo = (B << 48) | (S << 32) | (H << 16) | d
+    prog += [ins(48, [rq, rk, rv, rdo], [st, dq, geo], flags=flags),
+             ins(49, [rq, rk, rv, rdo], [st, dk, geo], flags=flags),
+             ins(50, [rq, rk, rv, rdo], [st, dv, geo], flags=flags)]
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    tol = TOL_BF16 if relaxed and d in (64, 128) else TOL
+    for name in ["o", "dq", "dk", "dv"]:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= tol, f"{name}: {e:.3g}"
+    sg, sc = ar.get(gpu, "stats"), ar.get(cpu, "stats")
+    assert bits_equal(sg[:, 3], sc[:, 3]), "document starts"
+    for col in range(3):
+        e = maxrel(sg[:, col], sc[:, col])
+        assert e <= tol, f"stats[{col}]: {e:.3g}"
+
+
+@pytest.mark.parametrize("B,S,H,d", [(1, 1, 1, 8), (2, 19, 2, 16), (1, 64, 2, 64)])
+def test_attention_cached_family(hip, orc, backend, B, S, H, d):
+    from tests.plan_ops import ins
+    r = rng(S * d + B)
+    shape = (B * S, H * d)
+    q, k, v, do = (r.standard_normal(shape).astype(np.float32) for _ in range(4))
+    ar = Arena()
+    rq, rk, rv, rdo = ar.add("q", q), ar.add("k", k), ar.add("v", v), ar.add("do", do)
+    o, P = ar.empty("o", shape), ar.empty("P", (B * H * S, S))
+    dP, dS = ar.empty("dP", (B * H * S, S)), ar.empty("dS", (B * H * S, S))
+    dq, dk, dv = ar.empty("dq", shape), ar.empty("dk", shape), ar.empty("dv", shape)
+    g0, g1 = (B << 32) | S, (H << 32) | d
+    prog = [ins(35, [rq, rk, rv, o], [P, g0, g1]), ins(36, [rdo, rv, dP], [g0, g1]),
+            ins(37, [P, rdo, dv], [g0, g1]), ins(38, [P, dP, dS], [(B * H * S << 32) | S]),
+            ins(39, [dS, rk, dq], [g0, g1]), ins(40, [dS, rq, dk], [g0, g1])]
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    for name in ["o", "P", "dP", "dS", "dq", "dk", "dv"]:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= TOL, f"{name}: {e:.3g}"
+
+
+# --- W8A8 and argmax through the op-family entry points --------------------------------------
+
+@pytest.mark.parametrize("M,N,K", [(5, 9, 7), (67, 129, 48), (32, 4096, 1024), (48, 200, 512),
+                                   (256, 512, 1024), (300, 260, 272), (2048, 2304, 512)])
+def test_w8a8_bit_exact(hip, orc, torch_cuda, M, N, K):
+    torch = torch_cuda
+    r = rng(M + N + K)
+    X = r.standard_normal((M, K)).astype(np.float32)
+    X[0, :] = 0.0  # an all-zero row takes scale 1
+    W = (r.standard_normal((K, N)) * 0.02).astype(np.float32)
+    QA_c, sa_c = orc.quantize_rows(X)
+    QW_c, sw_c = orc.quantize_cols(W)
+    acc_c, C_c = orc.gemm_w8a8(QA_c, sa_c, QW_c, sw_c)
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    dX, dW = torch.from_numpy(X).cuda(), torch.from_numpy(W).cuda()
+    QA = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    sa = torch.empty(M, dtype=torch.float32, device="cuda")
+    QWt = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    sw = torch.empty(N, dtype=torch.float32, device="cuda")
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    ctx.call("seeai_w8a8_quantize_rows", dX.data_ptr(), QA.data_ptr(), sa.data_ptr(), M, K)
+    ctx.call("seeai_w8a8_pack_weights", dW.data_ptr(), QWt.data_ptr(), sw.data_ptr(), K, N)
+    ctx.call("seeai_w8a8_gemm", QA.data_ptr(), sa.data_ptr(), QWt.data_ptr(), sw.data_ptr(),
+             C.data_ptr(), acc.data_ptr(), M, N, K)
+    torch.cuda.synchronize()
+    assert bits_equal(QA.cpu().numpy(), QA_c) and bits_equal(sa.cpu().numpy(), sa_c)
+    assert bits_equal(QWt.cpu().numpy(), np.ascontiguousarray(QW_c.T))
+    assert bits_equal(sw.cpu().numpy(), sw_c)
+    assert bits_equal(acc.cpu().numpy(), acc_c), "int32 accumulators"
+    assert bits_equal(C.cpu().numpy(), C_c), "dequantized output"
+    ctx.close()
+
+
+def test_argmax_first_max_wins(hip, orc, torch_cuda):
+    torch = torch_cuda
+    r = rng(3)
+    P = r.integers(0, 5, (300, 777)).astype(np.float32)  # many ties
+    P[5, :] = np.nan
+    P[6, 3] = np.nan
+    P[7, 0] = np.nan
+    want = orc.argmax_rows(P)
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    dP = torch.from_numpy(P).cuda()
+    out = torch.empty(300, dtype=torch.int32, device="cuda")
+    ctx.call("seeai_argmax_rows", dP.data_ptr(), 300, 777, out.data_ptr())
+    torch.cuda.synchronize()
+    assert bits_equal(out.cpu().numpy(), want)
+    ctx.close()
