@@ -296,7 +296,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
     case 11:
     case 51: {  // SoftmaxXEntFwd (+masked)
       void* ws;
-      if (int rc = Scratch(c, 8 * ins.out[0] + 64, &ws)) return rc;
+      if (int rc = Scratch(c, XEntFwdScratchBytes(ins.out[0]), &ws)) return rc;
       SEEAI_TRY(c,
                 LaunchXEntFwd(R.f(ins.in[0]), R.i32(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
                               ins.out[0], ins.out[1], ins.opcode == 51, ws, s),
@@ -798,7 +798,7 @@ int seeai_xent_fwd(seeai_ctx* c, const float* logits, const int32_t* labels, flo
                    float* probs, uint64_t N, uint64_t C, int masked) {
   if (!c) return SEEAI_INVALID;
   void* ws;
-  if (int rc = Scratch(c, 8 * N + 64, &ws)) return rc;
+  if (int rc = Scratch(c, XEntFwdScratchBytes(N), &ws)) return rc;
   SEEAI_TRY(c, LaunchXEntFwd(logits, labels, loss, probs, N, C, masked, ws, c->stream), "xent_fwd");
   return SEEAI_OK;
 }

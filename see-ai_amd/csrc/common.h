@@ -168,7 +168,9 @@ hipError_t LaunchSegmentStarts(const int32_t* tokens, int32_t* starts, size_t B,
 hipError_t LaunchArgmaxRows(const float* probs, size_t rows, size_t cols, int32_t* out,
                             hipStream_t s);
 
-// Loss family (k_loss.hip).  ws: 8 * rows bytes.
+// Loss family (k_loss.hip).  ws: XEntFwdScratchBytes(rows) for the forward,
+// 64 bytes for the backward.
+size_t XEntFwdScratchBytes(size_t rows);
 hipError_t LaunchXEntFwd(const float* logits, const int32_t* labels, float* loss, float* probs,
                          size_t N, size_t C, int masked, void* ws, hipStream_t s);
 hipError_t LaunchXEntBwd(const float* probs, const int32_t* labels, const float* seed,

@@ -1,12 +1,12 @@
 // k_loss.hip -- softmax cross-entropy forward / backward (and the masked
 // pair) on gfx950 (runtime/executor/loss.cc:21-126).
 //
-// Forward: one 1024-lane workgroup per row holds the row in registers (up
-// to 32 floats a lane, so a 32k vocabulary is read from HBM exactly once),
-// reduces the max and the exp-sum in a fixed butterfly order, writes the
-// probabilities once, and leaves the row's -log p[label] as a double.  A
-// second one-workgroup kernel sums those doubles in a fixed tree and writes
-// the f32 mean into the loss slot -- deterministic at any grid, no atomics.
+// Forward, four kernels: the row max; the exp-sum in the reference's own
+// association (a serial f32 chain per row, fed by a parallel exp pass -- at
+// a 32k vocabulary a tree sum differs from the reference's chain by more
+// than the 1e-5 parity bar); the probabilities with each row's
+// -log p[label] as a double; and a one-workgroup kernel summing those
+// doubles in a fixed tree into the f32 mean -- deterministic, no atomics.
 // Backward: scale = seed / N (or / T) divided on the device exactly as the
 // reference divides it, then one coalesced pass.
 #include "common.h"
@@ -14,71 +14,83 @@
 namespace seeai {
 namespace {
 
-constexpr int kRowThreads = 1024;
-constexpr int kPerLane = 32;  // register-resident row up to 32768 classes
+// --- pass 1: row max (order-free: fmax ignores NaN as std::fmax does) ------
+constexpr int kMaxThreads = 256;
 
-__global__ void __launch_bounds__(kRowThreads)
-XEntFwdRowKernel(const float* __restrict__ logits, const int32_t* __restrict__ labels,
-                 float* __restrict__ probs, double* __restrict__ row_loss, size_t C, int masked) {
-  __shared__ float redf[kRowThreads / kWave];
+__global__ void __launch_bounds__(kMaxThreads)
+XEntRowMaxKernel(const float* __restrict__ logits, float* __restrict__ row_max, size_t C) {
+  __shared__ float red[kMaxThreads / kWave];
+  const float* x = logits + static_cast<size_t>(blockIdx.x) * C;
+  float mx = NAN;  // the identity of fmax
+  for (size_t c = threadIdx.x; c < C; c += kMaxThreads) mx = fmaxf(mx, x[c]);
+  mx = BlockMaxF<kMaxThreads>(mx, red);
+  if (threadIdx.x == 0) row_max[blockIdx.x] = mx;
+}
+
+// --- pass 2: the exp-sum in the reference's order ------------------------------
+// loss.cc:24-29 sums exp(x - max) in f32, column by column, one chain per
+// row.  That association is reproduced exactly: all 256 lanes of a
+// workgroup evaluate exp over a 16-row x 256-column tile into LDS (double
+// buffered), and lane r of wave 0 then adds its row's 256 values in column
+// order.  The chain is serial by definition; the exps around it are not.
+constexpr int kSumThreads = 256;
+constexpr int kSumRows = 16;
+constexpr int kTileCols = 256;
+
+__global__ void __launch_bounds__(kSumThreads)
+XEntSerialSumKernel(const float* __restrict__ logits, const float* __restrict__ row_max,
+                    float* __restrict__ row_sum, size_t N, size_t C) {
+  __shared__ float tile[2][kSumRows][kTileCols + 1];
+  const size_t r0 = static_cast<size_t>(blockIdx.x) * kSumRows;
+  const int t = threadIdx.x;
+  const size_t ntiles = (C + kTileCols - 1) / kTileCols;
+  float mx[kSumRows];
+#pragma unroll
+  for (int r = 0; r < kSumRows; ++r) mx[r] = r0 + r < N ? row_max[r0 + r] : 0.0f;
+  auto fill = [&](size_t k, int buf) {
+    const size_t c = k * kTileCols + t;
+#pragma unroll
+    for (int r = 0; r < kSumRows; ++r) {
+      float e = 0.0f;
+      if (r0 + r < N && c < C) e = expf(logits[(r0 + r) * C + c] - mx[r]);
+      tile[buf][r][t] = e;
+    }
+  };
+  fill(0, 0);
+  __syncthreads();
+  float sum = 0.0f;
+  for (size_t k = 0; k < ntiles; ++k) {
+    if (k + 1 < ntiles) fill(k + 1, (k + 1) & 1);
+    if (t < kSumRows) {
+      const float* row = tile[k & 1][t];
+      const size_t w = k + 1 < ntiles ? kTileCols : C - k * kTileCols;
+      for (size_t j = 0; j < w; ++j) sum += row[j];
+    }
+    __syncthreads();
+  }
+  if (t < kSumRows && r0 + t < N) row_sum[r0 + t] = sum;
+}
+
+// --- pass 3: probabilities and the label term ----------------------------------
+constexpr int kProbThreads = 256;
+
+__global__ void __launch_bounds__(kProbThreads)
+XEntProbsKernel(const float* __restrict__ logits, const int32_t* __restrict__ labels,
+                const float* __restrict__ row_max, const float* __restrict__ row_sum,
+                float* __restrict__ probs, double* __restrict__ row_loss, size_t C, int masked) {
   const size_t r = blockIdx.x;
   const float* x = logits + r * C;
   float* p = probs + r * C;
-  const bool resident = C <= static_cast<size_t>(kRowThreads) * kPerLane;
-  float v[kPerLane];
-  float mx = -INFINITY;
-  bool any = false;
-  if (resident) {
-#pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-      const size_t c = threadIdx.x + static_cast<size_t>(i) * kRowThreads;
-      v[i] = c < C ? x[c] : -INFINITY;
-      if (c < C) {
-        mx = any ? fmaxf(mx, v[i]) : v[i];
-        any = true;
-      }
-    }
-  } else {
-    for (size_t c = threadIdx.x; c < C; c += kRowThreads) {
-      mx = any ? fmaxf(mx, x[c]) : x[c];
-      any = true;
-    }
-  }
-  // fmax ignores NaN exactly as the reference's std::fmax chain does.
-  if (!any) mx = NAN;  // no element on this lane: the identity of fmax
-  mx = BlockMaxF<kRowThreads>(mx, redf);
-  float sum = 0.0f;
-  if (resident) {
-#pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-      const size_t c = threadIdx.x + static_cast<size_t>(i) * kRowThreads;
-      if (c < C) {
-        v[i] = expf(v[i] - mx);
-        sum += v[i];
-      }
-    }
-  } else {
-    for (size_t c = threadIdx.x; c < C; c += kRowThreads) sum += expf(x[c] - mx);
-  }
-  sum = BlockSumF<kRowThreads>(sum, redf);
-  const float inv_sum = 1.0f / sum;
-  if (resident) {
-#pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-      const size_t c = threadIdx.x + static_cast<size_t>(i) * kRowThreads;
-      if (c < C) p[c] = v[i] * inv_sum;
-    }
-  } else {
-    for (size_t c = threadIdx.x; c < C; c += kRowThreads) p[c] = expf(x[c] - mx) * inv_sum;
-  }
+  const float mx = row_max[r];
+  const float inv_sum = 1.0f / row_sum[r];  // loss.cc:30
+  for (size_t c = threadIdx.x; c < C; c += kProbThreads) p[c] = expf(x[c] - mx) * inv_sum;
   if (threadIdx.x == 0) {
     const int32_t lab = labels[r];
     double term = 0.0;
     if (!(masked && lab < 0)) {
-      // The label's probability as this workgroup computed and stored it;
-      // NaN propagates, the clamp only rescues underflow (loss.cc:45-51).
-      const size_t c = static_cast<size_t>(lab);
-      const float pl = expf(x[c] - mx) * inv_sum;
+      // The label's probability exactly as stored; NaN propagates, the
+      // clamp only rescues underflow (loss.cc:45-51).
+      const float pl = expf(x[static_cast<size_t>(lab)] - mx) * inv_sum;
       const double safe = pl != pl ? static_cast<double>(pl) : static_cast<double>(fmaxf(pl, 1e-12f));
       term = -log(safe);
     }
@@ -147,12 +159,20 @@ XEntBwdKernel(const float* __restrict__ probs, const int32_t* __restrict__ label
 
 }  // namespace
 
+size_t XEntFwdScratchBytes(size_t N) { return N * (8 + 4 + 4) + 256; }
+
 hipError_t LaunchXEntFwd(const float* logits, const int32_t* labels, float* loss, float* probs,
                          size_t N, size_t C, int masked, void* ws, hipStream_t s) {
   if (N == 0) return hipSuccess;
   double* row_loss = static_cast<double*>(ws);
-  hipLaunchKernelGGL(XEntFwdRowKernel, dim3(static_cast<unsigned>(N)), dim3(kRowThreads), 0, s,
-                     logits, labels, probs, row_loss, C, masked);
+  float* row_max = reinterpret_cast<float*>(row_loss + N);
+  float* row_sum = row_max + N;
+  const unsigned rows = static_cast<unsigned>(N);
+  hipLaunchKernelGGL(XEntRowMaxKernel, dim3(rows), dim3(kMaxThreads), 0, s, logits, row_max, C);
+  hipLaunchKernelGGL(XEntSerialSumKernel, dim3(static_cast<unsigned>((N + kSumRows - 1) / kSumRows)),
+                     dim3(kSumThreads), 0, s, logits, row_max, row_sum, N, C);
+  hipLaunchKernelGGL(XEntProbsKernel, dim3(rows), dim3(kProbThreads), 0, s, logits, labels, row_max,
+                     row_sum, probs, row_loss, C, masked);
   hipLaunchKernelGGL(XEntFinishKernel, dim3(1), dim3(1024), 0, s, row_loss, labels, loss, N, masked);
   return hipGetLastError();
 }

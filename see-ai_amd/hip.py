@@ -21,6 +21,15 @@ import struct
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libseeai_hip.so")
 
+# torch wheels ship their own libamdhip64.so.7 under the same SONAME as
+# ROCm's; whichever loads first serves the whole process.  Load torch's
+# first (when torch is installed) so the library and torch share one HIP
+# runtime -- loading ours first leaves torch without a usable device.
+try:  # noqa: SIM105
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 if not os.path.exists(LIB_PATH):
     raise ImportError(
         f"{LIB_PATH} is not built: run __graft_entry__.build() (hipcc, gfx950)")
