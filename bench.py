@@ -1,0 +1,287 @@
+"""Benchmark of the gfx950 executor's hot path (one MI355X).
+
+Workload: the W8A8 GEMM -- activations f32
+[4096, 4096] ~ N(0,1) quantized per row to int8, weights [4096, 4096]
+~ N(0, 0.02) quantized per output channel (packed once, frozen), int32
+accumulation, f32 dequant.  One step = quantize the activations + the int8
+GEMM with its dequant epilogue, inputs resident in HBM.  ``value`` is the
+whole job's throughput in int8 tera-ops per second (2*M*N*K per step).
+
+The JSON line also carries:
+  roofline      the dominant kernel (the int8 MFMA GEMM): algorithmic ops
+                per launch / its mean launch time measured here with HIP
+                events on the stream it runs on, against MI355X's dense int8
+                peak (5.0 POP/s); traffic from profiles/ when measured;
+  cpu_baseline  the oracle's W8A8 (scalar C, 1 thread) timed on this host on
+                a bounded row sample of the same GEMM;
+  extra         the decode-shaped GEMM (M = 32), causal attention fwd+bwd at
+                BASELINE config 3, softmax-xent and AdamW, each with its
+                roofline fraction.
+
+--gpus N with N > 1 exits: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8, POP/s x 1000
+PEAK_BF16_TFLOPS = 2500.0    # dense bf16
+PEAK_FP32_TFLOPS = 157.3     # fp32 MFMA
+PEAK_HBM_GBS = 8000.0        # HBM3E
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
+    p.add_argument("--pmc-probe", action="store_true",
+                   help="for rocprofv3 --pmc runs: one W8A8 step plus a 256 MiB device copy "
+                        "(the counter calibration: a copy's known bytes)")
+    return p.parse_args()
+
+
+def pmc_probe():
+    """One quantize + GEMM at the bench shape, then a plain 256 MiB copy whose
+    FETCH_SIZE / WRITE_SIZE readings calibrate the counters' byte scale."""
+    import torch
+    hip = importlib.import_module("see-ai_amd.hip")
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    M = N = K = 4096
+    X = torch.randn((M, K), device="cuda")
+    W = torch.randn((K, N), device="cuda") * 0.02
+    QA = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    sa = torch.empty(M, device="cuda")
+    QWt = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    sw = torch.empty(N, device="cuda")
+    C = torch.empty((M, N), device="cuda")
+    ctx.call("seeai_w8a8_pack_weights", W.data_ptr(), QWt.data_ptr(), sw.data_ptr(), K, N)
+    for _ in range(3):
+        ctx.call("seeai_w8a8_quantize_rows", X.data_ptr(), QA.data_ptr(), sa.data_ptr(), M, K)
+        ctx.call("seeai_w8a8_gemm", QA.data_ptr(), sa.data_ptr(), QWt.data_ptr(), sw.data_ptr(),
+                 C.data_ptr(), None, M, N, K)
+    src = torch.empty(64 * 1024 * 1024, device="cuda")  # 256 MiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ctx.close()
+    print("pmc probe: 3 x (quantize 4096x4096 + W8A8 GEMM 4096^3), 3 x copy 256 MiB", flush=True)
+    return 0
+
+
+def load_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get(name)
+
+
+def main():
+    args = parse()
+    if args.pmc_probe:
+        return pmc_probe()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              "(the path shards by GEMM column blocks / attention (b, h) -- see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+
+    hip = importlib.import_module("see-ai_amd.hip")
+    torch.cuda.set_device(0)
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+
+    M = N = K = 4096
+    g = torch.Generator(device="cuda").manual_seed(20261201)
+    X = torch.randn((M, K), device="cuda", generator=g)
+    W = torch.randn((K, N), device="cuda", generator=g) * 0.02
+    QA = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    sa = torch.empty(M, dtype=torch.float32, device="cuda")
+    QWt = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    sw = torch.empty(N, dtype=torch.float32, device="cuda")
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ctx.call("seeai_w8a8_pack_weights", W.data_ptr(), QWt.data_ptr(), sw.data_ptr(), K, N)
+
+    def quantize():
+        ctx.call("seeai_w8a8_quantize_rows", X.data_ptr(), QA.data_ptr(), sa.data_ptr(), M, K)
+
+    def gemm():
+        ctx.call("seeai_w8a8_gemm", QA.data_ptr(), sa.data_ptr(), QWt.data_ptr(), sw.data_ptr(),
+                 C.data_ptr(), None, M, N, K)
+
+    for _ in range(args.warmup):
+        quantize()
+        gemm()
+    torch.cuda.synchronize()
+    # Per-step events around the GEMM launch (same stream: torch's current).
+    g_start = [ev() for _ in range(args.steps)]
+    g_end = [ev() for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        quantize()
+        g_start[i].record()
+        gemm()
+        g_end[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gemm_ms = sum(a.elapsed_time(b) for a, b in zip(g_start, g_end)) / args.steps
+    ms_per_step = wall * 1000.0 / args.steps
+    ops = 2.0 * M * N * K
+    value = ops / (ms_per_step * 1e-3) / 1e12
+    achieved = ops / (gemm_ms * 1e-3) / 1e12
+
+    line = {
+        "metric": "int8 GEMM TOPS + LoRA train-step tokens/s on 1 MI355X; % of MFMA/HBM roofline",
+        "value": round(value, 2),
+        "unit": "TOPS (int8, quantize + GEMM + dequant per step)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 (int32 accumulate, f32 dequant)",
+        "data": "synthetic: X ~ N(0,1), W ~ N(0,0.02), seeded on device",
+        "config": {"workload": "W8A8 GEMM M=4096 K=4096 N=4096 (BASELINE configs[1])",
+                   "M": M, "N": N, "K": K, "parallelism": "single GPU"},
+        "roofline": {
+            "kernel": "GemmI8TileKernel<256,256,64>",
+            "bound": "mfma",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TFLOP/s",
+            "op": "int8 multiply-accumulate counted as 2 ops",
+            "frac": round(achieved / PEAK_INT8_TOPS, 4),
+            "algorithmic_per_launch": ops,
+            "kernel_ms": round(gemm_ms, 5),
+            "traffic": load_traffic("w8a8_4096"),
+        },
+    }
+
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(M, N, K)
+    if not args.no_extra:
+        line["extra"] = extras(ctx, torch, hip)
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    return 0
+
+
+def cpu_baseline(M, N, K):
+    """The oracle's W8A8 (quantize + int32 GEMM + dequant) on a row sample."""
+    import numpy as np
+    from oracle.oracle import oracle
+    orc = oracle()
+    rows = 1024
+    r = np.random.default_rng(1)
+    X = r.standard_normal((rows, K)).astype(np.float32)
+    W = (r.standard_normal((K, N)) * 0.02).astype(np.float32)
+    QW, sw = orc.quantize_cols(W)  # weights are packed once, outside the step
+    t0 = time.perf_counter()
+    QA, sa = orc.quantize_rows(X)
+    orc.gemm_w8a8(QA, sa, QW, sw)
+    dt = time.perf_counter() - t0
+    return {"value": round(2.0 * rows * N * K / dt / 1e12, 5), "unit": "TOPS", "cores": 1,
+            "kind": "port",
+            "sample": f"{rows} of the {M} activation rows (quantize + int32 GEMM + dequant "
+                      f"against all {N}x{K} weights), {dt:.2f} s on one host core"}
+
+
+def extras(ctx, torch, hip):
+    out = {}
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+
+    def timed(fn, iters, warm=2):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        a, b = ev(), ev()
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters
+
+    # Decode-shaped W8A8: HBM-bound on the weight stream.
+    M, N, K = 32, 4096, 4096
+    QA = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda")
+    QW = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda")
+    sa, sw = torch.rand(M, device="cuda"), torch.rand(N, device="cuda")
+    C = torch.empty((M, N), device="cuda")
+    ms = timed(lambda: ctx.call("seeai_w8a8_gemm", QA.data_ptr(), sa.data_ptr(), QW.data_ptr(),
+                                sw.data_ptr(), C.data_ptr(), None, M, N, K), 200)
+    alg_bytes = M * K + N * K + 4 * M * N + 4 * (M + N)
+    out["w8a8_m32"] = {"ms": round(ms, 5), "TOPS": round(2 * M * N * K / ms / 1e9, 1),
+                       "GB_s": round(alg_bytes / ms / 1e6, 1),
+                       "hbm_frac": round(alg_bytes / ms / 1e6 / PEAK_HBM_GBS, 4)}
+
+    # Causal attention fwd+bwd, BASELINE config 3 (B16 H16 S2048 d64).
+    B, S, H, d = 16, 2048, 16, 64
+    flops = 412518187008.0  # causal-exact fwd + bwd
+    q, k, v, do = (torch.randn((B * S, H * d), device="cuda") for _ in range(4))
+    o, st = torch.empty_like(q), torch.empty((B * H * S, 4), device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    for dt, name in [(1, "attention_bf16"), (0, "attention_f32")]:
+        def step(dt=dt):
+            ctx.call("seeai_attn_fwd", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                     st.data_ptr(), B, S, H, d, None)
+            ctx.call("seeai_attn_dq", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                     st.data_ptr(), dq.data_ptr(), B, S, H, d)
+            ctx.call("seeai_attn_dk", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                     st.data_ptr(), dk.data_ptr(), B, S, H, d)
+            ctx.call("seeai_attn_dv", dt, q.data_ptr(), k.data_ptr(), do.data_ptr(), st.data_ptr(),
+                     dv.data_ptr(), B, S, H, d)
+        ms = timed(step, 3, 1)
+        tf = flops / ms / 1e9
+        peak = PEAK_BF16_TFLOPS if dt else PEAK_FP32_TFLOPS
+        out[name] = {"ms_fwd_bwd": round(ms, 3), "TFLOP_s": round(tf, 1),
+                     "mfma_frac": round(tf / peak, 4), "config": "B16 H16 S2048 d64 causal"}
+    del q, k, v, do, o, st, dq, dk, dv
+
+    # Softmax cross-entropy fwd at the decoders' 8192 x 32000 logits.
+    Nr, Cc = 8192, 32000
+    logits = torch.randn((Nr, Cc), device="cuda") * 3
+    labels = torch.randint(0, Cc, (Nr,), dtype=torch.int32, device="cuda")
+    probs = torch.empty_like(logits)
+    loss = torch.empty(1, device="cuda")
+    ms = timed(lambda: ctx.call("seeai_xent_fwd", logits.data_ptr(), labels.data_ptr(),
+                                loss.data_ptr(), probs.data_ptr(), Nr, Cc, 0), 10)
+    by = 2 * Nr * Cc * 4
+    out["xent_fwd_8192x32000"] = {"ms": round(ms, 4), "GB_s": round(by / ms / 1e6, 1),
+                                  "hbm_frac": round(by / ms / 1e6 / PEAK_HBM_GBS, 4)}
+    del logits, probs
+
+    # AdamW over config 5's 4,194,304 LoRA parameters (28 B/param).
+    n = 4194304
+    p, gr, m, vv = (torch.randn(n, device="cuda") for _ in range(4))
+    vv.abs_()
+    sp = hip.StepParams(1e-3, 0.9, 0.999, 1e-8, 0.01, 0, 3)
+    import ctypes
+    ms = timed(lambda: ctx.call("seeai_adamw_step", p.data_ptr(), gr.data_ptr(), m.data_ptr(),
+                                vv.data_ptr(), n, ctypes.byref(sp), ctypes.c_float(0.0)), 50)
+    by = 28 * n
+    out["adamw_4M"] = {"ms": round(ms, 4), "GB_s": round(by / ms / 1e6, 1),
+                       "hbm_frac": round(by / ms / 1e6 / PEAK_HBM_GBS, 4)}
+    return out
+
+
+if __name__ == "__main__":
+    sys.exit(main())
