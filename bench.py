@@ -162,7 +162,7 @@ def main():
         "config": {"workload": "W8A8 GEMM M=4096 K=4096 N=4096 (BASELINE configs[1])",
                    "M": M, "N": N, "K": K, "parallelism": "single GPU"},
         "roofline": {
-            "kernel": "GemmI8TileKernel<256,256,64>",
+            "kernel": "GemmI8TileKernel<256,256,128,4,4>",
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": PEAK_INT8_TOPS,

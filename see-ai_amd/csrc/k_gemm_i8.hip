@@ -14,12 +14,15 @@
 // QWt [N, K] (K contiguous: both MFMA operands then read 16 contiguous
 // bytes per lane).
 //
-// Large M: a 256 x 256 tile per 256-lane workgroup, four waves in 2 x 2,
-// each a 128 x 128 block of v_mfma_i32_32x32x32_i8 tiles (16 accumulators
-// of 16 int32 -- the compiler places them in AGPRs); K walks BK bytes at a
-// time through padded LDS rows (a 16-byte pad per row: the 16-byte lane
-// reads of a wave fall in distinct banks), the next K tile prefetched into
-// registers while the current one multiplies.
+// Large M: a 256 x 256 tile per 1024-lane workgroup, sixteen waves in 4 x 4,
+// each a 64 x 64 block of v_mfma_i32_32x32x32_i8 tiles (4 accumulators of
+// 16 int32; four waves per SIMD hide each other's LDS and memory latency --
+// measured faster than 8 waves of 128 x 64 and than 4 waves of 128 x 128,
+// which spills); K walks 128 bytes per step through two
+// padded LDS buffers (a 16-byte pad per row spreads a wave's 16-byte reads
+// over the banks), the next step's global loads in flight during the
+// current step's MFMAs; workgroups are ordered so each XCD's L2 serves a
+// compact block of tiles.
 // Small M (decode-like, M <= 64): one 16-column slice of C per workgroup,
 // its four waves each reducing a quarter of K on v_mfma_i32_16x16x64_i8
 // straight from global memory (each weight byte is read once), then summed
@@ -48,6 +51,18 @@ __device__ __forceinline__ int8_t QuantLevel(float x, float scale) {
 
 constexpr int kQThreads = 256;
 
+// One workgroup per row.  Rows up to kQThreads * 4 * kQRegs floats stay in
+// registers between the max pass and the level pass, so X is read from HBM
+// once; longer (or unaligned) rows are read twice.
+constexpr int kQRegs = 8;
+
+__device__ __forceinline__ uint32_t PackLevels(float4 v, float s) {
+  return static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.x, s))) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.y, s))) << 8) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.z, s))) << 16) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.w, s))) << 24);
+}
+
 __global__ void __launch_bounds__(kQThreads)
 QuantizeRowsKernel(const float* __restrict__ X, int8_t* __restrict__ Q, float* __restrict__ scale,
                    size_t cols) {
@@ -57,8 +72,18 @@ QuantizeRowsKernel(const float* __restrict__ X, int8_t* __restrict__ Q, float* _
   int8_t* q = Q + r * cols;
   const bool vec = (cols % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(q) & 3) == 0);
+  const bool resident = vec && cols <= static_cast<size_t>(kQThreads) * 4 * kQRegs;
   float mx = 0.0f;
-  if (vec) {
+  float4 keep[kQRegs];
+  if (resident) {
+#pragma unroll
+    for (int i = 0; i < kQRegs; ++i) {
+      const size_t c = (threadIdx.x + static_cast<size_t>(i) * kQThreads) * 4;
+      keep[i] = c < cols ? *reinterpret_cast<const float4*>(x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(keep[i].x), fabsf(keep[i].y)),
+                           fmaxf(fabsf(keep[i].z), fabsf(keep[i].w))));
+    }
+  } else if (vec) {
     for (size_t c = threadIdx.x * 4; c < cols; c += kQThreads * 4) {
       const float4 v = *reinterpret_cast<const float4*>(x + c);
       mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -69,15 +94,15 @@ QuantizeRowsKernel(const float* __restrict__ X, int8_t* __restrict__ Q, float* _
   mx = BlockMaxF<kQThreads>(mx, red);
   const float s = QuantScale(mx);
   if (threadIdx.x == 0) scale[r] = s;
-  if (vec) {
-    for (size_t c = threadIdx.x * 4; c < cols; c += kQThreads * 4) {
-      const float4 v = *reinterpret_cast<const float4*>(x + c);
-      const uint32_t packed = static_cast<uint8_t>(QuantLevel(v.x, s)) |
-                              (static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.y, s))) << 8) |
-                              (static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.z, s))) << 16) |
-                              (static_cast<uint32_t>(static_cast<uint8_t>(QuantLevel(v.w, s))) << 24);
-      *reinterpret_cast<uint32_t*>(q + c) = packed;
+  if (resident) {
+#pragma unroll
+    for (int i = 0; i < kQRegs; ++i) {
+      const size_t c = (threadIdx.x + static_cast<size_t>(i) * kQThreads) * 4;
+      if (c < cols) *reinterpret_cast<uint32_t*>(q + c) = PackLevels(keep[i], s);
     }
+  } else if (vec) {
+    for (size_t c = threadIdx.x * 4; c < cols; c += kQThreads * 4)
+      *reinterpret_cast<uint32_t*>(q + c) = PackLevels(*reinterpret_cast<const float4*>(x + c), s);
   } else {
     for (size_t c = threadIdx.x; c < cols; c += kQThreads) q[c] = QuantLevel(x[c], s);
   }
@@ -115,24 +140,58 @@ PackTransposeKernel(const float* __restrict__ W, const float* __restrict__ scale
 
 constexpr int kThreads = 256;
 
-template <int BM, int BN, int BK>
-__global__ void __launch_bounds__(kThreads)
+// Tile -> workgroup order.  The hardware deals workgroups round-robin over
+// the 8 XCDs (workgroup b runs on XCD b % 8), each with its own L2.  When
+// the tile count divides by 8, the tiles are renumbered so each XCD owns a
+// contiguous run, and the run walks column-major within bands of kGroupM
+// row tiles: an XCD's 32 concurrent tiles at 4096^2 share 4 row panels of A
+// and 8 column panels of W, so each k-slice of A and W leaves HBM once per
+// XCD instead of once per tile row or column.
+constexpr int kGroupM = 4;
+
+__device__ __forceinline__ void TileOf(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int ntiles = tiles_m * tiles_n;
+  int t = b;
+  if (ntiles % 8 == 0) t = (b % 8) * (ntiles / 8) + b / 8;
+  const int per_group = kGroupM * tiles_n;
+  const int g = t / per_group;
+  const int first_m = g * kGroupM;
+  const int rows = min(tiles_m - first_m, kGroupM);
+  const int off = t % per_group;
+  tm = first_m + off % rows;
+  tn = off / rows;
+}
+
+// BM x BN tile per workgroup of WGM x WGN waves, each wave a (BM/WGM) x
+// (BN/WGN) block of 32 x 32 x 32 int8 MFMAs.  K advances BK bytes per step
+// through two LDS buffers (rows padded by 16 bytes): the next step's global
+// loads are issued before the current step's MFMAs and land in the other
+// buffer after them, so one barrier per step orders both hazards.
+template <int BM, int BN, int BK, int WGM, int WGN>
+__global__ void __launch_bounds__(WGM * WGN * kWave)
 GemmI8TileKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
                  const int8_t* __restrict__ QW, const float* __restrict__ sw,
                  float* __restrict__ C, int32_t* __restrict__ acc_out, int M, int N, int K) {
+  constexpr int kT = WGM * WGN * kWave;        // lanes per workgroup
   constexpr int LDK = BK + 16;                 // padded LDS row stride (bytes)
-  constexpr int WM = BM / 2, WN = BN / 2;      // per-wave block
+  constexpr int WM = BM / WGM, WN = BN / WGN;  // per-wave block
   constexpr int TM = WM / 32, TN = WN / 32;    // 32 x 32 MFMA tiles per wave
   constexpr int kChunksRow = BK / 16;          // 16-byte chunks per tile row
-  constexpr int NA = BM * kChunksRow / kThreads;
-  constexpr int NB = BN * kChunksRow / kThreads;
-  __shared__ __attribute__((aligned(16))) int8_t As[BM * LDK];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[BN * LDK];
+  constexpr int NA = BM * kChunksRow / kT;
+  constexpr int NB = BN * kChunksRow / kT;
+  static_assert(NA * kT == BM * kChunksRow && NB * kT == BN * kChunksRow, "tile / lanes");
+  // One LDS block: two A buffers then two B buffers (rows padded by 16 B);
+  // the epilogue reuses all of it as per-wave staging.
+  __shared__ __attribute__((aligned(16))) int8_t smem[2 * (BM + BN) * LDK];
+  auto As = [&](int buf) { return smem + buf * (BM * LDK); };
+  auto Bs = [&](int buf) { return smem + 2 * BM * LDK + buf * (BN * LDK); };
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
-  const int wm = (wave / 2) * WM, wn = (wave % 2) * WN;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
+  int tm, tn;
+  TileOf(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
 
   v16i acc[TM][TN];
 #pragma unroll
@@ -146,7 +205,7 @@ GemmI8TileKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
   auto load = [&](int k0) {
 #pragma unroll
     for (int e = 0; e < NA; ++e) {
-      const int c = tid + e * kThreads;
+      const int c = tid + e * kT;
       const int row = c / kChunksRow, kc = c % kChunksRow;
       const int m = m0 + row, k = k0 + kc * 16;
       ra[e] = (m < M && k < K) ? *reinterpret_cast<const v4i*>(QA + static_cast<size_t>(m) * K + k)
@@ -154,68 +213,132 @@ GemmI8TileKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
     }
 #pragma unroll
     for (int e = 0; e < NB; ++e) {
-      const int c = tid + e * kThreads;
+      const int c = tid + e * kT;
       const int row = c / kChunksRow, kc = c % kChunksRow;
       const int n = n0 + row, k = k0 + kc * 16;
       rb[e] = (n < N && k < K) ? *reinterpret_cast<const v4i*>(QW + static_cast<size_t>(n) * K + k)
                                : v4i{0, 0, 0, 0};
     }
   };
-  auto store = [&]() {
+  auto store = [&](int buf) {
 #pragma unroll
     for (int e = 0; e < NA; ++e) {
-      const int c = tid + e * kThreads;
-      *reinterpret_cast<v4i*>(As + (c / kChunksRow) * LDK + (c % kChunksRow) * 16) = ra[e];
+      const int c = tid + e * kT;
+      *reinterpret_cast<v4i*>(As(buf) + (c / kChunksRow) * LDK + (c % kChunksRow) * 16) = ra[e];
     }
 #pragma unroll
     for (int e = 0; e < NB; ++e) {
-      const int c = tid + e * kThreads;
-      *reinterpret_cast<v4i*>(Bs + (c / kChunksRow) * LDK + (c % kChunksRow) * 16) = rb[e];
+      const int c = tid + e * kT;
+      *reinterpret_cast<v4i*>(Bs(buf) + (c / kChunksRow) * LDK + (c % kChunksRow) * 16) = rb[e];
     }
   };
 
+  const int nsteps = (K + BK - 1) / BK;
+  constexpr int KS = BK / 32;  // 32-byte k-steps per LDS buffer
+  v4i af[2][TM], bf[2][TN];
+  auto read_frags = [&](int buf, int ks, int slot) {
+    const int koff = ks * 32 + (lane / 32) * 16;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      af[slot][i] = *reinterpret_cast<const v4i*>(As(buf) + (wm + i * 32 + lane % 32) * LDK + koff);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      bf[slot][j] = *reinterpret_cast<const v4i*>(Bs(buf) + (wn + j * 32 + lane % 32) * LDK + koff);
+  };
   load(0);
-  for (int k0 = 0; k0 < K; k0 += BK) {
-    __syncthreads();
-    store();
-    __syncthreads();
-    if (k0 + BK < K) load(k0 + BK);
+  store(0);
+  __syncthreads();
+  for (int it = 0; it < nsteps; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < nsteps) load((it + 1) * BK);
+    // Fragments double-buffered in registers: the next k-step's LDS reads
+    // are in flight while the current k-step's MFMAs issue.
+    read_frags(buf, 0, 0);
 #pragma unroll
-    for (int ks = 0; ks < BK; ks += 32) {
-      v4i af[TM], bf[TN];
-      const int koff = ks + (lane / 32) * 16;
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const v4i*>(As + (wm + i * 32 + lane % 32) * LDK + koff);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const v4i*>(Bs + (wn + j * 32 + lane % 32) * LDK + koff);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) read_frags(buf, ks + 1, (ks + 1) & 1);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks & 1][i], bf[ks & 1][j],
+                                                            acc[i][j], 0, 0, 0);
     }
+    if (it + 1 < nsteps) store(buf ^ 1);
+    __syncthreads();
   }
 
-  // Lane holds column (lane % 32) and rows 8*(r/4) + 4*(lane/32) + r%4.
+  // Epilogue.  Lane holds column (lane % 32) and rows 8*(r/4) + 4*(lane/32)
+  // + r%4 of each 32 x 32 tile.  The dequantized tile goes through this
+  // wave's slice of LDS (free now: the loop ended on a barrier) so C leaves
+  // in row-contiguous 16-byte stores; the row scales are read once per
+  // 4-row group as float4.
+  if (acc_out) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn + j * 32 + lane % 32;
-      if (n >= N) continue;
-      const float swn = sw[n];
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-        if (m >= M) continue;
-        const size_t o = static_cast<size_t>(m) * N + n;
-        const int32_t v = acc[i][j][r];
-        if (acc_out) acc_out[o] = v;
-        C[o] = (static_cast<float>(v) * sa[m]) * swn;
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+          const int n = n0 + wn + j * 32 + lane % 32;
+          if (m < M && n < N) acc_out[static_cast<size_t>(m) * N + n] = acc[i][j][r];
+        }
+  }
+  constexpr int SLD = WN + 4;  // staging row stride (floats)
+  static_assert(WGM * WGN * 32 * SLD * 4 <= 2 * (BM + BN) * LDK, "staging fits in LDS");
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
+  const bool vec_out = (N % 4) == 0;
+  float swv[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn + j * 32 + lane % 32;
+    swv[j] = n < N ? sw[n] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int mb = m0 + wm + i * 32;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m4 = mb + 8 * q + 4 * (lane / 32);
+      float sav[4];
+      if (m4 + 3 < M && (M % 4) == 0) {
+        const float4 v = *reinterpret_cast<const float4*>(sa + m4);
+        sav[0] = v.x, sav[1] = v.y, sav[2] = v.z, sav[3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sav[e] = m4 + e < M ? sa[m4 + e] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = 8 * q + 4 * (lane / 32) + e;
+          stage[row * SLD + j * 32 + lane % 32] =
+              (static_cast<float>(acc[i][j][4 * q + e]) * sav[e]) * swv[j];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    constexpr int kVecRow = WN / 4;  // float4 per staged row
+#pragma unroll
+    for (int t = 0; t < 32 * kVecRow / kWave; ++t) {
+      const int idx = lane + t * kWave;
+      const int row = idx / kVecRow, c4 = idx % kVecRow;
+      const int m = mb + row, n = n0 + wn + c4 * 4;
+      const float4 v = *reinterpret_cast<const float4*>(stage + row * SLD + c4 * 4);
+      if (m >= M) continue;
+      float* dst = C + static_cast<size_t>(m) * N + n;
+      if (vec_out && n + 3 < N) {
+        *reinterpret_cast<float4*>(dst) = v;
+      } else {
+        if (n < N) dst[0] = v.x;
+        if (n + 1 < N) dst[1] = v.y;
+        if (n + 2 < N) dst[2] = v.z;
+        if (n + 3 < N) dst[3] = v.w;
       }
     }
+    __builtin_amdgcn_wave_barrier();
+  }
 }
 
 // --- the small-M GEMM (decode-like) ---------------------------------------------
@@ -329,21 +452,24 @@ hipError_t LaunchGemmW8A8(const int8_t* QA, const float* sa, const int8_t* QWt, 
     return hipGetLastError();
   }
   if (vec_ok) {
-    // Tile geometry: 256 x 256 once the grid still fills the chip, else
-    // 128 x 128.  SEEAI_I8_TILE=128|256 overrides (measurement sweeps).
+    // Tile geometry: 256 x 256 (16 waves of 64 x 64, four per SIMD) once the
+    // grid still fills the chip, else 128 x 128 (4 waves).  SEEAI_I8_TILE=128|256 overrides
+    // (measurement sweeps).
     static const int forced = [] {
       const char* e = std::getenv("SEEAI_I8_TILE");
       return e ? std::atoi(e) : 0;
     }();
     const bool big = forced ? forced == 256 : (M >= 2048 && N >= 2048);
     if (big) {
-      const dim3 grid(static_cast<unsigned>((N + 255) / 256), static_cast<unsigned>((M + 255) / 256));
-      hipLaunchKernelGGL((GemmI8TileKernel<256, 256, 64>), grid, dim3(kThreads), 0, s, QA, sa, QWt,
-                         sw, C, acc, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+      const unsigned tiles = static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256));
+      hipLaunchKernelGGL((GemmI8TileKernel<256, 256, 128, 4, 4>), dim3(tiles), dim3(1024), 0, s, QA,
+                         sa, QWt, sw, C, acc, static_cast<int>(M), static_cast<int>(N),
+                         static_cast<int>(K));
     } else {
-      const dim3 grid(static_cast<unsigned>((N + 127) / 128), static_cast<unsigned>((M + 127) / 128));
-      hipLaunchKernelGGL((GemmI8TileKernel<128, 128, 128>), grid, dim3(kThreads), 0, s, QA, sa, QWt,
-                         sw, C, acc, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+      const unsigned tiles = static_cast<unsigned>(((M + 127) / 128) * ((N + 127) / 128));
+      hipLaunchKernelGGL((GemmI8TileKernel<128, 128, 128, 2, 2>), dim3(tiles), dim3(256), 0, s, QA,
+                         sa, QWt, sw, C, acc, static_cast<int>(M), static_cast<int>(N),
+                         static_cast<int>(K));
     }
     return hipGetLastError();
   }
