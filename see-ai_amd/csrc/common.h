@@ -234,6 +234,17 @@ hipError_t LaunchAttnDKTiled(int dtype, const float* q, const float* k, const fl
 hipError_t LaunchAttnDVTiled(int dtype, const float* q, const float* k, const float* dout,
                              const float* stats, float* dv, size_t B, size_t S, size_t H,
                              size_t d, hipStream_t s);
+// Relaxed tiled attention on bf16 MFMA (k_flash.hip), d in {64, 128}; dk or
+// dv may be null in LaunchFlashDKDV (both non-null = the fused pass).
+hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float* o, float* stats,
+                          size_t B, size_t S, size_t H, size_t d, const int32_t* starts,
+                          hipStream_t s);
+hipError_t LaunchFlashDQ(const float* q, const float* k, const float* v, const float* dout,
+                         float* stats, float* dq, size_t B, size_t S, size_t H, size_t d,
+                         int delta_given, hipStream_t s);
+hipError_t LaunchFlashDKDV(const float* q, const float* k, const float* v, const float* dout,
+                           const float* stats, float* dk, float* dv, size_t B, size_t S, size_t H,
+                           size_t d, hipStream_t s);
 hipError_t LaunchAttnFwdCached(const float* q, const float* k, const float* v, float* o,
                                float* probs, size_t B, size_t S, size_t H, size_t d,
                                const int32_t* starts, hipStream_t s);

@@ -17,9 +17,9 @@
 // c -- is exactly the B-operand layout the next product (O^T += V^T P^T)
 // wants, so probabilities never leave registers.  The row softmax becomes a
 // column reduction: in-lane over 4 values, then two lane swaps.
-//   dtype 0 (exact family): v_mfma_f32_16x16x4_f32 on f32 operands.
-//   dtype 1 (relaxed, kFlagRelaxed): operands rounded to bf16 (RNE) on load,
-//           v_mfma_f32_16x16x16_bf16 with f32 accumulation; softmax in f32.
+// These are the exact family (v_mfma_f32_16x16x4_f32 on f32 operands); the
+// relaxed family (kFlagRelaxed) at d in {64, 128} runs the bf16 kernels of
+// k_flash.hip.
 // Other head widths run the per-row kernels below (double dots, the
 // reference's loop order).
 #include "common.h"
@@ -28,10 +28,6 @@ namespace seeai {
 namespace {
 
 constexpr int kThreads = 256;
-typedef short v4s __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ short Bf(float x) { return static_cast<short>(F32ToBf16(x)); }
-
 __device__ __forceinline__ size_t AttnStart(float stored, size_t i) {
   // instruction.h:246-250: clamped into [0, i], NaN to 0.
   if (!(stored > 0.0f)) return 0;
@@ -41,30 +37,19 @@ __device__ __forceinline__ size_t AttnStart(float stored, size_t i) {
 
 // out[r] = X[xr(4g+r)] . Y[yr(c)] over D dims, where this lane passes the
 // row pointers of tile row c: xrow = X row (x0 + c), yrow = Y row (y0 + c).
-template <int D, int kDt>
+template <int D>
 __device__ __forceinline__ v4f DotTile(const float* __restrict__ xrow,
                                        const float* __restrict__ yrow, int g) {
   v4f acc = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (kDt == 0) {
 #pragma unroll
-    for (int s = 0; s < D / 4; ++s)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xrow[4 * s + g], yrow[4 * s + g], acc, 0, 0, 0);
-  } else {
-#pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      const float4 xa = *reinterpret_cast<const float4*>(xrow + 16 * s + 4 * g);
-      const float4 ya = *reinterpret_cast<const float4*>(yrow + 16 * s + 4 * g);
-      const v4s a = {Bf(xa.x), Bf(xa.y), Bf(xa.z), Bf(xa.w)};
-      const v4s b = {Bf(ya.x), Bf(ya.y), Bf(ya.z), Bf(ya.w)};
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
-    }
-  }
+  for (int s = 0; s < D / 4; ++s)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xrow[4 * s + g], yrow[4 * s + g], acc, 0, 0, 0);
   return acc;
 }
 
 // acc[dt] (rows = dims dt*16 + 4g + r, column c) += sum_t Z[z(t)][dim] * W[t][c]
 // where this lane holds W[4g + r][c] = w[r] and zrow(t) points at Z row t.
-template <int D, int kDt>
+template <int D>
 __device__ __forceinline__ void AccumRows(v4f* acc, const float* __restrict__ z, size_t ld,
                                           const float* w, int g, int c, size_t zmax) {
   // Z rows for this lane's four k-values: t = 4g + r (clamped in bounds; the
@@ -76,18 +61,10 @@ __device__ __forceinline__ void AccumRows(v4f* acc, const float* __restrict__ z,
     zr[r] = z + (t < zmax ? t : 0) * ld;
   }
 #pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) {
-    if constexpr (kDt == 0) {
+  for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(zr[r][dt * 16 + c], w[r], acc[dt], 0, 0, 0);
-    } else {
-      const v4s a = {Bf(zr[0][dt * 16 + c]), Bf(zr[1][dt * 16 + c]), Bf(zr[2][dt * 16 + c]),
-                     Bf(zr[3][dt * 16 + c])};
-      const v4s b = {Bf(w[0]), Bf(w[1]), Bf(w[2]), Bf(w[3])};
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc[dt], 0, 0, 0);
-    }
-  }
+    for (int r = 0; r < 4; ++r)
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(zr[r][dt * 16 + c], w[r], acc[dt], 0, 0, 0);
 }
 
 __device__ __forceinline__ float ColMax(float v) {
@@ -102,7 +79,7 @@ __device__ __forceinline__ float ColSum(float v) {
 // ---------------------------------------------------------------------------
 // Forward (attention.cc:448-493 semantics; online softmax over key tiles).
 // ---------------------------------------------------------------------------
-template <int D, int kDt>
+template <int D>
 __global__ void __launch_bounds__(kThreads)
 AttnFwdMfma(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
             float* __restrict__ o, float* __restrict__ stats, int S, int H,
@@ -138,7 +115,7 @@ AttnFwdMfma(const float* __restrict__ q, const float* __restrict__ k, const floa
   const int i_hi = min(i0 + 15, S - 1);
   for (int j0 = (tile_lo / 16) * 16; j0 <= i_hi; j0 += 16) {
     const int jr = min(j0 + c, S - 1);
-    const v4f st = DotTile<D, kDt>(kb + static_cast<size_t>(jr) * ld, qrow, g);
+    const v4f st = DotTile<D>(kb + static_cast<size_t>(jr) * ld, qrow, g);
     float s[4], tmax = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -161,7 +138,7 @@ AttnFwdMfma(const float* __restrict__ q, const float* __restrict__ k, const floa
     m = m_new;
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) oacc[dt] *= alpha;
-    AccumRows<D, kDt>(oacc, vb + static_cast<size_t>(j0) * ld, ld, p, g, c,
+    AccumRows<D>(oacc, vb + static_cast<size_t>(j0) * ld, ld, p, g, c,
                       static_cast<size_t>(S - j0));
   }
   if (i >= S) return;
@@ -186,7 +163,7 @@ AttnFwdMfma(const float* __restrict__ q, const float* __restrict__ k, const floa
 // dQ (attention.cc:495-535): pass 1 forms delta = sum_j p dP over the row,
 // pass 2 forms dS = p (dP - delta) and dQ = dS K / sqrt(d).
 // ---------------------------------------------------------------------------
-template <int D, int kDt>
+template <int D>
 __global__ void __launch_bounds__(kThreads)
 AttnDQMfma(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
            const float* __restrict__ dout, float* __restrict__ stats, float* __restrict__ dq,
@@ -215,8 +192,8 @@ AttnDQMfma(const float* __restrict__ q, const float* __restrict__ k, const float
 
   auto probs = [&](int j0, float* p, float* dp) {
     const int jr = min(j0 + c, S - 1);
-    const v4f sc = DotTile<D, kDt>(k + base + static_cast<size_t>(jr) * ld, qrow, g);
-    const v4f dpt = DotTile<D, kDt>(v + base + static_cast<size_t>(jr) * ld, dorow, g);
+    const v4f sc = DotTile<D>(k + base + static_cast<size_t>(jr) * ld, qrow, g);
+    const v4f dpt = DotTile<D>(v + base + static_cast<size_t>(jr) * ld, dorow, g);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int j = j0 + 4 * g + r;
@@ -243,7 +220,7 @@ AttnDQMfma(const float* __restrict__ q, const float* __restrict__ k, const float
     probs(j0, p, dp);
 #pragma unroll
     for (int r = 0; r < 4; ++r) w[r] = (p[r] * (dp[r] - delta)) * inv_sqrt_d;
-    AccumRows<D, kDt>(acc, k + base + static_cast<size_t>(j0) * ld, ld, w, g, c,
+    AccumRows<D>(acc, k + base + static_cast<size_t>(j0) * ld, ld, w, g, c,
                       static_cast<size_t>(S - j0));
   }
   if (i >= S) return;
@@ -260,7 +237,7 @@ AttnDQMfma(const float* __restrict__ q, const float* __restrict__ k, const float
 // tiles from the diagonal down; S and dP are formed query-major so that the
 // accumulator layout is the B operand of dK^T += Q^T dS (dV^T += dO^T P).
 // ---------------------------------------------------------------------------
-template <int D, int kDt, bool kDV>
+template <int D, bool kDV>
 __global__ void __launch_bounds__(kThreads)
 AttnDKDVMfma(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
              const float* __restrict__ dout, const float* __restrict__ stats,
@@ -284,9 +261,9 @@ AttnDKDVMfma(const float* __restrict__ q, const float* __restrict__ k, const flo
   for (int it0 = j0; it0 < S; it0 += 16) {
     // Query rows of this lane's four accumulator entries: i = it0 + 4g + r.
     const int ir = min(it0 + c, S - 1);
-    const v4f sc = DotTile<D, kDt>(q + base + static_cast<size_t>(ir) * ld, krow, g);
+    const v4f sc = DotTile<D>(q + base + static_cast<size_t>(ir) * ld, krow, g);
     v4f dpt = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (!kDV) dpt = DotTile<D, kDt>(dout + base + static_cast<size_t>(ir) * ld, vrow, g);
+    if constexpr (!kDV) dpt = DotTile<D>(dout + base + static_cast<size_t>(ir) * ld, vrow, g);
     float w[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -301,7 +278,7 @@ AttnDKDVMfma(const float* __restrict__ q, const float* __restrict__ k, const flo
       }
       w[r] = val;
     }
-    AccumRows<D, kDt>(acc, (kDV ? dout : q) + base + static_cast<size_t>(it0) * ld, ld, w, g, c,
+    AccumRows<D>(acc, (kDV ? dout : q) + base + static_cast<size_t>(it0) * ld, ld, w, g, c,
                       static_cast<size_t>(S - it0));
   }
   if (j >= S) return;
@@ -504,48 +481,47 @@ bool MfmaShape(size_t d, const void* a, const void* b) {
          (reinterpret_cast<uintptr_t>(b) & 15) == 0;
 }
 
-template <template <int, int> class F, typename... Args>
-hipError_t ByShape(int dtype, size_t d, Args... args) {
-  if (d == 64) return dtype ? F<64, 1>::Run(args...) : F<64, 0>::Run(args...);
-  return dtype ? F<128, 1>::Run(args...) : F<128, 0>::Run(args...);
+template <template <int> class F, typename... Args>
+hipError_t ByShape(size_t d, Args... args) {
+  return d == 64 ? F<64>::Run(args...) : F<128>::Run(args...);
 }
 
-template <int D, int kDt>
+template <int D>
 struct FwdL {
   static hipError_t Run(const float* q, const float* k, const float* v, float* o, float* st,
                         size_t B, size_t S, size_t H, const int32_t* starts, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>((S + 63) / 64), static_cast<unsigned>(B * H));
-    hipLaunchKernelGGL((AttnFwdMfma<D, kDt>), grid, dim3(kThreads), 0, s, q, k, v, o, st,
+    hipLaunchKernelGGL((AttnFwdMfma<D>), grid, dim3(kThreads), 0, s, q, k, v, o, st,
                        static_cast<int>(S), static_cast<int>(H), starts);
     return hipGetLastError();
   }
 };
-template <int D, int kDt>
+template <int D>
 struct DQL {
   static hipError_t Run(const float* q, const float* k, const float* v, const float* dout,
                         float* st, float* dq, size_t B, size_t S, size_t H, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>((S + 63) / 64), static_cast<unsigned>(B * H));
-    hipLaunchKernelGGL((AttnDQMfma<D, kDt>), grid, dim3(kThreads), 0, s, q, k, v, dout, st, dq,
+    hipLaunchKernelGGL((AttnDQMfma<D>), grid, dim3(kThreads), 0, s, q, k, v, dout, st, dq,
                        static_cast<int>(S), static_cast<int>(H));
     return hipGetLastError();
   }
 };
-template <int D, int kDt>
+template <int D>
 struct DKL {
   static hipError_t Run(const float* q, const float* k, const float* v, const float* dout,
                         const float* st, float* out, size_t B, size_t S, size_t H, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>((S + 63) / 64), static_cast<unsigned>(B * H));
-    hipLaunchKernelGGL((AttnDKDVMfma<D, kDt, false>), grid, dim3(kThreads), 0, s, q, k, v, dout, st,
+    hipLaunchKernelGGL((AttnDKDVMfma<D, false>), grid, dim3(kThreads), 0, s, q, k, v, dout, st,
                        out, static_cast<int>(S), static_cast<int>(H));
     return hipGetLastError();
   }
 };
-template <int D, int kDt>
+template <int D>
 struct DVL {
   static hipError_t Run(const float* q, const float* k, const float* v, const float* dout,
                         const float* st, float* out, size_t B, size_t S, size_t H, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>((S + 63) / 64), static_cast<unsigned>(B * H));
-    hipLaunchKernelGGL((AttnDKDVMfma<D, kDt, true>), grid, dim3(kThreads), 0, s, q, k, v, dout, st,
+    hipLaunchKernelGGL((AttnDKDVMfma<D, true>), grid, dim3(kThreads), 0, s, q, k, v, dout, st,
                        out, static_cast<int>(S), static_cast<int>(H));
     return hipGetLastError();
   }
@@ -560,7 +536,8 @@ hipError_t LaunchAttnFwdTiled(int dtype, const float* q, const float* k, const f
                               const int32_t* starts, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   if (MfmaShape(d, q, k) && MfmaShape(d, v, o))
-    return ByShape<FwdL>(dtype, d, q, k, v, o, stats, B, S, H, starts, s);
+    return dtype ? LaunchFlashFwd(q, k, v, o, stats, B, S, H, d, starts, s)
+                 : ByShape<FwdL>(d, q, k, v, o, stats, B, S, H, starts, s);
   hipLaunchKernelGGL(AttnFwdRowKernel, dim3(UnitsGrid(B * H * S)), dim3(kThreads), 0, s, q, k, v, o,
                      stats, static_cast<float*>(nullptr), B, S, H, d, starts);
   return hipGetLastError();
@@ -571,7 +548,8 @@ hipError_t LaunchAttnDQTiled(int dtype, const float* q, const float* k, const fl
                              size_t H, size_t d, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   if (MfmaShape(d, q, k) && MfmaShape(d, v, dout) && MfmaShape(d, dq, q))
-    return ByShape<DQL>(dtype, d, q, k, v, dout, stats, dq, B, S, H, s);
+    return dtype ? LaunchFlashDQ(q, k, v, dout, stats, dq, B, S, H, d, 0, s)
+                 : ByShape<DQL>(d, q, k, v, dout, stats, dq, B, S, H, s);
   hipLaunchKernelGGL(AttnDQRowKernel, dim3(UnitsGrid(B * H * S)), dim3(kThreads), 0, s, q, k, v,
                      dout, stats, dq, B, S, H, d);
   return hipGetLastError();
@@ -582,7 +560,8 @@ hipError_t LaunchAttnDKTiled(int dtype, const float* q, const float* k, const fl
                              size_t S, size_t H, size_t d, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   if (MfmaShape(d, q, k) && MfmaShape(d, v, dout) && MfmaShape(d, dk, q))
-    return ByShape<DKL>(dtype, d, q, k, v, dout, stats, dk, B, S, H, s);
+    return dtype ? LaunchFlashDKDV(q, k, v, dout, stats, dk, nullptr, B, S, H, d, s)
+                 : ByShape<DKL>(d, q, k, v, dout, stats, dk, B, S, H, s);
   hipLaunchKernelGGL(AttnDKDVRowKernel<false>, dim3(UnitsGrid(B * H * S)), dim3(kThreads), 0, s, q,
                      k, v, dout, stats, dk, B, S, H, d);
   return hipGetLastError();
@@ -593,8 +572,9 @@ hipError_t LaunchAttnDVTiled(int dtype, const float* q, const float* k, const fl
                              size_t d, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   if (MfmaShape(d, q, k) && MfmaShape(d, dout, dv))
-    return ByShape<DVL>(dtype, d, q, k, static_cast<const float*>(nullptr), dout, stats, dv, B, S,
-                        H, s);
+    return dtype ? LaunchFlashDKDV(q, k, nullptr, dout, stats, nullptr, dv, B, S, H, d, s)
+                 : ByShape<DVL>(d, q, k, static_cast<const float*>(nullptr), dout, stats,
+                                dv, B, S, H, s);
   hipLaunchKernelGGL(AttnDKDVRowKernel<true>, dim3(UnitsGrid(B * H * S)), dim3(kThreads), 0, s, q,
                      k, static_cast<const float*>(nullptr), dout, stats, dv, B, S, H, d);
   return hipGetLastError();

@@ -1,0 +1,531 @@
+// k_flash.hip -- the relaxed (kFlagRelaxed, instruction.h:356-384) tiled
+// attention family on CDNA4 bf16 MFMA: forward, dQ, and dK / dV (fused when
+// both are wanted), over the stats-row contract of the exact family
+// (instruction.h:174-190, 234-259).  Operands arrive as f32 and are rounded
+// to bf16 (RNE) as they are staged; products accumulate in f32; softmax
+// runs in f32 in the base-2 domain.
+//
+// Geometry: one workgroup = 4 waves = 128 rows of one (b, h) -- queries for
+// the forward and dQ, keys for dK/dV -- each wave owning 32 rows; the other
+// side streams through LDS in blocks of 64, double buffered, converted to
+// bf16 once per block and stored in both the row layout (A operand of the
+// score product) and the transposed layout (operand of the accumulation).
+// Scores are formed transposed -- S^T = K Q^T (forward, dQ) or S = Q K^T
+// (dK/dV) -- so the v_mfma_f32_32x32x16_bf16 accumulator layout (lane
+// (g = lane/32, c = lane%32) holds rows 8q + 4g + e, q < 4, e < 4, of
+// column c) is exactly the operand layout of the next product: the
+// probabilities never leave registers.  Row reductions over the streamed
+// side are in-lane plus one lane swap.  Every output element has one
+// writer; no atomics.
+#include "common.h"
+
+namespace seeai {
+namespace {
+
+constexpr int kFThreads = 256;   // 4 waves
+constexpr int kRows = 128;       // rows owned per workgroup (32 per wave)
+constexpr int kBlk = 64;         // streamed rows per block
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float Exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ v16f Mfma(const bf16x8& a, const bf16x8& b, const v16f& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x4 Cvt4(float4 v) {
+  return bf16x4{static_cast<__bf16>(v.x), static_cast<__bf16>(v.y), static_cast<__bf16>(v.z),
+                static_cast<__bf16>(v.w)};
+}
+
+__device__ __forceinline__ size_t StatsStart(float stored, int i) {
+  if (!(stored > 0.0f)) return 0;
+  const float cap = static_cast<float>(i);
+  return stored >= cap ? static_cast<size_t>(i) : static_cast<size_t>(stored);
+}
+
+// One streamed block of 64 rows x D dims (f32 in HBM) staged as bf16 into
+// a row tile [64][D + 8] and, optionally, a transposed tile [D][64 + 4].
+// Lane t handles 4 rows x 4 dims per pass: 16 lanes cover one row's 64
+// dims (256 contiguous bytes), the 4 x 4 block transposes in registers.
+template <int D>
+struct Stager {
+  static constexpr int RLD = D + 8;        // row tile stride (bf16)
+  static constexpr int TLD = kBlk + 4;     // transposed tile stride (bf16)
+  static constexpr int kD4 = D / 4;
+  static constexpr int kPasses = (kBlk / 4) * kD4 / kFThreads;  // 1 (D=64) or 2 (D=128)
+  float4 reg[kPasses][4];
+
+  __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int row0,
+                                       int rows_valid) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int t = threadIdx.x + p * kFThreads;
+      const int d4 = t % kD4, rg = t / kD4;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = rg * 4 + k;
+        reg[p][k] = r < rows_valid
+                        ? *reinterpret_cast<const float4*>(base + static_cast<size_t>(row0 + r) * ld + d4 * 4)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(__bf16* __restrict__ rows, __bf16* __restrict__ trans) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int t = threadIdx.x + p * kFThreads;
+      const int d4 = t % kD4, rg = t / kD4;
+      if (rows) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          *reinterpret_cast<bf16x4*>(rows + (rg * 4 + k) * RLD + d4 * 4) = Cvt4(reg[p][k]);
+      }
+      if (trans) {
+        const float* f = reinterpret_cast<const float*>(&reg[p][0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16x4 col = {static_cast<__bf16>(f[0 * 4 + e]), static_cast<__bf16>(f[1 * 4 + e]),
+                              static_cast<__bf16>(f[2 * 4 + e]), static_cast<__bf16>(f[3 * 4 + e])};
+          *reinterpret_cast<bf16x4*>(trans + (d4 * 4 + e) * TLD + rg * 4) = col;
+        }
+      }
+    }
+  }
+};
+
+// This lane's 32 owned rows as a B (or A) operand over D dims: row c of the
+// wave's tile, dims 16s + 8g .. +8.
+template <int D>
+__device__ __forceinline__ void LoadOwned(const float* __restrict__ row, int g, bf16x8* out) {
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) {
+    const float4 a = *reinterpret_cast<const float4*>(row + 16 * s + 8 * g);
+    const float4 b = *reinterpret_cast<const float4*>(row + 16 * s + 8 * g + 4);
+    out[s] = bf16x8{static_cast<__bf16>(a.x), static_cast<__bf16>(a.y), static_cast<__bf16>(a.z),
+                    static_cast<__bf16>(a.w), static_cast<__bf16>(b.x), static_cast<__bf16>(b.y),
+                    static_cast<__bf16>(b.z), static_cast<__bf16>(b.w)};
+  }
+}
+
+// acc[kt] (32 streamed rows kt*32.. of the block x this wave's 32 owned
+// columns) = rowtile[kt*32 + c] . owned[c] over D dims.
+template <int D>
+__device__ __forceinline__ void ScoreTiles(const __bf16* __restrict__ tile, const bf16x8* owned,
+                                           int lane, v16f* acc) {
+  constexpr int RLD = D + 8;
+  const int g = lane / 32, c = lane % 32;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    v16f a = {};
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(tile + (kt * 32 + c) * RLD + 16 * s + 8 * g);
+      a = Mfma(kf, owned[s], a);
+    }
+    acc[kt] = a;
+  }
+}
+
+// out[dt] (dims dt*32 + 8q + 4g + e, column c) += sum over the 64 streamed
+// rows of trans[dim][row] * w(row, c), where this lane holds w for rows
+// kt*32 + 8q + 4g + e in w[kt][4q + e].
+template <int D>
+__device__ __forceinline__ void AccumTiles(const __bf16* __restrict__ trans, const float (*w)[16],
+                                           int lane, v16f* out) {
+  constexpr int TLD = kBlk + 4;
+  const int g = lane / 32, c = lane % 32;
+#pragma unroll
+  for (int s = 0; s < kBlk / 16; ++s) {
+    const int kt = s / 2, q0 = 2 * (s % 2);
+    const bf16x8 bw = {static_cast<__bf16>(w[kt][4 * q0 + 0]), static_cast<__bf16>(w[kt][4 * q0 + 1]),
+                       static_cast<__bf16>(w[kt][4 * q0 + 2]), static_cast<__bf16>(w[kt][4 * q0 + 3]),
+                       static_cast<__bf16>(w[kt][4 * q0 + 4]), static_cast<__bf16>(w[kt][4 * q0 + 5]),
+                       static_cast<__bf16>(w[kt][4 * q0 + 6]), static_cast<__bf16>(w[kt][4 * q0 + 7])};
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      const __bf16* r = trans + (dt * 32 + c) * TLD + 16 * s + 4 * g;
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(r);
+      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(r + 8);
+      const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      out[dt] = Mfma(av, bw, out[dt]);
+    }
+  }
+}
+
+__device__ __forceinline__ float SwapMax(float v) { return fmaxf(v, __shfl_xor(v, 32, kWave)); }
+__device__ __forceinline__ float SwapSum(float v) { return v + __shfl_xor(v, 32, kWave); }
+
+// ---------------------------------------------------------------------------
+// Forward: O = softmax(mask(Q K^T / sqrt d)) V and the stats row.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ void __launch_bounds__(kFThreads)
+FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+         float* __restrict__ o, float* __restrict__ stats, int S, int H,
+         const int32_t* __restrict__ starts) {
+  using St = Stager<D>;
+  __shared__ __attribute__((aligned(16))) __bf16 Ks[2][kBlk * St::RLD];
+  __shared__ __attribute__((aligned(16))) __bf16 Vt[2][D * St::TLD];
+  __shared__ int min_start;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / 32, c = lane % 32;
+  const int qblk = gridDim.x - 1 - blockIdx.x;  // the longest causal rows first
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const size_t ld = static_cast<size_t>(H) * D;
+  const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * D;
+  const int i0 = qblk * kRows + wave * 32;
+  const int i = i0 + c;
+  const int ic = min(i, S - 1);
+  int j_start = 0;
+  if (starts) {
+    const int s0 = starts[static_cast<size_t>(b) * S + ic];
+    j_start = s0 <= 0 ? 0 : min(s0, ic);
+  }
+  if (threadIdx.x == 0) min_start = S;
+  __syncthreads();
+  atomicMin(&min_start, j_start);  // integer min: order-independent
+  __syncthreads();
+  const int blk_lo = min_start / kBlk;
+  const int q_hi = min(qblk * kRows + kRows - 1, S - 1);
+  const int nblk = q_hi / kBlk + 1 - blk_lo;
+
+  bf16x8 qf[D / 16];
+  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, qf);
+  const float c2 = (1.0f / sqrtf(static_cast<float>(D))) * kLog2e;
+
+  v16f oacc[D / 32] = {};
+  float m2 = -INFINITY, l = 0.0f;
+  St sk, sv;
+  auto load = [&](int jb) {
+    const int j0 = (blk_lo + jb) * kBlk;
+    sk.load(k + base, ld, j0, S - j0);
+    sv.load(v + base, ld, j0, S - j0);
+  };
+  load(0);
+  sk.store(Ks[0], nullptr);
+  sv.store(nullptr, Vt[0]);
+  __syncthreads();
+  for (int jb = 0; jb < nblk; ++jb) {
+    const int buf = jb & 1;
+    if (jb + 1 < nblk) load(jb + 1);
+    const int j0 = (blk_lo + jb) * kBlk;
+    if (j0 <= i0 + 31) {  // a block wholly after this wave's queries is masked
+      v16f st[2];
+      ScoreTiles<D>(Ks[buf], qf, lane, st);
+      float p[2][16];
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = j0 + kt * 32 + 8 * (r / 4) + 4 * g + (r % 4);
+          const bool ok = i < S && j <= i && j >= j_start;
+          const float t = ok ? st[kt][r] * c2 : -INFINITY;
+          p[kt][r] = t;
+          bmax = fmaxf(bmax, t);
+        }
+      bmax = SwapMax(bmax);
+      const float m_new = fmaxf(m2, bmax);
+      const float alpha = m2 == -INFINITY ? 0.0f : Exp2(m2 - m_new);
+      float psum = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = p[kt][r] == -INFINITY ? 0.0f : Exp2(p[kt][r] - m_new);
+          p[kt][r] = e;
+          psum += e;
+        }
+      psum = SwapSum(psum);
+      l = l * alpha + psum;
+      m2 = m_new;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= alpha;
+      AccumTiles<D>(Vt[buf], p, lane, oacc);
+    }
+    if (jb + 1 < nblk) {
+      sk.store(Ks[buf ^ 1], nullptr);
+      sv.store(nullptr, Vt[buf ^ 1]);
+    }
+    __syncthreads();
+  }
+  if (i >= S) return;
+  const float inv = 1.0f / l;
+  float* orow = o + base + static_cast<size_t>(i) * ld;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+      *reinterpret_cast<float4*>(orow + dt * 32 + 8 * qq + 4 * g) =
+          make_float4(oacc[dt][4 * qq] * inv, oacc[dt][4 * qq + 1] * inv, oacc[dt][4 * qq + 2] * inv,
+                      oacc[dt][4 * qq + 3] * inv);
+  if (g == 0) {
+    float* st = stats + (static_cast<size_t>(bh) * S + i) * 4;
+    st[0] = m2 * kLn2;
+    st[1] = inv;
+    st[2] = 0.0f;
+    st[3] = static_cast<float>(j_start);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ: pass 1 delta = sum_j p dP, pass 2 dS = p (dP - delta), dQ^T = K^T dS^T.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ void __launch_bounds__(kFThreads)
+FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+        const float* __restrict__ dout, float* __restrict__ stats, float* __restrict__ dq, int S,
+        int H, int delta_given) {
+  using St = Stager<D>;
+  __shared__ __attribute__((aligned(16))) __bf16 Ks[2][kBlk * St::RLD];
+  __shared__ __attribute__((aligned(16))) __bf16 Kt[2][D * St::TLD];
+  __shared__ __attribute__((aligned(16))) __bf16 Vs[2][kBlk * St::RLD];
+  __shared__ int min_start;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / 32, c = lane % 32;
+  const int qblk = gridDim.x - 1 - blockIdx.x;
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const size_t ld = static_cast<size_t>(H) * D;
+  const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * D;
+  const int i0 = qblk * kRows + wave * 32;
+  const int i = i0 + c;
+  const int ic = min(i, S - 1);
+  float* st = stats + (static_cast<size_t>(bh) * S + ic) * 4;
+  const float m2 = st[0] * kLog2e, inv = st[1];
+  const int j_start = static_cast<int>(StatsStart(st[3], ic));
+  if (threadIdx.x == 0) min_start = S;
+  __syncthreads();
+  atomicMin(&min_start, j_start);
+  __syncthreads();
+  const int blk_lo = min_start / kBlk;
+  const int q_hi = min(qblk * kRows + kRows - 1, S - 1);
+  const int nblk = q_hi / kBlk + 1 - blk_lo;
+  const float isd = 1.0f / sqrtf(static_cast<float>(D));
+  const float c2 = isd * kLog2e;
+
+  bf16x8 qf[D / 16], df[D / 16];
+  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, qf);
+  LoadOwned<D>(dout + base + static_cast<size_t>(ic) * ld, g, df);
+
+  St sk, sv;
+  auto load = [&](int jb) {
+    const int j0 = (blk_lo + jb) * kBlk;
+    sk.load(k + base, ld, j0, S - j0);
+    sv.load(v + base, ld, j0, S - j0);
+  };
+  auto probs = [&](int buf, int j0, float (*p)[16], float (*dp)[16]) {
+    v16f sc[2], dpt[2];
+    ScoreTiles<D>(Ks[buf], qf, lane, sc);
+    ScoreTiles<D>(Vs[buf], df, lane, dpt);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int j = j0 + kt * 32 + 8 * (r / 4) + 4 * g + (r % 4);
+        const bool ok = i < S && j <= i && j >= j_start;
+        p[kt][r] = ok ? Exp2(sc[kt][r] * c2 - m2) * inv : 0.0f;
+        dp[kt][r] = ok ? dpt[kt][r] : 0.0f;
+      }
+  };
+
+  float delta = 0.0f;
+  for (int pass = delta_given ? 1 : 0; pass < 2; ++pass) {
+    if (pass == 1 && delta_given) delta = st[2];
+    v16f acc[D / 32] = {};
+    load(0);
+    sk.store(Ks[0], Kt[0]);
+    sv.store(Vs[0], nullptr);
+    __syncthreads();
+    for (int jb = 0; jb < nblk; ++jb) {
+      const int buf = jb & 1;
+      if (jb + 1 < nblk) load(jb + 1);
+      const int j0 = (blk_lo + jb) * kBlk;
+      if (j0 <= i0 + 31) {
+        float p[2][16], dp[2][16];
+        probs(buf, j0, p, dp);
+        if (pass == 0) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) delta += dp[kt][r] * p[kt][r];
+        } else {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[kt][r] = (p[kt][r] * (dp[kt][r] - delta)) * isd;
+          AccumTiles<D>(Kt[buf], p, lane, acc);
+        }
+      }
+      if (jb + 1 < nblk) {
+        sk.store(Ks[buf ^ 1], Kt[buf ^ 1]);
+        sv.store(Vs[buf ^ 1], nullptr);
+      }
+      __syncthreads();
+    }
+    if (pass == 0) {
+      delta = SwapSum(delta);
+      continue;
+    }
+    if (i < S) {
+      float* drow = dq + base + static_cast<size_t>(i) * ld;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq)
+          *reinterpret_cast<float4*>(drow + dt * 32 + 8 * qq + 4 * g) =
+              make_float4(acc[dt][4 * qq], acc[dt][4 * qq + 1], acc[dt][4 * qq + 2], acc[dt][4 * qq + 3]);
+      if (g == 0 && !delta_given) st[2] = delta;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV: one wave per 32 keys walking the query blocks from the diagonal;
+// S = Q K^T and dP = dO V^T formed query-major, dK^T += Q^T dS, dV^T += dO^T P.
+// ---------------------------------------------------------------------------
+template <int D, bool kDK, bool kDV>
+__global__ void __launch_bounds__(kFThreads)
+FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+          const float* __restrict__ dout, const float* __restrict__ stats, float* __restrict__ dk,
+          float* __restrict__ dv, int S, int H) {
+  using St = Stager<D>;
+  __shared__ __attribute__((aligned(16))) __bf16 Qs[2][kBlk * St::RLD];
+  __shared__ __attribute__((aligned(16))) __bf16 Qt[2][kDK ? D * St::TLD : 1];
+  __shared__ __attribute__((aligned(16))) __bf16 Ds[2][kDK ? kBlk * St::RLD : 1];
+  __shared__ __attribute__((aligned(16))) __bf16 Dt[2][kDV ? D * St::TLD : 1];
+  __shared__ float4 Sts[2][kBlk];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / 32, c = lane % 32;
+  const int kblk = blockIdx.x;  // the longest causal columns are the first
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const size_t ld = static_cast<size_t>(H) * D;
+  const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * D;
+  const int j0w = kblk * kRows + wave * 32;
+  const int j = j0w + c;
+  const int jc = min(j, S - 1);
+  const float isd = 1.0f / sqrtf(static_cast<float>(D));
+  const float c2 = isd * kLog2e;
+  const float4* st_bh = reinterpret_cast<const float4*>(stats) + static_cast<size_t>(bh) * S;
+
+  bf16x8 kf[D / 16], vf[D / 16];
+  LoadOwned<D>(k + base + static_cast<size_t>(jc) * ld, g, kf);
+  if (kDK) LoadOwned<D>(v + base + static_cast<size_t>(jc) * ld, g, vf);
+
+  const int blk_first = (kblk * kRows) / kBlk;
+  const int nblk = (S + kBlk - 1) / kBlk - blk_first;
+  St sq, sd;
+  auto load = [&](int ib) {
+    const int r0 = (blk_first + ib) * kBlk;
+    sq.load(q + base, ld, r0, S - r0);
+    sd.load(dout + base, ld, r0, S - r0);
+  };
+  auto stage = [&](int buf, int ib) {
+    sq.store(Qs[buf], kDK ? Qt[buf] : nullptr);
+    sd.store(kDK ? Ds[buf] : nullptr, kDV ? Dt[buf] : nullptr);
+    const int r0 = (blk_first + ib) * kBlk;
+    if (threadIdx.x < kBlk)
+      Sts[buf][threadIdx.x] = r0 + threadIdx.x < S ? st_bh[r0 + threadIdx.x] : make_float4(0.f, 1.f, 0.f, 0.f);
+  };
+
+  v16f dka[D / 32] = {}, dva[D / 32] = {};
+  load(0);
+  stage(0, 0);
+  __syncthreads();
+  for (int ib = 0; ib < nblk; ++ib) {
+    const int buf = ib & 1;
+    if (ib + 1 < nblk) load(ib + 1);
+    const int r0 = (blk_first + ib) * kBlk;
+    if (r0 + kBlk - 1 >= j0w) {  // some query of the block reaches this wave's keys
+      v16f sc[2], dpt[2];
+      ScoreTiles<D>(Qs[buf], kf, lane, sc);
+      if (kDK) ScoreTiles<D>(Ds[buf], vf, lane, dpt);
+      float p[2][16], w[2][16];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int il = kt * 32 + 8 * (r / 4) + 4 * g + (r % 4);
+          const int iq = r0 + il;
+          const float4 s4 = Sts[buf][il];
+          const bool ok = iq < S && j < S && j <= iq && static_cast<size_t>(j) >= StatsStart(s4.w, iq);
+          const float pp = ok ? Exp2(sc[kt][r] * c2 - s4.x * kLog2e) * s4.y : 0.0f;
+          p[kt][r] = pp;
+          if (kDK) w[kt][r] = ok ? (pp * (dpt[kt][r] - s4.z)) * isd : 0.0f;
+        }
+      if (kDK) AccumTiles<D>(Qt[buf], w, lane, dka);
+      if (kDV) AccumTiles<D>(Dt[buf], p, lane, dva);
+    }
+    if (ib + 1 < nblk) stage(buf ^ 1, ib + 1);
+    __syncthreads();
+  }
+  if (j >= S) return;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int off = dt * 32 + 8 * qq + 4 * g;
+      if (kDK)
+        *reinterpret_cast<float4*>(dk + base + static_cast<size_t>(j) * ld + off) =
+            make_float4(dka[dt][4 * qq], dka[dt][4 * qq + 1], dka[dt][4 * qq + 2], dka[dt][4 * qq + 3]);
+      if (kDV)
+        *reinterpret_cast<float4*>(dv + base + static_cast<size_t>(j) * ld + off) =
+            make_float4(dva[dt][4 * qq], dva[dt][4 * qq + 1], dva[dt][4 * qq + 2], dva[dt][4 * qq + 3]);
+    }
+}
+
+}  // namespace
+
+
+hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float* o, float* stats,
+                          size_t B, size_t S, size_t H, size_t d, const int32_t* starts,
+                          hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((S + kRows - 1) / kRows), static_cast<unsigned>(B * H));
+  if (d == 64)
+    hipLaunchKernelGGL(FlashFwd<64>, grid, dim3(kFThreads), 0, s, q, k, v, o, stats,
+                       static_cast<int>(S), static_cast<int>(H), starts);
+  else
+    hipLaunchKernelGGL(FlashFwd<128>, grid, dim3(kFThreads), 0, s, q, k, v, o, stats,
+                       static_cast<int>(S), static_cast<int>(H), starts);
+  return hipGetLastError();
+}
+
+hipError_t LaunchFlashDQ(const float* q, const float* k, const float* v, const float* dout,
+                         float* stats, float* dq, size_t B, size_t S, size_t H, size_t d,
+                         int delta_given, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((S + kRows - 1) / kRows), static_cast<unsigned>(B * H));
+  if (d == 64)
+    hipLaunchKernelGGL(FlashDQ<64>, grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dq,
+                       static_cast<int>(S), static_cast<int>(H), delta_given);
+  else
+    hipLaunchKernelGGL(FlashDQ<128>, grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dq,
+                       static_cast<int>(S), static_cast<int>(H), delta_given);
+  return hipGetLastError();
+}
+
+hipError_t LaunchFlashDKDV(const float* q, const float* k, const float* v, const float* dout,
+                           const float* stats, float* dk, float* dv, size_t B, size_t S, size_t H,
+                           size_t d, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((S + kRows - 1) / kRows), static_cast<unsigned>(B * H));
+  const int Si = static_cast<int>(S), Hi = static_cast<int>(H);
+#define SEEAI_DKDV(DD, A, Bv)                                                                  \
+  hipLaunchKernelGGL((FlashDKDV<DD, A, Bv>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dk, \
+                     dv, Si, Hi)
+  if (d == 64) {
+    if (dk && dv) SEEAI_DKDV(64, true, true);
+    else if (dk) SEEAI_DKDV(64, true, false);
+    else SEEAI_DKDV(64, false, true);
+  } else {
+    if (dk && dv) SEEAI_DKDV(128, true, true);
+    else if (dk) SEEAI_DKDV(128, true, false);
+    else SEEAI_DKDV(128, false, true);
+  }
+#undef SEEAI_DKDV
+  return hipGetLastError();
+}
+
+}  // namespace seeai

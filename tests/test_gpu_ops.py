@@ -322,7 +322,7 @@ def test_bad_clip_threshold_is_refused(hip, backend):
 # --- attention ---------------------------------------------------------------------------------
 
 ATTN_SHAPES = [(1, 1, 1, 64), (2, 67, 2, 64), (1, 130, 3, 128), (2, 33, 2, 16), (1, 9, 2, 4),
-               (1, 512, 2, 64)]
+               (1, 512, 2, 64), (2, 300, 2, 64), (1, 1024, 2, 128)]
 
 
 @pytest.mark.parametrize("B,S,H,d", ATTN_SHAPES)
