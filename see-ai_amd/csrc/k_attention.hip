@@ -536,7 +536,7 @@ hipError_t LaunchAttnFwdTiled(int dtype, const float* q, const float* k, const f
                               const int32_t* starts, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   if (MfmaShape(d, q, k) && MfmaShape(d, v, o))
-    return dtype ? LaunchFlashFwd(q, k, v, o, stats, B, S, H, d, starts, s)
+    return dtype && FlashFits(B, S, H, d) ? LaunchFlashFwd(q, k, v, o, stats, B, S, H, d, starts, s)
                  : ByShape<FwdL>(d, q, k, v, o, stats, B, S, H, starts, s);
   hipLaunchKernelGGL(AttnFwdRowKernel, dim3(UnitsGrid(B * H * S)), dim3(kThreads), 0, s, q, k, v, o,
                      stats, static_cast<float*>(nullptr), B, S, H, d, starts);
@@ -548,7 +548,7 @@ hipError_t LaunchAttnDQTiled(int dtype, const float* q, const float* k, const fl
                              size_t H, size_t d, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   if (MfmaShape(d, q, k) && MfmaShape(d, v, dout) && MfmaShape(d, dq, q))
-    return dtype ? LaunchFlashDQ(q, k, v, dout, stats, dq, B, S, H, d, 0, s)
+    return dtype && FlashFits(B, S, H, d) ? LaunchFlashDQ(q, k, v, dout, stats, dq, B, S, H, d, 0, s)
                  : ByShape<DQL>(d, q, k, v, dout, stats, dq, B, S, H, s);
   hipLaunchKernelGGL(AttnDQRowKernel, dim3(UnitsGrid(B * H * S)), dim3(kThreads), 0, s, q, k, v,
                      dout, stats, dq, B, S, H, d);
@@ -560,7 +560,7 @@ hipError_t LaunchAttnDKTiled(int dtype, const float* q, const float* k, const fl
                              size_t S, size_t H, size_t d, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   if (MfmaShape(d, q, k) && MfmaShape(d, v, dout) && MfmaShape(d, dk, q))
-    return dtype ? LaunchFlashDKDV(q, k, v, dout, stats, dk, nullptr, B, S, H, d, s)
+    return dtype && FlashFits(B, S, H, d) ? LaunchFlashDKDV(q, k, v, dout, stats, dk, nullptr, B, S, H, d, s)
                  : ByShape<DKL>(d, q, k, v, dout, stats, dk, B, S, H, s);
   hipLaunchKernelGGL(AttnDKDVRowKernel<false>, dim3(UnitsGrid(B * H * S)), dim3(kThreads), 0, s, q,
                      k, v, dout, stats, dk, B, S, H, d);
@@ -572,12 +572,24 @@ hipError_t LaunchAttnDVTiled(int dtype, const float* q, const float* k, const fl
                              size_t d, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   if (MfmaShape(d, q, k) && MfmaShape(d, dout, dv))
-    return dtype ? LaunchFlashDKDV(q, k, nullptr, dout, stats, nullptr, dv, B, S, H, d, s)
+    return dtype && FlashFits(B, S, H, d) ? LaunchFlashDKDV(q, k, nullptr, dout, stats, nullptr, dv, B, S, H, d, s)
                  : ByShape<DVL>(d, q, k, static_cast<const float*>(nullptr), dout, stats,
                                 dv, B, S, H, s);
   hipLaunchKernelGGL(AttnDKDVRowKernel<true>, dim3(UnitsGrid(B * H * S)), dim3(kThreads), 0, s, q,
                      k, static_cast<const float*>(nullptr), dout, stats, dv, B, S, H, d);
   return hipGetLastError();
+}
+
+hipError_t LaunchAttnDKDVTiled(int dtype, const float* q, const float* k, const float* v,
+                               const float* dout, const float* stats, float* dk, float* dv,
+                               size_t B, size_t S, size_t H, size_t d, hipStream_t s) {
+  if (B * H * S == 0) return hipSuccess;
+  // The fused bf16 pass holds both accumulators and both score tiles; at
+  // d = 128 that exceeds the register file, so there the passes run apart.
+  if (dtype && d == 64 && FlashFits(B, S, H, d) && MfmaShape(d, q, k) && MfmaShape(d, v, dout) && MfmaShape(d, dk, dv))
+    return LaunchFlashDKDV(q, k, v, dout, stats, dk, dv, B, S, H, d, s);
+  const hipError_t e = LaunchAttnDKTiled(dtype, q, k, v, dout, stats, dk, B, S, H, d, s);
+  return e != hipSuccess ? e : LaunchAttnDVTiled(dtype, q, k, dout, stats, dv, B, S, H, d, s);
 }
 
 hipError_t LaunchAttnFwdCached(const float* q, const float* k, const float* v, float* o,

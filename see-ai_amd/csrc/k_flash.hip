@@ -31,6 +31,10 @@ constexpr float kLn2 = 0.6931471805599453f;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
+// Word 3 of a raw (stride 0) buffer resource on CDNA: 32-bit data format,
+// out-of-range reads return zero.
+constexpr int kRsrcWord3 = 0x00020000;
+
 __device__ __forceinline__ float Exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ v16f Mfma(const bf16x8& a, const bf16x8& b, const v16f& c) {
@@ -52,6 +56,10 @@ __device__ __forceinline__ size_t StatsStart(float stored, int i) {
 // a row tile [64][D + 8] and, optionally, a transposed tile [D][64 + 4].
 // Lane t handles 4 rows x 4 dims per pass: 16 lanes cover one row's 64
 // dims (256 contiguous bytes), the 4 x 4 block transposes in registers.
+// Rows are read through a buffer resource spanning the valid rows of the
+// (b, h) slice, so rows past the sequence end read as zeros without a
+// branch; the per-lane byte offsets are fixed, the block start moves the
+// resource base.
 template <int D>
 struct Stager {
   static constexpr int RLD = D + 8;        // row tile stride (bf16)
@@ -59,21 +67,32 @@ struct Stager {
   static constexpr int kD4 = D / 4;
   static constexpr int kPasses = (kBlk / 4) * kD4 / kFThreads;  // 1 (D=64) or 2 (D=128)
   float4 reg[kPasses][4];
+  uint32_t voff[kPasses][4];
 
-  __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int row0,
-                                       int rows_valid) {
+  __device__ __forceinline__ explicit Stager(uint32_t ld) {
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
       const int t = threadIdx.x + p * kFThreads;
       const int d4 = t % kD4, rg = t / kD4;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int r = rg * 4 + k;
-        reg[p][k] = r < rows_valid
-                        ? *reinterpret_cast<const float4*>(base + static_cast<size_t>(row0 + r) * ld + d4 * 4)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      for (int k = 0; k < 4; ++k) voff[p][k] = ((rg * 4 + k) * ld + d4 * 4) * 4u;
     }
+  }
+  // slice: row 0 of the (b, h) slice; slice_bytes: through the end of its
+  // last valid row; rows row0 .. row0 + 63 are read.
+  __device__ __forceinline__ void load(const float* slice, uint32_t slice_bytes, uint32_t ld,
+                                       int row0) {
+    const uint32_t skip = static_cast<uint32_t>(row0) * ld * 4u;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(slice) + static_cast<size_t>(row0) * ld, 0,
+        static_cast<int>(slice_bytes - skip), kRsrcWord3);
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff[p][k], 0, 0);
+        reg[p][k] = *reinterpret_cast<const float4*>(&v);
+      }
   }
   __device__ __forceinline__ void store(__bf16* __restrict__ rows, __bf16* __restrict__ trans) {
 #pragma unroll
@@ -131,38 +150,70 @@ __device__ __forceinline__ void ScoreTiles(const __bf16* __restrict__ tile, cons
   }
 }
 
+// The weights of one 32-row score tile kt (this lane's 16 values, rows
+// 8q + 4g + e in w[4q + e]) as the two B operands of AccumTiles.
+__device__ __forceinline__ void PackTile(const float* w, bf16x8* out) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    out[h] = bf16x8{static_cast<__bf16>(w[8 * h + 0]), static_cast<__bf16>(w[8 * h + 1]),
+                    static_cast<__bf16>(w[8 * h + 2]), static_cast<__bf16>(w[8 * h + 3]),
+                    static_cast<__bf16>(w[8 * h + 4]), static_cast<__bf16>(w[8 * h + 5]),
+                    static_cast<__bf16>(w[8 * h + 6]), static_cast<__bf16>(w[8 * h + 7])};
+}
+
 // out[dt] (dims dt*32 + 8q + 4g + e, column c) += sum over the 64 streamed
-// rows of trans[dim][row] * w(row, c), where this lane holds w for rows
-// kt*32 + 8q + 4g + e in w[kt][4q + e].
+// rows of trans[dim][row] * w(row, c), with w packed by PackTile: bw[s]
+// holds rows 16s + 4g + {0..3} and 16s + 8 + 4g + {0..3}.  The k order of
+// the product is permuted alike on both operands.
 template <int D>
-__device__ __forceinline__ void AccumTiles(const __bf16* __restrict__ trans, const float (*w)[16],
+__device__ __forceinline__ void AccumTiles(const __bf16* __restrict__ trans, const bf16x8* bw,
                                            int lane, v16f* out) {
   constexpr int TLD = kBlk + 4;
   const int g = lane / 32, c = lane % 32;
 #pragma unroll
   for (int s = 0; s < kBlk / 16; ++s) {
-    const int kt = s / 2, q0 = 2 * (s % 2);
-    const bf16x8 bw = {static_cast<__bf16>(w[kt][4 * q0 + 0]), static_cast<__bf16>(w[kt][4 * q0 + 1]),
-                       static_cast<__bf16>(w[kt][4 * q0 + 2]), static_cast<__bf16>(w[kt][4 * q0 + 3]),
-                       static_cast<__bf16>(w[kt][4 * q0 + 4]), static_cast<__bf16>(w[kt][4 * q0 + 5]),
-                       static_cast<__bf16>(w[kt][4 * q0 + 6]), static_cast<__bf16>(w[kt][4 * q0 + 7])};
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
       const __bf16* r = trans + (dt * 32 + c) * TLD + 16 * s + 4 * g;
       const bf16x4 lo = *reinterpret_cast<const bf16x4*>(r);
       const bf16x4 hi = *reinterpret_cast<const bf16x4*>(r + 8);
       const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      out[dt] = Mfma(av, bw, out[dt]);
+      out[dt] = Mfma(av, bw[s], out[dt]);
     }
   }
 }
 
 __device__ __forceinline__ float SwapMax(float v) { return fmaxf(v, __shfl_xor(v, 32, kWave)); }
 __device__ __forceinline__ float SwapSum(float v) { return v + __shfl_xor(v, 32, kWave); }
+__device__ __forceinline__ int WaveMaxI(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Streamed row of score element r of tile kt, relative to the block start.
+__device__ __forceinline__ int RowOf(int kt, int r, int g) { return kt * 32 + 8 * (r / 4) + 4 * g + (r % 4); }
+
+// Work unit of this workgroup: (bh, rank) with rank 0 the heaviest of the
+// nq row blocks of one (b, h).  Consecutive workgroup ids land on the 8 XCDs
+// in turn, so ids are regrouped to give each XCD whole (b, h) slices, heavy
+// blocks first: the K / V (or Q / dO) of a slice is then read into one L2.
+__device__ __forceinline__ void UnitOf(int nq, int& bh, int& rank) {
+  const int w = blockIdx.x, total = gridDim.x;
+  const int t = total % 8 == 0 ? (w % 8) * (total / 8) + w / 8 : w;
+  bh = t / nq;
+  rank = t % nq;
+}
 
 // ---------------------------------------------------------------------------
-// Forward: O = softmax(mask(Q K^T / sqrt d)) V and the stats row.
+// Forward: O = softmax(mask(Q K^T / sqrt d)) V and the stats row.  The
+// running maximum used for the exponentials moves only when a block's
+// maximum exceeds it by more than 2^8 (values stay below 2^8 in f32); the
+// true row maximum is tracked beside it and the stats row is stated against
+// it, so the row (m, 1/l) is the reference's.
 // ---------------------------------------------------------------------------
+constexpr float kLazy = 8.0f;
+
 template <int D>
 __global__ void __launch_bounds__(kFThreads)
 FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
@@ -174,8 +225,11 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
   __shared__ int min_start;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int g = lane / 32, c = lane % 32;
-  const int qblk = gridDim.x - 1 - blockIdx.x;  // the longest causal rows first
-  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int nq = (S + kRows - 1) / kRows;
+  int bh, rank;
+  UnitOf(nq, bh, rank);
+  const int qblk = nq - 1 - rank;
+  const int b = bh / H, h = bh % H;
   const size_t ld = static_cast<size_t>(H) * D;
   const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * D;
   const int i0 = qblk * kRows + wave * 32;
@@ -190,6 +244,7 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
   __syncthreads();
   atomicMin(&min_start, j_start);  // integer min: order-independent
   __syncthreads();
+  const int wave_max_start = WaveMaxI(j_start);
   const int blk_lo = min_start / kBlk;
   const int q_hi = min(qblk * kRows + kRows - 1, S - 1);
   const int nblk = q_hi / kBlk + 1 - blk_lo;
@@ -199,13 +254,59 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
   const float c2 = (1.0f / sqrtf(static_cast<float>(D))) * kLog2e;
 
   v16f oacc[D / 32] = {};
-  float m2 = -INFINITY, l = 0.0f;
-  St sk, sv;
+  float m_use = -INFINITY, m_true = -INFINITY, l = 0.0f;
+  const uint32_t ld32 = static_cast<uint32_t>(ld);
+  const uint32_t slice_bytes = static_cast<uint32_t>(((S - 1) * ld + D) * 4);
+  St sk(ld32), sv(ld32);
   auto load = [&](int jb) {
     const int j0 = (blk_lo + jb) * kBlk;
-    sk.load(k + base, ld, j0, S - j0);
-    sv.load(v + base, ld, j0, S - j0);
+    sk.load(k + base, slice_bytes, ld32, j0);
+    sv.load(v + base, slice_bytes, ld32, j0);
   };
+  auto block = [&](auto masked, int buf, int j0) {
+    constexpr bool kMask = decltype(masked)::value;
+    v16f st[2];
+    ScoreTiles<D>(Ks[buf], qf, lane, st);
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (kMask) {
+          const int j = j0 + RowOf(kt, r, g);
+          if (j > i || j < j_start) st[kt][r] = -INFINITY;
+        }
+        bmax = fmaxf(bmax, st[kt][r]);
+      }
+    const float mb = SwapMax(bmax) * c2;
+    m_true = fmaxf(m_true, mb);
+    const bool need = mb > m_use + kLazy;
+    if (__any(need)) {
+      const float m_new = need ? mb : m_use;
+      const float alpha = !need ? 1.0f : (m_use == -INFINITY ? 0.0f : Exp2(m_use - m_new));
+      m_use = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= alpha;
+    }
+    bf16x8 pb[4];
+    float psum = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float e = Exp2(__builtin_fmaf(st[kt][r], c2, -m_use));
+        if constexpr (kMask) e = st[kt][r] == -INFINITY ? 0.0f : e;
+        p[r] = e;
+        psum += e;
+      }
+      PackTile(p, pb + 2 * kt);
+    }
+    l += SwapSum(psum);
+    AccumTiles<D>(Vt[buf], pb, lane, oacc);
+  };
+
   load(0);
   sk.store(Ks[0], nullptr);
   sv.store(nullptr, Vt[0]);
@@ -214,40 +315,10 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
     const int buf = jb & 1;
     if (jb + 1 < nblk) load(jb + 1);
     const int j0 = (blk_lo + jb) * kBlk;
-    if (j0 <= i0 + 31) {  // a block wholly after this wave's queries is masked
-      v16f st[2];
-      ScoreTiles<D>(Ks[buf], qf, lane, st);
-      float p[2][16];
-      float bmax = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = j0 + kt * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-          const bool ok = i < S && j <= i && j >= j_start;
-          const float t = ok ? st[kt][r] * c2 : -INFINITY;
-          p[kt][r] = t;
-          bmax = fmaxf(bmax, t);
-        }
-      bmax = SwapMax(bmax);
-      const float m_new = fmaxf(m2, bmax);
-      const float alpha = m2 == -INFINITY ? 0.0f : Exp2(m2 - m_new);
-      float psum = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = p[kt][r] == -INFINITY ? 0.0f : Exp2(p[kt][r] - m_new);
-          p[kt][r] = e;
-          psum += e;
-        }
-      psum = SwapSum(psum);
-      l = l * alpha + psum;
-      m2 = m_new;
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= alpha;
-      AccumTiles<D>(Vt[buf], p, lane, oacc);
-    }
+    if (j0 + kBlk - 1 <= i0 && j0 >= wave_max_start)
+      block(std::false_type{}, buf, j0);
+    else if (j0 <= i0 + 31)  // a block wholly after this wave's queries is masked
+      block(std::true_type{}, buf, j0);
     if (jb + 1 < nblk) {
       sk.store(Ks[buf ^ 1], nullptr);
       sv.store(nullptr, Vt[buf ^ 1]);
@@ -266,12 +337,16 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
                       oacc[dt][4 * qq + 3] * inv);
   if (g == 0) {
     float* st = stats + (static_cast<size_t>(bh) * S + i) * 4;
-    st[0] = m2 * kLn2;
-    st[1] = inv;
+    st[0] = m_true * kLn2;
+    st[1] = inv * Exp2(m_true - m_use);  // 1 / sum exp(s - m_true)
     st[2] = 0.0f;
     st[3] = static_cast<float>(j_start);
   }
 }
+
+// Row offset of the base-2 exponent: p = 2^(s c2 - mm) with mm = m log2(e)
+// + log2(l), from the stats row (m, 1/l).
+__device__ __forceinline__ float RowOffset(float m, float inv) { return m * kLog2e - log2f(inv); }
 
 // ---------------------------------------------------------------------------
 // dQ: pass 1 delta = sum_j p dP, pass 2 dS = p (dP - delta), dQ^T = K^T dS^T.
@@ -288,20 +363,24 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
   __shared__ int min_start;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int g = lane / 32, c = lane % 32;
-  const int qblk = gridDim.x - 1 - blockIdx.x;
-  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int nq = (S + kRows - 1) / kRows;
+  int bh, rank;
+  UnitOf(nq, bh, rank);
+  const int qblk = nq - 1 - rank;
+  const int b = bh / H, h = bh % H;
   const size_t ld = static_cast<size_t>(H) * D;
   const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * D;
   const int i0 = qblk * kRows + wave * 32;
   const int i = i0 + c;
   const int ic = min(i, S - 1);
   float* st = stats + (static_cast<size_t>(bh) * S + ic) * 4;
-  const float m2 = st[0] * kLog2e, inv = st[1];
+  const float mm = RowOffset(st[0], st[1]);
   const int j_start = static_cast<int>(StatsStart(st[3], ic));
   if (threadIdx.x == 0) min_start = S;
   __syncthreads();
   atomicMin(&min_start, j_start);
   __syncthreads();
+  const int wave_max_start = WaveMaxI(j_start);
   const int blk_lo = min_start / kBlk;
   const int q_hi = min(qblk * kRows + kRows - 1, S - 1);
   const int nblk = q_hi / kBlk + 1 - blk_lo;
@@ -312,24 +391,30 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
   LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, qf);
   LoadOwned<D>(dout + base + static_cast<size_t>(ic) * ld, g, df);
 
-  St sk, sv;
+  const uint32_t ld32 = static_cast<uint32_t>(ld);
+  const uint32_t slice_bytes = static_cast<uint32_t>(((S - 1) * ld + D) * 4);
+  St sk(ld32), sv(ld32);
   auto load = [&](int jb) {
     const int j0 = (blk_lo + jb) * kBlk;
-    sk.load(k + base, ld, j0, S - j0);
-    sv.load(v + base, ld, j0, S - j0);
+    sk.load(k + base, slice_bytes, ld32, j0);
+    sv.load(v + base, slice_bytes, ld32, j0);
   };
-  auto probs = [&](int buf, int j0, float (*p)[16], float (*dp)[16]) {
-    v16f sc[2], dpt[2];
+  // p and dP of one block; masked entries get p = 0.
+  auto probs = [&](auto masked, int buf, int j0, float (*p)[16], v16f* dpt) {
+    constexpr bool kMask = decltype(masked)::value;
+    v16f sc[2];
     ScoreTiles<D>(Ks[buf], qf, lane, sc);
     ScoreTiles<D>(Vs[buf], df, lane, dpt);
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int j = j0 + kt * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-        const bool ok = i < S && j <= i && j >= j_start;
-        p[kt][r] = ok ? Exp2(sc[kt][r] * c2 - m2) * inv : 0.0f;
-        dp[kt][r] = ok ? dpt[kt][r] : 0.0f;
+        float e = Exp2(__builtin_fmaf(sc[kt][r], c2, -mm));
+        if constexpr (kMask) {
+          const int j = j0 + RowOf(kt, r, g);
+          e = (j <= i && j >= j_start) ? e : 0.0f;
+        }
+        p[kt][r] = e;
       }
   };
 
@@ -337,32 +422,40 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
   for (int pass = delta_given ? 1 : 0; pass < 2; ++pass) {
     if (pass == 1 && delta_given) delta = st[2];
     v16f acc[D / 32] = {};
+    auto run = [&](auto masked, int buf, int j0) {
+      float p[2][16];
+      v16f dpt[2];
+      probs(masked, buf, j0, p, dpt);
+      if (pass == 0) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) delta = __builtin_fmaf(dpt[kt][r], p[kt][r], delta);
+      } else {
+        bf16x8 wb[4];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) p[kt][r] = (p[kt][r] * (dpt[kt][r] - delta)) * isd;
+          PackTile(p[kt], wb + 2 * kt);
+        }
+        AccumTiles<D>(Kt[buf], wb, lane, acc);
+      }
+    };
     load(0);
-    sk.store(Ks[0], Kt[0]);
+    sk.store(Ks[0], pass ? Kt[0] : nullptr);
     sv.store(Vs[0], nullptr);
     __syncthreads();
     for (int jb = 0; jb < nblk; ++jb) {
       const int buf = jb & 1;
       if (jb + 1 < nblk) load(jb + 1);
       const int j0 = (blk_lo + jb) * kBlk;
-      if (j0 <= i0 + 31) {
-        float p[2][16], dp[2][16];
-        probs(buf, j0, p, dp);
-        if (pass == 0) {
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) delta += dp[kt][r] * p[kt][r];
-        } else {
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) p[kt][r] = (p[kt][r] * (dp[kt][r] - delta)) * isd;
-          AccumTiles<D>(Kt[buf], p, lane, acc);
-        }
-      }
+      if (j0 + kBlk - 1 <= i0 && j0 >= wave_max_start)
+        run(std::false_type{}, buf, j0);
+      else if (j0 <= i0 + 31)
+        run(std::true_type{}, buf, j0);
       if (jb + 1 < nblk) {
-        sk.store(Ks[buf ^ 1], Kt[buf ^ 1]);
+        sk.store(Ks[buf ^ 1], pass ? Kt[buf ^ 1] : nullptr);
         sv.store(Vs[buf ^ 1], nullptr);
       }
       __syncthreads();
@@ -398,11 +491,18 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
   __shared__ __attribute__((aligned(16))) __bf16 Qt[2][kDK ? D * St::TLD : 1];
   __shared__ __attribute__((aligned(16))) __bf16 Ds[2][kDK ? kBlk * St::RLD : 1];
   __shared__ __attribute__((aligned(16))) __bf16 Dt[2][kDV ? D * St::TLD : 1];
-  __shared__ float4 Sts[2][kBlk];
+  // Per streamed query row: exponent offset, delta, document start; and the
+  // block's largest start.
+  __shared__ __attribute__((aligned(16))) float Smm[2][kBlk];
+  __shared__ __attribute__((aligned(16))) float Sdl[2][kBlk];
+  __shared__ int Sst[2][kBlk];
+  __shared__ int Smax[2];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int g = lane / 32, c = lane % 32;
-  const int kblk = blockIdx.x;  // the longest causal columns are the first
-  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int nk = (S + kRows - 1) / kRows;
+  int bh, kblk;
+  UnitOf(nk, bh, kblk);  // rank 0 = the first keys, the longest columns
+  const int b = bh / H, h = bh % H;
   const size_t ld = static_cast<size_t>(H) * D;
   const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * D;
   const int j0w = kblk * kRows + wave * 32;
@@ -418,21 +518,71 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
 
   const int blk_first = (kblk * kRows) / kBlk;
   const int nblk = (S + kBlk - 1) / kBlk - blk_first;
-  St sq, sd;
+  const uint32_t ld32 = static_cast<uint32_t>(ld);
+  const uint32_t slice_bytes = static_cast<uint32_t>(((S - 1) * ld + D) * 4);
+  St sq(ld32), sd(ld32);
   auto load = [&](int ib) {
     const int r0 = (blk_first + ib) * kBlk;
-    sq.load(q + base, ld, r0, S - r0);
-    sd.load(dout + base, ld, r0, S - r0);
+    sq.load(q + base, slice_bytes, ld32, r0);
+    sd.load(dout + base, slice_bytes, ld32, r0);
   };
   auto stage = [&](int buf, int ib) {
     sq.store(Qs[buf], kDK ? Qt[buf] : nullptr);
     sd.store(kDK ? Ds[buf] : nullptr, kDV ? Dt[buf] : nullptr);
-    const int r0 = (blk_first + ib) * kBlk;
-    if (threadIdx.x < kBlk)
-      Sts[buf][threadIdx.x] = r0 + threadIdx.x < S ? st_bh[r0 + threadIdx.x] : make_float4(0.f, 1.f, 0.f, 0.f);
+    if (threadIdx.x < kBlk) {  // wave 0
+      const int t = threadIdx.x, iq = (blk_first + ib) * kBlk + t;
+      int start = 0;
+      if (iq < S) {
+        const float4 s4 = st_bh[iq];
+        Smm[buf][t] = RowOffset(s4.x, s4.y);
+        Sdl[buf][t] = s4.z;
+        start = static_cast<int>(StatsStart(s4.w, iq));
+      } else {
+        Smm[buf][t] = 0.0f;
+        Sdl[buf][t] = 0.0f;
+      }
+      Sst[buf][t] = start;
+      const int mx = WaveMaxI(start);
+      if (t == 0) Smax[buf] = mx;
+    }
   };
 
   v16f dka[D / 32] = {}, dva[D / 32] = {};
+  auto run = [&](auto masked, int buf, int r0) {
+    constexpr bool kMask = decltype(masked)::value;
+    v16f sc[2], dpt[2];
+    ScoreTiles<D>(Qs[buf], kf, lane, sc);
+    if (kDK) ScoreTiles<D>(Ds[buf], vf, lane, dpt);
+    bf16x8 pb[4], wb[4];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      float p[16], w[16];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int il0 = kt * 32 + 8 * q4 + 4 * g;  // rows il0 .. il0 + 3
+        const float4 mm4 = *reinterpret_cast<const float4*>(&Smm[buf][il0]);
+        const float4 dl4 = *reinterpret_cast<const float4*>(&Sdl[buf][il0]);
+        const float mmv[4] = {mm4.x, mm4.y, mm4.z, mm4.w};
+        const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * q4 + e;
+          float pp = Exp2(__builtin_fmaf(sc[kt][r], c2, -mmv[e]));
+          if constexpr (kMask) {
+            const int iq = r0 + il0 + e;
+            pp = (iq < S && j <= iq && j >= Sst[buf][il0 + e]) ? pp : 0.0f;
+          }
+          p[r] = pp;
+          if (kDK) w[r] = (pp * (dpt[kt][r] - dlv[e])) * isd;
+        }
+      }
+      if (kDV) PackTile(p, pb + 2 * kt);
+      if (kDK) PackTile(w, wb + 2 * kt);
+    }
+    if (kDK) AccumTiles<D>(Qt[buf], wb, lane, dka);
+    if (kDV) AccumTiles<D>(Dt[buf], pb, lane, dva);
+  };
+
   load(0);
   stage(0, 0);
   __syncthreads();
@@ -440,26 +590,10 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
     const int buf = ib & 1;
     if (ib + 1 < nblk) load(ib + 1);
     const int r0 = (blk_first + ib) * kBlk;
-    if (r0 + kBlk - 1 >= j0w) {  // some query of the block reaches this wave's keys
-      v16f sc[2], dpt[2];
-      ScoreTiles<D>(Qs[buf], kf, lane, sc);
-      if (kDK) ScoreTiles<D>(Ds[buf], vf, lane, dpt);
-      float p[2][16], w[2][16];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int il = kt * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-          const int iq = r0 + il;
-          const float4 s4 = Sts[buf][il];
-          const bool ok = iq < S && j < S && j <= iq && static_cast<size_t>(j) >= StatsStart(s4.w, iq);
-          const float pp = ok ? Exp2(sc[kt][r] * c2 - s4.x * kLog2e) * s4.y : 0.0f;
-          p[kt][r] = pp;
-          if (kDK) w[kt][r] = ok ? (pp * (dpt[kt][r] - s4.z)) * isd : 0.0f;
-        }
-      if (kDK) AccumTiles<D>(Qt[buf], w, lane, dka);
-      if (kDV) AccumTiles<D>(Dt[buf], p, lane, dva);
-    }
+    if (r0 >= j0w + 31 && r0 + kBlk <= S && Smax[buf] <= j0w)
+      run(std::false_type{}, buf, r0);
+    else if (r0 + kBlk - 1 >= j0w)  // some query of the block reaches this wave's keys
+      run(std::true_type{}, buf, r0);
     if (ib + 1 < nblk) stage(buf ^ 1, ib + 1);
     __syncthreads();
   }
@@ -480,11 +614,22 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
 
 }  // namespace
 
+// The staging reads address one (b, h) slice with 32-bit byte offsets, and
+// the grid is one-dimensional.
+bool FlashFits(size_t B, size_t S, size_t H, size_t d) {
+  return S > 0 && S * H * d * 4 < (size_t{1} << 31) &&
+         (S + kRows - 1) / kRows * B * H < (size_t{1} << 31);
+}
+
+// One workgroup per (b, h, 128-row block), a 1D grid regrouped per XCD.
+inline dim3 FlashGrid(size_t B, size_t S, size_t H) {
+  return dim3(static_cast<unsigned>((S + kRows - 1) / kRows * B * H));
+}
 
 hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float* o, float* stats,
                           size_t B, size_t S, size_t H, size_t d, const int32_t* starts,
                           hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((S + kRows - 1) / kRows), static_cast<unsigned>(B * H));
+  const dim3 grid = FlashGrid(B, S, H);
   if (d == 64)
     hipLaunchKernelGGL(FlashFwd<64>, grid, dim3(kFThreads), 0, s, q, k, v, o, stats,
                        static_cast<int>(S), static_cast<int>(H), starts);
@@ -497,7 +642,7 @@ hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float*
 hipError_t LaunchFlashDQ(const float* q, const float* k, const float* v, const float* dout,
                          float* stats, float* dq, size_t B, size_t S, size_t H, size_t d,
                          int delta_given, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((S + kRows - 1) / kRows), static_cast<unsigned>(B * H));
+  const dim3 grid = FlashGrid(B, S, H);
   if (d == 64)
     hipLaunchKernelGGL(FlashDQ<64>, grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dq,
                        static_cast<int>(S), static_cast<int>(H), delta_given);
@@ -510,7 +655,7 @@ hipError_t LaunchFlashDQ(const float* q, const float* k, const float* v, const f
 hipError_t LaunchFlashDKDV(const float* q, const float* k, const float* v, const float* dout,
                            const float* stats, float* dk, float* dv, size_t B, size_t S, size_t H,
                            size_t d, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((S + kRows - 1) / kRows), static_cast<unsigned>(B * H));
+  const dim3 grid = FlashGrid(B, S, H);
   const int Si = static_cast<int>(S), Hi = static_cast<int>(H);
 #define SEEAI_DKDV(DD, A, Bv)                                                                  \
   hipLaunchKernelGGL((FlashDKDV<DD, A, Bv>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dk, \
@@ -520,8 +665,8 @@ hipError_t LaunchFlashDKDV(const float* q, const float* k, const float* v, const
     else if (dk) SEEAI_DKDV(64, true, false);
     else SEEAI_DKDV(64, false, true);
   } else {
-    if (dk && dv) SEEAI_DKDV(128, true, true);
-    else if (dk) SEEAI_DKDV(128, true, false);
+    if (dk && dv) return hipErrorInvalidValue;  // d = 128 runs the passes apart
+    if (dk) SEEAI_DKDV(128, true, false);
     else SEEAI_DKDV(128, false, true);
   }
 #undef SEEAI_DKDV
