@@ -153,14 +153,6 @@ int seeai_attn_dv(seeai_ctx* ctx, int dtype, const float* d_q,
                   const float* d_k, const float* d_dout, const float* d_stats,
                   float* d_dv, uint64_t B, uint64_t S, uint64_t H,
                   uint64_t d);
-/* dK and dV in one call: the results of seeai_attn_dk then seeai_attn_dv,
- * formed in one pass over the score tiles for dtype 1 at d in {64, 128}.
- * The executor takes this path for a kAttnDKTiled / kAttnDVTiled pair that
- * shares its inputs (attention.cc:537-590 run as one). */
-int seeai_attn_dkdv(seeai_ctx* ctx, int dtype, const float* d_q,
-                    const float* d_k, const float* d_v, const float* d_dout,
-                    const float* d_stats, float* d_dk, float* d_dv, uint64_t B,
-                    uint64_t S, uint64_t H, uint64_t d);
 
 /* SoftmaxXEntFwd / Bwd and the masked pair (loss.cc:35-126). */
 int seeai_xent_fwd(seeai_ctx* ctx, const float* d_logits,

@@ -10,6 +10,10 @@ Flags:
                       keeps the compiler from forming packed-f32 VALU ops
                       (this pool's rule; the host pass warns it does not know
                       the feature, which is harmless)
+  -mllvm -amdgpu-mfma-vgpr-form  (k_flash.hip only)
+                      MFMA accumulators in VGPRs: the attention kernels run
+                      VALU softmax on every score tile, and AGPR-resident
+                      tiles cost a copy per element each way
 """
 from __future__ import annotations
 
@@ -33,6 +37,9 @@ COMMON = [
 ]
 
 
+PER_FILE = {"k_flash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def sources():
     out = []
     for name in sorted(os.listdir(CSRC)):
@@ -43,7 +50,7 @@ def sources():
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *PER_FILE.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)

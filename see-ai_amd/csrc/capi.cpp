@@ -525,50 +525,6 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
   }
 }
 
-// kAttnDKTiled followed at once by kAttnDVTiled over the same q, k, dO,
-// stats and geometry (the order the planner emits a tiled attention
-// backward in) runs as one pass that forms each score tile once.  Sound
-// only when neither output overlaps an input of the pair or the other
-// output: the fused pass interleaves what the pair does in turn.
-bool FusableDKDV(const Instruction& a, const Instruction& b) {
-  if (a.opcode != 49 || b.opcode != 50 || a.flags != b.flags) return false;
-  if (a.in[0] != b.in[0] || a.in[1] != b.in[1] || a.in[3] != b.in[3] || a.out[0] != b.out[0] ||
-      a.out[2] != b.out[2])
-    return false;
-  const uint64_t g = a.out[2];
-  const uint64_t B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
-  const uint64_t t = B * S * H * d * 4, st = B * H * S * 16;
-  struct Ext {
-    uint64_t ref, bytes;
-  };
-  auto overlap = [](Ext x, Ext y) {
-    // Distinct segments (arena / rodata / source) never overlap.
-    if ((x.ref & (kRodataBit | kSourceBit)) != (y.ref & (kRodataBit | kSourceBit))) return false;
-    const uint64_t xo = x.ref & ~(kRodataBit | kSourceBit), yo = y.ref & ~(kRodataBit | kSourceBit);
-    return xo < yo + y.bytes && yo < xo + x.bytes;
-  };
-  const Ext dk{a.out[1], t}, dv{b.out[1], t};
-  const Ext ins[] = {{a.in[0], t}, {a.in[1], t}, {a.in[2], t}, {a.in[3], t}, {a.out[0], st}};
-  if (overlap(dk, dv)) return false;
-  for (const Ext& x : ins)
-    if (overlap(dk, x) || overlap(dv, x)) return false;
-  return true;
-}
-
-int ExecuteDKDV(seeai_ctx* c, const Instruction& a, const Instruction& b) {
-  const Ptrs R{c};
-  const uint64_t g = a.out[2];
-  const uint64_t B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
-  const int dt = (a.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
-  c->relaxed += 2 * dt;
-  SEEAI_TRY(c,
-            LaunchAttnDKDVTiled(dt, R.f(a.in[0]), R.f(a.in[1]), R.f(a.in[2]), R.f(a.in[3]),
-                                R.f(a.out[0]), R.f(a.out[1]), R.f(b.out[1]), B, S, H, d,
-                                c->stream),
-            "attn.dkdv_tiled");
-  return SEEAI_OK;
-}
-
 }  // namespace
 
 extern "C" {
@@ -698,19 +654,6 @@ int seeai_execute_range(seeai_ctx* c, const void* instructions, uint64_t count,
   if (!c || (!instructions && count)) return SEEAI_INVALID;
   const auto* base = static_cast<const uint8_t*>(instructions);
   for (uint64_t i = 0; i < count; ++i) {
-    if (i + 1 < count && c->arena) {
-      Instruction a, b;
-      std::memcpy(&a, base + i * 64, sizeof a);
-      std::memcpy(&b, base + (i + 1) * 64, sizeof b);
-      if (FusableDKDV(a, b)) {
-        if (int rc = ExecuteDKDV(c, a, b)) {
-          if (failed_at) *failed_at = i;
-          return rc;
-        }
-        ++i;
-        continue;
-      }
-    }
     if (int rc = seeai_execute(c, base + i * 64, params)) {
       if (failed_at) *failed_at = i;
       return rc;
@@ -844,15 +787,6 @@ int seeai_attn_dk(seeai_ctx* c, int dtype, const float* q, const float* k, const
   SEEAI_TRY(c, LaunchAttnDKTiled(dtype, q, k, v, dout, stats, dk, B, S, H, d, c->stream), "attn_dk");
   return SEEAI_OK;
 }
-int seeai_attn_dkdv(seeai_ctx* c, int dtype, const float* q, const float* k, const float* v,
-                    const float* dout, const float* stats, float* dk, float* dv, uint64_t B,
-                    uint64_t S, uint64_t H, uint64_t d) {
-  if (!c || dtype < 0 || dtype > 1) return Fail(c, SEEAI_INVALID, "attn_dkdv: dtype is 0 or 1");
-  SEEAI_TRY(c, LaunchAttnDKDVTiled(dtype, q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
-            "attn_dkdv");
-  return SEEAI_OK;
-}
-
 int seeai_attn_dv(seeai_ctx* c, int dtype, const float* q, const float* k, const float* dout,
                   const float* stats, float* dv, uint64_t B, uint64_t S, uint64_t H, uint64_t d) {
   if (!c || dtype < 0 || dtype > 1) return Fail(c, SEEAI_INVALID, "attn_dv: dtype is 0 or 1");

@@ -234,13 +234,8 @@ hipError_t LaunchAttnDKTiled(int dtype, const float* q, const float* k, const fl
 hipError_t LaunchAttnDVTiled(int dtype, const float* q, const float* k, const float* dout,
                              const float* stats, float* dv, size_t B, size_t S, size_t H,
                              size_t d, hipStream_t s);
-// dK and dV together: the fused bf16 pass for the relaxed family at d in
-// {64, 128}, otherwise the two exact passes in turn.
-hipError_t LaunchAttnDKDVTiled(int dtype, const float* q, const float* k, const float* v,
-                               const float* dout, const float* stats, float* dk, float* dv,
-                               size_t B, size_t S, size_t H, size_t d, hipStream_t s);
 // Relaxed tiled attention on bf16 MFMA (k_flash.hip), d in {64, 128}; dk or
-// dv may be null in LaunchFlashDKDV (both non-null = the fused pass, d = 64 only).
+// exactly one of dk, dv is non-null in LaunchFlashDKDV.
 bool FlashFits(size_t B, size_t S, size_t H, size_t d);
 hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float* o, float* stats,
                           size_t B, size_t S, size_t H, size_t d, const int32_t* starts,

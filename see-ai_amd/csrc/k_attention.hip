@@ -580,18 +580,6 @@ hipError_t LaunchAttnDVTiled(int dtype, const float* q, const float* k, const fl
   return hipGetLastError();
 }
 
-hipError_t LaunchAttnDKDVTiled(int dtype, const float* q, const float* k, const float* v,
-                               const float* dout, const float* stats, float* dk, float* dv,
-                               size_t B, size_t S, size_t H, size_t d, hipStream_t s) {
-  if (B * H * S == 0) return hipSuccess;
-  // The fused bf16 pass holds both accumulators and both score tiles; at
-  // d = 128 that exceeds the register file, so there the passes run apart.
-  if (dtype && d == 64 && FlashFits(B, S, H, d) && MfmaShape(d, q, k) && MfmaShape(d, v, dout) && MfmaShape(d, dk, dv))
-    return LaunchFlashDKDV(q, k, v, dout, stats, dk, dv, B, S, H, d, s);
-  const hipError_t e = LaunchAttnDKTiled(dtype, q, k, v, dout, stats, dk, B, S, H, d, s);
-  return e != hipSuccess ? e : LaunchAttnDVTiled(dtype, q, k, dout, stats, dv, B, S, H, d, s);
-}
-
 hipError_t LaunchAttnFwdCached(const float* q, const float* k, const float* v, float* o,
                                float* probs, size_t B, size_t S, size_t H, size_t d,
                                const int32_t* starts, hipStream_t s) {

@@ -1,6 +1,6 @@
 // k_flash.hip -- the relaxed (kFlagRelaxed, instruction.h:356-384) tiled
-// attention family on CDNA4 bf16 MFMA: forward, dQ, and dK / dV (fused when
-// both are wanted), over the stats-row contract of the exact family
+// attention family on CDNA4 bf16 MFMA: forward, dQ, dK and dV
+// over the stats-row contract of the exact family
 // (instruction.h:174-190, 234-259).  Operands arrive as f32 and are rounded
 // to bf16 (RNE) as they are staged; products accumulate in f32; softmax
 // runs in f32 in the base-2 domain.
@@ -30,12 +30,16 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Word 3 of a raw (stride 0) buffer resource on CDNA: 32-bit data format,
 // out-of-range reads return zero.
 constexpr int kRsrcWord3 = 0x00020000;
 
 __device__ __forceinline__ float Exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// A wave-uniform value held in a vector register, as a scalar.
+__device__ __forceinline__ int Uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 __device__ __forceinline__ v16f Mfma(const bf16x8& a, const bf16x8& b, const v16f& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -66,6 +70,7 @@ struct Stager {
   static constexpr int TLD = kBlk + 4;     // transposed tile stride (bf16)
   static constexpr int kD4 = D / 4;
   static constexpr int kPasses = (kBlk / 4) * kD4 / kFThreads;  // 1 (D=64) or 2 (D=128)
+  static constexpr int kPassRows = kBlk / kPasses;                 // rows one pass covers
   float4 reg[kPasses][4];
   uint32_t voff[kPasses][4];
 
@@ -78,14 +83,12 @@ struct Stager {
       for (int k = 0; k < 4; ++k) voff[p][k] = ((rg * 4 + k) * ld + d4 * 4) * 4u;
     }
   }
-  // slice: row 0 of the (b, h) slice; slice_bytes: through the end of its
-  // last valid row; rows row0 .. row0 + 63 are read.
   __device__ __forceinline__ void load(const float* slice, uint32_t slice_bytes, uint32_t ld,
                                        int row0) {
     const uint32_t skip = static_cast<uint32_t>(row0) * ld * 4u;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(slice) + static_cast<size_t>(row0) * ld, 0,
-        static_cast<int>(slice_bytes - skip), kRsrcWord3);
+        Uniform(static_cast<int>(slice_bytes - skip)), kRsrcWord3);
 #pragma unroll
     for (int p = 0; p < kPasses; ++p)
 #pragma unroll
@@ -117,37 +120,45 @@ struct Stager {
   }
 };
 
-// This lane's 32 owned rows as a B (or A) operand over D dims: row c of the
-// wave's tile, dims 16s + 8g .. +8.
+// This lane's 32 owned rows as a B (or A) operand over D dims, scaled by
+// `scale` before rounding: row c of the wave's tile, dims 16s + 8g .. +8.
 template <int D>
-__device__ __forceinline__ void LoadOwned(const float* __restrict__ row, int g, bf16x8* out) {
+__device__ __forceinline__ void LoadOwned(const float* __restrict__ row, int g, float scale,
+                                          bf16x8* out) {
 #pragma unroll
   for (int s = 0; s < D / 16; ++s) {
     const float4 a = *reinterpret_cast<const float4*>(row + 16 * s + 8 * g);
     const float4 b = *reinterpret_cast<const float4*>(row + 16 * s + 8 * g + 4);
-    out[s] = bf16x8{static_cast<__bf16>(a.x), static_cast<__bf16>(a.y), static_cast<__bf16>(a.z),
-                    static_cast<__bf16>(a.w), static_cast<__bf16>(b.x), static_cast<__bf16>(b.y),
-                    static_cast<__bf16>(b.z), static_cast<__bf16>(b.w)};
+    out[s] = bf16x8{static_cast<__bf16>(a.x * scale), static_cast<__bf16>(a.y * scale),
+                    static_cast<__bf16>(a.z * scale), static_cast<__bf16>(a.w * scale),
+                    static_cast<__bf16>(b.x * scale), static_cast<__bf16>(b.y * scale),
+                    static_cast<__bf16>(b.z * scale), static_cast<__bf16>(b.w * scale)};
   }
 }
 
-// acc[kt] (32 streamed rows kt*32.. of the block x this wave's 32 owned
-// columns) = rowtile[kt*32 + c] . owned[c] over D dims.
+// acc = init + rowtile[kt*32 + c] . owned[c] over D dims: 32 streamed rows
+// kt*32.. of the block x this wave's 32 owned columns.  The accumulator
+// starts from `init`, which carries each element's offset (the softmax
+// row offset, or -delta) so the product arrives already shifted.
 template <int D>
-__device__ __forceinline__ void ScoreTiles(const __bf16* __restrict__ tile, const bf16x8* owned,
-                                           int lane, v16f* acc) {
+__device__ __forceinline__ v16f ScoreTile(const __bf16* __restrict__ tile, const bf16x8* owned,
+                                          int lane, int kt, const v16f& init) {
   constexpr int RLD = D + 8;
   const int g = lane / 32, c = lane % 32;
+  v16f a = init;
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    v16f a = {};
-#pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(tile + (kt * 32 + c) * RLD + 16 * s + 8 * g);
-      a = Mfma(kf, owned[s], a);
-    }
-    acc[kt] = a;
+  for (int s = 0; s < D / 16; ++s) {
+    const bf16x8 kf = *reinterpret_cast<const bf16x8*>(tile + (kt * 32 + c) * RLD + 16 * s + 8 * g);
+    a = Mfma(kf, owned[s], a);
   }
+  return a;
+}
+
+__device__ __forceinline__ v16f Splat(float x) {
+  v16f v;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) v[r] = x;
+  return v;
 }
 
 // The weights of one 32-row score tile kt (this lane's 16 values, rows
@@ -185,14 +196,29 @@ __device__ __forceinline__ void AccumTiles(const __bf16* __restrict__ trans, con
 
 __device__ __forceinline__ float SwapMax(float v) { return fmaxf(v, __shfl_xor(v, 32, kWave)); }
 __device__ __forceinline__ float SwapSum(float v) { return v + __shfl_xor(v, 32, kWave); }
+// Wave maximum, returned as a scalar (the value is the same in every lane).
 __device__ __forceinline__ int WaveMaxI(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
-  return v;
+  return __builtin_amdgcn_readfirstlane(v);
 }
 
-// Streamed row of score element r of tile kt, relative to the block start.
+
+// Streamed row of score element r of tile kt, relative to the block start;
+// RowConst is its lane-independent part (the lane adds 4g).
 __device__ __forceinline__ int RowOf(int kt, int r, int g) { return kt * 32 + 8 * (r / 4) + 4 * g + (r % 4); }
+__device__ __forceinline__ constexpr int RowConst(int kt, int r) { return kt * 32 + 8 * (r / 4) + (r % 4); }
+
+// Masks built from sign bits rather than comparisons, so the 32 per-element
+// tests of a diagonal block stay in vector registers: all ones when a < 0
+// or b < 0.
+__device__ __forceinline__ int Outside(int a, int b) { return (a | b) >> 31; }
+// x where the mask is clear, -inf where it is set.
+__device__ __forceinline__ float OrNegInf(float x, int bad) {
+  return __int_as_float((__float_as_int(x) & ~bad) | (static_cast<int>(0xff800000u) & bad));
+}
+// x where the mask is clear, +0 where it is set.
+__device__ __forceinline__ float OrZero(float x, int bad) { return __int_as_float(__float_as_int(x) & ~bad); }
 
 // Work unit of this workgroup: (bh, rank) with rank 0 the heaviest of the
 // nq row blocks of one (b, h).  Consecutive workgroup ids land on the 8 XCDs
@@ -206,11 +232,15 @@ __device__ __forceinline__ void UnitOf(int nq, int& bh, int& rank) {
 }
 
 // ---------------------------------------------------------------------------
-// Forward: O = softmax(mask(Q K^T / sqrt d)) V and the stats row.  The
-// running maximum used for the exponentials moves only when a block's
-// maximum exceeds it by more than 2^8 (values stay below 2^8 in f32); the
-// true row maximum is tracked beside it and the stats row is stated against
-// it, so the row (m, 1/l) is the reference's.
+// Forward: O = softmax(mask(Q K^T / sqrt d)) V and the stats row.
+//
+// Q is staged pre-scaled by log2(e)/sqrt(d), so a score tile is in base-2
+// units, and its accumulator starts at -m_use: the tile arrives as
+// s' - m_use and one v_exp gives the weight.  m_use moves only when a
+// block's maximum exceeds it by more than 2^8 (weights stay below 2^8 in
+// f32) or on the first block a row sees; the true row maximum is tracked
+// beside it and the stats row is stated against it, so (m, 1/l) is the
+// reference's.  l sums the bf16-rounded weights that the P V product uses.
 // ---------------------------------------------------------------------------
 constexpr float kLazy = 8.0f;
 
@@ -245,16 +275,17 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
   atomicMin(&min_start, j_start);  // integer min: order-independent
   __syncthreads();
   const int wave_max_start = WaveMaxI(j_start);
-  const int blk_lo = min_start / kBlk;
+  const int blk_lo = Uniform(min_start) / kBlk;
   const int q_hi = min(qblk * kRows + kRows - 1, S - 1);
   const int nblk = q_hi / kBlk + 1 - blk_lo;
 
   bf16x8 qf[D / 16];
-  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, qf);
-  const float c2 = (1.0f / sqrtf(static_cast<float>(D))) * kLog2e;
+  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, kLog2e / sqrtf(static_cast<float>(D)), qf);
 
   v16f oacc[D / 32] = {};
-  float m_use = -INFINITY, m_true = -INFINITY, l = 0.0f;
+  float m_use = 0.0f, m_true = -INFINITY, l = 0.0f;
+  v16f cneg = {};  // splat(-m_use)
+  const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
   const uint32_t ld32 = static_cast<uint32_t>(ld);
   const uint32_t slice_bytes = static_cast<uint32_t>(((S - 1) * ld + D) * 4);
   St sk(ld32), sv(ld32);
@@ -265,29 +296,33 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
   };
   auto block = [&](auto masked, int buf, int j0) {
     constexpr bool kMask = decltype(masked)::value;
+    const int hi_rel = i - j0 - 4 * g, lo_rel = j_start - j0 - 4 * g;
     v16f st[2];
-    ScoreTiles<D>(Ks[buf], qf, lane, st);
     float bmax = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < 2; ++kt) {
+      st[kt] = ScoreTile<D>(Ks[buf], qf, lane, kt, cneg);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        if constexpr (kMask) {
-          const int j = j0 + RowOf(kt, r, g);
-          if (j > i || j < j_start) st[kt][r] = -INFINITY;
-        }
+        if constexpr (kMask)  // keep j0 + row in [j_start, i]
+          st[kt][r] = OrNegInf(st[kt][r], Outside(hi_rel - RowConst(kt, r), RowConst(kt, r) - lo_rel));
         bmax = fmaxf(bmax, st[kt][r]);
       }
-    const float mb = SwapMax(bmax) * c2;
-    m_true = fmaxf(m_true, mb);
-    const bool need = mb > m_use + kLazy;
+    }
+    bmax = SwapMax(bmax);  // relative to m_use
+    const bool first = m_true == -INFINITY;
+    if (bmax != -INFINITY) m_true = fmaxf(m_true, m_use + bmax);
+    const bool need = first ? bmax != -INFINITY : bmax > kLazy;
     if (__any(need)) {
-      const float m_new = need ? mb : m_use;
-      const float alpha = !need ? 1.0f : (m_use == -INFINITY ? 0.0f : Exp2(m_use - m_new));
-      m_use = m_new;
+      const float shift = need ? bmax : 0.0f;
+      const float alpha = first ? 0.0f : Exp2(-shift);
+      m_use += shift;
+      cneg = Splat(-m_use);
       l *= alpha;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= alpha;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) st[kt] -= shift;
     }
     bf16x8 pb[4];
     float psum = 0.0f;
@@ -295,13 +330,14 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
     for (int kt = 0; kt < 2; ++kt) {
       float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float e = Exp2(__builtin_fmaf(st[kt][r], c2, -m_use));
-        if constexpr (kMask) e = st[kt][r] == -INFINITY ? 0.0f : e;
-        p[r] = e;
-        psum += e;
-      }
+      for (int r = 0; r < 16; ++r) p[r] = Exp2(st[kt][r]);
       PackTile(p, pb + 2 * kt);
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          psum = __builtin_amdgcn_fdot2_f32_bf16(
+              bf16x2{pb[2 * kt + h2][2 * e], pb[2 * kt + h2][2 * e + 1]}, ones, psum, false);
     }
     l += SwapSum(psum);
     AccumTiles<D>(Vt[buf], pb, lane, oacc);
@@ -344,12 +380,15 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
   }
 }
 
-// Row offset of the base-2 exponent: p = 2^(s c2 - mm) with mm = m log2(e)
-// + log2(l), from the stats row (m, 1/l).
+// Row offset of the base-2 exponent: p = 2^(s' - mm) with s' = s log2(e)
+// and mm = m log2(e) + log2(l), from the stats row (m, 1/l).
 __device__ __forceinline__ float RowOffset(float m, float inv) { return m * kLog2e - log2f(inv); }
 
 // ---------------------------------------------------------------------------
-// dQ: pass 1 delta = sum_j p dP, pass 2 dS = p (dP - delta), dQ^T = K^T dS^T.
+// dQ: pass 1 delta = sum_j p dP, pass 2 dS = p (dP - delta), dQ^T = K^T dS^T
+// (times 1/sqrt d once, at the end).  Q is staged pre-scaled as in the
+// forward and the score accumulators start at -mm; in pass 2 the dP
+// accumulators start at -delta.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ void __launch_bounds__(kFThreads)
@@ -374,22 +413,21 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
   const int i = i0 + c;
   const int ic = min(i, S - 1);
   float* st = stats + (static_cast<size_t>(bh) * S + ic) * 4;
-  const float mm = RowOffset(st[0], st[1]);
+  const v16f cs = Splat(-RowOffset(st[0], st[1]));
   const int j_start = static_cast<int>(StatsStart(st[3], ic));
   if (threadIdx.x == 0) min_start = S;
   __syncthreads();
   atomicMin(&min_start, j_start);
   __syncthreads();
   const int wave_max_start = WaveMaxI(j_start);
-  const int blk_lo = min_start / kBlk;
+  const int blk_lo = Uniform(min_start) / kBlk;
   const int q_hi = min(qblk * kRows + kRows - 1, S - 1);
   const int nblk = q_hi / kBlk + 1 - blk_lo;
   const float isd = 1.0f / sqrtf(static_cast<float>(D));
-  const float c2 = isd * kLog2e;
 
   bf16x8 qf[D / 16], df[D / 16];
-  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, qf);
-  LoadOwned<D>(dout + base + static_cast<size_t>(ic) * ld, g, df);
+  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, kLog2e * isd, qf);
+  LoadOwned<D>(dout + base + static_cast<size_t>(ic) * ld, g, 1.0f, df);
 
   const uint32_t ld32 = static_cast<uint32_t>(ld);
   const uint32_t slice_bytes = static_cast<uint32_t>(((S - 1) * ld + D) * 4);
@@ -399,48 +437,34 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
     sk.load(k + base, slice_bytes, ld32, j0);
     sv.load(v + base, slice_bytes, ld32, j0);
   };
-  // p and dP of one block; masked entries get p = 0.
-  auto probs = [&](auto masked, int buf, int j0, float (*p)[16], v16f* dpt) {
-    constexpr bool kMask = decltype(masked)::value;
-    v16f sc[2];
-    ScoreTiles<D>(Ks[buf], qf, lane, sc);
-    ScoreTiles<D>(Vs[buf], df, lane, dpt);
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float e = Exp2(__builtin_fmaf(sc[kt][r], c2, -mm));
-        if constexpr (kMask) {
-          const int j = j0 + RowOf(kt, r, g);
-          e = (j <= i && j >= j_start) ? e : 0.0f;
-        }
-        p[kt][r] = e;
-      }
-  };
 
   float delta = 0.0f;
   for (int pass = delta_given ? 1 : 0; pass < 2; ++pass) {
     if (pass == 1 && delta_given) delta = st[2];
+    const v16f cp = Splat(-delta);  // pass 1: dP - delta
     v16f acc[D / 32] = {};
     auto run = [&](auto masked, int buf, int j0) {
-      float p[2][16];
-      v16f dpt[2];
-      probs(masked, buf, j0, p, dpt);
-      if (pass == 0) {
+      constexpr bool kMask = decltype(masked)::value;
+      const int hi_rel = i - j0 - 4 * g, lo_rel = j_start - j0 - 4 * g;
+      bf16x8 wb[4];
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < 2; ++kt) {
+        const v16f sc = ScoreTile<D>(Ks[buf], qf, lane, kt, cs);
+        const v16f dpt = ScoreTile<D>(Vs[buf], df, lane, kt, cp);
+        float w[16];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) delta = __builtin_fmaf(dpt[kt][r], p[kt][r], delta);
-      } else {
-        bf16x8 wb[4];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) p[kt][r] = (p[kt][r] * (dpt[kt][r] - delta)) * isd;
-          PackTile(p[kt], wb + 2 * kt);
+        for (int r = 0; r < 16; ++r) {
+          float e = Exp2(sc[r]);
+          if constexpr (kMask)  // keep j0 + row in [j_start, i]
+            e = OrZero(e, Outside(hi_rel - RowConst(kt, r), RowConst(kt, r) - lo_rel));
+          if (pass == 0)
+            delta = __builtin_fmaf(dpt[r], e, delta);
+          else
+            w[r] = e * dpt[r];
         }
-        AccumTiles<D>(Kt[buf], wb, lane, acc);
+        if (pass == 1) PackTile(w, wb + 2 * kt);
       }
+      if (pass == 1) AccumTiles<D>(Kt[buf], wb, lane, acc);
     };
     load(0);
     sk.store(Ks[0], pass ? Kt[0] : nullptr);
@@ -471,28 +495,32 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq)
           *reinterpret_cast<float4*>(drow + dt * 32 + 8 * qq + 4 * g) =
-              make_float4(acc[dt][4 * qq], acc[dt][4 * qq + 1], acc[dt][4 * qq + 2], acc[dt][4 * qq + 3]);
+              make_float4(acc[dt][4 * qq] * isd, acc[dt][4 * qq + 1] * isd, acc[dt][4 * qq + 2] * isd,
+                          acc[dt][4 * qq + 3] * isd);
       if (g == 0 && !delta_given) st[2] = delta;
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV: one wave per 32 keys walking the query blocks from the diagonal;
-// S = Q K^T and dP = dO V^T formed query-major, dK^T += Q^T dS, dV^T += dO^T P.
+// dK or dV: one wave per 32 keys walking the query blocks from the diagonal;
+// S = Q K^T and dP = dO V^T formed query-major, dK^T += Q^T dS (times
+// 1/sqrt d at the end), dV^T += dO^T P.  K is staged pre-scaled as in the
+// forward; the score and dP accumulators start at each query row's -mm and
+// -delta, read from LDS.
 // ---------------------------------------------------------------------------
-template <int D, bool kDK, bool kDV>
+template <int D, bool kDK>
 __global__ void __launch_bounds__(kFThreads)
 FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-          const float* __restrict__ dout, const float* __restrict__ stats, float* __restrict__ dk,
-          float* __restrict__ dv, int S, int H) {
+          const float* __restrict__ dout, const float* __restrict__ stats, float* __restrict__ out,
+          int S, int H) {
   using St = Stager<D>;
   __shared__ __attribute__((aligned(16))) __bf16 Qs[2][kBlk * St::RLD];
   __shared__ __attribute__((aligned(16))) __bf16 Qt[2][kDK ? D * St::TLD : 1];
   __shared__ __attribute__((aligned(16))) __bf16 Ds[2][kDK ? kBlk * St::RLD : 1];
-  __shared__ __attribute__((aligned(16))) __bf16 Dt[2][kDV ? D * St::TLD : 1];
-  // Per streamed query row: exponent offset, delta, document start; and the
-  // block's largest start.
+  __shared__ __attribute__((aligned(16))) __bf16 Dt[2][kDK ? 1 : D * St::TLD];
+  // Per streamed query row: -mm, -delta, document start; and the block's
+  // largest start.
   __shared__ __attribute__((aligned(16))) float Smm[2][kBlk];
   __shared__ __attribute__((aligned(16))) float Sdl[2][kBlk];
   __shared__ int Sst[2][kBlk];
@@ -509,12 +537,11 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
   const int j = j0w + c;
   const int jc = min(j, S - 1);
   const float isd = 1.0f / sqrtf(static_cast<float>(D));
-  const float c2 = isd * kLog2e;
   const float4* st_bh = reinterpret_cast<const float4*>(stats) + static_cast<size_t>(bh) * S;
 
   bf16x8 kf[D / 16], vf[D / 16];
-  LoadOwned<D>(k + base + static_cast<size_t>(jc) * ld, g, kf);
-  if (kDK) LoadOwned<D>(v + base + static_cast<size_t>(jc) * ld, g, vf);
+  LoadOwned<D>(k + base + static_cast<size_t>(jc) * ld, g, kLog2e * isd, kf);
+  if (kDK) LoadOwned<D>(v + base + static_cast<size_t>(jc) * ld, g, 1.0f, vf);
 
   const int blk_first = (kblk * kRows) / kBlk;
   const int nblk = (S + kBlk - 1) / kBlk - blk_first;
@@ -528,17 +555,17 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
   };
   auto stage = [&](int buf, int ib) {
     sq.store(Qs[buf], kDK ? Qt[buf] : nullptr);
-    sd.store(kDK ? Ds[buf] : nullptr, kDV ? Dt[buf] : nullptr);
+    sd.store(kDK ? Ds[buf] : nullptr, kDK ? nullptr : Dt[buf]);
     if (threadIdx.x < kBlk) {  // wave 0
       const int t = threadIdx.x, iq = (blk_first + ib) * kBlk + t;
       int start = 0;
       if (iq < S) {
         const float4 s4 = st_bh[iq];
-        Smm[buf][t] = RowOffset(s4.x, s4.y);
-        Sdl[buf][t] = s4.z;
+        Smm[buf][t] = -RowOffset(s4.x, s4.y);
+        Sdl[buf][t] = -s4.z;
         start = static_cast<int>(StatsStart(s4.w, iq));
       } else {
-        Smm[buf][t] = 0.0f;
+        Smm[buf][t] = -INFINITY;  // weight 0 past the sequence end
         Sdl[buf][t] = 0.0f;
       }
       Sst[buf][t] = start;
@@ -546,41 +573,43 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
       if (t == 0) Smax[buf] = mx;
     }
   };
+  // The 16 per-row values of tile kt for this lane (rows 8q + 4g + e).
+  auto rows16 = [&](const float* src, int kt) {
+    v16f x;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const float4 f = *reinterpret_cast<const float4*>(src + kt * 32 + 8 * q4 + 4 * g);
+      x[4 * q4] = f.x;
+      x[4 * q4 + 1] = f.y;
+      x[4 * q4 + 2] = f.z;
+      x[4 * q4 + 3] = f.w;
+    }
+    return x;
+  };
 
-  v16f dka[D / 32] = {}, dva[D / 32] = {};
+  v16f acc[D / 32] = {};
   auto run = [&](auto masked, int buf, int r0) {
     constexpr bool kMask = decltype(masked)::value;
-    v16f sc[2], dpt[2];
-    ScoreTiles<D>(Qs[buf], kf, lane, sc);
-    if (kDK) ScoreTiles<D>(Ds[buf], vf, lane, dpt);
-    bf16x8 pb[4], wb[4];
+    const int lo_rel = r0 + 4 * g - j;  // query row r0 + il minus this lane's key
+    bf16x8 wb[4];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      float p[16], w[16];
+      const v16f sc = ScoreTile<D>(Qs[buf], kf, lane, kt, rows16(Smm[buf], kt));
+      v16f dpt;
+      if (kDK) dpt = ScoreTile<D>(Ds[buf], vf, lane, kt, rows16(Sdl[buf], kt));
+      float w[16];
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int il0 = kt * 32 + 8 * q4 + 4 * g;  // rows il0 .. il0 + 3
-        const float4 mm4 = *reinterpret_cast<const float4*>(&Smm[buf][il0]);
-        const float4 dl4 = *reinterpret_cast<const float4*>(&Sdl[buf][il0]);
-        const float mmv[4] = {mm4.x, mm4.y, mm4.z, mm4.w};
-        const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * q4 + e;
-          float pp = Exp2(__builtin_fmaf(sc[kt][r], c2, -mmv[e]));
-          if constexpr (kMask) {
-            const int iq = r0 + il0 + e;
-            pp = (iq < S && j <= iq && j >= Sst[buf][il0 + e]) ? pp : 0.0f;
-          }
-          p[r] = pp;
-          if (kDK) w[r] = (pp * (dpt[kt][r] - dlv[e])) * isd;
+      for (int r = 0; r < 16; ++r) {
+        float e = Exp2(sc[r]);
+        if constexpr (kMask) {  // keep query row r0 + il >= j and its start <= j
+          const int il = RowOf(kt, r, g);
+          e = OrZero(e, Outside(lo_rel + RowConst(kt, r), j - Sst[buf][il]));
         }
+        w[r] = kDK ? e * dpt[r] : e;
       }
-      if (kDV) PackTile(p, pb + 2 * kt);
-      if (kDK) PackTile(w, wb + 2 * kt);
+      PackTile(w, wb + 2 * kt);
     }
-    if (kDK) AccumTiles<D>(Qt[buf], wb, lane, dka);
-    if (kDV) AccumTiles<D>(Dt[buf], pb, lane, dva);
+    AccumTiles<D>(kDK ? Qt[buf] : Dt[buf], wb, lane, acc);
   };
 
   load(0);
@@ -590,7 +619,7 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
     const int buf = ib & 1;
     if (ib + 1 < nblk) load(ib + 1);
     const int r0 = (blk_first + ib) * kBlk;
-    if (r0 >= j0w + 31 && r0 + kBlk <= S && Smax[buf] <= j0w)
+    if (r0 >= j0w + 31 && r0 + kBlk <= S && Uniform(Smax[buf]) <= j0w)
       run(std::false_type{}, buf, r0);
     else if (r0 + kBlk - 1 >= j0w)  // some query of the block reaches this wave's keys
       run(std::true_type{}, buf, r0);
@@ -598,18 +627,14 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
     __syncthreads();
   }
   if (j >= S) return;
+  const float scale = kDK ? isd : 1.0f;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      const int off = dt * 32 + 8 * qq + 4 * g;
-      if (kDK)
-        *reinterpret_cast<float4*>(dk + base + static_cast<size_t>(j) * ld + off) =
-            make_float4(dka[dt][4 * qq], dka[dt][4 * qq + 1], dka[dt][4 * qq + 2], dka[dt][4 * qq + 3]);
-      if (kDV)
-        *reinterpret_cast<float4*>(dv + base + static_cast<size_t>(j) * ld + off) =
-            make_float4(dva[dt][4 * qq], dva[dt][4 * qq + 1], dva[dt][4 * qq + 2], dva[dt][4 * qq + 3]);
-    }
+    for (int qq = 0; qq < 4; ++qq)
+      *reinterpret_cast<float4*>(out + base + static_cast<size_t>(j) * ld + dt * 32 + 8 * qq + 4 * g) =
+          make_float4(acc[dt][4 * qq] * scale, acc[dt][4 * qq + 1] * scale,
+                      acc[dt][4 * qq + 2] * scale, acc[dt][4 * qq + 3] * scale);
 }
 
 }  // namespace
@@ -655,21 +680,21 @@ hipError_t LaunchFlashDQ(const float* q, const float* k, const float* v, const f
 hipError_t LaunchFlashDKDV(const float* q, const float* k, const float* v, const float* dout,
                            const float* stats, float* dk, float* dv, size_t B, size_t S, size_t H,
                            size_t d, hipStream_t s) {
+  if ((dk == nullptr) == (dv == nullptr)) return hipErrorInvalidValue;
   const dim3 grid = FlashGrid(B, S, H);
   const int Si = static_cast<int>(S), Hi = static_cast<int>(H);
-#define SEEAI_DKDV(DD, A, Bv)                                                                  \
-  hipLaunchKernelGGL((FlashDKDV<DD, A, Bv>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dk, \
-                     dv, Si, Hi)
+  float* out = dk ? dk : dv;
   if (d == 64) {
-    if (dk && dv) SEEAI_DKDV(64, true, true);
-    else if (dk) SEEAI_DKDV(64, true, false);
-    else SEEAI_DKDV(64, false, true);
+    if (dk)
+      hipLaunchKernelGGL((FlashDKDV<64, true>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, out, Si, Hi);
+    else
+      hipLaunchKernelGGL((FlashDKDV<64, false>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, out, Si, Hi);
   } else {
-    if (dk && dv) return hipErrorInvalidValue;  // d = 128 runs the passes apart
-    if (dk) SEEAI_DKDV(128, true, false);
-    else SEEAI_DKDV(128, false, true);
+    if (dk)
+      hipLaunchKernelGGL((FlashDKDV<128, true>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, out, Si, Hi);
+    else
+      hipLaunchKernelGGL((FlashDKDV<128, false>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, out, Si, Hi);
   }
-#undef SEEAI_DKDV
   return hipGetLastError();
 }
 
