@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--pmc-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: one W8A8 step plus a 256 MiB device copy "
                         "(the counter calibration: a copy's known bytes)")
+    p.add_argument("--attn-probe", action="store_true",
+                   help="for rocprofv3 runs: BASELINE configs[2] attention fwd+bwd, bf16 x3, f32 x1")
     return p.parse_args()
 
 
@@ -81,6 +83,35 @@ def pmc_probe():
     return 0
 
 
+def attn_probe():
+    """BASELINE configs[2] once per family for the profilers: causal
+    attention fwd + dQ + dK + dV at B16 H16 S2048 d64, relaxed (bf16) three
+    times, exact (f32) once."""
+    import torch
+    hip = importlib.import_module("see-ai_amd.hip")
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    B, S, H, d = 16, 2048, 16, 64
+    g = torch.Generator(device="cuda").manual_seed(20261202)
+    q, k, v, do = (torch.randn((B * S, H * d), device="cuda", generator=g) for _ in range(4))
+    o, st = torch.empty_like(q), torch.empty((B * H * S, 4), device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    for dt, reps in [(1, 3), (0, 1)]:
+        for _ in range(reps):
+            ctx.call("seeai_attn_fwd", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                     st.data_ptr(), B, S, H, d, None)
+            ctx.call("seeai_attn_dq", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                     st.data_ptr(), dq.data_ptr(), B, S, H, d)
+            ctx.call("seeai_attn_dk", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                     st.data_ptr(), dk.data_ptr(), B, S, H, d)
+            ctx.call("seeai_attn_dv", dt, q.data_ptr(), k.data_ptr(), do.data_ptr(), st.data_ptr(),
+                     dv.data_ptr(), B, S, H, d)
+    torch.cuda.synchronize()
+    ctx.close()
+    print("attention probe: B16 H16 S2048 d64 causal, 3 x bf16 fwd+bwd, 1 x f32 fwd+bwd", flush=True)
+    return 0
+
+
 def load_traffic(name: str):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
@@ -93,6 +124,8 @@ def main():
     args = parse()
     if args.pmc_probe:
         return pmc_probe()
+    if args.attn_probe:
+        return attn_probe()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the path shards by GEMM column blocks / attention (b, h) -- see DESIGN.md)",
