@@ -1227,3 +1227,46 @@ int orc_execute(const void* instruction, uint8_t* arena, const uint8_t* rodata,
 #undef IP
   return 0;
 }
+
+/* --- plan self-hash (source/identity/hash.h:31-158) --------------------- */
+static const uint64_t kFnvBasis = 0xcbf29ce484222325ULL;
+static const uint64_t kFnvPrime = 0x100000001b3ULL;
+
+/* hash.h:71-78: a 64-bit word folded low byte first. */
+static uint64_t fnv_word(uint64_t h, uint64_t w) {
+  for (int b = 0; b < 8; ++b) {
+    h ^= (w >> (8 * b)) & 0xffu;
+    h *= kFnvPrime;
+  }
+  return h;
+}
+
+/* hash.h:82-100, with the byte at `zero_at` (if inside) read as zero. */
+static uint64_t striped(const uint8_t* p, size_t n, size_t base, size_t zero_lo, size_t zero_hi) {
+  uint64_t lane[8];
+  for (size_t l = 0; l < 8; ++l) lane[l] = kFnvBasis ^ (0x9E3779B97F4A7C15ULL * (l + 1));
+  for (size_t i = 0; i < n; ++i) {
+    const size_t at = base + i;
+    const uint8_t byte = (at >= zero_lo && at < zero_hi) ? 0 : p[i];
+    lane[i % 8] ^= byte;
+    lane[i % 8] *= kFnvPrime;
+  }
+  uint64_t h = kFnvBasis;
+  for (size_t l = 0; l < 8; ++l) h = fnv_word(h, lane[l]);
+  return fnv_word(h, (uint64_t)n);
+}
+
+uint64_t orc_plan_self_hash(const uint8_t* plan, size_t size, size_t hash_offset) {
+  const size_t grain = orc_chunk_grain(size, (size_t)1 << 20); /* hash.h:63 */
+  const size_t chunks = orc_chunk_count(size, (size_t)1 << 20);
+  uint64_t h = kFnvBasis;
+  if (chunks == 0) {
+    h = fnv_word(h, striped(plan, 0, 0, hash_offset, hash_offset + 8));
+  } else {
+    for (size_t c = 0; c < chunks; ++c) {
+      const size_t b = c * grain, e = (b + grain < size) ? b + grain : size;
+      h = fnv_word(h, striped(plan + b, e - b, b, hash_offset, hash_offset + 8));
+    }
+  }
+  return fnv_word(h, (uint64_t)size);
+}

@@ -170,6 +170,11 @@ void orc_argmax_tally(const float* probs, const int32_t* labels, size_t rows,
 void orc_argmax_rows(const float* probs, size_t rows, size_t cols,
                      int32_t* out);
 
+/* PlanSelfHash (source/identity/hash.h:136-158): 8 interleaved FNV-1a
+ * chains per chunk (hash.h:82-100), chunk digests folded in chunk order,
+ * then the size; the 8 bytes at hash_offset read as zero. */
+uint64_t orc_plan_self_hash(const uint8_t* plan, size_t size, size_t hash_offset);
+
 /* --- Instruction interpreter (runtime/executor/cpu_backend.cc:260-646) --- */
 /* Runs one 64-byte UpdateInstruction against an arena / rodata pair.
  * Returns 0 ok, 1 refusal (non-finite norm), 4 clip-threshold refusal,

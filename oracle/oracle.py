@@ -84,6 +84,7 @@ SIGS = {
     "clip_global": (_I, [_P, _Z, _P, _F]),
     "sgd_step": (_I, [_P, _P, _Z, _F, _F, _F]),
     "adamw_step": (_I, [_P, _P, _P, _P, _Z, _F, _F, _F, _F, _F, _U64, _F]),
+    "plan_self_hash": (_U64, [_P, _Z, _Z]),
 }
 # Oracle-only entry points (no reference counterpart or engine-side code).
 ORACLE_ONLY = {
@@ -496,6 +497,10 @@ class Kernels:
         b = np.zeros(1, np.float32)
         self._fn("adamw_bias_corrections")(b1, b2, step, _ptr(a), _ptr(b))
         return float(a[0]), float(b[0])
+
+    def plan_self_hash(self, blob, hash_offset: int = 216) -> int:
+        buf = np.frombuffer(bytes(blob), np.uint8)
+        return int(self._fn("plan_self_hash")(_ptr(buf), buf.size, hash_offset))
 
     def execute(self, ins_bytes: bytes, arena: np.ndarray, rodata: np.ndarray, params):
         buf = C.create_string_buffer(bytes(ins_bytes), 64)

@@ -13,6 +13,7 @@
 #include <cstdint>
 
 #include "runtime/executor/update_kernels.h"
+#include "source/identity/hash.h"
 #include "source/parallel/parallel_for.h"
 
 namespace k = seeml::update_rt::kernels;
@@ -186,6 +187,10 @@ int ref_adamw_step(float* p, const float* g, float* m, float* v, size_t n, float
                    float b1, float b2, float eps, float wd, uint64_t step,
                    float clip) {
   return k::AdamWStep(p, g, m, v, n, lr, b1, b2, eps, wd, step, clip) ? 1 : 0;
+}
+
+uint64_t ref_plan_self_hash(const uint8_t* plan, size_t size, size_t hash_offset) {
+  return seeml::update::PlanSelfHash(plan, size, hash_offset);
 }
 
 }  // extern "C"

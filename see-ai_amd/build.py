@@ -25,6 +25,8 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+HOST = os.path.join(HERE, "host")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libseeai_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -40,18 +42,31 @@ COMMON = [
 PER_FILE = {"k_flash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
+# The host layer above the C ABI (plan reader, backend, engine): C++20,
+# no device code.
+ROCM = os.path.dirname(os.path.dirname(os.path.realpath(HIPCC)))
+HOST_FLAGS = ["-O2", "-fPIC", "-std=c++20", "-Wall", "-Wextra", f"-I{INCLUDE}",
+              f"-I{os.path.join(ROCM, 'include')}", "-D__HIP_PLATFORM_AMD__", "-x", "c++"]
+
+
 def sources():
     out = []
     for name in sorted(os.listdir(CSRC)):
         if name.endswith(".hip") or name.endswith(".cpp"):
             out.append(os.path.join(CSRC, name))
+    for name in sorted(os.listdir(HOST)):
+        if name.endswith(".cc"):
+            out.append(os.path.join(HOST, name))
     return out
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, *PER_FILE.get(os.path.basename(src), []), "-c", src, "-o", obj]
-    if src.endswith(".cpp"):
+    if os.path.dirname(src) == HOST:
+        cmd = [HIPCC, *HOST_FLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *COMMON, *PER_FILE.get(os.path.basename(src), []), "-c", src, "-o", obj]
+    if src.endswith(".cpp"):  # the C ABI over the kernels: host code beside HIP launches
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

@@ -161,6 +161,14 @@ int AdamWLaunch(seeai_ctx* c, float* p, const float* g, float* m, float* v, uint
   return SEEAI_OK;
 }
 
+// kFlagRelaxed (instruction.h:356-384) taken as a permission when the
+// context allows it; each relaxed execution is counted (backend.h:149-162).
+int Relaxed(seeai_ctx* c, const Instruction& ins) {
+  const int r = (ins.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
+  c->relaxed += r;
+  return r;
+}
+
 int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P) {
   if (!c->arena) return Fail(c, SEEAI_INVALID, "execute: no arena is bound");
   const Ptrs R{c};
@@ -190,6 +198,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       a.addend = (ins.flags & kFlagGemmAddend) ? R.f(ins.in[3]) : nullptr;
       a.bias = (ins.opcode == 1 && (ins.flags & kFlagEpilogueBias)) ? R.f(ins.in[3]) : nullptr;
       a.act = ins.opcode == 1 ? act : 0;
+      a.relaxed = Relaxed(c, ins);
       SEEAI_TRY(c, LaunchGemm(a, s), "gemm");
       return SEEAI_OK;
     }
@@ -205,6 +214,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       a.alpha_a = BitsToF32(ins.in[3]);
       a.alpha_dot = 1.0f;
       a.accumulate = 1;
+      a.relaxed = Relaxed(c, ins);
       SEEAI_TRY(c, LaunchGemm(a, s), "gemm.acc_nn");
       return SEEAI_OK;
     }
@@ -234,6 +244,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
           a.b_col_scale = R.f(ins.in[3]);
       }
       a.act = nt ? 0 : act;
+      a.relaxed = Relaxed(c, ins);
       SEEAI_TRY(c, LaunchGemm(a, s), "gemm.q8");
       return SEEAI_OK;
     }
@@ -253,6 +264,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       a.alpha_dot = 1.0f;
       a.bias = (!nt && (ins.flags & kFlagEpilogueBias)) ? R.f(ins.in[3]) : nullptr;
       a.act = nt ? 0 : act;
+      a.relaxed = Relaxed(c, ins);
       SEEAI_TRY(c, LaunchGemm(a, s), "gemm.bf16");
       return SEEAI_OK;
     }
@@ -489,8 +501,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
         B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
         starts = R.i32(ins.out[2]);
       }
-      const int dt = (ins.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
-      c->relaxed += dt;
+      const int dt = Relaxed(c, ins);
       SEEAI_TRY(c,
                 LaunchAttnFwdTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]),
                                    R.f(ins.in[3]), R.f(ins.out[0]), B, S, H, d, starts, s),
@@ -502,8 +513,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
     case 50: {  // AttnDQTiled / DKTiled / DVTiled
       const uint64_t g = ins.out[2];
       const uint64_t B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
-      const int dt = (ins.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
-      c->relaxed += dt;
+      const int dt = Relaxed(c, ins);
       hipError_t e;
       if (ins.opcode == 48)
         e = LaunchAttnDQTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),

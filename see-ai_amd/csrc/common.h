@@ -209,9 +209,11 @@ struct GemmArgs {
   const float* bias;         // epilogue bias [N]
   int act;                   // epilogue activation
   int accumulate;            // C += (GemmAccNN)
-  int relaxed;               // bf16 MFMA over bf16-rounded A (kFlagRelaxed)
+  int relaxed;               // kFlagRelaxed taken: MFMA summation order
 };
+// Relaxed -> MFMA (k_gemm_f32.hip); otherwise the reference's order.
 hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s);
+hipError_t LaunchGemmExact(const GemmArgs& a, hipStream_t s);
 
 // W8A8 (k_gemm_i8.hip).
 hipError_t LaunchQuantizeRows(const float* X, int8_t* Q, float* scale, size_t rows, size_t cols,

@@ -18,7 +18,9 @@
 // k-scale multiplies A's elements; the NT alpha multiplies the finished dot.
 // Then C = [D +] dot, and act(C + bias).  The products are exact and the
 // MFMA sums them in f32 in its own order, so results agree with the
-// reference to rounding (the parity tests bound it at max-rel 1e-5).
+// reference to rounding (max-rel 1e-5): this is the relaxed family's path
+// (kFlagRelaxed); the exact family runs the reference's order in
+// k_gemm_exact.hip.
 #include "common.h"
 
 namespace seeai {
@@ -187,11 +189,9 @@ hipError_t Dispatch(const GemmArgs& a, hipStream_t s) {
 
 hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s) {
   if (a.M == 0 || a.N == 0) return hipSuccess;
-  if (a.K == 0) {
-    // An empty reduction: every dot is +0 (the reference zeroes C first).
-    GemmArgs z = a;
-    (void)z;
-  }
+  // The exact family keeps the reference's reduction order (bit-exact,
+  // k_gemm_exact.hip); MFMA's own summation order is the relaxed family's.
+  if (!a.relaxed) return LaunchGemmExact(a, s);
   switch (a.layout * 3 + a.b_kind) {
     case 0: return Dispatch<0, 0>(a, s);
     case 1: return Dispatch<0, 1>(a, s);

@@ -92,6 +92,28 @@ EXPORTS = {
     "seeai_adamw_step": (_I, [_P, _P, _P, _P, _P, _U64, C.POINTER(StepParams), _F]),
     "seeai_argmax_rows": (_I, [_P, _P, _U64, _U64, _P]),
 }
+# include/seeai_engine.h: the plan engine (see-ai_amd/host/).
+ENGINE_EXPORTS = {
+    "seeai_plan_self_hash": (_U64, [_P, _U64, _U64]),
+    "seeai_plan_check": (_I, [_P, _U64, _P, _U64]),
+    "seeai_engine_create": (_I, [_I, _P, _U64, C.POINTER(_P), _P, _U64]),
+    "seeai_engine_destroy": (None, [_P]),
+    "seeai_engine_last_error": (C.c_char_p, [_P]),
+    "seeai_engine_header": (_I, [_P, _P]),
+    "seeai_engine_train_step": (_I, [_P, _P, _P, C.POINTER(_F)]),
+    "seeai_engine_train_resident": (_I, [_P, C.POINTER(_F)]),
+    "seeai_engine_evaluate": (_I, [_P, _P, _P, C.POINTER(_F)]),
+    "seeai_engine_merge": (_I, [_P]),
+    "seeai_engine_read": (_I, [_P, _U64, _P, _U64]),
+    "seeai_engine_write": (_I, [_P, _U64, _P, _U64]),
+    "seeai_engine_step": (_U64, [_P]),
+    "seeai_engine_set_step": (None, [_P, _U64]),
+    "seeai_engine_set_horizon": (None, [_P, _U64]),
+    "seeai_engine_lr": (_F, [_P]),
+    "seeai_engine_relaxed_executions": (_U64, [_P]),
+    "seeai_engine_context": (_P, [_P]),
+}
+EXPORTS.update(ENGINE_EXPORTS)
 for _name, (_res, _args) in EXPORTS.items():
     _fn = getattr(_lib, _name)
     _fn.restype = _res
@@ -236,3 +258,115 @@ def pack_instruction(opcode: int, flags: int = 0, imm: int = 0, ins=(), outs=())
     i4 = list(ins) + [null] * (4 - len(ins))
     o3 = list(outs) + [0] * (3 - len(outs))
     return struct.pack("<HHI4Q3Q", opcode, flags, imm, *i4, *o3)
+
+
+def plan_self_hash(blob: bytes, hash_offset: int = 216) -> int:
+    """PlanSelfHash (source/identity/hash.h:136-158) of a plan blob."""
+    buf = C.create_string_buffer(bytes(blob), max(len(blob), 1))
+    return int(_lib.seeai_plan_self_hash(buf, _U64(len(blob)), _U64(hash_offset)))
+
+
+def plan_check(blob: bytes) -> str:
+    """The loader's header contract on a blob: '' if readable, else the
+    reference's refusal message (runtime/loader/plan_loader.cc:19-49)."""
+    buf = C.create_string_buffer(bytes(blob), max(len(blob), 1))
+    msg = C.create_string_buffer(512)
+    _lib.seeai_plan_check(buf, _U64(len(blob)), msg, _U64(512))
+    return msg.value.decode("utf-8", "replace")
+
+
+class Engine:
+    """A loaded plan on one device (include/seeai_engine.h): the reference's
+    UpdateEngine verbs over the gfx950 HipBackend."""
+
+    def __init__(self, blob: bytes, device: int = 0):
+        self._blob = bytes(blob)
+        buf = C.create_string_buffer(self._blob, max(len(self._blob), 1))
+        h = _P()
+        msg = C.create_string_buffer(512)
+        rc = _lib.seeai_engine_create(device, buf, _U64(len(self._blob)), C.byref(h), msg,
+                                      _U64(512))
+        if rc != OK:
+            raise BackendError(rc, msg.value.decode("utf-8", "replace"))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            _lib.seeai_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 -- interpreter shutdown
+            pass
+
+    def _check(self, rc: int):
+        if rc != OK:
+            raise BackendError(rc, _lib.seeai_engine_last_error(self.h).decode("utf-8", "replace"))
+
+    def header(self) -> bytes:
+        buf = C.create_string_buffer(320)
+        self._check(_lib.seeai_engine_header(self.h, buf))
+        return buf.raw
+
+    def train_step(self, inputs, labels=None) -> float:
+        import numpy as np
+        x = np.ascontiguousarray(inputs, np.float32)
+        lab = None if labels is None else np.ascontiguousarray(labels)
+        loss = _F(0.0)
+        self._check(_lib.seeai_engine_train_step(
+            self.h, x.ctypes.data, None if lab is None else lab.ctypes.data, C.byref(loss)))
+        return loss.value
+
+    def train_resident(self) -> float:
+        loss = _F(0.0)
+        self._check(_lib.seeai_engine_train_resident(self.h, C.byref(loss)))
+        return loss.value
+
+    def evaluate(self, inputs, labels=None) -> float:
+        import numpy as np
+        x = np.ascontiguousarray(inputs, np.float32)
+        lab = None if labels is None else np.ascontiguousarray(labels)
+        loss = _F(0.0)
+        self._check(_lib.seeai_engine_evaluate(
+            self.h, x.ctypes.data, None if lab is None else lab.ctypes.data, C.byref(loss)))
+        return loss.value
+
+    def merge(self):
+        self._check(_lib.seeai_engine_merge(self.h))
+
+    def read(self, offset: int, nbytes: int) -> bytes:
+        buf = C.create_string_buffer(max(nbytes, 1))
+        self._check(_lib.seeai_engine_read(self.h, _U64(offset), buf, _U64(nbytes)))
+        return buf.raw[:nbytes]
+
+    def write(self, offset: int, data: bytes):
+        buf = C.create_string_buffer(bytes(data), max(len(data), 1))
+        self._check(_lib.seeai_engine_write(self.h, _U64(offset), buf, _U64(len(data))))
+
+    @property
+    def step(self) -> int:
+        return int(_lib.seeai_engine_step(self.h))
+
+    @step.setter
+    def step(self, value: int):
+        _lib.seeai_engine_set_step(self.h, _U64(value))
+
+    def set_horizon(self, steps: int):
+        _lib.seeai_engine_set_horizon(self.h, _U64(steps))
+
+    def lr(self) -> float:
+        return float(_lib.seeai_engine_lr(self.h))
+
+    def relaxed_executions(self) -> int:
+        return int(_lib.seeai_engine_relaxed_executions(self.h))
+
+    def use_torch_stream(self):
+        """Run the engine's kernels on torch's current stream."""
+        import torch
+        handle = torch.cuda.current_stream().cuda_stream
+        ctx = _lib.seeai_engine_context(self.h)
+        rc = _lib.seeai_set_stream(ctx, _P(handle) if handle else None)
+        if rc != OK:
+            raise BackendError(rc, _lib.seeai_last_error(ctx).decode("utf-8", "replace"))

@@ -1,0 +1,187 @@
+// engine.cc -- the plan engine's step loop (see engine.h).
+#include "engine.h"
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+
+namespace seeai::host {
+namespace {
+
+constexpr uint16_t kOpSoftmaxXEntFwd = 11, kOpSoftmaxXEntBwd = 12;              // instruction.h:63-64
+constexpr uint16_t kOpSoftmaxXEntMaskedFwd = 51, kOpSoftmaxXEntMaskedBwd = 52;  // v22 masked pair
+
+bool IsXent(uint16_t op) {
+  return op == kOpSoftmaxXEntFwd || op == kOpSoftmaxXEntBwd || op == kOpSoftmaxXEntMaskedFwd ||
+         op == kOpSoftmaxXEntMaskedBwd;
+}
+
+}  // namespace
+
+Result<std::unique_ptr<PlanEngine>> PlanEngine::Load(std::span<const uint8_t> blob, int device) {
+  std::unique_ptr<PlanEngine> e(new PlanEngine());
+  e->blob_.assign(blob.begin(), blob.end());
+  auto plan = ReadPlan(e->blob_);
+  if (!plan) return Fail(plan.error());
+  e->plan_ = std::move(*plan);
+  const PlanHeader& h = e->plan_.header;
+
+  // plan_loader.cc:151-166: the narrowest softmax width anywhere bounds the
+  // class labels the feeder may stage.
+  for (const auto* program : {&e->plan_.train, &e->plan_.merge, &e->plan_.eval, &e->plan_.step})
+    for (const Instruction& ins : *program) {
+      if (IsXent(ins.opcode) && ins.out[1] != 0 &&
+          (e->num_classes_ == 0 || ins.out[1] < e->num_classes_))
+        e->num_classes_ = ins.out[1];
+      if (ins.opcode == kOpSoftmaxXEntMaskedFwd || ins.opcode == kOpSoftmaxXEntMaskedBwd)
+        e->masked_labels_ = true;
+    }
+  if (h.label_kind == 1 && e->num_classes_ == 0)
+    return Fail("class-label plan carries no softmax cross-entropy \xe2\x80\x94 its labels could "
+                "never be validated");
+
+  // plan_loader.cc:251-288: one zeroed, 16 KiB-aligned allocation holding
+  // the persistent image at offset 0.
+  e->arena_bytes_ = (h.arena_size + (kArenaAlignment - 1)) & ~(kArenaAlignment - 1);
+  if (e->arena_bytes_ == 0) e->arena_bytes_ = kArenaAlignment;
+  e->arena_ = static_cast<uint8_t*>(std::aligned_alloc(kArenaAlignment, e->arena_bytes_));
+  if (!e->arena_) return Fail("arena allocation failed");
+  std::memset(e->arena_, 0, e->arena_bytes_);
+  if (!e->plan_.persist_init.empty())
+    std::memcpy(e->arena_, e->plan_.persist_init.data(), e->plan_.persist_init.size());
+
+  auto backend = HipBackend::Create(device);
+  if (!backend) return Fail(backend.error());
+  e->backend_ = std::move(*backend);
+  if (auto r = e->backend_->Bind(e->arena_, e->arena_bytes_, e->plan_.rodata.data(),
+                                 e->plan_.rodata.size(), e->plan_.rodata.size());
+      !r)
+    return Fail(r.error());
+  e->backend_->Configure();
+  return e;
+}
+
+PlanEngine::~PlanEngine() {
+  backend_.reset();  // the backend's views die before the memory they view
+  std::free(arena_);
+}
+
+float PlanEngine::EffectiveLr() const {
+  const PlanHeader& h = plan_.header;
+  const float base = h.lr;
+  if (static_cast<LrSchedule>(h.lr_schedule) != LrSchedule::kCosineWithWarmup) return base;
+  if (h.warmup_steps > 0 && step_ <= h.warmup_steps)
+    return base * static_cast<float>(step_) / static_cast<float>(h.warmup_steps);
+  const uint64_t run = horizon();
+  const uint64_t span = run > h.warmup_steps ? run - h.warmup_steps : 0;
+  const float floor = base * h.min_lr_factor;
+  if (span == 0 || step_ - h.warmup_steps >= span) return floor;
+  const float t = static_cast<float>(step_ - h.warmup_steps) / static_cast<float>(span);
+  constexpr float kPi = 3.14159265358979323846f;
+  return floor + (base - floor) * 0.5f * (1.0f + std::cos(kPi * t));
+}
+
+Result<void> PlanEngine::Stage(const float* input, const void* labels) {
+  const PlanHeader& h = plan_.header;
+  const uint64_t in_off = RefOffset(h.input_ref), in_bytes = h.input_floats * sizeof(float);
+  std::memcpy(arena_ + in_off, input, in_bytes);
+  if (auto r = backend_->SyncToDevice(in_off, in_bytes); !r) return r;
+  if (h.label_kind == 0) return {};
+  if (!labels) return Fail("this plan trains on labels: none were staged");
+  if (h.label_kind == 1) {
+    // The feeder's value contract: every class index below the plan's
+    // narrowest softmax width (-1, an ignored position, only where the
+    // plan's masked loss expects it).
+    const bool masked = masked_labels_;
+    const auto* lab = static_cast<const int32_t*>(labels);
+    for (uint64_t i = 0; i < h.label_bytes / sizeof(int32_t); ++i)
+      if (lab[i] >= static_cast<int64_t>(num_classes_) || lab[i] < (masked ? -1 : 0))
+        return Fail("label " + std::to_string(lab[i]) + " at position " + std::to_string(i) +
+                    " is outside the plan's " + std::to_string(num_classes_) + " classes");
+  }
+  const uint64_t lab_off = RefOffset(h.label_ref);
+  std::memcpy(arena_ + lab_off, labels, h.label_bytes);
+  return backend_->SyncToDevice(lab_off, h.label_bytes);
+}
+
+Result<void> PlanEngine::ExecuteRange(const std::vector<Instruction>& program, size_t begin,
+                                      size_t end) {
+  const PlanHeader& h = plan_.header;
+  const StepParams params{EffectiveLr(), h.beta1, h.beta2, h.eps, h.weight_decay, step_};
+  backend_->BeginRange(std::span<const Instruction>(program), begin, end);
+  for (size_t idx = begin; idx < end; ++idx)
+    if (auto r = backend_->Execute(program[idx], params); !r) {
+      backend_->EndRange();
+      return Fail(std::string("backend '") + backend_->name() + "' failed at instruction " +
+                  std::to_string(idx) + ": " + r.error());
+    }
+  auto flushed = backend_->Flush();
+  backend_->EndRange();
+  if (!flushed)
+    return Fail(std::string("backend '") + backend_->name() + "' failed to complete: " +
+                flushed.error());
+  return {};
+}
+
+Result<float> PlanEngine::Loss() {
+  const uint64_t off = RefOffset(plan_.header.loss_ref);
+  if (auto r = backend_->SyncToHost(off, sizeof(float)); !r) return Fail(r.error());
+  float loss;
+  std::memcpy(&loss, arena_ + off, sizeof(loss));
+  return loss;
+}
+
+Result<float> PlanEngine::TrainStep(const float* inputs, const void* labels) {
+  const PlanHeader& h = plan_.header;
+  const uint64_t micro = h.grad_accum_steps > 1 ? h.grad_accum_steps : 1;
+  ++step_;  // the 1-indexed timestep of this optimizer step
+  double loss_sum = 0.0;
+  for (uint64_t g = 0; g < micro; ++g) {
+    const auto* lab = labels ? static_cast<const uint8_t*>(labels) + g * h.label_bytes : nullptr;
+    if (auto r = Stage(inputs + g * h.input_floats, lab); !r) return Fail(r.error());
+    if (auto r = ExecuteRange(plan_.train, 0, plan_.train.size()); !r) return Fail(r.error());
+    auto loss = Loss();
+    if (!loss) return loss;
+    loss_sum += *loss;
+  }
+  if (!plan_.step.empty())
+    if (auto r = ExecuteRange(plan_.step, 0, plan_.step.size()); !r) return Fail(r.error());
+  return static_cast<float>(loss_sum / static_cast<double>(micro));
+}
+
+Result<float> PlanEngine::TrainStepResident() {
+  if (plan_.header.grad_accum_steps > 1)
+    return Fail("a resident step replays one staged batch; this plan accumulates micro-batches");
+  ++step_;
+  if (auto r = ExecuteRange(plan_.train, 0, plan_.train.size()); !r) return Fail(r.error());
+  return Loss();
+}
+
+Result<float> PlanEngine::Evaluate(const float* input, const void* labels) {
+  if (plan_.eval.empty()) return Fail("plan carries no eval program");
+  if (auto r = Stage(input, labels); !r) return Fail(r.error());
+  if (auto r = ExecuteRange(plan_.eval, 0, plan_.eval.size()); !r) return Fail(r.error());
+  return Loss();
+}
+
+Result<void> PlanEngine::Merge() {
+  if (auto r = ExecuteRange(plan_.merge, 0, plan_.merge.size()); !r) return r;
+  for (const EmitEntry& e : plan_.emit)
+    if (auto r = backend_->SyncToHost(e.arena_offset, e.byte_size); !r) return r;
+  return {};
+}
+
+Result<void> PlanEngine::Read(uint64_t offset, void* dst, uint64_t bytes) {
+  if (auto r = backend_->SyncToHost(offset, bytes); !r) return r;
+  std::memcpy(dst, arena_ + offset, bytes);
+  return {};
+}
+
+Result<void> PlanEngine::Write(uint64_t offset, const void* src, uint64_t bytes) {
+  if (offset > arena_bytes_ || bytes > arena_bytes_ - offset)
+    return Fail("arena write outside the arena");
+  std::memcpy(arena_ + offset, src, bytes);
+  return backend_->SyncToDevice(offset, bytes);
+}
+
+}  // namespace seeai::host

@@ -1,0 +1,74 @@
+// hip_backend.cc -- ExecutorBackend over the C ABI (see hip_backend.h).
+#include "hip_backend.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include "seeai_hip.h"
+
+namespace seeai::host {
+
+Result<std::unique_ptr<HipBackend>> HipBackend::Create(int device) {
+  seeai_ctx* ctx = nullptr;
+  if (seeai_create(device, &ctx) != SEEAI_OK) {
+    std::string why = ctx ? seeai_last_error(ctx) : "no HIP device";
+    if (ctx) seeai_destroy(ctx);
+    return Fail("hip backend: " + why);
+  }
+  return std::unique_ptr<HipBackend>(new HipBackend(ctx));
+}
+
+HipBackend::~HipBackend() { seeai_destroy(ctx_); }
+
+std::string HipBackend::device() const {
+  int dev = 0;
+  hipDeviceProp_t prop{};
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
+    return "AMD GPU";
+  return std::string(prop.name) + " (" + prop.gcnArchName + ")";
+}
+
+Result<void> HipBackend::Check(int status) const {
+  if (status == SEEAI_OK) return {};
+  return Fail(seeai_last_error(ctx_));  // refusals carry the reference's exact words
+}
+
+Result<void> HipBackend::Bind(uint8_t* arena, uint64_t arena_bytes, const uint8_t* rodata,
+                              uint64_t rodata_bytes, uint64_t /*rodata_mapped_bytes*/) {
+  if (auto r = Check(seeai_bind(ctx_, arena_bytes, rodata, rodata_bytes)); !r) return r;
+  host_ = arena;
+  host_bytes_ = arena_bytes;
+  // The engine's arena holds the persistent image (and zeros elsewhere):
+  // the device arena starts as its copy.
+  return Check(seeai_upload(ctx_, 0, arena, arena_bytes));
+}
+
+Result<void> HipBackend::BindSource(const uint8_t* data, uint64_t bytes) {
+  return Check(seeai_bind_source(ctx_, data, bytes));
+}
+
+Result<void> HipBackend::Execute(const Instruction& ins, const StepParams& p) {
+  const seeai_step_params sp{p.lr, p.beta1, p.beta2, p.eps, p.weight_decay, 0, p.step};
+  return Check(seeai_execute(ctx_, &ins, &sp));
+}
+
+void HipBackend::BeginRange(std::span<const Instruction>, size_t, size_t) {}
+
+Result<void> HipBackend::Flush() { return Check(seeai_flush(ctx_)); }
+
+uint64_t HipBackend::relaxed_executions() const { return seeai_relaxed_executions(ctx_); }
+
+void HipBackend::SetRelaxed(bool allow) { seeai_set_relaxed(ctx_, allow ? 1 : 0); }
+
+Result<void> HipBackend::SyncToDevice(uint64_t offset, uint64_t bytes) {
+  if (!host_ || offset > host_bytes_ || bytes > host_bytes_ - offset)
+    return Fail("hip backend: sync range outside the bound arena");
+  return Check(seeai_upload(ctx_, offset, host_ + offset, bytes));
+}
+
+Result<void> HipBackend::SyncToHost(uint64_t offset, uint64_t bytes) {
+  if (!host_ || offset > host_bytes_ || bytes > host_bytes_ - offset)
+    return Fail("hip backend: sync range outside the bound arena");
+  return Check(seeai_download(ctx_, offset, host_ + offset, bytes));
+}
+
+}  // namespace seeai::host

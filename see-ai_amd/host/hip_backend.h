@@ -1,0 +1,78 @@
+// hip_backend.h -- the executor seam (runtime/executor/backend.h:82-166,
+// class ExecutorBackend) implemented over this repository's C ABI
+// (include/seeai_hip.h).  The reference's engine calls exactly these
+// methods: Bind (+ Configure) at load, BeginRange / Execute* / Flush /
+// EndRange per range, relaxed_executions() for reporting.  A discrete GPU
+// also needs the two host-sync verbs the seam lacks (the reference's Metal
+// arena is zero-copy shared memory): SyncToDevice for the feeder's I/O
+// slots before a range, SyncToHost for what the engine reads after Flush.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <span>
+#include <string>
+
+#include "plan.h"
+#include "result.h"
+
+struct seeai_ctx;
+
+namespace seeai::host {
+
+// backend.h:56-63: the per-range scalars the optimizer instructions read.
+struct StepParams {
+  float lr = 0.0f;
+  float beta1 = 0.0f;
+  float beta2 = 0.0f;
+  float eps = 0.0f;
+  float weight_decay = 0.0f;
+  uint64_t step = 0;
+};
+
+class HipBackend {
+ public:
+  // The device is opened here: no GPU, or no library, is a failure value.
+  static Result<std::unique_ptr<HipBackend>> Create(int device);
+  ~HipBackend();
+  HipBackend(const HipBackend&) = delete;
+  HipBackend& operator=(const HipBackend&) = delete;
+
+  const char* name() const { return "hip"; }
+  std::string device() const;
+
+  // backend.h:89-101: the engine's host arena stays the host mirror; the
+  // device arena is allocated at the same size and initialised from it;
+  // rodata is uploaded once.  A refused Bind leaves the previous binding
+  // executable.
+  Result<void> Bind(uint8_t* arena, uint64_t arena_bytes, const uint8_t* rodata,
+                    uint64_t rodata_bytes, uint64_t rodata_mapped_bytes);
+  Result<void> BindSource(const uint8_t* data, uint64_t bytes);
+  // backend.h:117: tile policy.  The gfx950 kernels pick their tiles per
+  // launch from the operand shapes, so the CPU tile words do not apply.
+  void Configure() {}
+  Result<void> Execute(const Instruction& ins, const StepParams& params);
+  // backend.h:139-142: whole-program visibility around a range.
+  void BeginRange(std::span<const Instruction> program, size_t begin, size_t end);
+  void EndRange() {}
+  // backend.h:147: drains the stream; reports a refused optimizer step.
+  Result<void> Flush();
+  uint64_t relaxed_executions() const;
+  uint64_t fused_dispatches() const { return 0; }
+  void SetRelaxed(bool allow);
+
+  Result<void> SyncToDevice(uint64_t offset, uint64_t bytes);
+  Result<void> SyncToHost(uint64_t offset, uint64_t bytes);
+
+  seeai_ctx* context() const { return ctx_; }
+
+ private:
+  explicit HipBackend(seeai_ctx* ctx) : ctx_(ctx) {}
+  Result<void> Check(int status) const;
+
+  seeai_ctx* ctx_;
+  uint8_t* host_ = nullptr;
+  uint64_t host_bytes_ = 0;
+};
+
+}  // namespace seeai::host

@@ -1,0 +1,284 @@
+"""Writes .seeu plans (format v26) for the executor's workloads.
+
+The reference compiles plans with its C++ compiler (``seeml-update-compile``:
+``MakeMlp`` / ``MakeTokenDecoderStack`` + ``UpdateCompiler``), which is not
+runnable in this build.  This module emits the same programs for the graphs
+the benchmarks use, instruction for instruction as the reference lowers them
+(the config-1 listing: ``seeml-seeu-dump --instrs`` of ``MakeMlp(256, 512,
+256)``, rank 8, alpha 16, AdamW), into the reference's container:
+
+* the 320-byte ``PlanHeader`` (``source/plan/schema.h:296-412``), sealed with
+  ``PlanSelfHash`` (``source/identity/hash.h:136-158``, computed by the
+  library's own implementation);
+* 64-byte instruction words (``source/plan/instruction.h:438-449``);
+* one arena ``[persistent | I/O | transient]``: LoRA parameters, then the
+  AdamW moments, then the staged input, labels and loss slot, then every
+  activation and gradient (``arena_binder.h:18-27``);
+* rodata holding the frozen base weights, page-aligned in the blob.
+
+The arena offsets are this writer's own (a bump allocator, 64-byte aligned
+transients); the reference's memory planner may place transients
+differently, which changes no instruction's meaning.
+"""
+from __future__ import annotations
+
+import struct
+from dataclasses import dataclass, field
+
+import numpy as np
+
+SEEU_MAGIC = 0x55454553       # schema.h:18
+SEEU_VERSION = 26             # schema.h:165
+NULL_REF = 0xFFFFFFFFFFFFFFFF
+RODATA_BIT = 1 << 63
+PLAN_HASH_OFFSET = 216        # offsetof(PlanHeader, plan_hash)
+
+# Opcodes (instruction.h:44-232).
+GEMM_NN, GEMM_NT, GEMM_TN, GEMM_ACC_NN = 1, 2, 3, 4
+ADD_BIAS, RELU_FWD, RELU_BWD = 6, 7, 8
+XENT_FWD, XENT_BWD = 11, 12
+ADAMW = 18
+FILL = 19
+FLAG_ADDEND = 1 << 3          # kFlagGemmAddend
+
+# PlanHeader field order and widths (schema.h:296-384); packed, little-endian.
+_HEADER_FIELDS = [
+    ("magic", "I"), ("version", "I"), ("arena_size", "Q"), ("persistent_size", "Q"),
+    ("input_ref", "Q"), ("input_floats", "Q"), ("label_ref", "Q"), ("label_bytes", "Q"),
+    ("label_kind", "I"), ("optimizer_kind", "I"), ("loss_ref", "Q"),
+    ("train_instr_offset", "Q"), ("train_instr_count", "Q"),
+    ("merge_instr_offset", "Q"), ("merge_instr_count", "Q"),
+    ("rodata_offset", "Q"), ("rodata_size", "Q"),
+    ("persist_init_offset", "Q"), ("persist_init_size", "Q"),
+    ("emit_table_offset", "Q"), ("emit_count", "Q"),
+    ("lr", "f"), ("beta1", "f"), ("beta2", "f"), ("eps", "f"), ("weight_decay", "f"),
+    ("gemm_tile_k", "I"), ("batch", "Q"), ("default_steps", "Q"),
+    ("eval_instr_offset", "Q"), ("eval_instr_count", "Q"),
+    ("source_model_hash", "Q"), ("plan_hash", "Q"),
+    ("lr_schedule", "I"), ("gemm_tile_n", "I"), ("warmup_steps", "Q"),
+    ("min_lr_factor", "f"), ("clip_norm", "f"), ("input_kind", "I"),
+    ("grad_accum_steps", "I"), ("seq_len", "Q"),
+    ("step_instr_offset", "Q"), ("step_instr_count", "Q"),
+    ("tokenizer_hash", "Q"), ("corpus_hash", "Q"), ("split_seed", "Q"),
+    ("val_split_hash", "Q"), ("val_frac_bits", "I"), ("data_flags", "I"),
+]
+HEADER_FORMAT = "<" + "".join(f for _, f in _HEADER_FIELDS)
+HEADER_NAMES = [n for n, _ in _HEADER_FIELDS]
+assert struct.calcsize(HEADER_FORMAT) == 320
+
+
+def f32_bits(x: float) -> int:
+    return struct.unpack("<I", struct.pack("<f", x))[0]
+
+
+def ins(opcode: int, ins4=(), outs3=(), flags: int = 0, imm: int = 0) -> bytes:
+    """One 64-byte instruction word (instruction.h:438-447)."""
+    i4 = list(ins4) + [NULL_REF] * (4 - len(ins4))
+    o3 = list(outs3) + [0] * (3 - len(outs3))
+    return struct.pack("<HHI4Q3Q", opcode, flags, imm, *[int(x) for x in i4],
+                       *[int(x) for x in o3])
+
+
+def parse_header(blob: bytes) -> dict:
+    return dict(zip(HEADER_NAMES, struct.unpack_from(HEADER_FORMAT, blob, 0)))
+
+
+def pack_header(h: dict) -> bytes:
+    return struct.pack(HEADER_FORMAT, *[h[n] for n in HEADER_NAMES])
+
+
+# --- deterministic inputs ------------------------------------------------------------------------
+def splitmix64(seed: int, n: int) -> np.ndarray:
+    """n successive SplitMix64 outputs from `seed` (uint64)."""
+    with np.errstate(over="ignore"):
+        idx = np.arange(1, n + 1, dtype=np.uint64)
+        z = np.uint64(seed) + idx * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def normal(seed: int, shape, std: float = 1.0) -> np.ndarray:
+    """N(0, std^2) f32 by Box-Muller in double over SplitMix64 uniforms."""
+    n = int(np.prod(shape))
+    m = (n + 1) // 2
+    u = splitmix64(seed, 2 * m)
+    u1 = ((u[0::2] >> np.uint64(11)).astype(np.float64) + 1.0) * (1.0 / 9007199254740992.0)
+    u2 = (u[1::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+    r = np.sqrt(-2.0 * np.log(u1))
+    z = np.empty(2 * m, np.float64)
+    z[0::2] = r * np.cos(2.0 * np.pi * u2)
+    z[1::2] = r * np.sin(2.0 * np.pi * u2)
+    return (z[:n] * std).astype(np.float32).reshape(shape)
+
+
+def uniform_ints(seed: int, n: int, high: int) -> np.ndarray:
+    return (splitmix64(seed, n) % np.uint64(high)).astype(np.int32)
+
+
+# --- plan assembly -------------------------------------------------------------------------------
+@dataclass
+class Region:
+    """Bump allocation in one address space (arena or rodata)."""
+    base_bit: int = 0
+    align: int = 64
+    size: int = 0
+    names: dict = field(default_factory=dict)
+
+    def alloc(self, name: str, nbytes: int, align: int | None = None) -> int:
+        a = self.align if align is None else align
+        off = (self.size + a - 1) // a * a
+        self.size = off + nbytes
+        self.names[name] = (off, nbytes)
+        return off | self.base_bit
+
+    def ref(self, name: str) -> int:
+        return self.names[name][0] | self.base_bit
+
+
+@dataclass
+class PlanImage:
+    blob: bytes
+    header: dict
+    arena: dict          # name -> (offset, bytes)
+    rodata: dict         # name -> (offset, bytes)
+    train: list
+    eval: list
+    merge: list
+    arrays: dict         # the frozen and initial values, by name
+
+
+def assemble(header: dict, train: list, eval_: list, merge: list, emit: list,
+             persist_init: bytes, rodata: bytes, self_hash) -> bytes:
+    """Lays the sections out after the header and seals the plan.
+    `self_hash(blob) -> int` is PlanSelfHash with the hash field zeroed."""
+    out = bytearray(320)
+    h = dict(header)
+
+    def section(payload: bytes, align: int = 64) -> int:
+        pad = (-len(out)) % align
+        out.extend(b"\0" * pad)
+        off = len(out)
+        out.extend(payload)
+        return off
+
+    h["train_instr_offset"] = section(b"".join(train))
+    h["train_instr_count"] = len(train)
+    h["eval_instr_offset"] = section(b"".join(eval_))
+    h["eval_instr_count"] = len(eval_)
+    h["merge_instr_offset"] = section(b"".join(merge))
+    h["merge_instr_count"] = len(merge)
+    h["emit_table_offset"] = section(b"".join(struct.pack("<3Q", *e) for e in emit))
+    h["emit_count"] = len(emit)
+    h["persist_init_offset"] = section(persist_init)
+    h["persist_init_size"] = len(persist_init)
+    h["rodata_offset"] = section(rodata, align=4096)
+    h["rodata_size"] = len(rodata)
+    h["plan_hash"] = 0
+    out[0:320] = pack_header(h)
+    h["plan_hash"] = self_hash(bytes(out))
+    out[0:320] = pack_header(h)
+    return bytes(out)
+
+
+def mlp_lora(self_hash, batch: int = 32, din: int = 256, hidden: int = 512, dout: int = 256,
+             rank: int = 8, alpha: float = 16.0, lr: float = 1e-3, weight_decay: float = 0.01,
+             seed: int = 20261201, default_steps: int = 100) -> PlanImage:
+    """MLP din -> hidden (ReLU) -> dout with AddBias and
+    LoRA (rank, alpha) on both MatMuls, softmax-xent over dout classes,
+    AdamW.  Base weights and biases N(0, 0.02); LoRA A N(0, 0.02), B = 0.
+
+    The train program is the reference's 25 instructions, eval its first
+    10, merge the 4-instruction delta program (fill, GemmAccNN per site)."""
+    s = alpha / rank
+    arrays = {
+        "W1": normal(seed + 1, (din, hidden), 0.02), "b1": normal(seed + 2, (hidden,), 0.02),
+        "W2": normal(seed + 3, (hidden, dout), 0.02), "b2": normal(seed + 4, (dout,), 0.02),
+        "A1": normal(seed + 5, (din, rank), 0.02), "B1": np.zeros((rank, hidden), np.float32),
+        "A2": normal(seed + 6, (hidden, rank), 0.02), "B2": np.zeros((rank, dout), np.float32),
+    }
+    ro = Region(base_bit=RODATA_BIT, align=16)
+    for n in ("W1", "b1", "W2", "b2"):
+        ro.alloc(n, arrays[n].nbytes)
+    ar = Region(align=64)
+    params = ["A1", "B1", "A2", "B2"]
+    for n in params:                                   # persistent: parameters,
+        ar.alloc(n, arrays[n].nbytes, align=4)
+    for n in params:                                   # then first moments,
+        ar.alloc("m_" + n, arrays[n].nbytes, align=4)
+    for n in params:                                   # then second moments
+        ar.alloc("v_" + n, arrays[n].nbytes, align=4)
+    persistent = ar.size
+    ar.alloc("X", batch * din * 4, align=4)            # I/O slots
+    ar.alloc("labels", batch * 4, align=4)
+    ar.alloc("loss", 4, align=4)
+    f = 4
+    for name, shape in [("Z1", (batch, hidden)), ("t1", (batch, rank)), ("Z1b", (batch, hidden)),
+                        ("Z1c", (batch, hidden)), ("H1", (batch, hidden)),
+                        ("Z2", (batch, dout)), ("t2", (batch, rank)), ("Z2b", (batch, dout)),
+                        ("logits", (batch, dout)), ("probs", (batch, dout)), ("seed", (1,)),
+                        ("dZ", (batch, dout)), ("dt2", (batch, rank)), ("dB2", (rank, dout)),
+                        ("dA2", (hidden, rank)), ("dh", (batch, hidden)), ("dh2", (batch, hidden)),
+                        ("dH", (batch, hidden)), ("dt1", (batch, rank)), ("dB1", (rank, hidden)),
+                        ("dA1", (din, rank)), ("D1", (din, hidden)), ("D2", (hidden, dout))]:
+        ar.alloc(name, int(np.prod(shape)) * f)
+    R, RO = ar.ref, ro.ref
+    sb = f32_bits(s)
+    train = [
+        ins(GEMM_NN, [R("X"), RO("W1"), R("Z1")], [batch, hidden, din]),
+        ins(GEMM_NN, [R("X"), R("A1"), R("t1")], [batch, rank, din]),
+        ins(GEMM_NN, [R("t1"), R("B1"), R("Z1b"), R("Z1")], [batch, hidden, rank],
+            flags=FLAG_ADDEND, imm=sb),
+        ins(ADD_BIAS, [R("Z1b"), RO("b1"), R("Z1c")], [batch, hidden]),
+        ins(RELU_FWD, [R("Z1c"), R("H1")], [batch * hidden]),
+        ins(GEMM_NN, [R("H1"), RO("W2"), R("Z2")], [batch, dout, hidden]),
+        ins(GEMM_NN, [R("H1"), R("A2"), R("t2")], [batch, rank, hidden]),
+        ins(GEMM_NN, [R("t2"), R("B2"), R("Z2b"), R("Z2")], [batch, dout, rank],
+            flags=FLAG_ADDEND, imm=sb),
+        ins(ADD_BIAS, [R("Z2b"), RO("b2"), R("logits")], [batch, dout]),
+        ins(XENT_FWD, [R("logits"), R("labels"), R("loss"), R("probs")], [batch, dout]),
+        ins(FILL, [R("seed"), f32_bits(1.0)], [1]),
+        ins(XENT_BWD, [R("probs"), R("labels"), R("seed"), R("dZ")], [batch, dout]),
+        ins(GEMM_NT, [R("dZ"), R("B2"), R("dt2")], [batch, rank, dout], imm=sb),
+        ins(GEMM_TN, [R("t2"), R("dZ"), R("dB2")], [rank, dout, batch], imm=sb),
+        ins(GEMM_TN, [R("H1"), R("dt2"), R("dA2")], [hidden, rank, batch]),
+        ins(GEMM_NT, [R("dZ"), RO("W2"), R("dh")], [batch, hidden, dout]),
+        ins(GEMM_NT, [R("dt2"), R("A2"), R("dh2"), R("dh")], [batch, hidden, rank],
+            flags=FLAG_ADDEND),
+        ins(RELU_BWD, [R("dh2"), R("Z1c"), R("dH")], [batch * hidden]),
+        ins(GEMM_NT, [R("dH"), R("B1"), R("dt1")], [batch, rank, hidden], imm=sb),
+        ins(GEMM_TN, [R("t1"), R("dH"), R("dB1")], [rank, hidden, batch], imm=sb),
+        ins(GEMM_TN, [R("X"), R("dt1"), R("dA1")], [din, rank, batch]),
+    ]
+    for p, g in [("A1", "dA1"), ("B1", "dB1"), ("A2", "dA2"), ("B2", "dB2")]:
+        train.append(ins(ADAMW, [R(p), R(g), R("m_" + p), R("v_" + p)],
+                         [arrays[p].size, 0]))
+    eval_ = train[:10]
+    merge = [
+        ins(FILL, [R("D1"), 0], [din * hidden]),
+        ins(GEMM_ACC_NN, [R("A1"), R("B1"), R("D1"), sb], [din, hidden, rank]),
+        ins(FILL, [R("D2"), 0], [hidden * dout]),
+        ins(GEMM_ACC_NN, [R("A2"), R("B2"), R("D2"), sb], [hidden, dout, rank]),
+    ]
+    # The emit table names W's byte range in the source model file; this
+    # build has no .smf, so the file offsets are the rodata offsets.
+    emit = [(ro.names["W1"][0], arrays["W1"].nbytes, ar.names["D1"][0]),
+            (ro.names["W2"][0], arrays["W2"].nbytes, ar.names["D2"][0])]
+    persist = bytearray(persistent)
+    for n in params:
+        off, nb = ar.names[n]
+        persist[off:off + nb] = arrays[n].tobytes()
+    rodata = bytearray(ro.size)
+    for n in ("W1", "b1", "W2", "b2"):
+        off, nb = ro.names[n]
+        rodata[off:off + nb] = arrays[n].tobytes()
+    header = {n: 0 for n in HEADER_NAMES}
+    header.update(
+        magic=SEEU_MAGIC, version=SEEU_VERSION, arena_size=ar.size, persistent_size=persistent,
+        input_ref=R("X"), input_floats=batch * din, label_ref=R("labels"), label_bytes=batch * 4,
+        label_kind=1, optimizer_kind=1, loss_ref=R("loss"), lr=lr, beta1=0.9, beta2=0.999,
+        eps=1e-8, weight_decay=weight_decay, batch=batch, default_steps=default_steps,
+        step_instr_offset=0, step_instr_count=0)
+    blob = assemble(header, train, eval_, merge, emit, bytes(persist), bytes(rodata), self_hash)
+    return PlanImage(blob=blob, header=parse_header(blob), arena=dict(ar.names),
+                     rodata=dict(ro.names), train=train, eval=eval_, merge=merge, arrays=arrays)
