@@ -10,6 +10,7 @@ namespace {
 
 constexpr uint16_t kOpSoftmaxXEntFwd = 11, kOpSoftmaxXEntBwd = 12;              // instruction.h:63-64
 constexpr uint16_t kOpSoftmaxXEntMaskedFwd = 51, kOpSoftmaxXEntMaskedBwd = 52;  // v22 masked pair
+constexpr uint16_t kOpEmbedFwd = 41;                                            // instruction.h:141
 
 bool IsXent(uint16_t op) {
   return op == kOpSoftmaxXEntFwd || op == kOpSoftmaxXEntBwd || op == kOpSoftmaxXEntMaskedFwd ||
@@ -35,7 +36,19 @@ Result<std::unique_ptr<PlanEngine>> PlanEngine::Load(std::span<const uint8_t> bl
         e->num_classes_ = ins.out[1];
       if (ins.opcode == kOpSoftmaxXEntMaskedFwd || ins.opcode == kOpSoftmaxXEntMaskedBwd)
         e->masked_labels_ = true;
+      // plan_loader.cc:196-204: the narrowest embedding bounds token ids.
+      if (ins.opcode == kOpEmbedFwd) {
+        const uint64_t vocab = ins.out[1] >> 32;
+        if (vocab != 0 && (e->vocab_bound_ == 0 || vocab < e->vocab_bound_)) e->vocab_bound_ = vocab;
+      }
     }
+  if (h.input_kind > 1) return Fail("unknown plan input kind " + std::to_string(h.input_kind));
+  if (h.input_kind == 1) {
+    if (e->vocab_bound_ == 0)
+      return Fail("token plan carries no embedding \xe2\x80\x94 its token ids could never be validated");
+    if (h.seq_len == 0 || h.batch % h.seq_len != 0)
+      return Fail("token plan sequence length must be nonzero and divide the batch");
+  }
   if (h.label_kind == 1 && e->num_classes_ == 0)
     return Fail("class-label plan carries no softmax cross-entropy \xe2\x80\x94 its labels could "
                 "never be validated");
@@ -84,6 +97,14 @@ float PlanEngine::EffectiveLr() const {
 Result<void> PlanEngine::Stage(const float* input, const void* labels) {
   const PlanHeader& h = plan_.header;
   const uint64_t in_off = RefOffset(h.input_ref), in_bytes = h.input_floats * sizeof(float);
+  if (h.input_kind == 1) {
+    // The feeder's token contract: every id indexes an embedding row.
+    const auto* tok = reinterpret_cast<const int32_t*>(input);
+    for (uint64_t i = 0; i < h.input_floats; ++i)
+      if (tok[i] < 0 || static_cast<uint64_t>(tok[i]) >= vocab_bound_)
+        return Fail("token " + std::to_string(tok[i]) + " at position " + std::to_string(i) +
+                    " is outside the plan's " + std::to_string(vocab_bound_) + "-token vocabulary");
+  }
   std::memcpy(arena_ + in_off, input, in_bytes);
   if (auto r = backend_->SyncToDevice(in_off, in_bytes); !r) return r;
   if (h.label_kind == 0) return {};

@@ -72,6 +72,7 @@ class PlanEngine {
   uint64_t horizon_ = 0;
   uint64_t num_classes_ = 0;
   bool masked_labels_ = false;  // the plan's loss ignores positions labelled -1
+  uint64_t vocab_bound_ = 0;     // token plans: the narrowest embedding's rows
 };
 
 }  // namespace seeai::host

@@ -282,3 +282,231 @@ def mlp_lora(self_hash, batch: int = 32, din: int = 256, hidden: int = 512, dout
     blob = assemble(header, train, eval_, merge, emit, bytes(persist), bytes(rodata), self_hash)
     return PlanImage(blob=blob, header=parse_header(blob), arena=dict(ar.names),
                      rodata=dict(ro.names), train=train, eval=eval_, merge=merge, arrays=arrays)
+
+
+# --- the decoder LoRA training step ----------------------------------------
+LAYERNORM_FWD, LAYERNORM_BWD = 26, 27
+ADD_EW = 5
+GELU_FWD, GELU_BWD = 22, 23
+ROPE_FWD, ROPE_BWD, ROPE_TABLE = 33, 34, 45
+EMBED_FWD = 41
+ATTN_FWD_TILED, ATTN_DQ_TILED, ATTN_DK_TILED, ATTN_DV_TILED = 47, 48, 49, 50
+FLAG_RELAXED = 1 << 5        # kFlagRelaxed
+
+
+class Builder:
+    """Arena / rodata allocation and the three programs of one plan."""
+
+    def __init__(self):
+        self.ro = Region(base_bit=RODATA_BIT, align=16)
+        self.ar = Region(align=256)
+        self.arrays: dict = {}
+        self.params: list = []
+        self.train: list = []
+
+    def const(self, name: str, array: np.ndarray) -> int:
+        self.arrays[name] = np.ascontiguousarray(array)
+        return self.ro.alloc(name, self.arrays[name].nbytes)
+
+    def param(self, name: str, array: np.ndarray) -> int:
+        self.arrays[name] = np.ascontiguousarray(array, np.float32)
+        self.params.append(name)
+        return self.ar.alloc(name, self.arrays[name].nbytes, align=4)
+
+    def buf(self, name: str, count: int, itemsize: int = 4) -> int:
+        return self.ar.alloc(name, count * itemsize)
+
+    def emit(self, word: bytes):
+        self.train.append(word)
+
+
+def decoder_lora(self_hash, vocab: int = 32000, dim: int = 768, heads: int = 12, ffn: int = 3072,
+                 layers: int = 12, seq: int = 1024, batch: int = 8, rank: int = 8,
+                 alpha: float = 16.0, relaxed: bool = True, rope_base: float = 10000.0,
+                 lr: float = 1e-3, weight_decay: float = 0.01, seed: int = 20261204,
+                 default_steps: int = 100) -> PlanImage:
+    """a pre-norm decoder of `layers` blocks -- LayerNorm,
+    Q / K / V projections with LoRA (rank, alpha) on Q and V, RoPE, causal
+    attention (the tiled family), output projection, residual; LayerNorm,
+    FFN dim -> ffn (GELU) -> dim, residual -- then a final LayerNorm, the
+    vocabulary head and next-token softmax-xent, AdamW on the adapters.
+    Frozen weights N(0, 0.02), gains 1, LoRA A N(0, 0.02), B = 0; token ids
+    are the input (input_kind 1), next tokens the labels.
+
+    The lowering follows the reference's rules: each adapted MatMul is the
+    NN + NN-addend pair forward and the NT / TN / TN / NT-addend family
+    backward (lora_grafter.cc:170-207, autodiff.cc:71-93); frozen MatMuls
+    contribute only dX (NT); a residual's two gradient paths add (kAddEW);
+    the tiled attention backward runs dQ before dK and dV; gradients no
+    trainable parameter needs are not formed (the first block's dX chain and
+    its dK).  `relaxed` sets kFlagRelaxed on the frozen-weight products and
+    on attention (bf16 activations, f32 master weights and adapters).
+    """
+    assert dim % heads == 0
+    T, D, F, H, d = batch * seq, dim, ffn, heads, dim // heads
+    s = alpha / rank
+    sb = f32_bits(s)
+    rf = FLAG_RELAXED if relaxed else 0
+    b = Builder()
+    R, RO = b.ar.ref, b.ro.ref
+    # Frozen weights (rodata) and adapters (persistent).
+    b.const("emb", normal(seed, (vocab, D), 0.02))
+    ones, zeros = np.ones(D, np.float32), np.zeros(D, np.float32)
+    for l in range(layers):
+        p = f"l{l}."
+        b.const(p + "g1", ones)
+        b.const(p + "b1", zeros)
+        for w in "qkvo":
+            b.const(p + "w" + w, normal(seed + 100 * l + ord(w), (D, D), 0.02))
+        b.const(p + "g2", ones)
+        b.const(p + "b2", zeros)
+        b.const(p + "wu", normal(seed + 100 * l + 1, (D, F), 0.02))
+        b.const(p + "wd", normal(seed + 100 * l + 2, (F, D), 0.02))
+    b.const("gf", ones)
+    b.const("bf", zeros)
+    b.const("wh", normal(seed + 7, (D, vocab), 0.02))
+    for l in range(layers):
+        p = f"l{l}."
+        for w in "qv":
+            b.param(p + "A" + w, normal(seed + 1000 + 10 * l + ord(w), (D, rank), 0.02))
+            b.param(p + "B" + w, np.zeros((rank, D), np.float32))
+    for n in list(b.params):
+        b.ar.alloc("m_" + n, b.arrays[n].nbytes, align=4)
+    for n in list(b.params):
+        b.ar.alloc("v_" + n, b.arrays[n].nbytes, align=4)
+    persistent = b.ar.size
+    b.buf("tokens", T)
+    b.buf("labels", T)
+    b.buf("loss", 1)
+    b.buf("seed", 1)
+    b.buf("rope", seq * (d // 2) * 2)
+    # Saved activations, per block.
+    TD, TF, Tr = T * D, T * F, T * rank
+    for l in range(layers):
+        p = f"l{l}."
+        for n, c in [("x", TD), ("n1", TD), ("mean1", T), ("rstd1", T), ("tq", Tr), ("tv", Tr),
+                     ("qr", TD), ("kr", TD), ("v", TD), ("a", TD), ("stats", T * H * 4),
+                     ("x1", TD), ("n2", TD), ("mean2", T), ("rstd2", T), ("f", TF)]:
+            b.buf(p + n, c)
+    for n, c in [("xL", TD), ("nf", TD), ("meanf", T), ("rstdf", T), ("logits", T * vocab),
+                 ("probs", T * vocab)]:
+        b.buf(n, c)
+    # Scratch shared by the blocks (forward products, backward gradients).
+    for n, c in [("q0", TD), ("q", TD), ("k", TD), ("v0", TD), ("o", TD), ("h", TF),
+                 ("dlogits", T * vocab), ("dnf", TD), ("dx2", TD), ("dh", TF), ("df", TF),
+                 ("dn2", TD), ("dx1b", TD), ("dx1", TD), ("da", TD), ("dqr", TD), ("dkr", TD),
+                 ("dv", TD), ("dq", TD), ("dk", TD), ("dtq", Tr), ("dtv", Tr),
+                 ("dn1a", TD), ("dn1b", TD), ("dxb", TD), ("dx", TD)]:
+        b.buf(n, c)
+    for l in range(layers):
+        p = f"l{l}."
+        for w in "qv":
+            b.buf(p + "dA" + w, D * rank)
+            b.buf(p + "dB" + w, rank * D)
+
+    E = b.emit
+    bs, hd = (batch << 32) | seq, (H << 32) | d
+    geo = (batch << 48) | (seq << 32) | (H << 16) | d
+    base_bits = f32_bits(rope_base)
+    # --- forward ---
+    E(ins(ROPE_TABLE, [R("rope")], [(seq << 32) | d, base_bits]))
+    E(ins(EMBED_FWD, [R("tokens"), RO("emb"), R("l0.x")], [T, (vocab << 32) | D]))
+
+    def adapted(x, w, A, B_, t, out0, out):
+        """C = x@W + s*(x@A)@B: NN, NN, NN-addend (the LoRA site, forward)."""
+        E(ins(GEMM_NN, [R(x), RO(w), R(out0)], [T, D, D], flags=rf))
+        E(ins(GEMM_NN, [R(x), R(A), R(t)], [T, rank, D]))
+        E(ins(GEMM_NN, [R(t), R(B_), R(out), R(out0)], [T, D, rank], flags=FLAG_ADDEND, imm=sb))
+
+    for l in range(layers):
+        p = f"l{l}."
+        nxt = f"l{l + 1}.x" if l + 1 < layers else "xL"
+        E(ins(LAYERNORM_FWD, [R(p + "x"), RO(p + "g1"), RO(p + "b1"), R(p + "n1")],
+              [(T << 32) | D, R(p + "mean1"), R(p + "rstd1")]))
+        adapted(p + "n1", p + "wq", p + "Aq", p + "Bq", p + "tq", "q0", "q")
+        E(ins(GEMM_NN, [R(p + "n1"), RO(p + "wk"), R("k")], [T, D, D], flags=rf))
+        adapted(p + "n1", p + "wv", p + "Av", p + "Bv", p + "tv", "v0", p + "v")
+        E(ins(ROPE_FWD, [R("q"), R(p + "qr"), R("rope")], [bs, hd, base_bits]))
+        E(ins(ROPE_FWD, [R("k"), R(p + "kr"), R("rope")], [bs, hd, base_bits]))
+        E(ins(ATTN_FWD_TILED, [R(p + "qr"), R(p + "kr"), R(p + "v"), R(p + "a")],
+              [R(p + "stats"), bs, hd], flags=rf))
+        E(ins(GEMM_NN, [R(p + "a"), RO(p + "wo"), R("o")], [T, D, D], flags=rf))
+        E(ins(ADD_EW, [R(p + "x"), R("o"), R(p + "x1")], [TD]))
+        E(ins(LAYERNORM_FWD, [R(p + "x1"), RO(p + "g2"), RO(p + "b2"), R(p + "n2")],
+              [(T << 32) | D, R(p + "mean2"), R(p + "rstd2")]))
+        E(ins(GEMM_NN, [R(p + "n2"), RO(p + "wu"), R(p + "f")], [T, F, D], flags=rf))
+        E(ins(GELU_FWD, [R(p + "f"), R("h")], [TF]))
+        E(ins(GEMM_NN, [R("h"), RO(p + "wd"), R("o")], [T, D, F], flags=rf))
+        E(ins(ADD_EW, [R(p + "x1"), R("o"), R(nxt)], [TD]))
+    E(ins(LAYERNORM_FWD, [R("xL"), RO("gf"), RO("bf"), R("nf")],
+          [(T << 32) | D, R("meanf"), R("rstdf")]))
+    E(ins(GEMM_NN, [R("nf"), RO("wh"), R("logits")], [T, vocab, D], flags=rf))
+    E(ins(XENT_FWD, [R("logits"), R("labels"), R("loss"), R("probs")], [T, vocab]))
+    n_eval = len(b.train)
+    # --- backward ---
+    E(ins(FILL, [R("seed"), f32_bits(1.0)], [1]))
+    E(ins(XENT_BWD, [R("probs"), R("labels"), R("seed"), R("dlogits")], [T, vocab]))
+    E(ins(GEMM_NT, [R("dlogits"), RO("wh"), R("dnf")], [T, D, vocab], flags=rf))
+    E(ins(LAYERNORM_BWD, [R("dnf"), R("xL"), RO("gf"), R("dx2")],
+          [R("meanf"), R("rstdf"), (T << 32) | D]))
+    for l in reversed(range(layers)):
+        p = f"l{l}."
+        # x2 = x1 + FFN(LN2(x1)): dx1 = dx2 + LN2_bwd(FFN_bwd(dx2))
+        E(ins(GEMM_NT, [R("dx2"), RO(p + "wd"), R("dh")], [T, F, D], flags=rf))
+        E(ins(GELU_BWD, [R("dh"), R(p + "f"), R("df")], [TF]))
+        E(ins(GEMM_NT, [R("df"), RO(p + "wu"), R("dn2")], [T, D, F], flags=rf))
+        E(ins(LAYERNORM_BWD, [R("dn2"), R(p + "x1"), RO(p + "g2"), R("dx1b")],
+              [R(p + "mean2"), R(p + "rstd2"), (T << 32) | D]))
+        E(ins(ADD_EW, [R("dx2"), R("dx1b"), R("dx1")], [TD]))
+        # x1 = x + Wo(attn(...)): the attention input gradients
+        E(ins(GEMM_NT, [R("dx1"), RO(p + "wo"), R("da")], [T, D, D], flags=rf))
+        qkv = [R(p + "qr"), R(p + "kr"), R(p + "v"), R("da")]
+        E(ins(ATTN_DQ_TILED, qkv, [R(p + "stats"), R("dqr"), geo], flags=rf))
+        if l > 0:
+            E(ins(ATTN_DK_TILED, qkv, [R(p + "stats"), R("dkr"), geo], flags=rf))
+        E(ins(ATTN_DV_TILED, qkv, [R(p + "stats"), R("dv"), geo], flags=rf))
+        E(ins(ROPE_BWD, [R("dqr"), R("dq"), R("rope")], [bs, hd, base_bits]))
+        if l > 0:
+            E(ins(ROPE_BWD, [R("dkr"), R("dk"), R("rope")], [bs, hd, base_bits]))
+        # the LoRA sites (Q, V): dt = s dC B^T, dB = s t^T dC, dA = X^T dt
+        for w, dC, t, dt in [("q", "dq", p + "tq", "dtq"), ("v", "dv", p + "tv", "dtv")]:
+            E(ins(GEMM_NT, [R(dC), R(p + "B" + w), R(dt)], [T, rank, D], imm=sb))
+            E(ins(GEMM_TN, [R(t), R(dC), R(p + "dB" + w)], [rank, D, T], imm=sb))
+            E(ins(GEMM_TN, [R(p + "n1"), R(dt), R(p + "dA" + w)], [D, rank, T]))
+        if l == 0:
+            continue  # nothing trainable below the first block's inputs
+        # dn1 = dq Wq^T + dtq Aq^T + dk Wk^T + dv Wv^T + dtv Av^T (NT + addend chain)
+        E(ins(GEMM_NT, [R("dq"), RO(p + "wq"), R("dn1a")], [T, D, D], flags=rf))
+        E(ins(GEMM_NT, [R("dtq"), R(p + "Aq"), R("dn1b"), R("dn1a")], [T, D, rank],
+              flags=FLAG_ADDEND))
+        E(ins(GEMM_NT, [R("dk"), RO(p + "wk"), R("dn1a"), R("dn1b")], [T, D, D],
+              flags=FLAG_ADDEND | rf))
+        E(ins(GEMM_NT, [R("dv"), RO(p + "wv"), R("dn1b"), R("dn1a")], [T, D, D],
+              flags=FLAG_ADDEND | rf))
+        E(ins(GEMM_NT, [R("dtv"), R(p + "Av"), R("dn1a"), R("dn1b")], [T, D, rank],
+              flags=FLAG_ADDEND))
+        E(ins(LAYERNORM_BWD, [R("dn1a"), R(p + "x"), RO(p + "g1"), R("dxb")],
+              [R(p + "mean1"), R(p + "rstd1"), (T << 32) | D]))
+        E(ins(ADD_EW, [R("dx1"), R("dxb"), R("dx2")], [TD]))  # dx2 of the block below
+    for n in b.params:
+        g = n.replace(".A", ".dA").replace(".B", ".dB")
+        E(ins(ADAMW, [R(n), R(g), R("m_" + n), R("v_" + n)], [b.arrays[n].size, 0]))
+    train = b.train
+    eval_ = train[:n_eval]
+    persist = bytearray(persistent)
+    for n in b.params:
+        off, nb = b.ar.names[n]
+        persist[off:off + nb] = b.arrays[n].tobytes()
+    rodata = bytearray(b.ro.size)
+    for n, (off, nb) in b.ro.names.items():
+        rodata[off:off + nb] = b.arrays[n].tobytes()
+    header = {n: 0 for n in HEADER_NAMES}
+    header.update(
+        magic=SEEU_MAGIC, version=SEEU_VERSION, arena_size=b.ar.size, persistent_size=persistent,
+        input_ref=R("tokens"), input_floats=T, label_ref=R("labels"), label_bytes=T * 4,
+        label_kind=1, optimizer_kind=1, loss_ref=R("loss"), lr=lr, beta1=0.9, beta2=0.999,
+        eps=1e-8, weight_decay=weight_decay, batch=T, default_steps=default_steps,
+        input_kind=1, seq_len=seq)
+    blob = assemble(header, train, eval_, [], [], bytes(persist), bytes(rodata), self_hash)
+    return PlanImage(blob=blob, header=parse_header(blob), arena=dict(b.ar.names),
+                     rodata=dict(b.ro.names), train=train, eval=eval_, merge=[], arrays=b.arrays)

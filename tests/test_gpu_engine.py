@@ -108,3 +108,95 @@ def test_corrupt_plan_is_refused_before_the_device(hip, torch_cuda, c1):
     with pytest.raises(hip.BackendError) as err:
         hip.Engine(bytes(blob))
     assert str(err.value) == "plan hash mismatch — the .seeu blob is corrupt"
+
+
+# --- the decoder LoRA step (BASELINE configs[3] at a small shape) --------------------------------
+
+TINY = dict(vocab=96, dim=128, heads=2, ffn=256, layers=2, seq=64, batch=2, rank=8)
+
+
+def tokens(step):
+    T = TINY["batch"] * TINY["seq"]
+    t = pw.uniform_ints(5000 + step, T + 1, TINY["vocab"])
+    return t[:T].copy(), t[1:].copy()
+
+
+def expect_close(what, got, want, rel, abs_floor):
+    """Elementwise |got - want| <= abs_floor + rel |want|, NaN failing
+    (the reference's ExpectClose, metal_backend_test.cc:85-106)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    bad = ~(err <= abs_floor + rel * np.abs(want))
+    assert not bad.any(), (f"{what}[{int(np.argmax(bad))}]: gpu {got[bad][0]} vs cpu {want[bad][0]}"
+                           f" ({int(bad.sum())} of {bad.size} outside)")
+
+
+def run_decoder(hip, orc, relaxed, steps):
+    img = pw.decoder_lora(hip.plan_self_hash, relaxed=relaxed, **TINY)
+    eng = hip.Engine(img.blob)
+    twin = OracleEngine(orc, img.blob) if orc is not None else None
+    curve, want = [], []
+    for s in range(steps):
+        x, y = tokens(s)
+        curve.append(eng.train_step(x.view(np.float32), y))
+        if twin:
+            want.append(twin.train_step(x.view(np.float32), y))
+    return img, eng, twin, np.array(curve), np.array(want)
+
+
+@pytest.mark.parametrize("relaxed", [False, True])
+def test_decoder_training_matches_the_oracle(hip, orc, torch_cuda, relaxed):
+    """Eight steps of the decoder plan against its CPU twin.
+
+    Per-instruction the exact family is bit-exact (GEMMs, elementwise) or
+    within 1e-5 (attention's f32 dots, the device libm's exp / tanh /
+    sin / cos, norm sums); AdamW then divides by sqrt(v) + eps, which turns
+    gradient differences far below 1e-5 of the tensor's scale into full-size
+    update differences wherever a gradient is near eps.  So the training
+    curve is held to the reference's own GPU-vs-CPU doctrine for 8 AdamW
+    steps (metal_backend_test.cc:210-232): losses rel 2e-3 / abs 1e-4, the
+    persistent segment (adapters and moments) rel 5e-3 / abs 1e-6 -- and
+    each step's loss to 1e-5 (exact) or 2e-2 (relaxed, bf16 attention).
+
+    Relaxed, the adapters are not compared elementwise: AdamW's first step
+    moves each element by lr * sign(g), and bf16 attention changes the sign
+    of gradients that sit at the noise floor, so single elements differ by
+    2 lr while the loss curve agrees to 1e-5.  The reference holds its
+    relaxed family per instruction (RelaxedGemmsMatchCpuAtTheBf16Tolerance,
+    metal_backend_test.cc:745-850), as test_gpu_ops.py does here."""
+    print(f"engine: decoder plan {TINY}, relaxed={relaxed}", flush=True)
+    img, eng, twin, curve, want = run_decoder(hip, orc, relaxed, 8)
+    step_tol = 2e-2 if relaxed else 1e-5
+    assert np.all(np.abs(curve - want) <= step_tol * np.abs(want)), (curve, want)
+    expect_close("loss curve", curve, want, 2e-3, 1e-4)
+    if not relaxed:
+        persistent = img.header["persistent_size"]
+        g = np.frombuffer(eng.read(0, persistent), np.float32)
+        c = np.frombuffer(twin.read(0, persistent), np.float32)
+        expect_close("persistent", g, c, 5e-3, 1e-6)
+    assert (eng.relaxed_executions() > 0) == relaxed
+    eng.close()
+
+
+def test_decoder_training_is_bitwise_reproducible(hip, torch_cuda):
+    """Run to run on one device the bits repeat: no float atomics, fixed
+    reduction orders (metal_backend_test.cc:234-251)."""
+    img, a, _, ca, _ = run_decoder(hip, None, True, 5)
+    _, b, _, cb, _ = run_decoder(hip, None, True, 5)
+    assert ca.tobytes() == cb.tobytes()
+    n = img.header["persistent_size"]
+    assert a.read(0, n) == b.read(0, n)
+    a.close()
+    b.close()
+
+
+def test_token_outside_the_vocabulary_is_refused(hip, torch_cuda):
+    img = pw.decoder_lora(hip.plan_self_hash, **TINY)
+    eng = hip.Engine(img.blob)
+    x, y = tokens(0)
+    x[7] = TINY["vocab"]
+    with pytest.raises(hip.BackendError) as err:
+        eng.train_step(x.view(np.float32), y)
+    assert "token 96 at position 7" in str(err.value)
+    eng.close()

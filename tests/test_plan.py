@@ -181,3 +181,44 @@ def test_effective_lr_schedule():
     assert effective_lr(h, 60, 0) == pytest.approx(1e-4 + 0.9e-3 * 0.5, rel=1e-6)
     assert effective_lr(h, 110, 0) == pytest.approx(1e-4)
     assert effective_lr({**h, "lr_schedule": 0}, 60, 0) == pytest.approx(1e-3)
+
+
+# --- the decoder plan (BASELINE configs[3] at a small shape) -----------------------------------------
+
+TINY = dict(vocab=96, dim=128, heads=2, ffn=256, layers=2, seq=64, batch=2, rank=8)
+
+
+@pytest.fixture(scope="module")
+def dec(hip):
+    return pw.decoder_lora(hip.plan_self_hash, **TINY)
+
+
+def test_decoder_plan_structure(hip, dec):
+    assert hip.plan_check(dec.blob) == ""
+    h = dec.header
+    assert h["input_kind"] == 1 and h["seq_len"] == 64 and h["batch"] == 128
+    ops = [struct.unpack_from("<HH", w) for w in dec.train]
+    opc = [o for o, _ in ops]
+    # per block: 1 LoRA site pair each on Q and V = 3 GEMMs forward each,
+    # and the tiled attention forward; the backward's dK only above block 0
+    assert opc.count(47) == 2 and opc.count(48) == 2 and opc.count(49) == 1 and opc.count(50) == 2
+    assert opc.count(18) == 2 * 2 * 2  # AdamW on Aq, Bq, Av, Bv of each block
+    assert opc.count(41) == 1 and opc.count(45) == 1
+    # relaxed: the frozen-weight products and attention; never the adapters
+    for w, (op, flags) in zip(dec.train, ops):
+        ins4 = struct.unpack_from("<4Q", w, 8)
+        if op in (47, 48, 49, 50):
+            assert flags & (1 << 5)
+        if op in (1, 2, 3) and not any(r >> 63 for r in ins4[:2]):
+            assert not flags & (1 << 5), "an adapter product carries the relaxed flag"
+    assert dec.eval == dec.train[:len(dec.eval)]
+    assert struct.unpack_from("<H", dec.eval[-1])[0] == 11
+
+
+def test_decoder_first_step_through_the_oracle(orc, dec):
+    eng = OracleEngine(orc, dec.blob)
+    T = TINY["batch"] * TINY["seq"]
+    toks = pw.uniform_ints(11, T, TINY["vocab"])
+    labels = np.roll(toks, -1)
+    loss = eng.train_step(toks.view(np.float32), labels)
+    assert abs(loss - math.log(TINY["vocab"])) < 0.05
