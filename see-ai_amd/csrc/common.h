@@ -214,6 +214,9 @@ struct GemmArgs {
 // Relaxed -> MFMA (k_gemm_f32.hip); otherwise the reference's order.
 hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s);
 hipError_t LaunchGemmExact(const GemmArgs& a, hipStream_t s);
+// Relaxed f32-weight NN / NT on bf16 MFMA (k_gemm_bf16.hip), when it fits.
+bool GemmBf16Fits(const GemmArgs& a);
+hipError_t LaunchGemmBf16(const GemmArgs& a, hipStream_t s);
 
 // W8A8 (k_gemm_i8.hip).
 hipError_t LaunchQuantizeRows(const float* X, int8_t* Q, float* scale, size_t rows, size_t cols,

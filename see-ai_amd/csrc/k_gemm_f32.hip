@@ -18,9 +18,10 @@
 // k-scale multiplies A's elements; the NT alpha multiplies the finished dot.
 // Then C = [D +] dot, and act(C + bias).  The products are exact and the
 // MFMA sums them in f32 in its own order, so results agree with the
-// reference to rounding (max-rel 1e-5): this is the relaxed family's path
-// (kFlagRelaxed); the exact family runs the reference's order in
-// k_gemm_exact.hip.
+// reference to rounding (max-rel 1e-5).  This serves the relaxed family
+// (kFlagRelaxed) where the bf16 MFMA kernel (k_gemm_bf16.hip: f32 weights,
+// tiles of 64 and more) does not; the exact family runs the reference's
+// order in k_gemm_exact.hip.
 #include "common.h"
 
 namespace seeai {
@@ -192,6 +193,7 @@ hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s) {
   // The exact family keeps the reference's reduction order (bit-exact,
   // k_gemm_exact.hip); MFMA's own summation order is the relaxed family's.
   if (!a.relaxed) return LaunchGemmExact(a, s);
+  if (GemmBf16Fits(a)) return LaunchGemmBf16(a, s);
   switch (a.layout * 3 + a.b_kind) {
     case 0: return Dispatch<0, 0>(a, s);
     case 1: return Dispatch<0, 1>(a, s);

@@ -492,7 +492,10 @@ def decoder_lora(self_hash, vocab: int = 32000, dim: int = 768, heads: int = 12,
         g = n.replace(".A", ".dA").replace(".B", ".dB")
         E(ins(ADAMW, [R(n), R(g), R("m_" + n), R("v_" + n)], [b.arrays[n].size, 0]))
     train = b.train
-    eval_ = train[:n_eval]
+    # The eval program scores what ships, in exact arithmetic: the forward
+    # without kFlagRelaxed (instruction.h:356-384).
+    eval_ = [w[:2] + struct.pack("<H", struct.unpack_from("<H", w, 2)[0] & ~FLAG_RELAXED) + w[4:]
+             for w in train[:n_eval]]
     persist = bytearray(persistent)
     for n in b.params:
         off, nb = b.ar.names[n]
