@@ -161,6 +161,17 @@ int AdamWLaunch(seeai_ctx* c, float* p, const float* g, float* m, float* v, uint
   return SEEAI_OK;
 }
 
+// A GEMM launch with the workspace its kernel may use.
+int Gemm(seeai_ctx* c, GemmArgs& a, const char* what) {
+  if (const size_t bytes = a.relaxed ? 0 : GemmExactScratchBytes(a)) {
+    void* ws;
+    if (int rc = Scratch(c, bytes, &ws)) return rc;
+    a.scratch = static_cast<float*>(ws);
+  }
+  SEEAI_TRY(c, LaunchGemm(a, c->stream), what);
+  return SEEAI_OK;
+}
+
 // kFlagRelaxed (instruction.h:356-384) taken as a permission when the
 // context allows it; each relaxed execution is counted (backend.h:149-162).
 int Relaxed(seeai_ctx* c, const Instruction& ins) {
@@ -199,8 +210,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       a.bias = (ins.opcode == 1 && (ins.flags & kFlagEpilogueBias)) ? R.f(ins.in[3]) : nullptr;
       a.act = ins.opcode == 1 ? act : 0;
       a.relaxed = Relaxed(c, ins);
-      SEEAI_TRY(c, LaunchGemm(a, s), "gemm");
-      return SEEAI_OK;
+      return Gemm(c, a, "gemm");
     }
     case 4: {  // kGemmAccNN: C += alpha A@B, alpha bits in in[3]
       GemmArgs a{};
@@ -215,8 +225,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       a.alpha_dot = 1.0f;
       a.accumulate = 1;
       a.relaxed = Relaxed(c, ins);
-      SEEAI_TRY(c, LaunchGemm(a, s), "gemm.acc_nn");
-      return SEEAI_OK;
+      return Gemm(c, a, "gemm.acc_nn");
     }
     case 29:    // kGemmNNQ8
     case 30: {  // kGemmNTQ8
@@ -245,8 +254,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       }
       a.act = nt ? 0 : act;
       a.relaxed = Relaxed(c, ins);
-      SEEAI_TRY(c, LaunchGemm(a, s), "gemm.q8");
-      return SEEAI_OK;
+      return Gemm(c, a, "gemm.q8");
     }
     case 43:    // kGemmNNBF16
     case 44: {  // kGemmNTBF16
@@ -265,8 +273,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       a.bias = (!nt && (ins.flags & kFlagEpilogueBias)) ? R.f(ins.in[3]) : nullptr;
       a.act = nt ? 0 : act;
       a.relaxed = Relaxed(c, ins);
-      SEEAI_TRY(c, LaunchGemm(a, s), "gemm.bf16");
-      return SEEAI_OK;
+      return Gemm(c, a, "gemm.bf16");
     }
     case 5:
       SEEAI_TRY(c, LaunchAddEW(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s), "add");
@@ -703,8 +710,7 @@ int seeai_gemm_f32(seeai_ctx* c, int layout, const float* A, const float* B, flo
   a.bias = bias;
   a.act = act;
   a.accumulate = accumulate;
-  SEEAI_TRY(c, LaunchGemm(a, c->stream), "gemm_f32");
-  return SEEAI_OK;
+  return Gemm(c, a, "gemm_f32");
 }
 
 int seeai_gemm_q8(seeai_ctx* c, int nt, const float* A, const int8_t* B, float* C, uint64_t M,
@@ -729,8 +735,7 @@ int seeai_gemm_q8(seeai_ctx* c, int nt, const float* A, const int8_t* B, float* 
       a.b_col_scale = col_scale;
   }
   a.act = act;
-  SEEAI_TRY(c, LaunchGemm(a, c->stream), "gemm_q8");
-  return SEEAI_OK;
+  return Gemm(c, a, "gemm_q8");
 }
 
 int seeai_gemm_bf16w(seeai_ctx* c, int nt, const float* A, const uint16_t* B, float* C, uint64_t M,
@@ -749,8 +754,7 @@ int seeai_gemm_bf16w(seeai_ctx* c, int nt, const float* A, const uint16_t* B, fl
   a.alpha_dot = 1.0f;
   a.bias = bias;
   a.act = act;
-  SEEAI_TRY(c, LaunchGemm(a, c->stream), "gemm_bf16w");
-  return SEEAI_OK;
+  return Gemm(c, a, "gemm_bf16w");
 }
 
 int seeai_w8a8_quantize_rows(seeai_ctx* c, const float* X, int8_t* Q, float* scale, uint64_t rows,

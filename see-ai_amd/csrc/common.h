@@ -210,10 +210,13 @@ struct GemmArgs {
   int act;                   // epilogue activation
   int accumulate;            // C += (GemmAccNN)
   int relaxed;               // kFlagRelaxed taken: MFMA summation order
+  float* scratch;            // device workspace (GemmExactScratchBytes), or null
 };
 // Relaxed -> MFMA (k_gemm_f32.hip); otherwise the reference's order.
 hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s);
 hipError_t LaunchGemmExact(const GemmArgs& a, hipStream_t s);
+// Workspace the exact kernels can use for this GEMM (0: none).
+size_t GemmExactScratchBytes(const GemmArgs& a);
 // Relaxed f32-weight NN / NT on bf16 MFMA (k_gemm_bf16.hip), when it fits.
 bool GemmBf16Fits(const GemmArgs& a);
 hipError_t LaunchGemmBf16(const GemmArgs& a, hipStream_t s);

@@ -324,59 +324,161 @@ __global__ void __launch_bounds__(kThreads) GemmPanelKernel(GemmArgs g) {
 
 // ---------------------------------------------------------------------------
 // Long reductions over few outputs (NN / TN, M*N small, K large: the LoRA
-// dA / dB over every token).  A workgroup owns 64 outputs.  K goes by in
-// chunks of kChunkQ quads: waves 1-3 form the chunk's quad sums into LDS
-// (lane = output, each wave every third quad) while wave 0 adds the
-// previous chunk's quads onto each output's chain in k order (double
-// buffered).  The quads and their order are the reference's, so the
-// result is too.
+// dA / dB over every token).  A workgroup owns a BMo x BNo block of C (32
+// outputs; BNo the largest power of two <= min(N, 32), so slice indices
+// are shifts) and walks K in chunks of 128.  Each chunk's
+// slices of A (128 x BMo) and B (128 x BNo) are staged through LDS, the next
+// chunk's loads in flight while the current one computes; 256 lanes form
+// the chunk's 32 quads for each of the 32 outputs, then 32 lanes add them
+// onto their output's chain in k order (double-buffered quad store).  The
+// quads and their order are the reference's, so the result is too.
 // ---------------------------------------------------------------------------
-constexpr int kChunkQ = 96;
+constexpr int kLongOut = 32, kChunkK = 128, kChunkQ = kChunkK / 4;
+constexpr int kLongLoads = kChunkK * kLongOut / kThreads;  // 16 per lane, per operand
 
 template <int kLayout, int kBKind>
-__global__ void __launch_bounds__(kThreads) GemmLongKKernel(GemmArgs g) {
-  __shared__ float Q[2][kChunkQ][64];
+__global__ void __launch_bounds__(kThreads) GemmLongKKernel(GemmArgs g, int lb) {
+  __shared__ float As[kChunkK][kLongOut];
+  __shared__ float Bs[kChunkK][kLongOut + 1];
+  __shared__ float Q[2][kChunkQ][kLongOut + 1];
+  const int BNo = 1 << lb, lbm = 5 - lb, BMo = 1 << lbm;  // 32 = 2^5 outputs
   const int tid = threadIdx.x;
-  const size_t total = g.M * g.N;
-  const int oi = tid % 64, wave = tid / 64;
-  const size_t o = static_cast<size_t>(blockIdx.x) * 64 + oi;
-  const bool live = o < total;
-  const size_t m = live ? o / g.N : 0, n = live ? o % g.N : 0;
-  const size_t quads = g.K / 4;
-  const size_t chunks = (quads + kChunkQ - 1) / kChunkQ;
-  auto count = [&](size_t ch) {
-    const size_t q0 = ch * kChunkQ;
-    return static_cast<int>(quads - q0 < static_cast<size_t>(kChunkQ) ? quads - q0 : kChunkQ);
+  const size_t m0 = static_cast<size_t>(blockIdx.y) * BMo, n0 = static_cast<size_t>(blockIdx.x) * BNo;
+  const size_t K = g.K;
+  float ra[kLongLoads], rb[kLongLoads];
+  // Element e of a staged slice: A as (kk, mm), B as (kk, nn).
+  auto a_of = [&](int e, int& kk, int& mm) {
+    if (kLayout == 2) {  // A[K, M]: the slice's rows are short, k outer
+      kk = e >> lbm;
+      mm = e & (BMo - 1);
+    } else {             // A[M, K]: k inner
+      mm = e / kChunkK;
+      kk = e % kChunkK;
+    }
   };
-  float c = (g.accumulate && live) ? g.C[m * g.N + n] : 0.0f;
+  auto load = [&](size_t k0) {
+#pragma unroll
+    for (int r = 0; r < kLongLoads; ++r) {
+      const int e = tid + r * kThreads;
+      float va = 0.0f, vb = 0.0f;
+      if (e < kChunkK * BMo) {
+        int kk, mm;
+        a_of(e, kk, mm);
+        const size_t k = k0 + kk, m = m0 + mm;
+        if (k < K && m < g.M) va = LoadA<kLayout>(g, m, k);
+      }
+      if (e < kChunkK * BNo) {
+        const int kk = e >> lb, nn = e & (BNo - 1);
+        const size_t k = k0 + kk, n = n0 + nn;
+        if (k < K && n < g.N) vb = LoadB<kLayout, kBKind>(g.B, g.N, K, n, k, g.b_col_scale);
+      }
+      ra[r] = va;
+      rb[r] = vb;
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int r = 0; r < kLongLoads; ++r) {
+      const int e = tid + r * kThreads;
+      if (e < kChunkK * BMo) {
+        int kk, mm;
+        a_of(e, kk, mm);
+        As[kk][mm] = ra[r];
+      }
+      if (e < kChunkK * BNo) Bs[e >> lb][e & (BNo - 1)] = rb[r];
+    }
+  };
+  // This lane's quads: output i (mm = i / BNo, nn = i % BNo), quads j, j+8, ...
+  const int i = tid % kLongOut, j0 = tid / kLongOut;
+  const int mm = i >> lb, nn = i & (BNo - 1);
+  const size_t quads = K / 4;
+  const size_t chunks = (quads + kChunkQ - 1) / kChunkQ;
+  const size_t mf = m0 + (tid >> lb), nf = n0 + (tid & (BNo - 1));  // the folding lane's output
+  const bool folds = tid < kLongOut && mf < g.M && nf < g.N;
+  float c = (folds && g.accumulate) ? g.C[mf * g.N + nf] : 0.0f;
+  load(0);
   for (size_t ch = 0; ch <= chunks; ++ch) {
     const int buf = ch & 1;
-    if (wave > 0 && ch < chunks) {
-      const int nq = count(ch);
-      for (int i = wave - 1; i < nq; i += 3) {
-        float q = 0.0f;
-        if (live) {
-          const size_t k = (ch * kChunkQ + i) * 4;
-          float p[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            p[t] = Mul(LoadA<kLayout>(g, m, k + t), LoadB<kLayout, kBKind>(g.B, g.N, g.K, n, k + t, g.b_col_scale));
-          q = Add(Add(Add(p[0], p[1]), p[2]), p[3]);
-        }
-        Q[buf][i][oi] = q;
+    if (ch < chunks) {
+      __syncthreads();  // the previous chunk's As / Bs reads are done
+      store();
+      __syncthreads();
+      if (ch + 1 < chunks) load((ch + 1) * kChunkK);
+      const size_t q0 = ch * kChunkQ;
+      const int nq = static_cast<int>(quads - q0 < static_cast<size_t>(kChunkQ) ? quads - q0 : kChunkQ);
+      for (int j = j0; j < nq; j += kThreads / kLongOut) {
+        const int k = 4 * j;
+        const float p0 = Mul(As[k][mm], Bs[k][nn]), p1 = Mul(As[k + 1][mm], Bs[k + 1][nn]);
+        const float p2 = Mul(As[k + 2][mm], Bs[k + 2][nn]), p3 = Mul(As[k + 3][mm], Bs[k + 3][nn]);
+        Q[buf][j][i] = Add(Add(Add(p0, p1), p2), p3);
       }
     }
-    if (wave == 0 && ch > 0) {
-      const int nq = count(ch - 1);
-      for (int i = 0; i < nq; ++i) c = Add(c, Q[buf ^ 1][i][oi]);
+    if (ch > 0 && folds) {  // the previous chunk, in k order
+      const size_t q0 = (ch - 1) * kChunkQ;
+      const int nq = static_cast<int>(quads - q0 < static_cast<size_t>(kChunkQ) ? quads - q0 : kChunkQ);
+      for (int j = 0; j < nq; ++j) c = Add(c, Q[buf ^ 1][j][tid]);
     }
-    __syncthreads();
   }
-  if (!live || wave != 0) return;
-  for (size_t k = quads * 4; k < g.K; ++k)  // the K % 4 tail
-    c = Add(c, Mul(LoadA<kLayout>(g, m, k), LoadB<kLayout, kBKind>(g.B, g.N, g.K, n, k, g.b_col_scale)));
-  g.C[m * g.N + n] = Epilogue(g, m, n, c);
+  if (!folds) return;
+  for (size_t k = quads * 4; k < K; ++k)  // the K % 4 tail
+    c = Add(c, Mul(LoadA<kLayout>(g, mf, k), LoadB<kLayout, kBKind>(g.B, g.N, K, nf, k, g.b_col_scale)));
+  g.C[mf * g.N + nf] = Epilogue(g, mf, nf, c);
 }
+
+// ---------------------------------------------------------------------------
+// Long reductions with a workspace: the same chains in two passes.  Pass 1
+// forms every quad sum, fully parallel (lane = output, four consecutive
+// quads per lane), into Q[o][j] (output-major); pass 2 gives each output one
+// lane that adds its quads in k order, reading them sixteen bytes at a time.
+// ---------------------------------------------------------------------------
+template <int kLayout, int kBKind>
+__global__ void __launch_bounds__(kThreads) LongKQuadsKernel(GemmArgs g, unsigned quads4) {
+  const unsigned MN = static_cast<unsigned>(g.M * g.N), N = static_cast<unsigned>(g.N);
+  const unsigned o = blockIdx.x * kThreads + threadIdx.x;
+  if (o >= MN) return;
+  const size_t m = o / N, n = o % N, Q = g.K / 4;
+  for (unsigned jq = blockIdx.y; jq < quads4; jq += gridDim.y) {
+    float q[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const size_t j = static_cast<size_t>(jq) * 4 + t;
+      float v = 0.0f;
+      if (j < Q) {
+        const size_t k = j * 4;
+        float p[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          p[u] = Mul(LoadA<kLayout>(g, m, k + u), LoadB<kLayout, kBKind>(g.B, g.N, g.K, n, k + u, g.b_col_scale));
+        v = Add(Add(Add(p[0], p[1]), p[2]), p[3]);
+      }
+      q[t] = v;
+    }
+    *reinterpret_cast<float4*>(g.scratch + static_cast<size_t>(o) * quads4 * 4 + static_cast<size_t>(jq) * 4) =
+        make_float4(q[0], q[1], q[2], q[3]);
+  }
+}
+
+template <int kLayout, int kBKind>
+__global__ void __launch_bounds__(kThreads) LongKFoldKernel(GemmArgs g, unsigned quads4) {
+  const unsigned MN = static_cast<unsigned>(g.M * g.N);
+  const unsigned o = blockIdx.x * kThreads + threadIdx.x;
+  if (o >= MN) return;
+  const size_t m = o / g.N, n = o % g.N, Q = g.K / 4;
+  float c = g.accumulate ? g.C[o] : 0.0f;
+  const float4* qs = reinterpret_cast<const float4*>(g.scratch + static_cast<size_t>(o) * quads4 * 4);
+  const size_t full = Q / 4;
+#pragma unroll 8
+  for (size_t jq = 0; jq < full; ++jq) {
+    const float4 v = qs[jq];
+    c = Add(Add(Add(Add(c, v.x), v.y), v.z), v.w);
+  }
+  for (size_t j = full * 4; j < Q; ++j) c = Add(c, g.scratch[static_cast<size_t>(o) * quads4 * 4 + j]);
+  for (size_t k = Q * 4; k < g.K; ++k)  // the K % 4 tail
+    c = Add(c, Mul(LoadA<kLayout>(g, m, k), LoadB<kLayout, kBKind>(g.B, g.N, g.K, n, k, g.b_col_scale)));
+  g.C[o] = Epilogue(g, m, n, c);
+}
+
+bool LongK(const GemmArgs& a) { return a.layout != 1 && a.M * a.N <= 16384 && a.K >= 1024; }
 
 template <int kLayout, int kBKind>
 hipError_t Run(const GemmArgs& a, hipStream_t s) {
@@ -387,9 +489,23 @@ hipError_t Run(const GemmArgs& a, hipStream_t s) {
     return hipGetLastError();
   }
   if constexpr (kLayout != 1) {
-    if (a.M * a.N <= 16384 && a.K >= 1024) {
-      const dim3 grid(static_cast<unsigned>((a.M * a.N + 63) / 64));
-      hipLaunchKernelGGL((GemmLongKKernel<kLayout, kBKind>), grid, dim3(kThreads), 0, s, a);
+    if (LongK(a) && a.scratch) {
+      const unsigned quads4 = static_cast<unsigned>((a.K / 4 + 3) / 4);
+      const unsigned ob = static_cast<unsigned>((a.M * a.N + kThreads - 1) / kThreads);
+      const dim3 g1(ob, quads4 < 1024 ? quads4 : 1024);
+      hipLaunchKernelGGL((LongKQuadsKernel<kLayout, kBKind>), g1, dim3(kThreads), 0, s, a, quads4);
+      if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+      hipLaunchKernelGGL((LongKFoldKernel<kLayout, kBKind>), dim3(ob), dim3(kThreads), 0, s, a, quads4);
+      return hipGetLastError();
+    }
+    if (LongK(a)) {
+      int lb = 0;
+      while (lb < 5 && (size_t{2} << lb) <= a.N) ++lb;  // BNo = 2^lb <= min(N, 32)
+      const size_t bno = size_t{1} << lb, bmo = kLongOut / bno;
+      const dim3 grid(static_cast<unsigned>((a.N + bno - 1) / bno),
+                      static_cast<unsigned>((a.M + bmo - 1) / bmo));
+      if (grid.y > 65535) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((GemmLongKKernel<kLayout, kBKind>), grid, dim3(kThreads), 0, s, a, lb);
       return hipGetLastError();
     }
   }
@@ -415,6 +531,11 @@ hipError_t LaunchGemmExact(const GemmArgs& a, hipStream_t s) {
     case 6: return Run<2, 0>(a, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+size_t GemmExactScratchBytes(const GemmArgs& a) {
+  if (!LongK(a)) return 0;
+  return a.M * a.N * ((a.K / 4 + 3) / 4) * 4 * sizeof(float);
 }
 
 }  // namespace seeai
