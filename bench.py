@@ -16,7 +16,10 @@ The JSON line also carries:
                 a bounded row sample of the same GEMM;
   extra         the decode-shaped GEMM (M = 32), causal attention fwd+bwd at
                 BASELINE config 3, softmax-xent and AdamW, each with its
-                roofline fraction.
+                roofline fraction; and the LoRA training steps through the
+                plan engine: the MLP (configs[0], us/step and rows/s) and the
+                12-layer decoder (configs[3], tokens/s relaxed and exact, with
+                the step's algorithmic TFLOP/s against the bf16 MFMA peak).
 
 --gpus N with N > 1 exits: this build measures one GPU.
 """
@@ -50,7 +53,34 @@ def parse():
                         "(the counter calibration: a copy's known bytes)")
     p.add_argument("--attn-probe", action="store_true",
                    help="for rocprofv3 runs: BASELINE configs[2] attention fwd+bwd, bf16 x3, f32 x1")
+    p.add_argument("--lora-probe", action="store_true",
+                   help="for rocprofv3 runs: BASELINE configs[3] decoder LoRA plan, one staged "
+                        "step then 5 resident steps (relaxed family)")
     return p.parse_args()
+
+
+def lora_probe():
+    """BASELINE configs[3] through the plan engine for the profilers: build
+    the decoder LoRA plan, one staged step, then five resident steps."""
+    import numpy as np
+    import torch
+    hip = importlib.import_module("see-ai_amd.hip")
+    pw = importlib.import_module("see-ai_amd.planwriter")
+    img = pw.decoder_lora(hip.plan_self_hash, relaxed=True)
+    eng = hip.Engine(img.blob)
+    del img
+    T = 8 * 1024
+    tok = pw.uniform_ints(9, T + 1, 32000)
+    eng.train_step(tok[:T].copy().view(np.float32), tok[1:].copy())
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        loss = eng.train_resident()
+    dt = (time.perf_counter() - t0) / 5
+    eng.close()
+    print(f"lora probe: decoder LoRA (configs[3]) relaxed, 5 resident steps, "
+          f"{dt * 1e3:.1f} ms/step, {T / dt:.0f} tokens/s, loss {loss:.4f}", flush=True)
+    return 0
 
 
 def pmc_probe():
@@ -126,6 +156,8 @@ def main():
         return pmc_probe()
     if args.attn_probe:
         return attn_probe()
+    if args.lora_probe:
+        return lora_probe()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the path shards by GEMM column blocks / attention (b, h) -- see DESIGN.md)",
@@ -313,6 +345,75 @@ def extras(ctx, torch, hip):
     by = 28 * n
     out["adamw_4M"] = {"ms": round(ms, 4), "GB_s": round(by / ms / 1e6, 1),
                        "hbm_frac": round(by / ms / 1e6 / PEAK_HBM_GBS, 4)}
+    del p, gr, m, vv
+    out.update(lora_steps(torch, hip))
+    return out
+
+
+def decoder_step_flops(layers, dim, ffn, vocab, T, batch, seq, heads):
+    """Algorithmic FLOP of one decoder LoRA training step: 2*T*P for the
+    frozen products' forward plus 2*T*P for their dX (P = frozen GEMM
+    parameters; an approximation: the step skips the dX below layer 0's
+    LoRA sites), plus causal-exact attention fwd + bwd (3 x 4*d*pairs per
+    (b, h) and layer).  LoRA products are negligible and not counted."""
+    P = layers * (4 * dim * dim + 2 * dim * ffn) + dim * vocab
+    d = dim // heads
+    pairs = seq * (seq + 1) // 2
+    attn = layers * batch * heads * 3 * 4 * d * pairs
+    return 4.0 * T * P + attn
+
+
+def lora_steps(torch, hip):
+    """The plan engine on BASELINE configs[0] (the LoRA MLP, one 32-row
+    step) and configs[3] (the 12-layer decoder, 8 x 1024 tokens per step),
+    plans from the in-repo plan writer, inputs resident.  The decoder runs
+    the relaxed family as written (bf16 MFMA where the plan marks it) and,
+    with relaxed execution switched off, the exact family."""
+    import numpy as np
+    pw = importlib.import_module("see-ai_amd.planwriter")
+    out = {}
+
+    def steps_per_s(eng, n, warm):
+        for _ in range(warm):
+            eng.train_resident()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            loss = eng.train_resident()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n, loss
+
+    img = pw.mlp_lora(hip.plan_self_hash)
+    eng = hip.Engine(img.blob)
+    eng.train_step(pw.normal(1, (32, 256)), pw.uniform_ints(2, 32, 256))
+    dt, loss = steps_per_s(eng, 200, 10)
+    out["lora_mlp_c1"] = {"us_per_step": round(dt * 1e6, 1), "rows_s": round(32 / dt),
+                          "gemm_flop_per_step": 27394048, "loss": loss,
+                          "bound": "launch latency (25 instructions per step)"}
+    eng.close()
+    del eng, img
+
+    t0 = time.perf_counter()
+    img = pw.decoder_lora(hip.plan_self_hash, relaxed=True)
+    build_s = time.perf_counter() - t0
+    eng = hip.Engine(img.blob)
+    del img
+    T = 8 * 1024
+    tok = pw.uniform_ints(9, T + 1, 32000)
+    eng.train_step(tok[:T].copy().view(np.float32), tok[1:].copy())
+    flops = decoder_step_flops(12, 768, 3072, 32000, T, 8, 1024, 12)
+    for name, allow, n in [("lora_decoder_c4_relaxed", True, 10),
+                           ("lora_decoder_c4_exact", False, 3)]:
+        eng.set_relaxed(allow)
+        dt, loss = steps_per_s(eng, n, 2)
+        tf = flops / dt / 1e12
+        out[name] = {"ms_per_step": round(dt * 1e3, 2), "tokens_s": round(T / dt),
+                     "TFLOP_s": round(tf, 1), "bf16_mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "flop_per_step": flops, "loss": loss, "steps_timed": n,
+                     "config": "12 layers, d768, 12 heads, FFN 3072, vocab 32000, B8 x S1024, "
+                               "LoRA r8 on Q/V",
+                     "plan_build_s": round(build_s, 1)}
+    eng.close()
     return out
 
 

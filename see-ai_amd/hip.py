@@ -260,18 +260,26 @@ def pack_instruction(opcode: int, flags: int = 0, imm: int = 0, ins=(), outs=())
     return struct.pack("<HHI4Q3Q", opcode, flags, imm, *i4, *o3)
 
 
-def plan_self_hash(blob: bytes, hash_offset: int = 216) -> int:
+def _view(blob) -> "np.ndarray":
+    """A uint8 view of any buffer (bytes, bytearray, memoryview) without a
+    copy; its .ctypes.data is the address the C ABI reads."""
+    import numpy as np
+    v = np.frombuffer(blob, np.uint8) if len(blob) else np.zeros(1, np.uint8)
+    return v
+
+
+def plan_self_hash(blob, hash_offset: int = 216) -> int:
     """PlanSelfHash (source/identity/hash.h:136-158) of a plan blob."""
-    buf = C.create_string_buffer(bytes(blob), max(len(blob), 1))
-    return int(_lib.seeai_plan_self_hash(buf, _U64(len(blob)), _U64(hash_offset)))
+    v = _view(blob)
+    return int(_lib.seeai_plan_self_hash(v.ctypes.data, _U64(len(blob)), _U64(hash_offset)))
 
 
 def plan_check(blob: bytes) -> str:
     """The loader's header contract on a blob: '' if readable, else the
     reference's refusal message (runtime/loader/plan_loader.cc:19-49)."""
-    buf = C.create_string_buffer(bytes(blob), max(len(blob), 1))
+    v = _view(blob)
     msg = C.create_string_buffer(512)
-    _lib.seeai_plan_check(buf, _U64(len(blob)), msg, _U64(512))
+    _lib.seeai_plan_check(v.ctypes.data, _U64(len(blob)), msg, _U64(512))
     return msg.value.decode("utf-8", "replace")
 
 
@@ -280,11 +288,10 @@ class Engine:
     UpdateEngine verbs over the gfx950 HipBackend."""
 
     def __init__(self, blob: bytes, device: int = 0):
-        self._blob = bytes(blob)
-        buf = C.create_string_buffer(self._blob, max(len(self._blob), 1))
+        v = _view(blob)
         h = _P()
         msg = C.create_string_buffer(512)
-        rc = _lib.seeai_engine_create(device, buf, _U64(len(self._blob)), C.byref(h), msg,
+        rc = _lib.seeai_engine_create(device, v.ctypes.data, _U64(len(blob)), C.byref(h), msg,
                                       _U64(512))
         if rc != OK:
             raise BackendError(rc, msg.value.decode("utf-8", "replace"))
@@ -361,6 +368,14 @@ class Engine:
 
     def relaxed_executions(self) -> int:
         return int(_lib.seeai_engine_relaxed_executions(self.h))
+
+    def set_relaxed(self, allow: bool):
+        """Whether kFlagRelaxed instructions may run relaxed; with False the
+        whole plan runs the exact family (source/plan/instruction.h:356-384)."""
+        ctx = _lib.seeai_engine_context(self.h)
+        rc = _lib.seeai_set_relaxed(ctx, int(bool(allow)))
+        if rc != OK:
+            raise BackendError(rc, _lib.seeai_last_error(ctx).decode("utf-8", "replace"))
 
     def use_torch_stream(self):
         """Run the engine's kernels on torch's current stream."""

@@ -22,6 +22,7 @@ differently, which changes no instruction's meaning.
 """
 from __future__ import annotations
 
+import os
 import struct
 from dataclasses import dataclass, field
 
@@ -88,28 +89,47 @@ def pack_header(h: dict) -> bytes:
 
 
 # --- deterministic inputs ------------------------------------------------------------------------
-def splitmix64(seed: int, n: int) -> np.ndarray:
-    """n successive SplitMix64 outputs from `seed` (uint64)."""
+def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
+    """SplitMix64 outputs start+1 .. start+n from `seed` (uint64)."""
     with np.errstate(over="ignore"):
-        idx = np.arange(1, n + 1, dtype=np.uint64)
+        idx = np.arange(start + 1, start + n + 1, dtype=np.uint64)
         z = np.uint64(seed) + idx * np.uint64(0x9E3779B97F4A7C15)
         z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
         z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
         return z ^ (z >> np.uint64(31))
 
 
+_PAIRS_PER_CHUNK = 1 << 19
+
+
 def normal(seed: int, shape, std: float = 1.0) -> np.ndarray:
-    """N(0, std^2) f32 by Box-Muller in double over SplitMix64 uniforms."""
+    """N(0, std^2) f32 by Box-Muller in double over SplitMix64 uniforms:
+    pair p takes outputs 2p+1 and 2p+2, giving elements 2p and 2p+1.
+    Large arrays are generated in chunks of pairs on a thread pool (numpy
+    releases the GIL); every element is the same function of its index, so
+    the bytes do not depend on the chunking."""
     n = int(np.prod(shape))
     m = (n + 1) // 2
-    u = splitmix64(seed, 2 * m)
-    u1 = ((u[0::2] >> np.uint64(11)).astype(np.float64) + 1.0) * (1.0 / 9007199254740992.0)
-    u2 = (u[1::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
-    r = np.sqrt(-2.0 * np.log(u1))
-    z = np.empty(2 * m, np.float64)
-    z[0::2] = r * np.cos(2.0 * np.pi * u2)
-    z[1::2] = r * np.sin(2.0 * np.pi * u2)
-    return (z[:n] * std).astype(np.float32).reshape(shape)
+    out = np.empty(2 * m, np.float32)
+
+    def pairs(p0: int, p1: int) -> None:
+        u = splitmix64(seed, 2 * (p1 - p0), start=2 * p0)
+        u1 = ((u[0::2] >> np.uint64(11)).astype(np.float64) + 1.0) * (1.0 / 9007199254740992.0)
+        u2 = (u[1::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+        r = np.sqrt(-2.0 * np.log(u1))
+        z = np.empty(2 * (p1 - p0), np.float64)
+        z[0::2] = r * np.cos(2.0 * np.pi * u2)
+        z[1::2] = r * np.sin(2.0 * np.pi * u2)
+        out[2 * p0:2 * p1] = (z * std).astype(np.float32)
+
+    if m <= _PAIRS_PER_CHUNK:
+        pairs(0, m)
+    else:
+        from concurrent.futures import ThreadPoolExecutor
+        bounds = [(p, min(p + _PAIRS_PER_CHUNK, m)) for p in range(0, m, _PAIRS_PER_CHUNK)]
+        with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
+            list(pool.map(lambda b: pairs(*b), bounds))
+    return out[:n].reshape(shape)
 
 
 def uniform_ints(seed: int, n: int, high: int) -> np.ndarray:
@@ -152,31 +172,34 @@ def assemble(header: dict, train: list, eval_: list, merge: list, emit: list,
              persist_init: bytes, rodata: bytes, self_hash) -> bytes:
     """Lays the sections out after the header and seals the plan.
     `self_hash(blob) -> int` is PlanSelfHash with the hash field zeroed."""
-    out = bytearray(320)
     h = dict(header)
-
-    def section(payload: bytes, align: int = 64) -> int:
-        pad = (-len(out)) % align
-        out.extend(b"\0" * pad)
-        off = len(out)
-        out.extend(payload)
-        return off
-
-    h["train_instr_offset"] = section(b"".join(train))
-    h["train_instr_count"] = len(train)
-    h["eval_instr_offset"] = section(b"".join(eval_))
-    h["eval_instr_count"] = len(eval_)
-    h["merge_instr_offset"] = section(b"".join(merge))
-    h["merge_instr_count"] = len(merge)
-    h["emit_table_offset"] = section(b"".join(struct.pack("<3Q", *e) for e in emit))
+    parts = [(b"".join(train), 64), (b"".join(eval_), 64), (b"".join(merge), 64),
+             (b"".join(struct.pack("<3Q", *e) for e in emit), 64), (persist_init, 64),
+             (rodata, 4096)]
+    offs, end = [], 320
+    for payload, align in parts:
+        end = (end + align - 1) // align * align
+        offs.append(end)
+        end += len(payload)
+    out = bytearray(end)
+    view = memoryview(out)
+    for (payload, _), off in zip(parts, offs):
+        view[off:off + len(payload)] = payload
+    del view
+    names = ["train_instr", "eval_instr", "merge_instr"]
+    for name, off, (payload, _), count in zip(names, offs, parts, (len(train), len(eval_),
+                                                                    len(merge))):
+        h[name + "_offset"] = off
+        h[name + "_count"] = count
+    h["emit_table_offset"] = offs[3]
     h["emit_count"] = len(emit)
-    h["persist_init_offset"] = section(persist_init)
+    h["persist_init_offset"] = offs[4]
     h["persist_init_size"] = len(persist_init)
-    h["rodata_offset"] = section(rodata, align=4096)
+    h["rodata_offset"] = offs[5]
     h["rodata_size"] = len(rodata)
     h["plan_hash"] = 0
     out[0:320] = pack_header(h)
-    h["plan_hash"] = self_hash(bytes(out))
+    h["plan_hash"] = self_hash(out)
     out[0:320] = pack_header(h)
     return bytes(out)
 
