@@ -9,9 +9,10 @@ whole job's throughput in int8 tera-ops per second (2*M*N*K per step).
 
 The JSON line also carries:
   roofline      the dominant kernel (the int8 MFMA GEMM): algorithmic ops
-                per launch / its mean launch time measured here with HIP
-                events on the stream it runs on, against MI355X's dense int8
-                peak (5.0 POP/s); traffic from profiles/ when measured;
+                per launch / its mean duration measured here with HIP events
+                around back-to-back launches on the stream it runs on,
+                against MI355X's dense int8 peak (5.0 POP/s); traffic from
+                profiles/ when measured;
   cpu_baseline  the oracle's W8A8 (scalar C, 1 thread) timed on this host on
                 a bounded row sample of the same GEMM;
   extra         the decode-shaped GEMM (M = 32), causal attention fwd+bwd at
@@ -53,10 +54,34 @@ def parse():
                         "(the counter calibration: a copy's known bytes)")
     p.add_argument("--attn-probe", action="store_true",
                    help="for rocprofv3 runs: BASELINE configs[2] attention fwd+bwd, bf16 x3, f32 x1")
+    p.add_argument("--mfma-ceiling", action="store_true",
+                   help="the int8 MFMA issue rate with register-resident operands (constant, "
+                        "random, small random levels) at 1, 2 and 4 waves per SIMD")
     p.add_argument("--lora-probe", action="store_true",
                    help="for rocprofv3 runs: BASELINE configs[3] decoder LoRA plan, one staged "
                         "step then 5 resident steps (relaxed family)")
     return p.parse_args()
+
+
+def mfma_ceiling():
+    """The int8 MFMA rate with nothing but MFMAs issuing, operands held in
+    registers (see-ai_amd/probe/mfma_ceiling.hip): how far data-dependent
+    power management keeps gfx950 from its 5.0 POP/s datasheet peak."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "see-ai_amd", "libseeai_probe.so"))
+    lib.seeai_probe_mfma_i8.restype = ctypes.c_float
+    lib.seeai_probe_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    out = torch.empty(1024 * 256, dtype=torch.int32, device="cuda")
+    iters = 10000
+    res = {}
+    for mode, name in [(0, "constant"), (1, "uniform_random"), (2, "random_abs_le_31")]:
+        for wgs in (256, 512, 1024):
+            ms = lib.seeai_probe_mfma_i8(wgs, iters, mode, out.data_ptr())
+            ops = 2.0 * 32 * 32 * 32 * 8 * iters * wgs * 4
+            res[f"{name}_{wgs // 256}wave_per_simd"] = round(ops / ms / 1e9, 1)
+    print(json.dumps({"mfma_i8_ceiling_TOPS": res, "peak_TOPS": PEAK_INT8_TOPS}), flush=True)
+    return 0
 
 
 def lora_probe():
@@ -158,6 +183,8 @@ def main():
         return attn_probe()
     if args.lora_probe:
         return lora_probe()
+    if args.mfma_ceiling:
+        return mfma_ceiling()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the path shards by GEMM column blocks / attention (b, h) -- see DESIGN.md)",
@@ -194,18 +221,22 @@ def main():
         quantize()
         gemm()
     torch.cuda.synchronize()
-    # Per-step events around the GEMM launch (same stream: torch's current).
-    g_start = [ev() for _ in range(args.steps)]
-    g_end = [ev() for _ in range(args.steps)]
     t0 = time.perf_counter()
     for i in range(args.steps):
         quantize()
-        g_start[i].record()
         gemm()
-        g_end[i].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    gemm_ms = sum(a.elapsed_time(b) for a, b in zip(g_start, g_end)) / args.steps
+    # The GEMM kernel's mean duration: HIP events (on torch's current stream,
+    # the one the library launches on) around the same number of GEMM-only
+    # launches back to back.
+    g_start, g_end = ev(), ev()
+    g_start.record()
+    for i in range(args.steps):
+        gemm()
+    g_end.record()
+    torch.cuda.synchronize()
+    gemm_ms = g_start.elapsed_time(g_end) / args.steps
     ms_per_step = wall * 1000.0 / args.steps
     ops = 2.0 * M * N * K
     value = ops / (ms_per_step * 1e-3) / 1e12
@@ -227,7 +258,7 @@ def main():
         "config": {"workload": "W8A8 GEMM M=4096 K=4096 N=4096 (BASELINE configs[1])",
                    "M": M, "N": N, "K": K, "parallelism": "single GPU"},
         "roofline": {
-            "kernel": "GemmI8TileKernel<256,256,128,4,4>",
+            "kernel": "GemmI8DmaKernel<4,2,4>",
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": PEAK_INT8_TOPS,

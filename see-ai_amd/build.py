@@ -29,6 +29,7 @@ HOST = os.path.join(HERE, "host")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libseeai_hip.so")
+PROBE_LIB = os.path.join(HERE, "libseeai_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -86,6 +87,14 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-6000:]}")
     os.replace(tmp, LIB)
+    # The measurement probe (bench.py --mfma-ceiling): its own library.
+    probe_src = os.path.join(HERE, "probe", "mfma_ceiling.hip")
+    probe_tmp = PROBE_LIB + ".tmp"
+    r = subprocess.run([HIPCC, *COMMON, "-shared", "-o", probe_tmp, probe_src],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on mfma_ceiling.hip:\n{r.stderr[-6000:]}")
+    os.replace(probe_tmp, PROBE_LIB)
     if verbose:
         print(f"built {LIB}")
     return LIB
@@ -93,8 +102,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
 
 def clean() -> None:
     shutil.rmtree(BUILD, ignore_errors=True)
-    if os.path.exists(LIB):
-        os.remove(LIB)
+    for lib in (LIB, PROBE_LIB):
+        if os.path.exists(lib):
+            os.remove(lib)
 
 
 if __name__ == "__main__":

@@ -20,6 +20,9 @@ typedef short v8s __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
 
+// A wave-uniform value held in a vector register, as a scalar.
+__device__ __forceinline__ int Uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 // The fused-epilogue activations (instruction.h:384-396, the expressions of
 // kernel_policy.h:122-136).  Built with -ffp-contract=off, so every product
 // and sum rounds where the reference's x86-64 build rounds it.

@@ -38,9 +38,6 @@ constexpr int kRsrcWord3 = 0x00020000;
 
 __device__ __forceinline__ float Exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// A wave-uniform value held in a vector register, as a scalar.
-__device__ __forceinline__ int Uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
 __device__ __forceinline__ v16f Mfma(const bf16x8& a, const bf16x8& b, const v16f& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }

@@ -14,15 +14,13 @@
 // QWt [N, K] (K contiguous: both MFMA operands then read 16 contiguous
 // bytes per lane).
 //
-// Large M: a 256 x 256 tile per 1024-lane workgroup, sixteen waves in 4 x 4,
-// each a 64 x 64 block of v_mfma_i32_32x32x32_i8 tiles (4 accumulators of
-// 16 int32; four waves per SIMD hide each other's LDS and memory latency --
-// measured faster than 8 waves of 128 x 64 and than 4 waves of 128 x 128,
-// which spills); K walks 128 bytes per step through two
-// padded LDS buffers (a 16-byte pad per row spreads a wave's 16-byte reads
-// over the banks), the next step's global loads in flight during the
-// current step's MFMAs; workgroups are ordered so each XCD's L2 serves a
-// compact block of tiles.
+// Large M (M, N >= 2048, K a multiple of 64): GemmI8DmaKernel, a 256 x 256
+// tile per workgroup of eight waves (two per SIMD, blocks of 128 x 64 on
+// v_mfma_i32_32x32x32_i8), K staged 64 bytes at a time through four LDS
+// buffers filled by direct-to-LDS buffer loads, three stages in flight;
+// workgroups are ordered so each XCD's L2 serves a compact block of tiles.
+// Other large shapes: GemmI8TileKernel (sixteen waves of 64 x 64, loads
+// staged through registers into two padded LDS buffers).
 // Small M (decode-like, M <= 64): one 16-column slice of C per workgroup,
 // its four waves each reducing a quarter of K on v_mfma_i32_16x16x64_i8
 // straight from global memory (each weight byte is read once), then summed
@@ -341,6 +339,261 @@ GemmI8TileKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
   }
 }
 
+// --- the large-M GEMM, staged by direct-to-LDS loads -----------------------------
+//
+// 256 x 256 tile per workgroup of WGM x WGN waves, each a (256/WGM) x
+// (256/WGN) block of v_mfma_i32_32x32x32_i8 accumulators.  The launcher runs
+// eight waves (two per SIMD, 2 x 4, blocks of 128 x 64: 128 int32
+// accumulators per lane), measured 6-7 % faster than four waves of 128 x 128
+// (one per SIMD, 256 accumulators) at 4096^3 and 8192^3: the second wave on
+// each SIMD issues MFMAs while the first waits on LDS or the barrier.  K moves 64 bytes per stage through kStages LDS buffers (32 KiB
+// each: 256 A rows + 256 W rows of 64 bytes) filled by buffer_load ... lds,
+// which writes a wave's 64 x 16 bytes to consecutive LDS addresses from M0
+// without passing through registers; kStages - 1 stages are in flight while
+// one is multiplied.  One barrier per stage: every wave's loads of the
+// stage it is about to read have landed (vmcnt), and every wave has
+// finished reading the buffer the next load overwrites.
+//
+// LDS rows are 64 bytes, four 16-byte chunks; chunk c of row r sits at
+// physical chunk (c + r/4) mod 4.  The fragment reads (lane l: row l % 32,
+// chunk 2ks + l / 32) are then free of bank conflicts -- measured with
+// SQ_LDS_BANK_CONFLICT on gfx950 for ds_read_b128, which also counts
+// conflicts for rotations that bring in r/8 or r/16.  Loads pick the global
+// chunk that belongs at each physical slot.  Rows past M (or N) read as zeros (buffer
+// range check); K must be a multiple of 64.
+constexpr int kDmaBK = 64;
+constexpr int kDmaChunks = kDmaBK / 16;
+
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+__device__ __forceinline__ int DmaPhys(int row, int c) { return (c + row / 4) & 3; }
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int n>
+__device__ __forceinline__ void WaitVm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+template <int kStages, int WGM, int WGN>
+__global__ void __launch_bounds__(WGM * WGN * kWave)
+GemmI8DmaKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
+                const int8_t* __restrict__ QW, const float* __restrict__ sw,
+                float* __restrict__ C, int32_t* __restrict__ acc_out, int M, int N, int K) {
+  constexpr int BM = 256, BN = 256;
+  constexpr int kWaves = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;       // per-wave block
+  constexpr int TM = WM / 32, TN = WN / 32;         // 32 x 32 accumulators per wave
+  constexpr int kRowsPerLoad = kWave / kDmaChunks;  // rows one wave-load fills (16)
+  constexpr int kLoads = BM / kRowsPerLoad / kWaves;  // wave-loads per operand, stage, wave
+  static_assert(kLoads * kRowsPerLoad * kWaves == BM, "loads cover the tile");
+  constexpr int kStageA = BM * kDmaBK;               // bytes
+  constexpr int kStage = (BM + BN) * kDmaBK;
+  constexpr int kPerStage = 2 * kLoads;              // vmcnt units per stage
+  __shared__ __attribute__((aligned(1024))) int8_t smem[kStages * kStage];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  int tm, tn;
+  TileOf(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  // Operand ranges start at this tile's first row: offsets stay below
+  // 256 * K, and rows past the operand's end fall outside num_records.
+  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(QA) + static_cast<size_t>(m0) * K, 0,
+      Uniform((M - m0) * K), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(QW) + static_cast<size_t>(n0) * K, 0,
+      Uniform((N - n0) * K), 0x00020000);
+  // This lane's slot in each wave-load: row rbase + lane / 4, physical chunk
+  // lane % 4, which holds logical chunk (p - r/4) mod 4.
+  // (Fixed capacity: an array sized by a template-dependent constant and
+  // captured by the lambdas below loses the kernel's host-side stub.)
+  static_assert(kLoads <= 4, "voff capacity");
+  int voff[4];
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j) {
+    const int row = (j * kWaves + wave) * kRowsPerLoad + lane / kDmaChunks;
+    const int c = (lane % kDmaChunks - row / 4) & 3;
+    voff[j] = row * K + c * 16;
+  }
+  auto issue = [&](int st, int buf) {
+    int8_t* sA = smem + buf * kStage;
+    int8_t* sB = sA + kStageA;
+    const int k0 = st * kDmaBK;
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      const int rbase = Uniform((j * kWaves + wave) * kRowsPerLoad);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (LdsPtr)(sA + rbase * kDmaBK), 16, voff[j],
+                                               k0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, (LdsPtr)(sB + rbase * kDmaBK), 16, voff[j],
+                                               k0, 0, 0);
+    }
+  };
+
+  v16i acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
+  const int lr = lane % 32, h = lane / 32;
+  // Fragment offsets within a buffer for k-steps 0 and 1 (logical chunks h
+  // and 2 + h of row lr; the tile rows wm + 32 i add multiples of 32 rows,
+  // which leave the swizzle unchanged).
+  const int frag0 = lr * kDmaBK + DmaPhys(lr, h) * 16;
+  const int frag1 = lr * kDmaBK + DmaPhys(lr, 2 + h) * 16;
+
+  // Software pipeline, one k-step (32 bytes of K) ahead in registers: while
+  // the MFMAs of one k-step issue, the fragments of the next are read from
+  // LDS (interleaved two MFMAs per read).  The barrier sits between a
+  // stage's two k-steps: after it, stage it + 1 has landed, and every wave
+  // has consumed its reads of stage it - 1 (their MFMAs were issued before
+  // the barrier), whose buffer then takes the loads of stage
+  // it + kStages - 1.
+  const int nsteps = K / kDmaBK;
+  v4i fa[2][TM], fb[2][TN];
+  auto read = [&](int buf, int fo, int slot) {
+    const int8_t* sA = smem + buf * kStage;
+    const int8_t* sB = sA + kStageA;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      fa[slot][i] = *reinterpret_cast<const v4i*>(sA + (wm + i * 32) * kDmaBK + fo);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      fb[slot][j] = *reinterpret_cast<const v4i*>(sB + (wn + j * 32) * kDmaBK + fo);
+  };
+  auto mfmas = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[slot][i], fb[slot][j], acc[i][j],
+                                                          0, 0, 0);
+  };
+  // The next k-step's TM + TN LDS reads spread one per MFMA from the start
+  // of a k-step's TM x TN MFMAs; after the barrier, the stage's loads take
+  // the following MFMA slots.
+  auto interleave = [&]() {
+#pragma unroll
+    for (int g = 0; g < TM + TN; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int g = TM + TN; g < TM * TN; ++g) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  };
+  auto interleave_loads = [&]() {
+#pragma unroll
+    for (int g = 0; g < TM * TN; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (g < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (g >= TM * TN - 2 * kLoads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+  };
+  static_assert(TM * TN >= TM + TN && TM * TN >= 2 * kLoads, "MFMA slots for the reads and loads");
+
+  // Every iteration loads one stage: past the last stage the loads repeat
+  // it (in bounds, into a buffer no later stage uses), so the number of
+  // stages in flight at each barrier is always kStages - 3.
+  const int last = nsteps - 1;
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s) issue(min(s, last), s);
+  WaitVm<(kStages - 2) * kPerStage>();
+  __builtin_amdgcn_s_barrier();
+  read(0, frag0, 0);
+  for (int it = 0; it < last; ++it) {
+    const int buf = it % kStages;
+    read(buf, frag1, 1);
+    mfmas(0);
+    interleave();
+    WaitVm<(kStages - 3) * kPerStage>();
+    __builtin_amdgcn_s_barrier();
+    issue(min(it + kStages - 1, last), (it + kStages - 1) % kStages);
+    read((it + 1) % kStages, frag0, 0);
+    mfmas(1);
+    interleave_loads();
+  }
+  read(last % kStages, frag1, 1);
+  mfmas(0);
+  interleave();
+  mfmas(1);
+  WaitVm<0>();  // the repeated loads have landed before LDS is reused
+  __syncthreads();  // every wave is done with the stage buffers: reuse them for staging
+
+  if (acc_out) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+          const int n = n0 + wn + j * 32 + lr;
+          if (m < M && n < N) acc_out[static_cast<size_t>(m) * N + n] = acc[i][j][r];
+        }
+  }
+  // Dequant epilogue through this wave's 32 x WN slice of LDS, 32 rows at a
+  // time, so C leaves in row-contiguous 16-byte stores.
+  constexpr int SLD = WN + 4;
+  static_assert(kWaves * 32 * SLD * 4 <= kStages * kStage, "staging fits in LDS");
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
+  const bool vec_out = (N % 4) == 0;
+  float swv[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn + j * 32 + lr;
+    swv[j] = n < N ? sw[n] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int mb = m0 + wm + i * 32;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m4 = mb + 8 * q + 4 * h;
+      float sav[4];
+      if (m4 + 3 < M && (M % 4) == 0) {
+        const float4 v = *reinterpret_cast<const float4*>(sa + m4);
+        sav[0] = v.x, sav[1] = v.y, sav[2] = v.z, sav[3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sav[e] = m4 + e < M ? sa[m4 + e] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          stage[(8 * q + 4 * h + e) * SLD + j * 32 + lr] =
+              (static_cast<float>(acc[i][j][4 * q + e]) * sav[e]) * swv[j];
+    }
+    __builtin_amdgcn_wave_barrier();
+    constexpr int kVecRow = WN / 4;  // float4 per staged row
+#pragma unroll
+    for (int t = 0; t < 32 * kVecRow / kWave; ++t) {
+      const int idx = lane + t * kWave;
+      const int row = idx / kVecRow, c4 = idx % kVecRow;
+      const int m = mb + row, n = n0 + wn + c4 * 4;
+      const float4 v = *reinterpret_cast<const float4*>(stage + row * SLD + c4 * 4);
+      if (m >= M) continue;
+      float* dst = C + static_cast<size_t>(m) * N + n;
+      if (vec_out && n + 3 < N) {
+        *reinterpret_cast<float4*>(dst) = v;
+      } else {
+        if (n < N) dst[0] = v.x;
+        if (n + 1 < N) dst[1] = v.y;
+        if (n + 2 < N) dst[2] = v.z;
+        if (n + 3 < N) dst[3] = v.w;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // --- the small-M GEMM (decode-like) ---------------------------------------------
 
 template <int MT>  // 16-row MFMA tiles covering M <= 16 * MT
@@ -459,8 +712,12 @@ hipError_t LaunchGemmW8A8(const int8_t* QA, const float* sa, const int8_t* QWt, 
       const char* e = std::getenv("SEEAI_I8_TILE");
       return e ? std::atoi(e) : 0;
     }();
-    const bool big = forced ? forced == 256 : (M >= 2048 && N >= 2048);
-    if (big) {
+    const bool big = forced ? forced >= 256 : (M >= 2048 && N >= 2048);
+    if (big && K >= kDmaBK && K % kDmaBK == 0 && K * 256 < (1ull << 31) && forced != 257) {
+      const unsigned tiles = static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256));
+      hipLaunchKernelGGL((GemmI8DmaKernel<4, 2, 4>), dim3(tiles), dim3(512), 0, s, QA, sa, QWt, sw, C,
+                         acc, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+    } else if (big) {
       const unsigned tiles = static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256));
       hipLaunchKernelGGL((GemmI8TileKernel<256, 256, 128, 4, 4>), dim3(tiles), dim3(1024), 0, s, QA,
                          sa, QWt, sw, C, acc, static_cast<int>(M), static_cast<int>(N),

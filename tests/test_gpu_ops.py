@@ -455,7 +455,8 @@ def test_attention_cached_family(hip, orc, backend, B, S, H, d):
 # --- W8A8 and argmax through the op-family entry points --------------------------------------
 
 @pytest.mark.parametrize("M,N,K", [(5, 9, 7), (67, 129, 48), (32, 4096, 1024), (48, 200, 512),
-                                   (256, 512, 1024), (300, 260, 272), (2048, 2304, 512)])
+                                   (256, 512, 1024), (300, 260, 272), (2048, 2304, 512),
+                                   (2100, 2200, 320), (2048, 2048, 64), (2304, 2048, 128)])
 def test_w8a8_bit_exact(hip, orc, torch_cuda, M, N, K):
     torch = torch_cuda
     r = rng(M + N + K)
