@@ -138,6 +138,25 @@ def pmc_probe():
     return 0
 
 
+def attention_step(ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d, parts=None):
+    """One causal attention fwd + bwd as a plan runs it: forward, dQ, then
+    dK and dV -- one fused pass in the relaxed family (an adjacent dK / dV
+    pair fuses in a range), two passes in the exact family.  `parts` picks a
+    subset ("fwd", "dq", "dkdv") for per-kernel timing."""
+    P = lambda t: t.data_ptr()
+    parts = parts or ("fwd", "dq", "dkdv")
+    if "fwd" in parts:
+        ctx.call("seeai_attn_fwd", dt, P(q), P(k), P(v), P(o), P(st), B, S, H, d, None)
+    if "dq" in parts:
+        ctx.call("seeai_attn_dq", dt, P(q), P(k), P(v), P(do), P(st), P(dq), B, S, H, d)
+    if "dkdv" in parts:
+        if dt:
+            ctx.call("seeai_attn_dkdv", P(q), P(k), P(v), P(do), P(st), P(dk), P(dv), B, S, H, d)
+        else:
+            ctx.call("seeai_attn_dk", dt, P(q), P(k), P(v), P(do), P(st), P(dk), B, S, H, d)
+            ctx.call("seeai_attn_dv", dt, P(q), P(k), P(do), P(st), P(dv), B, S, H, d)
+
+
 def attn_probe():
     """BASELINE configs[2] once per family for the profilers: causal
     attention fwd + dQ + dK + dV at B16 H16 S2048 d64, relaxed (bf16) three
@@ -153,14 +172,7 @@ def attn_probe():
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
     for dt, reps in [(1, 3), (0, 1)]:
         for _ in range(reps):
-            ctx.call("seeai_attn_fwd", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                     st.data_ptr(), B, S, H, d, None)
-            ctx.call("seeai_attn_dq", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                     st.data_ptr(), dq.data_ptr(), B, S, H, d)
-            ctx.call("seeai_attn_dk", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                     st.data_ptr(), dk.data_ptr(), B, S, H, d)
-            ctx.call("seeai_attn_dv", dt, q.data_ptr(), k.data_ptr(), do.data_ptr(), st.data_ptr(),
-                     dv.data_ptr(), B, S, H, d)
+            attention_step(ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d)
     torch.cuda.synchronize()
     ctx.close()
     print("attention probe: B16 H16 S2048 d64 causal, 3 x bf16 fwd+bwd, 1 x f32 fwd+bwd", flush=True)
@@ -336,20 +348,16 @@ def extras(ctx, torch, hip):
     o, st = torch.empty_like(q), torch.empty((B * H * S, 4), device="cuda")
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
     for dt, name in [(1, "attention_bf16"), (0, "attention_f32")]:
-        def step(dt=dt):
-            ctx.call("seeai_attn_fwd", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                     st.data_ptr(), B, S, H, d, None)
-            ctx.call("seeai_attn_dq", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                     st.data_ptr(), dq.data_ptr(), B, S, H, d)
-            ctx.call("seeai_attn_dk", dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                     st.data_ptr(), dk.data_ptr(), B, S, H, d)
-            ctx.call("seeai_attn_dv", dt, q.data_ptr(), k.data_ptr(), do.data_ptr(), st.data_ptr(),
-                     dv.data_ptr(), B, S, H, d)
-        ms = timed(step, 3, 1)
+        args_ = (ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d)
+        ms = timed(lambda: attention_step(*args_), 3 if dt else 1, 1)
         tf = flops / ms / 1e9
         peak = PEAK_BF16_TFLOPS if dt else PEAK_FP32_TFLOPS
         out[name] = {"ms_fwd_bwd": round(ms, 3), "TFLOP_s": round(tf, 1),
                      "mfma_frac": round(tf / peak, 4), "config": "B16 H16 S2048 d64 causal"}
+        if dt:
+            out[name]["ms_parts"] = {
+                part: round(timed(lambda part=part: attention_step(*args_, parts=(part,)), 5, 1), 4)
+                for part in ("fwd", "dq", "dkdv")}
     del q, k, v, do, o, st, dq, dk, dv
 
     # Softmax cross-entropy fwd at the decoders' 8192 x 32000 logits.

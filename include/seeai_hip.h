@@ -95,6 +95,20 @@ int seeai_execute(seeai_ctx* ctx, const void* instruction,
 int seeai_execute_range(seeai_ctx* ctx, const void* instructions,
                         uint64_t count, const seeai_step_params* params,
                         uint64_t* failed_at);
+/* ExecutorBackend::BeginRange / EndRange (backend.h:139-142): the whole
+ * program of the range about to run, `count` 64-byte words of which
+ * [begin, end) execute.  The caller keeps `program` alive until
+ * seeai_end_range and passes seeai_execute pointers into it; two adjacent
+ * instructions may then run as one dispatch (relaxed kAttnDKTiled +
+ * kAttnDVTiled of one attention), the second returning at once.  Without a
+ * range every instruction runs alone. */
+int seeai_begin_range(seeai_ctx* ctx, const void* program, uint64_t count,
+                      uint64_t begin, uint64_t end);
+int seeai_end_range(seeai_ctx* ctx);
+/* Whether adjacent instructions may fuse (default 1), and how many fused
+ * dispatches ran (ExecutorBackend::fused_dispatches, backend.h:165). */
+int seeai_set_fusion(seeai_ctx* ctx, int allow);
+uint64_t seeai_fused_dispatches(const seeai_ctx* ctx);
 /* Waits for the stream; reports a refusal raised on the device since the
  * last flush (non-finite clip norm: nothing it guarded was written). */
 int seeai_flush(seeai_ctx* ctx);
@@ -153,6 +167,13 @@ int seeai_attn_dv(seeai_ctx* ctx, int dtype, const float* d_q,
                   const float* d_k, const float* d_dout, const float* d_stats,
                   float* d_dv, uint64_t B, uint64_t S, uint64_t H,
                   uint64_t d);
+/* AttnDKTiled + AttnDVTiled (attention.cc:537-590) in one relaxed pass
+ * (bf16 MFMA): what a fused pair of the two instructions runs.  d = 64,
+ * 16-byte aligned operands; status 2 otherwise. */
+int seeai_attn_dkdv(seeai_ctx* ctx, const float* d_q, const float* d_k,
+                    const float* d_v, const float* d_dout,
+                    const float* d_stats, float* d_dk, float* d_dv,
+                    uint64_t B, uint64_t S, uint64_t H, uint64_t d);
 
 /* SoftmaxXEntFwd / Bwd and the masked pair (loss.cc:35-126). */
 int seeai_xent_fwd(seeai_ctx* ctx, const float* d_logits,

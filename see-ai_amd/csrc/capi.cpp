@@ -82,6 +82,13 @@ struct seeai_ctx {
   size_t scratch_bytes = 0;
   int allow_relaxed = 1;
   uint64_t relaxed = 0;
+  // The program of the range being executed (seeai_begin_range, the seam's
+  // BeginRange): lets two adjacent instructions run as one dispatch.
+  const uint8_t* prog = nullptr;
+  uint64_t prog_count = 0, range_end = 0;
+  const uint8_t* done = nullptr;  // the next instruction, already run by a fused dispatch
+  int allow_fusion = 1;
+  uint64_t fused = 0;
   std::string err;
 
   int* flag() { return reinterpret_cast<int*>(small); }
@@ -178,6 +185,61 @@ int Relaxed(seeai_ctx* c, const Instruction& ins) {
   const int r = (ins.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
   c->relaxed += r;
   return r;
+}
+
+bool Overlap(const uint8_t* a, uint64_t na, const uint8_t* b, uint64_t nb) {
+  return a < b + nb && b < a + na;
+}
+
+// Range-level fusion of the attention backward (the seam's whole-program
+// visibility, backend.h:139-142; the reference's Metal backend fuses the
+// low-rank pair the same way, metal_backend.mm:1155-1340).  kAttnDKTiled and
+// kAttnDVTiled of one attention -- adjacent in the range, same q, k, dO,
+// stats and geometry, both relaxed -- run as one pass that forms S, P and dP
+// once for both accumulations; the second instruction is then skipped at its
+// own place.  Each output keeps its one writer and the products and their
+// order of the separate kernels, so the arena holds the same bytes.  Refused
+// (the two run apart) when either output overlaps the other or anything the
+// pass reads: the separate order may legally reuse a buffer the first
+// instruction alone still reads.  Returns -1 when the pair does not fuse.
+int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
+  if (!c->allow_fusion || !c->allow_relaxed || !c->prog || at < c->prog ||
+      at >= c->prog + c->prog_count * 64 || (at - c->prog) % 64 != 0)
+    return -1;
+  const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
+  if (idx + 1 >= c->range_end) return -1;
+  Instruction nx;
+  std::memcpy(&nx, at + 64, sizeof nx);
+  if (ins.opcode + nx.opcode != 49 + 50 || (ins.opcode != 49 && ins.opcode != 50)) return -1;
+  if (!(ins.flags & kFlagRelaxed) || !(nx.flags & kFlagRelaxed)) return -1;
+  if (ins.in[0] != nx.in[0] || ins.in[1] != nx.in[1] || ins.in[3] != nx.in[3] ||
+      ins.out[0] != nx.out[0] || ins.out[2] != nx.out[2])
+    return -1;
+  const Instruction& dki = ins.opcode == 49 ? ins : nx;
+  const Instruction& dvi = ins.opcode == 49 ? nx : ins;
+  const uint64_t g = ins.out[2];
+  const uint64_t B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
+  const Ptrs R{c};
+  const float *q = R.f(dki.in[0]), *k = R.f(dki.in[1]), *v = R.f(dki.in[2]), *dout = R.f(dki.in[3]);
+  const float* stats = R.f(dki.out[0]);
+  float *dk = R.f(dki.out[1]), *dv = R.f(dvi.out[1]);
+  if (!AttnDKDVFusable(q, k, v, dout, dk, dv, B, S, H, d)) return -1;
+  const uint64_t act = B * S * H * d * 4, st = B * H * S * 16;
+  const auto* o1 = reinterpret_cast<const uint8_t*>(dk);
+  const auto* o2 = reinterpret_cast<const uint8_t*>(dv);
+  if (Overlap(o1, act, o2, act)) return -1;
+  for (const float* in : {q, k, v, dout})
+    for (const uint8_t* o : {o1, o2})
+      if (Overlap(o, act, reinterpret_cast<const uint8_t*>(in), act)) return -1;
+  for (const uint8_t* o : {o1, o2})
+    if (Overlap(o, act, reinterpret_cast<const uint8_t*>(stats), st)) return -1;
+  Relaxed(c, ins);
+  Relaxed(c, nx);
+  SEEAI_TRY(c, LaunchAttnDKDVFused(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
+            "attn.dkdv_fused");
+  c->done = at + 64;
+  ++c->fused;
+  return SEEAI_OK;
 }
 
 int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P) {
@@ -659,23 +721,70 @@ uint64_t seeai_arena_bytes(const seeai_ctx* c) { return c ? c->arena_bytes : 0; 
 
 int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params* params) {
   if (!c || !instruction) return SEEAI_INVALID;
+  const auto* at = static_cast<const uint8_t*>(instruction);
+  const uint8_t* done = c->done;
+  c->done = nullptr;
+  if (at == done) return SEEAI_OK;  // ran with the previous instruction
   Instruction ins;
   std::memcpy(&ins, instruction, sizeof ins);
+  if (!c->arena) return Fail(c, SEEAI_INVALID, "execute: no arena is bound");
+  if (int rc = TryFuseAttnBwd(c, ins, at); rc >= 0) return rc;
   seeai_step_params P{};
   if (params) P = *params;
   return ExecuteOne(c, ins, P);
 }
 
+int seeai_begin_range(seeai_ctx* c, const void* program, uint64_t count, uint64_t begin,
+                      uint64_t end) {
+  if (!c || (!program && count) || begin > end || end > count) return SEEAI_INVALID;
+  c->prog = static_cast<const uint8_t*>(program);
+  c->prog_count = count;
+  c->range_end = end;
+  c->done = nullptr;
+  return SEEAI_OK;
+}
+
+int seeai_end_range(seeai_ctx* c) {
+  if (!c) return SEEAI_INVALID;
+  c->prog = nullptr;
+  c->prog_count = c->range_end = 0;
+  c->done = nullptr;
+  return SEEAI_OK;
+}
+
+int seeai_set_fusion(seeai_ctx* c, int allow) {
+  if (!c) return SEEAI_INVALID;
+  c->allow_fusion = allow ? 1 : 0;
+  return SEEAI_OK;
+}
+
+uint64_t seeai_fused_dispatches(const seeai_ctx* c) { return c ? c->fused : 0; }
+
 int seeai_execute_range(seeai_ctx* c, const void* instructions, uint64_t count,
                         const seeai_step_params* params, uint64_t* failed_at) {
   if (!c || (!instructions && count)) return SEEAI_INVALID;
   const auto* base = static_cast<const uint8_t*>(instructions);
+  seeai_begin_range(c, instructions, count, 0, count);
   for (uint64_t i = 0; i < count; ++i) {
     if (int rc = seeai_execute(c, base + i * 64, params)) {
       if (failed_at) *failed_at = i;
+      seeai_end_range(c);
       return rc;
     }
   }
+  seeai_end_range(c);
+  return SEEAI_OK;
+}
+
+int seeai_attn_dkdv(seeai_ctx* c, const float* q, const float* k, const float* v,
+                    const float* dout, const float* stats, float* dk, float* dv, uint64_t B,
+                    uint64_t S, uint64_t H, uint64_t d) {
+  if (!c) return SEEAI_INVALID;
+  if (!AttnDKDVFusable(q, k, v, dout, dk, dv, B, S, H, d))
+    return Fail(c, SEEAI_INVALID, "attn_dkdv: the fused pass takes d = 64 with 16-byte aligned "
+                                  "operands and slices under 2 GiB");
+  SEEAI_TRY(c, LaunchAttnDKDVFused(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
+            "attn_dkdv");
   return SEEAI_OK;
 }
 

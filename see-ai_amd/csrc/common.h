@@ -245,9 +245,19 @@ hipError_t LaunchAttnDKTiled(int dtype, const float* q, const float* k, const fl
 hipError_t LaunchAttnDVTiled(int dtype, const float* q, const float* k, const float* dout,
                              const float* stats, float* dv, size_t B, size_t S, size_t H,
                              size_t d, hipStream_t s);
-// Relaxed tiled attention on bf16 MFMA (k_flash.hip), d in {64, 128}; dk or
-// exactly one of dk, dv is non-null in LaunchFlashDKDV.
+// dK and dV in one pass (relaxed family; k_attention.hip).  Fusable says
+// whether the fused launch takes the shape; otherwise it returns
+// hipErrorNotSupported and launches nothing.
+bool AttnDKDVFusable(const float* q, const float* k, const float* v, const float* dout,
+                     const float* dk, const float* dv, size_t B, size_t S, size_t H, size_t d);
+hipError_t LaunchAttnDKDVFused(const float* q, const float* k, const float* v, const float* dout,
+                               const float* stats, float* dk, float* dv, size_t B, size_t S,
+                               size_t H, size_t d, hipStream_t s);
+// Relaxed tiled attention on bf16 MFMA (k_flash.hip), d in {64, 128}.  In
+// LaunchFlashDKDV one or both of dk, dv are non-null; both only where
+// FlashFusedDKDV(d).
 bool FlashFits(size_t B, size_t S, size_t H, size_t d);
+bool FlashFusedDKDV(size_t d);
 hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float* o, float* stats,
                           size_t B, size_t S, size_t H, size_t d, const int32_t* starts,
                           hipStream_t s);

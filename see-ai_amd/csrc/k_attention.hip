@@ -580,6 +580,21 @@ hipError_t LaunchAttnDVTiled(int dtype, const float* q, const float* k, const fl
   return hipGetLastError();
 }
 
+// dK and dV of one attention in a single pass: the relaxed family only,
+// where the flash kernels take the shape and fuse at this head size.
+bool AttnDKDVFusable(const float* q, const float* k, const float* v, const float* dout,
+                     const float* dk, const float* dv, size_t B, size_t S, size_t H, size_t d) {
+  return B * H * S > 0 && MfmaShape(d, q, k) && MfmaShape(d, v, dout) && MfmaShape(d, dk, dv) &&
+         FlashFits(B, S, H, d) && FlashFusedDKDV(d);
+}
+
+hipError_t LaunchAttnDKDVFused(const float* q, const float* k, const float* v, const float* dout,
+                               const float* stats, float* dk, float* dv, size_t B, size_t S,
+                               size_t H, size_t d, hipStream_t s) {
+  if (!AttnDKDVFusable(q, k, v, dout, dk, dv, B, S, H, d)) return hipErrorNotSupported;
+  return LaunchFlashDKDV(q, k, v, dout, stats, dk, dv, B, S, H, d, s);
+}
+
 hipError_t LaunchAttnFwdCached(const float* q, const float* k, const float* v, float* o,
                                float* probs, size_t B, size_t S, size_t H, size_t d,
                                const int32_t* starts, hipStream_t s) {

@@ -500,22 +500,25 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
 }
 
 // ---------------------------------------------------------------------------
-// dK or dV: one wave per 32 keys walking the query blocks from the diagonal;
-// S = Q K^T and dP = dO V^T formed query-major, dK^T += Q^T dS (times
-// 1/sqrt d at the end), dV^T += dO^T P.  K is staged pre-scaled as in the
-// forward; the score and dP accumulators start at each query row's -mm and
-// -delta, read from LDS.
+// dK and / or dV: one wave per 32 keys walking the query blocks from the
+// diagonal; S = Q K^T and dP = dO V^T formed query-major, dK^T += Q^T dS
+// (times 1/sqrt d at the end), dV^T += dO^T P.  K is staged pre-scaled as in
+// the forward; the score and dP accumulators start at each query row's -mm
+// and -delta, read from LDS.  With both outputs (kDK && kDV) one pass forms
+// S, P and dP once per block and feeds both accumulations: four products
+// per block instead of the five of two passes, one exponential per score
+// instead of two.
 // ---------------------------------------------------------------------------
-template <int D, bool kDK>
+template <int D, bool kDK, bool kDV>
 __global__ void __launch_bounds__(kFThreads)
 FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-          const float* __restrict__ dout, const float* __restrict__ stats, float* __restrict__ out,
-          int S, int H) {
+          const float* __restrict__ dout, const float* __restrict__ stats,
+          float* __restrict__ out_k, float* __restrict__ out_v, int S, int H) {
   using St = Stager<D>;
   __shared__ __attribute__((aligned(16))) __bf16 Qs[2][kBlk * St::RLD];
   __shared__ __attribute__((aligned(16))) __bf16 Qt[2][kDK ? D * St::TLD : 1];
   __shared__ __attribute__((aligned(16))) __bf16 Ds[2][kDK ? kBlk * St::RLD : 1];
-  __shared__ __attribute__((aligned(16))) __bf16 Dt[2][kDK ? 1 : D * St::TLD];
+  __shared__ __attribute__((aligned(16))) __bf16 Dt[2][kDV ? D * St::TLD : 1];
   // Per streamed query row: -mm, -delta, document start; and the block's
   // largest start.
   __shared__ __attribute__((aligned(16))) float Smm[2][kBlk];
@@ -552,7 +555,7 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
   };
   auto stage = [&](int buf, int ib) {
     sq.store(Qs[buf], kDK ? Qt[buf] : nullptr);
-    sd.store(kDK ? Ds[buf] : nullptr, kDK ? nullptr : Dt[buf]);
+    sd.store(kDK ? Ds[buf] : nullptr, kDV ? Dt[buf] : nullptr);
     if (threadIdx.x < kBlk) {  // wave 0
       const int t = threadIdx.x, iq = (blk_first + ib) * kBlk + t;
       int start = 0;
@@ -584,17 +587,17 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
     return x;
   };
 
-  v16f acc[D / 32] = {};
+  v16f acc_k[kDK ? D / 32 : 1] = {}, acc_v[kDV ? D / 32 : 1] = {};
   auto run = [&](auto masked, int buf, int r0) {
     constexpr bool kMask = decltype(masked)::value;
     const int lo_rel = r0 + 4 * g - j;  // query row r0 + il minus this lane's key
-    bf16x8 wb[4];
+    bf16x8 wb[kDK ? 4 : 1], pb[kDV ? 4 : 1];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       const v16f sc = ScoreTile<D>(Qs[buf], kf, lane, kt, rows16(Smm[buf], kt));
       v16f dpt;
       if (kDK) dpt = ScoreTile<D>(Ds[buf], vf, lane, kt, rows16(Sdl[buf], kt));
-      float w[16];
+      float p[16], w[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float e = Exp2(sc[r]);
@@ -602,11 +605,14 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
           const int il = RowOf(kt, r, g);
           e = OrZero(e, Outside(lo_rel + RowConst(kt, r), j - Sst[buf][il]));
         }
-        w[r] = kDK ? e * dpt[r] : e;
+        p[r] = e;
+        if (kDK) w[r] = e * dpt[r];
       }
-      PackTile(w, wb + 2 * kt);
+      if (kDK) PackTile(w, wb + 2 * kt);
+      if (kDV) PackTile(p, pb + 2 * kt);
     }
-    AccumTiles<D>(kDK ? Qt[buf] : Dt[buf], wb, lane, acc);
+    if (kDK) AccumTiles<D>(Qt[buf], wb, lane, acc_k);
+    if (kDV) AccumTiles<D>(Dt[buf], pb, lane, acc_v);
   };
 
   load(0);
@@ -624,14 +630,20 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
     __syncthreads();
   }
   if (j >= S) return;
-  const float scale = kDK ? isd : 1.0f;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq)
-      *reinterpret_cast<float4*>(out + base + static_cast<size_t>(j) * ld + dt * 32 + 8 * qq + 4 * g) =
-          make_float4(acc[dt][4 * qq] * scale, acc[dt][4 * qq + 1] * scale,
-                      acc[dt][4 * qq + 2] * scale, acc[dt][4 * qq + 3] * scale);
+    for (int qq = 0; qq < 4; ++qq) {
+      const size_t at = base + static_cast<size_t>(j) * ld + dt * 32 + 8 * qq + 4 * g;
+      if (kDK)
+        *reinterpret_cast<float4*>(out_k + at) =
+            make_float4(acc_k[dt][4 * qq] * isd, acc_k[dt][4 * qq + 1] * isd,
+                        acc_k[dt][4 * qq + 2] * isd, acc_k[dt][4 * qq + 3] * isd);
+      if (kDV)
+        *reinterpret_cast<float4*>(out_v + at) =
+            make_float4(acc_v[dt][4 * qq], acc_v[dt][4 * qq + 1], acc_v[dt][4 * qq + 2],
+                        acc_v[dt][4 * qq + 3]);
+    }
 }
 
 }  // namespace
@@ -677,22 +689,27 @@ hipError_t LaunchFlashDQ(const float* q, const float* k, const float* v, const f
 hipError_t LaunchFlashDKDV(const float* q, const float* k, const float* v, const float* dout,
                            const float* stats, float* dk, float* dv, size_t B, size_t S, size_t H,
                            size_t d, hipStream_t s) {
-  if ((dk == nullptr) == (dv == nullptr)) return hipErrorInvalidValue;
+  if (!dk && !dv) return hipErrorInvalidValue;
   const dim3 grid = FlashGrid(B, S, H);
   const int Si = static_cast<int>(S), Hi = static_cast<int>(H);
-  float* out = dk ? dk : dv;
+#define SEEAI_DKDV(DD, KK, VV)                                                                    \
+  hipLaunchKernelGGL((FlashDKDV<DD, KK, VV>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dk, \
+                     dv, Si, Hi)
   if (d == 64) {
-    if (dk)
-      hipLaunchKernelGGL((FlashDKDV<64, true>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, out, Si, Hi);
-    else
-      hipLaunchKernelGGL((FlashDKDV<64, false>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, out, Si, Hi);
+    if (dk && dv) SEEAI_DKDV(64, true, true);
+    else if (dk) SEEAI_DKDV(64, true, false);
+    else SEEAI_DKDV(64, false, true);
   } else {
-    if (dk)
-      hipLaunchKernelGGL((FlashDKDV<128, true>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, out, Si, Hi);
-    else
-      hipLaunchKernelGGL((FlashDKDV<128, false>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, out, Si, Hi);
+    // d = 128 runs the two passes apart: both accumulators and both score
+    // tiles at once exceed the register file (occupancy 1 with spills).
+    if (dk && dv) return hipErrorInvalidValue;
+    if (dk) SEEAI_DKDV(128, true, false);
+    else SEEAI_DKDV(128, false, true);
   }
+#undef SEEAI_DKDV
   return hipGetLastError();
 }
+
+bool FlashFusedDKDV(size_t d) { return d == 64; }
 
 }  // namespace seeai

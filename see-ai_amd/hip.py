@@ -76,6 +76,10 @@ EXPORTS = {
     "seeai_arena_bytes": (_U64, [_P]),
     "seeai_execute": (_I, [_P, _P, _P]),
     "seeai_execute_range": (_I, [_P, _P, _U64, _P, C.POINTER(_U64)]),
+    "seeai_begin_range": (_I, [_P, _P, _U64, _U64, _U64]),
+    "seeai_end_range": (_I, [_P]),
+    "seeai_set_fusion": (_I, [_P, _I]),
+    "seeai_fused_dispatches": (_U64, [_P]),
     "seeai_flush": (_I, [_P]),
     "seeai_gemm_f32": (_I, [_P, _I, _P, _P, _P, _U64, _U64, _U64, _P, _I, _P, _F, _I]),
     "seeai_gemm_q8": (_I, [_P, _I, _P, _P, _P, _U64, _U64, _U64, _F, _P, _I]),
@@ -87,6 +91,7 @@ EXPORTS = {
     "seeai_attn_dq": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
     "seeai_attn_dk": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
     "seeai_attn_dv": (_I, [_P, _I, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
+    "seeai_attn_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
     "seeai_xent_fwd": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _I]),
     "seeai_xent_bwd": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _I]),
     "seeai_adamw_step": (_I, [_P, _P, _P, _P, _P, _U64, C.POINTER(StepParams), _F]),
@@ -235,6 +240,12 @@ class HipBackend:
     def relaxed_executions(self) -> int:
         return int(_lib.seeai_relaxed_executions(self.ctx.h))
 
+    def fused_dispatches(self) -> int:  # backend.h:165
+        return int(_lib.seeai_fused_dispatches(self.ctx.h))
+
+    def SetFusion(self, allow: bool):
+        self.ctx.call("seeai_set_fusion", int(bool(allow)))
+
     def SetRelaxed(self, allow: bool):
         self.ctx.call("seeai_set_relaxed", int(bool(allow)))
 
@@ -374,6 +385,16 @@ class Engine:
         whole plan runs the exact family (source/plan/instruction.h:356-384)."""
         ctx = _lib.seeai_engine_context(self.h)
         rc = _lib.seeai_set_relaxed(ctx, int(bool(allow)))
+        if rc != OK:
+            raise BackendError(rc, _lib.seeai_last_error(ctx).decode("utf-8", "replace"))
+
+    def fused_dispatches(self) -> int:
+        return int(_lib.seeai_fused_dispatches(_lib.seeai_engine_context(self.h)))
+
+    def set_fusion(self, allow: bool):
+        """Whether adjacent relaxed dK / dV instructions run as one dispatch."""
+        ctx = _lib.seeai_engine_context(self.h)
+        rc = _lib.seeai_set_fusion(ctx, int(bool(allow)))
         if rc != OK:
             raise BackendError(rc, _lib.seeai_last_error(ctx).decode("utf-8", "replace"))
 

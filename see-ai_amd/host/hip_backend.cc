@@ -51,7 +51,14 @@ Result<void> HipBackend::Execute(const Instruction& ins, const StepParams& p) {
   return Check(seeai_execute(ctx_, &ins, &sp));
 }
 
-void HipBackend::BeginRange(std::span<const Instruction>, size_t, size_t) {}
+void HipBackend::BeginRange(std::span<const Instruction> program, size_t begin, size_t end) {
+  static_assert(sizeof(Instruction) == 64);
+  (void)seeai_begin_range(ctx_, program.data(), program.size(), begin, end);
+}
+
+void HipBackend::EndRange() { (void)seeai_end_range(ctx_); }
+
+uint64_t HipBackend::fused_dispatches() const { return seeai_fused_dispatches(ctx_); }
 
 Result<void> HipBackend::Flush() { return Check(seeai_flush(ctx_)); }
 

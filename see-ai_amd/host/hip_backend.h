@@ -53,12 +53,15 @@ class HipBackend {
   void Configure() {}
   Result<void> Execute(const Instruction& ins, const StepParams& params);
   // backend.h:139-142: whole-program visibility around a range.
+  // The backend keeps the span until EndRange: Execute is then called with
+  // references into it, and adjacent relaxed dK / dV instructions of one
+  // attention run as one dispatch.
   void BeginRange(std::span<const Instruction> program, size_t begin, size_t end);
-  void EndRange() {}
+  void EndRange();
   // backend.h:147: drains the stream; reports a refused optimizer step.
   Result<void> Flush();
   uint64_t relaxed_executions() const;
-  uint64_t fused_dispatches() const { return 0; }
+  uint64_t fused_dispatches() const;
   void SetRelaxed(bool allow);
 
   Result<void> SyncToDevice(uint64_t offset, uint64_t bytes);

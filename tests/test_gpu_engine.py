@@ -191,6 +191,28 @@ def test_decoder_training_is_bitwise_reproducible(hip, torch_cuda):
     b.close()
 
 
+def test_decoder_fused_backward_is_bitwise_the_separate_passes(hip, torch_cuda):
+    """The engine shows the backend each range (BeginRange), so adjacent
+    relaxed dK / dV instructions run as one pass; the losses and every
+    persistent byte are those of the plan run with the pairs apart."""
+    curves, states, fused = [], [], []
+    for allow in (True, False):
+        img = pw.decoder_lora(hip.plan_self_hash, relaxed=True, **TINY)
+        eng = hip.Engine(img.blob)
+        eng.set_fusion(allow)
+        curve = []
+        for s in range(3):
+            x, y = tokens(s)
+            curve.append(eng.train_step(x.view(np.float32), y))
+        curves.append(np.array(curve, np.float32))
+        states.append(eng.read(0, img.header["persistent_size"]))
+        fused.append(eng.fused_dispatches())
+        eng.close()
+    assert fused[0] > 0 and fused[1] == 0
+    assert curves[0].tobytes() == curves[1].tobytes()
+    assert states[0] == states[1]
+
+
 def test_token_outside_the_vocabulary_is_refused(hip, torch_cuda):
     img = pw.decoder_lora(hip.plan_self_hash, **TINY)
     eng = hip.Engine(img.blob)

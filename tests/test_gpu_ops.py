@@ -431,6 +431,104 @@ def test_attention_tiled(hip, orc, backend, B, S, H, d, seg, relaxed):
         assert e <= tol, f"stats[{col}]: {e:.3g}"
 
 
+@pytest.mark.parametrize("B,S,H,d,seg", [(2, 67, 2, 64, False), (1, 512, 2, 64, True),
+                                         (2, 300, 2, 64, False)])
+@pytest.mark.parametrize("order", ["dk_dv", "dv_dk"])
+def test_attention_backward_pair_fuses_bitwise(hip, orc, backend, B, S, H, d, seg, order):
+    """Adjacent relaxed kAttnDKTiled / kAttnDVTiled of one attention run as
+    one pass when a range shows the backend the program (ExecuteRange): the
+    arena bytes are those of the two instructions run one by one, and the
+    pass is counted as a fused dispatch."""
+    from tests.plan_ops import ins
+    r = rng(B * 7 + S + d)
+    shape = (B * S, H * d)
+    ar = Arena()
+    rq, rk, rv, rdo = (ar.add(n, r.standard_normal(shape).astype(np.float32))
+                       for n in ("q", "k", "v", "do"))
+    o, st = ar.empty("o", shape), ar.empty("stats", (B * H * S, 4))
+    dq, dk, dv = ar.empty("dq", shape), ar.empty("dk", shape), ar.empty("dv", shape)
+    geo = (B << 48) | (S << 32) | (H << 16) | d
+    prog = []
+    if seg:
+        rt, rs = ar.add("toks", r.integers(0, 4, B * S).astype(np.int32)), ar.empty("starts", (B * S,), np.int32)
+        prog += [ins(55, [rt, rs], [(B << 32) | S, 3]), ins(57, [rq, rk, rv, o], [st, geo, rs], flags=32)]
+    else:
+        prog.append(ins(47, [rq, rk, rv, o], [st, (B << 32) | S, (H << 32) | d], flags=32))
+    pair = [ins(49, [rq, rk, rv, rdo], [st, dk, geo], flags=32),
+            ins(50, [rq, rk, rv, rdo], [st, dv, geo], flags=32)]
+    prog += [ins(48, [rq, rk, rv, rdo], [st, dq, geo], flags=32)] + (
+        pair if order == "dk_dv" else pair[::-1])
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before = backend.fused_dispatches()
+    relaxed_before = backend.relaxed_executions()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    fused = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.fused_dispatches() - before == 1
+    assert backend.relaxed_executions() - relaxed_before == len(prog) - (1 if seg else 0)
+    for name in ["dk", "dv", "dq", "o", "stats"]:
+        assert bits_equal(ar.get(fused, name), ar.get(apart, name)), name
+    for name in ["dk", "dv"]:
+        e = maxrel(ar.get(fused, name), ar.get(cpu, name))
+        assert e <= TOL_BF16, f"{name}: {e:.3g}"
+
+
+def test_attention_backward_pair_refuses_to_fuse_over_a_reused_buffer(hip, orc, backend):
+    """dV written over v, which only the dK before it reads: legal in the
+    separate order, a race in one pass.  The range runs the two apart."""
+    from tests.plan_ops import ins
+    B, S, H, d = 1, 256, 2, 64
+    r = rng(99)
+    shape = (B * S, H * d)
+    ar = Arena()
+    rq, rk, rv, rdo = (ar.add(n, r.standard_normal(shape).astype(np.float32))
+                       for n in ("q", "k", "v", "do"))
+    o, st = ar.empty("o", shape), ar.empty("stats", (B * H * S, 4))
+    dq, dk = ar.empty("dq", shape), ar.empty("dk", shape)
+    geo = (B << 48) | (S << 32) | (H << 16) | d
+    prog = [ins(47, [rq, rk, rv, o], [st, (B << 32) | S, (H << 32) | d], flags=32),
+            ins(48, [rq, rk, rv, rdo], [st, dq, geo], flags=32),
+            ins(49, [rq, rk, rv, rdo], [st, dk, geo], flags=32),
+            ins(50, [rq, rk, rv, rdo], [st, rv, geo], flags=32)]
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before = backend.fused_dispatches()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.fused_dispatches() == before
+    assert ranged.tobytes() == apart.tobytes()
+    e = maxrel(ar.get(ranged, "v"), ar.get(cpu, "v"))
+    assert e <= TOL_BF16, f"dv over v: {e:.3g}"
+
+
+def test_attn_dkdv_entry_point_matches_the_separate_passes(hip, torch_cuda):
+    import torch
+    B, S, H, d = 2, 384, 3, 64
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q, k, v, do = (torch.randn(B * S, H * d, device="cuda", generator=g) for _ in range(4))
+    o = torch.empty_like(q)
+    st = torch.empty(B * H * S, 4, device="cuda")
+    dq, dk, dv, dk2, dv2 = (torch.empty_like(q) for _ in range(5))
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    P = lambda t: t.data_ptr()
+    ctx.call("seeai_attn_fwd", 1, P(q), P(k), P(v), P(o), P(st), B, S, H, d, None)
+    ctx.call("seeai_attn_dq", 1, P(q), P(k), P(v), P(do), P(st), P(dq), B, S, H, d)
+    ctx.call("seeai_attn_dk", 1, P(q), P(k), P(v), P(do), P(st), P(dk), B, S, H, d)
+    ctx.call("seeai_attn_dv", 1, P(q), P(k), P(do), P(st), P(dv), B, S, H, d)
+    ctx.call("seeai_attn_dkdv", P(q), P(k), P(v), P(do), P(st), P(dk2), P(dv2), B, S, H, d)
+    torch.cuda.synchronize()
+    assert torch.equal(dk.view(torch.int32), dk2.view(torch.int32))
+    assert torch.equal(dv.view(torch.int32), dv2.view(torch.int32))
+    with pytest.raises(hip.BackendError):
+        ctx.call("seeai_attn_dkdv", P(q), P(k), P(v), P(do), P(st), P(dk2), P(dv2), B, S, H, 128 // 2 + 1)
+    ctx.close()
+
+
 @pytest.mark.parametrize("B,S,H,d", [(1, 1, 1, 8), (2, 19, 2, 16), (1, 64, 2, 64)])
 def test_attention_cached_family(hip, orc, backend, B, S, H, d):
     from tests.plan_ops import ins
