@@ -263,7 +263,7 @@ hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float*
                           hipStream_t s);
 hipError_t LaunchFlashDQ(const float* q, const float* k, const float* v, const float* dout,
                          float* stats, float* dq, size_t B, size_t S, size_t H, size_t d,
-                         int delta_given, hipStream_t s);
+                         int one_pass, hipStream_t s);
 hipError_t LaunchFlashDKDV(const float* q, const float* k, const float* v, const float* dout,
                            const float* stats, float* dk, float* dv, size_t B, size_t S, size_t H,
                            size_t d, hipStream_t s);

@@ -22,6 +22,8 @@
 // k_flash.hip.
 // Other head widths run the per-row kernels below (double dots, the
 // reference's loop order).
+#include <cstdlib>
+
 #include "common.h"
 
 namespace seeai {
@@ -543,12 +545,23 @@ hipError_t LaunchAttnFwdTiled(int dtype, const float* q, const float* k, const f
   return hipGetLastError();
 }
 
+// The relaxed dQ runs in one pass (dQ = K^T (p dP) - delta K^T p) unless
+// SEEAI_DQ_TWO_PASS=1 selects the two-pass form (delta first), kept for
+// comparison.
+int FlashDQOnePass() {
+  static const int one = [] {
+    const char* e = std::getenv("SEEAI_DQ_TWO_PASS");
+    return e && e[0] == '1' ? 0 : 1;
+  }();
+  return one;
+}
+
 hipError_t LaunchAttnDQTiled(int dtype, const float* q, const float* k, const float* v,
                              const float* dout, float* stats, float* dq, size_t B, size_t S,
                              size_t H, size_t d, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   if (MfmaShape(d, q, k) && MfmaShape(d, v, dout) && MfmaShape(d, dq, q))
-    return dtype && FlashFits(B, S, H, d) ? LaunchFlashDQ(q, k, v, dout, stats, dq, B, S, H, d, 0, s)
+    return dtype && FlashFits(B, S, H, d) ? LaunchFlashDQ(q, k, v, dout, stats, dq, B, S, H, d, FlashDQOnePass(), s)
                  : ByShape<DQL>(d, q, k, v, dout, stats, dq, B, S, H, s);
   hipLaunchKernelGGL(AttnDQRowKernel, dim3(UnitsGrid(B * H * S)), dim3(kThreads), 0, s, q, k, v,
                      dout, stats, dq, B, S, H, d);

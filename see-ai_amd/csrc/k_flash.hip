@@ -382,16 +382,26 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
 __device__ __forceinline__ float RowOffset(float m, float inv) { return m * kLog2e - log2f(inv); }
 
 // ---------------------------------------------------------------------------
-// dQ: pass 1 delta = sum_j p dP, pass 2 dS = p (dP - delta), dQ^T = K^T dS^T
-// (times 1/sqrt d once, at the end).  Q is staged pre-scaled as in the
-// forward and the score accumulators start at -mm; in pass 2 the dP
-// accumulators start at -delta.
+// dQ and the stats row's delta = sum_j p dP.  Q is staged pre-scaled as in
+// the forward and the score accumulators start at -mm (p = 2^score).
+//
+// kOnePass: dS = p (dP - delta) is linear in delta, so
+//   dQ^T = K^T (p dP)^T - delta K^T p^T,
+// and delta itself accumulates in the same pass: one walk over K / V, four
+// products per block (S, dP and the two accumulations) and one exponential
+// per score.  The bf16 operands are p dP and p instead of p (dP - delta),
+// so each term's rounding is relative to |dP| + |delta| rather than
+// |dP - delta|.
+// Otherwise two walks: delta first (S and dP), then S, dP and
+// dQ^T += K^T dS^T with the dP accumulators started at -delta: five
+// products and two exponentials per score.
+// dQ is scaled by 1/sqrt d once, at the end.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool kOnePass>
 __global__ void __launch_bounds__(kFThreads)
 FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
         const float* __restrict__ dout, float* __restrict__ stats, float* __restrict__ dq, int S,
-        int H, int delta_given) {
+        int H) {
   using St = Stager<D>;
   __shared__ __attribute__((aligned(16))) __bf16 Ks[2][kBlk * St::RLD];
   __shared__ __attribute__((aligned(16))) __bf16 Kt[2][D * St::TLD];
@@ -436,32 +446,39 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
   };
 
   float delta = 0.0f;
-  for (int pass = delta_given ? 1 : 0; pass < 2; ++pass) {
-    if (pass == 1 && delta_given) delta = st[2];
-    const v16f cp = Splat(-delta);  // pass 1: dP - delta
-    v16f acc[D / 32] = {};
+  v16f acc[D / 32], acc_p[kOnePass ? D / 32 : 1];
+  // pass 0: delta only; pass 1: dQ (and, in one pass, delta beside it)
+  for (int pass = kOnePass ? 1 : 0; pass < 2; ++pass) {
+    const v16f cp = Splat(kOnePass ? 0.0f : -delta);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = v16f{};
+    if constexpr (kOnePass) {
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) acc_p[dt] = v16f{};
+    }
     auto run = [&](auto masked, int buf, int j0) {
       constexpr bool kMask = decltype(masked)::value;
       const int hi_rel = i - j0 - 4 * g, lo_rel = j_start - j0 - 4 * g;
-      bf16x8 wb[4];
+      bf16x8 wb[4], pb[kOnePass ? 4 : 1];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         const v16f sc = ScoreTile<D>(Ks[buf], qf, lane, kt, cs);
         const v16f dpt = ScoreTile<D>(Vs[buf], df, lane, kt, cp);
-        float w[16];
+        float w[16], p[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           float e = Exp2(sc[r]);
           if constexpr (kMask)  // keep j0 + row in [j_start, i]
             e = OrZero(e, Outside(hi_rel - RowConst(kt, r), RowConst(kt, r) - lo_rel));
-          if (pass == 0)
-            delta = __builtin_fmaf(dpt[r], e, delta);
-          else
-            w[r] = e * dpt[r];
+          if (kOnePass || pass == 0) delta = __builtin_fmaf(dpt[r], e, delta);
+          if (pass == 1) w[r] = e * dpt[r];
+          p[r] = e;
         }
         if (pass == 1) PackTile(w, wb + 2 * kt);
+        if (kOnePass) PackTile(p, pb + 2 * kt);
       }
       if (pass == 1) AccumTiles<D>(Kt[buf], wb, lane, acc);
+      if (kOnePass) AccumTiles<D>(Kt[buf], pb, lane, acc_p);
     };
     load(0);
     sk.store(Ks[0], pass ? Kt[0] : nullptr);
@@ -481,22 +498,23 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
       }
       __syncthreads();
     }
-    if (pass == 0) {
-      delta = SwapSum(delta);
-      continue;
-    }
-    if (i < S) {
-      float* drow = dq + base + static_cast<size_t>(i) * ld;
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq)
-          *reinterpret_cast<float4*>(drow + dt * 32 + 8 * qq + 4 * g) =
-              make_float4(acc[dt][4 * qq] * isd, acc[dt][4 * qq + 1] * isd, acc[dt][4 * qq + 2] * isd,
-                          acc[dt][4 * qq + 3] * isd);
-      if (g == 0 && !delta_given) st[2] = delta;
-    }
+    if (!kOnePass && pass == 0) delta = SwapSum(delta);
   }
+  if (kOnePass) delta = SwapSum(delta);
+  if (i >= S) return;
+  if constexpr (kOnePass) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) acc[dt] -= delta * acc_p[dt];
+  }
+  float* drow = dq + base + static_cast<size_t>(i) * ld;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+      *reinterpret_cast<float4*>(drow + dt * 32 + 8 * qq + 4 * g) =
+          make_float4(acc[dt][4 * qq] * isd, acc[dt][4 * qq + 1] * isd, acc[dt][4 * qq + 2] * isd,
+                      acc[dt][4 * qq + 3] * isd);
+  if (g == 0) st[2] = delta;
 }
 
 // ---------------------------------------------------------------------------
@@ -675,14 +693,19 @@ hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float*
 
 hipError_t LaunchFlashDQ(const float* q, const float* k, const float* v, const float* dout,
                          float* stats, float* dq, size_t B, size_t S, size_t H, size_t d,
-                         int delta_given, hipStream_t s) {
+                         int one_pass, hipStream_t s) {
   const dim3 grid = FlashGrid(B, S, H);
-  if (d == 64)
-    hipLaunchKernelGGL(FlashDQ<64>, grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dq,
-                       static_cast<int>(S), static_cast<int>(H), delta_given);
-  else
-    hipLaunchKernelGGL(FlashDQ<128>, grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dq,
-                       static_cast<int>(S), static_cast<int>(H), delta_given);
+  const int Si = static_cast<int>(S), Hi = static_cast<int>(H);
+#define SEEAI_DQ(DD, OP) \
+  hipLaunchKernelGGL((FlashDQ<DD, OP>), grid, dim3(kFThreads), 0, s, q, k, v, dout, stats, dq, Si, Hi)
+  if (d == 64) {
+    if (one_pass) SEEAI_DQ(64, true);
+    else SEEAI_DQ(64, false);
+  } else {
+    if (one_pass) SEEAI_DQ(128, true);
+    else SEEAI_DQ(128, false);
+  }
+#undef SEEAI_DQ
   return hipGetLastError();
 }
 
