@@ -57,9 +57,9 @@ def parse():
     p.add_argument("--mfma-ceiling", action="store_true",
                    help="the int8 MFMA issue rate with register-resident operands (constant, "
                         "random, small random levels) at 1, 2 and 4 waves per SIMD")
-    p.add_argument("--lora-probe", action="store_true",
-                   help="for rocprofv3 runs: BASELINE configs[3] decoder LoRA plan, one staged "
-                        "step then 5 resident steps (relaxed family)")
+    p.add_argument("--lora-probe", nargs="?", const="c4", choices=["c4", "c5"],
+                   help="for rocprofv3 runs: BASELINE configs[3] (c4) or configs[4] (c5) decoder "
+                        "LoRA plan, one staged step then resident steps (relaxed family)")
     return p.parse_args()
 
 
@@ -84,26 +84,30 @@ def mfma_ceiling():
     return 0
 
 
-def lora_probe():
-    """BASELINE configs[3] through the plan engine for the profilers: build
-    the decoder LoRA plan, one staged step, then five resident steps."""
+def lora_probe(which: str):
+    """BASELINE configs[3] (c4) or configs[4] (c5) through the plan engine
+    for the profilers: build the decoder LoRA plan, one staged step, then
+    resident steps (five for c4, two for c5)."""
     import numpy as np
     import torch
     hip = importlib.import_module("see-ai_amd.hip")
     pw = importlib.import_module("see-ai_amd.planwriter")
-    img = pw.decoder_lora(hip.plan_self_hash, relaxed=True)
+    if which == "c5":
+        img, T, n = pw.decoder_q8_lora(hip.plan_self_hash, relaxed=True), 4 * 2048, 2
+    else:
+        img, T, n = pw.decoder_lora(hip.plan_self_hash, relaxed=True), 8 * 1024, 5
+    print(f"lora probe {which}: plan built", flush=True)
     eng = hip.Engine(img.blob)
     del img
-    T = 8 * 1024
     tok = pw.uniform_ints(9, T + 1, 32000)
     eng.train_step(tok[:T].copy().view(np.float32), tok[1:].copy())
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(5):
+    for _ in range(n):
         loss = eng.train_resident()
-    dt = (time.perf_counter() - t0) / 5
+    dt = (time.perf_counter() - t0) / n
     eng.close()
-    print(f"lora probe: decoder LoRA (configs[3]) relaxed, 5 resident steps, "
+    print(f"lora probe: decoder LoRA ({which}) relaxed, {n} resident steps, "
           f"{dt * 1e3:.1f} ms/step, {T / dt:.0f} tokens/s, loss {loss:.4f}", flush=True)
     return 0
 
@@ -194,7 +198,7 @@ def main():
     if args.attn_probe:
         return attn_probe()
     if args.lora_probe:
-        return lora_probe()
+        return lora_probe(args.lora_probe)
     if args.mfma_ceiling:
         return mfma_ceiling()
     if args.gpus != 1:
@@ -389,13 +393,13 @@ def extras(ctx, torch, hip):
     return out
 
 
-def decoder_step_flops(layers, dim, ffn, vocab, T, batch, seq, heads):
+def decoder_step_flops(layers, dim, ffn, vocab, T, batch, seq, heads, ffn_mats=2):
     """Algorithmic FLOP of one decoder LoRA training step: 2*T*P for the
     frozen products' forward plus 2*T*P for their dX (P = frozen GEMM
     parameters; an approximation: the step skips the dX below layer 0's
     LoRA sites), plus causal-exact attention fwd + bwd (3 x 4*d*pairs per
     (b, h) and layer).  LoRA products are negligible and not counted."""
-    P = layers * (4 * dim * dim + 2 * dim * ffn) + dim * vocab
+    P = layers * (4 * dim * dim + ffn_mats * dim * ffn) + dim * vocab
     d = dim // heads
     pairs = seq * (seq + 1) // 2
     attn = layers * batch * heads * 3 * 4 * d * pairs
@@ -452,6 +456,35 @@ def lora_steps(torch, hip):
                      "config": "12 layers, d768, 12 heads, FFN 3072, vocab 32000, B8 x S1024, "
                                "LoRA r8 on Q/V",
                      "plan_build_s": round(build_s, 1)}
+    eng.close()
+    del eng
+
+    # 16 layers, d2048, 32 heads, SiLU-gated FFN 5632, RMSNorm,
+    # frozen int8 base (per-column scales), LoRA r16 on Q/K/V/O, 4 x 2048
+    # tokens per step; the relaxed family (bf16 MFMA over the exact int8
+    # levels).  The exact family at this size is parity-tested at a small
+    # shape, not timed.
+    t0 = time.perf_counter()
+    img = pw.decoder_q8_lora(hip.plan_self_hash, relaxed=True)
+    build_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    eng = hip.Engine(img.blob)
+    load_s = time.perf_counter() - t0
+    del img
+    T = 4 * 2048
+    tok = pw.uniform_ints(10, T + 1, 32000)
+    eng.train_step(tok[:T].copy().view(np.float32), tok[1:].copy())
+    flops = decoder_step_flops(16, 2048, 5632, 32000, T, 4, 2048, 32, ffn_mats=3)
+    n = 3
+    dt, loss = steps_per_s(eng, n, 1)
+    tf = flops / dt / 1e12
+    out["lora_decoder_c5_relaxed"] = {
+        "ms_per_step": round(dt * 1e3, 2), "tokens_s": round(T / dt), "TFLOP_s": round(tf, 1),
+        "bf16_mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop_per_step": flops, "loss": loss,
+        "steps_timed": n, "fused_dispatches": eng.fused_dispatches(),
+        "config": "16 layers, d2048, 32 heads, SiLU-gated FFN 5632, RMSNorm, vocab 32000, "
+                  "B4 x S2048, int8 base (per-column scales), LoRA r16 on Q/K/V/O",
+        "plan_build_s": round(build_s, 1), "plan_load_s": round(load_s, 1)}
     eng.close()
     return out
 

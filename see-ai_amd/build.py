@@ -30,6 +30,7 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libseeai_hip.so")
 PROBE_LIB = os.path.join(HERE, "libseeai_probe.so")
+PLANGEN_LIB = os.path.join(HERE, "libseeai_plangen.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -95,6 +96,14 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on mfma_ceiling.hip:\n{r.stderr[-6000:]}")
     os.replace(probe_tmp, PROBE_LIB)
+    # The plan writer's bulk generator (host code only).
+    gen_src = os.path.join(HERE, "plangen", "plangen.cc")
+    gen_tmp = PLANGEN_LIB + ".tmp"
+    r = subprocess.run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-pthread",
+                        "-ffp-contract=off", "-o", gen_tmp, gen_src], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed on plangen.cc:\n{r.stderr[-6000:]}")
+    os.replace(gen_tmp, PLANGEN_LIB)
     if verbose:
         print(f"built {LIB}")
     return LIB
@@ -102,7 +111,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
 
 def clean() -> None:
     shutil.rmtree(BUILD, ignore_errors=True)
-    for lib in (LIB, PROBE_LIB):
+    for lib in (LIB, PROBE_LIB, PLANGEN_LIB):
         if os.path.exists(lib):
             os.remove(lib)
 

@@ -220,7 +220,8 @@ hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s);
 hipError_t LaunchGemmExact(const GemmArgs& a, hipStream_t s);
 // Workspace the exact kernels can use for this GEMM (0: none).
 size_t GemmExactScratchBytes(const GemmArgs& a);
-// Relaxed f32-weight NN / NT on bf16 MFMA (k_gemm_bf16.hip), when it fits.
+// Relaxed NN / NT with f32 or int8 weights on bf16 MFMA (k_gemm_bf16.hip),
+// when it fits.
 bool GemmBf16Fits(const GemmArgs& a);
 hipError_t LaunchGemmBf16(const GemmArgs& a, hipStream_t s);
 

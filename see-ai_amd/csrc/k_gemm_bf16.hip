@@ -1,7 +1,11 @@
 // k_gemm_bf16.hip -- the relaxed family's frozen-weight products on bf16
-// MFMA (kFlagRelaxed on kGemmNN / kGemmNT with f32 weights,
-// source/plan/instruction.h:356-384: the activations rounded to bf16 once at
-// the GEMM input, the f32 weight in reduced precision, f32 accumulation).
+// MFMA (kFlagRelaxed on kGemmNN / kGemmNT with f32 weights and on kGemmNNQ8
+// / kGemmNTQ8 with int8 levels, source/plan/instruction.h:356-384: the
+// activations rounded to bf16 once at the GEMM input, the weight in reduced
+// precision, f32 accumulation).  int8 levels are exact in bf16, so a q8
+// product's only rounding is the activation's: the per-tensor scale and the
+// NT k-scale multiply A before it rounds (gemm.cc:626-674), the NN column
+// scale multiplies the finished dot.
 //
 // A 128 x 128 tile of C per 256-lane workgroup: four waves in 2 x 2, each a
 // 64 x 64 block of 2 x 2 v_mfma_f32_32x32x16_bf16 tiles.  K walks in steps
@@ -29,9 +33,14 @@ __device__ __forceinline__ bf16x4 ToBf16(float4 v) {
                 static_cast<__bf16>(v.w)};
 }
 
-// kLayout 0 = NN (B[K, N]), 1 = NT (B[N, K]).  Requires K % 4 == 0, and for
-// NN N % 4 == 0, with 16-byte aligned operands (checked by the launcher).
-template <int kLayout>
+__device__ __forceinline__ __bf16 Level(uint32_t w, int c) {
+  return static_cast<__bf16>(static_cast<float>(static_cast<int8_t>(w >> (8 * c))));
+}
+
+// kLayout 0 = NN (B[K, N]), 1 = NT (B[N, K]); kBKind 0 = f32 weights, 1 =
+// int8 levels.  Requires K % 4 == 0, and for NN N % 4 == 0, with 16-byte
+// aligned A and f32 B, 4-byte aligned int8 B (checked by the launcher).
+template <int kLayout, int kBKind>
 __global__ void __launch_bounds__(kThreads) GemmBf16Kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) __bf16 As[2][BM * LDK];
   __shared__ __attribute__((aligned(16))) __bf16 Bs[2][BN * LDK];
@@ -44,6 +53,7 @@ __global__ void __launch_bounds__(kThreads) GemmBf16Kernel(GemmArgs g) {
   const size_t m0 = (blockIdx.x % tiles_m) * BM, n0 = (blockIdx.x / tiles_m) * BN;
   const float* __restrict__ A = g.A;
   const float* __restrict__ B = static_cast<const float*>(g.B);
+  const int8_t* __restrict__ Bq = static_cast<const int8_t*>(g.B);
   const float alpha = g.alpha_a;
 
   // Staging: a row-major operand (A, or NT's B) moves as 16 lanes x 4 k per
@@ -51,6 +61,7 @@ __global__ void __launch_bounds__(kThreads) GemmBf16Kernel(GemmArgs g) {
   // 32 n-quads = 512 blocks, 2 per lane), consecutive lanes on consecutive
   // k-quads so the transposed LDS writes of a wave fill whole rows.
   float4 ra[8], rb[8];
+  uint32_t rq[8];  // int8 weights: four levels per register
   auto load_rows = [&](const float* src, size_t rows, size_t r0, size_t k0, float4* dst,
                        bool scale_a) {
 #pragma unroll
@@ -90,9 +101,31 @@ __global__ void __launch_bounds__(kThreads) GemmBf16Kernel(GemmArgs g) {
       }
     }
   };
+  auto load_q8 = [&](size_t k0) {
+    if constexpr (kLayout == 1) {  // rows n of [N, K], four k per lane
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        const int r = p * 16 + tid / 16, k4 = (tid % 16) * 4;
+        const size_t row = n0 + r, k = k0 + k4;
+        rq[p] = (row < N && k < K) ? *reinterpret_cast<const uint32_t*>(Bq + row * K + k) : 0u;
+      }
+    } else {  // 4 x 4 blocks of [K, N]: four k rows of four n
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int blk = tid + h * kThreads, kq = blk % 16, nq = blk / 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const size_t k = k0 + kq * 4 + r, n = n0 + nq * 4;
+          rq[h * 4 + r] = (k < K && n < N) ? *reinterpret_cast<const uint32_t*>(Bq + k * N + n) : 0u;
+        }
+      }
+    }
+  };
   auto load = [&](size_t k0) {
     load_rows(A, M, m0, k0, ra, true);
-    if constexpr (kLayout == 1)
+    if constexpr (kBKind == 1)
+      load_q8(k0);
+    else if constexpr (kLayout == 1)
       load_rows(B, N, n0, k0, rb, false);
     else
       load_nn_b(k0);
@@ -103,7 +136,24 @@ __global__ void __launch_bounds__(kThreads) GemmBf16Kernel(GemmArgs g) {
       const int r = p * 16 + tid / 16, k4 = (tid % 16) * 4;
       *reinterpret_cast<bf16x4*>(&As[buf][r * LDK + k4]) = ToBf16(ra[p]);
     }
-    if constexpr (kLayout == 1) {
+    if constexpr (kBKind == 1 && kLayout == 1) {
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        const int r = p * 16 + tid / 16, k4 = (tid % 16) * 4;
+        *reinterpret_cast<bf16x4*>(&Bs[buf][r * LDK + k4]) =
+            bf16x4{Level(rq[p], 0), Level(rq[p], 1), Level(rq[p], 2), Level(rq[p], 3)};
+      }
+    } else if constexpr (kBKind == 1) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int blk = tid + h * kThreads, kq = blk % 16, nq = blk / 16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)  // rq[h*4 + r] byte c: k row r, n col c
+          *reinterpret_cast<bf16x4*>(&Bs[buf][(nq * 4 + c) * LDK + kq * 4]) =
+              bf16x4{Level(rq[h * 4], c), Level(rq[h * 4 + 1], c), Level(rq[h * 4 + 2], c),
+                     Level(rq[h * 4 + 3], c)};
+      }
+    } else if constexpr (kLayout == 1) {
 #pragma unroll
       for (int p = 0; p < 8; ++p) {
         const int r = p * 16 + tid / 16, k4 = (tid % 16) * 4;
@@ -168,6 +218,7 @@ __global__ void __launch_bounds__(kThreads) GemmBf16Kernel(GemmArgs g) {
         const size_t n = n0 + wn + j * 32 + c32;
         if (m >= M || n >= N) continue;
         float v = acc[i][j][r];
+        if (kBKind == 1 && g.b_col_scale) v = v * g.b_col_scale[n];
         if (g.alpha_dot != 1.0f) v = g.alpha_dot * v;
         const size_t o = m * N + n;
         if (g.addend) v = g.addend[o] + v;
@@ -183,19 +234,23 @@ bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 }  // namespace
 
 bool GemmBf16Fits(const GemmArgs& a) {
-  if (a.b_kind != 0 || a.layout > 1 || a.M < 64 || a.N < 64 || a.K < 64) return false;
+  if (a.b_kind > 1 || a.layout > 1 || a.M < 64 || a.N < 64 || a.K < 64) return false;
   if (a.K % 4 != 0 || (a.layout == 0 && a.N % 4 != 0)) return false;
-  if (!Aligned16(a.A) || !Aligned16(a.B)) return false;
+  if (!Aligned16(a.A)) return false;
+  if (a.b_kind == 0 ? !Aligned16(a.B) : (reinterpret_cast<uintptr_t>(a.B) & 3) != 0) return false;
   const size_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   return tiles < (size_t{1} << 31);
 }
 
 hipError_t LaunchGemmBf16(const GemmArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN)));
-  if (a.layout == 0)
-    hipLaunchKernelGGL(GemmBf16Kernel<0>, grid, dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(GemmBf16Kernel<1>, grid, dim3(kThreads), 0, s, a);
+  switch (a.layout * 2 + a.b_kind) {
+    case 0: hipLaunchKernelGGL((GemmBf16Kernel<0, 0>), grid, dim3(kThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((GemmBf16Kernel<0, 1>), grid, dim3(kThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((GemmBf16Kernel<1, 0>), grid, dim3(kThreads), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((GemmBf16Kernel<1, 1>), grid, dim3(kThreads), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

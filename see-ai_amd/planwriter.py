@@ -102,12 +102,49 @@ def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
 _PAIRS_PER_CHUNK = 1 << 19
 
 
+_GEN = None
+
+
+def _gen():
+    """The threaded C++ restatement of normal() and quantize_cols()
+    (plangen/plangen.cc, built beside the executor), or None."""
+    global _GEN
+    if _GEN is None:
+        import ctypes
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libseeai_plangen.so")
+        if not os.path.exists(path):
+            _GEN = False
+            return None
+        lib = ctypes.CDLL(path)
+        lib.seeai_plangen_normal.restype = ctypes.c_int
+        lib.seeai_plangen_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double,
+                                             ctypes.c_void_p]
+        lib.seeai_plangen_quantize_cols.restype = ctypes.c_int
+        lib.seeai_plangen_quantize_cols.argtypes = [ctypes.c_void_p, ctypes.c_uint64,
+                                                    ctypes.c_uint64, ctypes.c_void_p,
+                                                    ctypes.c_void_p]
+        _GEN = lib
+    return _GEN or None
+
+
 def normal(seed: int, shape, std: float = 1.0) -> np.ndarray:
     """N(0, std^2) f32 by Box-Muller in double over SplitMix64 uniforms:
-    pair p takes outputs 2p+1 and 2p+2, giving elements 2p and 2p+1.
-    Large arrays are generated in chunks of pairs on a thread pool (numpy
-    releases the GIL); every element is the same function of its index, so
-    the bytes do not depend on the chunking."""
+    pair p takes outputs 2p+1 and 2p+2, giving elements 2p and 2p+1
+    (normal_numpy states it).  Generated by the threaded C++ restatement
+    when it is built, which gives the same bytes."""
+    lib = _gen()
+    if lib is None:
+        return normal_numpy(seed, shape, std)
+    out = np.empty(int(np.prod(shape)), np.float32)
+    if lib.seeai_plangen_normal(seed & (2**64 - 1), out.size, float(std), out.ctypes.data) != 0:
+        raise RuntimeError("plangen normal failed")
+    return out.reshape(shape)
+
+
+def normal_numpy(seed: int, shape, std: float = 1.0) -> np.ndarray:
+    """normal() in numpy.  Large arrays are generated in chunks of pairs on a
+    thread pool (numpy releases the GIL); every element is the same
+    function of its index, so the bytes do not depend on the chunking."""
     n = int(np.prod(shape))
     m = (n + 1) // 2
     out = np.empty(2 * m, np.float32)
@@ -134,6 +171,40 @@ def normal(seed: int, shape, std: float = 1.0) -> np.ndarray:
 
 def uniform_ints(seed: int, n: int, high: int) -> np.ndarray:
     return (splitmix64(seed, n) % np.uint64(high)).astype(np.int32)
+
+
+def quantize_cols(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per-output-column symmetric int8 of W [K, M] by the reference's rule
+    (arena_binder.cc:129-177): column scale max|w| / 127, 1 for an all-zero
+    column, at least FLT_MIN; level = clamp(round(w / scale), -127, 127)
+    with the quotient in f32 and halves rounded away from zero
+    (std::round).  quantize_cols_numpy states it; the C++ restatement runs
+    when built."""
+    lib = _gen()
+    w = np.ascontiguousarray(w, np.float32)
+    if lib is None or w.ndim != 2:
+        return quantize_cols_numpy(w)
+    levels = np.empty(w.shape, np.int8)
+    sc = np.empty(w.shape[1], np.float32)
+    if lib.seeai_plangen_quantize_cols(w.ctypes.data, w.shape[0], w.shape[1], levels.ctypes.data,
+                                       sc.ctypes.data) != 0:
+        raise RuntimeError("plangen quantize failed")
+    return levels, sc
+
+
+def quantize_cols_numpy(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """quantize_cols() in numpy."""
+    w = np.ascontiguousarray(w, np.float32)
+    mx = np.max(np.abs(w), axis=0)
+    sc = np.where(mx == 0, np.float32(1.0),
+                  np.maximum(mx / np.float32(127.0), np.finfo(np.float32).tiny)).astype(np.float32)
+    levels = np.empty(w.shape, np.int8)
+    rows = max(1, (1 << 22) // max(1, w.shape[1]))
+    for r0 in range(0, w.shape[0], rows):
+        q = (w[r0:r0 + rows] / sc).astype(np.float64)          # the f32 quotient, widened
+        q = np.sign(q) * np.floor(np.abs(q) + 0.5)              # halves away from zero
+        levels[r0:r0 + rows] = np.clip(q, -127, 127).astype(np.int8)
+    return levels, sc
 
 
 # --- plan assembly -------------------------------------------------------------------------------
@@ -201,7 +272,9 @@ def assemble(header: dict, train: list, eval_: list, merge: list, emit: list,
     out[0:320] = pack_header(h)
     h["plan_hash"] = self_hash(out)
     out[0:320] = pack_header(h)
-    return bytes(out)
+    # A plan of a gigabyte and more stays the buffer it was built in (one
+    # copy fewer); every reader takes any bytes-like object.
+    return out if len(out) >= (1 << 30) else bytes(out)
 
 
 def mlp_lora(self_hash, batch: int = 32, din: int = 256, hidden: int = 512, dout: int = 256,
@@ -315,6 +388,11 @@ ROPE_FWD, ROPE_BWD, ROPE_TABLE = 33, 34, 45
 EMBED_FWD = 41
 ATTN_FWD_TILED, ATTN_DQ_TILED, ATTN_DK_TILED, ATTN_DV_TILED = 47, 48, 49, 50
 FLAG_RELAXED = 1 << 5        # kFlagRelaxed
+MUL_EW = 21
+SILU_FWD, SILU_BWD = 24, 25
+GEMM_NN_Q8, GEMM_NT_Q8 = 29, 30
+RMSNORM_FWD, RMSNORM_BWD = 31, 32
+FLAG_Q8_COL_SCALE = 1 << 4   # kFlagQ8ColScale
 
 
 class Builder:
@@ -335,6 +413,19 @@ class Builder:
         self.arrays[name] = np.ascontiguousarray(array, np.float32)
         self.params.append(name)
         return self.ar.alloc(name, self.arrays[name].nbytes, align=4)
+
+    def const_q8(self, name: str, w: np.ndarray) -> tuple[int, int]:
+        """A frozen weight W [K, M] packed as the reference's compiler packs
+        an int8 base with per-column scales (arena_binder.cc:129-202,
+        283-287): the levels, then one f32 scale per output column right
+        after them (4-byte aligned).  Returns the levels' and the scales'
+        refs."""
+        levels, scales = quantize_cols(w)
+        self.arrays[name] = levels
+        self.arrays[name + ".s"] = scales
+        ref = self.ro.alloc(name, levels.nbytes, align=256)
+        sref = self.ro.alloc(name + ".s", scales.nbytes, align=4)
+        return ref, sref
 
     def buf(self, name: str, count: int, itemsize: int = 4) -> int:
         return self.ar.alloc(name, count * itemsize)
@@ -533,6 +624,210 @@ def decoder_lora(self_hash, vocab: int = 32000, dim: int = 768, heads: int = 12,
         label_kind=1, optimizer_kind=1, loss_ref=R("loss"), lr=lr, beta1=0.9, beta2=0.999,
         eps=1e-8, weight_decay=weight_decay, batch=T, default_steps=default_steps,
         input_kind=1, seq_len=seq)
-    blob = assemble(header, train, eval_, [], [], bytes(persist), bytes(rodata), self_hash)
+    blob = assemble(header, train, eval_, [], [], bytes(persist), rodata, self_hash)
+    return PlanImage(blob=blob, header=parse_header(blob), arena=dict(b.ar.names),
+                     rodata=dict(b.ro.names), train=train, eval=eval_, merge=[], arrays=b.arrays)
+
+
+# --- the larger decoder with a frozen int8 base ---------------------------
+def decoder_q8_lora(self_hash, vocab: int = 32000, dim: int = 2048, heads: int = 32,
+                    ffn: int = 5632, layers: int = 16, seq: int = 2048, batch: int = 4,
+                    rank: int = 16, alpha: float = 32.0, relaxed: bool = True,
+                    rope_base: float = 10000.0, lr: float = 1e-3, weight_decay: float = 0.01,
+                    seed: int = 20261205, default_steps: int = 100) -> PlanImage:
+    """a pre-norm decoder of `layers` blocks -- RMSNorm,
+    Q / K / V projections, RoPE on Q and K, causal attention (tiled family),
+    output projection, residual; RMSNorm, SiLU-gated FFN (gate and up
+    dim -> ffn, SiLU(gate) * up, down ffn -> dim), residual -- then RMSNorm,
+    the vocabulary head and next-token softmax-xent, AdamW on the adapters.
+    The frozen base (Q, K, V, O, gate, up, down) is int8 with per-column
+    scales (kGemmNNQ8 / kGemmNTQ8 with kFlagQ8ColScale, packed as the
+    reference packs it); embedding, gains and head stay f32.  LoRA (rank,
+    alpha) on Q, K, V and O; alpha = 2 rank, so s = 2 is a power of two and
+    alpha's placement is exact on every backend.  Weights N(0, 0.02), gains
+    1, A N(0, 0.02), B = 0; token ids in, next tokens as labels.
+
+    The lowering follows decoder_lora's (lora_grafter.cc:170-207,
+    autodiff.cc:71-93), with the rules the narrow-weight GEMMs add: a q8
+    product takes no addend (instruction.h:318-330), so a q8 dX joins its
+    LoRA dX through the f32 NT's addend slot, and two q8 dX paths add with
+    kAddEW; the gated FFN's backward is two kMulEW (dh * up, dh * SiLU(gate))
+    and kSiluBwd.  Every block's dQ, dK, dV feed an adapter, so all three run
+    in every block; the first block forms no dX below its norm.  `relaxed`
+    sets kFlagRelaxed on the frozen products (q8 and the head) and on
+    attention."""
+    assert dim % heads == 0
+    T, D, F, H, d = batch * seq, dim, ffn, heads, dim // heads
+    s = alpha / rank
+    sb = f32_bits(s)
+    rf = FLAG_RELAXED if relaxed else 0
+    qf = FLAG_Q8_COL_SCALE | rf
+    b = Builder()
+    R, RO = b.ar.ref, b.ro.ref
+    b.const("emb", normal(seed, (vocab, D), 0.02))
+    ones = np.ones(D, np.float32)
+    sites = "qkvo"
+    for l in range(layers):
+        p = f"l{l}."
+        b.const(p + "g1", ones)
+        for w in sites:
+            b.const_q8(p + "w" + w, normal(seed + 100 * l + ord(w), (D, D), 0.02))
+        b.const(p + "g2", ones)
+        b.const_q8(p + "wg", normal(seed + 100 * l + 1, (D, F), 0.02))
+        b.const_q8(p + "wu", normal(seed + 100 * l + 2, (D, F), 0.02))
+        b.const_q8(p + "wd", normal(seed + 100 * l + 3, (F, D), 0.02))
+    b.const("gf", ones)
+    b.const("wh", normal(seed + 7, (D, vocab), 0.02))
+    for l in range(layers):
+        p = f"l{l}."
+        for w in sites:
+            b.param(p + "A" + w, normal(seed + 1000 + 10 * l + ord(w), (D, rank), 0.02))
+            b.param(p + "B" + w, np.zeros((rank, D), np.float32))
+    for n in list(b.params):
+        b.ar.alloc("m_" + n, b.arrays[n].nbytes, align=4)
+    for n in list(b.params):
+        b.ar.alloc("v_" + n, b.arrays[n].nbytes, align=4)
+    persistent = b.ar.size
+    b.buf("tokens", T)
+    b.buf("labels", T)
+    b.buf("loss", 1)
+    b.buf("seed", 1)
+    b.buf("rope", seq * (d // 2) * 2)
+    TD, TF, Tr = T * D, T * F, T * rank
+    for l in range(layers):
+        p = f"l{l}."
+        for n, c in [("x", TD), ("n1", TD), ("rstd1", T), ("tq", Tr), ("tk", Tr), ("tv", Tr),
+                     ("to", Tr), ("qr", TD), ("kr", TD), ("v", TD), ("a", TD),
+                     ("stats", T * H * 4), ("x1", TD), ("n2", TD), ("rstd2", T), ("gt", TF),
+                     ("up", TF), ("sg", TF)]:
+            b.buf(p + n, c)
+    for n, c in [("xL", TD), ("nf", TD), ("rstdf", T), ("logits", T * vocab),
+                 ("probs", T * vocab)]:
+        b.buf(n, c)
+    for n, c in [("q0", TD), ("q", TD), ("k0", TD), ("k", TD), ("v0", TD), ("o0", TD),
+                 ("o", TD), ("h", TF), ("dn", TD),
+                 ("dlogits", T * vocab), ("dnf", TD), ("dx2", TD), ("dh", TF), ("dsg", TF),
+                 ("dup", TF), ("dgt", TF), ("dn2a", TD), ("dn2b", TD), ("dn2", TD),
+                 ("dx1b", TD), ("dx1", TD), ("da0", TD), ("da", TD), ("dqr", TD), ("dkr", TD),
+                 ("dv", TD), ("dq", TD), ("dk", TD), ("dtq", Tr), ("dtk", Tr), ("dtv", Tr),
+                 ("dto", Tr), ("P1", TD), ("P2", TD), ("P3", TD), ("dxb", TD)]:
+        b.buf(n, c)
+    for l in range(layers):
+        p = f"l{l}."
+        for w in sites:
+            b.buf(p + "dA" + w, D * rank)
+            b.buf(p + "dB" + w, rank * D)
+
+    E = b.emit
+    bs, hd = (batch << 32) | seq, (H << 32) | d
+    geo = (batch << 48) | (seq << 32) | (H << 16) | d
+    nd = (T << 32) | D
+    base_bits = f32_bits(rope_base)
+
+    def q8(opcode, x, w, out, m, n, k):
+        E(ins(opcode, [R(x), RO(w), R(out), RO(w + ".s")], [m, n, k], flags=qf))
+
+    def adapted(x, w, A, B_, t, out0, out):
+        """C = x@W + s*(x@A)@B over the int8 base: NN-q8, NN, NN-addend."""
+        q8(GEMM_NN_Q8, x, w, out0, T, D, D)
+        E(ins(GEMM_NN, [R(x), R(A), R(t)], [T, rank, D]))
+        E(ins(GEMM_NN, [R(t), R(B_), R(out), R(out0)], [T, D, rank], flags=FLAG_ADDEND, imm=sb))
+
+    E(ins(ROPE_TABLE, [R("rope")], [(seq << 32) | d, base_bits]))
+    E(ins(EMBED_FWD, [R("tokens"), RO("emb"), R("l0.x")], [T, (vocab << 32) | D]))
+    for l in range(layers):
+        p = f"l{l}."
+        nxt = f"l{l + 1}.x" if l + 1 < layers else "xL"
+        E(ins(RMSNORM_FWD, [R(p + "x"), RO(p + "g1"), R(p + "n1"), R(p + "rstd1")], [nd]))
+        adapted(p + "n1", p + "wq", p + "Aq", p + "Bq", p + "tq", "q0", "q")
+        adapted(p + "n1", p + "wk", p + "Ak", p + "Bk", p + "tk", "k0", "k")
+        adapted(p + "n1", p + "wv", p + "Av", p + "Bv", p + "tv", "v0", p + "v")
+        E(ins(ROPE_FWD, [R("q"), R(p + "qr"), R("rope")], [bs, hd, base_bits]))
+        E(ins(ROPE_FWD, [R("k"), R(p + "kr"), R("rope")], [bs, hd, base_bits]))
+        E(ins(ATTN_FWD_TILED, [R(p + "qr"), R(p + "kr"), R(p + "v"), R(p + "a")],
+              [R(p + "stats"), bs, hd], flags=rf))
+        adapted(p + "a", p + "wo", p + "Ao", p + "Bo", p + "to", "o0", "o")
+        E(ins(ADD_EW, [R(p + "x"), R("o"), R(p + "x1")], [TD]))
+        E(ins(RMSNORM_FWD, [R(p + "x1"), RO(p + "g2"), R(p + "n2"), R(p + "rstd2")], [nd]))
+        q8(GEMM_NN_Q8, p + "n2", p + "wg", p + "gt", T, F, D)
+        q8(GEMM_NN_Q8, p + "n2", p + "wu", p + "up", T, F, D)
+        E(ins(SILU_FWD, [R(p + "gt"), R(p + "sg")], [TF]))
+        E(ins(MUL_EW, [R(p + "sg"), R(p + "up"), R("h")], [TF]))
+        q8(GEMM_NN_Q8, "h", p + "wd", "dn", T, D, F)
+        E(ins(ADD_EW, [R(p + "x1"), R("dn"), R(nxt)], [TD]))
+    E(ins(RMSNORM_FWD, [R("xL"), RO("gf"), R("nf"), R("rstdf")], [nd]))
+    E(ins(GEMM_NN, [R("nf"), RO("wh"), R("logits")], [T, vocab, D], flags=rf))
+    E(ins(XENT_FWD, [R("logits"), R("labels"), R("loss"), R("probs")], [T, vocab]))
+    n_eval = len(b.train)
+    # --- backward ---
+    E(ins(FILL, [R("seed"), f32_bits(1.0)], [1]))
+    E(ins(XENT_BWD, [R("probs"), R("labels"), R("seed"), R("dlogits")], [T, vocab]))
+    E(ins(GEMM_NT, [R("dlogits"), RO("wh"), R("dnf")], [T, D, vocab], flags=rf))
+    E(ins(RMSNORM_BWD, [R("dnf"), R("xL"), RO("gf"), R("dx2")], [R("rstdf"), nd]))
+    for l in reversed(range(layers)):
+        p = f"l{l}."
+        # x2 = x1 + down(SiLU(gate n2) * up n2), n2 = RMSNorm(x1)
+        q8(GEMM_NT_Q8, "dx2", p + "wd", "dh", T, F, D)
+        E(ins(MUL_EW, [R("dh"), R(p + "up"), R("dsg")], [TF]))
+        E(ins(MUL_EW, [R("dh"), R(p + "sg"), R("dup")], [TF]))
+        E(ins(SILU_BWD, [R("dsg"), R(p + "gt"), R("dgt")], [TF]))
+        q8(GEMM_NT_Q8, "dgt", p + "wg", "dn2a", T, D, F)
+        q8(GEMM_NT_Q8, "dup", p + "wu", "dn2b", T, D, F)
+        E(ins(ADD_EW, [R("dn2a"), R("dn2b"), R("dn2")], [TD]))
+        E(ins(RMSNORM_BWD, [R("dn2"), R(p + "x1"), RO(p + "g2"), R("dx1b")], [R(p + "rstd2"), nd]))
+        E(ins(ADD_EW, [R("dx2"), R("dx1b"), R("dx1")], [TD]))
+        # x1 = x + O(attn(...)): the O site, then the attention gradients
+        q8(GEMM_NT_Q8, "dx1", p + "wo", "da0", T, D, D)
+        E(ins(GEMM_NT, [R("dx1"), R(p + "Bo"), R("dto")], [T, rank, D], imm=sb))
+        E(ins(GEMM_TN, [R(p + "to"), R("dx1"), R(p + "dBo")], [rank, D, T], imm=sb))
+        E(ins(GEMM_TN, [R(p + "a"), R("dto"), R(p + "dAo")], [D, rank, T]))
+        E(ins(GEMM_NT, [R("dto"), R(p + "Ao"), R("da"), R("da0")], [T, D, rank],
+              flags=FLAG_ADDEND))
+        qkv = [R(p + "qr"), R(p + "kr"), R(p + "v"), R("da")]
+        E(ins(ATTN_DQ_TILED, qkv, [R(p + "stats"), R("dqr"), geo], flags=rf))
+        E(ins(ATTN_DK_TILED, qkv, [R(p + "stats"), R("dkr"), geo], flags=rf))
+        E(ins(ATTN_DV_TILED, qkv, [R(p + "stats"), R("dv"), geo], flags=rf))
+        E(ins(ROPE_BWD, [R("dqr"), R("dq"), R("rope")], [bs, hd, base_bits]))
+        E(ins(ROPE_BWD, [R("dkr"), R("dk"), R("rope")], [bs, hd, base_bits]))
+        for w, dC, dt in [("q", "dq", "dtq"), ("k", "dk", "dtk"), ("v", "dv", "dtv")]:
+            E(ins(GEMM_NT, [R(dC), R(p + "B" + w), R(dt)], [T, rank, D], imm=sb))
+            E(ins(GEMM_TN, [R(p + "t" + w), R(dC), R(p + "dB" + w)], [rank, D, T], imm=sb))
+            E(ins(GEMM_TN, [R(p + "n1"), R(dt), R(p + "dA" + w)], [D, rank, T]))
+        if l == 0:
+            continue  # nothing trainable below the first block's inputs
+        # dn1 = (dq Wq^T + dtq Aq^T) + (dk Wk^T + dtk Ak^T) + (dv Wv^T + dtv Av^T)
+        q8(GEMM_NT_Q8, "dq", p + "wq", "P1", T, D, D)
+        E(ins(GEMM_NT, [R("dtq"), R(p + "Aq"), R("P2"), R("P1")], [T, D, rank], flags=FLAG_ADDEND))
+        q8(GEMM_NT_Q8, "dk", p + "wk", "P1", T, D, D)
+        E(ins(GEMM_NT, [R("dtk"), R(p + "Ak"), R("P3"), R("P1")], [T, D, rank], flags=FLAG_ADDEND))
+        E(ins(ADD_EW, [R("P2"), R("P3"), R("P1")], [TD]))
+        q8(GEMM_NT_Q8, "dv", p + "wv", "P2", T, D, D)
+        E(ins(GEMM_NT, [R("dtv"), R(p + "Av"), R("P3"), R("P2")], [T, D, rank], flags=FLAG_ADDEND))
+        E(ins(ADD_EW, [R("P1"), R("P3"), R("dn2")], [TD]))
+        E(ins(RMSNORM_BWD, [R("dn2"), R(p + "x"), RO(p + "g1"), R("dxb")], [R(p + "rstd1"), nd]))
+        E(ins(ADD_EW, [R("dx1"), R("dxb"), R("dx2")], [TD]))  # dx2 of the block below
+    for n in b.params:
+        g = n.replace(".A", ".dA").replace(".B", ".dB")
+        E(ins(ADAMW, [R(n), R(g), R("m_" + n), R("v_" + n)], [b.arrays[n].size, 0]))
+    train = b.train
+    eval_ = [w[:2] + struct.pack("<H", struct.unpack_from("<H", w, 2)[0] & ~FLAG_RELAXED) + w[4:]
+             for w in train[:n_eval]]
+    persist = bytearray(persistent)
+    for n in b.params:
+        off, nb = b.ar.names[n]
+        persist[off:off + nb] = b.arrays[n].tobytes()
+    rodata = bytearray(b.ro.size)
+    view = memoryview(rodata)
+    for n, (off, nb) in b.ro.names.items():
+        view[off:off + nb] = b.arrays[n].reshape(-1).view(np.uint8)
+    del view
+    header = {n: 0 for n in HEADER_NAMES}
+    header.update(
+        magic=SEEU_MAGIC, version=SEEU_VERSION, arena_size=b.ar.size, persistent_size=persistent,
+        input_ref=R("tokens"), input_floats=T, label_ref=R("labels"), label_bytes=T * 4,
+        label_kind=1, optimizer_kind=1, loss_ref=R("loss"), lr=lr, beta1=0.9, beta2=0.999,
+        eps=1e-8, weight_decay=weight_decay, batch=T, default_steps=default_steps,
+        input_kind=1, seq_len=seq)
+    blob = assemble(header, train, eval_, [], [], bytes(persist), rodata, self_hash)
     return PlanImage(blob=blob, header=parse_header(blob), arena=dict(b.ar.names),
                      rodata=dict(b.ro.names), train=train, eval=eval_, merge=[], arrays=b.arrays)

@@ -149,6 +149,43 @@ def test_relaxed_gemms_on_bf16_mfma(hip, orc, backend, M, N, K):
     assert bits_equal(gpu, again)
 
 
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (129, 260, 132), (200, 300, 4100),
+                                   (512, 384, 640), (100, 68, 72)])
+def test_relaxed_q8_gemms_on_bf16_mfma(hip, orc, backend, M, N, K):
+    """kFlagRelaxed int8-weight products (the frozen int8 base of a q8 plan)
+    on bf16 MFMA: the levels are exact in bf16, A is rounded once after the
+    per-tensor or k-scale multiplies it, the NN column scale multiplies the
+    finished dot.  Against the exact result at 2e-2; repeatable bit for bit."""
+    r = rng(M * 13 + N * 5 + K)
+    A = r.standard_normal((M, K)).astype(np.float32)
+    Wq = r.integers(-127, 128, (K, N)).astype(np.int8)
+    Wqt = r.integers(-127, 128, (N, K)).astype(np.int8)
+    cs = r.uniform(1e-3, 5e-2, N).astype(np.float32)
+    ks = r.uniform(1e-3, 5e-2, K).astype(np.float32)
+    ar = Arena()
+    a = ar.add("A", A)
+    wq, wqt = ar.add("Wq", Wq, rodata=True), ar.add("Wqt", Wqt, rodata=True)
+    csr, ksr = ar.add("cs", cs, rodata=True), ar.add("ks", ks, rodata=True)
+    names = ["q8", "q8cs", "q8nt", "q8ntks"]
+    o = {n: ar.empty(n, (M, N)) for n in names}
+    from tests.plan_ops import ins
+    rx = 1 << 5
+    prog = [
+        ins(29, [a, wq, o["q8"], f32_bits(0.013)], [M, N, K], flags=rx | (1 << 1)),
+        ins(29, [a, wq, o["q8cs"], csr], [M, N, K], flags=rx | (1 << 4) | (3 << 1)),
+        ins(30, [a, wqt, o["q8nt"], f32_bits(0.021)], [M, N, K], flags=rx),
+        ins(30, [a, wqt, o["q8ntks"], ksr], [M, N, K], flags=rx | (1 << 4)),
+    ]
+    before = backend.relaxed_executions()
+    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    assert backend.relaxed_executions() - before == len(prog)
+    for name in names:
+        e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
+        assert e <= TOL_BF16, f"{name} {M}x{N}x{K}: max-rel {e:.3g}"
+    _, again = execute(hip, orc, backend, ar, prog)
+    assert bits_equal(gpu, again)
+
+
 @pytest.mark.parametrize("M,N,K", [(3, 5, 7), (67, 129, 66), (131, 517, 203), (32, 512, 256),
                                    (2, 700, 900)])
 def test_gemm_narrow_weights(hip, orc, backend, M, N, K):

@@ -226,3 +226,104 @@ def test_decoder_first_step_through_the_oracle(orc, dec):
     labels = np.roll(toks, -1)
     loss = eng.train_step(toks.view(np.float32), labels)
     assert abs(loss - math.log(TINY["vocab"])) < 0.05
+
+
+# --- the int8-base decoder plan (BASELINE configs[4] at a small shape) ------------------------------
+
+TINY_Q8 = dict(vocab=96, dim=128, heads=2, ffn=352, layers=2, seq=64, batch=2, rank=16)
+
+
+@pytest.fixture(scope="module")
+def dq8(hip):
+    return pw.decoder_q8_lora(hip.plan_self_hash, **TINY_Q8)
+
+
+def test_quantize_cols_follows_the_reference_packing_rule():
+    """arena_binder.cc:129-177: scale = max|w| / 127 per column (1 for a zero
+    column, FLT_MIN for a subnormal quotient); level = clamp(round(w / s),
+    -127, 127) with halves away from zero."""
+    tiny = np.float32(np.finfo(np.float32).tiny)
+    u = 2.0 ** -7  # column 0's scale exactly: max |w| = 127 u
+    w = np.array([[127 * u, 0.0, 3e-38],
+                  [0.5 * u, 0.0, -1.2e-38],
+                  [-1.5 * u, 0.0, 0.0],
+                  [2.5 * u, 0.0, 0.0]], np.float32)
+    levels, sc = pw.quantize_cols(w)
+    assert sc[0] == np.float32(u) and sc[1] == 1.0 and sc[2] == tiny
+    assert list(levels[:, 0]) == [127, 1, -2, 3]   # halves away from zero, not to even
+    assert list(levels[:, 1]) == [0, 0, 0, 0]      # an all-zero column
+    assert list(levels[:, 2]) == [3, -1, 0, 0]     # subnormal max / 127: the FLT_MIN scale
+    # brute force on random columns against a plain-Python restatement
+    r = np.random.default_rng(3).standard_normal((37, 11)).astype(np.float32) * 0.02
+    lv, s2 = pw.quantize_cols(r)
+    for j in range(r.shape[1]):
+        m = max(abs(float(x)) for x in r[:, j])
+        assert s2[j] == np.float32(np.float32(m) / np.float32(127.0))
+        for i in range(r.shape[0]):
+            x = float(np.float32(r[i, j] / s2[j]))
+            want = math.floor(abs(x) + 0.5) * (1 if x >= 0 else -1)
+            assert lv[i, j] == max(-127, min(127, want))
+
+
+def test_q8_decoder_plan_structure(hip, dq8):
+    assert hip.plan_check(dq8.blob) == ""
+    ops = [struct.unpack_from("<HH", w) for w in dq8.train]
+    opc = [o for o, _ in ops]
+    L = TINY_Q8["layers"]
+    # Q, K, V, O adapted in every block; gate, up, down on the int8 base
+    assert opc.count(29) == L * 7                       # NN q8: q, k, v, o, gate, up, down
+    assert opc.count(30) == L * 4 + (L - 1) * 3         # NT q8: down, gate, up, o; q, k, v above 0
+    assert opc.count(47) == L and opc.count(48) == L and opc.count(49) == L and opc.count(50) == L
+    assert opc.count(31) == 2 * L + 1 and opc.count(32) == 1 + L + (L - 1)  # no norm dX below block 0
+    assert opc.count(24) == L and opc.count(25) == L and opc.count(21) == 3 * L
+    assert opc.count(18) == L * 4 * 2                   # AdamW on A and B of four sites
+    n_params = sum(dq8.arrays[n].size for n in dq8.arrays if ".A" in n or ".B" in n)
+    assert n_params == L * 4 * 2 * TINY_Q8["dim"] * TINY_Q8["rank"]
+    for w, (op, flags) in zip(dq8.train, ops):
+        ins4 = struct.unpack_from("<4Q", w, 8)
+        if op in (29, 30):
+            assert flags & (1 << 4) and flags & (1 << 5)
+            lv, sc = ins4[1], ins4[3]
+            assert lv >> 63 and sc >> 63
+            # the scales sit right after the levels (arena_binder.cc:283-287)
+            name = next(n for n, (off, _) in dq8.rodata.items() if off == (lv & ~(1 << 63)))
+            off, nb = dq8.rodata[name]
+            assert (sc & ~(1 << 63)) == (off + nb + 3) // 4 * 4
+        if op in (1, 2, 3) and not any(r >> 63 for r in ins4[:2]):
+            assert not flags & (1 << 5), "an adapter product carries the relaxed flag"
+    # adjacent dQ, dK, dV per block: the backward pair fuses
+    idx = [i for i, o in enumerate(opc) if o == 48]
+    assert all(opc[i + 1] == 49 and opc[i + 2] == 50 for i in idx)
+    for e, t in zip(dq8.eval, dq8.train):
+        assert e[:2] == t[:2] and e[4:] == t[4:]
+        assert not struct.unpack_from("<H", e, 2)[0] & (1 << 5)
+    assert struct.unpack_from("<H", dq8.eval[-1])[0] == 11
+    # the packed levels are the quantizer applied to the generated weights
+    lv, sc = pw.quantize_cols(pw.normal(20261205 + ord("q"), (TINY_Q8["dim"], TINY_Q8["dim"]), 0.02))
+    assert np.array_equal(dq8.arrays["l0.wq"], lv) and np.array_equal(dq8.arrays["l0.wq.s"], sc)
+
+
+def test_q8_decoder_first_step_through_the_oracle(orc, dq8):
+    eng = OracleEngine(orc, dq8.blob)
+    T = TINY_Q8["batch"] * TINY_Q8["seq"]
+    toks = pw.uniform_ints(12, T, TINY_Q8["vocab"])
+    labels = np.roll(toks, -1)
+    loss = eng.train_step(toks.view(np.float32), labels)
+    assert abs(loss - math.log(TINY_Q8["vocab"])) < 0.1
+    loss2 = eng.train_step(toks.view(np.float32), labels)
+    assert loss2 < loss  # the adapters learned from the first step
+
+
+def test_plan_generator_matches_its_numpy_definition():
+    """The threaded C++ generator (plangen.cc) gives the numpy definitions'
+    bytes: normals (SplitMix64 -> Box-Muller in double) and int8 packing."""
+    assert pw._gen() is not None, "libseeai_plangen.so is not built"
+    for seed, shape, std in [(5, (513, 771), 0.02), (2 ** 63 + 11, (300001,), 2.0), (7, (3, 5), 0.5)]:
+        a, b = pw.normal(seed, shape, std), pw.normal_numpy(seed, shape, std)
+        assert a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    w = pw.normal(9, (700, 333), 0.02)
+    w[:, 5] = 0.0
+    w[:, 7] *= 1e-38
+    l1, s1 = pw.quantize_cols(w)
+    l2, s2 = pw.quantize_cols_numpy(w)
+    assert np.array_equal(l1, l2) and np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
