@@ -27,6 +27,8 @@
 // current one accumulates.  Every output has one writer.  The chains are
 // VALU multiply-adds (two operations per product), which bounds the kernel
 // at half the non-packed f32 VALU rate.
+#include <cstdlib>
+
 #include "common.h"
 
 namespace seeai {
@@ -478,7 +480,163 @@ __global__ void __launch_bounds__(kThreads) LongKFoldKernel(GemmArgs g, unsigned
   g.C[o] = Epilogue(g, m, n, c);
 }
 
+// ---------------------------------------------------------------------------
+// Long reductions over a few hundred thousand outputs or fewer (the LoRA
+// products t = X A, dt = dC B^T and the adapter gradients dA = X^T dt,
+// dB = t^T dC): one output per lane, BM x BN = 256 outputs per workgroup,
+// so the grid has M N / 256 workgroups where the tiled kernel would have
+// M N / 4096.  K walks in chunks of kChainK through LDS, stored k-contiguous
+// per row (As[m][k], Bs[n][k]) so a lane reads a quad of A and of B as one
+// 16-byte read each; the next chunk's loads are in flight while the lanes
+// run their chains.  The chains are the tiled kernel's: quads from k = 0
+// then the K % 4 tail (NN / TN / AccNN), or eight lanes by k mod 8 added
+// in lane order then alpha (NT).
+// ---------------------------------------------------------------------------
+constexpr int kChainK = 32, kChainLd = kChainK + 4;
+
+template <int kLayout, int kBKind, int BM, int BN>
+__global__ void __launch_bounds__(kThreads) GemmChainKernel(GemmArgs g) {
+  static_assert(BM * BN == kThreads, "one output per lane");
+  constexpr bool kNT = kLayout == 1;
+  constexpr int kAPer = BM * kChainK / kThreads, kBPer = BN * kChainK / kThreads;
+  __shared__ __attribute__((aligned(16))) float As[BM][kChainLd];
+  __shared__ __attribute__((aligned(16))) float Bs[BN][kChainLd];
+  const int tid = threadIdx.x;
+  const int mi = tid / BN, ni = tid % BN;
+  const size_t m0 = static_cast<size_t>(blockIdx.y) * BM, n0 = static_cast<size_t>(blockIdx.x) * BN;
+  const size_t M = g.M, N = g.N, K = g.K;
+  // Element e of a chunk: A's (mm, kk) with the contiguous index fastest.
+  auto a_of = [&](int e, int& mm, int& kk) {
+    if constexpr (kLayout == 2) {  // A[K, M]
+      kk = e / BM;
+      mm = e % BM;
+    } else {                       // A[M, K]
+      mm = e / kChainK;
+      kk = e % kChainK;
+    }
+  };
+  auto b_of = [&](int e, int& nn, int& kk) {
+    if constexpr (kNT) {           // B[N, K]
+      nn = e / kChainK;
+      kk = e % kChainK;
+    } else {                       // B[K, N]
+      kk = e / BN;
+      nn = e % BN;
+    }
+  };
+  float ra[kAPer], rb[kBPer];
+  auto load = [&](size_t k0) {
+#pragma unroll
+    for (int r = 0; r < kAPer; ++r) {
+      int mm, kk;
+      a_of(tid + r * kThreads, mm, kk);
+      const size_t m = m0 + mm, k = k0 + kk;
+      ra[r] = (m < M && k < K) ? LoadA<kLayout>(g, m, k) : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < kBPer; ++r) {
+      int nn, kk;
+      b_of(tid + r * kThreads, nn, kk);
+      const size_t n = n0 + nn, k = k0 + kk;
+      rb[r] = (n < N && k < K) ? LoadB<kLayout, kBKind>(g.B, N, K, n, k, g.b_col_scale) : 0.0f;
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int r = 0; r < kAPer; ++r) {
+      int mm, kk;
+      a_of(tid + r * kThreads, mm, kk);
+      As[mm][kk] = ra[r];
+    }
+#pragma unroll
+    for (int r = 0; r < kBPer; ++r) {
+      int nn, kk;
+      b_of(tid + r * kThreads, nn, kk);
+      Bs[nn][kk] = rb[r];
+    }
+  };
+  const size_t m = m0 + mi, n = n0 + ni;
+  const bool live = m < M && n < N;
+  float c = (live && g.accumulate) ? g.C[m * N + n] : 0.0f;
+  float lane[kNT ? 8 : 1];
+#pragma unroll
+  for (int l = 0; l < (kNT ? 8 : 1); ++l) lane[l] = 0.0f;
+  load(0);
+  for (size_t k0 = 0; k0 < K; k0 += kChainK) {
+    __syncthreads();  // the previous chunk's reads are done
+    store();
+    __syncthreads();
+    if (k0 + kChainK < K) load(k0 + kChainK);
+    const int kn = K - k0 < static_cast<size_t>(kChainK) ? static_cast<int>(K - k0) : kChainK;
+    const float* ar = As[mi];
+    const float* br = Bs[ni];
+    if (kn == kChainK) {
+#pragma unroll
+      for (int kk = 0; kk < kChainK; kk += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(ar + kk);
+        const float4 b = *reinterpret_cast<const float4*>(br + kk);
+        if constexpr (kNT) {  // k0 is a multiple of 8: lane = kk % 8 + t
+          const int l = kk % 8;
+          lane[l] = Add(lane[l], Mul(a.x, b.x));
+          lane[l + 1] = Add(lane[l + 1], Mul(a.y, b.y));
+          lane[l + 2] = Add(lane[l + 2], Mul(a.z, b.z));
+          lane[l + 3] = Add(lane[l + 3], Mul(a.w, b.w));
+        } else {
+          c = Add(c, Add(Add(Add(Mul(a.x, b.x), Mul(a.y, b.y)), Mul(a.z, b.z)), Mul(a.w, b.w)));
+        }
+      }
+    } else if constexpr (kNT) {
+      for (int kk = 0; kk < kn; ++kk)
+#pragma unroll
+        for (int l = 0; l < 8; ++l)
+          if ((kk & 7) == l) lane[l] = Add(lane[l], Mul(ar[kk], br[kk]));
+    } else {
+      const int kq = kn & ~3;
+      for (int kk = 0; kk < kq; kk += 4)
+        c = Add(c, Add(Add(Add(Mul(ar[kk], br[kk]), Mul(ar[kk + 1], br[kk + 1])),
+                           Mul(ar[kk + 2], br[kk + 2])),
+                       Mul(ar[kk + 3], br[kk + 3])));
+      for (int kk = kq; kk < kn; ++kk) c = Add(c, Mul(ar[kk], br[kk]));  // the K % 4 tail
+    }
+  }
+  if (!live) return;
+  if constexpr (kNT) {
+    c = lane[0];
+#pragma unroll
+    for (int l = 1; l < 8; ++l) c = Add(c, lane[l]);
+    c = Mul(g.alpha_dot, c);
+  }
+  g.C[m * N + n] = Epilogue(g, m, n, c);
+}
+
+// The chain kernel where the tiled kernel's grid would be small for the
+// reduction it carries: under 512 tiles of 64 x 64 and K above the panel.
+bool Chain(const GemmArgs& a) {
+  const size_t tiles = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+  return a.K > static_cast<size_t>(kPanelK) && tiles < 512;
+}
+
+template <int kLayout, int kBKind, int BM, int BN>
+hipError_t LaunchChain(const GemmArgs& a, hipStream_t s) {
+  const size_t gy = (a.M + BM - 1) / BM, gx = (a.N + BN - 1) / BN;
+  if (gy > 65535 || gx > (size_t{1} << 31)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((GemmChainKernel<kLayout, kBKind, BM, BN>),
+                     dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)), dim3(kThreads), 0,
+                     s, a);
+  return hipGetLastError();
+}
+
 bool LongK(const GemmArgs& a) { return a.layout != 1 && a.M * a.N <= 16384 && a.K >= 1024; }
+
+// Where both apply, the two-pass workspace form runs before the chain
+// kernel unless SEEAI_EXACT_LONGK=0 (a same-session comparison switch).
+bool LongKFirst() {
+  static const bool first = [] {
+    const char* e = std::getenv("SEEAI_EXACT_LONGK");
+    return !(e && e[0] == '0');
+  }();
+  return first;
+}
 
 template <int kLayout, int kBKind>
 hipError_t Run(const GemmArgs& a, hipStream_t s) {
@@ -487,6 +645,11 @@ hipError_t Run(const GemmArgs& a, hipStream_t s) {
     const size_t lds = 2 * 16 * a.K * sizeof(float);
     hipLaunchKernelGGL((GemmPanelKernel<kLayout, kBKind>), grid, dim3(kThreads), lds, s, a);
     return hipGetLastError();
+  }
+  if (Chain(a) && !(kLayout != 1 && LongK(a) && a.scratch && LongKFirst())) {
+    if (a.N <= 8) return LaunchChain<kLayout, kBKind, 32, 8>(a, s);
+    if (a.M <= 8) return LaunchChain<kLayout, kBKind, 8, 32>(a, s);
+    return LaunchChain<kLayout, kBKind, 16, 16>(a, s);
   }
   if constexpr (kLayout != 1) {
     if (LongK(a) && a.scratch) {

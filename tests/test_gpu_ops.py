@@ -31,7 +31,10 @@ GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 
                (131, 517, 203), (8, 1100, 300), (2, 700, 900), (257, 33, 64), (66, 131, 65),
                (32, 512, 256), (32, 8, 256), (32, 512, 8), (8, 256, 32), (512, 8, 32),
                # the decoder steps' long reductions: LoRA dA / dB over 8192 tokens
-               (768, 8, 8192), (8, 768, 8192)]
+               (768, 8, 8192), (8, 768, 8192),
+               # few outputs over long K: the chain kernel (one output per lane),
+               # ragged chunks and a K % 4 tail
+               (1040, 16, 2050), (8200, 8, 600), (16, 1030, 1000)]
 
 
 @pytest.fixture(scope="module")
