@@ -13,8 +13,11 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <map>
 #include <string>
+#include <tuple>
 
 #include "../../include/seeai_hip.h"
 #include "common.h"
@@ -88,7 +91,11 @@ struct seeai_ctx {
   uint64_t prog_count = 0, range_end = 0;
   const uint8_t* done = nullptr;  // the next instruction, already run by a fused dispatch
   int allow_fusion = 1;
+  int allow_dma = 1;  // relaxed frozen-weight GEMMs on the bf16 shadow path
   uint64_t fused = 0;
+  // bf16 copies [N, Kp] of frozen weights for the relaxed GEMMs, keyed by
+  // (weight, layout, kind, N, K); valid until the next bind.
+  std::map<std::tuple<const void*, int, int, uint64_t, uint64_t>, void*> shadows;
   std::string err;
 
   int* flag() { return reinterpret_cast<int*>(small); }
@@ -168,8 +175,42 @@ int AdamWLaunch(seeai_ctx* c, float* p, const float* g, float* m, float* v, uint
   return SEEAI_OK;
 }
 
+void DropShadows(seeai_ctx* c) {
+  for (auto& kv : c->shadows) (void)hipFree(kv.second);
+  c->shadows.clear();
+}
+
+// Memory no instruction writes between binds: the rodata and source images.
+bool Immutable(const seeai_ctx* c, const void* p) {
+  const auto* q = static_cast<const uint8_t*>(p);
+  return (c->rodata && q >= c->rodata && q < c->rodata + c->rodata_bytes) ||
+         (c->source && q >= c->source && q < c->source + c->source_bytes);
+}
+
+// The relaxed frozen-weight product on the bf16 direct-to-LDS kernel: the
+// weight's bf16 shadow (made once), A rounded into the workspace with its
+// scales, then the GEMM and its epilogue.
+int GemmBf16Dma(seeai_ctx* c, GemmArgs& a, const char* what) {
+  const auto key = std::make_tuple(a.B, a.layout, a.b_kind, static_cast<uint64_t>(a.N),
+                                   static_cast<uint64_t>(a.K));
+  void* shadow = nullptr;
+  if (auto it = c->shadows.find(key); it != c->shadows.end()) {
+    shadow = it->second;
+  } else {
+    SEEAI_TRY(c, hipMalloc(&shadow, a.N * Bf16DmaKp(a.K) * 2), "weight shadow alloc");
+    c->shadows[key] = shadow;
+    SEEAI_TRY(c, LaunchWeightShadow(a, shadow, c->stream), "weight shadow");
+  }
+  void* ws;
+  if (int rc = Scratch(c, a.M * Bf16DmaKp(a.K) * 2, &ws)) return rc;
+  SEEAI_TRY(c, LaunchConvertRowsBf16(a.A, a.M, a.K, a.alpha_a, a.a_k_scale, ws, c->stream), what);
+  SEEAI_TRY(c, LaunchGemmBf16Dma(ws, shadow, a, c->stream), what);
+  return SEEAI_OK;
+}
+
 // A GEMM launch with the workspace its kernel may use.
 int Gemm(seeai_ctx* c, GemmArgs& a, const char* what) {
+  if (a.relaxed && c->allow_dma && Bf16DmaFits(a) && Immutable(c, a.B)) return GemmBf16Dma(c, a, what);
   if (const size_t bytes = a.relaxed ? 0 : GemmExactScratchBytes(a)) {
     void* ws;
     if (int rc = Scratch(c, bytes, &ws)) return rc;
@@ -615,6 +656,9 @@ int seeai_create(int device, seeai_ctx** out) {
   if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) return SEEAI_HIP_ERROR;
   auto* c = new seeai_ctx();
   c->device = device;
+  // SEEAI_RELAXED_DMA=0 keeps the relaxed frozen-weight GEMMs on the
+  // register-staged kernel (a same-session comparison switch).
+  if (const char* e = std::getenv("SEEAI_RELAXED_DMA"); e && e[0] == '0') c->allow_dma = 0;
   int rc = Hip(c, hipSetDevice(device), "set device");
   if (rc == SEEAI_OK) rc = Hip(c, hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "stream");
   if (rc == SEEAI_OK) rc = Hip(c, hipMalloc(&c->small, kSmallBytes), "small alloc");
@@ -637,6 +681,7 @@ void seeai_destroy(seeai_ctx* c) {
   if (c->rodata) (void)hipFree(c->rodata);
   if (c->source) (void)hipFree(c->source);
   if (c->scratch) (void)hipFree(c->scratch);
+  DropShadows(c);
   if (c->small) (void)hipFree(c->small);
   if (c->host_flag) (void)hipHostFree(c->host_flag);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
@@ -676,6 +721,7 @@ int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t 
     if (ro) (void)hipFree(ro);
     return Hip(c, e, "bind");
   }
+  DropShadows(c);  // made from the old rodata
   if (c->arena) (void)hipFree(c->arena);
   if (c->rodata) (void)hipFree(c->rodata);
   c->arena = arena;
@@ -688,6 +734,7 @@ int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t 
 int seeai_bind_source(seeai_ctx* c, const void* data, uint64_t bytes) {
   if (!c) return SEEAI_INVALID;
   SEEAI_TRY(c, hipStreamSynchronize(c->stream), "bind_source drain");
+  DropShadows(c);  // some may be of the old source image
   if (c->source) (void)hipFree(c->source);
   c->source = nullptr;
   c->source_bytes = 0;

@@ -220,6 +220,15 @@ hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s);
 hipError_t LaunchGemmExact(const GemmArgs& a, hipStream_t s);
 // Workspace the exact kernels can use for this GEMM (0: none).
 size_t GemmExactScratchBytes(const GemmArgs& a);
+// Relaxed NN / NT on bf16 operands staged by direct-to-LDS loads
+// (k_gemm_bf16dma.hip): A converted into a bf16 workspace [M, Kp] with its
+// scales, the weight's bf16 shadow [N, Kp] made once; Kp = K rounded up to 32.
+size_t Bf16DmaKp(size_t K);
+bool Bf16DmaFits(const GemmArgs& a);
+hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,
+                                 const float* kscale, void* out, hipStream_t s);
+hipError_t LaunchWeightShadow(const GemmArgs& a, void* out, hipStream_t s);
+hipError_t LaunchGemmBf16Dma(const void* A, const void* W, const GemmArgs& a, hipStream_t s);
 // Relaxed NN / NT with f32 or int8 weights on bf16 MFMA (k_gemm_bf16.hip),
 // when it fits.
 bool GemmBf16Fits(const GemmArgs& a);

@@ -1,0 +1,385 @@
+// k_gemm_bf16dma.hip -- the relaxed family's frozen-weight products
+// (kFlagRelaxed on kGemmNN / kGemmNT / kGemmNNQ8 / kGemmNTQ8,
+// source/plan/instruction.h:356-384) with both operands in bf16 in HBM,
+// staged into LDS by direct-to-LDS buffer loads.
+//
+// The relaxed family rounds the activations to bf16 once at the GEMM input
+// and takes the frozen weight in reduced precision:
+//   * ConvertRowsKernel writes A' [M, Kp] bf16 = RNE(alpha * (A * kscale))
+//     -- the per-tensor scale (NN) or alpha and the q8 k-scale (NT) multiply
+//     A before it rounds, as gemm.cc:626-674 places them -- zero past K;
+//   * ShadowKernel writes the weight once as W' [N, Kp] bf16 (K contiguous):
+//     f32 rounded, int8 levels and bf16 exactly; a weight in rodata or the
+//     source image cannot change until the next bind, so the launcher keeps
+//     the shadow and reuses it;
+//   * GemmBf16DmaKernel: a BM x BN tile per workgroup of WGM x WGN waves, each
+//     a (BM/WGM) x (BN/WGN) block of v_mfma_f32_32x32x16_bf16 accumulators.
+//     K moves 64 bytes (32 bf16) per stage through kStages LDS buffers filled
+//     by buffer_load ... lds; kStages - 1 stages are in flight while one is
+//     multiplied, one barrier per stage.  LDS rows are 64 bytes, four 16-byte
+//     chunks; chunk c of row r sits at physical chunk (c + r/4) mod 4, which
+//     keeps the fragment reads (lane l: row l % 32, chunk 2ks + l / 32) free
+//     of bank conflicts.  The epilogue (NN column scale, alpha, addend,
+//     accumulate, bias, activation -- the exact family's order) runs on rows
+//     staged through LDS so C leaves in row-contiguous 16-byte stores.
+// Rows past M or N read as zeros through the buffer range check; Kp is K
+// rounded up to 32.
+#include <cstdint>
+
+#include "common.h"
+
+namespace seeai {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+constexpr int kRowBytes = 64;             // K bytes of one row per stage (32 bf16)
+constexpr int kChunks = kRowBytes / 16;   // 16-byte chunks per staged row
+constexpr int kRsrcWord3 = 0x00020000;    // raw buffer, out-of-range reads give 0
+
+__device__ __forceinline__ int Phys(int row, int c) { return (c + row / 4) & 3; }
+
+// s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void WaitVm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+// Tile -> workgroup order: the 8 XCDs each take a contiguous run of tiles
+// (workgroup b runs on XCD b % 8) walked column-major in bands of kGroupM
+// row tiles, so concurrent tiles of one XCD share A row panels and W column
+// panels in its L2.
+constexpr int kGroupM = 4;
+__device__ __forceinline__ void TileOf(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int ntiles = tiles_m * tiles_n;
+  int t = b;
+  if (ntiles % 8 == 0) t = (b % 8) * (ntiles / 8) + b / 8;
+  const int per_group = kGroupM * tiles_n;
+  const int g = t / per_group;
+  const int first_m = g * kGroupM;
+  const int rows = min(tiles_m - first_m, kGroupM);
+  const int off = t % per_group;
+  tm = first_m + off % rows;
+  tn = off / rows;
+}
+
+__device__ __forceinline__ float ActF(int act, float v) { return act ? ActExpr(act, v) : v; }
+
+template <int BM, int BN, int WGM, int WGN, int kStages>
+__global__ void __launch_bounds__(WGM * WGN * kWave)
+GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, int Kp, GemmArgs g) {
+  constexpr int kWaves = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int kRowsPerLoad = kWave / kChunks;           // 16 rows per wave-load
+  constexpr int kLoadsA = BM / kRowsPerLoad / kWaves;     // wave-loads per stage, per wave
+  constexpr int kLoadsB = BN / kRowsPerLoad / kWaves;
+  static_assert(kLoadsA * kRowsPerLoad * kWaves == BM && kLoadsB * kRowsPerLoad * kWaves == BN,
+                "loads cover the tile");
+  static_assert(kLoadsA <= 4 && kLoadsB <= 4, "voff capacity");
+  constexpr int kStageA = BM * kRowBytes;
+  constexpr int kStage = (BM + BN) * kRowBytes;
+  constexpr int kPerStage = kLoadsA + kLoadsB;            // vmcnt units per stage
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
+
+  const int M = static_cast<int>(g.M), N = static_cast<int>(g.N);
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  int tm, tn;
+  TileOf(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kb = Kp * 2;  // row bytes
+
+  // Ranges cover this tile's rows only: offsets stay below BM * kb.
+  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__bf16*>(A) + static_cast<size_t>(m0) * Kp, 0, Uniform(min(M - m0, BM) * kb),
+      kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__bf16*>(W) + static_cast<size_t>(n0) * Kp, 0, Uniform(min(N - n0, BN) * kb),
+      kRsrcWord3);
+  // This lane's slot in a wave-load: row rbase + lane / 4, physical chunk
+  // lane % 4, which holds logical chunk (p - r/4) mod 4.
+  int voff_a[4], voff_b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int ra = (j * kWaves + wave) * kRowsPerLoad + lane / kChunks;
+    voff_a[j] = ra * kb + ((lane % kChunks - ra / 4) & 3) * 16;
+    voff_b[j] = voff_a[j];
+  }
+  auto issue = [&](int st, int buf) {
+    uint8_t* sA = smem + buf * kStage;
+    uint8_t* sB = sA + kStageA;
+    const int k0 = st * kRowBytes;
+#pragma unroll
+    for (int j = 0; j < kLoadsA; ++j) {
+      const int rbase = Uniform((j * kWaves + wave) * kRowsPerLoad);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (LdsPtr)(sA + rbase * kRowBytes), 16,
+                                               voff_a[j], k0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < kLoadsB; ++j) {
+      const int rbase = Uniform((j * kWaves + wave) * kRowsPerLoad);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, (LdsPtr)(sB + rbase * kRowBytes), 16,
+                                               voff_b[j], k0, 0, 0);
+    }
+  };
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = v16f{};
+
+  const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
+  const int lr = lane % 32, h = lane / 32;
+  const int frag0 = lr * kRowBytes + Phys(lr, h) * 16;
+  const int frag1 = lr * kRowBytes + Phys(lr, 2 + h) * 16;
+
+  const int nsteps = Kp / 32;
+  bf16x8 fa[2][TM], fb[2][TN];
+  auto read = [&](int buf, int fo, int slot) {
+    const uint8_t* sA = smem + buf * kStage;
+    const uint8_t* sB = sA + kStageA;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      fa[slot][i] = *reinterpret_cast<const bf16x8*>(sA + (wm + i * 32) * kRowBytes + fo);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      fb[slot][j] = *reinterpret_cast<const bf16x8*>(sB + (wn + j * 32) * kRowBytes + fo);
+  };
+  auto mfmas = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j],
+                                                            0, 0, 0);
+  };
+  // The next k-step's TM + TN LDS reads spread one per MFMA; after the
+  // barrier the stage's loads take the last MFMA slots.
+  auto interleave = [&]() {
+#pragma unroll
+    for (int s = 0; s < TM + TN; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int s = TM + TN; s < TM * TN; ++s) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  };
+  auto interleave_loads = [&]() {
+#pragma unroll
+    for (int s = 0; s < TM * TN; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (s < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (s >= TM * TN - kPerStage) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+  };
+  static_assert(TM * TN >= TM + TN && TM * TN >= kPerStage, "MFMA slots for the reads and loads");
+
+  // Every iteration loads one stage; past the last the loads repeat it (in
+  // bounds, into a buffer no later stage uses), so the stages in flight at
+  // each barrier are always kStages - 3.
+  const int last = nsteps - 1;
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s) issue(min(s, last), s);
+  WaitVm<(kStages - 2) * kPerStage>();
+  __builtin_amdgcn_s_barrier();
+  read(0, frag0, 0);
+  for (int it = 0; it < last; ++it) {
+    const int buf = it % kStages;
+    read(buf, frag1, 1);
+    mfmas(0);
+    interleave();
+    WaitVm<(kStages - 3) * kPerStage>();
+    __builtin_amdgcn_s_barrier();
+    issue(min(it + kStages - 1, last), (it + kStages - 1) % kStages);
+    read((it + 1) % kStages, frag0, 0);
+    mfmas(1);
+    interleave_loads();
+  }
+  read(last % kStages, frag1, 1);
+  mfmas(0);
+  interleave();
+  mfmas(1);
+  WaitVm<0>();
+  __syncthreads();  // every wave is done with the stage buffers: reuse them for staging
+
+  // Epilogue through this wave's 32 x WN slice of LDS, 32 rows at a time.
+  constexpr int SLD = WN + 4;
+  static_assert(kWaves * 32 * SLD * 4 <= kStages * kStage, "staging fits in LDS");
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
+  const bool vec = (N % 4) == 0;
+  const float alpha = g.alpha_dot;
+  const float* __restrict__ cs = g.b_col_scale;
+  const float* __restrict__ add = g.addend;
+  const float* __restrict__ bias = g.bias;
+  float* __restrict__ C = g.C;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int mb = m0 + wm + i * 32;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) stage[(8 * q + 4 * h + e) * SLD + j * 32 + lr] = acc[i][j][4 * q + e];
+    __builtin_amdgcn_wave_barrier();
+    constexpr int kVecRow = WN / 4;
+#pragma unroll
+    for (int t = 0; t < 32 * kVecRow / kWave; ++t) {
+      const int idx = lane + t * kWave;
+      const int row = idx / kVecRow, c4 = idx % kVecRow;
+      const int m = mb + row, n = n0 + wn + c4 * 4;
+      if (m >= M || n >= N) continue;
+      float v[4];
+      const float4 s4 = *reinterpret_cast<const float4*>(stage + row * SLD + c4 * 4);
+      v[0] = s4.x, v[1] = s4.y, v[2] = s4.z, v[3] = s4.w;
+      const size_t o = static_cast<size_t>(m) * N + n;
+      const int cnt = vec ? 4 : min(4, N - n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (e >= cnt) break;
+        float x = v[e];
+        if (cs) x = x * cs[n + e];
+        if (alpha != 1.0f) x = alpha * x;
+        if (add) x = add[o + e] + x;
+        if (g.accumulate) x = C[o + e] + x;
+        if (bias) x = x + bias[n + e];
+        v[e] = ActF(g.act, x);
+      }
+      if (vec) {
+        *reinterpret_cast<float4*>(C + o) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+        for (int e = 0; e < cnt; ++e) C[o + e] = v[e];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// A' [M, Kp] bf16 = RNE(alpha * (A[m, k] * kscale[k])), zero for k >= K;
+// one row per workgroup, eight elements per lane per pass.
+constexpr int kCvtThreads = 256;
+
+__global__ void __launch_bounds__(kCvtThreads)
+ConvertRowsKernel(const float* __restrict__ A, size_t K, size_t Kp, float alpha,
+                  const float* __restrict__ ks, __bf16* __restrict__ out) {
+  const size_t m = blockIdx.x;
+  const float* row = A + m * K;
+  __bf16* orow = out + m * Kp;
+  const bool vec = (K % 4) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  for (size_t k = static_cast<size_t>(threadIdx.x) * 8; k < Kp; k += kCvtThreads * 8) {
+    float x[8];
+    if (vec && k + 8 <= K) {
+      const float4 a = *reinterpret_cast<const float4*>(row + k);
+      const float4 b = *reinterpret_cast<const float4*>(row + k + 4);
+      x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = k + e < K ? row[k + e] : 0.0f;
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = x[e];
+      if (ks && k + e < K) v = v * ks[k + e];
+      if (alpha != 1.0f) v = alpha * v;
+      o[e] = static_cast<__bf16>(v);
+    }
+    *reinterpret_cast<bf16x8*>(orow + k) = o;
+  }
+}
+
+// W' [N, Kp] bf16 from the weight as the instruction reads it: NN's W[K, N]
+// (transposed through a 32 x 32 LDS tile) or NT's W[N, K]; f32 rounded
+// (RNE), int8 levels and bf16 exact; zero for k >= K.
+template <int kLayout, int kBKind>
+__global__ void __launch_bounds__(kCvtThreads)
+ShadowKernel(const void* __restrict__ W, size_t N, size_t K, size_t Kp, __bf16* __restrict__ out) {
+  __shared__ float tile[32][33];
+  const size_t k0 = static_cast<size_t>(blockIdx.x) * 32, n0 = static_cast<size_t>(blockIdx.y) * 32;
+  const int tx = threadIdx.x % 32, ty = threadIdx.x / 32;  // 32 x 8
+  auto src = [&](size_t n, size_t k) -> float {
+    const size_t idx = kLayout == 1 ? n * K + k : k * N + n;
+    if constexpr (kBKind == 0) return static_cast<const float*>(W)[idx];
+    else if constexpr (kBKind == 1) return static_cast<float>(static_cast<const int8_t*>(W)[idx]);
+    else return Bf16ToF32(static_cast<const uint16_t*>(W)[idx]);
+  };
+  for (int r = ty; r < 32; r += 8) {
+    // NN reads along n (coalesced in W[K, N]); NT along k.
+    const size_t n = kLayout == 1 ? n0 + r : n0 + tx, k = kLayout == 1 ? k0 + tx : k0 + r;
+    const float v = (n < N && k < K) ? src(n, k) : 0.0f;
+    if (kLayout == 1) tile[r][tx] = v;  // [n][k]
+    else tile[tx][r] = v;               // [n][k]
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const size_t n = n0 + r, k = k0 + tx;
+    if (n < N && k < Kp) out[n * Kp + k] = static_cast<__bf16>(tile[r][tx]);
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, int kStages>
+hipError_t Launch(const __bf16* A, const __bf16* W, size_t Kp, const GemmArgs& g, hipStream_t s) {
+  const size_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+  hipLaunchKernelGGL((GemmBf16DmaKernel<BM, BN, WGM, WGN, kStages>), dim3(static_cast<unsigned>(tiles)),
+                     dim3(WGM * WGN * kWave), 0, s, A, W, static_cast<int>(Kp), g);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t Bf16DmaKp(size_t K) { return (K + 31) / 32 * 32; }
+
+bool Bf16DmaFits(const GemmArgs& a) {
+  if (!a.relaxed || a.layout > 1 || a.b_kind > 2) return false;
+  if (a.M < 128 || a.N < 128 || a.K < 64) return false;
+  // NT over a short K measured faster on the register-staged kernel (the
+  // conversion pass costs more than it saves: 8192 x 768 x 768 and
+  // 8192 x 3072 x 768).
+  if (a.layout == 1 && a.K < 1024) return false;
+  const size_t Kp = Bf16DmaKp(a.K);
+  // 32-bit buffer offsets within a tile and int tile indices.
+  if (Kp * 2 * 256 >= (size_t{1} << 31) || a.M >= (size_t{1} << 30) || a.N >= (size_t{1} << 30))
+    return false;
+  return ((a.M + 127) / 128) * ((a.N + 127) / 128) < (size_t{1} << 31);
+}
+
+hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,
+                                 const float* kscale, void* out, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  hipLaunchKernelGGL(ConvertRowsKernel, dim3(static_cast<unsigned>(M)), dim3(kCvtThreads), 0, s, A, K,
+                     Bf16DmaKp(K), alpha, kscale, static_cast<__bf16*>(out));
+  return hipGetLastError();
+}
+
+hipError_t LaunchWeightShadow(const GemmArgs& a, void* out, hipStream_t s) {
+  const size_t Kp = Bf16DmaKp(a.K);
+  const dim3 grid(static_cast<unsigned>(Kp / 32), static_cast<unsigned>((a.N + 31) / 32));
+  __bf16* o = static_cast<__bf16*>(out);
+  switch (a.layout * 3 + a.b_kind) {
+    case 0: hipLaunchKernelGGL((ShadowKernel<0, 0>), grid, dim3(kCvtThreads), 0, s, a.B, a.N, a.K, Kp, o); break;
+    case 1: hipLaunchKernelGGL((ShadowKernel<0, 1>), grid, dim3(kCvtThreads), 0, s, a.B, a.N, a.K, Kp, o); break;
+    case 2: hipLaunchKernelGGL((ShadowKernel<0, 2>), grid, dim3(kCvtThreads), 0, s, a.B, a.N, a.K, Kp, o); break;
+    case 3: hipLaunchKernelGGL((ShadowKernel<1, 0>), grid, dim3(kCvtThreads), 0, s, a.B, a.N, a.K, Kp, o); break;
+    case 4: hipLaunchKernelGGL((ShadowKernel<1, 1>), grid, dim3(kCvtThreads), 0, s, a.B, a.N, a.K, Kp, o); break;
+    case 5: hipLaunchKernelGGL((ShadowKernel<1, 2>), grid, dim3(kCvtThreads), 0, s, a.B, a.N, a.K, Kp, o); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// 256 x 256 tiles (eight waves of 128 x 64) where they give at least one
+// tile per CU; otherwise 128 x 128 (four waves of 64 x 64).
+hipError_t LaunchGemmBf16Dma(const void* A, const void* W, const GemmArgs& a, hipStream_t s) {
+  const size_t Kp = Bf16DmaKp(a.K);
+  const auto* Ab = static_cast<const __bf16*>(A);
+  const auto* Wb = static_cast<const __bf16*>(W);
+  const size_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+  if (t256 >= 256) return Launch<256, 256, 2, 4, 4>(Ab, Wb, Kp, a, s);
+  return Launch<128, 128, 2, 2, 4>(Ab, Wb, Kp, a, s);
+}
+
+}  // namespace seeai

@@ -152,6 +152,24 @@ def test_relaxed_gemms_on_bf16_mfma(hip, orc, backend, M, N, K):
     assert bits_equal(gpu, again)
 
 
+def test_relaxed_gemm_weight_shadow_follows_rebind(hip, orc, backend):
+    """The relaxed frozen-weight GEMM keeps a bf16 copy of each rodata weight;
+    a new binding (new rodata, possibly at the same device address) must
+    not reuse the old copy."""
+    from tests.plan_ops import ins
+    M, N, K = 256, 384, 512
+    r = rng(4242)
+    for trial in range(3):
+        ar = Arena()
+        a = ar.add("A", r.standard_normal((M, K)).astype(np.float32))
+        b = ar.add("B", (r.standard_normal((K, N)) * 0.05).astype(np.float32), rodata=True)
+        c = ar.empty("C", (M, N))
+        prog = [ins(1, [a, b, c], [M, N, K], flags=1 << 5)]
+        cpu, gpu = execute(hip, orc, backend, ar, prog)
+        e = maxrel(ar.get(gpu, "C"), ar.get(cpu, "C"))
+        assert e <= TOL_BF16, f"trial {trial}: max-rel {e:.3g}"
+
+
 @pytest.mark.parametrize("M,N,K", [(64, 64, 64), (129, 260, 132), (200, 300, 4100),
                                    (512, 384, 640), (100, 68, 72)])
 def test_relaxed_q8_gemms_on_bf16_mfma(hip, orc, backend, M, N, K):
