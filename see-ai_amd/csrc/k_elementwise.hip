@@ -190,39 +190,58 @@ RmsNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
     dxr[c] = rs * (dyr[c] * g[c] - xr[c] * rs * rs * mgx);
 }
 
-// RoPE (attention.cc:103-174): one lane per (b, s, h) head segment, walking
-// the pairs in order with the reference's frequency recurrence, so every
-// angle is the reference's float; cos/sin are the device's.
+// RoPE (attention.cc:103-174): one lane per interleaved pair (c, c+1) of a
+// (b, s, h) head segment, so a wave moves 512 contiguous bytes in and out
+// (float2 where the operands are 8-byte aligned).  The rotation is the
+// reference's expression per pair.  Without a table the lane forms its
+// pair's frequency by the reference's recurrence from 1 (c/2 products of
+// `step`, rounded in order), so every angle is the reference's float;
+// cos/sin are the device's.
+template <bool kVec>
 __global__ void __launch_bounds__(kThreads)
 RopeKernel(const float* __restrict__ x, float* __restrict__ y, size_t B, size_t S, size_t H,
            size_t d, float step, const float* __restrict__ table, int backward) {
-  const size_t u = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (u >= B * S * H) return;
-  const size_t D = H * d, half = d / 2;
-  const size_t s = (u / H) % S;
-  const float* xr = x + (u / H) * D + (u % H) * d;
-  float* yr = y + (u / H) * D + (u % H) * d;
-  const float* row = table ? table + s * half * 2 : nullptr;
-  float freq = 1.0f;
-  for (size_t c = 0; c + 1 < d; c += 2) {
-    float cs, sn;
-    if (row) {
-      cs = row[c];
-      sn = row[c + 1];
-    } else {
-      const float theta = static_cast<float>(s) * freq;
-      cs = cosf(theta);
-      sn = sinf(theta);
-      freq *= step;
-    }
-    const float a = xr[c], b2 = xr[c + 1];
-    if (backward) {
-      yr[c] = a * cs + b2 * sn;
-      yr[c + 1] = -a * sn + b2 * cs;
-    } else {
-      yr[c] = a * cs - b2 * sn;
-      yr[c + 1] = a * sn + b2 * cs;
-    }
+  const size_t half = d / 2, n = B * S * H * half;
+  for (size_t u = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; u < n;
+       u += static_cast<size_t>(gridDim.x) * kThreads) {
+  const size_t p = u % half, seg = u / half;  // seg = (b s) H + h
+  const size_t s = (seg / H) % S;
+  const size_t at = seg * d + 2 * p;           // [B S, H d] row-major: seg * d
+  float cs, sn;
+  if (table) {
+    const float* row = table + s * half * 2 + 2 * p;
+    cs = row[0];
+    sn = row[1];
+  } else {
+    float freq = 1.0f;
+    for (size_t c = 0; c < p; ++c) freq *= step;
+    const float theta = static_cast<float>(s) * freq;
+    cs = cosf(theta);
+    sn = sinf(theta);
+  }
+  float a, b2;
+  if constexpr (kVec) {
+    const float2 v = *reinterpret_cast<const float2*>(x + at);
+    a = v.x;
+    b2 = v.y;
+  } else {
+    a = x[at];
+    b2 = x[at + 1];
+  }
+  float o0, o1;
+  if (backward) {
+    o0 = a * cs + b2 * sn;
+    o1 = -a * sn + b2 * cs;
+  } else {
+    o0 = a * cs - b2 * sn;
+    o1 = a * sn + b2 * cs;
+  }
+  if constexpr (kVec) {
+    *reinterpret_cast<float2*>(y + at) = make_float2(o0, o1);
+  } else {
+    y[at] = o0;
+    y[at + 1] = o1;
+  }
   }
 }
 
@@ -408,10 +427,15 @@ hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, con
 }
 hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
                       float step, const float* table, int backward, hipStream_t s) {
-  const size_t n = B * S * H;
+  const size_t n = B * S * H * (d / 2);
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(RopeKernel, dim3(GridFor(n, kThreads)), dim3(kThreads), 0, s, x, y, B, S, H,
-                     d, step, table, backward);
+  const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 7) == 0;
+  if (vec)
+    hipLaunchKernelGGL(RopeKernel<true>, dim3(GridFor(n, kThreads)), dim3(kThreads), 0, s, x, y, B,
+                       S, H, d, step, table, backward);
+  else
+    hipLaunchKernelGGL(RopeKernel<false>, dim3(GridFor(n, kThreads)), dim3(kThreads), 0, s, x, y, B,
+                       S, H, d, step, table, backward);
   return hipGetLastError();
 }
 hipError_t LaunchRopeTable(float* table, size_t S, size_t d, float step, hipStream_t s) {

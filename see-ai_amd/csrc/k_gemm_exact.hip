@@ -485,22 +485,28 @@ __global__ void __launch_bounds__(kThreads) LongKFoldKernel(GemmArgs g, unsigned
 // products t = X A, dt = dC B^T and the adapter gradients dA = X^T dt,
 // dB = t^T dC): one output per lane, BM x BN = 256 outputs per workgroup,
 // so the grid has M N / 256 workgroups where the tiled kernel would have
-// M N / 4096.  K walks in chunks of kChainK through LDS, stored k-contiguous
-// per row (As[m][k], Bs[n][k]) so a lane reads a quad of A and of B as one
-// 16-byte read each; the next chunk's loads are in flight while the lanes
-// run their chains.  The chains are the tiled kernel's: quads from k = 0
-// then the K % 4 tail (NN / TN / AccNN), or eight lanes by k mod 8 added
-// in lane order then alpha (NT).
+// M N / 4096.  K walks in chunks of kChainK through two LDS buffers, stored
+// k-contiguous per row (As[m][k], Bs[n][k]) so a lane reads a quad of A and
+// of B as one 16-byte read each.  With one output per lane there are few
+// waves to hide memory latency, so the loads run kChainDepth chunks ahead
+// of the chunk being reduced (a chunk of 256 holds more arithmetic than
+// one load round trip), in a ring of registers; one barrier per
+// chunk.  The chains are the tiled kernel's: quads from k = 0 then the
+// K % 4 tail (NN / TN / AccNN), or eight lanes by k mod 8 added in lane
+// order then alpha (NT).
 // ---------------------------------------------------------------------------
-constexpr int kChainK = 32, kChainLd = kChainK + 4;
+constexpr int kChainK = 128, kChainLd = kChainK + 4, kChainDepth = 2;
+
+// s_waitcnt vmcnt(0), the other counters untouched (gfx9 encoding).
+__device__ __forceinline__ void WaitVmAll() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
 
 template <int kLayout, int kBKind, int BM, int BN>
 __global__ void __launch_bounds__(kThreads) GemmChainKernel(GemmArgs g) {
   static_assert(BM * BN == kThreads, "one output per lane");
   constexpr bool kNT = kLayout == 1;
   constexpr int kAPer = BM * kChainK / kThreads, kBPer = BN * kChainK / kThreads;
-  __shared__ __attribute__((aligned(16))) float As[BM][kChainLd];
-  __shared__ __attribute__((aligned(16))) float Bs[BN][kChainLd];
+  __shared__ __attribute__((aligned(16))) float As[2][BM][kChainLd];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN][kChainLd];
   const int tid = threadIdx.x;
   const int mi = tid / BN, ni = tid % BN;
   const size_t m0 = static_cast<size_t>(blockIdx.y) * BM, n0 = static_cast<size_t>(blockIdx.x) * BN;
@@ -524,35 +530,67 @@ __global__ void __launch_bounds__(kThreads) GemmChainKernel(GemmArgs g) {
       nn = e % BN;
     }
   };
-  float ra[kAPer], rb[kBPer];
-  auto load = [&](size_t k0) {
+  // The ring holds the operands as loaded (A as floats, B as raw bits):
+  // a value the lane does not touch until it is stored needs no wait for
+  // its load.  Loads are branch-free (indices clamped into the operand; a
+  // branch around a load makes the compiler wait for every load at the
+  // join); out-of-range elements become zero at the store, where the scales
+  // (alpha, the q8 k- and column scales) and the widening also apply, in
+  // the order LoadA / LoadB apply them.
+  constexpr bool kKScale = kLayout == 1 && kBKind == 1;  // NT q8: k-scale on A
+  constexpr bool kColScale = kLayout != 1 && kBKind == 1;  // NN q8: column scale on B
+  float ra[kChainDepth][kAPer];
+  uint32_t rb[kChainDepth][kBPer];
+  auto load = [&](size_t k0, float* dra, uint32_t* drb) {
 #pragma unroll
     for (int r = 0; r < kAPer; ++r) {
       int mm, kk;
       a_of(tid + r * kThreads, mm, kk);
-      const size_t m = m0 + mm, k = k0 + kk;
-      ra[r] = (m < M && k < K) ? LoadA<kLayout>(g, m, k) : 0.0f;
+      const size_t m = min(m0 + mm, M - 1), k = min(k0 + kk, K - 1);
+      dra[r] = kLayout == 2 ? g.A[k * M + m] : g.A[m * K + k];
+    }
+#pragma unroll
+    for (int r = 0; r < kBPer; ++r) {
+      int nn, kk;
+      b_of(tid + r * kThreads, nn, kk);
+      const size_t n = min(n0 + nn, N - 1), k = min(k0 + kk, K - 1);
+      const size_t idx = kNT ? n * K + k : k * N + n;
+      if constexpr (kBKind == 0)
+        drb[r] = __float_as_uint(static_cast<const float*>(g.B)[idx]);
+      else if constexpr (kBKind == 1)
+        drb[r] = static_cast<uint32_t>(static_cast<int32_t>(static_cast<const int8_t*>(g.B)[idx]));
+      else
+        drb[r] = static_cast<const uint16_t*>(g.B)[idx];
+    }
+  };
+  auto store = [&](int buf, size_t k0, const float* sra, const uint32_t* srb) {
+#pragma unroll
+    for (int r = 0; r < kAPer; ++r) {
+      int mm, kk;
+      a_of(tid + r * kThreads, mm, kk);
+      const size_t k = k0 + kk;
+      float v = sra[r];
+      if constexpr (kKScale)
+        if (g.a_k_scale) v = Mul(v, g.a_k_scale[min(k, K - 1)]);
+      if (g.alpha_a != 1.0f) v = Mul(g.alpha_a, v);
+      As[buf][mm][kk] = (m0 + mm < M && k < K) ? v : 0.0f;
     }
 #pragma unroll
     for (int r = 0; r < kBPer; ++r) {
       int nn, kk;
       b_of(tid + r * kThreads, nn, kk);
       const size_t n = n0 + nn, k = k0 + kk;
-      rb[r] = (n < N && k < K) ? LoadB<kLayout, kBKind>(g.B, N, K, n, k, g.b_col_scale) : 0.0f;
-    }
-  };
-  auto store = [&]() {
-#pragma unroll
-    for (int r = 0; r < kAPer; ++r) {
-      int mm, kk;
-      a_of(tid + r * kThreads, mm, kk);
-      As[mm][kk] = ra[r];
-    }
-#pragma unroll
-    for (int r = 0; r < kBPer; ++r) {
-      int nn, kk;
-      b_of(tid + r * kThreads, nn, kk);
-      Bs[nn][kk] = rb[r];
+      float v;
+      if constexpr (kBKind == 0) {
+        v = __uint_as_float(srb[r]);
+      } else if constexpr (kBKind == 1) {
+        v = static_cast<float>(static_cast<int32_t>(srb[r]));
+        if constexpr (kColScale)
+          if (g.b_col_scale) v = Mul(v, g.b_col_scale[min(n, N - 1)]);
+      } else {
+        v = Bf16ToF32(static_cast<uint16_t>(srb[r]));
+      }
+      Bs[buf][nn][kk] = (n < N && k < K) ? v : 0.0f;
     }
   };
   const size_t m = m0 + mi, n = n0 + ni;
@@ -561,42 +599,78 @@ __global__ void __launch_bounds__(kThreads) GemmChainKernel(GemmArgs g) {
   float lane[kNT ? 8 : 1];
 #pragma unroll
   for (int l = 0; l < (kNT ? 8 : 1); ++l) lane[l] = 0.0f;
-  load(0);
-  for (size_t k0 = 0; k0 < K; k0 += kChainK) {
-    __syncthreads();  // the previous chunk's reads are done
-    store();
-    __syncthreads();
-    if (k0 + kChainK < K) load(k0 + kChainK);
-    const int kn = K - k0 < static_cast<size_t>(kChainK) ? static_cast<int>(K - k0) : kChainK;
-    const float* ar = As[mi];
-    const float* br = Bs[ni];
-    if (kn == kChainK) {
-#pragma unroll
-      for (int kk = 0; kk < kChainK; kk += 4) {
-        const float4 a = *reinterpret_cast<const float4*>(ar + kk);
-        const float4 b = *reinterpret_cast<const float4*>(br + kk);
-        if constexpr (kNT) {  // k0 is a multiple of 8: lane = kk % 8 + t
+  auto reduce = [&](int buf, int kn) {
+    const float* ar = As[buf][mi];
+    const float* br = Bs[buf][ni];
+    if constexpr (kNT) {
+      if (kn == kChainK) {
+#pragma unroll 8
+        for (int kk = 0; kk < kChainK; kk += 4) {  // k0 is a multiple of 8: lane = kk % 8 + t
+          const float4 a = *reinterpret_cast<const float4*>(ar + kk);
+          const float4 b = *reinterpret_cast<const float4*>(br + kk);
           const int l = kk % 8;
           lane[l] = Add(lane[l], Mul(a.x, b.x));
           lane[l + 1] = Add(lane[l + 1], Mul(a.y, b.y));
           lane[l + 2] = Add(lane[l + 2], Mul(a.z, b.z));
           lane[l + 3] = Add(lane[l + 3], Mul(a.w, b.w));
-        } else {
-          c = Add(c, Add(Add(Add(Mul(a.x, b.x), Mul(a.y, b.y)), Mul(a.z, b.z)), Mul(a.w, b.w)));
         }
-      }
-    } else if constexpr (kNT) {
-      for (int kk = 0; kk < kn; ++kk)
+      } else {
+        for (int kk = 0; kk < kn; ++kk)
 #pragma unroll
-        for (int l = 0; l < 8; ++l)
-          if ((kk & 7) == l) lane[l] = Add(lane[l], Mul(ar[kk], br[kk]));
+          for (int l = 0; l < 8; ++l)
+            if ((kk & 7) == l) lane[l] = Add(lane[l], Mul(ar[kk], br[kk]));
+      }
     } else {
+      // One loop for full and partial chunks.  (A copy of this loop
+      // unrolled for full chunks, next to it for a partial last chunk,
+      // gave wrong sums when the last chunk held whole quads -- K = 520,
+      // 600 -- while each form alone was exact for every K tried; kept to
+      // the single loop.)
       const int kq = kn & ~3;
-      for (int kk = 0; kk < kq; kk += 4)
-        c = Add(c, Add(Add(Add(Mul(ar[kk], br[kk]), Mul(ar[kk + 1], br[kk + 1])),
-                           Mul(ar[kk + 2], br[kk + 2])),
-                       Mul(ar[kk + 3], br[kk + 3])));
+      for (int kk = 0; kk < kq; kk += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(ar + kk);
+        const float4 b = *reinterpret_cast<const float4*>(br + kk);
+        c = Add(c, Add(Add(Add(Mul(a.x, b.x), Mul(a.y, b.y)), Mul(a.z, b.z)), Mul(a.w, b.w)));
+      }
       for (int kk = kq; kk < kn; ++kk) c = Add(c, Mul(ar[kk], br[kk]));  // the K % 4 tail
+    }
+  };
+  const size_t chunks = (K + kChainK - 1) / kChainK;
+  // The compiler places each store's wait by counting the loads issued
+  // after the ring slot's own: kChainDepth - 1 chunks of them in the steady
+  // state.  Near the end fewer follow (no chunk to load), so there the
+  // store waits for every load itself.  (Loads past the end are not issued
+  // instead: registers of a load nothing reads are taken as free while the
+  // load is still in flight.)
+  // Prologue: chunks 0 .. depth-1 in flight, chunk 0 stored.
+#pragma unroll
+  for (int u = 0; u < kChainDepth; ++u)
+    if (static_cast<size_t>(u) < chunks) load(static_cast<size_t>(u) * kChainK, ra[u], rb[u]);
+  WaitVmAll();
+  store(0, 0, ra[0], rb[0]);
+  if (static_cast<size_t>(kChainDepth) < chunks)
+    load(static_cast<size_t>(kChainDepth) * kChainK, ra[0], rb[0]);
+  __syncthreads();
+  // Chunk i sits in LDS buffer i & 1 and came from ring slot i % depth; the
+  // ring slot of chunk i + 1 is stored after chunk i is reduced and then
+  // refilled with chunk i + 1 + depth.  The loop is unrolled by the ring
+  // depth so every slot index is a constant.
+  for (size_t i0 = 0; i0 < chunks; i0 += kChainDepth) {
+#pragma unroll
+    for (int u = 0; u < kChainDepth; ++u) {
+      const size_t i = i0 + u;
+      if (i < chunks) {
+        const size_t k0 = i * kChainK;
+        const int kn = K - k0 < static_cast<size_t>(kChainK) ? static_cast<int>(K - k0) : kChainK;
+        reduce(static_cast<int>(i & 1), kn);
+        const int nx = (u + 1) % kChainDepth;  // a constant once unrolled
+        if (i + 1 < chunks) {
+          if (i + kChainDepth >= chunks) WaitVmAll();  // fewer loads follow this slot's
+          store(static_cast<int>((i + 1) & 1), (i + 1) * kChainK, ra[nx], rb[nx]);
+          if (i + 1 + kChainDepth < chunks) load((i + 1 + kChainDepth) * kChainK, ra[nx], rb[nx]);
+        }
+        __syncthreads();
+      }
     }
   }
   if (!live) return;

@@ -34,7 +34,7 @@ GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 
                (768, 8, 8192), (8, 768, 8192),
                # few outputs over long K: the chain kernel (one output per lane),
                # ragged chunks and a K % 4 tail
-               (1040, 16, 2050), (8200, 8, 600), (16, 1030, 1000)]
+               (1040, 16, 2050), (8200, 8, 600), (16, 1030, 1000), (300, 8, 520), (40, 16, 1300)]
 
 
 @pytest.fixture(scope="module")
@@ -324,10 +324,10 @@ def test_norms(hip, orc, backend, rows, cols):
         assert e <= TOL, f"{name}: {e:.3g}"
 
 
-def test_rope(hip, orc, backend):
+@pytest.mark.parametrize("B,S,H,d", [(2, 33, 3, 16), (2, 300, 4, 64)])
+def test_rope(hip, orc, backend, B, S, H, d):
     from tests.plan_ops import ins
-    B, S, H, d = 2, 33, 3, 16
-    r = rng(9)
+    r = rng(9 + S)
     x = r.standard_normal((B * S, H * d)).astype(np.float32)
     ar = Arena()
     rx = ar.add("x", x)
@@ -344,6 +344,9 @@ def test_rope(hip, orc, backend):
     for name in ["tab", "f", "b", "ft", "bt"]:
         e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
         assert e <= TOL, f"{name}: {e:.3g}"
+    # the table feeds the rotation the recurrence's own floats (attention.cc:98-102)
+    assert bits_equal(ar.get(gpu, "f"), ar.get(gpu, "ft"))
+    assert bits_equal(ar.get(gpu, "b"), ar.get(gpu, "bt"))
 
 
 # --- losses ---------------------------------------------------------------------------
