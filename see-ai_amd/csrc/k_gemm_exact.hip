@@ -325,6 +325,136 @@ __global__ void __launch_bounds__(kThreads) GemmPanelKernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// Rank-r products (K <= 32, f32 B, N % 4 == 0: the LoRA site's s (t B) + C
+// and dt A^T + dX, wide outputs over a tiny reduction).  The output and the
+// addend are the traffic, so a lane owns four consecutive outputs of one
+// row and moves them as 16-byte loads and stores; a workgroup covers 4 rows
+// x 256 columns.  A's row (K values, alpha applied as staged) is common to
+// the row's 64 lanes; B is small enough to stay in cache.  The chains are
+// the reference's: NN / TN / AccNN quads from k = 0 then the tail; NT eight
+// lanes by k mod 8, added in lane order, then alpha.
+// ---------------------------------------------------------------------------
+constexpr int kRankK = 32, kRankRows = 32;
+
+template <int kLayout>
+__global__ void __launch_bounds__(kThreads) GemmRankKernel(GemmArgs g) {
+  constexpr bool kNT = kLayout == 1;
+  __shared__ __attribute__((aligned(16))) float Bt[kRankK][256 + 4];  // B tile as [k][n]
+  __shared__ float At[kRankRows][kRankK + 1];                          // A rows, alpha applied
+  const size_t M = g.M, N = g.N;
+  const int K = static_cast<int>(g.K);
+  const int tid = threadIdx.x, tx = tid % 64, ty = tid / 64;
+  const size_t n0 = static_cast<size_t>(blockIdx.x) * 256;
+  const size_t mb = static_cast<size_t>(blockIdx.y) * kRankRows;
+  const float* __restrict__ B = static_cast<const float*>(g.B);
+  for (int e = tid; e < kRankRows * K; e += kThreads) {
+    const int r = e / K, k = e % K;
+    At[r][k] = mb + r < M ? LoadA<kLayout>(g, mb + r, k) : 0.0f;
+  }
+  for (int e = tid; e < K * 256; e += kThreads) {  // coalesced along B's contiguous index
+    int k, nn;
+    if constexpr (kNT) {  // B[N, K]
+      nn = e / K;
+      k = e % K;
+    } else {              // B[K, N]
+      k = e / 256;
+      nn = e % 256;
+    }
+    const size_t n = n0 + nn;
+    Bt[k][nn] = n < N ? (kNT ? B[n * K + k] : B[static_cast<size_t>(k) * N + n]) : 0.0f;
+  }
+  __syncthreads();
+  const size_t n = n0 + tx * 4;
+  if (n >= N) return;
+  for (int r = 0; r < kRankRows / 4; ++r) {
+    const int rr = r * 4 + ty;
+    const size_t m = mb + rr;
+    if (m >= M) return;
+    float c[4];
+    if constexpr (kNT) {
+      float lane[4][8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) lane[e][l] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kRankK; ++k) {
+        if (k < K) {
+          const float a = At[rr][k];
+          const float4 b = *reinterpret_cast<const float4*>(&Bt[k][tx * 4]);
+          lane[0][k % 8] = Add(lane[0][k % 8], Mul(a, b.x));
+          lane[1][k % 8] = Add(lane[1][k % 8], Mul(a, b.y));
+          lane[2][k % 8] = Add(lane[2][k % 8], Mul(a, b.z));
+          lane[3][k % 8] = Add(lane[3][k % 8], Mul(a, b.w));
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = lane[e][0];
+#pragma unroll
+        for (int l = 1; l < 8; ++l) v = Add(v, lane[e][l]);
+        c[e] = Mul(g.alpha_dot, v);
+      }
+    } else {
+      if (g.accumulate) {
+        const float4 c0 = *reinterpret_cast<const float4*>(g.C + m * N + n);
+        c[0] = c0.x, c[1] = c0.y, c[2] = c0.z, c[3] = c0.w;
+      } else {
+        c[0] = c[1] = c[2] = c[3] = 0.0f;
+      }
+      const int kq = K & ~3;
+#pragma unroll
+      for (int k = 0; k < kRankK; k += 4) {
+        if (k < kq) {
+          float a[4];
+          float4 b[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            a[t] = At[rr][k + t];
+            b[t] = *reinterpret_cast<const float4*>(&Bt[k + t][tx * 4]);
+          }
+          c[0] = Add(c[0], Add(Add(Add(Mul(a[0], b[0].x), Mul(a[1], b[1].x)), Mul(a[2], b[2].x)), Mul(a[3], b[3].x)));
+          c[1] = Add(c[1], Add(Add(Add(Mul(a[0], b[0].y), Mul(a[1], b[1].y)), Mul(a[2], b[2].y)), Mul(a[3], b[3].y)));
+          c[2] = Add(c[2], Add(Add(Add(Mul(a[0], b[0].z), Mul(a[1], b[1].z)), Mul(a[2], b[2].z)), Mul(a[3], b[3].z)));
+          c[3] = Add(c[3], Add(Add(Add(Mul(a[0], b[0].w), Mul(a[1], b[1].w)), Mul(a[2], b[2].w)), Mul(a[3], b[3].w)));
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kRankK; ++k) {
+        if (k >= kq && k < K) {  // the K % 4 tail
+          const float a = At[rr][k];
+          const float4 b = *reinterpret_cast<const float4*>(&Bt[k][tx * 4]);
+          c[0] = Add(c[0], Mul(a, b.x));
+          c[1] = Add(c[1], Mul(a, b.y));
+          c[2] = Add(c[2], Mul(a, b.z));
+          c[3] = Add(c[3], Mul(a, b.w));
+        }
+      }
+    }
+    const size_t o = m * N + n;
+    float4 d = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (g.addend) d = *reinterpret_cast<const float4*>(g.addend + o);
+    const float dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = c[e];
+      if (g.addend) x = Add(dv[e], x);
+      if (g.bias) x = Add(x, g.bias[n + e]);
+      if (g.act) x = ActExpr(g.act, x);
+      c[e] = x;
+    }
+    *reinterpret_cast<float4*>(g.C + o) = make_float4(c[0], c[1], c[2], c[3]);
+  }
+}
+
+bool RankFits(const GemmArgs& a) {
+  const auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return a.b_kind == 0 && a.K > 0 && a.K <= static_cast<size_t>(kRankK) && a.N % 4 == 0 &&
+         a.M >= 64 && a.N >= 256 && al(a.C) && (!a.addend || al(a.addend)) &&
+         (a.M + kRankRows - 1) / kRankRows <= 65535;
+}
+
+// ---------------------------------------------------------------------------
 // Long reductions over few outputs (NN / TN, M*N small, K large: the LoRA
 // dA / dB over every token).  A workgroup owns a BMo x BNo block of C (32
 // outputs; BNo the largest power of two <= min(N, 32), so slice indices
@@ -714,6 +844,12 @@ bool LongKFirst() {
 
 template <int kLayout, int kBKind>
 hipError_t Run(const GemmArgs& a, hipStream_t s) {
+  if (kBKind == 0 && RankFits(a)) {
+    const dim3 grid(static_cast<unsigned>((a.N + 255) / 256),
+                    static_cast<unsigned>((a.M + kRankRows - 1) / kRankRows));
+    hipLaunchKernelGGL((GemmRankKernel<kLayout>), grid, dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+  }
   if (a.K <= static_cast<size_t>(kPanelK) && a.K > 0 && (a.M + 15) / 16 <= 65535) {
     const dim3 grid(static_cast<unsigned>((a.N + 15) / 16), static_cast<unsigned>((a.M + 15) / 16));
     const size_t lds = 2 * 16 * a.K * sizeof(float);
