@@ -813,6 +813,145 @@ __global__ void __launch_bounds__(kThreads) GemmChainKernel(GemmArgs g) {
   g.C[m * N + n] = Epilogue(g, m, n, c);
 }
 
+// ---------------------------------------------------------------------------
+// Long reductions over few outputs, NN / TN (the adapter gradients
+// dA = X^T dt and dB = s t^T dC over every token): the quads of a chunk are
+// independent, only their sum into the output is a chain.  A workgroup owns
+// 64 outputs (BMo x BNo) and walks K in chunks of kFoldK: four lanes per
+// output form the chunk's quads ((a0 b0 + a1 b1) + a2 b2) + a3 b3 into LDS,
+// then one lane per output adds them onto its output in k order -- the
+// reference's chain, with four times the lanes of one output per lane.  The
+// operands are staged k-contiguous per row (a quad is one 16-byte read of
+// A and of B); the next chunk's raw loads are in flight while the current
+// one is reduced, its scales applied at the store.
+// ---------------------------------------------------------------------------
+constexpr int kFoldK = 512, kFoldQ = kFoldK / 4, kFoldOut = 64, kFoldLd = kFoldK + 4;
+
+template <int kLayout, int BNo>
+__global__ void __launch_bounds__(kThreads) GemmFoldKernel(GemmArgs g) {
+  static_assert(kLayout != 1, "NT keeps its eight k-lanes");
+  constexpr int BMo = kFoldOut / BNo;
+  constexpr int kAPer = BMo * kFoldK / kThreads, kBPer = BNo * kFoldK / kThreads;
+  static_assert(kAPer * kThreads == BMo * kFoldK && kBPer * kThreads == BNo * kFoldK,
+                "every chunk element has a lane");
+  __shared__ __attribute__((aligned(16))) float As[BMo][kFoldLd];
+  __shared__ __attribute__((aligned(16))) float Bs[BNo][kFoldLd];
+  __shared__ float Q[kFoldQ][kFoldOut + 1];
+  const int tid = threadIdx.x;
+  const size_t M = g.M, N = g.N, K = g.K;
+  // Workgroup b runs on XCD b % 8, each XCD with its own L2.  A workgroup
+  // reads BMo- and BNo-wide strips of rows far longer than a cache line, so
+  // the strips of neighbouring workgroups share lines: each XCD takes a
+  // contiguous run of blocks, and a line leaves HBM once instead of once
+  // per XCD.
+  const unsigned total = gridDim.x * gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
+  const unsigned t = total % 8 == 0 ? (lin % 8) * (total / 8) + lin / 8 : lin;
+  const size_t m0 = static_cast<size_t>(t / gridDim.x) * BMo, n0 = static_cast<size_t>(t % gridDim.x) * BNo;
+  const float* __restrict__ B = static_cast<const float*>(g.B);
+  // Chunk element e: A's (mm, kk), B's (nn, kk), the contiguous index fastest.
+  auto a_of = [&](int e, int& mm, int& kk) {
+    if constexpr (kLayout == 2) {  // A[K, M]
+      kk = e / BMo;
+      mm = e % BMo;
+    } else {                       // A[M, K]
+      mm = e / kFoldK;
+      kk = e % kFoldK;
+    }
+  };
+  auto b_of = [&](int e, int& nn, int& kk) {  // B[K, N]
+    kk = e / BNo;
+    nn = e % BNo;
+  };
+  float ra[kAPer], rb[kBPer];
+  auto load = [&](size_t k0) {  // raw and branch-free: indices clamped into the operand
+#pragma unroll
+    for (int r = 0; r < kAPer; ++r) {
+      int mm, kk;
+      a_of(tid + r * kThreads, mm, kk);
+      const size_t m = min(m0 + mm, M - 1), k = min(k0 + kk, K - 1);
+      ra[r] = kLayout == 2 ? g.A[k * M + m] : g.A[m * K + k];
+    }
+#pragma unroll
+    for (int r = 0; r < kBPer; ++r) {
+      int nn, kk;
+      b_of(tid + r * kThreads, nn, kk);
+      const size_t n = min(n0 + nn, N - 1), k = min(k0 + kk, K - 1);
+      rb[r] = B[k * N + n];
+    }
+  };
+  auto store = [&](size_t k0) {
+#pragma unroll
+    for (int r = 0; r < kAPer; ++r) {
+      int mm, kk;
+      a_of(tid + r * kThreads, mm, kk);
+      float v = ra[r];
+      if (g.alpha_a != 1.0f) v = Mul(g.alpha_a, v);
+      As[mm][kk] = (m0 + mm < M && k0 + kk < K) ? v : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < kBPer; ++r) {
+      int nn, kk;
+      b_of(tid + r * kThreads, nn, kk);
+      Bs[nn][kk] = (n0 + nn < N && k0 + kk < K) ? rb[r] : 0.0f;
+    }
+  };
+  const int o = tid % kFoldOut, slot = tid / kFoldOut;  // this lane's output and quad slot
+  const int mo = o / BNo, no = o % BNo;
+  const size_t mf = m0 + mo, nf = n0 + no;
+  const bool folds = tid < kFoldOut && mf < M && nf < N;
+  float c = (folds && g.accumulate) ? g.C[mf * N + nf] : 0.0f;
+  const size_t quads = K / 4;
+  const size_t chunks = (quads + kFoldQ - 1) / kFoldQ;
+  load(0);
+  for (size_t ch = 0; ch < chunks; ++ch) {
+    const size_t k0 = ch * kFoldK;
+    __syncthreads();  // the previous chunk's As / Bs / Q reads are done
+    if (ch + 1 == chunks) WaitVmAll();  // no loads follow this chunk's (see GemmChainKernel)
+    store(k0);
+    __syncthreads();
+    if (ch + 1 < chunks) load(k0 + kFoldK);
+    const int nq = static_cast<int>(quads - ch * kFoldQ < static_cast<size_t>(kFoldQ) ? quads - ch * kFoldQ : kFoldQ);
+    for (int j = slot; j < nq; j += kThreads / kFoldOut) {
+      const float4 a = *reinterpret_cast<const float4*>(&As[mo][4 * j]);
+      const float4 b = *reinterpret_cast<const float4*>(&Bs[no][4 * j]);
+      Q[j][o] = Add(Add(Add(Mul(a.x, b.x), Mul(a.y, b.y)), Mul(a.z, b.z)), Mul(a.w, b.w));
+    }
+    __syncthreads();
+    if (folds)
+      for (int j = 0; j < nq; ++j) c = Add(c, Q[j][o]);
+  }
+  if (!folds) return;
+  for (size_t k = quads * 4; k < K; ++k)  // the K % 4 tail, one term at a time
+    c = Add(c, Mul(LoadA<kLayout>(g, mf, k), B[k * N + nf]));
+  g.C[mf * N + nf] = Epilogue(g, mf, nf, c);
+}
+
+// The fold kernel for TN with f32 B over K >= 1024 when the outputs fill at
+// most a few thousand workgroups (NN over these shapes measured faster on
+// the chain kernel).
+bool Fold(const GemmArgs& a) {
+  return a.layout == 2 && a.b_kind == 0 && a.K >= 1024 && a.M * a.N <= (size_t{1} << 18);
+}
+
+template <int kLayout>
+hipError_t LaunchFold(const GemmArgs& a, hipStream_t s) {
+  // BNo: N rounded up to a power of two in [2, 16] (a chunk of B then spans
+  // whole lanes: BNo * kFoldK >= 256).
+  int bno = 2;
+  while (bno < 16 && static_cast<size_t>(bno) < a.N) bno *= 2;
+  const size_t bmo = kFoldOut / bno;
+  const size_t gx = (a.N + bno - 1) / bno, gy = (a.M + bmo - 1) / bmo;
+  if (gy > 65535) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  switch (bno) {
+    case 2: hipLaunchKernelGGL((GemmFoldKernel<kLayout, 2>), grid, dim3(kThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((GemmFoldKernel<kLayout, 4>), grid, dim3(kThreads), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((GemmFoldKernel<kLayout, 8>), grid, dim3(kThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL((GemmFoldKernel<kLayout, 16>), grid, dim3(kThreads), 0, s, a); break;
+  }
+  return hipGetLastError();
+}
+
 // The chain kernel where the tiled kernel's grid would be small for the
 // reduction it carries: under 512 tiles of 64 x 64 and K above the panel.
 bool Chain(const GemmArgs& a) {
@@ -856,6 +995,8 @@ hipError_t Run(const GemmArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((GemmPanelKernel<kLayout, kBKind>), grid, dim3(kThreads), lds, s, a);
     return hipGetLastError();
   }
+  if constexpr (kLayout == 2 && kBKind == 0)
+    if (Fold(a)) return LaunchFold<kLayout>(a, s);
   if (Chain(a) && !(kLayout != 1 && LongK(a) && a.scratch && LongKFirst())) {
     if (a.N <= 8) return LaunchChain<kLayout, kBKind, 32, 8>(a, s);
     if (a.M <= 8) return LaunchChain<kLayout, kBKind, 8, 32>(a, s);
