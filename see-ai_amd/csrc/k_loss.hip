@@ -17,13 +17,27 @@ namespace {
 // --- pass 1: row max (order-free: fmax ignores NaN as std::fmax does) ------
 constexpr int kMaxThreads = 256;
 
+// Rows of 16-byte multiples move as float4 with two running maxima per lane.
+__device__ __forceinline__ bool Vec4Rows(const void* p, size_t C) {
+  return C % 4 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+}
+
 __global__ void __launch_bounds__(kMaxThreads)
 XEntRowMaxKernel(const float* __restrict__ logits, float* __restrict__ row_max, size_t C) {
   __shared__ float red[kMaxThreads / kWave];
   const float* x = logits + static_cast<size_t>(blockIdx.x) * C;
-  float mx = NAN;  // the identity of fmax
-  for (size_t c = threadIdx.x; c < C; c += kMaxThreads) mx = fmaxf(mx, x[c]);
-  mx = BlockMaxF<kMaxThreads>(mx, red);
+  float mx = NAN, mx2 = NAN;  // the identity of fmax
+  if (Vec4Rows(logits, C)) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    for (size_t c = threadIdx.x; c < C / 4; c += kMaxThreads) {
+      const float4 v = x4[c];
+      mx = fmaxf(mx, fmaxf(v.x, v.y));
+      mx2 = fmaxf(mx2, fmaxf(v.z, v.w));
+    }
+  } else {
+    for (size_t c = threadIdx.x; c < C; c += kMaxThreads) mx = fmaxf(mx, x[c]);
+  }
+  mx = BlockMaxF<kMaxThreads>(fmaxf(mx, mx2), red);
   if (threadIdx.x == 0) row_max[blockIdx.x] = mx;
 }
 
@@ -40,7 +54,7 @@ constexpr int kTileCols = 256;
 __global__ void __launch_bounds__(kSumThreads)
 XEntSerialSumKernel(const float* __restrict__ logits, const float* __restrict__ row_max,
                     float* __restrict__ row_sum, size_t N, size_t C) {
-  __shared__ float tile[2][kSumRows][kTileCols + 1];
+  __shared__ __attribute__((aligned(16))) float tile[2][kSumRows][kTileCols + 4];
   const size_t r0 = static_cast<size_t>(blockIdx.x) * kSumRows;
   const int t = threadIdx.x;
   const size_t ntiles = (C + kTileCols - 1) / kTileCols;
@@ -64,7 +78,25 @@ XEntSerialSumKernel(const float* __restrict__ logits, const float* __restrict__ 
     if (t < kSumRows) {
       const float* row = tile[k & 1][t];
       const size_t w = k + 1 < ntiles ? kTileCols : C - k * kTileCols;
-      for (size_t j = 0; j < w; ++j) sum += row[j];
+      if (w == kTileCols) {
+        // The adds are the chain; their LDS reads are not: sixteen values
+        // are read ahead of their adds, which stay in column order.
+#pragma unroll 2
+        for (int j0 = 0; j0 < kTileCols; j0 += 16) {
+          float4 v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const float4*>(row + j0 + 4 * q);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            sum += v[q].x;
+            sum += v[q].y;
+            sum += v[q].z;
+            sum += v[q].w;
+          }
+        }
+      } else {
+        for (size_t j = 0; j < w; ++j) sum += row[j];
+      }
     }
     __syncthreads();
   }
@@ -83,7 +115,17 @@ XEntProbsKernel(const float* __restrict__ logits, const int32_t* __restrict__ la
   float* p = probs + r * C;
   const float mx = row_max[r];
   const float inv_sum = 1.0f / row_sum[r];  // loss.cc:30
-  for (size_t c = threadIdx.x; c < C; c += kProbThreads) p[c] = expf(x[c] - mx) * inv_sum;
+  if (Vec4Rows(logits, C) && Vec4Rows(probs, C)) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float4* p4 = reinterpret_cast<float4*>(p);
+    for (size_t c = threadIdx.x; c < C / 4; c += kProbThreads) {
+      const float4 v = x4[c];
+      p4[c] = make_float4(expf(v.x - mx) * inv_sum, expf(v.y - mx) * inv_sum,
+                          expf(v.z - mx) * inv_sum, expf(v.w - mx) * inv_sum);
+    }
+  } else {
+    for (size_t c = threadIdx.x; c < C; c += kProbThreads) p[c] = expf(x[c] - mx) * inv_sum;
+  }
   if (threadIdx.x == 0) {
     const int32_t lab = labels[r];
     double term = 0.0;
@@ -137,23 +179,48 @@ XEntScaleKernel(const int32_t* __restrict__ labels, const float* __restrict__ se
   }
 }
 
+// One workgroup per row (grid-stride over rows): the label is read once,
+// the row moves as float4 where it can.
 __global__ void __launch_bounds__(256)
 XEntBwdKernel(const float* __restrict__ probs, const int32_t* __restrict__ labels,
               const float* __restrict__ scale_p, float* __restrict__ dl, size_t N, size_t C,
               int masked) {
   const float scale = *scale_p;
-  const size_t total = N * C;
-  const size_t stride = static_cast<size_t>(gridDim.x) * 256;
-  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
-    const size_t r = i / C, c = i % C;
+  const bool vec = Vec4Rows(probs, C) && Vec4Rows(dl, C);
+  for (size_t r = blockIdx.x; r < N; r += gridDim.x) {
     const int32_t lab = labels[r];
-    if (masked && lab < 0) {
-      dl[i] = 0.0f;
-      continue;
+    const float* pr = probs + r * C;
+    float* dr = dl + r * C;
+    const bool zero = masked && lab < 0;
+    const size_t lc = static_cast<size_t>(lab);
+    if (vec) {
+      const float4* p4 = reinterpret_cast<const float4*>(pr);
+      float4* d4 = reinterpret_cast<float4*>(dr);
+      for (size_t c = threadIdx.x; c < C / 4; c += 256) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!zero) {
+          const float4 q = p4[c];
+          v = make_float4(scale * q.x, scale * q.y, scale * q.z, scale * q.w);
+          if (lc / 4 == c) {  // the label's element, by component
+            const size_t l = lc % 4;
+            if (l == 0) v.x -= scale;
+            else if (l == 1) v.y -= scale;
+            else if (l == 2) v.z -= scale;
+            else v.w -= scale;
+          }
+        }
+        d4[c] = v;
+      }
+    } else {
+      for (size_t c = threadIdx.x; c < C; c += 256) {
+        float v = 0.0f;
+        if (!zero) {
+          v = scale * pr[c];
+          if (lc == c) v -= scale;
+        }
+        dr[c] = v;
+      }
     }
-    float v = scale * probs[i];
-    if (static_cast<size_t>(lab) == c) v -= scale;
-    dl[i] = v;
   }
 }
 
@@ -183,8 +250,8 @@ hipError_t LaunchXEntBwd(const float* probs, const int32_t* labels, const float*
   if (N == 0) return hipSuccess;
   float* scale = static_cast<float*>(ws);
   hipLaunchKernelGGL(XEntScaleKernel, dim3(1), dim3(1024), 0, s, labels, seed, scale, N, masked);
-  hipLaunchKernelGGL(XEntBwdKernel, dim3(GridFor(N * C, 256, 16384)), dim3(256), 0, s, probs,
-                     labels, scale, dlogits, N, C, masked);
+  hipLaunchKernelGGL(XEntBwdKernel, dim3(static_cast<unsigned>(N < 65536 ? N : 65536)), dim3(256), 0,
+                     s, probs, labels, scale, dlogits, N, C, masked);
   return hipGetLastError();
 }
 
