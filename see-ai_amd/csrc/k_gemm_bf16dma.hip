@@ -292,6 +292,37 @@ ConvertRowsKernel(const float* __restrict__ A, size_t K, size_t Kp, float alpha,
   }
 }
 
+// K a multiple of 32 (Kp == K): A' is A element for element, so the rows
+// flatten into one array; each lane converts two groups of eight per trip
+// (four 16-byte loads in flight), grid-stride.  The k-scale index is the
+// flat index mod K.
+__global__ void __launch_bounds__(kCvtThreads)
+ConvertFlatKernel(const float* __restrict__ A, size_t groups, size_t K, float alpha,
+                  const float* __restrict__ ks, __bf16* __restrict__ out) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kCvtThreads;
+  auto convert = [&](size_t gi) {
+    const float4 a = reinterpret_cast<const float4*>(A)[2 * gi];
+    const float4 b = reinterpret_cast<const float4*>(A)[2 * gi + 1];
+    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const size_t k0 = (gi * 8) % K;
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = x[e];
+      if (ks) v = v * ks[k0 + e];
+      if (alpha != 1.0f) v = alpha * v;
+      o[e] = static_cast<__bf16>(v);
+    }
+    reinterpret_cast<bf16x8*>(out)[gi] = o;
+  };
+  size_t gi = static_cast<size_t>(blockIdx.x) * kCvtThreads + threadIdx.x;
+  for (; gi + stride < groups; gi += 2 * stride) {
+    convert(gi);
+    convert(gi + stride);
+  }
+  if (gi < groups) convert(gi);
+}
+
 // W' [N, Kp] bf16 from the weight as the instruction reads it: NN's W[K, N]
 // (transposed through a 32 x 32 LDS tile) or NT's W[N, K]; f32 rounded
 // (RNE), int8 levels and bf16 exact; zero for k >= K.
@@ -350,6 +381,13 @@ bool Bf16DmaFits(const GemmArgs& a) {
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,
                                  const float* kscale, void* out, hipStream_t s) {
   if (M == 0) return hipSuccess;
+  if (K % 32 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0) {
+    const size_t groups = M * K / 8;
+    hipLaunchKernelGGL(ConvertFlatKernel, dim3(GridFor(groups / 2, kCvtThreads, 16384)),
+                       dim3(kCvtThreads), 0, s, A, groups, K, alpha, kscale,
+                       static_cast<__bf16*>(out));
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(ConvertRowsKernel, dim3(static_cast<unsigned>(M)), dim3(kCvtThreads), 0, s, A, K,
                      Bf16DmaKp(K), alpha, kscale, static_cast<__bf16*>(out));
   return hipGetLastError();
