@@ -271,6 +271,15 @@ def main():
     g_end.record()
     torch.cuda.synchronize()
     gemm_ms = g_start.elapsed_time(g_end) / args.steps
+    # The activation quantize alone (HBM-bound: reads 4MK bytes, writes MK + 4M).
+    q_start, q_end = ev(), ev()
+    q_start.record()
+    for i in range(args.steps):
+        quantize()
+    q_end.record()
+    torch.cuda.synchronize()
+    quant_ms = q_start.elapsed_time(q_end) / args.steps
+    quant_bytes = 4 * M * K + M * K + 4 * M
     ms_per_step = wall * 1000.0 / args.steps
     ops = 2.0 * M * N * K
     value = ops / (ms_per_step * 1e-3) / 1e12
@@ -303,6 +312,9 @@ def main():
             "kernel_ms": round(gemm_ms, 5),
             "traffic": load_traffic("w8a8_4096"),
         },
+        "quantize": {"kernel": "QuantizeRowsWaveKernel<16>", "ms": round(quant_ms, 5),
+                     "bytes": quant_bytes, "GB_s": round(quant_bytes / quant_ms / 1e6, 1),
+                     "hbm_frac": round(quant_bytes / quant_ms / 1e6 / PEAK_HBM_GBS, 4)},
     }
 
     if not args.no_cpu:

@@ -113,6 +113,33 @@ uint64_t seeai_fused_dispatches(const seeai_ctx* ctx);
  * last flush (non-finite clip norm: nothing it guarded was written). */
 int seeai_flush(seeai_ctx* ctx);
 
+/* --- Kernel geometry: ExecutorBackend::Configure (backend.h:117) -------- */
+/* The gfx950 member of the reference's schema-1 kernel-policy table
+ * (compiler/backend/architecture/kernel_policy_table.cc:294-404 reads
+ * hosts.<key>.cpu; this backend's table reader takes hosts.<key>.gfx950
+ * beside it).  Every field chooses among kernels that give identical bits,
+ * so a policy changes time, never results; 0 keeps the built-in default. */
+typedef struct seeai_tile_policy {
+  uint32_t w8a8_large_kernel;     /* 1 direct-to-LDS 256x256 (default), 2 register-staged 256x256,
+                                     3 register-staged 128x128 */
+  uint32_t w8a8_large_min;        /* M and N from which it applies (default 4096) */
+  uint32_t quantize_waves_per_cu; /* waves per CU walking the quantizer's rows (default 32, <= 32) */
+  uint32_t relaxed_min_tiles_256; /* relaxed bf16 GEMM: 256x256 tiles from this many (default 256) */
+  uint32_t relaxed_min_fill_256;  /* ... and when their last round over the CUs is at least
+                                     this percent full (<= 100) */
+  uint32_t exact_longk_first;     /* exact skinny long-K GEMM: 1 the two-pass form before the
+                                     chain kernel (default), 2 the chain kernel first */
+} seeai_tile_policy;
+/* NULL restores the defaults; an out-of-range field is status 2 and leaves
+ * the policy in force unchanged. */
+int seeai_configure(seeai_ctx* ctx, const seeai_tile_policy* policy);
+/* The policy in force, defaults filled in. */
+int seeai_policy(const seeai_ctx* ctx, seeai_tile_policy* out);
+/* The device's table key, the GPU counterpart of HostKey
+ * (compiler/backend/architecture/host_arch.h:41-50): one line,
+ * "<gfx arch>;<device name>;cus=<n>;lds=<bytes per CU>;l2=<bytes>;wave=<lanes>". */
+int seeai_device_key(int device, char* buf, uint64_t bytes);
+
 /* --- Op-family entry points on caller-owned device memory --------------- */
 /* GemmNN / NT / TN / AccNN (runtime/executor/gemm.cc:582-624).
  * layout 0 NN (A[M,K], B[K,N]), 1 NT (B[N,K]), 2 TN (A[K,M]);

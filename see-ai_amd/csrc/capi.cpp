@@ -92,6 +92,7 @@ struct seeai_ctx {
   const uint8_t* done = nullptr;  // the next instruction, already run by a fused dispatch
   int allow_fusion = 1;
   int allow_dma = 1;  // relaxed frozen-weight GEMMs on the bf16 shadow path
+  TilePolicy policy;  // kernel geometry (seeai_configure)
   uint64_t fused = 0;
   // bf16 copies [N, Kp] of frozen weights for the relaxed GEMMs, keyed by
   // (weight, layout, kind, N, K); valid until the next bind.
@@ -210,6 +211,7 @@ int GemmBf16Dma(seeai_ctx* c, GemmArgs& a, const char* what) {
 
 // A GEMM launch with the workspace its kernel may use.
 int Gemm(seeai_ctx* c, GemmArgs& a, const char* what) {
+  a.policy = &c->policy;
   if (a.relaxed && c->allow_dma && Bf16DmaFits(a) && Immutable(c, a.B)) return GemmBf16Dma(c, a, what);
   if (const size_t bytes = a.relaxed ? 0 : GemmExactScratchBytes(a)) {
     void* ws;
@@ -807,6 +809,62 @@ int seeai_set_fusion(seeai_ctx* c, int allow) {
 
 uint64_t seeai_fused_dispatches(const seeai_ctx* c) { return c ? c->fused : 0; }
 
+int seeai_configure(seeai_ctx* c, const seeai_tile_policy* p) {
+  if (!c) return SEEAI_INVALID;
+  TilePolicy t;  // defaults
+  if (p) {
+    // CheckEntry's role (kernel_policy_table.cc:280-289): refuse what no
+    // kernel implements, leave the previous policy in force.
+    if (p->w8a8_large_kernel > 3)
+      return Fail(c, SEEAI_INVALID, "tile policy: w8a8_large_kernel %u is not 1, 2 or 3",
+                  p->w8a8_large_kernel);
+    if (p->exact_longk_first > 2)
+      return Fail(c, SEEAI_INVALID, "tile policy: exact_longk_first %u is not 1 or 2",
+                  p->exact_longk_first);
+    if (p->relaxed_min_fill_256 > 100)
+      return Fail(c, SEEAI_INVALID, "tile policy: relaxed_min_fill_256 %u exceeds 100 percent",
+                  p->relaxed_min_fill_256);
+    if (p->quantize_waves_per_cu > 32)
+      return Fail(c, SEEAI_INVALID, "tile policy: quantize_waves_per_cu %u exceeds 32 waves per CU",
+                  p->quantize_waves_per_cu);
+    if (p->w8a8_large_kernel) t.w8a8_large_kernel = static_cast<int>(p->w8a8_large_kernel);
+    if (p->w8a8_large_min) t.w8a8_large_min = p->w8a8_large_min;
+    if (p->quantize_waves_per_cu) t.quantize_waves_per_cu = static_cast<int>(p->quantize_waves_per_cu);
+    if (p->relaxed_min_tiles_256) t.relaxed_min_tiles_256 = p->relaxed_min_tiles_256;
+    if (p->relaxed_min_fill_256) t.relaxed_min_fill_256 = static_cast<int>(p->relaxed_min_fill_256);
+    if (p->exact_longk_first) t.exact_longk_first = static_cast<int>(p->exact_longk_first);
+  }
+  c->policy = t;
+  return SEEAI_OK;
+}
+
+int seeai_policy(const seeai_ctx* c, seeai_tile_policy* out) {
+  if (!c || !out) return SEEAI_INVALID;
+  out->w8a8_large_kernel = static_cast<uint32_t>(c->policy.w8a8_large_kernel);
+  out->w8a8_large_min = static_cast<uint32_t>(c->policy.w8a8_large_min);
+  out->quantize_waves_per_cu = static_cast<uint32_t>(c->policy.quantize_waves_per_cu);
+  out->relaxed_min_tiles_256 = static_cast<uint32_t>(c->policy.relaxed_min_tiles_256);
+  out->relaxed_min_fill_256 = static_cast<uint32_t>(c->policy.relaxed_min_fill_256);
+  out->exact_longk_first = static_cast<uint32_t>(c->policy.exact_longk_first);
+  return SEEAI_OK;
+}
+
+int seeai_device_key(int device, char* buf, uint64_t bytes) {
+  if (!buf || bytes == 0) return SEEAI_INVALID;
+  hipDeviceProp_t p{};
+  if (hipGetDeviceProperties(&p, device) != hipSuccess) return SEEAI_HIP_ERROR;
+  std::string arch(p.gcnArchName);
+  if (const size_t colon = arch.find(':'); colon != std::string::npos) arch.resize(colon);
+  char key[512];
+  std::snprintf(key, sizeof key, "%s;%s;cus=%d;lds=%zu;l2=%d;wave=%d", arch.c_str(), p.name,
+                p.multiProcessorCount, static_cast<size_t>(p.maxSharedMemoryPerMultiProcessor),
+                p.l2CacheSize, p.warpSize);
+  const size_t n = std::strlen(key);
+  if (n + 1 > bytes) return SEEAI_INVALID;
+  std::memcpy(buf, key, n + 1);
+  return SEEAI_OK;
+}
+
 int seeai_execute_range(seeai_ctx* c, const void* instructions, uint64_t count,
                         const seeai_step_params* params, uint64_t* failed_at) {
   if (!c || (!instructions && count)) return SEEAI_INVALID;
@@ -916,7 +974,7 @@ int seeai_gemm_bf16w(seeai_ctx* c, int nt, const float* A, const uint16_t* B, fl
 int seeai_w8a8_quantize_rows(seeai_ctx* c, const float* X, int8_t* Q, float* scale, uint64_t rows,
                              uint64_t cols) {
   if (!c) return SEEAI_INVALID;
-  SEEAI_TRY(c, LaunchQuantizeRows(X, Q, scale, rows, cols, c->stream), "quantize_rows");
+  SEEAI_TRY(c, LaunchQuantizeRows(X, Q, scale, rows, cols, c->policy.quantize_waves_per_cu, c->stream), "quantize_rows");
   return SEEAI_OK;
 }
 
@@ -932,7 +990,7 @@ int seeai_w8a8_gemm(seeai_ctx* c, const int8_t* QA, const float* sa, const int8_
   if (!c) return SEEAI_INVALID;
   if (K > 133144) return Fail(c, SEEAI_INVALID, "w8a8_gemm: K = %llu could overflow the int32 accumulator",
                              static_cast<unsigned long long>(K));
-  SEEAI_TRY(c, LaunchGemmW8A8(QA, sa, QWt, sw, C, acc, M, N, K, c->stream), "w8a8_gemm");
+  SEEAI_TRY(c, LaunchGemmW8A8(QA, sa, QWt, sw, C, acc, M, N, K, c->policy, c->stream), "w8a8_gemm");
   return SEEAI_OK;
 }
 

@@ -197,6 +197,21 @@ hipError_t LaunchSgd(float* p, const float* g, size_t n, float lr, float wd, con
                      const int* flag, hipStream_t s);
 
 // fp32-output GEMM family on MFMA (k_gemm_f32.hip).
+// Kernel-geometry choices (the C ABI's seeai_tile_policy): each field picks
+// among kernels that give identical bits, so a policy changes time, never
+// results.  A default-constructed policy is the built-in choice.
+struct TilePolicy {
+  int w8a8_large_kernel = 1;           // 1 direct-to-LDS 256 x 256, 2 register-staged 256 x 256,
+                                       // 3 register-staged 128 x 128
+  size_t w8a8_large_min = 4096;        // M and N from which w8a8_large_kernel applies
+  int quantize_waves_per_cu = 32;      // waves per CU walking the rows of the quantizer
+  size_t relaxed_min_tiles_256 = 256;  // relaxed bf16 GEMM: 256 x 256 tiles from this many
+  int relaxed_min_fill_256 = 0;        // ... and when their last round of tiles over
+                                       // the CUs is at least this percent full
+  int exact_longk_first = 1;           // exact skinny long-K GEMM: 1 the two-pass workspace
+                                       // form before the chain kernel, 2 the chain kernel first
+};
+
 struct GemmArgs {
   int layout;          // 0 NN (A[M,K], B[K,N]), 1 NT (B[N,K]), 2 TN (A[K,M])
   int b_kind;          // 0 f32, 1 int8, 2 bf16
@@ -214,6 +229,7 @@ struct GemmArgs {
   int accumulate;            // C += (GemmAccNN)
   int relaxed;               // kFlagRelaxed taken: MFMA summation order
   float* scratch;            // device workspace (GemmExactScratchBytes), or null
+  const TilePolicy* policy;  // kernel geometry (null: the defaults)
 };
 // Relaxed -> MFMA (k_gemm_f32.hip); otherwise the reference's order.
 hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s);
@@ -234,13 +250,17 @@ hipError_t LaunchGemmBf16Dma(const void* A, const void* W, const GemmArgs& a, hi
 bool GemmBf16Fits(const GemmArgs& a);
 hipError_t LaunchGemmBf16(const GemmArgs& a, hipStream_t s);
 
+// Compute units of the current device (cached per device).
+int DeviceCUs();
+
 // W8A8 (k_gemm_i8.hip).
 hipError_t LaunchQuantizeRows(const float* X, int8_t* Q, float* scale, size_t rows, size_t cols,
-                              hipStream_t s);
+                              int waves_per_cu, hipStream_t s);
 hipError_t LaunchPackWeightsI8(const float* W, int8_t* Qt, float* scale, size_t K, size_t N,
                                hipStream_t s);
 hipError_t LaunchGemmW8A8(const int8_t* QA, const float* sa, const int8_t* QWt, const float* sw,
-                          float* C, int32_t* acc, size_t M, size_t N, size_t K, hipStream_t s);
+                          float* C, int32_t* acc, size_t M, size_t N, size_t K,
+                          const TilePolicy& policy, hipStream_t s);
 
 // Attention (k_attention.hip).  dtype 0 = f32 exact family, 1 = bf16 MFMA.
 hipError_t LaunchAttnFwdTiled(int dtype, const float* q, const float* k, const float* v, float* o,

@@ -409,14 +409,23 @@ hipError_t LaunchWeightShadow(const GemmArgs& a, void* out, hipStream_t s) {
   return hipGetLastError();
 }
 
-// 256 x 256 tiles (eight waves of 128 x 64) where they give at least one
-// tile per CU; otherwise 128 x 128 (four waves of 64 x 64).
+// 256 x 256 tiles (eight waves of 128 x 64) where the grid has at least the
+// policy's relaxed_min_tiles_256 of them (default 256: one per CU) and they
+// fill the CUs' last round of tiles to at least relaxed_min_fill_256 percent
+// (384 tiles on 256 CUs: 75 %); otherwise
+// 128 x 128 (four waves of 64 x 64).  Both accumulate each output over k in
+// the same 16-deep MFMA steps: the same bits.
 hipError_t LaunchGemmBf16Dma(const void* A, const void* W, const GemmArgs& a, hipStream_t s) {
   const size_t Kp = Bf16DmaKp(a.K);
   const auto* Ab = static_cast<const __bf16*>(A);
   const auto* Wb = static_cast<const __bf16*>(W);
   const size_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
-  if (t256 >= 256) return Launch<256, 256, 2, 4, 4>(Ab, Wb, Kp, a, s);
+  const size_t min256 = a.policy ? a.policy->relaxed_min_tiles_256 : 256;
+  const int fill = a.policy ? a.policy->relaxed_min_fill_256 : 0;
+  const size_t cus = static_cast<size_t>(DeviceCUs());
+  const size_t rounds = (t256 + cus - 1) / cus;
+  const bool full = 100 * t256 >= static_cast<size_t>(fill) * rounds * cus;
+  if (t256 >= min256 && full) return Launch<256, 256, 2, 4, 4>(Ab, Wb, Kp, a, s);
   return Launch<128, 128, 2, 2, 4>(Ab, Wb, Kp, a, s);
 }
 

@@ -972,14 +972,8 @@ hipError_t LaunchChain(const GemmArgs& a, hipStream_t s) {
 bool LongK(const GemmArgs& a) { return a.layout != 1 && a.M * a.N <= 16384 && a.K >= 1024; }
 
 // Where both apply, the two-pass workspace form runs before the chain
-// kernel unless SEEAI_EXACT_LONGK=0 (a same-session comparison switch).
-bool LongKFirst() {
-  static const bool first = [] {
-    const char* e = std::getenv("SEEAI_EXACT_LONGK");
-    return !(e && e[0] == '0');
-  }();
-  return first;
-}
+// kernel unless the tile policy puts the chain kernel first.
+bool LongKFirst(const GemmArgs& a) { return !a.policy || a.policy->exact_longk_first != 2; }
 
 template <int kLayout, int kBKind>
 hipError_t Run(const GemmArgs& a, hipStream_t s) {
@@ -997,7 +991,7 @@ hipError_t Run(const GemmArgs& a, hipStream_t s) {
   }
   if constexpr (kLayout == 2 && kBKind == 0)
     if (Fold(a)) return LaunchFold<kLayout>(a, s);
-  if (Chain(a) && !(kLayout != 1 && LongK(a) && a.scratch && LongKFirst())) {
+  if (Chain(a) && !(kLayout != 1 && LongK(a) && a.scratch && LongKFirst(a))) {
     if (a.N <= 8) return LaunchChain<kLayout, kBKind, 32, 8>(a, s);
     if (a.M <= 8) return LaunchChain<kLayout, kBKind, 8, 32>(a, s);
     return LaunchChain<kLayout, kBKind, 16, 16>(a, s);

@@ -14,7 +14,8 @@
 // QWt [N, K] (K contiguous: both MFMA operands then read 16 contiguous
 // bytes per lane).
 //
-// Large M (M, N >= 2048, K a multiple of 64): GemmI8DmaKernel, a 256 x 256
+// Large M (M, N >= the tile policy's w8a8_large_min, 4096 by default; K a
+// multiple of 64): GemmI8DmaKernel, a 256 x 256
 // tile per workgroup of eight waves (two per SIMD, blocks of 128 x 64 on
 // v_mfma_i32_32x32x32_i8), K staged 64 bytes at a time through four LDS
 // buffers filled by direct-to-LDS buffer loads, three stages in flight;
@@ -26,6 +27,8 @@
 // straight from global memory (each weight byte is read once), then summed
 // through LDS -- the weight stream is the whole cost, spread over N/16
 // workgroups.
+#include <algorithm>
+#include <atomic>
 #include <cfloat>
 #include <cstdlib>
 
@@ -103,6 +106,99 @@ QuantizeRowsKernel(const float* __restrict__ X, int8_t* __restrict__ Q, float* _
       *reinterpret_cast<uint32_t*>(q + c) = PackLevels(*reinterpret_cast<const float4*>(x + c), s);
   } else {
     for (size_t c = threadIdx.x; c < cols; c += kQThreads) q[c] = QuantLevel(x[c], s);
+  }
+}
+
+// The level of x at scale s from the reciprocal: a = fl(x * fl(1/s)) is
+// within 2^-24 + 2^-24 (relative) of x / s, so for |x / s| <= 128 it lies
+// within 2^-15 of the correctly rounded quotient fl(x / s).  Round-half-away
+// and the clamp can then only disagree when a is within 2^-15 of a half
+// integer; a group of four with any element inside 2^-12 of one is redone by
+// the true division (QuantLevel).  So the levels are bitwise QuantLevel(x, s)
+// for every |x| <= 128 s, which the row's own max guarantees (NaN and
+// infinities give what the division gives: inf * 0 and inf / inf are both
+// NaN, clamped alike).
+__device__ __forceinline__ uint32_t LevelByteFast(float x, float inv, bool& near) {
+  const float a = x * inv;
+  near = near || fabsf(fabsf(a - truncf(a)) - 0.5f) < 0x1p-12f;
+  const float l = fminf(fmaxf(roundf(a), -127.0f), 127.0f);
+  return static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(l)));
+}
+
+__device__ __forceinline__ uint32_t PackLevelsInv(float4 v, float s, float inv) {
+  bool near = false;
+  const uint32_t w = LevelByteFast(v.x, inv, near) | (LevelByteFast(v.y, inv, near) << 8) |
+                     (LevelByteFast(v.z, inv, near) << 16) | (LevelByteFast(v.w, inv, near) << 24);
+  return near ? PackLevels(v, s) : w;
+}
+
+// Rows of at most 256 * kR floats (16-byte aligned, a multiple of 4): each
+// wave walks rows g, g + W, g + 2W, ... (W waves in the grid) with the next
+// row's loads in flight while it quantizes the current one.  Lane l holds
+// float4 chunks l, l + 64, ... of a row, read by buffer loads over a range of
+// exactly that row: chunks past the row end, and the whole of a row past the
+// matrix end (the last prefetch), read as zeros without touching memory, so
+// every load is issued unconditionally.  The max is a butterfly inside the
+// wave (no LDS, no barrier).
+template <int kR>
+__device__ __forceinline__ void LoadRowChunks(const float* X, size_t row, size_t rows, size_t cols,
+                                              int lane, float4 (&v)[kR]) {
+  const size_t r = row < rows ? row : rows;
+  const bool live = r < rows;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(X) + (live ? r * cols : 0), 0,
+      live ? static_cast<int>(cols * 4) : 0, 0x00020000);
+#pragma unroll
+  for (int i = 0; i < kR; ++i) {
+    const auto q = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + i * kWave) * 16, 0, 0);
+    v[i] = *reinterpret_cast<const float4*>(&q);
+  }
+}
+
+template <int kR>
+__device__ __forceinline__ void QuantizeRowChunks(const float4 (&v)[kR], int8_t* q, float* scale,
+                                                  size_t cols, int lane) {
+  float mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kR; ++i) {
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+  }
+  mx = WaveMaxF(mx);
+  const float s = QuantScale(mx);
+  const float inv = 1.0f / s;
+  if (lane == 0) *scale = s;
+  // The level bytes leave through a buffer range of exactly this row: the
+  // stores of chunks past its end are dropped by the range check.
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(q, 0, static_cast<int>(cols), 0x00020000);
+#pragma unroll
+  for (int i = 0; i < kR; ++i)
+    __builtin_amdgcn_raw_buffer_store_b32(PackLevelsInv(v[i], s, inv), rs, (lane + i * kWave) * 4,
+                                          0, 0);
+}
+
+template <int kR>
+__global__ void __launch_bounds__(kQThreads)
+QuantizeRowsWaveKernel(const float* __restrict__ X, int8_t* __restrict__ Q,
+                       float* __restrict__ scale, size_t rows, size_t cols) {
+  const int lane = threadIdx.x % kWave;
+  const size_t W = static_cast<size_t>(gridDim.x) * (kQThreads / kWave);
+  // The row index is wave-uniform: kept in scalar registers, so the buffer
+  // ranges built from it need no per-lane resolution.
+  size_t r = static_cast<size_t>(
+      Uniform(static_cast<int>(blockIdx.x * (kQThreads / kWave) + threadIdx.x / kWave)));
+  if (r >= rows) return;
+  float4 a[kR], b[kR];
+  LoadRowChunks<kR>(X, r, rows, cols, lane, a);
+  for (;;) {
+    LoadRowChunks<kR>(X, r + W, rows, cols, lane, b);
+    QuantizeRowChunks<kR>(a, Q + r * cols, scale + r, cols, lane);
+    r += W;
+    if (r >= rows) break;
+    LoadRowChunks<kR>(X, r + W, rows, cols, lane, a);
+    QuantizeRowChunks<kR>(b, Q + r * cols, scale + r, cols, lane);
+    r += W;
+    if (r >= rows) break;
   }
 }
 
@@ -668,9 +764,39 @@ inline bool Aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintp
 
 }  // namespace
 
+int DeviceCUs() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 hipError_t LaunchQuantizeRows(const float* X, int8_t* Q, float* scale, size_t rows, size_t cols,
-                              hipStream_t s) {
+                              int waves_per_cu, hipStream_t s) {
   if (rows == 0) return hipSuccess;
+  if (cols > 0 && cols % 4 == 0 && Aligned(X, 16) && Aligned(Q, 4) && cols <= 16 * 256 &&
+      rows < (size_t{1} << 31)) {
+    // waves_per_cu waves per compute unit walk the rows (at least one row each).
+    const int cus = DeviceCUs();
+    const size_t waves = std::min(rows, static_cast<size_t>(cus) * static_cast<size_t>(waves_per_cu > 0 ? waves_per_cu : 32));
+    const size_t per_wg = kQThreads / kWave;
+    const dim3 grid(static_cast<unsigned>((waves + per_wg - 1) / per_wg));
+    if (cols <= 4 * 256)
+      hipLaunchKernelGGL(QuantizeRowsWaveKernel<4>, grid, dim3(kQThreads), 0, s, X, Q, scale,
+                         rows, cols);
+    else if (cols <= 8 * 256)
+      hipLaunchKernelGGL(QuantizeRowsWaveKernel<8>, grid, dim3(kQThreads), 0, s, X, Q, scale,
+                         rows, cols);
+    else
+      hipLaunchKernelGGL(QuantizeRowsWaveKernel<16>, grid, dim3(kQThreads), 0, s, X, Q, scale,
+                         rows, cols);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(QuantizeRowsKernel, dim3(static_cast<unsigned>(rows)), dim3(kQThreads), 0, s,
                      X, Q, scale, cols);
   return hipGetLastError();
@@ -689,7 +815,8 @@ hipError_t LaunchPackWeightsI8(const float* W, int8_t* Qt, float* scale, size_t 
 }
 
 hipError_t LaunchGemmW8A8(const int8_t* QA, const float* sa, const int8_t* QWt, const float* sw,
-                          float* C, int32_t* acc, size_t M, size_t N, size_t K, hipStream_t s) {
+                          float* C, int32_t* acc, size_t M, size_t N, size_t K,
+                          const TilePolicy& policy, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
   const bool vec_ok = K % 16 == 0 && Aligned(QA, 16) && Aligned(QWt, 16) && M < (1u << 30) &&
                       N < (1u << 30) && K < (1u << 30) && M * K < (1ull << 31) &&
@@ -705,19 +832,17 @@ hipError_t LaunchGemmW8A8(const int8_t* QA, const float* sa, const int8_t* QWt, 
     return hipGetLastError();
   }
   if (vec_ok) {
-    // Tile geometry: 256 x 256 (16 waves of 64 x 64, four per SIMD) once the
-    // grid still fills the chip, else 128 x 128 (4 waves).  SEEAI_I8_TILE=128|256 overrides
-    // (measurement sweeps).
-    static const int forced = [] {
-      const char* e = std::getenv("SEEAI_I8_TILE");
-      return e ? std::atoi(e) : 0;
-    }();
-    const bool big = forced ? forced >= 256 : (M >= 2048 && N >= 2048);
-    if (big && K >= kDmaBK && K % kDmaBK == 0 && K * 256 < (1ull << 31) && forced != 257) {
+    // Tile geometry (TilePolicy): from M, N >= w8a8_large_min the policy's
+    // large kernel -- by default the direct-to-LDS 256 x 256 when K is a
+    // multiple of its 64-byte stage -- else 128 x 128 (four waves).
+    const bool big = M >= policy.w8a8_large_min && N >= policy.w8a8_large_min;
+    const int pick = !big ? 3 : policy.w8a8_large_kernel;
+    const bool dma_ok = K >= kDmaBK && K % kDmaBK == 0 && K * 256 < (1ull << 31);
+    if (pick == 1 && dma_ok) {
       const unsigned tiles = static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256));
       hipLaunchKernelGGL((GemmI8DmaKernel<4, 2, 4>), dim3(tiles), dim3(512), 0, s, QA, sa, QWt, sw, C,
                          acc, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
-    } else if (big) {
+    } else if (pick <= 2) {
       const unsigned tiles = static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256));
       hipLaunchKernelGGL((GemmI8TileKernel<256, 256, 128, 4, 4>), dim3(tiles), dim3(1024), 0, s, QA,
                          sa, QWt, sw, C, acc, static_cast<int>(M), static_cast<int>(N),

@@ -59,6 +59,14 @@ class StepParams(C.Structure):
                 ("reserved", C.c_uint32), ("step", C.c_uint64)]
 
 
+class TilePolicy(C.Structure):
+    """seeai_tile_policy: the gfx950 kernel geometry (fields as in
+    see-ai_amd/policy.py; 0 keeps a default)."""
+    _fields_ = [("w8a8_large_kernel", C.c_uint32), ("w8a8_large_min", C.c_uint32),
+                ("quantize_waves_per_cu", C.c_uint32), ("relaxed_min_tiles_256", C.c_uint32),
+                ("relaxed_min_fill_256", C.c_uint32), ("exact_longk_first", C.c_uint32)]
+
+
 # Every exported symbol with its ctypes signature: the header, one to one.
 EXPORTS = {
     "seeai_create": (_I, [_I, C.POINTER(_P)]),
@@ -81,6 +89,9 @@ EXPORTS = {
     "seeai_set_fusion": (_I, [_P, _I]),
     "seeai_fused_dispatches": (_U64, [_P]),
     "seeai_flush": (_I, [_P]),
+    "seeai_configure": (_I, [_P, C.POINTER(TilePolicy)]),
+    "seeai_policy": (_I, [_P, C.POINTER(TilePolicy)]),
+    "seeai_device_key": (_I, [_I, C.c_char_p, _U64]),
     "seeai_gemm_f32": (_I, [_P, _I, _P, _P, _P, _U64, _U64, _U64, _P, _I, _P, _F, _I]),
     "seeai_gemm_q8": (_I, [_P, _I, _P, _P, _P, _U64, _U64, _U64, _F, _P, _I]),
     "seeai_gemm_bf16w": (_I, [_P, _I, _P, _P, _P, _U64, _U64, _U64, _P, _I]),
@@ -142,6 +153,38 @@ def ptr(t) -> int | None:
     return t.data_ptr()
 
 
+def device_key(device: int = 0) -> str:
+    """The device's kernel-policy table key (the GPU's HostKey)."""
+    buf = C.create_string_buffer(512)
+    rc = _lib.seeai_device_key(device, buf, _U64(512))
+    if rc != OK:
+        raise BackendError(rc, f"seeai_device_key({device}) failed with status {rc}")
+    return buf.value.decode("utf-8", "replace")
+
+
+def _policy_struct(policy) -> "TilePolicy | None":
+    if policy is None:
+        return None
+    if isinstance(policy, TilePolicy):
+        return policy
+    return TilePolicy(**{k: int(v) for k, v in policy.items()})
+
+
+def _configure(ctx_handle, policy):
+    p = _policy_struct(policy)
+    rc = _lib.seeai_configure(ctx_handle, C.byref(p) if p is not None else None)
+    if rc != OK:
+        raise BackendError(rc, _lib.seeai_last_error(ctx_handle).decode("utf-8", "replace"))
+
+
+def _policy_of(ctx_handle) -> dict:
+    p = TilePolicy()
+    rc = _lib.seeai_policy(ctx_handle, C.byref(p))
+    if rc != OK:
+        raise BackendError(rc, "seeai_policy failed")
+    return {name: int(getattr(p, name)) for name, _ in TilePolicy._fields_}
+
+
 class Context:
     """One seeai_ctx: a device, a stream, scratch and (optionally) an arena."""
 
@@ -170,6 +213,14 @@ class Context:
 
     def call(self, name: str, *args):
         self.check(getattr(_lib, name)(self.h, *args))
+
+    def configure(self, policy=None):
+        """seeai_configure: a policy dict (see-ai_amd/policy.py fields), a
+        TilePolicy, or None for the defaults."""
+        _configure(self.h, policy)
+
+    def policy(self) -> dict:
+        return _policy_of(self.h)
 
     def use_torch_stream(self):
         """Enqueue on torch's current stream (0 is the null stream) so torch's
@@ -210,8 +261,12 @@ class HipBackend:
         buf = C.create_string_buffer(bytes(data), len(data))
         self.ctx.call("seeai_bind_source", buf, _U64(len(data)))
 
-    def Configure(self, policy=None):  # backend.h:117 -- the GPU keeps its own tiles
-        return None
+    def Configure(self, policy=None):
+        """backend.h:117, called after every successful Bind: the gfx950
+        member of the kernel-policy table (a dict from policy.resolve), or
+        None for the built-in geometry.  The plan header's CPU tiles
+        (gemm_tile_k / n) do not apply to this backend."""
+        self.ctx.configure(policy)
 
     def Execute(self, instruction: bytes, params: StepParams | None = None):
         assert len(instruction) == 64
@@ -390,6 +445,13 @@ class Engine:
 
     def fused_dispatches(self) -> int:
         return int(_lib.seeai_fused_dispatches(_lib.seeai_engine_context(self.h)))
+
+    def configure(self, policy=None):
+        """The backend's kernel geometry (HipBackend.Configure)."""
+        _configure(_lib.seeai_engine_context(self.h), policy)
+
+    def policy(self) -> dict:
+        return _policy_of(_lib.seeai_engine_context(self.h))
 
     def set_fusion(self, allow: bool):
         """Whether adjacent relaxed dK / dV instructions run as one dispatch."""

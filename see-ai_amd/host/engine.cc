@@ -70,7 +70,7 @@ Result<std::unique_ptr<PlanEngine>> PlanEngine::Load(std::span<const uint8_t> bl
                                  e->plan_.rodata.size(), e->plan_.rodata.size());
       !r)
     return Fail(r.error());
-  e->backend_->Configure();
+  if (auto r = e->backend_->Configure(); !r) return Fail(r.error());
   return e;
 }
 

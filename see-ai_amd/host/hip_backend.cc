@@ -46,6 +46,10 @@ Result<void> HipBackend::BindSource(const uint8_t* data, uint64_t bytes) {
   return Check(seeai_bind_source(ctx_, data, bytes));
 }
 
+Result<void> HipBackend::Configure(const seeai_tile_policy* policy) {
+  return Check(seeai_configure(ctx_, policy));
+}
+
 Result<void> HipBackend::Execute(const Instruction& ins, const StepParams& p) {
   const seeai_step_params sp{p.lr, p.beta1, p.beta2, p.eps, p.weight_decay, 0, p.step};
   return Check(seeai_execute(ctx_, &ins, &sp));

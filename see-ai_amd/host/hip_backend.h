@@ -17,6 +17,7 @@
 #include "result.h"
 
 struct seeai_ctx;
+struct seeai_tile_policy;
 
 namespace seeai::host {
 
@@ -48,9 +49,11 @@ class HipBackend {
   Result<void> Bind(uint8_t* arena, uint64_t arena_bytes, const uint8_t* rodata,
                     uint64_t rodata_bytes, uint64_t rodata_mapped_bytes);
   Result<void> BindSource(const uint8_t* data, uint64_t bytes);
-  // backend.h:117: tile policy.  The gfx950 kernels pick their tiles per
-  // launch from the operand shapes, so the CPU tile words do not apply.
-  void Configure() {}
+  // backend.h:117: the kernel geometry, called after every successful Bind.
+  // The plan header's CPU tile words do not apply to the gfx950 kernels; the
+  // policy is the gfx950 member of the kernel-policy table (null: the
+  // built-in geometry).  Every choice gives the same bits.
+  Result<void> Configure(const seeai_tile_policy* policy = nullptr);
   Result<void> Execute(const Instruction& ins, const StepParams& params);
   // backend.h:139-142: whole-program visibility around a range.
   // The backend keeps the span until EndRange: Execute is then called with

@@ -685,6 +685,50 @@ def test_w8a8_bit_exact(hip, orc, torch_cuda, M, N, K):
     assert bits_equal(sw.cpu().numpy(), sw_c)
     assert bits_equal(acc.cpu().numpy(), acc_c), "int32 accumulators"
     assert bits_equal(C.cpu().numpy(), C_c), "dequantized output"
+    # from M, N >= 2048 on: the large kernels (the direct-to-LDS one where
+    # K % 64 == 0), which the built-in policy keeps for M, N >= 4096
+    ctx.configure({"w8a8_large_min": 2048})
+    C.fill_(float("nan"))
+    acc.zero_()
+    ctx.call("seeai_w8a8_gemm", QA.data_ptr(), sa.data_ptr(), QWt.data_ptr(), sw.data_ptr(),
+             C.data_ptr(), acc.data_ptr(), M, N, K)
+    torch.cuda.synchronize()
+    assert bits_equal(acc.cpu().numpy(), acc_c), "int32 accumulators (large kernels)"
+    assert bits_equal(C.cpu().numpy(), C_c), "dequantized output (large kernels)"
+    ctx.close()
+
+
+@pytest.mark.parametrize("cols", [1024, 2052, 4096, 4100])
+def test_w8a8_quantizer_on_half_level_quotients(hip, orc, torch_cuda, cols):
+    """Every element's quotient x / scale sits within a few ulps of a half
+    integer, where round-half-away decides the level; the levels and scales
+    must still be the oracle's bit for bit (the wave-per-row quantizer takes
+    the true division there, the reciprocal elsewhere)."""
+    torch = torch_cuda
+    rows = 96
+    r = rng(cols)
+    s0 = np.float32(10.0) ** r.uniform(-4, 2, rows).astype(np.float32)
+    k = r.integers(0, 127, (rows, cols)).astype(np.float32)
+    X = (k + np.float32(0.5)) * s0[:, None]
+    ulps = r.integers(-3, 4, (rows, cols))
+    for step in range(1, 4):
+        up, dn = ulps >= step, ulps <= -step
+        X[up] = np.nextafter(X[up], np.float32(np.inf))
+        X[dn] = np.nextafter(X[dn], np.float32(-np.inf))
+    X *= np.where(r.random((rows, cols)) < 0.5, np.float32(-1), np.float32(1))
+    X[:, 0] = np.float32(127) * s0  # fixes the row max (and with it the scale near s0)
+    X[1, :] = 0.0
+    X = X.astype(np.float32)
+    Q_c, s_c = orc.quantize_rows(X)
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    dX = torch.from_numpy(X).cuda()
+    Q = torch.empty((rows, cols), dtype=torch.int8, device="cuda")
+    s = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.call("seeai_w8a8_quantize_rows", dX.data_ptr(), Q.data_ptr(), s.data_ptr(), rows, cols)
+    torch.cuda.synchronize()
+    assert bits_equal(s.cpu().numpy(), s_c)
+    assert bits_equal(Q.cpu().numpy(), Q_c)
     ctx.close()
 
 
