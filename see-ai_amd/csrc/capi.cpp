@@ -89,9 +89,14 @@ struct seeai_ctx {
   // BeginRange): lets two adjacent instructions run as one dispatch.
   const uint8_t* prog = nullptr;
   uint64_t prog_count = 0, range_end = 0;
-  const uint8_t* done = nullptr;  // the next instruction, already run by a fused dispatch
+  // Instructions of the range already run by a fused dispatch, in the order
+  // the engine will present them (at most two: a LoRA site's t product and
+  // rank-r product).
+  const uint8_t* done[2] = {nullptr, nullptr};
+  int ndone = 0;
   int allow_fusion = 1;
   int allow_dma = 1;  // relaxed frozen-weight GEMMs on the bf16 shadow path
+  int allow_lowrank = 1;  // LoRA sites folded into the frozen product's epilogue
   TilePolicy policy;  // kernel geometry (seeai_configure)
   uint64_t fused = 0;
   // bf16 copies [N, Kp] of frozen weights for the relaxed GEMMs, keyed by
@@ -280,71 +285,55 @@ int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   Relaxed(c, nx);
   SEEAI_TRY(c, LaunchAttnDKDVFused(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
             "attn.dkdv_fused");
-  c->done = at + 64;
+  c->done[0] = at + 64;
+  c->ndone = 1;
   ++c->fused;
   return SEEAI_OK;
 }
 
-int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P) {
-  if (!c->arena) return Fail(c, SEEAI_INVALID, "execute: no arena is bound");
+// A GEMM instruction's operands (every GEMM opcode; the caller sets
+// `relaxed`).  Returns the op's name for messages, or null for another opcode.
+const char* DecodeGemm(seeai_ctx* c, const Instruction& ins, GemmArgs* out) {
   const Ptrs R{c};
-  hipStream_t s = c->stream;
   const int act = (ins.flags >> 1) & 3;
   const float alpha = ins.imm == 0 ? 1.0f : BitsToF32(ins.imm);
-  const float norm_eps = ins.imm == 0 ? 1e-5f : BitsToF32(ins.imm);
-  const uint64_t hi0 = ins.out[0] >> 32, lo0 = ins.out[0] & 0xFFFFFFFFu;
+  GemmArgs a{};
+  a.A = R.f(ins.in[0]);
+  a.C = R.f(ins.in[2]);
+  a.M = ins.out[0];
+  a.N = ins.out[1];
+  a.K = ins.out[2];
+  const char* what = nullptr;
   switch (ins.opcode) {
-    case 0:  // kNop
-      return SEEAI_OK;
     case 1:    // kGemmNN
     case 2:    // kGemmNT
-    case 3: {  // kGemmTN
-      GemmArgs a{};
+    case 3:    // kGemmTN
       a.layout = ins.opcode - 1;
       a.b_kind = 0;
-      a.A = R.f(ins.in[0]);
       a.B = R.f(ins.in[1]);
-      a.C = R.f(ins.in[2]);
-      a.M = ins.out[0];
-      a.N = ins.out[1];
-      a.K = ins.out[2];
       // instruction.h:384-404: NN / TN fold alpha into A, NT onto the dot.
       a.alpha_a = ins.opcode == 2 ? 1.0f : alpha;
       a.alpha_dot = ins.opcode == 2 ? alpha : 1.0f;
       a.addend = (ins.flags & kFlagGemmAddend) ? R.f(ins.in[3]) : nullptr;
       a.bias = (ins.opcode == 1 && (ins.flags & kFlagEpilogueBias)) ? R.f(ins.in[3]) : nullptr;
       a.act = ins.opcode == 1 ? act : 0;
-      a.relaxed = Relaxed(c, ins);
-      return Gemm(c, a, "gemm");
-    }
-    case 4: {  // kGemmAccNN: C += alpha A@B, alpha bits in in[3]
-      GemmArgs a{};
+      what = "gemm";
+      break;
+    case 4:  // kGemmAccNN: C += alpha A@B, alpha bits in in[3]
       a.layout = 0;
-      a.A = R.f(ins.in[0]);
       a.B = R.f(ins.in[1]);
-      a.C = R.f(ins.in[2]);
-      a.M = ins.out[0];
-      a.N = ins.out[1];
-      a.K = ins.out[2];
       a.alpha_a = BitsToF32(ins.in[3]);
       a.alpha_dot = 1.0f;
       a.accumulate = 1;
-      a.relaxed = Relaxed(c, ins);
-      return Gemm(c, a, "gemm.acc_nn");
-    }
+      what = "gemm.acc_nn";
+      break;
     case 29:    // kGemmNNQ8
     case 30: {  // kGemmNTQ8
       const bool nt = ins.opcode == 30;
       const bool cs = (ins.flags & kFlagQ8ColScale) != 0;
-      GemmArgs a{};
       a.layout = nt ? 1 : 0;
       a.b_kind = 1;
-      a.A = R.f(ins.in[0]);
       a.B = R.at(ins.in[1]);
-      a.C = R.f(ins.in[2]);
-      a.M = ins.out[0];
-      a.N = ins.out[1];
-      a.K = ins.out[2];
       const float scale = cs ? 1.0f : BitsToF32(ins.in[3]);
       // gemm.cc:626-674: NN per-tensor scale folds into A, a column scale
       // joins the widening; NT per-tensor scale multiplies the dot, a
@@ -358,27 +347,52 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
           a.b_col_scale = R.f(ins.in[3]);
       }
       a.act = nt ? 0 : act;
-      a.relaxed = Relaxed(c, ins);
-      return Gemm(c, a, "gemm.q8");
+      what = "gemm.q8";
+      break;
     }
     case 43:    // kGemmNNBF16
     case 44: {  // kGemmNTBF16
       const bool nt = ins.opcode == 44;
-      GemmArgs a{};
       a.layout = nt ? 1 : 0;
       a.b_kind = 2;
-      a.A = R.f(ins.in[0]);
       a.B = R.at(ins.in[1]);
-      a.C = R.f(ins.in[2]);
-      a.M = ins.out[0];
-      a.N = ins.out[1];
-      a.K = ins.out[2];
       a.alpha_a = 1.0f;
       a.alpha_dot = 1.0f;
       a.bias = (!nt && (ins.flags & kFlagEpilogueBias)) ? R.f(ins.in[3]) : nullptr;
       a.act = nt ? 0 : act;
+      what = "gemm.bf16";
+      break;
+    }
+    default:
+      return nullptr;
+  }
+  *out = a;
+  return what;
+}
+
+int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P) {
+  if (!c->arena) return Fail(c, SEEAI_INVALID, "execute: no arena is bound");
+  const Ptrs R{c};
+  hipStream_t s = c->stream;
+  const int act = (ins.flags >> 1) & 3;
+  const float alpha = ins.imm == 0 ? 1.0f : BitsToF32(ins.imm);
+  const float norm_eps = ins.imm == 0 ? 1e-5f : BitsToF32(ins.imm);
+  const uint64_t hi0 = ins.out[0] >> 32, lo0 = ins.out[0] & 0xFFFFFFFFu;
+  switch (ins.opcode) {
+    case 0:  // kNop
+      return SEEAI_OK;
+    case 1:     // kGemmNN
+    case 2:     // kGemmNT
+    case 3:     // kGemmTN
+    case 4:     // kGemmAccNN
+    case 29:    // kGemmNNQ8
+    case 30:    // kGemmNTQ8
+    case 43:    // kGemmNNBF16
+    case 44: {  // kGemmNTBF16
+      GemmArgs a{};
+      const char* what = DecodeGemm(c, ins, &a);
       a.relaxed = Relaxed(c, ins);
-      return Gemm(c, a, "gemm.bf16");
+      return Gemm(c, a, what);
     }
     case 5:
       SEEAI_TRY(c, LaunchAddEW(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s), "add");
@@ -661,6 +675,10 @@ int seeai_create(int device, seeai_ctx** out) {
   // SEEAI_RELAXED_DMA=0 keeps the relaxed frozen-weight GEMMs on the
   // register-staged kernel (a same-session comparison switch).
   if (const char* e = std::getenv("SEEAI_RELAXED_DMA"); e && e[0] == '0') c->allow_dma = 0;
+  // SEEAI_UNFUSED_LOWRANK=1 keeps each LoRA site's products apart: the
+  // same-session control of the low-rank fold (the reference's Metal backend
+  // keeps SEEML_METAL_UNFUSED_LOWRANK for the same purpose).
+  if (const char* e = std::getenv("SEEAI_UNFUSED_LOWRANK"); e && e[0] == '1') c->allow_lowrank = 0;
   int rc = Hip(c, hipSetDevice(device), "set device");
   if (rc == SEEAI_OK) rc = Hip(c, hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "stream");
   if (rc == SEEAI_OK) rc = Hip(c, hipMalloc(&c->small, kSmallBytes), "small alloc");
@@ -768,18 +786,137 @@ int seeai_download(seeai_ctx* c, uint64_t off, void* dst, uint64_t bytes) {
 void* seeai_arena(seeai_ctx* c) { return c ? c->arena : nullptr; }
 uint64_t seeai_arena_bytes(const seeai_ctx* c) { return c ? c->arena_bytes : 0; }
 
+namespace {
+
+// Byte extents a GEMM reads and writes.
+struct Extent {
+  const uint8_t* p;
+  uint64_t n;
+};
+uint64_t BElem(const GemmArgs& a) { return a.b_kind == 1 ? 1 : a.b_kind == 2 ? 2 : 4; }
+int GemmReads(const GemmArgs& a, Extent* out) {
+  int k = 0;
+  const auto add = [&](const void* p, uint64_t n) {
+    if (p && n) out[k++] = {static_cast<const uint8_t*>(p), n};
+  };
+  add(a.A, a.M * a.K * 4);
+  add(a.B, a.N * a.K * BElem(a));
+  add(a.addend, a.M * a.N * 4);
+  add(a.bias, a.N * 4);
+  add(a.b_col_scale, a.N * 4);
+  add(a.a_k_scale, a.K * 4);
+  if (a.accumulate) add(a.C, a.M * a.N * 4);
+  return k;
+}
+Extent GemmWrites(const GemmArgs& a) { return {reinterpret_cast<const uint8_t*>(a.C), a.M * a.N * 4}; }
+bool Hits(const Extent& x, const Extent* set, int n) {
+  for (int i = 0; i < n; ++i)
+    if (Overlap(x.p, x.n, set[i].p, set[i].n)) return true;
+  return false;
+}
+
+// Range-level fusion of a LoRA site (the seam's whole-program visibility,
+// backend.h:139-142; the reference's Metal backend folds the same pair,
+// metal_kernels.h:290-358, docs/runtime.md:119).  A relaxed frozen-weight
+// product writing C on the direct-to-LDS kernel, followed -- next, or after
+// one exact GEMM (the site's t = x A) that neither touches C nor writes what
+// the product reads -- by an exact rank-r GEMM (NN or NT, r <= 16, no bias or
+// activation) whose addend is C, runs as one dispatch: the in-between GEMM
+// first, then the frozen product with the rank-r term in its epilogue, which
+// forms C as before, stores it, and writes C' = C + the rank-r product in the
+// rank-r instruction's own chain.  The arena holds the bytes of the separate
+// dispatches.  Refused (each runs at its place) when an output overlaps
+// anything the fused pass reads or the other output.  Returns -1 when the
+// instructions do not fuse.
+int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
+                   const seeai_step_params& P) {
+  if (!c->allow_fusion || !c->allow_lowrank || !c->allow_relaxed || !c->allow_dma || !c->prog ||
+      at < c->prog ||
+      at >= c->prog + c->prog_count * 64 || (at - c->prog) % 64 != 0)
+    return -1;
+  if (!(ins.flags & kFlagRelaxed)) return -1;
+  GemmArgs a{};
+  if (!DecodeGemm(c, ins, &a)) return -1;
+  a.relaxed = 1;
+  if (a.accumulate || !Bf16DmaFits(a) || !Immutable(c, a.B)) return -1;
+  const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
+  Extent reads_a[8];
+  const int na = GemmReads(a, reads_a);
+  const Extent out_a = GemmWrites(a);
+  for (uint64_t gap = 0; gap <= 1; ++gap) {
+    const uint64_t j = idx + 1 + gap;
+    if (j >= c->range_end) return -1;
+    Instruction nj;
+    std::memcpy(&nj, c->prog + j * 64, sizeof nj);
+    const bool exact_j = !(nj.flags & kFlagRelaxed);
+    if ((nj.opcode == 1 || nj.opcode == 2) && exact_j && (nj.flags & kFlagGemmAddend) &&
+        ((nj.flags >> 1) & 3) == 0 && nj.in[3] == ins.in[2]) {
+      GemmArgs b{};
+      DecodeGemm(c, nj, &b);
+      if (b.M != a.M || b.N != a.N || b.bias) return -1;
+      Instruction mid{};
+      GemmArgs m{};
+      if (gap) {  // the in-between instruction: an exact GEMM clear of the product
+        std::memcpy(&mid, c->prog + (idx + 1) * 64, sizeof mid);
+        if (!DecodeGemm(c, mid, &m) || ((mid.flags & kFlagRelaxed) && c->allow_relaxed))
+          return -1;
+        Extent reads_m[8];
+        const int nm = GemmReads(m, reads_m);
+        const Extent out_m = GemmWrites(m);
+        if (Hits(out_m, reads_a, na) || Overlap(out_m.p, out_m.n, out_a.p, out_a.n) ||
+            Hits(out_a, reads_m, nm))
+          return -1;
+      }
+      a.lr_t = b.A;
+      a.lr_b = static_cast<const float*>(b.B);
+      a.lr_out = b.C;
+      a.lr_layout = b.layout;
+      a.lr_k = static_cast<int>(b.K);
+      a.lr_alpha = b.layout == 0 ? b.alpha_a : b.alpha_dot;
+      a.lr_store_c = 1;
+      if (!Bf16DmaLowRankFits(a)) return -1;
+      // The fused pass reads A, the scales, t and the rank operand, writes C
+      // and C'.
+      const Extent out_b = GemmWrites(b);
+      const Extent t_b{reinterpret_cast<const uint8_t*>(b.A), b.M * b.K * 4};
+      const Extent r_b{static_cast<const uint8_t*>(b.B), b.N * b.K * 4};
+      if (Overlap(out_a.p, out_a.n, out_b.p, out_b.n) || Hits(out_a, &t_b, 1) ||
+          Hits(out_a, &r_b, 1) || Hits(out_b, reads_a, na) || Hits(out_b, &t_b, 1) ||
+          Hits(out_b, &r_b, 1))
+        return -1;
+      if (gap) {
+        if (int rc = ExecuteOne(c, mid, P)) return rc;
+      }
+      Relaxed(c, ins);
+      if (int rc = GemmBf16Dma(c, a, "gemm.low_rank")) return rc;
+      c->ndone = 0;
+      if (gap) c->done[c->ndone++] = c->prog + (idx + 1) * 64;
+      c->done[c->ndone++] = c->prog + j * 64;
+      ++c->fused;
+      return SEEAI_OK;
+    }
+  }
+  return -1;
+}
+
+}  // namespace
+
 int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params* params) {
   if (!c || !instruction) return SEEAI_INVALID;
   const auto* at = static_cast<const uint8_t*>(instruction);
-  const uint8_t* done = c->done;
-  c->done = nullptr;
-  if (at == done) return SEEAI_OK;  // ran with the previous instruction
+  if (c->ndone > 0 && at == c->done[0]) {  // ran with an earlier instruction
+    c->done[0] = c->done[1];
+    --c->ndone;
+    return SEEAI_OK;
+  }
+  c->ndone = 0;  // any other order runs every instruction as given
   Instruction ins;
   std::memcpy(&ins, instruction, sizeof ins);
   if (!c->arena) return Fail(c, SEEAI_INVALID, "execute: no arena is bound");
-  if (int rc = TryFuseAttnBwd(c, ins, at); rc >= 0) return rc;
   seeai_step_params P{};
   if (params) P = *params;
+  if (int rc = TryFuseLowRank(c, ins, at, P); rc >= 0) return rc;
+  if (int rc = TryFuseAttnBwd(c, ins, at); rc >= 0) return rc;
   return ExecuteOne(c, ins, P);
 }
 
@@ -789,7 +926,7 @@ int seeai_begin_range(seeai_ctx* c, const void* program, uint64_t count, uint64_
   c->prog = static_cast<const uint8_t*>(program);
   c->prog_count = count;
   c->range_end = end;
-  c->done = nullptr;
+  c->ndone = 0;
   return SEEAI_OK;
 }
 
@@ -797,7 +934,7 @@ int seeai_end_range(seeai_ctx* c) {
   if (!c) return SEEAI_INVALID;
   c->prog = nullptr;
   c->prog_count = c->range_end = 0;
-  c->done = nullptr;
+  c->ndone = 0;
   return SEEAI_OK;
 }
 

@@ -230,7 +230,22 @@ struct GemmArgs {
   int relaxed;               // kFlagRelaxed taken: MFMA summation order
   float* scratch;            // device workspace (GemmExactScratchBytes), or null
   const TilePolicy* policy;  // kernel geometry (null: the defaults)
+  // Low-rank epilogue (the relaxed direct-to-LDS kernel): the next
+  // instruction of a LoRA site, lr_out = C + rank-r product with C as its
+  // addend, joins this product's epilogue.  C's value is formed as without
+  // it (and stored when lr_store_c); the rank-r dot follows that
+  // instruction's exact chain -- NN: quads of (lr_alpha * t) * b from k = 0,
+  // then the tail; NT: eight lanes by k mod 8 added in order, times
+  // lr_alpha -- and the addend comes first: lr_out = C + dot.
+  const float* lr_t;   // [M, lr_k]
+  const float* lr_b;   // NN: [lr_k, N]; NT: [N, lr_k]
+  float* lr_out;       // [M, N]; null: no low-rank epilogue
+  int lr_layout;       // 0 NN, 1 NT
+  int lr_k;            // 1..kLowRankMaxK
+  int lr_store_c;      // also store C
+  float lr_alpha;
 };
+constexpr int kLowRankMaxK = 16;
 // Relaxed -> MFMA (k_gemm_f32.hip); otherwise the reference's order.
 hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s);
 hipError_t LaunchGemmExact(const GemmArgs& a, hipStream_t s);
@@ -241,6 +256,9 @@ size_t GemmExactScratchBytes(const GemmArgs& a);
 // scales, the weight's bf16 shadow [N, Kp] made once; Kp = K rounded up to 32.
 size_t Bf16DmaKp(size_t K);
 bool Bf16DmaFits(const GemmArgs& a);
+// Whether the low-rank epilogue can join this product (N % 4 == 0, rank
+// operands 16-byte aligned, 1 <= lr_k <= kLowRankMaxK).
+bool Bf16DmaLowRankFits(const GemmArgs& a);
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,
                                  const float* kscale, void* out, hipStream_t s);
 hipError_t LaunchWeightShadow(const GemmArgs& a, void* out, hipStream_t s);

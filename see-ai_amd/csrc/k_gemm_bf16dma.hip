@@ -67,9 +67,46 @@ __device__ __forceinline__ void TileOf(int b, int tiles_m, int tiles_n, int& tm,
 
 __device__ __forceinline__ float ActF(int act, float v) { return act ? ActExpr(act, v) : v; }
 
-template <int BM, int BN, int WGM, int WGN, int kStages>
+__device__ __forceinline__ float MulRn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float AddRn(float a, float b) { return __fadd_rn(a, b); }
+
+// The low-rank term of one output: the rank-r product's exact chain over
+// the row's t values and the column's rank-operand values (GemmArgs).
+template <int kLayout>
+__device__ __forceinline__ float LowRankDot(const float (&t)[kLowRankMaxK],
+                                            const float (&b)[kLowRankMaxK], int r, float alpha) {
+  if constexpr (kLayout == 0) {  // quads of (alpha t) b from k = 0 (r % 4 == 0: no tail)
+    float c = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kLowRankMaxK; k += 4) {
+      if (k < r) {
+        float a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = alpha != 1.0f ? MulRn(alpha, t[k + u]) : t[k + u];
+        c = AddRn(c, AddRn(AddRn(AddRn(MulRn(a[0], b[k]), MulRn(a[1], b[k + 1])),
+                                 MulRn(a[2], b[k + 2])), MulRn(a[3], b[k + 3])));
+      }
+    }
+    return c;
+  } else {  // eight lanes by k mod 8, added in lane order, then alpha
+    // Lane l holds 0 + t[l] b[l] (+ t[l+8] b[l+8]); each lane is formed
+    // just before it joins the running sum, so few values are live at once.
+    float c = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      float lane = 0.0f;
+      if (l < r) lane = AddRn(lane, MulRn(t[l], b[l]));
+      if (l + 8 < r) lane = AddRn(lane, MulRn(t[l + 8], b[l + 8]));
+      c = l == 0 ? lane : AddRn(c, lane);
+    }
+    return MulRn(alpha, c);
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, int kStages, int kLR>
 __global__ void __launch_bounds__(WGM * WGN * kWave)
 GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, int Kp, GemmArgs g) {
+  // kLR: 0 none, 1 NN low-rank epilogue, 2 NT low-rank epilogue.
   constexpr int kWaves = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -216,6 +253,30 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
   const float* __restrict__ add = g.addend;
   const float* __restrict__ bias = g.bias;
   float* __restrict__ C = g.C;
+  constexpr int kVecRow = WN / 4;
+  static_assert(kWave % kVecRow == 0, "a lane keeps one column quad through the epilogue");
+  // Low-rank epilogue: this lane's four columns of the rank operand, every k,
+  // in registers for the whole epilogue (its column quad never changes).
+  float lb[4][kLowRankMaxK];
+  const int lr_r = kLR ? g.lr_k : 0;
+  if constexpr (kLR != 0) {
+    const int nl = n0 + wn + (lane % kVecRow) * 4;
+#pragma unroll
+    for (int k = 0; k < kLowRankMaxK; ++k) {
+      float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (k < lr_r && nl < N) {
+        if constexpr (kLR == 1) {
+          b = *reinterpret_cast<const float4*>(g.lr_b + static_cast<size_t>(k) * N + nl);
+        } else {
+          b.x = g.lr_b[static_cast<size_t>(nl) * lr_r + k];
+          b.y = g.lr_b[static_cast<size_t>(nl + 1) * lr_r + k];
+          b.z = g.lr_b[static_cast<size_t>(nl + 2) * lr_r + k];
+          b.w = g.lr_b[static_cast<size_t>(nl + 3) * lr_r + k];
+        }
+      }
+      lb[0][k] = b.x, lb[1][k] = b.y, lb[2][k] = b.z, lb[3][k] = b.w;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int mb = m0 + wm + i * 32;
@@ -226,7 +287,6 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
 #pragma unroll
         for (int e = 0; e < 4; ++e) stage[(8 * q + 4 * h + e) * SLD + j * 32 + lr] = acc[i][j][4 * q + e];
     __builtin_amdgcn_wave_barrier();
-    constexpr int kVecRow = WN / 4;
 #pragma unroll
     for (int t = 0; t < 32 * kVecRow / kWave; ++t) {
       const int idx = lane + t * kWave;
@@ -249,7 +309,23 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
         if (bias) x = x + bias[n + e];
         v[e] = ActF(g.act, x);
       }
-      if (vec) {
+      if constexpr (kLR != 0) {
+        // N % 4 == 0 here: the whole quad is in range.
+        if (g.lr_store_c) *reinterpret_cast<float4*>(C + o) = make_float4(v[0], v[1], v[2], v[3]);
+        float t[kLowRankMaxK];
+        const float* __restrict__ tr = g.lr_t + static_cast<size_t>(m) * lr_r;
+#pragma unroll
+        for (int k = 0; k < kLowRankMaxK; k += 4) {
+          float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (k < lr_r) q = *reinterpret_cast<const float4*>(tr + k);
+          t[k] = q.x, t[k + 1] = q.y, t[k + 2] = q.z, t[k + 3] = q.w;
+        }
+        float o4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o4[e] = AddRn(v[e], LowRankDot<kLR - 1>(t, lb[e], lr_r, g.lr_alpha));
+        *reinterpret_cast<float4*>(g.lr_out + o) = make_float4(o4[0], o4[1], o4[2], o4[3]);
+      } else if (vec) {
         *reinterpret_cast<float4*>(C + o) = make_float4(v[0], v[1], v[2], v[3]);
       } else {
         for (int e = 0; e < cnt; ++e) C[o + e] = v[e];
@@ -355,8 +431,16 @@ ShadowKernel(const void* __restrict__ W, size_t N, size_t K, size_t Kp, __bf16* 
 template <int BM, int BN, int WGM, int WGN, int kStages>
 hipError_t Launch(const __bf16* A, const __bf16* W, size_t Kp, const GemmArgs& g, hipStream_t s) {
   const size_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  hipLaunchKernelGGL((GemmBf16DmaKernel<BM, BN, WGM, WGN, kStages>), dim3(static_cast<unsigned>(tiles)),
-                     dim3(WGM * WGN * kWave), 0, s, A, W, static_cast<int>(Kp), g);
+  const dim3 grid(static_cast<unsigned>(tiles)), block(WGM * WGN * kWave);
+  if (!g.lr_out)
+    hipLaunchKernelGGL((GemmBf16DmaKernel<BM, BN, WGM, WGN, kStages, 0>), grid, block, 0, s, A, W,
+                       static_cast<int>(Kp), g);
+  else if (g.lr_layout == 0)
+    hipLaunchKernelGGL((GemmBf16DmaKernel<BM, BN, WGM, WGN, kStages, 1>), grid, block, 0, s, A, W,
+                       static_cast<int>(Kp), g);
+  else
+    hipLaunchKernelGGL((GemmBf16DmaKernel<BM, BN, WGM, WGN, kStages, 2>), grid, block, 0, s, A, W,
+                       static_cast<int>(Kp), g);
   return hipGetLastError();
 }
 
@@ -376,6 +460,13 @@ bool Bf16DmaFits(const GemmArgs& a) {
   if (Kp * 2 * 256 >= (size_t{1} << 31) || a.M >= (size_t{1} << 30) || a.N >= (size_t{1} << 30))
     return false;
   return ((a.M + 127) / 128) * ((a.N + 127) / 128) < (size_t{1} << 31);
+}
+
+bool Bf16DmaLowRankFits(const GemmArgs& a) {
+  const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return a.lr_out && a.lr_t && a.lr_b && a.lr_layout >= 0 && a.lr_layout <= 1 && a.lr_k >= 1 &&
+         a.lr_k <= kLowRankMaxK && a.lr_k % 4 == 0 && a.N % 4 == 0 && !a.accumulate &&
+         al16(a.lr_t) && al16(a.lr_out) && al16(a.C) && (a.lr_layout == 1 || al16(a.lr_b));
 }
 
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,

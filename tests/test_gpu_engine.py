@@ -216,6 +216,31 @@ def test_decoder_fused_backward_is_bitwise_the_separate_passes(hip, torch_cuda):
 TINY_Q8 = dict(vocab=96, dim=128, heads=2, ffn=352, layers=2, seq=64, batch=2, rank=16)
 
 
+def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch_cuda):
+    """On the int8-base decoder the range fusions include the LoRA sites'
+    low-rank epilogue (the frozen Q / K / V / O products with the rank-r
+    term folded in) beside the dK / dV pairs: three steps with fusion on and
+    off give the same losses and persistent bytes."""
+    T = TINY_Q8["batch"] * TINY_Q8["seq"]
+    curves, states, fused = [], [], []
+    for allow in (True, False):
+        img = pw.decoder_q8_lora(hip.plan_self_hash, relaxed=True, **TINY_Q8)
+        eng = hip.Engine(img.blob)
+        eng.set_fusion(allow)
+        curve = []
+        for s in range(3):
+            t = pw.uniform_ints(7100 + s, T + 1, TINY_Q8["vocab"])
+            curve.append(eng.train_step(t[:T].copy().view(np.float32), t[1:].copy()))
+        curves.append(np.array(curve, np.float32))
+        states.append(eng.read(0, img.header["persistent_size"]))
+        fused.append(eng.fused_dispatches())
+        eng.close()
+    # per step: 2 blocks x (4 LoRA forwards + 1 dK/dV pair)
+    assert fused[0] == 3 * TINY_Q8["layers"] * 5 and fused[1] == 0
+    assert curves[0].tobytes() == curves[1].tobytes()
+    assert states[0] == states[1]
+
+
 @pytest.mark.parametrize("relaxed", [False, True])
 def test_q8_decoder_training_matches_the_oracle(hip, orc, torch_cuda, relaxed):
     """BASELINE configs[4]'s lowering at a small shape -- RMSNorm, the frozen

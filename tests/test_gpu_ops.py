@@ -607,6 +607,81 @@ def test_attention_backward_pair_refuses_to_fuse_over_a_reused_buffer(hip, orc, 
     assert e <= TOL_BF16, f"dv over v: {e:.3g}"
 
 
+def _lora_site_program(ar, r, kind, M, Din, Dout, rank, t_over_c0=False):
+    """A LoRA site as the plan writer lowers it (lora_grafter.cc:170-207): the
+    forward C = x W + s (x A) B and the input gradient dX = dC W^T + dt A^T,
+    the frozen products relaxed (kFlagRelaxed), the adapters exact."""
+    from tests.plan_ops import ins
+    rx, cs_flag = 1 << 5, 1 << 4
+    x = ar.add("x", r.standard_normal((M, Din)).astype(np.float32))
+    dC = ar.add("dC", r.standard_normal((M, Dout)).astype(np.float32))
+    A = ar.add("A", (r.standard_normal((Din, rank)) * 0.02).astype(np.float32))
+    B = ar.add("B", (r.standard_normal((rank, Dout)) * 0.02).astype(np.float32))
+    dt = ar.add("dt", r.standard_normal((M, rank)).astype(np.float32))
+    c0, c = ar.empty("C0", (M, Dout)), ar.empty("C", (M, Dout))
+    p1, p2 = ar.empty("P1", (M, Din)), ar.empty("P2", (M, Din))
+    t = c0 if t_over_c0 else ar.empty("t", (M, rank))
+    if kind == "q8":
+        w = ar.add("W", r.integers(-127, 128, (Din, Dout)).astype(np.int8), rodata=True)
+        ws = ar.add("Ws", r.uniform(1e-3, 5e-2, Dout).astype(np.float32), rodata=True)
+        fwd0 = ins(29, [x, w, c0, ws], [M, Dout, Din], flags=rx | cs_flag)
+        bwd0 = ins(30, [dC, w, p1, ws], [M, Din, Dout], flags=rx | cs_flag)
+    else:
+        w = ar.add("W", (r.standard_normal((Din, Dout)) * 0.02).astype(np.float32), rodata=True)
+        fwd0 = ins(1, [x, w, c0], [M, Dout, Din], flags=rx)
+        bwd0 = ins(2, [dC, w, p1], [M, Din, Dout], flags=rx)
+    return [fwd0,
+            ins(1, [x, A, t], [M, rank, Din]),
+            ins(1, [t, B, c, c0], [M, Dout, rank], flags=1 << 3, imm=f32_bits(2.0)),
+            bwd0,
+            ins(2, [dt, A, p2, p1], [M, Din, rank], flags=1 << 3)]
+
+
+@pytest.mark.parametrize("kind", ["q8", "f32"])
+@pytest.mark.parametrize("M,Din,Dout,rank", [(512, 1024, 1024, 16), (300, 1024, 2048, 8),
+                                             (2048, 2048, 1280, 16)])
+def test_lora_site_folds_into_the_frozen_product_bitwise(hip, orc, backend, kind, M, Din, Dout,
+                                                         rank):
+    """With the range visible, each LoRA site runs as one dispatch: the
+    frozen product with the rank-r term in its epilogue (C stored as before,
+    C' = C + s (t B) in the rank-r instruction's exact chain).  The arena is
+    bitwise that of the five instructions run one by one; the relaxed count
+    is unchanged and two fused dispatches are counted."""
+    ar = Arena()
+    prog = _lora_site_program(ar, rng(M + Din + rank), kind, M, Din, Dout, rank)
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before, relaxed_before = backend.fused_dispatches(), backend.relaxed_executions()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    fused = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.fused_dispatches() - before == 2
+    assert backend.relaxed_executions() - relaxed_before == 2
+    assert fused.tobytes() == apart.tobytes()
+    for name in ["C0", "C", "P1", "P2"]:
+        e = maxrel(ar.get(fused, name), ar.get(cpu, name))
+        assert e <= TOL_BF16, f"{name}: {e:.3g}"
+    assert bits_equal(ar.get(fused, "t"), ar.get(cpu, "t"))  # the exact t product
+
+
+def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
+    """t written over the frozen product's C: legal one by one (C is then
+    read back with t's bytes in it), wrong once the frozen product moves after
+    t.  The forward site runs apart; the dX site still folds."""
+    ar = Arena()
+    prog = _lora_site_program(ar, rng(7), "q8", 256, 1024, 1024, 16, t_over_c0=True)
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before = backend.fused_dispatches()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.fused_dispatches() - before == 1
+    assert ranged.tobytes() == apart.tobytes()
+
+
 def test_attn_dkdv_entry_point_matches_the_separate_passes(hip, torch_cuda):
     import torch
     B, S, H, d = 2, 384, 3, 64
