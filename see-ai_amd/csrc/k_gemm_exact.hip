@@ -926,6 +926,151 @@ __global__ void __launch_bounds__(kThreads) GemmFoldKernel(GemmArgs g) {
   g.C[mf * N + nf] = Epilogue(g, mf, nf, c);
 }
 
+// The fold kernel with 16-byte staging: TN with f32 operands, 16-byte
+// aligned, M a multiple of BMo and N of BNo (both >= 4), K * M and K * N
+// below 2^31; a BMo x BNo block of outputs per workgroup, K in chunks of
+// kKc.  A chunk row contributes BMo / 4 float4 of A (A[k][m0 ...]) and
+// BNo / 4 of B, read with one 32-bit offset each and transposed into the
+// k-contiguous LDS rows as they are stored.  Each lane forms the quads of a
+// 2 x 2 block of outputs (two A and two B reads give four quads), and the
+// lanes below BMo x BNo fold them in k order, sixteen LDS reads in flight
+// ahead of the adds -- GemmFoldKernel's chains, with a quarter of its
+// instructions for staging and half its operand reads.
+template <int BMo, int BNo, int kKc>
+__global__ void __launch_bounds__(kThreads) GemmFoldVecKernel(GemmArgs g) {
+  static_assert(BMo >= 4 && BNo >= 4, "whole float4 row segments");
+  constexpr int kOut = BMo * BNo, kQc = kKc / 4, kLd = kKc + 4;
+  constexpr int kAv = kKc * BMo / 4 / kThreads, kBv = kKc * BNo / 4 / kThreads;
+  static_assert(kAv * kThreads * 4 == kKc * BMo && kBv * kThreads * 4 == kKc * BNo,
+                "every chunk float4 has a lane");
+  __shared__ __attribute__((aligned(16))) float As[BMo][kLd];
+  __shared__ __attribute__((aligned(16))) float Bs[BNo][kLd];
+  __shared__ float Q[kQc][kOut + 1];
+  const int tid = threadIdx.x;
+  const unsigned M = static_cast<unsigned>(g.M), N = static_cast<unsigned>(g.N),
+                 K = static_cast<unsigned>(g.K);
+  const unsigned total = gridDim.x * gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
+  const unsigned t = total % 8 == 0 ? (lin % 8) * (total / 8) + lin / 8 : lin;
+  const unsigned m0 = (t / gridDim.x) * BMo, n0 = (t % gridDim.x) * BNo;
+  const float* __restrict__ A = g.A;
+  const float* __restrict__ B = static_cast<const float*>(g.B);
+  float4 ra[kAv], rb[kBv];
+  auto load = [&](unsigned k0) {  // rows past K re-read row K - 1 (zeroed at the store)
+#pragma unroll
+    for (int r = 0; r < kAv; ++r) {
+      const int f = tid + r * kThreads, kk = f / (BMo / 4), c4 = f % (BMo / 4);
+      const unsigned k = min(k0 + kk, K - 1);
+      ra[r] = *reinterpret_cast<const float4*>(A + k * M + m0 + 4 * c4);
+    }
+#pragma unroll
+    for (int r = 0; r < kBv; ++r) {
+      const int f = tid + r * kThreads, kk = f / (BNo / 4), c4 = f % (BNo / 4);
+      const unsigned k = min(k0 + kk, K - 1);
+      rb[r] = *reinterpret_cast<const float4*>(B + k * N + n0 + 4 * c4);
+    }
+  };
+  auto store = [&](unsigned k0) {
+#pragma unroll
+    for (int r = 0; r < kAv; ++r) {
+      const int f = tid + r * kThreads, kk = f / (BMo / 4), c4 = f % (BMo / 4);
+      float4 v = ra[r];
+      if (g.alpha_a != 1.0f)
+        v = make_float4(Mul(g.alpha_a, v.x), Mul(g.alpha_a, v.y), Mul(g.alpha_a, v.z),
+                        Mul(g.alpha_a, v.w));
+      if (k0 + kk >= K) v = make_float4(0.f, 0.f, 0.f, 0.f);
+      As[4 * c4 + 0][kk] = v.x;
+      As[4 * c4 + 1][kk] = v.y;
+      As[4 * c4 + 2][kk] = v.z;
+      As[4 * c4 + 3][kk] = v.w;
+    }
+#pragma unroll
+    for (int r = 0; r < kBv; ++r) {
+      const int f = tid + r * kThreads, kk = f / (BNo / 4), c4 = f % (BNo / 4);
+      float4 v = rb[r];
+      if (k0 + kk >= K) v = make_float4(0.f, 0.f, 0.f, 0.f);
+      Bs[4 * c4 + 0][kk] = v.x;
+      Bs[4 * c4 + 1][kk] = v.y;
+      Bs[4 * c4 + 2][kk] = v.z;
+      Bs[4 * c4 + 3][kk] = v.w;
+    }
+  };
+  const int o = tid % kOut;  // the output this lane folds (lanes below kOut)
+  const int mo = o / BNo, no = o % BNo;
+  const unsigned mf = m0 + mo, nf = n0 + no;
+  const bool folds = tid < kOut;  // M % BMo == N % BNo == 0: every output exists
+  float c = (folds && g.accumulate) ? g.C[static_cast<size_t>(mf) * N + nf] : 0.0f;
+  const unsigned quads = K / 4;
+  const unsigned chunks = (quads + kQc - 1) / kQc;
+  load(0);
+  for (unsigned ch = 0; ch < chunks; ++ch) {
+    const unsigned k0 = ch * kKc;
+    __syncthreads();
+    if (ch + 1 == chunks) WaitVmAll();
+    store(k0);
+    __syncthreads();
+    if (ch + 1 < chunks) load(k0 + kKc);
+    const int nq = static_cast<int>(min(quads - ch * kQc, static_cast<unsigned>(kQc)));
+    // Quads in 2 x 2 output blocks: a lane reads two A rows and two B rows
+    // of quad j (four 16-byte reads) and forms the four outputs' quads.
+    // Block qb covers outputs (2 bm + u, 2 bn + v).
+    {
+      constexpr int kBlk = kOut / 4, kBlkN = BNo / 2, kQSlots = kThreads / kBlk;
+      static_assert(kThreads % kBlk == 0 && kQc % kQSlots == 0, "whole quad steps");
+      const int qb = tid % kBlk, qs = tid / kBlk;
+      const int bm = qb / kBlkN, bn = qb % kBlkN;
+      auto quad4 = [&](int j) {
+        const float4 a0 = *reinterpret_cast<const float4*>(&As[2 * bm][4 * j]);
+        const float4 a1 = *reinterpret_cast<const float4*>(&As[2 * bm + 1][4 * j]);
+        const float4 b0 = *reinterpret_cast<const float4*>(&Bs[2 * bn][4 * j]);
+        const float4 b1 = *reinterpret_cast<const float4*>(&Bs[2 * bn + 1][4 * j]);
+        const auto q = [](float4 a, float4 b) {
+          return Add(Add(Add(Mul(a.x, b.x), Mul(a.y, b.y)), Mul(a.z, b.z)), Mul(a.w, b.w));
+        };
+        Q[j][(2 * bm) * BNo + 2 * bn] = q(a0, b0);
+        Q[j][(2 * bm) * BNo + 2 * bn + 1] = q(a0, b1);
+        Q[j][(2 * bm + 1) * BNo + 2 * bn] = q(a1, b0);
+        Q[j][(2 * bm + 1) * BNo + 2 * bn + 1] = q(a1, b1);
+      };
+      if (nq == kQc) {
+#pragma unroll
+        for (int j = qs; j < kQc; j += kQSlots) quad4(j);
+      } else {
+        for (int j = qs; j < nq; j += kQSlots) quad4(j);
+      }
+    }
+    __syncthreads();
+    if (folds) {
+      if (nq == kQc) {
+        // Quads read sixteen at a time into registers, the next sixteen in
+        // flight while these are added in order: the chain waits on LDS once.
+        static_assert(kQc % 32 == 0, "whole pairs of sixteen");
+        float qa[16], qb[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) qa[u] = Q[u][o];
+#pragma unroll
+        for (int j = 0; j < kQc; j += 32) {
+#pragma unroll
+          for (int u = 0; u < 16; ++u) qb[u] = Q[j + 16 + u][o];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) c = Add(c, qa[u]);
+          if (j + 32 < kQc) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) qa[u] = Q[j + 32 + u][o];
+          }
+#pragma unroll
+          for (int u = 0; u < 16; ++u) c = Add(c, qb[u]);
+        }
+      } else {
+        for (int j = 0; j < nq; ++j) c = Add(c, Q[j][o]);
+      }
+    }
+  }
+  if (!folds) return;
+  for (unsigned k = quads * 4; k < K; ++k)  // the K % 4 tail, one term at a time
+    c = Add(c, Mul(LoadA<2>(g, mf, k), B[static_cast<size_t>(k) * N + nf]));
+  g.C[static_cast<size_t>(mf) * N + nf] = Epilogue(g, mf, nf, c);
+}
+
 // The fold kernel for TN with f32 B over K >= 1024 when the outputs fill at
 // most a few thousand workgroups (NN over these shapes measured faster on
 // the chain kernel).
@@ -939,6 +1084,23 @@ hipError_t LaunchFold(const GemmArgs& a, hipStream_t s) {
   // whole lanes: BNo * kFoldK >= 256).
   int bno = 2;
   while (bno < 16 && static_cast<size_t>(bno) < a.N) bno *= 2;
+  const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  // 16-byte staging over 256-deep chunks: 4 x 16 output blocks where that
+  // still gives at least 512 workgroups, else 4 x 8 (half the LDS, twice the
+  // workgroups: C4's 768 x 8 and 8 x 768 gradients run 33 us against 44).
+  if (kLayout == 2 && a.M % 4 == 0 && a.N % 8 == 0 && a.K * a.M < (size_t{1} << 31) &&
+      a.K * a.N < (size_t{1} << 31) && al16(a.A) && al16(a.B) && !a.a_k_scale) {
+    if (a.N % 16 == 0 && a.M * a.N >= 512 * 64) {
+      const dim3 grid(static_cast<unsigned>(a.N / 16), static_cast<unsigned>(a.M / 4));
+      if (grid.y > 65535) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((GemmFoldVecKernel<4, 16, 256>), grid, dim3(kThreads), 0, s, a);
+    } else {
+      const dim3 grid(static_cast<unsigned>(a.N / 8), static_cast<unsigned>(a.M / 4));
+      if (grid.y > 65535) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((GemmFoldVecKernel<4, 8, 256>), grid, dim3(kThreads), 0, s, a);
+    }
+    return hipGetLastError();
+  }
   const size_t bmo = kFoldOut / bno;
   const size_t gx = (a.N + bno - 1) / bno, gy = (a.M + bmo - 1) / bmo;
   if (gy > 65535) return hipErrorInvalidValue;

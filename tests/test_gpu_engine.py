@@ -269,7 +269,9 @@ def test_q8_decoder_training_matches_the_oracle(hip, orc, torch_cuda, relaxed):
         c = np.frombuffer(twin.read(0, persistent), np.float32)
         expect_close("persistent", g, c, 5e-3, 1e-6)
     assert (eng.relaxed_executions() > 0) == relaxed
-    assert (eng.fused_dispatches() == TINY_Q8["layers"] * 6) == relaxed
+    # per step and block: the dK / dV pair and the four LoRA forwards fold
+    # (the dX sites' NT products are below the direct-to-LDS kernel's K)
+    assert (eng.fused_dispatches() == TINY_Q8["layers"] * 6 * 5) == relaxed
     eng.close()
 
 
