@@ -24,6 +24,7 @@
 //     staged through LDS so C leaves in row-contiguous 16-byte stores.
 // Rows past M or N read as zeros through the buffer range check; Kp is K
 // rounded up to 32.
+#include <algorithm>
 #include <cstdint>
 
 #include "common.h"
@@ -369,34 +370,42 @@ ConvertRowsKernel(const float* __restrict__ A, size_t K, size_t Kp, float alpha,
 }
 
 // K a multiple of 32 (Kp == K): A' is A element for element, so the rows
-// flatten into one array; each lane converts two groups of eight per trip
-// (four 16-byte loads in flight), grid-stride.  The k-scale index is the
-// flat index mod K.
+// flatten into one array of groups of eight, walked grid-stride by a grid
+// of a few workgroups per CU; each lane keeps four groups (eight 16-byte
+// loads) in flight per trip.  The k-scale index is the flat index mod K
+// (32-bit: fewer than 2^32 groups), its eight values two 16-byte loads.
+template <bool kScale>
 __global__ void __launch_bounds__(kCvtThreads)
-ConvertFlatKernel(const float* __restrict__ A, size_t groups, size_t K, float alpha,
+ConvertFlatKernel(const float* __restrict__ A, unsigned groups, unsigned kgroups, float alpha,
                   const float* __restrict__ ks, __bf16* __restrict__ out) {
-  const size_t stride = static_cast<size_t>(gridDim.x) * kCvtThreads;
-  auto convert = [&](size_t gi) {
-    const float4 a = reinterpret_cast<const float4*>(A)[2 * gi];
-    const float4 b = reinterpret_cast<const float4*>(A)[2 * gi + 1];
-    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    const size_t k0 = (gi * 8) % K;
+  const unsigned stride = gridDim.x * kCvtThreads;
+  auto convert = [&](unsigned gi, float4 a, float4 b) {
+    float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    if constexpr (kScale) {
+      const float4* k4 = reinterpret_cast<const float4*>(ks + (gi % kgroups) * 8);
+      const float4 s0 = k4[0], s1 = k4[1];
+      const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = x[e] * sc[e];
+    }
     bf16x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = x[e];
-      if (ks) v = v * ks[k0 + e];
-      if (alpha != 1.0f) v = alpha * v;
-      o[e] = static_cast<__bf16>(v);
-    }
+    for (int e = 0; e < 8; ++e) o[e] = static_cast<__bf16>(alpha != 1.0f ? alpha * x[e] : x[e]);
     reinterpret_cast<bf16x8*>(out)[gi] = o;
   };
-  size_t gi = static_cast<size_t>(blockIdx.x) * kCvtThreads + threadIdx.x;
-  for (; gi + stride < groups; gi += 2 * stride) {
-    convert(gi);
-    convert(gi + stride);
+  const float4* A4 = reinterpret_cast<const float4*>(A);
+  unsigned gi = blockIdx.x * kCvtThreads + threadIdx.x;
+  for (; gi + 3 * stride < groups; gi += 4 * stride) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v[2 * u] = A4[2 * (gi + u * stride)];
+      v[2 * u + 1] = A4[2 * (gi + u * stride) + 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) convert(gi + u * stride, v[2 * u], v[2 * u + 1]);
   }
-  if (gi < groups) convert(gi);
+  for (; gi < groups; gi += stride) convert(gi, A4[2 * gi], A4[2 * gi + 1]);
 }
 
 // W' [N, Kp] bf16 from the weight as the instruction reads it: NN's W[K, N]
@@ -472,11 +481,20 @@ bool Bf16DmaLowRankFits(const GemmArgs& a) {
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,
                                  const float* kscale, void* out, hipStream_t s) {
   if (M == 0) return hipSuccess;
-  if (K % 32 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0) {
-    const size_t groups = M * K / 8;
-    hipLaunchKernelGGL(ConvertFlatKernel, dim3(GridFor(groups / 2, kCvtThreads, 16384)),
-                       dim3(kCvtThreads), 0, s, A, groups, K, alpha, kscale,
-                       static_cast<__bf16*>(out));
+  const size_t groups = M * K / 8;
+  if (K % 32 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(kscale) & 15) == 0 && groups < (size_t{1} << 31)) {
+    // Eight workgroups per CU, four groups per lane per trip.
+    const unsigned grid = static_cast<unsigned>(
+        std::min<size_t>((groups + 4 * kCvtThreads - 1) / (4 * kCvtThreads),
+                         static_cast<size_t>(DeviceCUs()) * 8));
+    const unsigned g = static_cast<unsigned>(groups), kg = static_cast<unsigned>(K / 8);
+    if (kscale)
+      hipLaunchKernelGGL((ConvertFlatKernel<true>), dim3(grid), dim3(kCvtThreads), 0, s, A, g, kg,
+                         alpha, kscale, static_cast<__bf16*>(out));
+    else
+      hipLaunchKernelGGL((ConvertFlatKernel<false>), dim3(grid), dim3(kCvtThreads), 0, s, A, g, kg,
+                         alpha, kscale, static_cast<__bf16*>(out));
     return hipGetLastError();
   }
   hipLaunchKernelGGL(ConvertRowsKernel, dim3(static_cast<unsigned>(M)), dim3(kCvtThreads), 0, s, A, K,
