@@ -98,6 +98,19 @@ struct seeai_ctx {
   int allow_dma = 1;  // relaxed frozen-weight GEMMs on the bf16 shadow path
   int allow_lowrank = 1;  // LoRA sites folded into the frozen product's epilogue
   TilePolicy policy;  // kernel geometry (seeai_configure)
+  // The relaxed GEMMs' bf16 copy of their activations, and what it holds:
+  // a later relaxed GEMM of the same range that rounds the same bytes the
+  // same way reuses it when every instruction between wrote elsewhere.
+  void* cvt = nullptr;
+  size_t cvt_bytes = 0;
+  struct {
+    const float* A = nullptr;
+    uint64_t M = 0, K = 0;
+    float alpha = 0.0f;
+    const float* ks = nullptr;
+    const uint8_t* at = nullptr;  // the converting instruction in the range; null: none
+  } cvt_key;
+  const uint8_t* cur_at = nullptr;  // the instruction being executed, when in the range
   uint64_t fused = 0;
   // bf16 copies [N, Kp] of frozen weights for the relaxed GEMMs, keyed by
   // (weight, layout, kind, N, K); valid until the next bind.
@@ -193,6 +206,32 @@ bool Immutable(const seeai_ctx* c, const void* p) {
          (c->source && q >= c->source && q < c->source + c->source_bytes);
 }
 
+const char* DecodeGemm(seeai_ctx* c, const Instruction& ins, GemmArgs* out);
+bool Overlap(const uint8_t* a, uint64_t na, const uint8_t* b, uint64_t nb);
+
+// Whether the conversion buffer already holds this GEMM's A' (range
+// fusion): the same A, shape, alpha and k-scale converted by an earlier
+// instruction of this range, and every instruction between them a GEMM
+// whose output misses A.  Anything else -- another opcode between, a write
+// into A, a copy of the instruction word run outside the range -- converts
+// again.
+bool ConvertedAlready(seeai_ctx* c, const GemmArgs& a) {
+  const auto& k = c->cvt_key;
+  if (!c->allow_fusion || !c->cur_at || !k.at || k.at >= c->cur_at || k.A != a.A || k.M != a.M ||
+      k.K != a.K || k.alpha != a.alpha_a || k.ks != a.a_k_scale)
+    return false;
+  const auto* A = reinterpret_cast<const uint8_t*>(a.A);
+  const uint64_t bytes = a.M * a.K * 4;
+  for (const uint8_t* p = k.at + 64; p < c->cur_at; p += 64) {
+    Instruction ins;
+    std::memcpy(&ins, p, sizeof ins);
+    GemmArgs g{};
+    if (!DecodeGemm(c, ins, &g)) return false;
+    if (Overlap(reinterpret_cast<const uint8_t*>(g.C), g.M * g.N * 4, A, bytes)) return false;
+  }
+  return true;
+}
+
 // The relaxed frozen-weight product on the bf16 direct-to-LDS kernel: the
 // weight's bf16 shadow (made once), A rounded into the workspace with its
 // scales, then the GEMM and its epilogue.
@@ -207,10 +246,21 @@ int GemmBf16Dma(seeai_ctx* c, GemmArgs& a, const char* what) {
     c->shadows[key] = shadow;
     SEEAI_TRY(c, LaunchWeightShadow(a, shadow, c->stream), "weight shadow");
   }
-  void* ws;
-  if (int rc = Scratch(c, a.M * Bf16DmaKp(a.K) * 2, &ws)) return rc;
-  SEEAI_TRY(c, LaunchConvertRowsBf16(a.A, a.M, a.K, a.alpha_a, a.a_k_scale, ws, c->stream), what);
-  SEEAI_TRY(c, LaunchGemmBf16Dma(ws, shadow, a, c->stream), what);
+  const size_t need = a.M * Bf16DmaKp(a.K) * 2;
+  if (!ConvertedAlready(c, a)) {
+    if (need > c->cvt_bytes) {  // grow after draining the stream
+      SEEAI_TRY(c, hipStreamSynchronize(c->stream), "conversion buffer drain");
+      if (c->cvt) SEEAI_TRY(c, hipFree(c->cvt), "conversion buffer free");
+      c->cvt = nullptr;
+      c->cvt_bytes = 0;
+      SEEAI_TRY(c, hipMalloc(&c->cvt, need), "conversion buffer alloc");
+      c->cvt_bytes = need;
+    }
+    c->cvt_key = {a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->cur_at};
+    SEEAI_TRY(c, LaunchConvertRowsBf16(a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->cvt, c->stream),
+              what);
+  }
+  SEEAI_TRY(c, LaunchGemmBf16Dma(c->cvt, shadow, a, c->stream), what);
   return SEEAI_OK;
 }
 
@@ -701,6 +751,7 @@ void seeai_destroy(seeai_ctx* c) {
   if (c->rodata) (void)hipFree(c->rodata);
   if (c->source) (void)hipFree(c->source);
   if (c->scratch) (void)hipFree(c->scratch);
+  if (c->cvt) (void)hipFree(c->cvt);
   DropShadows(c);
   if (c->small) (void)hipFree(c->small);
   if (c->host_flag) (void)hipHostFree(c->host_flag);
@@ -725,6 +776,7 @@ uint64_t seeai_relaxed_executions(const seeai_ctx* c) { return c ? c->relaxed : 
 
 int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t rodata_bytes) {
   if (!c) return SEEAI_INVALID;
+  c->cvt_key.at = nullptr;
   const uint64_t bytes = (arena_bytes + kArenaAlignment - 1) / kArenaAlignment * kArenaAlignment;
   uint8_t* arena = nullptr;
   uint8_t* ro = nullptr;
@@ -752,6 +804,7 @@ int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t 
 }
 
 int seeai_bind_source(seeai_ctx* c, const void* data, uint64_t bytes) {
+  if (c) c->cvt_key.at = nullptr;
   if (!c) return SEEAI_INVALID;
   SEEAI_TRY(c, hipStreamSynchronize(c->stream), "bind_source drain");
   DropShadows(c);  // some may be of the old source image
@@ -768,6 +821,7 @@ int seeai_bind_source(seeai_ctx* c, const void* data, uint64_t bytes) {
 int seeai_upload(seeai_ctx* c, uint64_t off, const void* src, uint64_t bytes) {
   if (!c || !c->arena || off + bytes > c->arena_bytes) return Fail(c, SEEAI_INVALID, "upload: extent outside the arena");
   if (!bytes) return SEEAI_OK;
+  c->cvt_key.at = nullptr;  // the arena changed outside the program
   SEEAI_TRY(c, hipMemcpyAsync(c->arena + off, src, bytes, hipMemcpyHostToDevice, c->stream), "upload");
   // The source buffer is the caller's pageable memory: complete the copy
   // before returning so the caller may reuse it at once.
@@ -915,9 +969,14 @@ int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params
   if (!c->arena) return Fail(c, SEEAI_INVALID, "execute: no arena is bound");
   seeai_step_params P{};
   if (params) P = *params;
-  if (int rc = TryFuseLowRank(c, ins, at, P); rc >= 0) return rc;
-  if (int rc = TryFuseAttnBwd(c, ins, at); rc >= 0) return rc;
-  return ExecuteOne(c, ins, P);
+  const bool in_range = c->prog && at >= c->prog && at < c->prog + c->prog_count * 64 &&
+                        (at - c->prog) % 64 == 0;
+  c->cur_at = in_range ? at : nullptr;
+  int rc = TryFuseLowRank(c, ins, at, P);
+  if (rc < 0) rc = TryFuseAttnBwd(c, ins, at);
+  if (rc < 0) rc = ExecuteOne(c, ins, P);
+  c->cur_at = nullptr;
+  return rc;
 }
 
 int seeai_begin_range(seeai_ctx* c, const void* program, uint64_t count, uint64_t begin,
@@ -927,6 +986,7 @@ int seeai_begin_range(seeai_ctx* c, const void* program, uint64_t count, uint64_
   c->prog_count = count;
   c->range_end = end;
   c->ndone = 0;
+  c->cvt_key.at = nullptr;
   return SEEAI_OK;
 }
 
@@ -935,6 +995,7 @@ int seeai_end_range(seeai_ctx* c) {
   c->prog = nullptr;
   c->prog_count = c->range_end = 0;
   c->ndone = 0;
+  c->cvt_key.at = nullptr;
   return SEEAI_OK;
 }
 

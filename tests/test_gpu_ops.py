@@ -682,6 +682,40 @@ def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
     assert ranged.tobytes() == apart.tobytes()
 
 
+@pytest.mark.parametrize("between", ["gemm_elsewhere", "gemm_into_x", "add_into_x"])
+def test_relaxed_gemms_reconvert_after_their_activation_changes(hip, orc, backend, between):
+    """Relaxed GEMMs of a range that round the same activation the same way
+    share one bf16 conversion.  Anything between them that writes into the
+    activation -- a GEMM, or any other opcode -- makes the second convert
+    again: the range's bytes are those of the instructions run one by one."""
+    from tests.plan_ops import ins
+    M, K, N = 512, 1024, 768
+    r = rng(hash(between) % 1000)
+    ar = Arena()
+    x = ar.add("x", r.standard_normal((M, K)).astype(np.float32))
+    y = ar.add("y", r.standard_normal((M, 64)).astype(np.float32))
+    b = ar.add("b", (r.standard_normal((64, K)) * 0.1).astype(np.float32))
+    w1 = ar.add("W1", r.integers(-127, 128, (K, N)).astype(np.int8), rodata=True)
+    w2 = ar.add("W2", r.integers(-127, 128, (K, N)).astype(np.int8), rodata=True)
+    s1 = ar.add("s1", r.uniform(1e-3, 5e-2, N).astype(np.float32), rodata=True)
+    c1, c3, z = ar.empty("C1", (M, N)), ar.empty("C3", (M, N)), ar.empty("z", (M, K))
+    rx = (1 << 5) | (1 << 4)
+    mid = {"gemm_elsewhere": ins(1, [y, b, z], [M, K, 64]),
+           "gemm_into_x": ins(1, [y, b, x], [M, K, 64]),
+           "add_into_x": ins(5, [x, x, x], [M * K])}[between]
+    prog = [ins(29, [x, w1, c1, s1], [M, N, K], flags=rx), mid,
+            ins(29, [x, w2, c3, s1], [M, N, K], flags=rx)]
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert ranged.tobytes() == apart.tobytes()
+    e = maxrel(ar.get(ranged, "C3"), ar.get(cpu, "C3"))
+    assert e <= TOL_BF16, f"C3: {e:.3g}"
+
+
 def test_attn_dkdv_entry_point_matches_the_separate_passes(hip, torch_cuda):
     import torch
     B, S, H, d = 2, 384, 3, 64
