@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <map>
 #include <string>
 #include <tuple>
@@ -953,6 +954,71 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
   return -1;
 }
 
+// Range-level fusion of SwiGLU's elementwise chains (the seam's
+// whole-program visibility, backend.h:139-142): kSiluFwd followed by a
+// kMulEW of its output (y = SiLU(x), h = y * u), and two kMulEW followed by
+// the kSiluBwd of one of their outputs (dsg = dh * up, dup = dh * sg,
+// dgt = SiluBwd(dsg, gt)) run as one pass each over the same n, with the
+// standalone kernels' expressions; every output is still written.  Refused
+// when the element counts differ or any output overlaps another operand.
+// Returns -1 when the instructions do not fuse.
+int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
+  if (!c->allow_fusion || !c->prog || at < c->prog || at >= c->prog + c->prog_count * 64 ||
+      (at - c->prog) % 64 != 0)
+    return -1;
+  const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
+  const auto next = [&](uint64_t k, Instruction* out) {
+    if (idx + k >= c->range_end) return false;
+    std::memcpy(out, c->prog + (idx + k) * 64, sizeof *out);
+    return true;
+  };
+  const Ptrs R{c};
+  const uint64_t n = ins.out[0];
+  const uint64_t nb = n * 4;
+  // Outputs must miss every other operand (inputs may repeat).
+  const auto clear = [&](std::initializer_list<const float*> outs,
+                         std::initializer_list<const float*> ins_) {
+    for (const float* o : outs) {
+      const auto* op = reinterpret_cast<const uint8_t*>(o);
+      for (const float* q : outs)
+        if (q != o && Overlap(op, nb, reinterpret_cast<const uint8_t*>(q), nb)) return false;
+      for (const float* q : ins_)
+        if (Overlap(op, nb, reinterpret_cast<const uint8_t*>(q), nb)) return false;
+    }
+    return true;
+  };
+  Instruction n1, n2;
+  if (ins.opcode == 24 && next(1, &n1) && n1.opcode == 21 && n1.out[0] == n &&
+      (n1.in[0] == ins.in[1]) != (n1.in[1] == ins.in[1])) {  // SiluFwd, MulEW(y, u)
+    const float *x = R.f(ins.in[0]), *u = R.f(n1.in[0] == ins.in[1] ? n1.in[1] : n1.in[0]);
+    float *y = R.f(ins.in[1]), *h = R.f(n1.in[2]);
+    if (!clear({y, h}, {x, u})) return -1;
+    SEEAI_TRY(c, LaunchSiluMul(x, u, y, h, n, c->stream), "silu_mul");
+    c->done[0] = at + 64;
+    c->ndone = 1;
+    ++c->fused;
+    return SEEAI_OK;
+  }
+  if (ins.opcode == 21 && next(1, &n1) && n1.opcode == 21 && next(2, &n2) && n2.opcode == 25 &&
+      n1.out[0] == n && n2.out[0] == n) {  // MulEW, MulEW, SiluBwd(one product, x)
+    const bool first = n2.in[0] == ins.in[2];
+    if (!first && n2.in[0] != n1.in[2]) return -1;
+    const Instruction& m1 = first ? ins : n1;  // the product SiluBwd reads
+    const Instruction& m2 = first ? n1 : ins;
+    const float *a1 = R.f(m1.in[0]), *b1 = R.f(m1.in[1]), *a2 = R.f(m2.in[0]),
+                *b2 = R.f(m2.in[1]), *x = R.f(n2.in[1]);
+    float *o1 = R.f(m1.in[2]), *o2 = R.f(m2.in[2]), *dx = R.f(n2.in[2]);
+    if (!clear({o1, o2, dx}, {a1, b1, a2, b2, x})) return -1;
+    SEEAI_TRY(c, LaunchSwigluBwd(a1, b1, o1, a2, b2, o2, x, dx, n, c->stream), "swiglu_bwd");
+    c->done[0] = at + 64;
+    c->done[1] = at + 128;
+    c->ndone = 2;
+    ++c->fused;
+    return SEEAI_OK;
+  }
+  return -1;
+}
+
 }  // namespace
 
 int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params* params) {
@@ -974,6 +1040,7 @@ int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params
   c->cur_at = in_range ? at : nullptr;
   int rc = TryFuseLowRank(c, ins, at, P);
   if (rc < 0) rc = TryFuseAttnBwd(c, ins, at);
+  if (rc < 0) rc = TryFuseElementwise(c, ins, at);
   if (rc < 0) rc = ExecuteOne(c, ins, P);
   c->cur_at = nullptr;
   return rc;

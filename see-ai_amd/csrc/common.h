@@ -36,6 +36,11 @@ __device__ __forceinline__ float GeluExpr(float x) {
   return 0.5f * x * (1.0f + t);
 }
 __device__ __forceinline__ float SiluExpr(float x) { return x * SigmoidExpr(x); }
+// SiluBwd (activation.cc:62-75): dy * (s (1 + x (1 - s))), s = sigmoid(x).
+__device__ __forceinline__ float SiluBwdExpr(float dy, float x) {
+  const float sg = SigmoidExpr(x);
+  return dy * (sg * (1.0f + x * (1.0f - sg)));
+}
 __device__ __forceinline__ float ActExpr(int act, float v) {
   switch (act) {
     case 1: return ReluExpr(v);
@@ -270,6 +275,16 @@ hipError_t LaunchGemmBf16(const GemmArgs& a, hipStream_t s);
 
 // Compute units of the current device (cached per device).
 int DeviceCUs();
+
+// SwiGLU's elementwise chains as one pass each (range fusion of adjacent
+// instructions over the same n; every output disjoint from every other
+// operand).  Forward: y = SiLU(x), h = y * u.  Backward: o1 = a1 * b1,
+// o2 = a2 * b2, dx = SiluBwd(o1, x).  The standalone kernels' expressions.
+hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, size_t n,
+                         hipStream_t s);
+hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const float* a2,
+                           const float* b2, float* o2, const float* x, float* dx, size_t n,
+                           hipStream_t s);
 
 // W8A8 (k_gemm_i8.hip).
 hipError_t LaunchQuantizeRows(const float* X, int8_t* Q, float* scale, size_t rows, size_t cols,

@@ -10,6 +10,8 @@
 // Every expression is the reference's own (built -ffp-contract=off), so the
 // arithmetic kernels reproduce the reference's bits wherever no libm call
 // is involved.
+#include <algorithm>
+
 #include "common.h"
 
 namespace seeai {
@@ -245,6 +247,40 @@ RopeKernel(const float* __restrict__ x, float* __restrict__ y, size_t B, size_t 
   }
 }
 
+// RoPE with the table, rows of the [B S, H d] activation on the grid: the
+// row's position s = row mod S is uniform across the workgroup, and a lane
+// rotates two pairs -- one 16-byte read of x and one of the table row
+// (cos p, sin p, cos p+1, sin p+1), 32-bit column arithmetic.  The same
+// expressions as RopeKernel.  d % 4 == 0, x, y and the table 16-byte aligned.
+__global__ void __launch_bounds__(kThreads)
+RopeRowsKernel(const float* __restrict__ x, float* __restrict__ y, unsigned rows, unsigned S,
+               unsigned width, unsigned d, const float* __restrict__ table, int backward) {
+  for (unsigned r = blockIdx.y; r < rows; r += gridDim.y) {
+    const unsigned s = r % S;
+    const float* __restrict__ trow = table + static_cast<size_t>(s) * d;  // d/2 pairs x 2
+    const size_t base = static_cast<size_t>(r) * width;
+    for (unsigned c = (blockIdx.x * kThreads + threadIdx.x) * 4; c < width;
+         c += gridDim.x * kThreads * 4) {
+      const unsigned j = c % d;  // 2p: the pair index times two
+      const float4 v = *reinterpret_cast<const float4*>(x + base + c);
+      const float4 t = *reinterpret_cast<const float4*>(trow + j);
+      float4 o;
+      if (backward) {
+        o.x = v.x * t.x + v.y * t.y;
+        o.y = -v.x * t.y + v.y * t.x;
+        o.z = v.z * t.z + v.w * t.w;
+        o.w = -v.z * t.w + v.w * t.z;
+      } else {
+        o.x = v.x * t.x - v.y * t.y;
+        o.y = v.x * t.y + v.y * t.x;
+        o.z = v.z * t.z - v.w * t.w;
+        o.w = v.z * t.w + v.w * t.z;
+      }
+      *reinterpret_cast<float4*>(y + base + c) = o;
+    }
+  }
+}
+
 __global__ void __launch_bounds__(kThreads)
 RopeTableKernel(float* __restrict__ table, size_t S, size_t d, float step) {
   const size_t s = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -309,6 +345,33 @@ ArgmaxKernel(const float* __restrict__ probs, size_t cols, int32_t* __restrict__
   }
 }
 
+__global__ void __launch_bounds__(kThreads)
+SiluMul4(const float4* __restrict__ x, const float4* __restrict__ u, float4* __restrict__ y,
+         float4* __restrict__ h, size_t n4) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
+    const float4 a = x[i], b = u[i];
+    const float4 g = make_float4(SiluExpr(a.x), SiluExpr(a.y), SiluExpr(a.z), SiluExpr(a.w));
+    y[i] = g;
+    h[i] = make_float4(g.x * b.x, g.y * b.y, g.z * b.z, g.w * b.w);
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+SwigluBwd4(const float4* __restrict__ a1, const float4* __restrict__ b1, float4* __restrict__ o1,
+           const float4* __restrict__ a2, const float4* __restrict__ b2, float4* __restrict__ o2,
+           const float4* __restrict__ x, float4* __restrict__ dx, size_t n4) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
+    const float4 p = a1[i], q = b1[i], r = a2[i], t = b2[i], v = x[i];
+    const float4 m1 = make_float4(p.x * q.x, p.y * q.y, p.z * q.z, p.w * q.w);
+    o1[i] = m1;
+    o2[i] = make_float4(r.x * t.x, r.y * t.y, r.z * t.z, r.w * t.w);
+    dx[i] = make_float4(SiluBwdExpr(m1.x, v.x), SiluBwdExpr(m1.y, v.y), SiluBwdExpr(m1.z, v.z),
+                        SiluBwdExpr(m1.w, v.w));
+  }
+}
+
 }  // namespace
 
 hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hipStream_t s) {
@@ -320,6 +383,40 @@ hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hip
     return hipGetLastError();
   }
   return Map(n, s, [=] __device__(size_t i) { out[i] = x[i] + y[i]; });
+}
+hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, size_t n,
+                         hipStream_t s) {
+  if (n % 4 == 0 && Aligned16(x) && Aligned16(u) && Aligned16(y) && Aligned16(h)) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(SiluMul4, dim3(GridFor(n / 4, kThreads, 8192)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const float4*>(x), reinterpret_cast<const float4*>(u),
+                       reinterpret_cast<float4*>(y), reinterpret_cast<float4*>(h), n / 4);
+    return hipGetLastError();
+  }
+  return Map(n, s, [=] __device__(size_t i) {
+    const float g = SiluExpr(x[i]);
+    y[i] = g;
+    h[i] = g * u[i];
+  });
+}
+hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const float* a2,
+                           const float* b2, float* o2, const float* x, float* dx, size_t n,
+                           hipStream_t s) {
+  if (n % 4 == 0 && Aligned16(a1) && Aligned16(b1) && Aligned16(o1) && Aligned16(a2) &&
+      Aligned16(b2) && Aligned16(o2) && Aligned16(x) && Aligned16(dx)) {
+    if (n == 0) return hipSuccess;
+    const auto c4 = [](const float* p) { return reinterpret_cast<const float4*>(p); };
+    const auto m4 = [](float* p) { return reinterpret_cast<float4*>(p); };
+    hipLaunchKernelGGL(SwigluBwd4, dim3(GridFor(n / 4, kThreads, 8192)), dim3(kThreads), 0, s,
+                       c4(a1), c4(b1), m4(o1), c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4);
+    return hipGetLastError();
+  }
+  return Map(n, s, [=] __device__(size_t i) {
+    const float m1 = a1[i] * b1[i];
+    o1[i] = m1;
+    o2[i] = a2[i] * b2[i];
+    dx[i] = SiluBwdExpr(m1, x[i]);
+  });
 }
 hipError_t LaunchMulEW(const float* x, const float* y, float* out, size_t n, hipStream_t s) {
   return Map(n, s, [=] __device__(size_t i) { out[i] = x[i] * y[i]; });
@@ -355,8 +452,7 @@ hipError_t LaunchBinaryBwd(int kind, const float* dy, const float* x, float* dx,
       });
     default:
       return Map(n, s, [=] __device__(size_t i) {
-        const float sg = SigmoidExpr(x[i]);
-        dx[i] = dy[i] * (sg * (1.0f + x[i] * (1.0f - sg)));
+        dx[i] = SiluBwdExpr(dy[i], x[i]);
       });
   }
 }
@@ -429,6 +525,17 @@ hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, si
                       float step, const float* table, int backward, hipStream_t s) {
   const size_t n = B * S * H * (d / 2);
   if (n == 0) return hipSuccess;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+                       reinterpret_cast<uintptr_t>(table);
+  if (table && d % 4 == 0 && (al & 15) == 0 && B * S < (size_t{1} << 31) &&
+      H * d < (size_t{1} << 31)) {
+    const unsigned width = static_cast<unsigned>(H * d), rows = static_cast<unsigned>(B * S);
+    const unsigned gx = static_cast<unsigned>(std::min<size_t>((width / 4 + kThreads - 1) / kThreads, 64));
+    const dim3 grid(gx, std::min(rows, 65535u));
+    hipLaunchKernelGGL(RopeRowsKernel, grid, dim3(kThreads), 0, s, x, y, rows,
+                       static_cast<unsigned>(S), width, static_cast<unsigned>(d), table, backward);
+    return hipGetLastError();
+  }
   const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 7) == 0;
   if (vec)
     hipLaunchKernelGGL(RopeKernel<true>, dim3(GridFor(n, kThreads)), dim3(kThreads), 0, s, x, y, B,

@@ -219,8 +219,9 @@ TINY_Q8 = dict(vocab=96, dim=128, heads=2, ffn=352, layers=2, seq=64, batch=2, r
 def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch_cuda):
     """On the int8-base decoder the range fusions include the LoRA sites'
     low-rank epilogue (the frozen Q / K / V / O products with the rank-r
-    term folded in) beside the dK / dV pairs: three steps with fusion on and
-    off give the same losses and persistent bytes."""
+    term folded in) and the SwiGLU elementwise chains beside the dK / dV
+    pairs: three steps with fusion on and off give the same losses and
+    persistent bytes."""
     T = TINY_Q8["batch"] * TINY_Q8["seq"]
     curves, states, fused = [], [], []
     for allow in (True, False):
@@ -235,8 +236,8 @@ def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch
         states.append(eng.read(0, img.header["persistent_size"]))
         fused.append(eng.fused_dispatches())
         eng.close()
-    # per step: 2 blocks x (4 LoRA forwards + 1 dK/dV pair)
-    assert fused[0] == 3 * TINY_Q8["layers"] * 5 and fused[1] == 0
+    # per step and block: 4 LoRA forwards, the dK / dV pair, 2 SwiGLU chains
+    assert fused[0] == 3 * TINY_Q8["layers"] * 7 and fused[1] == 0
     assert curves[0].tobytes() == curves[1].tobytes()
     assert states[0] == states[1]
 
@@ -269,9 +270,11 @@ def test_q8_decoder_training_matches_the_oracle(hip, orc, torch_cuda, relaxed):
         c = np.frombuffer(twin.read(0, persistent), np.float32)
         expect_close("persistent", g, c, 5e-3, 1e-6)
     assert (eng.relaxed_executions() > 0) == relaxed
-    # per step and block: the dK / dV pair and the four LoRA forwards fold
-    # (the dX sites' NT products are below the direct-to-LDS kernel's K)
-    assert (eng.fused_dispatches() == TINY_Q8["layers"] * 6 * 5) == relaxed
+    # per step and block: the dK / dV pair, the four LoRA forwards (the dX
+    # sites' NT products are below the direct-to-LDS kernel's K) and the two
+    # SwiGLU chains; the elementwise chains fuse in the exact family too
+    per_block = 7 if relaxed else 2
+    assert eng.fused_dispatches() == TINY_Q8["layers"] * 6 * per_block
     eng.close()
 
 

@@ -328,7 +328,7 @@ def test_norms(hip, orc, backend, rows, cols):
         assert e <= TOL, f"{name}: {e:.3g}"
 
 
-@pytest.mark.parametrize("B,S,H,d", [(2, 33, 3, 16), (2, 300, 4, 64)])
+@pytest.mark.parametrize("B,S,H,d", [(2, 33, 3, 16), (2, 300, 4, 64), (1, 17, 2, 6)])
 def test_rope(hip, orc, backend, B, S, H, d):
     from tests.plan_ops import ins
     r = rng(9 + S)
@@ -714,6 +714,59 @@ def test_relaxed_gemms_reconvert_after_their_activation_changes(hip, orc, backen
     assert ranged.tobytes() == apart.tobytes()
     e = maxrel(ar.get(ranged, "C3"), ar.get(cpu, "C3"))
     assert e <= TOL_BF16, f"C3: {e:.3g}"
+
+
+@pytest.mark.parametrize("n", [4096, 1003])
+@pytest.mark.parametrize("order", ["as_planned", "swapped"])
+def test_swiglu_chains_fuse_bitwise(hip, orc, backend, n, order):
+    """SwiGLU's chains as the plan writer lowers them -- y = SiLU(g), h = y * u;
+    dsg = dh * u, dup = dh * y, dg = SiluBwd(dsg, g) -- run as one pass each in
+    a range: bitwise the instructions one by one (and the oracle's within
+    libm), two fused dispatches.  With the two products in the other order,
+    SiluBwd reads the second one: still one pass."""
+    from tests.plan_ops import ins
+    r = rng(n)
+    ar = Arena()
+    g, u, dh = (ar.add(k, r.standard_normal(n).astype(np.float32)) for k in ("g", "u", "dh"))
+    y, h, dsg, dup, dg = (ar.empty(k, (n,)) for k in ("y", "h", "dsg", "dup", "dg"))
+    mults = [ins(21, [dh, u, dsg], [n]), ins(21, [dh, y, dup], [n])]
+    if order == "swapped":
+        mults = mults[::-1]
+    prog = [ins(24, [g, y], [n]), ins(21, [y, u, h], [n])] + mults + [ins(25, [dsg, g, dg], [n])]
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before = backend.fused_dispatches()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    fused = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.fused_dispatches() - before == 2
+    assert fused.tobytes() == apart.tobytes()
+    for name in ["y", "h", "dsg", "dup", "dg"]:
+        e = maxrel(ar.get(fused, name), ar.get(cpu, name))
+        assert e <= TOL, f"{name}: {e:.3g}"
+
+
+def test_swiglu_chain_refuses_to_fuse_over_an_input(hip, orc, backend):
+    """h written over u, which the product reads: one pass would still be
+    right element by element, but the rule is simple -- an output touching an
+    input runs apart."""
+    from tests.plan_ops import ins
+    n = 2048
+    r = rng(5)
+    ar = Arena()
+    g, u = ar.add("g", r.standard_normal(n).astype(np.float32)), ar.add("u", r.standard_normal(n).astype(np.float32))
+    y = ar.empty("y", (n,))
+    prog = [ins(24, [g, y], [n]), ins(21, [y, u, u], [n])]
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before = backend.fused_dispatches()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.fused_dispatches() == before
+    assert ranged.tobytes() == apart.tobytes()
 
 
 def test_attn_dkdv_entry_point_matches_the_separate_passes(hip, torch_cuda):
