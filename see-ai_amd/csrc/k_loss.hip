@@ -43,44 +43,70 @@ XEntRowMaxKernel(const float* __restrict__ logits, float* __restrict__ row_max, 
 
 // --- pass 2: the exp-sum in the reference's order ------------------------------
 // loss.cc:24-29 sums exp(x - max) in f32, column by column, one chain per
-// row.  That association is reproduced exactly: all 256 lanes of a
-// workgroup evaluate exp over a 16-row x 256-column tile into LDS (double
-// buffered), and lane r of wave 0 then adds its row's 256 values in column
-// order.  The chain is serial by definition; the exps around it are not.
-constexpr int kSumThreads = 256;
-constexpr int kSumRows = 16;
-constexpr int kTileCols = 256;
+// row.  That association is reproduced exactly, with the chain apart from
+// the exps: a workgroup takes 32 rows; waves 1-7 evaluate exp over 32-row x
+// 224-column tiles into LDS (16-byte loads, double-buffered) while lane r
+// of wave 0 adds row r's previous tile in column order, sixteen LDS values
+// read ahead of its adds.  The chain wave does nothing else, so a tile
+// costs the longer of its 224 dependent adds and the producers' exps.
+constexpr int kSumThreads = 512;
+constexpr int kSumRows = 32;
+constexpr int kTileCols = 224;                      // 56 float4 per row
+constexpr int kTileLd = kTileCols + 4;
+constexpr int kProducers = kSumThreads - kWave;     // waves 1-7
 
 __global__ void __launch_bounds__(kSumThreads)
 XEntSerialSumKernel(const float* __restrict__ logits, const float* __restrict__ row_max,
                     float* __restrict__ row_sum, size_t N, size_t C) {
-  __shared__ __attribute__((aligned(16))) float tile[2][kSumRows][kTileCols + 4];
+  __shared__ __attribute__((aligned(16))) float tile[2][kSumRows][kTileLd];
   const size_t r0 = static_cast<size_t>(blockIdx.x) * kSumRows;
   const int t = threadIdx.x;
   const size_t ntiles = (C + kTileCols - 1) / kTileCols;
-  float mx[kSumRows];
-#pragma unroll
-  for (int r = 0; r < kSumRows; ++r) mx[r] = r0 + r < N ? row_max[r0 + r] : 0.0f;
+  const bool vec = Vec4Rows(logits, C);
+  // Producer p fills float4 slots p + 448 i (i < 4): row = slot / 56,
+  // column quad = slot % 56 (consecutive lanes read consecutive quads); the
+  // four loads are issued before any exp.
+  constexpr int kSlots = kSumRows * (kTileCols / 4) / kProducers;
+  static_assert(kSlots * kProducers == kSumRows * (kTileCols / 4), "whole slots per producer");
   auto fill = [&](size_t k, int buf) {
-    const size_t c = k * kTileCols + t;
+    const int p = t - kWave;
+    float4 v[kSlots];
+    float mx[kSlots];
+    bool full[kSlots];
 #pragma unroll
-    for (int r = 0; r < kSumRows; ++r) {
-      float e = 0.0f;
-      if (r0 + r < N && c < C) e = expf(logits[(r0 + r) * C + c] - mx[r]);
-      tile[buf][r][t] = e;
+    for (int i = 0; i < kSlots; ++i) {
+      const int f = p + i * kProducers, r = f / (kTileCols / 4), c4 = f % (kTileCols / 4);
+      const size_t row = r0 + r, c = k * kTileCols + 4 * c4;
+      full[i] = vec && row < N && c + 4 <= C;
+      mx[i] = row < N ? row_max[row] : 0.0f;
+      v[i] = full[i] ? *reinterpret_cast<const float4*>(logits + row * C + c)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int f = p + i * kProducers, r = f / (kTileCols / 4), c4 = f % (kTileCols / 4);
+      const size_t row = r0 + r, c = k * kTileCols + 4 * c4;
+      float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (full[i]) {
+        e[0] = expf(v[i].x - mx[i]), e[1] = expf(v[i].y - mx[i]);
+        e[2] = expf(v[i].z - mx[i]), e[3] = expf(v[i].w - mx[i]);
+      } else if (row < N) {
+        for (int u = 0; u < 4; ++u)
+          if (c + u < C) e[u] = expf(logits[row * C + c + u] - mx[i]);
+      }
+      *reinterpret_cast<float4*>(&tile[buf][r][4 * c4]) = make_float4(e[0], e[1], e[2], e[3]);
     }
   };
-  fill(0, 0);
+  if (t >= kWave) fill(0, 0);
   __syncthreads();
   float sum = 0.0f;
   for (size_t k = 0; k < ntiles; ++k) {
-    if (k + 1 < ntiles) fill(k + 1, (k + 1) & 1);
-    if (t < kSumRows) {
+    if (t >= kWave) {
+      if (k + 1 < ntiles) fill(k + 1, (k + 1) & 1);
+    } else if (t < kSumRows) {
       const float* row = tile[k & 1][t];
       const size_t w = k + 1 < ntiles ? kTileCols : C - k * kTileCols;
       if (w == kTileCols) {
-        // The adds are the chain; their LDS reads are not: sixteen values
-        // are read ahead of their adds, which stay in column order.
 #pragma unroll 2
         for (int j0 = 0; j0 < kTileCols; j0 += 16) {
           float4 v[4];
