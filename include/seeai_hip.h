@@ -127,6 +127,8 @@ typedef struct seeai_tile_policy {
   uint32_t relaxed_min_tiles_256; /* relaxed bf16 GEMM: 256x256 tiles from this many (default 256) */
   uint32_t relaxed_min_fill_256;  /* ... and when their last round over the CUs is at least
                                      this percent full (<= 100) */
+  uint32_t relaxed_nt_dma_min_k;  /* relaxed NT on rodata weights: the direct-to-LDS kernel from
+                                     this K, the register-staged one below (default 1024) */
   uint32_t exact_longk_first;     /* exact skinny long-K GEMM: 1 the two-pass form before the
                                      chain kernel (default), 2 the chain kernel first */
 } seeai_tile_policy;

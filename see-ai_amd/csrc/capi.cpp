@@ -1097,6 +1097,7 @@ int seeai_configure(seeai_ctx* c, const seeai_tile_policy* p) {
     if (p->quantize_waves_per_cu) t.quantize_waves_per_cu = static_cast<int>(p->quantize_waves_per_cu);
     if (p->relaxed_min_tiles_256) t.relaxed_min_tiles_256 = p->relaxed_min_tiles_256;
     if (p->relaxed_min_fill_256) t.relaxed_min_fill_256 = static_cast<int>(p->relaxed_min_fill_256);
+    if (p->relaxed_nt_dma_min_k) t.relaxed_nt_dma_min_k = p->relaxed_nt_dma_min_k;
     if (p->exact_longk_first) t.exact_longk_first = static_cast<int>(p->exact_longk_first);
   }
   c->policy = t;
@@ -1110,6 +1111,7 @@ int seeai_policy(const seeai_ctx* c, seeai_tile_policy* out) {
   out->quantize_waves_per_cu = static_cast<uint32_t>(c->policy.quantize_waves_per_cu);
   out->relaxed_min_tiles_256 = static_cast<uint32_t>(c->policy.relaxed_min_tiles_256);
   out->relaxed_min_fill_256 = static_cast<uint32_t>(c->policy.relaxed_min_fill_256);
+  out->relaxed_nt_dma_min_k = static_cast<uint32_t>(c->policy.relaxed_nt_dma_min_k);
   out->exact_longk_first = static_cast<uint32_t>(c->policy.exact_longk_first);
   return SEEAI_OK;
 }

@@ -460,10 +460,10 @@ size_t Bf16DmaKp(size_t K) { return (K + 31) / 32 * 32; }
 bool Bf16DmaFits(const GemmArgs& a) {
   if (!a.relaxed || a.layout > 1 || a.b_kind > 2) return false;
   if (a.M < 128 || a.N < 128 || a.K < 64) return false;
-  // NT over a short K measured faster on the register-staged kernel (the
-  // conversion pass costs more than it saves: 8192 x 768 x 768 and
-  // 8192 x 3072 x 768).
-  if (a.layout == 1 && a.K < 1024) return false;
+  // NT below the tile policy's relaxed_nt_dma_min_k runs the
+  // register-staged kernel (the conversion pass can cost more than it saves
+  // at short K: 8192 x 768 x 768 and 8192 x 3072 x 768).
+  if (a.layout == 1 && a.K < (a.policy ? a.policy->relaxed_nt_dma_min_k : 1024)) return false;
   const size_t Kp = Bf16DmaKp(a.K);
   // 32-bit buffer offsets within a tile and int tile indices.
   if (Kp * 2 * 256 >= (size_t{1} << 31) || a.M >= (size_t{1} << 30) || a.N >= (size_t{1} << 30))

@@ -43,6 +43,8 @@ FIELDS = {
     "relaxed_min_fill_256": (0, ("range", 0, 100),
                              "relaxed bf16 GEMM: 256x256 tiles only when their last round over "
                              "the CUs is at least this percent full"),
+    "relaxed_nt_dma_min_k": (1024, ("range", 64, 1 << 30),
+                             "relaxed NT on rodata weights: the direct-to-LDS kernel from this K"),
     "exact_longk_first": (1, ("choice", 1, 2),
                           "exact skinny long-K GEMM: 1 two-pass workspace form first, "
                           "2 chain kernel first"),

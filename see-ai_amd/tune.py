@@ -45,6 +45,7 @@ ARMS = {
     "quantize_waves_per_cu": [4, 8, 16, 32],
     "relaxed_min_tiles_256": [1, 128, 256, 1 << 30],
     "relaxed_min_fill_256": [0, 50, 80, 95],
+    "relaxed_nt_dma_min_k": [512, 768, 1024, 4096],
     "exact_longk_first": [1, 2],
 }
 
@@ -148,6 +149,17 @@ class Bench:
                 def setup(nt=nt, M=M, N=N, K=K):
                     return self._relaxed_q8(nt, M, N, K)
                 yield f"relaxed q8 {'NT' if nt else 'NN'} {M}x{N}x{K}", setup
+        elif field == "relaxed_nt_dma_min_k":
+            # C4's dX products over f32 weights (K = 768 and 3072) and C5's
+            # q8 ones (K = 2048, 5632): NT, K either side of the threshold.
+            shapes = [("f32", 8192, 768, 768), ("f32", 8192, 3072, 768), ("f32", 8192, 768, 3072),
+                      ("q8", 8192, 2048, 2048), ("q8", 8192, 5632, 2048)]
+            if self.quick:
+                shapes = shapes[:2]
+            for kind, M, N, K in shapes:
+                def setup(kind=kind, M=M, N=N, K=K):
+                    return self._relaxed_nt(kind, M, N, K)
+                yield f"relaxed {kind} NT {M}x{N}x{K}", setup
         elif field == "exact_longk_first":
             for M, N, K in [(64, 64, 8192), (16, 128, 16384)]:
                 def setup(M=M, N=N, K=K):
@@ -199,6 +211,36 @@ class Bench:
         flags = (1 << 5) | (1 << 4)  # kFlagRelaxed | kFlagQ8ColScale
         word = hip.pack_instruction(30 if nt else 29, flags, 0,
                                     [a_off, rb | w_off, c_off, rb | s_off], [M, N, K])
+        self._relaxed_backends.append(be)
+        return (lambda: be.Execute(word), 2.0 * M * N * K, be)
+
+    def _relaxed_nt(self, kind, M, N, K):
+        """A relaxed NT product on a rodata weight [N, K]: f32 (C4's dX) or
+        int8 with k-scales (C5's)."""
+        import numpy as np
+        hip = self.hip
+        be = hip.HipBackend(0)
+        be.ctx.use_torch_stream()
+        r = np.random.default_rng(M + N + K + len(kind))
+        if kind == "q8":
+            W = r.integers(-127, 128, (N, K)).astype(np.int8)
+        else:
+            W = (r.standard_normal((N, K)) * 0.02).astype(np.float32)
+        sc = r.uniform(1e-3, 5e-2, K).astype(np.float32)
+        s_off = (W.nbytes + 255) // 256 * 256
+        rodata = bytearray(s_off + sc.nbytes)
+        rodata[:W.nbytes] = W.tobytes()
+        rodata[s_off:] = sc.tobytes()
+        c_off = (4 * M * K + 16383) // 16384 * 16384
+        be.Bind(None, c_off + 4 * M * N, bytes(rodata))
+        be.Configure(self.ctx.policy())
+        be.Upload(0, r.standard_normal((M, K)).astype(np.float32).tobytes())
+        rb = 1 << 63
+        if kind == "q8":
+            word = hip.pack_instruction(30, (1 << 5) | (1 << 4), 0, [0, rb, c_off, rb | s_off],
+                                        [M, N, K])
+        else:
+            word = hip.pack_instruction(2, 1 << 5, 0, [0, rb, c_off], [M, N, K])
         self._relaxed_backends.append(be)
         return (lambda: be.Execute(word), 2.0 * M * N * K, be)
 

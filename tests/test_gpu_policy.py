@@ -138,3 +138,41 @@ def test_exact_longk_arms_are_bitwise_equal(hip, orc, ctx, torch_cuda):
         outs.append(C.cpu().numpy())
     assert bits_equal(outs[1], outs[0])
     assert bits_equal(outs[0], orc.gemm_nn(A, B))  # both are the reference's quad order
+
+
+@pytest.mark.parametrize("kind", ["f32", "q8"])
+def test_relaxed_nt_kernel_arms_are_bitwise_equal(hip, torch_cuda, kind):
+    """Relaxed NT products below and above relaxed_nt_dma_min_k: the
+    register-staged and the direct-to-LDS bf16 kernels give the same bits
+    (operands rounded once to bf16, MFMA k-slices in order, the same
+    epilogue)."""
+    M, N, K = 384, 768, 768
+    r = rng(21 + len(kind))
+    A = r.standard_normal((M, K)).astype(np.float32)
+    if kind == "q8":
+        W = r.integers(-127, 128, (N, K)).astype(np.int8)
+    else:
+        W = (r.standard_normal((N, K)) * 0.02).astype(np.float32)
+    ks = r.uniform(1e-3, 5e-2, K).astype(np.float32)
+    ar = Arena()
+    a = ar.add("A", A)
+    w, s = ar.add("W", W, rodata=True), ar.add("ks", ks, rodata=True)
+    o = ar.empty("C", (M, N))
+    from tests.plan_ops import ins
+    from tests.arena import f32_bits
+    if kind == "q8":
+        word = ins(30, [a, w, o, s], [M, N, K], flags=(1 << 5) | (1 << 4))
+    else:
+        word = ins(2, [a, w, o], [M, N, K], flags=1 << 5, imm=f32_bits(0.37))
+    arena, ro = ar.images()
+    outs = []
+    for arm in ({"relaxed_nt_dma_min_k": 512}, None):
+        be = hip.HipBackend(0)
+        be.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+        be.Configure(arm)
+        be.Execute(word)
+        be.Flush()
+        outs.append(ar.get(np.frombuffer(be.Download(0, arena.nbytes), np.uint8), "C"))
+        be.ctx.close()
+    assert np.isfinite(outs[0]).all()
+    assert bits_equal(outs[1], outs[0])
