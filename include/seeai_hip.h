@@ -129,6 +129,8 @@ typedef struct seeai_tile_policy {
                                      this percent full (<= 100) */
   uint32_t relaxed_nt_dma_min_k;  /* relaxed NT on rodata weights: the direct-to-LDS kernel from
                                      this K, the register-staged one below (default 1024) */
+  uint32_t convert_wgs_per_cu;    /* workgroups per CU of the relaxed GEMMs' activation
+                                     conversion (default 8, <= 64) */
   uint32_t exact_longk_first;     /* exact skinny long-K GEMM: 1 the two-pass form before the
                                      chain kernel (default), 2 the chain kernel first */
 } seeai_tile_policy;

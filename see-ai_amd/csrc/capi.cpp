@@ -258,7 +258,9 @@ int GemmBf16Dma(seeai_ctx* c, GemmArgs& a, const char* what) {
       c->cvt_bytes = need;
     }
     c->cvt_key = {a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->cur_at};
-    SEEAI_TRY(c, LaunchConvertRowsBf16(a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->cvt, c->stream),
+    SEEAI_TRY(c,
+              LaunchConvertRowsBf16(a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->cvt,
+                                    c->policy.convert_wgs_per_cu, c->stream),
               what);
   }
   SEEAI_TRY(c, LaunchGemmBf16Dma(c->cvt, shadow, a, c->stream), what);
@@ -1089,6 +1091,9 @@ int seeai_configure(seeai_ctx* c, const seeai_tile_policy* p) {
     if (p->relaxed_min_fill_256 > 100)
       return Fail(c, SEEAI_INVALID, "tile policy: relaxed_min_fill_256 %u exceeds 100 percent",
                   p->relaxed_min_fill_256);
+    if (p->convert_wgs_per_cu > 64)
+      return Fail(c, SEEAI_INVALID, "tile policy: convert_wgs_per_cu %u exceeds 64",
+                  p->convert_wgs_per_cu);
     if (p->quantize_waves_per_cu > 32)
       return Fail(c, SEEAI_INVALID, "tile policy: quantize_waves_per_cu %u exceeds 32 waves per CU",
                   p->quantize_waves_per_cu);
@@ -1098,6 +1103,7 @@ int seeai_configure(seeai_ctx* c, const seeai_tile_policy* p) {
     if (p->relaxed_min_tiles_256) t.relaxed_min_tiles_256 = p->relaxed_min_tiles_256;
     if (p->relaxed_min_fill_256) t.relaxed_min_fill_256 = static_cast<int>(p->relaxed_min_fill_256);
     if (p->relaxed_nt_dma_min_k) t.relaxed_nt_dma_min_k = p->relaxed_nt_dma_min_k;
+    if (p->convert_wgs_per_cu) t.convert_wgs_per_cu = static_cast<int>(p->convert_wgs_per_cu);
     if (p->exact_longk_first) t.exact_longk_first = static_cast<int>(p->exact_longk_first);
   }
   c->policy = t;
@@ -1112,6 +1118,7 @@ int seeai_policy(const seeai_ctx* c, seeai_tile_policy* out) {
   out->relaxed_min_tiles_256 = static_cast<uint32_t>(c->policy.relaxed_min_tiles_256);
   out->relaxed_min_fill_256 = static_cast<uint32_t>(c->policy.relaxed_min_fill_256);
   out->relaxed_nt_dma_min_k = static_cast<uint32_t>(c->policy.relaxed_nt_dma_min_k);
+  out->convert_wgs_per_cu = static_cast<uint32_t>(c->policy.convert_wgs_per_cu);
   out->exact_longk_first = static_cast<uint32_t>(c->policy.exact_longk_first);
   return SEEAI_OK;
 }

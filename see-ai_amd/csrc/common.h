@@ -215,6 +215,7 @@ struct TilePolicy {
                                        // the CUs is at least this percent full
   size_t relaxed_nt_dma_min_k = 1024;  // relaxed NT: the direct-to-LDS kernel from this K
                                        // (below it the register-staged bf16 kernel)
+  int convert_wgs_per_cu = 8;          // workgroups per CU of the activation conversion
   int exact_longk_first = 1;           // exact skinny long-K GEMM: 1 the two-pass workspace
                                        // form before the chain kernel, 2 the chain kernel first
 };
@@ -267,7 +268,7 @@ bool Bf16DmaFits(const GemmArgs& a);
 // operands 16-byte aligned, 1 <= lr_k <= kLowRankMaxK).
 bool Bf16DmaLowRankFits(const GemmArgs& a);
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,
-                                 const float* kscale, void* out, hipStream_t s);
+                                 const float* kscale, void* out, int wgs_per_cu, hipStream_t s);
 hipError_t LaunchWeightShadow(const GemmArgs& a, void* out, hipStream_t s);
 hipError_t LaunchGemmBf16Dma(const void* A, const void* W, const GemmArgs& a, hipStream_t s);
 // Relaxed NN / NT with f32 or int8 weights on bf16 MFMA (k_gemm_bf16.hip),

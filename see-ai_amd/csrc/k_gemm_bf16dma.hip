@@ -479,15 +479,15 @@ bool Bf16DmaLowRankFits(const GemmArgs& a) {
 }
 
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,
-                                 const float* kscale, void* out, hipStream_t s) {
+                                 const float* kscale, void* out, int wgs_per_cu, hipStream_t s) {
   if (M == 0) return hipSuccess;
   const size_t groups = M * K / 8;
   if (K % 32 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(kscale) & 15) == 0 && groups < (size_t{1} << 31)) {
-    // Eight workgroups per CU, four groups per lane per trip.
+    // wgs_per_cu workgroups per CU (tile policy), four groups per lane per trip.
     const unsigned grid = static_cast<unsigned>(
         std::min<size_t>((groups + 4 * kCvtThreads - 1) / (4 * kCvtThreads),
-                         static_cast<size_t>(DeviceCUs()) * 8));
+                         static_cast<size_t>(DeviceCUs()) * (wgs_per_cu > 0 ? wgs_per_cu : 8)));
     const unsigned g = static_cast<unsigned>(groups), kg = static_cast<unsigned>(K / 8);
     if (kscale)
       hipLaunchKernelGGL((ConvertFlatKernel<true>), dim3(grid), dim3(kCvtThreads), 0, s, A, g, kg,

@@ -65,6 +65,7 @@ class TilePolicy(C.Structure):
     _fields_ = [("w8a8_large_kernel", C.c_uint32), ("w8a8_large_min", C.c_uint32),
                 ("quantize_waves_per_cu", C.c_uint32), ("relaxed_min_tiles_256", C.c_uint32),
                 ("relaxed_min_fill_256", C.c_uint32), ("relaxed_nt_dma_min_k", C.c_uint32),
+                ("convert_wgs_per_cu", C.c_uint32),
                 ("exact_longk_first", C.c_uint32)]
 
 

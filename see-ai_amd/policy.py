@@ -45,6 +45,8 @@ FIELDS = {
                              "the CUs is at least this percent full"),
     "relaxed_nt_dma_min_k": (1024, ("range", 64, 1 << 30),
                              "relaxed NT on rodata weights: the direct-to-LDS kernel from this K"),
+    "convert_wgs_per_cu": (8, ("range", 1, 64),
+                           "workgroups per CU of the relaxed GEMMs' activation conversion"),
     "exact_longk_first": (1, ("choice", 1, 2),
                           "exact skinny long-K GEMM: 1 two-pass workspace form first, "
                           "2 chain kernel first"),

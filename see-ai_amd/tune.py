@@ -46,6 +46,7 @@ ARMS = {
     "relaxed_min_tiles_256": [1, 128, 256, 1 << 30],
     "relaxed_min_fill_256": [0, 50, 80, 95],
     "relaxed_nt_dma_min_k": [512, 768, 1024, 4096],
+    "convert_wgs_per_cu": [2, 4, 8, 16, 32],
     "exact_longk_first": [1, 2],
 }
 
@@ -160,6 +161,18 @@ class Bench:
                 def setup(kind=kind, M=M, N=N, K=K):
                     return self._relaxed_nt(kind, M, N, K)
                 yield f"relaxed {kind} NT {M}x{N}x{K}", setup
+        elif field == "convert_wgs_per_cu":
+            # Relaxed products whose A conversion dominates (N = 128): the
+            # decoder's activation widths, NN and NT (k-scaled).
+            for kind, nt, M, K in [("q8", 0, 8192, 2048), ("q8", 0, 8192, 5632), ("q8", 1, 8192, 2048),
+                                   ("f32", 0, 8192, 768)]:
+                def setup(kind=kind, nt=nt, M=M, K=K):
+                    if nt:
+                        return self._relaxed_nt(kind, M, 128, K)
+                    if kind == "q8":
+                        return self._relaxed_q8(0, M, 128, K)
+                    return self._relaxed_f32_nn(M, 128, K)
+                yield f"convert {kind} {'NT' if nt else 'NN'} {M}x{K}", setup
         elif field == "exact_longk_first":
             for M, N, K in [(64, 64, 8192), (16, 128, 16384)]:
                 def setup(M=M, N=N, K=K):
@@ -241,6 +254,22 @@ class Bench:
                                         [M, N, K])
         else:
             word = hip.pack_instruction(2, 1 << 5, 0, [0, rb, c_off], [M, N, K])
+        self._relaxed_backends.append(be)
+        return (lambda: be.Execute(word), 2.0 * M * N * K, be)
+
+    def _relaxed_f32_nn(self, M, N, K):
+        """A relaxed NN product on an f32 rodata weight [K, N] (C4's forward)."""
+        import numpy as np
+        hip = self.hip
+        be = hip.HipBackend(0)
+        be.ctx.use_torch_stream()
+        r = np.random.default_rng(M + N + K + 7)
+        W = (r.standard_normal((K, N)) * 0.02).astype(np.float32)
+        c_off = (4 * M * K + 16383) // 16384 * 16384
+        be.Bind(None, c_off + 4 * M * N, W.tobytes())
+        be.Configure(self.ctx.policy())
+        be.Upload(0, r.standard_normal((M, K)).astype(np.float32).tobytes())
+        word = hip.pack_instruction(1, 1 << 5, 0, [0, 1 << 63, c_off], [M, N, K])
         self._relaxed_backends.append(be)
         return (lambda: be.Execute(word), 2.0 * M * N * K, be)
 

@@ -107,7 +107,8 @@ def test_relaxed_tile_arms_are_bitwise_equal(hip, torch_cuda, nt):
     arena, ro = ar.images()
     outs = []
     for arm in ({"relaxed_min_tiles_256": 1}, {"relaxed_min_tiles_256": 1 << 30}, None,
-                {"relaxed_min_tiles_256": 1, "relaxed_min_fill_256": 100}):
+                {"relaxed_min_tiles_256": 1, "relaxed_min_fill_256": 100},
+                {"convert_wgs_per_cu": 1}, {"convert_wgs_per_cu": 64}):
         be = hip.HipBackend(0)
         be.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
         be.Configure(arm)
