@@ -124,9 +124,11 @@ def lora_probe(which: str):
     for _ in range(n):
         loss = eng.train_resident()
     dt = (time.perf_counter() - t0) / n
+    fused, dropped = eng.fused_dispatches(), eng.dropped_stores()
     eng.close()
     print(f"lora probe: decoder LoRA ({which}) relaxed, {n} resident steps, "
-          f"{dt * 1e3:.1f} ms/step, {T / dt:.0f} tokens/s, loss {loss:.4f}", flush=True)
+          f"{dt * 1e3:.1f} ms/step, {T / dt:.0f} tokens/s, loss {loss:.4f}, "
+          f"{fused} fused dispatches, {dropped} dead stores dropped", flush=True)
     return 0
 
 
@@ -512,6 +514,7 @@ def lora_steps(torch, hip):
         "ms_per_step": round(dt * 1e3, 2), "tokens_s": round(T / dt), "TFLOP_s": round(tf, 1),
         "bf16_mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop_per_step": flops, "loss": loss,
         "steps_timed": n, "fused_dispatches": eng.fused_dispatches(),
+        "dropped_stores": eng.dropped_stores(),
         "config": "16 layers, d2048, 32 heads, SiLU-gated FFN 5632, RMSNorm, vocab 32000, "
                   "B4 x S2048, int8 base (per-column scales), LoRA r16 on Q/K/V/O",
         "plan_build_s": round(build_s, 1), "plan_load_s": round(load_s, 1)}

@@ -109,6 +109,11 @@ int seeai_end_range(seeai_ctx* ctx);
  * dispatches ran (ExecutorBackend::fused_dispatches, backend.h:165). */
 int seeai_set_fusion(seeai_ctx* ctx, int allow);
 uint64_t seeai_fused_dispatches(const seeai_ctx* ctx);
+/* How many stores fused passes skipped as dead: a LoRA site's base value,
+ * or the SwiGLU backward's dh*up product, that the program overwrites before
+ * any read or never touches again (metal_backend.mm:1281-1313).
+ * SEEAI_KEEP_DEAD_STORES=1 at seeai_create keeps every store. */
+uint64_t seeai_dropped_stores(const seeai_ctx* ctx);
 /* Waits for the stream; reports a refusal raised on the device since the
  * last flush (non-finite clip norm: nothing it guarded was written). */
 int seeai_flush(seeai_ctx* ctx);

@@ -19,6 +19,7 @@
 #include <map>
 #include <string>
 #include <tuple>
+#include <vector>
 
 #include "../../include/seeai_hip.h"
 #include "common.h"
@@ -98,6 +99,10 @@ struct seeai_ctx {
   int allow_fusion = 1;
   int allow_dma = 1;  // relaxed frozen-weight GEMMs on the bf16 shadow path
   int allow_lowrank = 1;  // LoRA sites folded into the frozen product's epilogue
+  int allow_dead_store_drop = 1;  // fused passes skip stores the range overwrites unread
+  uint64_t dropped_stores = 0;
+  const uint8_t* dead_prog = nullptr;  // the program `dead` was decided for
+  std::vector<int8_t> dead;  // per instruction: -1 undecided, 0 kept, 1 dropped
   TilePolicy policy;  // kernel geometry (seeai_configure)
   // The relaxed GEMMs' bf16 copy of their activations, and what it holds:
   // a later relaxed GEMM of the same range that rounds the same bytes the
@@ -732,6 +737,10 @@ int seeai_create(int device, seeai_ctx** out) {
   // same-session control of the low-rank fold (the reference's Metal backend
   // keeps SEEML_METAL_UNFUSED_LOWRANK for the same purpose).
   if (const char* e = std::getenv("SEEAI_UNFUSED_LOWRANK"); e && e[0] == '1') c->allow_lowrank = 0;
+  // SEEAI_KEEP_DEAD_STORES=1 keeps every store of a fused pass (the
+  // same-session control of the dead-store scan).
+  if (const char* e = std::getenv("SEEAI_KEEP_DEAD_STORES"); e && e[0] == '1')
+    c->allow_dead_store_drop = 0;
   int rc = Hip(c, hipSetDevice(device), "set device");
   if (rc == SEEAI_OK) rc = Hip(c, hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "stream");
   if (rc == SEEAI_OK) rc = Hip(c, hipMalloc(&c->small, kSmallBytes), "small alloc");
@@ -780,6 +789,7 @@ uint64_t seeai_relaxed_executions(const seeai_ctx* c) { return c ? c->relaxed : 
 int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t rodata_bytes) {
   if (!c) return SEEAI_INVALID;
   c->cvt_key.at = nullptr;
+  c->dead_prog = nullptr;  // dead-store decisions name the old binding's pointers
   const uint64_t bytes = (arena_bytes + kArenaAlignment - 1) / kArenaAlignment * kArenaAlignment;
   uint8_t* arena = nullptr;
   uint8_t* ro = nullptr;
@@ -807,8 +817,9 @@ int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t 
 }
 
 int seeai_bind_source(seeai_ctx* c, const void* data, uint64_t bytes) {
-  if (c) c->cvt_key.at = nullptr;
   if (!c) return SEEAI_INVALID;
+  c->cvt_key.at = nullptr;
+  c->dead_prog = nullptr;
   SEEAI_TRY(c, hipStreamSynchronize(c->stream), "bind_source drain");
   DropShadows(c);  // some may be of the old source image
   if (c->source) (void)hipFree(c->source);
@@ -870,6 +881,219 @@ bool Hits(const Extent& x, const Extent* set, int n) {
   for (int i = 0; i < n; ++i)
     if (Overlap(x.p, x.n, set[i].p, set[i].n)) return true;
   return false;
+}
+
+// --- Dead-store scan ----------------------------------------------------------
+// One operand's byte extent and whether the instruction writes it (a
+// read-modify-write operand is one write extent, as the reference's
+// validator describes it, plan_validator.cc:365-745).
+struct Touch {
+  const uint8_t* p;
+  uint64_t n;
+  bool write;
+};
+
+// Every operand extent of an instruction, with the validator's roles and
+// sizes (plan_validator.cc:368-745).  False for opcodes not modelled here.
+bool TouchExtents(seeai_ctx* c, const Instruction& ins, Touch* out, int* n) {
+  const Ptrs R{c};
+  int k = 0;
+  const auto add = [&](uint64_t ref, uint64_t floats, bool w) {
+    if (ref != kNullRef && floats) out[k++] = {R.at(ref), floats * 4, w};
+  };
+  const uint64_t d0 = ins.out[0], d1 = ins.out[1];
+  const uint64_t hi0 = d0 >> 32, lo0 = d0 & 0xFFFFFFFFu;
+  GemmArgs g{};
+  if (DecodeGemm(c, ins, &g)) {
+    Extent r[8];
+    const int nr = GemmReads(g, r);
+    for (int i = 0; i < nr; ++i) out[k++] = {r[i].p, r[i].n, false};
+    const Extent w = GemmWrites(g);
+    out[k++] = {w.p, w.n, true};
+    *n = k;
+    return true;
+  }
+  // Attention geometry: (B, S, H, d) from two words or one packed word.
+  const auto split = [](uint64_t bs, uint64_t hd, uint64_t* B, uint64_t* S, uint64_t* H,
+                        uint64_t* d) {
+    *B = bs >> 32, *S = bs & 0xFFFFFFFFu, *H = hd >> 32, *d = hd & 0xFFFFFFFFu;
+  };
+  const auto packed = [](uint64_t w, uint64_t* B, uint64_t* S, uint64_t* H, uint64_t* d) {
+    *B = w >> 48, *S = (w >> 32) & 0xFFFF, *H = (w >> 16) & 0xFFFF, *d = w & 0xFFFF;
+  };
+  uint64_t B, S, H, d;
+  switch (ins.opcode) {
+    case 0:
+      break;
+    case 5: case 21: case 8: case 23: case 25:  // AddEW, MulEW, activation backward
+      add(ins.in[0], d0, false), add(ins.in[1], d0, false), add(ins.in[2], d0, true);
+      break;
+    case 6:  // AddBias
+      add(ins.in[0], d0 * d1, false), add(ins.in[1], d1, false), add(ins.in[2], d0 * d1, true);
+      break;
+    case 7: case 22: case 24: case 9: case 20:  // activation forward, Scale, Copy
+      add(ins.in[0], d0, false), add(ins.in[1], d0, true);
+      break;
+    case 42:  // Accumulate: dst read and written, src
+      add(ins.in[0], d0, true), add(ins.in[1], d0, false);
+      break;
+    case 19:  // Fill
+      add(ins.in[0], d0, true);
+      break;
+    case 10:  // ReduceRows
+      add(ins.in[0], d0 * d1, false), add(ins.in[1], d1, true);
+      break;
+    case 11: case 51:  // SoftmaxXEnt forward: logits, labels, loss, probabilities
+      add(ins.in[0], d0 * d1, false), add(ins.in[1], d0, false), add(ins.in[2], 1, true),
+          add(ins.in[3], d0 * d1, true);
+      break;
+    case 12: case 52:  // SoftmaxXEnt backward
+      add(ins.in[0], d0 * d1, false), add(ins.in[1], d0, false), add(ins.in[2], 1, false),
+          add(ins.in[3], d0 * d1, true);
+      break;
+    case 17:  // SgdStep
+      add(ins.in[0], d0, true), add(ins.in[1], d0, false);
+      break;
+    case 18:  // AdamWStep
+      add(ins.in[0], d0, true), add(ins.in[1], d0, false), add(ins.in[2], d0, true),
+          add(ins.in[3], d0, true);
+      break;
+    case 28:  // ClipNorm
+      add(ins.in[0], d0, true);
+      break;
+    case 53:  // SqNormAccum
+      add(ins.in[0], d0, false), add(ins.in[1], 1, true);
+      break;
+    case 54:  // ClipGlobal
+      add(ins.in[0], d0, true), add(ins.in[1], 1, false);
+      break;
+    case 26:  // LayerNormFwd: x, gamma, beta -> y, mean, rstd
+      add(ins.in[0], hi0 * lo0, false), add(ins.in[1], lo0, false), add(ins.in[2], lo0, false),
+          add(ins.in[3], hi0 * lo0, true), add(ins.out[1], hi0, true), add(ins.out[2], hi0, true);
+      break;
+    case 27: {  // LayerNormBwd: dy, x, gamma, mean, rstd -> dx
+      const uint64_t rows = ins.out[2] >> 32, cols = ins.out[2] & 0xFFFFFFFFu;
+      add(ins.in[0], rows * cols, false), add(ins.in[1], rows * cols, false),
+          add(ins.in[2], cols, false), add(ins.in[3], rows * cols, true),
+          add(ins.out[0], rows, false), add(ins.out[1], rows, false);
+      break;
+    }
+    case 31:  // RmsNormFwd: x, g -> y, rstd
+      add(ins.in[0], hi0 * lo0, false), add(ins.in[1], lo0, false),
+          add(ins.in[2], hi0 * lo0, true), add(ins.in[3], hi0, true);
+      break;
+    case 32: {  // RmsNormBwd: dy, x, g, rstd -> dx
+      const uint64_t rows = d1 >> 32, cols = d1 & 0xFFFFFFFFu;
+      add(ins.in[0], rows * cols, false), add(ins.in[1], rows * cols, false),
+          add(ins.in[2], cols, false), add(ins.in[3], rows * cols, true),
+          add(ins.out[0], rows, false);
+      break;
+    }
+    case 33: case 34:  // RoPE: x -> y, optional [S, d] table
+      split(d0, d1, &B, &S, &H, &d);
+      add(ins.in[0], B * S * H * d, false), add(ins.in[1], B * S * H * d, true),
+          add(ins.in[2], S * d, false);
+      break;
+    case 45:  // RopeTable
+      add(ins.in[0], hi0 * lo0, true);
+      break;
+    case 46:  // FusedMap
+      add(ins.in[0], d0, false), add(ins.in[1], d0, false), add(ins.in[2], d0, false),
+          add(ins.in[3], d0, true);
+      break;
+    case 41:  // EmbedFwd: tokens, [V, D] table -> rows
+      add(ins.in[0], d0, false), add(ins.in[1], (d1 >> 32) * (d1 & 0xFFFFFFFFu), false),
+          add(ins.in[2], d0 * (d1 & 0xFFFFFFFFu), true);
+      break;
+    case 55:  // SegmentStarts
+      add(ins.in[0], hi0 * lo0, false), add(ins.in[1], hi0 * lo0, true);
+      break;
+    case 35: case 56:  // AttnFwd (+Seg): q, k, v -> o, probabilities
+      if (ins.opcode == 35) split(d1, ins.out[2], &B, &S, &H, &d);
+      else packed(d1, &B, &S, &H, &d), add(ins.out[2], B * S, false);
+      for (int i = 0; i < 3; ++i) add(ins.in[i], B * S * H * d, false);
+      add(ins.in[3], B * S * H * d, true), add(ins.out[0], B * H * S * S, true);
+      break;
+    case 36:  // AttnDP
+      split(d0, d1, &B, &S, &H, &d);
+      add(ins.in[0], B * S * H * d, false), add(ins.in[1], B * S * H * d, false),
+          add(ins.in[2], B * H * S * S, true);
+      break;
+    case 37: case 39: case 40:  // AttnDV, AttnDQ, AttnDK
+      split(d0, d1, &B, &S, &H, &d);
+      add(ins.in[0], B * H * S * S, false), add(ins.in[1], B * S * H * d, false),
+          add(ins.in[2], B * S * H * d, true);
+      break;
+    case 38:  // SoftmaxRowsBwd
+      add(ins.in[0], hi0 * lo0, false), add(ins.in[1], hi0 * lo0, false),
+          add(ins.in[2], hi0 * lo0, true);
+      break;
+    case 47: case 57:  // AttnFwdTiled (+Seg): q, k, v -> o, [B*H*S, 4] stats
+      if (ins.opcode == 47) split(d1, ins.out[2], &B, &S, &H, &d);
+      else packed(d1, &B, &S, &H, &d), add(ins.out[2], B * S, false);
+      for (int i = 0; i < 3; ++i) add(ins.in[i], B * S * H * d, false);
+      add(ins.in[3], B * S * H * d, true), add(ins.out[0], B * S * H * 4, true);
+      break;
+    case 48: case 49: case 50:  // tiled dQ / dK / dV: dQ also writes the stats
+      packed(ins.out[2], &B, &S, &H, &d);
+      for (int i = 0; i < 4; ++i) add(ins.in[i], B * S * H * d, false);
+      add(ins.out[0], B * S * H * 4, ins.opcode == 48), add(ins.out[1], B * S * H * d, true);
+      break;
+    default:
+      return false;
+  }
+  *n = k;
+  return true;
+}
+
+// Whether an opcode's write extents are stores alone; the others read what
+// they write (metal_backend.mm:1139-1152).
+bool OverwritesWhatItWrites(uint16_t op) {
+  switch (op) {
+    case 4: case 42: case 28: case 53: case 54: case 17: case 18: case 48:
+      return false;
+    default:
+      return true;
+  }
+}
+
+// Whether the store of E made by the instruction before index `from` is
+// dead, under the reference's rule for a LoRA site's base value
+// (metal_backend.mm:1281-1313): over the whole program, not the range, the
+// first instruction at or after `from` to touch E writes all of it, reads
+// none of it and overwrites what it writes, or no instruction touches it.
+// An instruction whose extents are not modelled keeps the store.
+bool DeadFrom(seeai_ctx* c, uint64_t from, const Extent& E) {
+  for (uint64_t k = from; k < c->prog_count; ++k) {
+    Instruction ins;
+    std::memcpy(&ins, c->prog + k * 64, sizeof ins);
+    Touch t[16];
+    int n = 0;
+    if (!TouchExtents(c, ins, t, &n)) return false;
+    bool touched = false, read = false, covered = false;
+    for (int i = 0; i < n; ++i) {
+      if (!Overlap(t[i].p, t[i].n, E.p, E.n)) continue;
+      touched = true;
+      if (!t[i].write) read = true;
+      else if (t[i].p <= E.p && E.p + E.n <= t[i].p + t[i].n) covered = true;
+    }
+    if (touched) return covered && !read && OverwritesWhatItWrites(ins.opcode);
+  }
+  return true;
+}
+
+// DeadFrom, decided once per program and instruction: the answer depends on
+// the program's words and the binding alone (dropped at bind).
+bool DeadStore(seeai_ctx* c, uint64_t at_idx, uint64_t from, const Extent& E) {
+  if (!c->allow_dead_store_drop) return false;
+  if (c->dead_prog != c->prog || c->dead.size() != c->prog_count) {
+    c->dead_prog = c->prog;
+    c->dead.assign(c->prog_count, -1);
+  }
+  int8_t& v = c->dead[at_idx];
+  if (v < 0) v = DeadFrom(c, from, E) ? 1 : 0;
+  if (v) ++c->dropped_stores;
+  return v != 0;
 }
 
 // Range-level fusion of a LoRA site (the seam's whole-program visibility,
@@ -941,6 +1165,9 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
           Hits(out_a, &r_b, 1) || Hits(out_b, reads_a, na) || Hits(out_b, &t_b, 1) ||
           Hits(out_b, &r_b, 1))
         return -1;
+      // C's store is dropped where the rest of the range overwrites C
+      // before anything reads it.
+      if (DeadStore(c, idx, j + 1, out_a)) a.lr_store_c = 0;
       if (gap) {
         if (int rc = ExecuteOne(c, mid, P)) return rc;
       }
@@ -1011,7 +1238,11 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
                 *b2 = R.f(m2.in[1]), *x = R.f(n2.in[1]);
     float *o1 = R.f(m1.in[2]), *o2 = R.f(m2.in[2]), *dx = R.f(n2.in[2]);
     if (!clear({o1, o2, dx}, {a1, b1, a2, b2, x})) return -1;
-    SEEAI_TRY(c, LaunchSwigluBwd(a1, b1, o1, a2, b2, o2, x, dx, n, c->stream), "swiglu_bwd");
+    // The product SiluBwd reads is stored only where the range reads it again.
+    float* o1_store = o1;
+    if (DeadStore(c, idx, idx + 3, Extent{reinterpret_cast<const uint8_t*>(o1), nb}))
+      o1_store = nullptr;
+    SEEAI_TRY(c, LaunchSwigluBwd(a1, b1, o1_store, a2, b2, o2, x, dx, n, c->stream), "swiglu_bwd");
     c->done[0] = at + 64;
     c->done[1] = at + 128;
     c->ndone = 2;
@@ -1075,6 +1306,7 @@ int seeai_set_fusion(seeai_ctx* c, int allow) {
 }
 
 uint64_t seeai_fused_dispatches(const seeai_ctx* c) { return c ? c->fused : 0; }
+uint64_t seeai_dropped_stores(const seeai_ctx* c) { return c ? c->dropped_stores : 0; }
 
 int seeai_configure(seeai_ctx* c, const seeai_tile_policy* p) {
   if (!c) return SEEAI_INVALID;

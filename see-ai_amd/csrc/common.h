@@ -282,7 +282,8 @@ int DeviceCUs();
 // SwiGLU's elementwise chains as one pass each (range fusion of adjacent
 // instructions over the same n; every output disjoint from every other
 // operand).  Forward: y = SiLU(x), h = y * u.  Backward: o1 = a1 * b1,
-// o2 = a2 * b2, dx = SiluBwd(o1, x).  The standalone kernels' expressions.
+// o2 = a2 * b2, dx = SiluBwd(o1, x), o1 not stored when null (a dead store).
+// The standalone kernels' expressions.
 hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, size_t n,
                          hipStream_t s);
 hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const float* a2,

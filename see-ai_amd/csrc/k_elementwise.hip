@@ -357,6 +357,8 @@ SiluMul4(const float4* __restrict__ x, const float4* __restrict__ u, float4* __r
   }
 }
 
+// kStoreO1 false: the first product is dead after the pass and is not stored.
+template <bool kStoreO1>
 __global__ void __launch_bounds__(kThreads)
 SwigluBwd4(const float4* __restrict__ a1, const float4* __restrict__ b1, float4* __restrict__ o1,
            const float4* __restrict__ a2, const float4* __restrict__ b2, float4* __restrict__ o2,
@@ -365,7 +367,7 @@ SwigluBwd4(const float4* __restrict__ a1, const float4* __restrict__ b1, float4*
   for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
     const float4 p = a1[i], q = b1[i], r = a2[i], t = b2[i], v = x[i];
     const float4 m1 = make_float4(p.x * q.x, p.y * q.y, p.z * q.z, p.w * q.w);
-    o1[i] = m1;
+    if constexpr (kStoreO1) o1[i] = m1;
     o2[i] = make_float4(r.x * t.x, r.y * t.y, r.z * t.z, r.w * t.w);
     dx[i] = make_float4(SiluBwdExpr(m1.x, v.x), SiluBwdExpr(m1.y, v.y), SiluBwdExpr(m1.z, v.z),
                         SiluBwdExpr(m1.w, v.w));
@@ -407,13 +409,18 @@ hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const fl
     if (n == 0) return hipSuccess;
     const auto c4 = [](const float* p) { return reinterpret_cast<const float4*>(p); };
     const auto m4 = [](float* p) { return reinterpret_cast<float4*>(p); };
-    hipLaunchKernelGGL(SwigluBwd4, dim3(GridFor(n / 4, kThreads, 8192)), dim3(kThreads), 0, s,
-                       c4(a1), c4(b1), m4(o1), c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4);
+    const dim3 grid(GridFor(n / 4, kThreads, 8192));
+    if (o1)
+      hipLaunchKernelGGL(SwigluBwd4<true>, grid, dim3(kThreads), 0, s, c4(a1), c4(b1), m4(o1),
+                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4);
+    else
+      hipLaunchKernelGGL(SwigluBwd4<false>, grid, dim3(kThreads), 0, s, c4(a1), c4(b1), m4(o1),
+                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4);
     return hipGetLastError();
   }
   return Map(n, s, [=] __device__(size_t i) {
     const float m1 = a1[i] * b1[i];
-    o1[i] = m1;
+    if (o1) o1[i] = m1;
     o2[i] = a2[i] * b2[i];
     dx[i] = SiluBwdExpr(m1, x[i]);
   });

@@ -90,6 +90,7 @@ EXPORTS = {
     "seeai_end_range": (_I, [_P]),
     "seeai_set_fusion": (_I, [_P, _I]),
     "seeai_fused_dispatches": (_U64, [_P]),
+    "seeai_dropped_stores": (_U64, [_P]),
     "seeai_flush": (_I, [_P]),
     "seeai_configure": (_I, [_P, C.POINTER(TilePolicy)]),
     "seeai_policy": (_I, [_P, C.POINTER(TilePolicy)]),
@@ -300,6 +301,9 @@ class HipBackend:
     def fused_dispatches(self) -> int:  # backend.h:165
         return int(_lib.seeai_fused_dispatches(self.ctx.h))
 
+    def dropped_stores(self) -> int:
+        return int(_lib.seeai_dropped_stores(self.ctx.h))
+
     def SetFusion(self, allow: bool):
         self.ctx.call("seeai_set_fusion", int(bool(allow)))
 
@@ -447,6 +451,9 @@ class Engine:
 
     def fused_dispatches(self) -> int:
         return int(_lib.seeai_fused_dispatches(_lib.seeai_engine_context(self.h)))
+
+    def dropped_stores(self) -> int:
+        return int(_lib.seeai_dropped_stores(_lib.seeai_engine_context(self.h)))
 
     def configure(self, policy=None):
         """The backend's kernel geometry (HipBackend.Configure)."""

@@ -223,7 +223,7 @@ def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch
     pairs: three steps with fusion on and off give the same losses and
     persistent bytes."""
     T = TINY_Q8["batch"] * TINY_Q8["seq"]
-    curves, states, fused = [], [], []
+    curves, states, fused, dropped = [], [], [], []
     for allow in (True, False):
         img = pw.decoder_q8_lora(hip.plan_self_hash, relaxed=True, **TINY_Q8)
         eng = hip.Engine(img.blob)
@@ -235,9 +235,12 @@ def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch
         curves.append(np.array(curve, np.float32))
         states.append(eng.read(0, img.header["persistent_size"]))
         fused.append(eng.fused_dispatches())
+        dropped.append(eng.dropped_stores())
         eng.close()
     # per step and block: 4 LoRA forwards, the dK / dV pair, 2 SwiGLU chains
     assert fused[0] == 3 * TINY_Q8["layers"] * 7 and fused[1] == 0
+    # the base values no later instruction reads (30 here): same bits without them
+    assert dropped[0] > 0 and dropped[1] == 0
     assert curves[0].tobytes() == curves[1].tobytes()
     assert states[0] == states[1]
 

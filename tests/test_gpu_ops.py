@@ -637,20 +637,50 @@ def _lora_site_program(ar, r, kind, M, Din, Dout, rank, t_over_c0=False):
             ins(2, [dt, A, p2, p1], [M, Din, rank], flags=1 << 3)]
 
 
+def _restored(image, ar, names, init):
+    """The arena image with the named slots put back to their bytes in
+    `init`: what a range leaves where a fused pass skipped a dead store."""
+    out = np.array(image, copy=True)
+    for name in names:
+        _, off, dtype, shape = ar.meta[name]
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        out[off:off + n] = init[off:off + n]
+    return out
+
+
+def _readers(ar, names):
+    """Copies of the named slots into fresh ones: later reads that keep the
+    stores of those slots live."""
+    from tests.plan_ops import ins
+    out = []
+    for name in names:
+        _, off, _, shape = ar.meta[name]
+        dst = ar.empty(name + "_read", shape)
+        out.append(ins(20, [off, dst], [int(np.prod(shape))]))
+    return out
+
+
 @pytest.mark.parametrize("kind", ["q8", "f32"])
-@pytest.mark.parametrize("M,Din,Dout,rank", [(512, 1024, 1024, 16), (300, 1024, 2048, 8),
-                                             (2048, 2048, 1280, 16)])
+@pytest.mark.parametrize("M,Din,Dout,rank,read_later", [
+    (512, 1024, 1024, 16, False), (512, 1024, 1024, 16, True), (300, 1024, 2048, 8, False),
+    (2048, 2048, 1280, 16, True)])
 def test_lora_site_folds_into_the_frozen_product_bitwise(hip, orc, backend, kind, M, Din, Dout,
-                                                         rank):
+                                                         rank, read_later):
     """With the range visible, each LoRA site runs as one dispatch: the
-    frozen product with the rank-r term in its epilogue (C stored as before,
-    C' = C + s (t B) in the rank-r instruction's exact chain).  The arena is
-    bitwise that of the five instructions run one by one; the relaxed count
-    is unchanged and two fused dispatches are counted."""
+    frozen product with the rank-r term in its epilogue (C' = C + s (t B) in
+    the rank-r instruction's exact chain).  C is stored where the program
+    reads it later (read_later: the arena is bitwise that of the
+    instructions run one by one) and dropped where nothing touches it again
+    (metal_backend.mm:1281-1313: the arena is that of the instructions one
+    by one with C0 and P1 as they were).  The relaxed count is unchanged and
+    two fused dispatches are counted."""
     ar = Arena()
     prog = _lora_site_program(ar, rng(M + Din + rank), kind, M, Din, Dout, rank)
+    if read_later:
+        prog += _readers(ar, ["C0", "P1"])
     cpu, apart = execute(hip, orc, backend, ar, prog)
     before, relaxed_before = backend.fused_dispatches(), backend.relaxed_executions()
+    dropped_before = backend.dropped_stores()
     arena, ro = ar.images()
     backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
     backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
@@ -658,11 +688,54 @@ def test_lora_site_folds_into_the_frozen_product_bitwise(hip, orc, backend, kind
     fused = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
     assert backend.fused_dispatches() - before == 2
     assert backend.relaxed_executions() - relaxed_before == 2
-    assert fused.tobytes() == apart.tobytes()
-    for name in ["C0", "C", "P1", "P2"]:
+    dead = [] if read_later else ["C0", "P1"]
+    assert backend.dropped_stores() - dropped_before == len(dead)
+    assert fused.tobytes() == _restored(apart, ar, dead, arena).tobytes()
+    for name in ["C", "P2"] + (["C0", "P1", "C0_read", "P1_read"] if read_later else []):
         e = maxrel(ar.get(fused, name), ar.get(cpu, name))
         assert e <= TOL_BF16, f"{name}: {e:.3g}"
     assert bits_equal(ar.get(fused, "t"), ar.get(cpu, "t"))  # the exact t product
+
+
+@pytest.mark.parametrize("after", ["overwrite", "partial", "accumulate", "unmodelled"])
+def test_lora_site_store_drop_follows_the_first_touch(hip, orc, backend, after):
+    """The first instruction after the site to touch C decides, over the
+    whole program and not the range (the reference's rule): a plain full
+    overwrite leaves the store dead; a partial write, an accumulation into C
+    (it reads what it writes) or an opcode whose extents are not modelled
+    (kMseFwd, named in a part of the program the range stops short of) keep
+    it.  Either way the arena holds the bytes of the instructions one by one."""
+    import ctypes as C
+    from tests.plan_ops import ins
+    M, Din, Dout, rank = 256, 1024, 1024, 16
+    ar = Arena()
+    prog = _lora_site_program(ar, rng(3), "q8", M, Din, Dout, rank)[:3]
+    c0 = ar.meta["C0"][1]
+    z = ar.add("z", rng(4).standard_normal((M, Dout)).astype(np.float32))
+    tail = {"overwrite": [ins(20, [z, c0], [M * Dout])],
+            "partial": [ins(20, [z, c0], [M * Dout // 2]), ins(20, [c0, z], [M * Dout])],
+            "accumulate": [ins(42, [c0, z], [M * Dout])],
+            "unmodelled": [ins(13, [z, z, c0], [M * Dout]), ins(20, [z, c0], [M * Dout])]}[after]
+    dead = after == "overwrite"
+    run = prog + ([] if after == "unmodelled" else tail)  # what executes
+    _, want = execute(hip, orc, backend, ar, run)
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    dropped_before = backend.dropped_stores()
+    whole = b"".join(prog + tail)
+    buf = C.create_string_buffer(whole, len(whole))
+    sp = hip.StepParams(*PARAMS[:5], 0, PARAMS[5])
+    ctx = backend.ctx
+    ctx.call("seeai_begin_range", buf, len(prog + tail), 0, len(run))
+    for i in range(len(run)):
+        ctx.call("seeai_execute", C.cast(C.addressof(buf) + 64 * i, C.c_void_p), C.byref(sp))
+    ctx.call("seeai_end_range")
+    backend.Flush()
+    got = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.fused_dispatches() > 0
+    assert backend.dropped_stores() - dropped_before == int(dead)
+    # a dropped store is one the program overwrites unread: the bytes agree
+    assert got.tobytes() == want.tobytes()
 
 
 def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
@@ -679,7 +752,8 @@ def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
     backend.Flush()
     ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
     assert backend.fused_dispatches() - before == 1
-    assert ranged.tobytes() == apart.tobytes()
+    # nothing reads the dX site's frozen product again: its store is dropped
+    assert ranged.tobytes() == _restored(apart, ar, ["P1"], arena).tobytes()
 
 
 @pytest.mark.parametrize("between", ["gemm_elsewhere", "gemm_into_x", "add_into_x"])
@@ -716,14 +790,15 @@ def test_relaxed_gemms_reconvert_after_their_activation_changes(hip, orc, backen
     assert e <= TOL_BF16, f"C3: {e:.3g}"
 
 
-@pytest.mark.parametrize("n", [4096, 1003])
+@pytest.mark.parametrize("n,read_later", [(4096, False), (4096, True), (1003, False)])
 @pytest.mark.parametrize("order", ["as_planned", "swapped"])
-def test_swiglu_chains_fuse_bitwise(hip, orc, backend, n, order):
+def test_swiglu_chains_fuse_bitwise(hip, orc, backend, n, order, read_later):
     """SwiGLU's chains as the plan writer lowers them -- y = SiLU(g), h = y * u;
     dsg = dh * u, dup = dh * y, dg = SiluBwd(dsg, g) -- run as one pass each in
     a range: bitwise the instructions one by one (and the oracle's within
     libm), two fused dispatches.  With the two products in the other order,
-    SiluBwd reads the second one: still one pass."""
+    SiluBwd reads the second one: still one pass.  dsg is stored only where
+    the program reads it again (read_later); otherwise it keeps its bytes."""
     from tests.plan_ops import ins
     r = rng(n)
     ar = Arena()
@@ -733,16 +808,20 @@ def test_swiglu_chains_fuse_bitwise(hip, orc, backend, n, order):
     if order == "swapped":
         mults = mults[::-1]
     prog = [ins(24, [g, y], [n]), ins(21, [y, u, h], [n])] + mults + [ins(25, [dsg, g, dg], [n])]
+    if read_later:
+        prog += _readers(ar, ["dsg"])
     cpu, apart = execute(hip, orc, backend, ar, prog)
-    before = backend.fused_dispatches()
+    before, dropped_before = backend.fused_dispatches(), backend.dropped_stores()
     arena, ro = ar.images()
     backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
     backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
     backend.Flush()
     fused = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
     assert backend.fused_dispatches() - before == 2
-    assert fused.tobytes() == apart.tobytes()
-    for name in ["y", "h", "dsg", "dup", "dg"]:
+    dead = [] if read_later else ["dsg"]
+    assert backend.dropped_stores() - dropped_before == len(dead)
+    assert fused.tobytes() == _restored(apart, ar, dead, arena).tobytes()
+    for name in ["y", "h", "dup", "dg"] + (["dsg", "dsg_read"] if read_later else []):
         e = maxrel(ar.get(fused, name), ar.get(cpu, name))
         assert e <= TOL, f"{name}: {e:.3g}"
 
