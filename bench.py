@@ -54,52 +54,10 @@ def parse():
                         "(the counter calibration: a copy's known bytes)")
     p.add_argument("--attn-probe", action="store_true",
                    help="for rocprofv3 runs: BASELINE configs[2] attention fwd+bwd, bf16 x3, f32 x1")
-    p.add_argument("--mfma-ceiling", action="store_true",
-                   help="the int8 MFMA issue rate with register-resident operands (constant, "
-                        "random, small random levels) at 1, 2 and 4 waves per SIMD")
     p.add_argument("--lora-probe", nargs="?", const="c4", choices=["c4", "c5"],
                    help="for rocprofv3 runs: BASELINE configs[3] (c4) or configs[4] (c5) decoder "
                         "LoRA plan, one staged step then resident steps (relaxed family)")
     return p.parse_args()
-
-
-def mfma_ceiling():
-    """The int8 and bf16 MFMA rates with nothing but MFMAs issuing, operands
-    held in registers (see-ai_amd/probe/mfma_ceiling.hip): how far
-    data-dependent power management keeps gfx950 from its 5.0 POP/s and
-    2.5 PFLOP/s datasheet peaks."""
-    import ctypes
-    import torch
-    lib = ctypes.CDLL(os.path.join(ROOT, "see-ai_amd", "libseeai_probe.so"))
-    lib.seeai_probe_mfma_i8.restype = ctypes.c_float
-    lib.seeai_probe_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    out = torch.empty(1024 * 256, dtype=torch.int32, device="cuda")
-    iters = 10000
-    res = {}
-    for mode, name in [(0, "constant"), (1, "uniform_random"), (2, "random_abs_le_31")]:
-        for wgs in (256, 512, 1024):
-            ms = lib.seeai_probe_mfma_i8(wgs, iters, mode, out.data_ptr())
-            ops = 2.0 * 32 * 32 * 32 * 8 * iters * wgs * 4
-            res[f"{name}_{wgs // 256}wave_per_simd"] = round(ops / ms / 1e9, 1)
-    lib.seeai_probe_mfma_bf16.restype = ctypes.c_float
-    lib.seeai_probe_mfma_bf16.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    outf = torch.empty(1024 * 256, dtype=torch.float32, device="cuda")
-    lib.seeai_probe_mfma_bf16_shape.restype = ctypes.c_float
-    lib.seeai_probe_mfma_bf16_shape.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                                ctypes.c_int, ctypes.c_void_p]
-    resb = {}
-    for shape, flop1 in [(32, 2.0 * 32 * 32 * 16), (16, 2.0 * 16 * 16 * 32), (33, 2.0 * 32 * 32 * 16)]:
-        for mode, name in [(0, "constant"), (1, "random_unit")]:
-            for wgs in (256, 512, 1024):
-                ms = lib.seeai_probe_mfma_bf16_shape(shape, wgs, iters, mode, outf.data_ptr())
-                flop = flop1 * 8 * iters * wgs * 4
-                label = {32: "bf16_32x32x16", 16: "bf16_16x16x32", 33: "f16_32x32x16"}[shape]
-                key = f"{label}_{name}_{wgs // 256}wave_per_simd"
-                resb[key] = round(flop / ms / 1e9, 1)
-    print(json.dumps({"mfma_i8_ceiling_TOPS": res, "peak_TOPS": PEAK_INT8_TOPS,
-                      "mfma_bf16_ceiling_TFLOPS": resb, "peak_bf16_TFLOPS": PEAK_BF16_TFLOPS}),
-          flush=True)
-    return 0
 
 
 def lora_probe(which: str):
@@ -219,8 +177,6 @@ def main():
         return attn_probe()
     if args.lora_probe:
         return lora_probe(args.lora_probe)
-    if args.mfma_ceiling:
-        return mfma_ceiling()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the path shards by GEMM column blocks / attention (b, h) -- see DESIGN.md)",

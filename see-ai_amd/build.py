@@ -29,7 +29,6 @@ HOST = os.path.join(HERE, "host")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libseeai_hip.so")
-PROBE_LIB = os.path.join(HERE, "libseeai_probe.so")
 PLANGEN_LIB = os.path.join(HERE, "libseeai_plangen.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -88,14 +87,6 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-6000:]}")
     os.replace(tmp, LIB)
-    # The measurement probe (bench.py --mfma-ceiling): its own library.
-    probe_src = os.path.join(HERE, "probe", "mfma_ceiling.hip")
-    probe_tmp = PROBE_LIB + ".tmp"
-    r = subprocess.run([HIPCC, *COMMON, "-shared", "-o", probe_tmp, probe_src],
-                       capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed on mfma_ceiling.hip:\n{r.stderr[-6000:]}")
-    os.replace(probe_tmp, PROBE_LIB)
     # The plan writer's bulk generator (host code only).
     gen_src = os.path.join(HERE, "plangen", "plangen.cc")
     gen_tmp = PLANGEN_LIB + ".tmp"
@@ -111,7 +102,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
 
 def clean() -> None:
     shutil.rmtree(BUILD, ignore_errors=True)
-    for lib in (LIB, PROBE_LIB, PLANGEN_LIB):
+    for lib in (LIB, PLANGEN_LIB):
         if os.path.exists(lib):
             os.remove(lib)
 

@@ -55,33 +55,51 @@ class TuneError(Exception):
     """A failure that ends the run with exit 1 and the message."""
 
 
-def geometric_mean(values):
-    values = list(values)
-    return math.exp(sum(math.log(v) for v in values) / len(values)) if values else 0.0
+def _median_table(rounds):
+    """One arm's rounds [{fixture: rate}, ...] -> {fixture: median rate}; every
+    round must measure the same fixtures."""
+    names = sorted(rounds[0])
+    for r in rounds:
+        if sorted(r) != names:
+            raise TuneError("the rounds of one arm measured different fixtures")
+    return {name: statistics.median([r[name] for r in rounds]) for name in names}
 
 
 def score_arms(per_arm_runs, default_arm):
-    """per_arm_runs: {arm: [{fixture: rate}, ...] over rounds} ->
-    {arm: {"rate": {fixture: median}, "speedup": {fixture: ratio}, "score": gmean}}."""
-    medians = {arm: {k: statistics.median(r[k] for r in runs) for k in runs[0]}
-               for arm, runs in per_arm_runs.items()}
-    base = medians[default_arm]
-    out = {}
-    for arm, med in medians.items():
-        ratios = {k: v / base[k] for k, v in med.items()}
-        out[arm] = {"rate": med, "speedup": ratios, "score": geometric_mean(ratios.values())}
-    return out
+    """Score each arm against the default arm.
+
+    per_arm_runs maps an arm to its rounds, each a {fixture: rate} dict.
+    Every arm's figure per fixture is its median over rounds; its speedup per
+    fixture is that median over the default arm's; its score is the mean of
+    the log speedups, exponentiated (the geometric mean), so a large fixture
+    counts no more than a small one.  Returns {arm: {"rate", "speedup",
+    "score"}}."""
+    table = {arm: _median_table(rounds) for arm, rounds in per_arm_runs.items()}
+    reference = table[default_arm]
+    if any(v <= 0 for v in reference.values()):
+        raise TuneError("the default arm measured a non-positive rate")
+    scored = {}
+    for arm, rates in table.items():
+        speedup = {name: rates[name] / reference[name] for name in reference}
+        logs = [math.log(x) for x in speedup.values()]
+        score = math.exp(math.fsum(logs) / len(logs)) if logs else 0.0
+        scored[arm] = {"rate": rates, "speedup": speedup, "score": score}
+    return scored
 
 
 def choose(scored, default_arm, min_gain):
-    best = max(scored, key=lambda a: (scored[a]["score"], a == default_arm))
-    gain = scored[best]["score"] - 1.0
-    if best == default_arm:
+    """(arm to record, why).  The default stays unless another arm's score
+    beats it by at least min_gain; a tie goes to the default."""
+    base = scored[default_arm]["score"]
+    challengers = [a for a in scored if a != default_arm and scored[a]["score"] > base]
+    if not challengers:
         return default_arm, "default-is-best"
-    if gain < min_gain:
-        return default_arm, (f"default-within-margin: best arm {best} gains {gain:.1%}, "
-                             f"below --min-gain {min_gain:.1%}")
-    return best, f"tuned: {best} gains {gain:.1%} over the default"
+    top = sorted(challengers, key=lambda a: scored[a]["score"], reverse=True)[0]
+    gain = scored[top]["score"] / base - 1.0
+    if gain >= min_gain:
+        return top, f"tuned: {top} gains {gain:.1%} over the default"
+    return default_arm, (f"default-within-margin: best arm {top} gains {gain:.1%}, "
+                         f"below --min-gain {min_gain:.1%}")
 
 
 # --- fixtures ----------------------------------------------------------------
