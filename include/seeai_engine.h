@@ -24,8 +24,12 @@ typedef struct seeai_engine seeai_engine;
  * 8-byte field at `hash_offset` (216 for the PlanHeader) read as zero. */
 uint64_t seeai_plan_self_hash(const void* blob, uint64_t bytes, uint64_t hash_offset);
 /* DecodePlan's header contract (plan_loader.cc:19-49, plan_contract.h:
- * 35-180) without a device: 0 if the plan is readable, else SEEAI_INVALID
- * and the refusal in `msg` (NUL-terminated, truncated to msg_bytes). */
+ * 35-180) and the executor contract (VerifyExecutorContract,
+ * runtime/loader/contract.cc:51-244: every operand of every program in
+ * bounds, unaliased where written, the flag bits each opcode takes, the
+ * feeder-bounded label / token operands, emit entries in the arena) without
+ * a device: 0 if the plan is loadable, else SEEAI_INVALID and the refusal in
+ * `msg` (NUL-terminated, truncated to msg_bytes). */
 int seeai_plan_check(const void* blob, uint64_t bytes, char* msg, uint64_t msg_bytes);
 
 /* Load a plan onto `device` (DecodePlan + AllocateArena + Bind).  On
@@ -47,6 +51,11 @@ int seeai_engine_train_resident(seeai_engine* engine, float* loss);
 int seeai_engine_evaluate(seeai_engine* engine, const float* input, const void* labels,
                           float* loss);
 int seeai_engine_merge(seeai_engine* engine);
+/* UpdateEngine::BindSourceModel (update_engine.cc:82): the source model
+ * file's image, read by source refs (bit 62).  Refused when smaller than the
+ * extent the plan's programs read; until one is bound, a plan that reads it
+ * refuses to run. */
+int seeai_engine_bind_source(seeai_engine* engine, const void* data, uint64_t bytes);
 /* Arena bytes through the host mirror. */
 int seeai_engine_read(seeai_engine* engine, uint64_t offset, void* dst, uint64_t bytes);
 int seeai_engine_write(seeai_engine* engine, uint64_t offset, const void* src, uint64_t bytes);

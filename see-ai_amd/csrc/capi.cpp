@@ -23,6 +23,7 @@
 
 #include "../../include/seeai_hip.h"
 #include "common.h"
+#include "operands.h"
 
 using namespace seeai;
 
@@ -101,7 +102,12 @@ struct seeai_ctx {
   int allow_lowrank = 1;  // LoRA sites folded into the frozen product's epilogue
   int allow_dead_store_drop = 1;  // fused passes skip stores the range overwrites unread
   uint64_t dropped_stores = 0;
-  const uint8_t* dead_prog = nullptr;  // the program `dead` was decided for
+  // The program `dead` was decided for: its address, length and a hash of
+  // its words (a caller may present another program of the same length at
+  // the same address, e.g. a temporary buffer freed and reallocated).
+  const uint8_t* dead_prog = nullptr;
+  uint64_t dead_hash = 0;
+  uint64_t prog_hash = 0;  // of the range's program, taken at begin_range
   std::vector<int8_t> dead;  // per instruction: -1 undecided, 0 kept, 1 dropped
   TilePolicy policy;  // kernel geometry (seeai_configure)
   // The relaxed GEMMs' bf16 copy of their activations, and what it holds:
@@ -893,155 +899,18 @@ struct Touch {
   bool write;
 };
 
-// Every operand extent of an instruction, with the validator's roles and
-// sizes (plan_validator.cc:368-745).  False for opcodes not modelled here.
+// Every operand extent of an instruction (the validator's roles and sizes,
+// plan_validator.cc:368-745, as operands.h states them), resolved to device
+// addresses.  False for opcodes not modelled there.
 bool TouchExtents(seeai_ctx* c, const Instruction& ins, Touch* out, int* n) {
   const Ptrs R{c};
+  OperandRef ops[kMaxOperands];
+  const int count = DescribeOperands(ins, ops);
+  if (count < 0) return false;
   int k = 0;
-  const auto add = [&](uint64_t ref, uint64_t floats, bool w) {
-    if (ref != kNullRef && floats) out[k++] = {R.at(ref), floats * 4, w};
-  };
-  const uint64_t d0 = ins.out[0], d1 = ins.out[1];
-  const uint64_t hi0 = d0 >> 32, lo0 = d0 & 0xFFFFFFFFu;
-  GemmArgs g{};
-  if (DecodeGemm(c, ins, &g)) {
-    Extent r[8];
-    const int nr = GemmReads(g, r);
-    for (int i = 0; i < nr; ++i) out[k++] = {r[i].p, r[i].n, false};
-    const Extent w = GemmWrites(g);
-    out[k++] = {w.p, w.n, true};
-    *n = k;
-    return true;
-  }
-  // Attention geometry: (B, S, H, d) from two words or one packed word.
-  const auto split = [](uint64_t bs, uint64_t hd, uint64_t* B, uint64_t* S, uint64_t* H,
-                        uint64_t* d) {
-    *B = bs >> 32, *S = bs & 0xFFFFFFFFu, *H = hd >> 32, *d = hd & 0xFFFFFFFFu;
-  };
-  const auto packed = [](uint64_t w, uint64_t* B, uint64_t* S, uint64_t* H, uint64_t* d) {
-    *B = w >> 48, *S = (w >> 32) & 0xFFFF, *H = (w >> 16) & 0xFFFF, *d = w & 0xFFFF;
-  };
-  uint64_t B, S, H, d;
-  switch (ins.opcode) {
-    case 0:
-      break;
-    case 5: case 21: case 8: case 23: case 25:  // AddEW, MulEW, activation backward
-      add(ins.in[0], d0, false), add(ins.in[1], d0, false), add(ins.in[2], d0, true);
-      break;
-    case 6:  // AddBias
-      add(ins.in[0], d0 * d1, false), add(ins.in[1], d1, false), add(ins.in[2], d0 * d1, true);
-      break;
-    case 7: case 22: case 24: case 9: case 20:  // activation forward, Scale, Copy
-      add(ins.in[0], d0, false), add(ins.in[1], d0, true);
-      break;
-    case 42:  // Accumulate: dst read and written, src
-      add(ins.in[0], d0, true), add(ins.in[1], d0, false);
-      break;
-    case 19:  // Fill
-      add(ins.in[0], d0, true);
-      break;
-    case 10:  // ReduceRows
-      add(ins.in[0], d0 * d1, false), add(ins.in[1], d1, true);
-      break;
-    case 11: case 51:  // SoftmaxXEnt forward: logits, labels, loss, probabilities
-      add(ins.in[0], d0 * d1, false), add(ins.in[1], d0, false), add(ins.in[2], 1, true),
-          add(ins.in[3], d0 * d1, true);
-      break;
-    case 12: case 52:  // SoftmaxXEnt backward
-      add(ins.in[0], d0 * d1, false), add(ins.in[1], d0, false), add(ins.in[2], 1, false),
-          add(ins.in[3], d0 * d1, true);
-      break;
-    case 17:  // SgdStep
-      add(ins.in[0], d0, true), add(ins.in[1], d0, false);
-      break;
-    case 18:  // AdamWStep
-      add(ins.in[0], d0, true), add(ins.in[1], d0, false), add(ins.in[2], d0, true),
-          add(ins.in[3], d0, true);
-      break;
-    case 28:  // ClipNorm
-      add(ins.in[0], d0, true);
-      break;
-    case 53:  // SqNormAccum
-      add(ins.in[0], d0, false), add(ins.in[1], 1, true);
-      break;
-    case 54:  // ClipGlobal
-      add(ins.in[0], d0, true), add(ins.in[1], 1, false);
-      break;
-    case 26:  // LayerNormFwd: x, gamma, beta -> y, mean, rstd
-      add(ins.in[0], hi0 * lo0, false), add(ins.in[1], lo0, false), add(ins.in[2], lo0, false),
-          add(ins.in[3], hi0 * lo0, true), add(ins.out[1], hi0, true), add(ins.out[2], hi0, true);
-      break;
-    case 27: {  // LayerNormBwd: dy, x, gamma, mean, rstd -> dx
-      const uint64_t rows = ins.out[2] >> 32, cols = ins.out[2] & 0xFFFFFFFFu;
-      add(ins.in[0], rows * cols, false), add(ins.in[1], rows * cols, false),
-          add(ins.in[2], cols, false), add(ins.in[3], rows * cols, true),
-          add(ins.out[0], rows, false), add(ins.out[1], rows, false);
-      break;
-    }
-    case 31:  // RmsNormFwd: x, g -> y, rstd
-      add(ins.in[0], hi0 * lo0, false), add(ins.in[1], lo0, false),
-          add(ins.in[2], hi0 * lo0, true), add(ins.in[3], hi0, true);
-      break;
-    case 32: {  // RmsNormBwd: dy, x, g, rstd -> dx
-      const uint64_t rows = d1 >> 32, cols = d1 & 0xFFFFFFFFu;
-      add(ins.in[0], rows * cols, false), add(ins.in[1], rows * cols, false),
-          add(ins.in[2], cols, false), add(ins.in[3], rows * cols, true),
-          add(ins.out[0], rows, false);
-      break;
-    }
-    case 33: case 34:  // RoPE: x -> y, optional [S, d] table
-      split(d0, d1, &B, &S, &H, &d);
-      add(ins.in[0], B * S * H * d, false), add(ins.in[1], B * S * H * d, true),
-          add(ins.in[2], S * d, false);
-      break;
-    case 45:  // RopeTable
-      add(ins.in[0], hi0 * lo0, true);
-      break;
-    case 46:  // FusedMap
-      add(ins.in[0], d0, false), add(ins.in[1], d0, false), add(ins.in[2], d0, false),
-          add(ins.in[3], d0, true);
-      break;
-    case 41:  // EmbedFwd: tokens, [V, D] table -> rows
-      add(ins.in[0], d0, false), add(ins.in[1], (d1 >> 32) * (d1 & 0xFFFFFFFFu), false),
-          add(ins.in[2], d0 * (d1 & 0xFFFFFFFFu), true);
-      break;
-    case 55:  // SegmentStarts
-      add(ins.in[0], hi0 * lo0, false), add(ins.in[1], hi0 * lo0, true);
-      break;
-    case 35: case 56:  // AttnFwd (+Seg): q, k, v -> o, probabilities
-      if (ins.opcode == 35) split(d1, ins.out[2], &B, &S, &H, &d);
-      else packed(d1, &B, &S, &H, &d), add(ins.out[2], B * S, false);
-      for (int i = 0; i < 3; ++i) add(ins.in[i], B * S * H * d, false);
-      add(ins.in[3], B * S * H * d, true), add(ins.out[0], B * H * S * S, true);
-      break;
-    case 36:  // AttnDP
-      split(d0, d1, &B, &S, &H, &d);
-      add(ins.in[0], B * S * H * d, false), add(ins.in[1], B * S * H * d, false),
-          add(ins.in[2], B * H * S * S, true);
-      break;
-    case 37: case 39: case 40:  // AttnDV, AttnDQ, AttnDK
-      split(d0, d1, &B, &S, &H, &d);
-      add(ins.in[0], B * H * S * S, false), add(ins.in[1], B * S * H * d, false),
-          add(ins.in[2], B * S * H * d, true);
-      break;
-    case 38:  // SoftmaxRowsBwd
-      add(ins.in[0], hi0 * lo0, false), add(ins.in[1], hi0 * lo0, false),
-          add(ins.in[2], hi0 * lo0, true);
-      break;
-    case 47: case 57:  // AttnFwdTiled (+Seg): q, k, v -> o, [B*H*S, 4] stats
-      if (ins.opcode == 47) split(d1, ins.out[2], &B, &S, &H, &d);
-      else packed(d1, &B, &S, &H, &d), add(ins.out[2], B * S, false);
-      for (int i = 0; i < 3; ++i) add(ins.in[i], B * S * H * d, false);
-      add(ins.in[3], B * S * H * d, true), add(ins.out[0], B * S * H * 4, true);
-      break;
-    case 48: case 49: case 50:  // tiled dQ / dK / dV: dQ also writes the stats
-      packed(ins.out[2], &B, &S, &H, &d);
-      for (int i = 0; i < 4; ++i) add(ins.in[i], B * S * H * d, false);
-      add(ins.out[0], B * S * H * 4, ins.opcode == 48), add(ins.out[1], B * S * H * d, true);
-      break;
-    default:
-      return false;
-  }
+  for (int i = 0; i < count; ++i)
+    if (ops[i].ref != kNullRef && ops[i].elems)
+      out[k++] = {R.at(ops[i].ref), ops[i].elems * ops[i].elem_bytes, ops[i].write};
   *n = k;
   return true;
 }
@@ -1086,8 +955,9 @@ bool DeadFrom(seeai_ctx* c, uint64_t from, const Extent& E) {
 // the program's words and the binding alone (dropped at bind).
 bool DeadStore(seeai_ctx* c, uint64_t at_idx, uint64_t from, const Extent& E) {
   if (!c->allow_dead_store_drop) return false;
-  if (c->dead_prog != c->prog || c->dead.size() != c->prog_count) {
+  if (c->dead_prog != c->prog || c->dead.size() != c->prog_count || c->dead_hash != c->prog_hash) {
     c->dead_prog = c->prog;
+    c->dead_hash = c->prog_hash;
     c->dead.assign(c->prog_count, -1);
   }
   int8_t& v = c->dead[at_idx];
@@ -1252,6 +1122,22 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
   return -1;
 }
 
+// A 64-bit hash of a program's words (FNV-1a over 8-byte words, then a
+// final avalanche): what the per-program dead-store decisions are keyed on
+// besides the program's address and length.
+uint64_t ProgramHash(const uint8_t* prog, uint64_t count) {
+  uint64_t h = 0xcbf29ce484222325ULL;
+  for (uint64_t i = 0; i < count * 8; ++i) {
+    uint64_t w;
+    std::memcpy(&w, prog + i * 8, 8);
+    h = (h ^ w) * 0x100000001b3ULL;
+  }
+  h ^= h >> 33;
+  h *= 0xff51afd7ed558ccdULL;
+  h ^= h >> 33;
+  return h;
+}
+
 }  // namespace
 
 int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params* params) {
@@ -1282,6 +1168,7 @@ int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params
 int seeai_begin_range(seeai_ctx* c, const void* program, uint64_t count, uint64_t begin,
                       uint64_t end) {
   if (!c || (!program && count) || begin > end || end > count) return SEEAI_INVALID;
+  c->prog_hash = ProgramHash(static_cast<const uint8_t*>(program), count);
   c->prog = static_cast<const uint8_t*>(program);
   c->prog_count = count;
   c->range_end = end;

@@ -123,6 +123,7 @@ ENGINE_EXPORTS = {
     "seeai_engine_train_resident": (_I, [_P, C.POINTER(_F)]),
     "seeai_engine_evaluate": (_I, [_P, _P, _P, C.POINTER(_F)]),
     "seeai_engine_merge": (_I, [_P]),
+    "seeai_engine_bind_source": (_I, [_P, _P, _U64]),
     "seeai_engine_read": (_I, [_P, _U64, _P, _U64]),
     "seeai_engine_write": (_I, [_P, _U64, _P, _U64]),
     "seeai_engine_step": (_U64, [_P]),
@@ -414,6 +415,12 @@ class Engine:
 
     def merge(self):
         self._check(_lib.seeai_engine_merge(self.h))
+
+    def bind_source(self, data: bytes | None):
+        """UpdateEngine::BindSourceModel: the source model's image."""
+        n = 0 if data is None else len(data)
+        buf = None if not n else C.create_string_buffer(bytes(data), n)
+        self._check(_lib.seeai_engine_bind_source(self.h, buf, _U64(n)))
 
     def read(self, offset: int, nbytes: int) -> bytes:
         buf = C.create_string_buffer(max(nbytes, 1))

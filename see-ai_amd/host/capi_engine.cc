@@ -51,12 +51,17 @@ uint64_t seeai_plan_self_hash(const void* blob, uint64_t bytes, uint64_t hash_of
 int seeai_plan_check(const void* blob, uint64_t bytes, char* msg, uint64_t msg_bytes) {
   if (!blob && bytes) return SEEAI_INVALID;
   auto plan = seeai::host::ReadPlan({static_cast<const uint8_t*>(blob), bytes});
-  if (plan) {
-    CopyMessage("", msg, msg_bytes);
-    return SEEAI_OK;
+  if (!plan) {
+    CopyMessage(plan.error(), msg, msg_bytes);
+    return SEEAI_INVALID;
   }
-  CopyMessage(plan.error(), msg, msg_bytes);
-  return SEEAI_INVALID;
+  uint64_t source = 0;
+  if (auto ok = seeai::host::VerifyPrograms(*plan, &source); !ok) {
+    CopyMessage(ok.error(), msg, msg_bytes);
+    return SEEAI_INVALID;
+  }
+  CopyMessage("", msg, msg_bytes);
+  return SEEAI_OK;
 }
 
 int seeai_engine_create(int device, const void* blob, uint64_t bytes, seeai_engine** out,
@@ -108,6 +113,11 @@ int seeai_engine_evaluate(seeai_engine* e, const float* input, const void* label
 int seeai_engine_merge(seeai_engine* e) {
   if (!e) return SEEAI_INVALID;
   return Report(e, e->engine->Merge());
+}
+
+int seeai_engine_bind_source(seeai_engine* e, const void* data, uint64_t bytes) {
+  if (!e || (!data && bytes)) return SEEAI_INVALID;
+  return Report(e, e->engine->BindSource(static_cast<const uint8_t*>(data), bytes));
 }
 
 int seeai_engine_read(seeai_engine* e, uint64_t offset, void* dst, uint64_t bytes) {

@@ -26,6 +26,7 @@ Result<std::unique_ptr<PlanEngine>> PlanEngine::Load(std::span<const uint8_t> bl
   if (!plan) return Fail(plan.error());
   e->plan_ = std::move(*plan);
   const PlanHeader& h = e->plan_.header;
+  if (auto ok = VerifyPrograms(e->plan_, &e->source_required_); !ok) return Fail(ok.error());
 
   // plan_loader.cc:151-166: the narrowest softmax width anywhere bounds the
   // class labels the feeder may stage.
@@ -128,6 +129,8 @@ Result<void> PlanEngine::Stage(const float* input, const void* labels) {
 Result<void> PlanEngine::ExecuteRange(const std::vector<Instruction>& program, size_t begin,
                                       size_t end) {
   const PlanHeader& h = plan_.header;
+  if (source_required_ > source_bytes_)
+    return Fail("this plan reads the source model: bind it with BindSource before running");
   const StepParams params{EffectiveLr(), h.beta1, h.beta2, h.eps, h.weight_decay, step_};
   backend_->BeginRange(std::span<const Instruction>(program), begin, end);
   for (size_t idx = begin; idx < end; ++idx)
@@ -141,6 +144,17 @@ Result<void> PlanEngine::ExecuteRange(const std::vector<Instruction>& program, s
   if (!flushed)
     return Fail(std::string("backend '") + backend_->name() + "' failed to complete: " +
                 flushed.error());
+  return {};
+}
+
+Result<void> PlanEngine::BindSource(const uint8_t* data, uint64_t bytes) {
+  // update_engine.cc:82: the source model's image; every source operand
+  // the programs name must lie inside it.
+  if (bytes < source_required_)
+    return Fail("source model is " + std::to_string(bytes) + " bytes; the plan reads " +
+                std::to_string(source_required_));
+  if (auto r = backend_->BindSource(data, bytes); !r) return r;
+  source_bytes_ = bytes;
   return {};
 }
 

@@ -53,6 +53,11 @@ class PlanEngine {
   // mirror (update_engine.cc:1028-1063).
   Result<void> Merge();
 
+  // update_engine.cc:82 (BindSourceModel): the source model file's image,
+  // which source refs (bit 62) read; refused when smaller than what the
+  // programs read.
+  Result<void> BindSource(const uint8_t* data, uint64_t bytes);
+
   // Arena access through the host mirror (checkpoint / parity reads).
   Result<void> Read(uint64_t offset, void* dst, uint64_t bytes);
   Result<void> Write(uint64_t offset, const void* src, uint64_t bytes);
@@ -73,6 +78,8 @@ class PlanEngine {
   uint64_t num_classes_ = 0;
   bool masked_labels_ = false;  // the plan's loss ignores positions labelled -1
   uint64_t vocab_bound_ = 0;     // token plans: the narrowest embedding's rows
+  uint64_t source_required_ = 0;  // bytes of the source model the programs read
+  uint64_t source_bytes_ = 0;     // bytes of the bound source model
 };
 
 }  // namespace seeai::host

@@ -6,11 +6,10 @@
 // enforces before any section is decoded (runtime/loader/plan_loader.cc:
 // 19-49, source/contract/plan_contract.h:35-180).
 //
-// What is not restated here is the per-instruction operand proof
-// (runtime/verifier, VerifyExecutorContract): as in the reference, the
-// backend executes instructions blindly once a plan is accepted, so plans
-// reach this reader from the reference's compiler or this repository's plan
-// writer, both of which emit in-bounds operands.
+// VerifyPrograms (verify.cc) is the per-instruction operand proof the
+// reference's loader runs before anything executes (VerifyExecutorContract,
+// runtime/loader/contract.cc:51-244): after it, the backend dispatches the
+// programs blindly, as the reference's does.
 #pragma once
 
 #include <cstddef>
@@ -135,5 +134,15 @@ struct Plan {
 // slot bounds, the hyperparameter ranges and the step-program rule; the
 // refusal strings are the reference's.  Sections are then decoded.
 Result<Plan> ReadPlan(std::span<const uint8_t> blob);
+
+// The executor contract (contract.cc:51-244 over plan_validator.cc:160-745):
+// every operand of every program non-null, aligned, in bounds of the space
+// its ref names, never a write into rodata or the source model, no written
+// operand overlapping another of the same instruction; only the flag bits
+// each opcode takes; the label, token and segment-start operands the
+// feeder's bounds cover; finite positive scales and clip thresholds; emit
+// entries inside the arena.  *source_extent receives the bytes of the
+// source model the programs read (0: none), checked when one is bound.
+Result<void> VerifyPrograms(const Plan& plan, uint64_t* source_extent);
 
 }  // namespace seeai::host

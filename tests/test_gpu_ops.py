@@ -738,6 +738,45 @@ def test_lora_site_store_drop_follows_the_first_touch(hip, orc, backend, after):
     assert got.tobytes() == want.tobytes()
 
 
+def test_store_drop_is_decided_per_program_not_per_address(hip, orc, backend):
+    """Two programs of the same length presented one after the other from
+    the same buffer, with no bind between: the first overwrites the site's C
+    unread (its store is dropped), the second reads C (its store must be
+    kept).  The decisions follow the program's words, not its address."""
+    import ctypes as C
+    from tests.plan_ops import ins
+    M, Din, Dout, rank = 256, 1024, 1024, 16
+    ar = Arena()
+    site = _lora_site_program(ar, rng(11), "q8", M, Din, Dout, rank)[:3]
+    c0 = ar.meta["C0"][1]
+    z = ar.add("z", rng(12).standard_normal((M, Dout)).astype(np.float32))
+    c0_read = ar.empty("C0_read", (M, Dout))
+    first = site + [ins(20, [z, c0], [M * Dout])]         # C overwritten unread
+    second = site + [ins(20, [c0, c0_read], [M * Dout])]  # C read
+    _, want = execute(hip, orc, backend, ar, second)
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    sp = hip.StepParams(*PARAMS[:5], 0, PARAMS[5])
+    ctx = backend.ctx
+    buf = C.create_string_buffer(64 * len(first))
+    drops = []
+    for prog in (first, second):
+        if prog is second:  # the second program starts from the same arena
+            backend.Upload(0, arena.tobytes())
+        C.memmove(buf, b"".join(prog), 64 * len(prog))
+        before = backend.dropped_stores()
+        ctx.call("seeai_begin_range", buf, len(prog), 0, len(prog))
+        for i in range(len(prog)):
+            ctx.call("seeai_execute", C.cast(C.addressof(buf) + 64 * i, C.c_void_p), C.byref(sp))
+        ctx.call("seeai_end_range")
+        backend.Flush()
+        drops.append(backend.dropped_stores() - before)
+    got = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert drops == [1, 0]
+    assert bits_equal(ar.get(got, "C0_read"), ar.get(want, "C0_read"))
+    assert got.tobytes() == want.tobytes()
+
+
 def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
     """t written over the frozen product's C: legal one by one (C is then
     read back with t's bytes in it), wrong once the frozen product moves after
