@@ -50,6 +50,12 @@ int seeai_engine_train_step(seeai_engine* engine, const float* inputs, const voi
 int seeai_engine_train_resident(seeai_engine* engine, float* loss);
 int seeai_engine_evaluate(seeai_engine* engine, const float* input, const void* labels,
                           float* loss);
+/* The eval program with its accuracy tally (update_engine.cc:437-565): the
+ * loss, the rows whose argmax (first maximum wins) is their label, and the
+ * rows judged (label not -1).  *judged is 0 where the plan tracks no
+ * accuracy (no class labels, or no eval softmax covering the batch). */
+int seeai_engine_evaluate_metrics(seeai_engine* engine, const float* input, const void* labels,
+                                  float* loss, uint64_t* hits, uint64_t* judged);
 int seeai_engine_merge(seeai_engine* engine);
 /* UpdateEngine::BindSourceModel (update_engine.cc:82): the source model
  * file's image, read by source refs (bit 62).  Refused when smaller than the

@@ -226,6 +226,12 @@ int seeai_adamw_step(seeai_ctx* ctx, float* d_p, const float* d_g,
 /* The eval argmax, first maximum wins (update_engine.cc:537-565). */
 int seeai_argmax_rows(seeai_ctx* ctx, const float* d_probs, uint64_t rows,
                       uint64_t cols, int32_t* d_out);
+/* The eval accuracy tally (update_engine.cc:537-565): over the rows whose
+ * label is not -1, *hits counts those whose label is the row's argmax (first
+ * maximum wins) and *judged those counted.  Device probabilities and i32
+ * labels in, host counts out; waits for the stream. */
+int seeai_argmax_tally(seeai_ctx* ctx, const float* d_probs, const int32_t* d_labels,
+                       uint64_t rows, uint64_t cols, uint64_t* hits, uint64_t* judged);
 
 #ifdef __cplusplus
 }

@@ -1002,18 +1002,33 @@ static float bits_f32(uint64_t w) {
   memcpy(&f, &u, 4);
   return f;
 }
-static void* ref_ptr(uint64_t ref, uint8_t* arena, const uint8_t* rodata) {
+/* cpu_backend.cc:221-240 (ReadPtr): bit 63 names rodata, bit 62 alone the
+ * source model file's image, neither the arena. */
+static void* ref_ptr(uint64_t ref, uint8_t* arena, const uint8_t* rodata,
+                     const uint8_t* source) {
   const uint64_t off = ref & ~(kRodataBit | kSourceBit);
   if (ref & kRodataBit) return (void*)(rodata + off);
+  if (ref & kSourceBit) return (void*)(source + off);
   return arena + off;
 }
 
 int orc_execute(const void* instruction, uint8_t* arena, const uint8_t* rodata,
                 const OrcStepParams* P) {
+  return orc_execute_src(instruction, arena, rodata, NULL, P);
+}
+
+int orc_execute_src(const void* instruction, uint8_t* arena, const uint8_t* rodata,
+                    const uint8_t* source, const OrcStepParams* P) {
   OrcIns ins;
   memcpy(&ins, instruction, sizeof ins);
-#define RP(r) ((float*)ref_ptr((r), arena, rodata))
-#define IP(r) ((int32_t*)ref_ptr((r), arena, rodata))
+  /* A source ref with no source image bound: refused before any read.  Only
+   * the in[] slots carry operand refs a source image may back. */
+  for (int i = 0; i < 4; ++i)
+    if (!source && ins.in[i] != kNullRef &&
+        (ins.in[i] & (kRodataBit | kSourceBit)) == kSourceBit)
+      return 3;
+#define RP(r) ((float*)ref_ptr((r), arena, rodata, source))
+#define IP(r) ((int32_t*)ref_ptr((r), arena, rodata, source))
   const int act = (ins.flags >> 1) & 3;
   const float alpha = ins.imm == 0 ? 1.0f : bits_f32(ins.imm);
   const float norm_eps = ins.imm == 0 ? 1e-5f : bits_f32(ins.imm);
@@ -1040,25 +1055,25 @@ int orc_execute(const void* instruction, uint8_t* arena, const uint8_t* rodata,
       break;
     case 29: {
       const int cs = (ins.flags & 16) != 0;
-      orc_gemm_nn_q8(RP(ins.in[0]), (const int8_t*)ref_ptr(ins.in[1], arena, rodata),
+      orc_gemm_nn_q8(RP(ins.in[0]), (const int8_t*)ref_ptr(ins.in[1], arena, rodata, source),
                      RP(ins.in[2]), ins.out[0], ins.out[1], ins.out[2],
                      cs ? 1.0f : bits_f32(ins.in[3]), act, cs ? RP(ins.in[3]) : NULL);
       break;
     }
     case 30: {
       const int cs = (ins.flags & 16) != 0;
-      orc_gemm_nt_q8(RP(ins.in[0]), (const int8_t*)ref_ptr(ins.in[1], arena, rodata),
+      orc_gemm_nt_q8(RP(ins.in[0]), (const int8_t*)ref_ptr(ins.in[1], arena, rodata, source),
                      RP(ins.in[2]), ins.out[0], ins.out[1], ins.out[2],
                      cs ? 1.0f : bits_f32(ins.in[3]), cs ? RP(ins.in[3]) : NULL);
       break;
     }
     case 43:
-      orc_gemm_nn_bf16(RP(ins.in[0]), (const uint16_t*)ref_ptr(ins.in[1], arena, rodata),
+      orc_gemm_nn_bf16(RP(ins.in[0]), (const uint16_t*)ref_ptr(ins.in[1], arena, rodata, source),
                        RP(ins.in[2]), ins.out[0], ins.out[1], ins.out[2],
                        (ins.flags & 1) ? RP(ins.in[3]) : NULL, act);
       break;
     case 44:
-      orc_gemm_nt_bf16(RP(ins.in[0]), (const uint16_t*)ref_ptr(ins.in[1], arena, rodata),
+      orc_gemm_nt_bf16(RP(ins.in[0]), (const uint16_t*)ref_ptr(ins.in[1], arena, rodata, source),
                        RP(ins.in[2]), ins.out[0], ins.out[1], ins.out[2]);
       break;
     case 5: orc_add_ew(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), ins.out[0]); break;

@@ -186,6 +186,11 @@ typedef struct OrcStepParams {
 } OrcStepParams;
 int orc_execute(const void* instruction, uint8_t* arena, const uint8_t* rodata,
                 const OrcStepParams* params);
+/* The same with the source model file's image bound (source refs, bit 62,
+ * read from it: cpu_backend.cc:221-240).  orc_execute binds none: an
+ * instruction naming a source ref there returns 3. */
+int orc_execute_src(const void* instruction, uint8_t* arena, const uint8_t* rodata,
+                    const uint8_t* source, const OrcStepParams* params);
 
 #ifdef __cplusplus
 }

@@ -95,6 +95,7 @@ ORACLE_ONLY = {
     "argmax_tally": (None, [_P, _P, _Z, _Z, _P, _P]),
     "adamw_bias_corrections": (None, [_F, _F, _U64, _P, _P]),
     "execute": (_I, [_P, _P, _P, _P]),
+    "execute_src": (_I, [_P, _P, _P, _P, _P]),
     "chunk_grain": (_Z, [_Z, _Z]),
     "chunk_count": (_Z, [_Z, _Z]),
 }
@@ -492,6 +493,17 @@ class Kernels:
         self._fn("argmax_rows")(_ptr(probs), probs.shape[0], probs.shape[1], _ptr(out))
         return out
 
+    def argmax_tally(self, probs, labels):
+        """(hits, judged rows) over rows whose label is not -1
+        (update_engine.cc:537-565)."""
+        probs = f32(probs)
+        labels = np.ascontiguousarray(labels, np.int32)
+        hits = np.zeros(1, np.uint64)
+        judged = np.zeros(1, np.uint64)
+        self._fn("argmax_tally")(_ptr(probs), _ptr(labels), probs.shape[0], probs.shape[1],
+                                 _ptr(hits), _ptr(judged))
+        return int(hits[0]), int(judged[0])
+
     def adamw_bias_corrections(self, b1, b2, step):
         a = np.zeros(1, np.float32)
         b = np.zeros(1, np.float32)
@@ -502,10 +514,15 @@ class Kernels:
         buf = np.frombuffer(bytes(blob), np.uint8)
         return int(self._fn("plan_self_hash")(_ptr(buf), buf.size, hash_offset))
 
-    def execute(self, ins_bytes: bytes, arena: np.ndarray, rodata: np.ndarray, params):
+    def execute(self, ins_bytes: bytes, arena: np.ndarray, rodata: np.ndarray, params,
+                source: np.ndarray | None = None):
+        """One instruction (cpu_backend.cc:260-646); `source` is the source
+        model file's image that bit-62 refs read (none bound: status 3)."""
         buf = C.create_string_buffer(bytes(ins_bytes), 64)
         sp = OrcStepParams(*params[:5], 0, params[5])
-        return self._fn("execute")(buf, _ptr(arena), _ptr(rodata), C.byref(sp))
+        if source is None:
+            return self._fn("execute")(buf, _ptr(arena), _ptr(rodata), C.byref(sp))
+        return self._fn("execute_src")(buf, _ptr(arena), _ptr(rodata), _ptr(source), C.byref(sp))
 
 
 _cache: dict = {}

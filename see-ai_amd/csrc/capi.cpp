@@ -67,7 +67,7 @@ float BitsToF32(uint64_t w) {
   return f;
 }
 
-constexpr size_t kSmallBytes = 4096;              // refusal word + scale slot
+constexpr size_t kSmallBytes = 4096;  // refusal word, scale slot, accuracy counts
 constexpr size_t kInitialScratch = 1u << 20;      // grown on demand
 
 }  // namespace
@@ -82,7 +82,7 @@ struct seeai_ctx {
   uint64_t rodata_bytes = 0;
   uint8_t* source = nullptr;
   uint64_t source_bytes = 0;
-  uint8_t* small = nullptr;  // [0] refusal word, [64] scale slot
+  uint8_t* small = nullptr;  // [0] refusal word, [64] scale slot, [128] two u64 counts
   int* host_flag = nullptr;  // pinned
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
@@ -131,6 +131,7 @@ struct seeai_ctx {
 
   int* flag() { return reinterpret_cast<int*>(small); }
   float* scale_slot() { return reinterpret_cast<float*>(small + 64); }
+  uint64_t* counts() { return reinterpret_cast<uint64_t*>(small + 128); }
 };
 
 namespace {
@@ -1439,6 +1440,20 @@ int seeai_adamw_step(seeai_ctx* c, float* p, const float* g, float* m, float* v,
 int seeai_argmax_rows(seeai_ctx* c, const float* probs, uint64_t rows, uint64_t cols, int32_t* out) {
   if (!c) return SEEAI_INVALID;
   SEEAI_TRY(c, LaunchArgmaxRows(probs, rows, cols, out, c->stream), "argmax");
+  return SEEAI_OK;
+}
+int seeai_argmax_tally(seeai_ctx* c, const float* probs, const int32_t* labels, uint64_t rows,
+                       uint64_t cols, uint64_t* hits, uint64_t* judged) {
+  if (!c || !hits || !judged || (rows && (!probs || !labels)))
+    return Fail(c, SEEAI_INVALID, "argmax_tally: null operand");
+  if (rows > 0x7FFFFFFFull) return Fail(c, SEEAI_INVALID, "argmax_tally: too many rows");
+  SEEAI_TRY(c, LaunchArgmaxTally(probs, labels, rows, cols, c->counts(), c->stream), "argmax_tally");
+  uint64_t host[2];
+  SEEAI_TRY(c, hipMemcpyAsync(host, c->counts(), sizeof host, hipMemcpyDeviceToHost, c->stream),
+            "argmax_tally counts");
+  SEEAI_TRY(c, hipStreamSynchronize(c->stream), "argmax_tally sync");
+  *hits = host[0];
+  *judged = host[1];
   return SEEAI_OK;
 }
 

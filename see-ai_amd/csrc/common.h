@@ -175,6 +175,10 @@ hipError_t LaunchSegmentStarts(const int32_t* tokens, int32_t* starts, size_t B,
                                int32_t eos, hipStream_t s);
 hipError_t LaunchArgmaxRows(const float* probs, size_t rows, size_t cols, int32_t* out,
                             hipStream_t s);
+// counts[0] = rows whose label (not -1) is their argmax, counts[1] = rows
+// with a label; both zeroed first on the stream.
+hipError_t LaunchArgmaxTally(const float* probs, const int32_t* labels, size_t rows, size_t cols,
+                             uint64_t* counts, hipStream_t s);
 
 // Loss family (k_loss.hip).  ws: XEntFwdScratchBytes(rows) for the forward,
 // 64 bytes for the backward.

@@ -310,11 +310,10 @@ __global__ void SegmentStartsKernel(const int32_t* __restrict__ tokens, int32_t*
 
 // Eval argmax (update_engine.cc:552-560): the first maximum wins; a NaN
 // never wins, and a NaN in column 0 keeps index 0 (no comparison beats it).
-__global__ void __launch_bounds__(kThreads)
-ArgmaxKernel(const float* __restrict__ probs, size_t cols, int32_t* __restrict__ out) {
+// One 256-lane workgroup per row; every lane gets the row's index.
+__device__ int RowArgmax(const float* __restrict__ row, size_t cols) {
   __shared__ float bv[kThreads];
   __shared__ int bi[kThreads];
-  const float* row = probs + static_cast<size_t>(blockIdx.x) * cols;
   float best = -INFINITY;
   int idx = -1;
   for (size_t c = threadIdx.x; c < cols; c += kThreads) {
@@ -339,9 +338,35 @@ ArgmaxKernel(const float* __restrict__ probs, size_t cols, int32_t* __restrict__
     }
     __syncthreads();
   }
+  const float v0 = row[0];
+  return (v0 != v0 || bi[0] < 0) ? 0 : bi[0];
+}
+
+__global__ void __launch_bounds__(kThreads)
+ArgmaxKernel(const float* __restrict__ probs, size_t cols, int32_t* __restrict__ out) {
+  const int am = RowArgmax(probs + static_cast<size_t>(blockIdx.x) * cols, cols);
+  if (threadIdx.x == 0) out[blockIdx.x] = am;
+}
+
+// The eval accuracy tally (update_engine.cc:537-565): over the rows whose
+// label is not -1, how many have their label as the argmax, and how many
+// were judged.  Integer counts, so the order of the additions cannot change
+// them; counts[0] = hits, counts[1] = judged rows, zeroed by ZeroCounts on
+// the same stream first (a kernel, not a memset, so a captured graph may
+// hold it).
+__global__ void ZeroCounts(unsigned long long* __restrict__ counts) {
+  if (threadIdx.x < 2) counts[threadIdx.x] = 0;
+}
+
+__global__ void __launch_bounds__(kThreads)
+ArgmaxTallyKernel(const float* __restrict__ probs, const int32_t* __restrict__ labels, size_t cols,
+                  unsigned long long* __restrict__ counts) {
+  const int32_t label = labels[blockIdx.x];
+  if (label < 0) return;  // uniform over the workgroup: an unjudged row
+  const int am = RowArgmax(probs + static_cast<size_t>(blockIdx.x) * cols, cols);
   if (threadIdx.x == 0) {
-    const float v0 = row[0];
-    out[blockIdx.x] = (v0 != v0 || bi[0] < 0) ? 0 : bi[0];
+    if (am == label) atomicAdd(&counts[0], 1ull);
+    atomicAdd(&counts[1], 1ull);
   }
 }
 
@@ -570,6 +595,15 @@ hipError_t LaunchArgmaxRows(const float* probs, size_t rows, size_t cols, int32_
   if (rows == 0 || cols == 0) return hipSuccess;
   hipLaunchKernelGGL(ArgmaxKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, probs,
                      cols, out);
+  return hipGetLastError();
+}
+hipError_t LaunchArgmaxTally(const float* probs, const int32_t* labels, size_t rows, size_t cols,
+                             uint64_t* counts, hipStream_t s) {
+  auto* c = reinterpret_cast<unsigned long long*>(counts);
+  hipLaunchKernelGGL(ZeroCounts, dim3(1), dim3(64), 0, s, c);
+  if (rows == 0 || cols == 0) return hipGetLastError();
+  hipLaunchKernelGGL(ArgmaxTallyKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s,
+                     probs, labels, cols, c);
   return hipGetLastError();
 }
 

@@ -110,6 +110,7 @@ EXPORTS = {
     "seeai_xent_bwd": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _I]),
     "seeai_adamw_step": (_I, [_P, _P, _P, _P, _P, _U64, C.POINTER(StepParams), _F]),
     "seeai_argmax_rows": (_I, [_P, _P, _U64, _U64, _P]),
+    "seeai_argmax_tally": (_I, [_P, _P, _P, _U64, _U64, C.POINTER(_U64), C.POINTER(_U64)]),
 }
 # include/seeai_engine.h: the plan engine (see-ai_amd/host/).
 ENGINE_EXPORTS = {
@@ -122,6 +123,8 @@ ENGINE_EXPORTS = {
     "seeai_engine_train_step": (_I, [_P, _P, _P, C.POINTER(_F)]),
     "seeai_engine_train_resident": (_I, [_P, C.POINTER(_F)]),
     "seeai_engine_evaluate": (_I, [_P, _P, _P, C.POINTER(_F)]),
+    "seeai_engine_evaluate_metrics": (_I, [_P, _P, _P, C.POINTER(_F), C.POINTER(_U64),
+                                          C.POINTER(_U64)]),
     "seeai_engine_merge": (_I, [_P]),
     "seeai_engine_bind_source": (_I, [_P, _P, _U64]),
     "seeai_engine_read": (_I, [_P, _U64, _P, _U64]),
@@ -412,6 +415,17 @@ class Engine:
         self._check(_lib.seeai_engine_evaluate(
             self.h, x.ctypes.data, None if lab is None else lab.ctypes.data, C.byref(loss)))
         return loss.value
+
+    def evaluate_metrics(self, inputs, labels=None):
+        """(loss, hits, judged): the eval program and its accuracy tally."""
+        import numpy as np
+        x = np.ascontiguousarray(inputs, np.float32)
+        lab = None if labels is None else np.ascontiguousarray(labels)
+        loss, hits, judged = _F(0.0), _U64(0), _U64(0)
+        self._check(_lib.seeai_engine_evaluate_metrics(
+            self.h, x.ctypes.data, None if lab is None else lab.ctypes.data, C.byref(loss),
+            C.byref(hits), C.byref(judged)))
+        return loss.value, int(hits.value), int(judged.value)
 
     def merge(self):
         self._check(_lib.seeai_engine_merge(self.h))

@@ -110,6 +110,18 @@ int seeai_engine_evaluate(seeai_engine* e, const float* input, const void* label
   return Report(e, r);
 }
 
+int seeai_engine_evaluate_metrics(seeai_engine* e, const float* input, const void* labels,
+                                  float* loss, uint64_t* hits, uint64_t* judged) {
+  if (!e || !input) return SEEAI_INVALID;
+  auto r = e->engine->EvaluateMetrics(input, labels);
+  if (r) {
+    if (loss) *loss = r->loss;
+    if (hits) *hits = r->hits;
+    if (judged) *judged = r->judged;
+  }
+  return Report(e, r);
+}
+
 int seeai_engine_merge(seeai_engine* e) {
   if (!e) return SEEAI_INVALID;
   return Report(e, e->engine->Merge());

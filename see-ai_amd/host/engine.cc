@@ -5,6 +5,8 @@
 #include <cstdlib>
 #include <cstring>
 
+#include "seeai_hip.h"
+
 namespace seeai::host {
 namespace {
 
@@ -42,6 +44,15 @@ Result<std::unique_ptr<PlanEngine>> PlanEngine::Load(std::span<const uint8_t> bl
         const uint64_t vocab = ins.out[1] >> 32;
         if (vocab != 0 && (e->vocab_bound_ == 0 || vocab < e->vocab_bound_)) e->vocab_bound_ = vocab;
       }
+    }
+  // update_engine.cc:474-478: accuracy is read from the eval program's
+  // softmax probabilities.
+  for (const Instruction& ins : e->plan_.eval)
+    if (ins.opcode == kOpSoftmaxXEntFwd || ins.opcode == kOpSoftmaxXEntMaskedFwd) {
+      e->eval_probs_ = IsArenaRef(ins.in[3]);
+      e->eval_probs_off_ = RefOffset(ins.in[3]);
+      e->eval_rows_ = ins.out[0];
+      e->eval_cols_ = ins.out[1];
     }
   if (h.input_kind > 1) return Fail("unknown plan input kind " + std::to_string(h.input_kind));
   if (h.input_kind == 1) {
@@ -192,11 +203,35 @@ Result<float> PlanEngine::TrainStepResident() {
   return Loss();
 }
 
-Result<float> PlanEngine::Evaluate(const float* input, const void* labels) {
+Result<PlanEngine::EvalMetrics> PlanEngine::EvaluateMetrics(const float* input,
+                                                             const void* labels) {
   if (plan_.eval.empty()) return Fail("plan carries no eval program");
   if (auto r = Stage(input, labels); !r) return Fail(r.error());
   if (auto r = ExecuteRange(plan_.eval, 0, plan_.eval.size()); !r) return Fail(r.error());
-  return Loss();
+  auto loss = Loss();
+  if (!loss) return Fail(loss.error());
+  EvalMetrics m;
+  m.loss = *loss;
+  const PlanHeader& h = plan_.header;
+  // update_engine.cc:467-470: class labels staged, and a softmax whose rows
+  // cover the batch.
+  if (h.label_kind == 1 && eval_probs_ && eval_cols_ > 0 && eval_rows_ >= h.batch) {
+    uint8_t* dev = static_cast<uint8_t*>(seeai_arena(backend_->context()));
+    const auto* probs = reinterpret_cast<const float*>(dev + eval_probs_off_);
+    const auto* lab = reinterpret_cast<const int32_t*>(dev + RefOffset(h.label_ref));
+    if (seeai_argmax_tally(backend_->context(), probs, lab, h.batch, eval_cols_, &m.hits,
+                           &m.judged) != SEEAI_OK)
+      return Fail(std::string("backend 'hip' failed to tally the eval accuracy: ") +
+                  seeai_last_error(backend_->context()));
+    m.tracked = true;
+  }
+  return m;
+}
+
+Result<float> PlanEngine::Evaluate(const float* input, const void* labels) {
+  auto m = EvaluateMetrics(input, labels);
+  if (!m) return Fail(m.error());
+  return m->loss;
 }
 
 Result<void> PlanEngine::Merge() {

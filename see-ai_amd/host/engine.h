@@ -47,7 +47,19 @@ class PlanEngine {
   // Runs the train program again on the batch already staged (the bench's
   // device-resident step: no host-to-device copy inside the step).
   Result<float> TrainStepResident();
-  // The eval program on one staged batch (update_engine.cc:437-565).
+  // The eval program on one staged batch (update_engine.cc:437-565): the
+  // loss, and -- where the plan trains on class labels and its eval program
+  // ends in a softmax over at least the batch's rows -- the accuracy tally:
+  // rows whose argmax (first maximum wins) is their label, over the rows
+  // whose label is not -1 (:537-565).  judged = 0 where accuracy is not
+  // tracked.
+  struct EvalMetrics {
+    float loss = 0.0f;
+    uint64_t hits = 0;
+    uint64_t judged = 0;
+    bool tracked = false;
+  };
+  Result<EvalMetrics> EvaluateMetrics(const float* input, const void* labels);
   Result<float> Evaluate(const float* input, const void* labels);
   // The merge program, then the emit entries' deltas copied to the host
   // mirror (update_engine.cc:1028-1063).
@@ -79,6 +91,10 @@ class PlanEngine {
   bool masked_labels_ = false;  // the plan's loss ignores positions labelled -1
   uint64_t vocab_bound_ = 0;     // token plans: the narrowest embedding's rows
   uint64_t source_required_ = 0;  // bytes of the source model the programs read
+  // The eval program's last softmax (update_engine.cc:474-478): its
+  // probabilities' arena offset, rows and width.
+  uint64_t eval_probs_off_ = 0, eval_rows_ = 0, eval_cols_ = 0;
+  bool eval_probs_ = false;
   uint64_t source_bytes_ = 0;     // bytes of the bound source model
 };
 

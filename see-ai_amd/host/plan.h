@@ -35,6 +35,9 @@ inline constexpr uint64_t kSourceBit = uint64_t{1} << 62;
 
 inline constexpr uint64_t RefOffset(uint64_t ref) { return ref & ~(kRodataBit | kSourceBit); }
 inline constexpr bool IsRodataRef(uint64_t ref) { return ref != kNullRef && (ref & kRodataBit); }
+inline constexpr bool IsArenaRef(uint64_t ref) {
+  return ref != kNullRef && (ref & (kRodataBit | kSourceBit)) == 0;
+}
 inline constexpr bool IsSourceRef(uint64_t ref) {
   return ref != kNullRef && (ref & (kRodataBit | kSourceBit)) == kSourceBit;
 }

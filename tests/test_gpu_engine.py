@@ -58,8 +58,20 @@ def test_c1_training_matches_the_oracle(hip, orc, torch_cuda, c1):
     assert eng.step == 6
     compare_arena(eng, twin, c1.arena, PERSISTENT)
     x, y = batch(99)
-    assert abs(eng.evaluate(x, y) - twin.evaluate(x, y)) <= TOL * 6
+    loss, hits, judged = eng.evaluate_metrics(x, y)
+    assert abs(loss - twin.evaluate(x, y)) <= TOL * 6
     compare_arena(eng, twin, c1.arena, ["probs", "logits"])
+    # the accuracy tally: the device's argmax over the device's probabilities
+    # is the oracle's over the same bytes, and -- where no row's top two
+    # classes lie within the 1e-5 parity bar -- the twin's
+    off, nb = c1.arena["probs"]
+    gp = np.frombuffer(eng.read(off, nb), np.float32).reshape(32, 256)
+    cp = np.frombuffer(twin.read(off, nb), np.float32).reshape(32, 256)
+    assert (hits, judged) == orc.argmax_tally(gp, y)
+    top2 = np.sort(cp, axis=1)[:, -2:]
+    if np.all(top2[:, 1] - top2[:, 0] > 1e-5 * top2[:, 1]):
+        assert (hits, judged) == orc.argmax_tally(cp, y)
+    assert judged == 32
     eng.merge()
     twin.do_merge()
     compare_arena(eng, twin, c1.arena, ["D1", "D2"])

@@ -777,6 +777,55 @@ def test_store_drop_is_decided_per_program_not_per_address(hip, orc, backend):
     assert got.tobytes() == want.tobytes()
 
 
+def test_source_refs_read_the_bound_source_model(hip, orc, backend):
+    """Bit 62 alone names the source model file's image (cpu_backend.cc:
+    221-240): a frozen weight, an int8 weight with its column scales and an
+    embedding table read from a source image bound by seeai_bind_source,
+    against the oracle given the same image.  Binding another image changes
+    what the same program reads."""
+    from tests.plan_ops import ins
+    SRC = 1 << 62
+    r = rng(21)
+    M, K, N, V = 64, 96, 80, 50
+    w = (r.standard_normal((K, N)) * 0.02).astype(np.float32)
+    q = r.integers(-127, 128, (K, N)).astype(np.int8)
+    qs = r.uniform(1e-3, 5e-2, N).astype(np.float32)
+    table = r.standard_normal((V, K)).astype(np.float32)
+
+    def source_image(scale):
+        img = np.zeros(65536, np.uint8)
+        for off, a in [(0, w * scale), (16384, q), (16384 + K * N, qs * scale),
+                       (32768, table * scale)]:
+            b = np.ascontiguousarray(a).view(np.uint8).ravel()
+            img[off:off + b.size] = b
+        return img
+
+    ar = Arena()
+    x = ar.add("x", r.standard_normal((M, K)).astype(np.float32))
+    tok = ar.add("tok", r.integers(0, V, M).astype(np.int32))
+    c1, c2, e = ar.empty("c1", (M, N)), ar.empty("c2", (M, N)), ar.empty("e", (M, K))
+    prog = [ins(1, [x, SRC | 0, c1], [M, N, K]),
+            ins(29, [x, SRC | 16384, c2, SRC | (16384 + K * N)], [M, N, K], flags=1 << 4),
+            ins(41, [tok, SRC | 32768, e], [M, (V << 32) | K])]
+    arena, ro = ar.images()
+    for scale in (1.0, -3.0):
+        src = source_image(scale)
+        cpu = arena.copy()
+        for word in prog:
+            assert orc.execute(word, cpu, ro, PARAMS, source=src) == 0
+        backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+        backend.BindSource(src.tobytes())
+        sp = hip.StepParams(*PARAMS[:5], 0, PARAMS[5])
+        for word in prog:
+            backend.Execute(word, sp)
+        backend.Flush()
+        gpu = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+        for name in ["c1", "c2", "e"]:
+            assert bits_equal(ar.get(gpu, name), ar.get(cpu, name)), name
+    assert orc.execute(prog[0], arena.copy(), ro, PARAMS) == 3  # no source image: refused
+    backend.BindSource(None)
+
+
 def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
     """t written over the frozen product's C: legal one by one (C is then
     read back with t's bytes in it), wrong once the frozen product moves after
@@ -1027,4 +1076,31 @@ def test_argmax_first_max_wins(hip, orc, torch_cuda):
     ctx.call("seeai_argmax_rows", dP.data_ptr(), 300, 777, out.data_ptr())
     torch.cuda.synchronize()
     assert bits_equal(out.cpu().numpy(), want)
+    ctx.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(300, 777), (1, 5), (4096, 256), (64, 32000)])
+def test_argmax_tally_skips_unlabelled_rows(hip, orc, torch_cuda, rows, cols):
+    """The eval accuracy tally (update_engine.cc:537-565) on the device:
+    hits and judged rows equal the oracle's, with -1 labels skipped, tied
+    maxima (first wins) and NaN rows; two calls in a row start from zero."""
+    import ctypes as C
+    torch = torch_cuda
+    r = rng(rows + cols)
+    P = r.integers(0, 4, (rows, cols)).astype(np.float32)
+    P[::5] = 1.0
+    if rows > 7:
+        P[7, :] = np.nan
+    labels = r.integers(-1, min(cols, 8), rows).astype(np.int32)
+    labels[::3] = np.argmax(P[::3], axis=1)  # plenty of hits
+    labels[::11] = -1
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    dP, dl = torch.from_numpy(P).cuda(), torch.from_numpy(labels).cuda()
+    for _ in range(2):
+        hits, judged = C.c_uint64(7), C.c_uint64(7)
+        ctx.call("seeai_argmax_tally", dP.data_ptr(), dl.data_ptr(), rows, cols, C.byref(hits),
+                 C.byref(judged))
+        assert (hits.value, judged.value) == orc.argmax_tally(P, labels)
+    assert judged.value == int((labels >= 0).sum())
     ctx.close()
