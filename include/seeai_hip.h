@@ -215,6 +215,18 @@ int seeai_attn_dkdv(seeai_ctx* ctx, const float* d_q, const float* d_k,
 int seeai_xent_fwd(seeai_ctx* ctx, const float* d_logits,
                    const int32_t* d_labels, float* d_loss, float* d_probs,
                    uint64_t N, uint64_t C, int masked);
+/* seeai_xent_fwd that allocates nothing -- no counterpart in the reference;
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * kernels and bits as seeai_xent_fwd; its per-row partials live in a 2 MiB
+ * device array the library holds on each GPU until the process ends, so N
+ * is at most SEEAI_XENT_NOALLOC_MAX_ROWS (status 2 beyond).  Every call on
+ * one GPU shares that array: calls that overlap on one GPU (several
+ * contexts or streams at once) race. */
+#define SEEAI_XENT_NOALLOC_MAX_ROWS 131056u
+int seeai_xent_fwd_noalloc(seeai_ctx* ctx, const float* d_logits,
+                           const int32_t* d_labels, float* d_loss, float* d_probs,
+                           uint64_t N, uint64_t C, int masked);
 int seeai_xent_bwd(seeai_ctx* ctx, const float* d_probs,
                    const int32_t* d_labels, const float* d_seed,
                    float* d_dlogits, uint64_t N, uint64_t C, int masked);

@@ -17,6 +17,7 @@
 #include <cstring>
 #include <initializer_list>
 #include <map>
+#include <mutex>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -69,6 +70,34 @@ float BitsToF32(uint64_t w) {
 
 constexpr size_t kSmallBytes = 4096;  // refusal word, scale slot, accuracy counts
 constexpr size_t kInitialScratch = 1u << 20;      // grown on demand
+
+// The no-allocation entry points' workspace (seeai_xent_fwd_noalloc): a
+// file-scope device array each GPU holds from the library's load to the
+// process's end.  Host code never uses its name as an address: the device
+// address of each GPU's copy comes from hipGetSymbolAddress, taken once per
+// device at seeai_create with that device current, and kept below.
+constexpr size_t kNoAllocScratchBytes = size_t{2} << 20;  // 2 MiB
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+struct NoAllocSlot {
+  std::once_flag once;
+  void* ptr = nullptr;       // this device's copy of `scratch`
+  hipError_t status = hipSuccess;
+};
+NoAllocSlot g_noalloc[kMaxDevices];
+
+// Looks the array's address up on `device` (which must be current), once.
+hipError_t NoAllocScratchInit(int device) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  NoAllocSlot& slot = g_noalloc[device];
+  std::call_once(slot.once, [&slot] {
+    void* p = nullptr;
+    slot.status = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (slot.status == hipSuccess) slot.ptr = p;
+  });
+  return slot.status;
+}
 
 }  // namespace
 
@@ -749,6 +778,7 @@ int seeai_create(int device, seeai_ctx** out) {
   if (const char* e = std::getenv("SEEAI_KEEP_DEAD_STORES"); e && e[0] == '1')
     c->allow_dead_store_drop = 0;
   int rc = Hip(c, hipSetDevice(device), "set device");
+  if (rc == SEEAI_OK) rc = Hip(c, NoAllocScratchInit(device), "no-allocation workspace address");
   if (rc == SEEAI_OK) rc = Hip(c, hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "stream");
   if (rc == SEEAI_OK) rc = Hip(c, hipMalloc(&c->small, kSmallBytes), "small alloc");
   if (rc == SEEAI_OK) rc = Hip(c, hipMemset(c->small, 0, kSmallBytes), "small clear");
@@ -1422,6 +1452,25 @@ int seeai_xent_fwd(seeai_ctx* c, const float* logits, const int32_t* labels, flo
   void* ws;
   if (int rc = Scratch(c, XEntFwdScratchBytes(N), &ws)) return rc;
   SEEAI_TRY(c, LaunchXEntFwd(logits, labels, loss, probs, N, C, masked, ws, c->stream), "xent_fwd");
+  return SEEAI_OK;
+}
+int seeai_xent_fwd_noalloc(seeai_ctx* c, const float* logits, const int32_t* labels, float* loss,
+                           float* probs, uint64_t N, uint64_t C, int masked) {
+  if (!c) return SEEAI_INVALID;
+  if (N > SEEAI_XENT_NOALLOC_MAX_ROWS)
+    return Fail(c, SEEAI_INVALID,
+                "xent_fwd_noalloc: %llu rows exceed the %llu-row workspace (%zu bytes); use "
+                "seeai_xent_fwd",
+                static_cast<unsigned long long>(N),
+                static_cast<unsigned long long>(SEEAI_XENT_NOALLOC_MAX_ROWS), kNoAllocScratchBytes);
+  if (XEntFwdScratchBytes(N) > kNoAllocScratchBytes)
+    return Fail(c, SEEAI_INVALID, "xent_fwd_noalloc: workspace too small");
+  void* ws = g_noalloc[c->device].ptr;
+  if (!ws) return Fail(c, SEEAI_HIP_ERROR, "xent_fwd_noalloc: no workspace address on this device");
+  // Every word of the workspace the kernels read (row maxima, sums and
+  // losses) is written by them first in this call: nothing to clear.
+  SEEAI_TRY(c, LaunchXEntFwd(logits, labels, loss, probs, N, C, masked, ws, c->stream),
+            "xent_fwd_noalloc");
   return SEEAI_OK;
 }
 int seeai_xent_bwd(seeai_ctx* c, const float* probs, const int32_t* labels, const float* seed,
