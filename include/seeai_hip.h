@@ -59,9 +59,18 @@ const char* seeai_last_error(const seeai_ctx* ctx);
  * returns right after seeai_create. */
 int seeai_set_stream(seeai_ctx* ctx, void* hip_stream);
 void* seeai_get_stream(seeai_ctx* ctx);
-/* Whether kFlagRelaxed (instruction.h:356-384) is taken as a permission
- * (default 1): relaxed tiled attention runs the bf16 MFMA kernels. */
+/* Whether kFlagRelaxed (instruction.h:356-390) is taken as a permission
+ * (default 1): relaxed frozen-weight GEMMs run on bf16 MFMA (bf16-rounded
+ * activations against the stored weight, f32 accumulation). */
 int seeai_set_relaxed(seeai_ctx* ctx, int allow);
+/* Relaxed tiled attention (kAttnFwdTiled .. kAttnDVTiled with kFlagRelaxed)
+ * grants f32 products with reordered sums (instruction.h:384-390), which the
+ * f32 MFMA family provides: the default (0).  With 1 it runs on bf16 MFMA
+ * instead -- Q, K, V, dO, P and dS rounded to bf16, f32 accumulation and
+ * softmax -- for models trained in bf16 activations (BASELINE configs[2]
+ * bf16, [3], [4]); each such run counts as a relaxed execution.  The
+ * environment variable SEEAI_ATTENTION_BF16=1 sets it at seeai_create. */
+int seeai_set_attention_bf16(seeai_ctx* ctx, int on);
 /* ExecutorBackend::relaxed_executions (backend.h:149-162). */
 uint64_t seeai_relaxed_executions(const seeai_ctx* ctx);
 

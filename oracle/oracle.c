@@ -13,6 +13,7 @@
 
 #include <float.h>
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -38,6 +39,67 @@ size_t orc_chunk_count(size_t n, size_t grain) {
 /* kernel_policy.h:43-45 */
 static size_t row_grain(size_t per_row, size_t budget) {
   return per_row == 0 ? budget : (budget / per_row > 0 ? budget / per_row : 1);
+}
+
+/* Threads.  Work is cut into the reference's ParallelFor chunks
+ * (parallel_for.h:50-67: chunk = max(grain, ceil(n / 256))) and the chunks
+ * are handed to the threads in any order; every chunk writes only its own
+ * outputs (and its own partial, combined afterwards in chunk order), so the
+ * bits are those of one thread at every thread count, as the reference's
+ * "same bits, any thread count" rule requires.  The count is
+ * orc_set_threads(), else SEEAI_ORACLE_THREADS, else 1. */
+typedef void (*orc_chunk_fn)(void* ctx, size_t begin, size_t end, size_t chunk);
+static int g_threads = 0;
+
+void orc_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+int orc_threads(void) {
+  if (g_threads <= 0) {
+    const char* e = getenv("SEEAI_ORACLE_THREADS");
+    const int n = e ? atoi(e) : 1;
+    g_threads = n > 0 ? n : 1;
+  }
+  return g_threads;
+}
+
+typedef struct {
+  orc_chunk_fn fn;
+  void* ctx;
+  size_t n, grain, count;
+  size_t next; /* the next chunk to take */
+} OrcWork;
+
+static void* orc_worker(void* arg) {
+  OrcWork* w = (OrcWork*)arg;
+  for (;;) {
+    const size_t c = __atomic_fetch_add(&w->next, 1, __ATOMIC_RELAXED);
+    if (c >= w->count) break;
+    const size_t b = c * w->grain;
+    const size_t e = b + w->grain < w->n ? b + w->grain : w->n;
+    w->fn(w->ctx, b, e, c);
+  }
+  return NULL;
+}
+
+/* Runs fn over [0, n) in chunks of orc_chunk_grain(n, grain); returns the
+ * chunk count. */
+static size_t orc_parallel(size_t n, size_t grain, orc_chunk_fn fn, void* ctx) {
+  if (n == 0) return 0;
+  OrcWork w = {fn, ctx, n, orc_chunk_grain(n, grain), 0, 0};
+  w.count = (n + w.grain - 1) / w.grain;
+  int t = orc_threads();
+  if ((size_t)t > w.count) t = (int)w.count;
+  if (t <= 1) {
+    orc_worker(&w);
+    return w.count;
+  }
+  pthread_t ids[256];
+  if (t > 256) t = 256;
+  int started = 0;
+  for (; started < t - 1; ++started)
+    if (pthread_create(&ids[started], NULL, orc_worker, &w) != 0) break;
+  orc_worker(&w);
+  for (int i = 0; i < started; ++i) pthread_join(ids[i], NULL);
+  return w.count;
 }
 
 /* kernel_policy.h:122-136: the shared activation expressions. */
@@ -78,64 +140,115 @@ static float bf16_to_f32(uint16_t b) {
  * B element kinds: 0 f32, 1 int8 (widened), 2 bf16 (widened); with a
  * column scale the widened int8 is multiplied by cs[n] (gemm.cc:98-104).
  * `accumulate` keeps C's prior contents (GemmAccNN, gemm.cc:617-624). */
+typedef struct {
+  const float* A;
+  const float* B; /* widened to f32 (int8 times its column scale, bf16) */
+  float* C;
+  size_t M, N, K;
+  float alpha;
+  int a_transposed, accumulate;
+} NnArgs;
+/* One output row at a time: the row's N sums advance together quad by quad,
+ * each element through exactly the chain above (its order of operations is
+ * unchanged; only independent elements sit side by side in vector lanes). */
+__attribute__((target_clones("avx2", "default")))
+static void nn_rows(void* ctx, size_t m0, size_t m1, size_t chunk) {
+  (void)chunk;
+  const NnArgs* g = (const NnArgs*)ctx;
+  const float* A = g->A;
+  const float* B = g->B;
+  const size_t M = g->M, N = g->N, K = g->K;
+  const float alpha = g->alpha;
+  for (size_t m = m0; m < m1; ++m) {
+    float* restrict c = g->C + m * N;
+    if (!g->accumulate)
+      for (size_t n = 0; n < N; ++n) c[n] = 0.0f;
+#define ORC_A(kk) (g->a_transposed ? A[(kk) * M + m] : A[m * K + (kk)])
+    size_t k = 0;
+    for (; k + 4 <= K; k += 4) {
+      const float a0 = alpha * ORC_A(k + 0);
+      const float a1 = alpha * ORC_A(k + 1);
+      const float a2 = alpha * ORC_A(k + 2);
+      const float a3 = alpha * ORC_A(k + 3);
+      const float* restrict b0 = B + (k + 0) * N;
+      const float* restrict b1 = B + (k + 1) * N;
+      const float* restrict b2 = B + (k + 2) * N;
+      const float* restrict b3 = B + (k + 3) * N;
+      for (size_t n = 0; n < N; ++n) c[n] += a0 * b0[n] + a1 * b1[n] + a2 * b2[n] + a3 * b3[n];
+    }
+    for (; k < K; ++k) {
+      const float a = alpha * ORC_A(k);
+      const float* restrict bk = B + k * N;
+      for (size_t n = 0; n < N; ++n) c[n] += a * bk[n];
+    }
+#undef ORC_A
+  }
+}
+/* B's elements as the core reads them: f32 as is; int8 widened, times the
+ * column scale where there is one (gemm.cc:98-104); bf16 widened.  Returns
+ * B itself for f32, else a buffer the caller frees. */
+static const float* widen(const void* B, int b_kind, const float* col_scale, size_t rows,
+                          size_t cols, int scale_by_col) {
+  if (b_kind == 0) return (const float*)B;
+  const size_t count = rows * cols;
+  float* w = (float*)malloc((count ? count : 1) * sizeof(float));
+  for (size_t r = 0; r < rows; ++r)
+    for (size_t c = 0; c < cols; ++c) {
+      const size_t i = r * cols + c;
+      if (b_kind == 1)
+        w[i] = scale_by_col && col_scale ? (float)((const int8_t*)B)[i] * col_scale[c]
+                                         : (float)((const int8_t*)B)[i];
+      else
+        w[i] = bf16_to_f32(((const uint16_t*)B)[i]);
+    }
+  return w;
+}
 static void nn_core(const float* A, const void* B, int b_kind,
                     const float* col_scale, float* C, size_t M, size_t N,
                     size_t K, float alpha, int a_transposed, int accumulate) {
-  for (size_t m = 0; m < M; ++m) {
-    for (size_t n = 0; n < N; ++n) {
-      float c = accumulate ? C[m * N + n] : 0.0f;
-      size_t k = 0;
-#define ORC_A(kk) (a_transposed ? A[(kk) * M + m] : A[m * K + (kk)])
-#define ORC_B(kk)                                                           \
-  (b_kind == 0   ? ((const float*)B)[(kk) * N + n]                           \
-   : b_kind == 1 ? (col_scale ? (float)((const int8_t*)B)[(kk) * N + n] *    \
-                                    col_scale[n]                            \
-                              : (float)((const int8_t*)B)[(kk) * N + n])     \
-                 : bf16_to_f32(((const uint16_t*)B)[(kk) * N + n]))
-      for (; k + 4 <= K; k += 4) {
-        const float a0 = alpha * ORC_A(k + 0);
-        const float a1 = alpha * ORC_A(k + 1);
-        const float a2 = alpha * ORC_A(k + 2);
-        const float a3 = alpha * ORC_A(k + 3);
-        const float v0 = ORC_B(k + 0), v1 = ORC_B(k + 1);
-        const float v2 = ORC_B(k + 2), v3 = ORC_B(k + 3);
-        c += a0 * v0 + a1 * v1 + a2 * v2 + a3 * v3;
-      }
-      for (; k < K; ++k) {
-        const float a = alpha * ORC_A(k);
-        c += a * ORC_B(k);
-      }
-#undef ORC_A
-#undef ORC_B
-      C[m * N + n] = c;
-    }
-  }
+  const float* Bf = widen(B, b_kind, col_scale, K, N, 1);
+  NnArgs g = {A, Bf, C, M, N, K, alpha, a_transposed, accumulate};
+  orc_parallel(M, 1, nn_rows, &g);
+  if (Bf != B) free((void*)Bf);
 }
 
 /* The NT core (gemm.cc:304-527; ReferenceNT, kernels_test.cc:1759-1775):
  * lane l accumulates every k = l (mod 8) in k order, the lanes combine in
- * lane order, and alpha multiplies the finished dot. */
-static void nt_core(const float* A, const void* B, int b_kind, float* C,
-                    size_t M, size_t N, size_t K, float alpha) {
-  for (size_t m = 0; m < M; ++m) {
-    const float* a = A + m * K;
+ * lane order, and alpha multiplies the finished dot.  The eight lanes are
+ * one 8-wide vector; each lane's chain is the reference's. */
+typedef struct {
+  const float* A;
+  const float* B; /* [N, K], widened to f32 */
+  float* C;
+  size_t N, K;
+  float alpha;
+} NtArgs;
+__attribute__((target_clones("avx2", "default")))
+static void nt_rows(void* ctx, size_t m0, size_t m1, size_t chunk) {
+  (void)chunk;
+  const NtArgs* g = (const NtArgs*)ctx;
+  const size_t N = g->N, K = g->K;
+  for (size_t m = m0; m < m1; ++m) {
+    const float* restrict a = g->A + m * K;
     for (size_t n = 0; n < N; ++n) {
+      const float* restrict b = g->B + n * K;
       float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (size_t k = 0; k < K; ++k) {
-        float b;
-        if (b_kind == 0)
-          b = ((const float*)B)[n * K + k];
-        else if (b_kind == 1)
-          b = (float)((const int8_t*)B)[n * K + k];
-        else
-          b = bf16_to_f32(((const uint16_t*)B)[n * K + k]);
-        lane[k % 8] += a[k] * b;
-      }
+      size_t k = 0;
+      for (; k + 8 <= K; k += 8)
+        for (int l = 0; l < 8; ++l) lane[l] += a[k + l] * b[k + l];
+      for (; k < K; ++k) lane[k % 8] += a[k] * b[k];
       float s = lane[0];
       for (int l = 1; l < 8; ++l) s += lane[l];
-      C[m * N + n] = alpha * s;
+      g->C[m * N + n] = g->alpha * s;
     }
   }
+}
+static void nt_core(const float* A, const void* B, int b_kind, float* C,
+                    size_t M, size_t N, size_t K, float alpha) {
+  const float* Bf = widen(B, b_kind, NULL, N, K, 0);
+  NtArgs g = {A, Bf, C, N, K, alpha};
+  orc_parallel(M, 1, nt_rows, &g);
+  if (Bf != B) free((void*)Bf);
 }
 
 /* gemm.cc:562-578: addend C = D + s, then the bias/act epilogue
@@ -251,11 +364,23 @@ void orc_quantize_cols(const float* W, int8_t* Q, float* scale, size_t K,
   for (size_t k = 0; k < K; ++k)
     for (size_t n = 0; n < N; ++n) Q[k * N + n] = quant_level(W[k * N + n], scale[n]);
 }
-void orc_gemm_w8a8(const int8_t* QA, const float* sa, const int8_t* QW,
-                   const float* sw, int32_t* acc, float* C, size_t M,
-                   size_t N, size_t K) {
+typedef struct {
+  const int8_t *QA, *QW;
+  const float *sa, *sw;
+  int32_t* acc;
+  float* C;
+  size_t N, K;
+} W8Args;
+static void w8a8_rows(void* ctx, size_t m0, size_t m1, size_t chunk) {
+  (void)chunk;
+  const W8Args* g = (const W8Args*)ctx;
+  const int8_t *QA = g->QA, *QW = g->QW;
+  const float *sa = g->sa, *sw = g->sw;
+  int32_t* acc = g->acc;
+  float* C = g->C;
+  const size_t N = g->N, K = g->K;
   int32_t* row = (int32_t*)malloc((N ? N : 1) * sizeof(int32_t));
-  for (size_t m = 0; m < M; ++m) {
+  for (size_t m = m0; m < m1; ++m) {
     memset(row, 0, N * sizeof(int32_t));
     for (size_t k = 0; k < K; ++k) {
       const int32_t a = QA[m * K + k];
@@ -268,6 +393,12 @@ void orc_gemm_w8a8(const int8_t* QA, const float* sa, const int8_t* QW,
     }
   }
   free(row);
+}
+void orc_gemm_w8a8(const int8_t* QA, const float* sa, const int8_t* QW,
+                   const float* sw, int32_t* acc, float* C, size_t M,
+                   size_t N, size_t K) {
+  W8Args g = {QA, QW, sa, sw, acc, C, N, K};
+  orc_parallel(M, 1, w8a8_rows, &g);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -656,13 +787,25 @@ static float prob_of(const float* qi, const float* kj, size_t d,
 }
 
 /* attention.cc:448-493 */
-void orc_attn_fwd_tiled(const float* q, const float* k, const float* v,
-                        float* o, float* stats, size_t B, size_t S, size_t H,
-                        size_t d, const int32_t* starts) {
+/* The tiled family's arguments; each unit u = (b, h, row) is independent. */
+typedef struct {
+  const float *q, *k, *v, *dout;
+  float *o, *stats, *out;
+  const int32_t* starts;
+  size_t B, S, H, d;
+} AttnArgs;
+
+static void attn_fwd_units(void* ctx, size_t u0, size_t u1, size_t chunk) {
+  (void)chunk;
+  const AttnArgs* a = (const AttnArgs*)ctx;
+  const float *q = a->q, *k = a->k, *v = a->v;
+  float *o = a->o, *stats = a->stats;
+  const int32_t* starts = a->starts;
+  const size_t S = a->S, H = a->H, d = a->d;
   const size_t D = H * d;
   const float inv_sqrt_d = 1.0f / sqrtf((float)d);
   float* prow = (float*)malloc((S ? S : 1) * sizeof(float));
-  for (size_t u = 0; u < B * H * S; ++u) {
+  for (size_t u = u0; u < u1; ++u) {
     const size_t b = u / (H * S), h = (u / S) % H, i = u % S;
     const float* qi = q + (b * S + i) * D + h * d;
     const size_t j0 = clamp_start(starts, b, S, i);
@@ -695,15 +838,24 @@ void orc_attn_fwd_tiled(const float* q, const float* k, const float* v,
   }
   free(prow);
 }
+void orc_attn_fwd_tiled(const float* q, const float* k, const float* v,
+                        float* o, float* stats, size_t B, size_t S, size_t H,
+                        size_t d, const int32_t* starts) {
+  AttnArgs a = {q, k, v, NULL, o, stats, NULL, starts, B, S, H, d};
+  orc_parallel(B * H * S, 1, attn_fwd_units, &a);
+}
 /* attention.cc:495-535 */
-void orc_attn_dq_tiled(const float* q, const float* k, const float* v,
-                       const float* dout, float* stats, float* dq, size_t B,
-                       size_t S, size_t H, size_t d) {
+static void attn_dq_units(void* ctx, size_t u0, size_t u1, size_t chunk) {
+  (void)chunk;
+  const AttnArgs* a = (const AttnArgs*)ctx;
+  const float *q = a->q, *k = a->k, *v = a->v, *dout = a->dout;
+  float *stats = a->stats, *dq = a->out;
+  const size_t S = a->S, H = a->H, d = a->d;
   const size_t D = H * d;
   const float inv_sqrt_d = 1.0f / sqrtf((float)d);
   float* prow = (float*)malloc((S ? 2 * S : 2) * sizeof(float));
   float* dprow = prow + S;
-  for (size_t u = 0; u < B * H * S; ++u) {
+  for (size_t u = u0; u < u1; ++u) {
     const size_t b = u / (H * S), h = (u / S) % H, i = u % S;
     const float* qi = q + (b * S + i) * D + h * d;
     const float* doi = dout + (b * S + i) * D + h * d;
@@ -729,13 +881,22 @@ void orc_attn_dq_tiled(const float* q, const float* k, const float* v,
   }
   free(prow);
 }
+void orc_attn_dq_tiled(const float* q, const float* k, const float* v,
+                       const float* dout, float* stats, float* dq, size_t B,
+                       size_t S, size_t H, size_t d) {
+  AttnArgs a = {q, k, v, dout, NULL, stats, dq, NULL, B, S, H, d};
+  orc_parallel(B * H * S, 1, attn_dq_units, &a);
+}
 /* attention.cc:537-563 */
-void orc_attn_dk_tiled(const float* q, const float* k, const float* v,
-                       const float* dout, const float* stats, float* dk,
-                       size_t B, size_t S, size_t H, size_t d) {
+static void attn_dk_units(void* ctx, size_t u0, size_t u1, size_t chunk) {
+  (void)chunk;
+  const AttnArgs* a = (const AttnArgs*)ctx;
+  const float *q = a->q, *k = a->k, *v = a->v, *dout = a->dout, *stats = a->stats;
+  float* dk = a->out;
+  const size_t S = a->S, H = a->H, d = a->d;
   const size_t D = H * d;
   const float inv_sqrt_d = 1.0f / sqrtf((float)d);
-  for (size_t u = 0; u < B * H * S; ++u) {
+  for (size_t u = u0; u < u1; ++u) {
     const size_t b = u / (H * S), h = (u / S) % H, j = u % S;
     const float* kj = k + (b * S + j) * D + h * d;
     const float* vj = v + (b * S + j) * D + h * d;
@@ -753,13 +914,22 @@ void orc_attn_dk_tiled(const float* q, const float* k, const float* v,
     }
   }
 }
+void orc_attn_dk_tiled(const float* q, const float* k, const float* v,
+                       const float* dout, const float* stats, float* dk,
+                       size_t B, size_t S, size_t H, size_t d) {
+  AttnArgs a = {q, k, v, dout, NULL, (float*)stats, dk, NULL, B, S, H, d};
+  orc_parallel(B * H * S, 1, attn_dk_units, &a);
+}
 /* attention.cc:565-590 */
-void orc_attn_dv_tiled(const float* q, const float* k, const float* dout,
-                       const float* stats, float* dv, size_t B, size_t S,
-                       size_t H, size_t d) {
+static void attn_dv_units(void* ctx, size_t u0, size_t u1, size_t chunk) {
+  (void)chunk;
+  const AttnArgs* a = (const AttnArgs*)ctx;
+  const float *q = a->q, *k = a->k, *dout = a->dout, *stats = a->stats;
+  float* dv = a->out;
+  const size_t S = a->S, H = a->H, d = a->d;
   const size_t D = H * d;
   const float inv_sqrt_d = 1.0f / sqrtf((float)d);
-  for (size_t u = 0; u < B * H * S; ++u) {
+  for (size_t u = u0; u < u1; ++u) {
     const size_t b = u / (H * S), h = (u / S) % H, j = u % S;
     const float* kj = k + (b * S + j) * D + h * d;
     float* dvj = dv + (b * S + j) * D + h * d;
@@ -773,6 +943,12 @@ void orc_attn_dv_tiled(const float* q, const float* k, const float* dout,
       for (size_t c = 0; c < d; ++c) dvj[c] += p * doi[c];
     }
   }
+}
+void orc_attn_dv_tiled(const float* q, const float* k, const float* dout,
+                       const float* stats, float* dv, size_t B, size_t S,
+                       size_t H, size_t d) {
+  AttnArgs a = {q, k, NULL, dout, NULL, (float*)stats, dv, NULL, B, S, H, d};
+  orc_parallel(B * H * S, 1, attn_dv_units, &a);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -797,19 +973,37 @@ static double safe_log_term(float p) {
   return log(safe);
 }
 /* loss.cc:35-59: one double partial per ParallelFor chunk, in chunk order. */
+typedef struct {
+  const float* logits;
+  const int32_t* labels;
+  float* probs;
+  size_t C;
+  int masked;
+  double part[kMaxChunks];
+  uint64_t targets[kMaxChunks];
+} XentArgs;
+static void xent_chunk(void* ctx, size_t r0, size_t r1, size_t chunk) {
+  XentArgs* a = (XentArgs*)ctx;
+  const size_t C = a->C;
+  double part = 0.0;
+  uint64_t t = 0;
+  for (size_t n = r0; n < r1; ++n) {
+    row_softmax(a->logits + n * C, a->probs + n * C, C);
+    if (a->masked && a->labels[n] < 0) continue;
+    part -= safe_log_term(a->probs[n * C + (size_t)a->labels[n]]);
+    ++t;
+  }
+  a->part[chunk] = part;
+  a->targets[chunk] = t;
+}
 void orc_xent_fwd(const float* logits, const int32_t* labels, float* loss,
                   float* probs, size_t N, size_t C) {
-  const size_t grain = orc_chunk_grain(N, row_grain(C, kGrainMath));
+  XentArgs* a = (XentArgs*)calloc(1, sizeof(XentArgs));
+  a->logits = logits, a->labels = labels, a->probs = probs, a->C = C, a->masked = 0;
+  const size_t chunks = orc_parallel(N, row_grain(C, kGrainMath), xent_chunk, a);
   double total = 0.0;
-  for (size_t r0 = 0; r0 < N; r0 += grain) {
-    const size_t r1 = r0 + grain < N ? r0 + grain : N;
-    double part = 0.0;
-    for (size_t n = r0; n < r1; ++n) {
-      row_softmax(logits + n * C, probs + n * C, C);
-      part -= safe_log_term(probs[n * C + (size_t)labels[n]]);
-    }
-    total += part;
-  }
+  for (size_t c = 0; c < chunks; ++c) total += a->part[c];  /* chunk order */
+  free(a);
   *loss = (float)(total / (double)N);
 }
 /* loss.cc:61-72 */
@@ -824,22 +1018,16 @@ void orc_xent_bwd(const float* probs, const int32_t* labels, const float* seed,
 /* loss.cc:74-105 */
 void orc_xent_masked_fwd(const float* logits, const int32_t* labels,
                          float* loss, float* probs, size_t N, size_t C) {
-  const size_t grain = orc_chunk_grain(N, row_grain(C, kGrainMath));
+  XentArgs* a = (XentArgs*)calloc(1, sizeof(XentArgs));
+  a->logits = logits, a->labels = labels, a->probs = probs, a->C = C, a->masked = 1;
+  const size_t chunks = orc_parallel(N, row_grain(C, kGrainMath), xent_chunk, a);
   double total = 0.0;
   uint64_t T = 0;
-  for (size_t r0 = 0; r0 < N; r0 += grain) {
-    const size_t r1 = r0 + grain < N ? r0 + grain : N;
-    double part = 0.0;
-    uint64_t t = 0;
-    for (size_t n = r0; n < r1; ++n) {
-      row_softmax(logits + n * C, probs + n * C, C);
-      if (labels[n] < 0) continue;
-      part -= safe_log_term(probs[n * C + (size_t)labels[n]]);
-      ++t;
-    }
-    total += part;
-    T += t;
+  for (size_t c = 0; c < chunks; ++c) {  /* chunk order */
+    total += a->part[c];
+    T += a->targets[c];
   }
+  free(a);
   *loss = T ? (float)(total / (double)T) : 0.0f;
 }
 /* loss.cc:107-126 */

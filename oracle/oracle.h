@@ -175,6 +175,13 @@ void orc_argmax_rows(const float* probs, size_t rows, size_t cols,
  * then the size; the 8 bytes at hash_offset read as zero. */
 uint64_t orc_plan_self_hash(const uint8_t* plan, size_t size, size_t hash_offset);
 
+/* --- Threads: every function gives the same bits at every count -------- */
+/* Work runs in the reference's ParallelFor chunks (parallel_for.h:50-67)
+ * spread over n threads; 0 or less means 1.  The default is
+ * SEEAI_ORACLE_THREADS, else 1. */
+void orc_set_threads(int n);
+int orc_threads(void);
+
 /* --- Instruction interpreter (runtime/executor/cpu_backend.cc:260-646) --- */
 /* Runs one 64-byte UpdateInstruction against an arena / rodata pair.
  * Returns 0 ok, 1 refusal (non-finite norm), 4 clip-threshold refusal,

@@ -96,6 +96,8 @@ ORACLE_ONLY = {
     "adamw_bias_corrections": (None, [_F, _F, _U64, _P, _P]),
     "execute": (_I, [_P, _P, _P, _P]),
     "execute_src": (_I, [_P, _P, _P, _P, _P]),
+    "set_threads": (None, [_I]),
+    "threads": (_I, []),
     "chunk_grain": (_Z, [_Z, _Z]),
     "chunk_count": (_Z, [_Z, _Z]),
 }
@@ -492,6 +494,13 @@ class Kernels:
         out = np.empty(probs.shape[0], np.int32)
         self._fn("argmax_rows")(_ptr(probs), probs.shape[0], probs.shape[1], _ptr(out))
         return out
+
+    def set_threads(self, n: int):
+        """Threads for the chunked loops; the bits do not depend on it."""
+        self._fn("set_threads")(int(n))
+
+    def threads(self) -> int:
+        return int(self._fn("threads")())
 
     def argmax_tally(self, probs, labels):
         """(hits, judged rows) over rows whose label is not -1

@@ -116,6 +116,9 @@ struct seeai_ctx {
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
   int allow_relaxed = 1;
+  // Relaxed tiled attention on bf16 operands (the flash kernels) instead of
+  // f32 products; off by default (seeai_set_attention_bf16).
+  int attn_bf16 = 0;
   uint64_t relaxed = 0;
   // The program of the range being executed (seeai_begin_range, the seam's
   // BeginRange): lets two adjacent instructions run as one dispatch.
@@ -329,6 +332,16 @@ int Relaxed(seeai_ctx* c, const Instruction& ins) {
   return r;
 }
 
+// A relaxed tiled-attention instruction (instruction.h:384-390: f32 products
+// with the sums reordered, at head widths up to 64) runs the f32 MFMA
+// family unless the backend is switched to bf16 attention; only the bf16
+// kernels are a relaxed execution.
+int RelaxedAttention(seeai_ctx* c, const Instruction& ins) {
+  const int r = (ins.flags & kFlagRelaxed) && c->allow_relaxed && c->attn_bf16 ? 1 : 0;
+  c->relaxed += r;
+  return r;
+}
+
 bool Overlap(const uint8_t* a, uint64_t na, const uint8_t* b, uint64_t nb) {
   return a < b + nb && b < a + na;
 }
@@ -345,7 +358,7 @@ bool Overlap(const uint8_t* a, uint64_t na, const uint8_t* b, uint64_t nb) {
 // pass reads: the separate order may legally reuse a buffer the first
 // instruction alone still reads.  Returns -1 when the pair does not fuse.
 int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
-  if (!c->allow_fusion || !c->allow_relaxed || !c->prog || at < c->prog ||
+  if (!c->allow_fusion || !c->allow_relaxed || !c->attn_bf16 || !c->prog || at < c->prog ||
       at >= c->prog + c->prog_count * 64 || (at - c->prog) % 64 != 0)
     return -1;
   const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
@@ -375,8 +388,8 @@ int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
       if (Overlap(o, act, reinterpret_cast<const uint8_t*>(in), act)) return -1;
   for (const uint8_t* o : {o1, o2})
     if (Overlap(o, act, reinterpret_cast<const uint8_t*>(stats), st)) return -1;
-  Relaxed(c, ins);
-  Relaxed(c, nx);
+  RelaxedAttention(c, ins);
+  RelaxedAttention(c, nx);
   SEEAI_TRY(c, LaunchAttnDKDVFused(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
             "attn.dkdv_fused");
   c->done[0] = at + 64;
@@ -721,7 +734,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
         B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
         starts = R.i32(ins.out[2]);
       }
-      const int dt = Relaxed(c, ins);
+      const int dt = RelaxedAttention(c, ins);
       SEEAI_TRY(c,
                 LaunchAttnFwdTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]),
                                    R.f(ins.in[3]), R.f(ins.out[0]), B, S, H, d, starts, s),
@@ -733,7 +746,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
     case 50: {  // AttnDQTiled / DKTiled / DVTiled
       const uint64_t g = ins.out[2];
       const uint64_t B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
-      const int dt = Relaxed(c, ins);
+      const int dt = RelaxedAttention(c, ins);
       hipError_t e;
       if (ins.opcode == 48)
         e = LaunchAttnDQTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
@@ -777,6 +790,9 @@ int seeai_create(int device, seeai_ctx** out) {
   // same-session control of the dead-store scan).
   if (const char* e = std::getenv("SEEAI_KEEP_DEAD_STORES"); e && e[0] == '1')
     c->allow_dead_store_drop = 0;
+  // SEEAI_ATTENTION_BF16=1: relaxed attention on bf16 operands from the
+  // start (seeai_set_attention_bf16 for a caller that sets it itself).
+  if (const char* e = std::getenv("SEEAI_ATTENTION_BF16"); e && e[0] == '1') c->attn_bf16 = 1;
   int rc = Hip(c, hipSetDevice(device), "set device");
   if (rc == SEEAI_OK) rc = Hip(c, NoAllocScratchInit(device), "no-allocation workspace address");
   if (rc == SEEAI_OK) rc = Hip(c, hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "stream");
@@ -822,6 +838,11 @@ int seeai_set_relaxed(seeai_ctx* c, int allow) {
   return SEEAI_OK;
 }
 uint64_t seeai_relaxed_executions(const seeai_ctx* c) { return c ? c->relaxed : 0; }
+int seeai_set_attention_bf16(seeai_ctx* c, int on) {
+  if (!c) return SEEAI_INVALID;
+  c->attn_bf16 = on ? 1 : 0;
+  return SEEAI_OK;
+}
 
 int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t rodata_bytes) {
   if (!c) return SEEAI_INVALID;

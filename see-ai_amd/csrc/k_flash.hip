@@ -1,9 +1,12 @@
-// k_flash.hip -- the relaxed (kFlagRelaxed, instruction.h:356-384) tiled
-// attention family on CDNA4 bf16 MFMA: forward, dQ, dK and dV
-// over the stats-row contract of the exact family
-// (instruction.h:174-190, 234-259).  Operands arrive as f32 and are rounded
-// to bf16 (RNE) as they are staged; products accumulate in f32; softmax
-// runs in f32 in the base-2 domain.
+// k_flash.hip -- the bf16-operand tiled attention family on CDNA4 bf16
+// MFMA: forward, dQ, dK and dV over the stats-row contract of the exact
+// family (instruction.h:174-190, 234-259).  It runs relaxed (kFlagRelaxed,
+// instruction.h:356-390) attention where the backend is switched to bf16
+// attention (seeai_set_attention_bf16: the BASELINE bf16 configurations).
+// Operands arrive as f32 and are rounded to bf16 (RNE) as they are staged,
+// unscaled, so bf16-valued inputs enter the products exactly; products
+// accumulate in f32; the 1/sqrt(d) and log2(e) factors multiply the f32
+// scores; softmax runs in f32 in the base-2 domain.
 //
 // Geometry: one workgroup = 4 waves = 128 rows of one (b, h) -- queries for
 // the forward and dQ, keys for dK/dV -- each wave owning 32 rows; the other
@@ -231,9 +234,9 @@ __device__ __forceinline__ void UnitOf(int nq, int& bh, int& rank) {
 // ---------------------------------------------------------------------------
 // Forward: O = softmax(mask(Q K^T / sqrt d)) V and the stats row.
 //
-// Q is staged pre-scaled by log2(e)/sqrt(d), so a score tile is in base-2
-// units, and its accumulator starts at -m_use: the tile arrives as
-// s' - m_use and one v_exp gives the weight.  m_use moves only when a
+// Q is staged unscaled; a score tile's accumulator starts at -m_use / c with
+// c = log2(e)/sqrt(d), so c times the tile is s' - m_use in base-2 units and
+// one v_exp gives the weight.  m_use moves only when a
 // block's maximum exceeds it by more than 2^8 (weights stay below 2^8 in
 // f32) or on the first block a row sees; the true row maximum is tracked
 // beside it and the stats row is stated against it, so (m, 1/l) is the
@@ -277,11 +280,12 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
   const int nblk = q_hi / kBlk + 1 - blk_lo;
 
   bf16x8 qf[D / 16];
-  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, kLog2e / sqrtf(static_cast<float>(D)), qf);
+  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, 1.0f, qf);
+  const float scl = kLog2e / sqrtf(static_cast<float>(D)), inv_scl = 1.0f / scl;
 
   v16f oacc[D / 32] = {};
   float m_use = 0.0f, m_true = -INFINITY, l = 0.0f;
-  v16f cneg = {};  // splat(-m_use)
+  v16f cneg = {};  // splat(-m_use / c)
   const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
   const uint32_t ld32 = static_cast<uint32_t>(ld);
   const uint32_t slice_bytes = static_cast<uint32_t>(((S - 1) * ld + D) * 4);
@@ -301,6 +305,7 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
       st[kt] = ScoreTile<D>(Ks[buf], qf, lane, kt, cneg);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
+        st[kt][r] *= scl;
         if constexpr (kMask)  // keep j0 + row in [j_start, i]
           st[kt][r] = OrNegInf(st[kt][r], Outside(hi_rel - RowConst(kt, r), RowConst(kt, r) - lo_rel));
         bmax = fmaxf(bmax, st[kt][r]);
@@ -314,7 +319,7 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
       const float shift = need ? bmax : 0.0f;
       const float alpha = first ? 0.0f : Exp2(-shift);
       m_use += shift;
-      cneg = Splat(-m_use);
+      cneg = Splat(-m_use * inv_scl);
       l *= alpha;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= alpha;
@@ -382,8 +387,8 @@ FlashFwd(const float* __restrict__ q, const float* __restrict__ k, const float* 
 __device__ __forceinline__ float RowOffset(float m, float inv) { return m * kLog2e - log2f(inv); }
 
 // ---------------------------------------------------------------------------
-// dQ and the stats row's delta = sum_j p dP.  Q is staged pre-scaled as in
-// the forward and the score accumulators start at -mm (p = 2^score).
+// dQ and the stats row's delta = sum_j p dP.  Q is staged unscaled as in the
+// forward and the score accumulators start at -mm / c (p = 2^(c score)).
 //
 // kOnePass: dS = p (dP - delta) is linear in delta, so
 //   dQ^T = K^T (p dP)^T - delta K^T p^T,
@@ -420,7 +425,9 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
   const int i = i0 + c;
   const int ic = min(i, S - 1);
   float* st = stats + (static_cast<size_t>(bh) * S + ic) * 4;
-  const v16f cs = Splat(-RowOffset(st[0], st[1]));
+  const float isd = 1.0f / sqrtf(static_cast<float>(D));
+  const float scl = kLog2e * isd;
+  const v16f cs = Splat(-RowOffset(st[0], st[1]) / scl);
   const int j_start = static_cast<int>(StatsStart(st[3], ic));
   if (threadIdx.x == 0) min_start = S;
   __syncthreads();
@@ -430,10 +437,9 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
   const int blk_lo = Uniform(min_start) / kBlk;
   const int q_hi = min(qblk * kRows + kRows - 1, S - 1);
   const int nblk = q_hi / kBlk + 1 - blk_lo;
-  const float isd = 1.0f / sqrtf(static_cast<float>(D));
 
   bf16x8 qf[D / 16], df[D / 16];
-  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, kLog2e * isd, qf);
+  LoadOwned<D>(q + base + static_cast<size_t>(ic) * ld, g, 1.0f, qf);
   LoadOwned<D>(dout + base + static_cast<size_t>(ic) * ld, g, 1.0f, df);
 
   const uint32_t ld32 = static_cast<uint32_t>(ld);
@@ -467,7 +473,7 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
         float w[16], p[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float e = Exp2(sc[r]);
+          float e = Exp2(sc[r] * scl);
           if constexpr (kMask)  // keep j0 + row in [j_start, i]
             e = OrZero(e, Outside(hi_rel - RowConst(kt, r), RowConst(kt, r) - lo_rel));
           if (kOnePass || pass == 0) delta = __builtin_fmaf(dpt[r], e, delta);
@@ -520,9 +526,9 @@ FlashDQ(const float* __restrict__ q, const float* __restrict__ k, const float* _
 // ---------------------------------------------------------------------------
 // dK and / or dV: one wave per 32 keys walking the query blocks from the
 // diagonal; S = Q K^T and dP = dO V^T formed query-major, dK^T += Q^T dS
-// (times 1/sqrt d at the end), dV^T += dO^T P.  K is staged pre-scaled as in
-// the forward; the score and dP accumulators start at each query row's -mm
-// and -delta, read from LDS.  With both outputs (kDK && kDV) one pass forms
+// (times 1/sqrt d at the end), dV^T += dO^T P.  K is staged unscaled; the
+// score and dP accumulators start at each query row's -mm / c and -delta,
+// read from LDS.  With both outputs (kDK && kDV) one pass forms
 // S, P and dP once per block and feeds both accumulations: four products
 // per block instead of the five of two passes, one exponential per score
 // instead of two.
@@ -555,10 +561,11 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
   const int j = j0w + c;
   const int jc = min(j, S - 1);
   const float isd = 1.0f / sqrtf(static_cast<float>(D));
+  const float scl = kLog2e * isd, inv_scl = 1.0f / scl;
   const float4* st_bh = reinterpret_cast<const float4*>(stats) + static_cast<size_t>(bh) * S;
 
   bf16x8 kf[D / 16], vf[D / 16];
-  LoadOwned<D>(k + base + static_cast<size_t>(jc) * ld, g, kLog2e * isd, kf);
+  LoadOwned<D>(k + base + static_cast<size_t>(jc) * ld, g, 1.0f, kf);
   if (kDK) LoadOwned<D>(v + base + static_cast<size_t>(jc) * ld, g, 1.0f, vf);
 
   const int blk_first = (kblk * kRows) / kBlk;
@@ -579,7 +586,7 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
       int start = 0;
       if (iq < S) {
         const float4 s4 = st_bh[iq];
-        Smm[buf][t] = -RowOffset(s4.x, s4.y);
+        Smm[buf][t] = -RowOffset(s4.x, s4.y) * inv_scl;
         Sdl[buf][t] = -s4.z;
         start = static_cast<int>(StatsStart(s4.w, iq));
       } else {
@@ -618,7 +625,7 @@ FlashDKDV(const float* __restrict__ q, const float* __restrict__ k, const float*
       float p[16], w[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float e = Exp2(sc[r]);
+        float e = Exp2(sc[r] * scl);
         if constexpr (kMask) {  // keep query row r0 + il >= j and its start <= j
           const int il = RowOf(kt, r, g);
           e = OrZero(e, Outside(lo_rel + RowConst(kt, r), j - Sst[buf][il]));

@@ -77,6 +77,7 @@ EXPORTS = {
     "seeai_set_stream": (_I, [_P, _P]),
     "seeai_get_stream": (_P, [_P]),
     "seeai_set_relaxed": (_I, [_P, _I]),
+    "seeai_set_attention_bf16": (_I, [_P, _I]),
     "seeai_relaxed_executions": (_U64, [_P]),
     "seeai_bind": (_I, [_P, _U64, _P, _U64]),
     "seeai_bind_source": (_I, [_P, _P, _U64]),
@@ -315,6 +316,11 @@ class HipBackend:
     def SetRelaxed(self, allow: bool):
         self.ctx.call("seeai_set_relaxed", int(bool(allow)))
 
+    def SetAttentionBf16(self, on: bool):
+        """Relaxed attention on bf16 operands (True) or f32 products (False,
+        the default)."""
+        self.ctx.call("seeai_set_attention_bf16", int(bool(on)))
+
     # host-sync verbs
     def Upload(self, offset: int, data: bytes):
         buf = C.create_string_buffer(bytes(data), max(len(data), 1))
@@ -468,6 +474,14 @@ class Engine:
         whole plan runs the exact family (source/plan/instruction.h:356-384)."""
         ctx = _lib.seeai_engine_context(self.h)
         rc = _lib.seeai_set_relaxed(ctx, int(bool(allow)))
+        if rc != OK:
+            raise BackendError(rc, _lib.seeai_last_error(ctx).decode("utf-8", "replace"))
+
+    def set_attention_bf16(self, on: bool):
+        """Relaxed attention on bf16 operands (True) or f32 products (False,
+        the default): HipBackend.SetAttentionBf16 underneath."""
+        ctx = _lib.seeai_engine_context(self.h)
+        rc = _lib.seeai_set_attention_bf16(ctx, int(bool(on)))
         if rc != OK:
             raise BackendError(rc, _lib.seeai_last_error(ctx).decode("utf-8", "replace"))
 

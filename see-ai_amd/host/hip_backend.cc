@@ -70,6 +70,8 @@ uint64_t HipBackend::relaxed_executions() const { return seeai_relaxed_execution
 
 void HipBackend::SetRelaxed(bool allow) { seeai_set_relaxed(ctx_, allow ? 1 : 0); }
 
+void HipBackend::SetAttentionBf16(bool on) { seeai_set_attention_bf16(ctx_, on ? 1 : 0); }
+
 Result<void> HipBackend::SyncToDevice(uint64_t offset, uint64_t bytes) {
   if (!host_ || offset > host_bytes_ || bytes > host_bytes_ - offset)
     return Fail("hip backend: sync range outside the bound arena");

@@ -66,6 +66,9 @@ class HipBackend {
   uint64_t relaxed_executions() const;
   uint64_t fused_dispatches() const;
   void SetRelaxed(bool allow);
+  // Relaxed tiled attention on bf16 operands (true) or f32 products (false,
+  // the default): seeai_set_attention_bf16.
+  void SetAttentionBf16(bool on);
 
   Result<void> SyncToDevice(uint64_t offset, uint64_t bytes);
   Result<void> SyncToHost(uint64_t offset, uint64_t bytes);

@@ -327,3 +327,35 @@ def test_plan_generator_matches_its_numpy_definition():
     l1, s1 = pw.quantize_cols(w)
     l2, s2 = pw.quantize_cols_numpy(w)
     assert np.array_equal(l1, l2) and np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+
+
+# --- the oracle's threads (the reference's "same bits, any thread count") -------------------------
+
+@pytest.mark.parametrize("which", ["c1", "dec", "dq8"])
+def test_oracle_threads_do_not_change_bits(hip, orc, which):
+    """Two training steps of each plan through the oracle at 1 and at 5
+    threads: the whole arena is the same bytes (chunks are the reference's
+    ParallelFor chunks; partials combine in chunk order)."""
+    if which == "c1":
+        img = pw.mlp_lora(hip.plan_self_hash)
+        batches = [(pw.normal(300 + s, (32, 256)), pw.uniform_ints(400 + s, 32, 256)) for s in range(2)]
+    else:
+        make = pw.decoder_lora if which == "dec" else pw.decoder_q8_lora
+        cfg = TINY if which == "dec" else TINY_Q8
+        img = make(hip.plan_self_hash, relaxed=False, **cfg)
+        T = cfg["batch"] * cfg["seq"]
+        batches = []
+        for s in range(2):
+            t = pw.uniform_ints(500 + s, T + 1, cfg["vocab"])
+            batches.append((t[:T].copy().view(np.float32), t[1:].copy()))
+    arenas = []
+    try:
+        for threads in (1, 5):
+            orc.set_threads(threads)
+            eng = OracleEngine(orc, img.blob)
+            for x, y in batches:
+                eng.train_step(x, y)
+            arenas.append(eng.arena.tobytes())
+    finally:
+        orc.set_threads(1)
+    assert arenas[0] == arenas[1]
