@@ -74,6 +74,7 @@ def lora_probe(which: str):
         img, T, n = pw.decoder_lora(hip.plan_self_hash, relaxed=True), 8 * 1024, 5
     print(f"lora probe {which}: plan built", flush=True)
     eng = hip.Engine(img.blob)
+    eng.set_attention_bf16(True)  # both configs train in bf16 activations
     del img
     tok = pw.uniform_ints(9, T + 1, 32000)
     eng.train_step(tok[:T].copy().view(np.float32), tok[1:].copy())
@@ -433,9 +434,12 @@ def lora_steps(torch, hip):
     tok = pw.uniform_ints(9, T + 1, 32000)
     eng.train_step(tok[:T].copy().view(np.float32), tok[1:].copy())
     flops = decoder_step_flops(12, 768, 3072, 32000, T, 8, 1024, 12)
+    # configs[3] trains in bf16 activations: relaxed attention on the bf16
+    # kernels; the exact leg runs every instruction in the exact family.
     for name, allow, n in [("lora_decoder_c4_relaxed", True, 10),
                            ("lora_decoder_c4_exact", False, 3)]:
         eng.set_relaxed(allow)
+        eng.set_attention_bf16(allow)
         dt, loss = steps_per_s(eng, n, 2)
         tf = flops / dt / 1e12
         out[name] = {"ms_per_step": round(dt * 1e3, 2), "tokens_s": round(T / dt),
@@ -458,6 +462,7 @@ def lora_steps(torch, hip):
     t0 = time.perf_counter()
     eng = hip.Engine(img.blob)
     load_s = time.perf_counter() - t0
+    eng.set_attention_bf16(True)  # configs[4]: bf16 activations
     del img
     T = 4 * 2048
     tok = pw.uniform_ints(10, T + 1, 32000)

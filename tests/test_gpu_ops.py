@@ -46,6 +46,14 @@ def backend(hip):
     return hip.HipBackend(0)
 
 
+@pytest.fixture
+def bf16_attention(backend):
+    """The backend's relaxed attention on bf16 operands for one test."""
+    backend.SetAttentionBf16(True)
+    yield
+    backend.SetAttentionBf16(False)
+
+
 def execute(hip, orc, backend, ar: Arena, program, params=PARAMS, expect_cpu=0):
     arena, ro = ar.images()
     cpu = arena.copy()
@@ -454,10 +462,14 @@ ATTN_SHAPES = [(1, 1, 1, 64), (2, 67, 2, 64), (1, 130, 3, 128), (2, 33, 2, 16), 
 
 @pytest.mark.parametrize("B,S,H,d", ATTN_SHAPES)
 @pytest.mark.parametrize("seg", [False, True])
-@pytest.mark.parametrize("relaxed", [False, True])
-def test_attention_tiled(hip, orc, backend, B, S, H, d, seg, relaxed):
+@pytest.mark.parametrize("mode", ["exact", "relaxed", "bf16"])
+def test_attention_tiled(hip, orc, backend, B, S, H, d, seg, mode):
+    """The tiled family against the oracle: exact (no flag) and relaxed (the
+    flag; f32 products, instruction.h:384-390) at 1e-5; relaxed with the
+    backend switched to bf16 attention at the bf16 bar 2e-2."""
     from tests.plan_ops import ins
-    if relaxed and B * H * S < 64:
+    relaxed = mode != "exact"
+    if mode == "bf16" and B * H * S < 64:
         # A bf16 dot of one row is measured against a one-element "tensor":
         # max-rel there is the relative error of a single cancelling dot,
         # which bf16 operands cannot hold to 2e-2.  The relaxed bar applies
@@ -484,8 +496,12 @@ def test_attention_tiled(hip, orc, backend, B, S, H, d, seg, relaxed):
     prog += [ins(48, [rq, rk, rv, rdo], [st, dq, geo], flags=flags),
              ins(49, [rq, rk, rv, rdo], [st, dk, geo], flags=flags),
              ins(50, [rq, rk, rv, rdo], [st, dv, geo], flags=flags)]
-    cpu, gpu = execute(hip, orc, backend, ar, prog)
-    tol = TOL_BF16 if relaxed and d in (64, 128) else TOL
+    backend.SetAttentionBf16(mode == "bf16")
+    try:
+        cpu, gpu = execute(hip, orc, backend, ar, prog)
+    finally:
+        backend.SetAttentionBf16(False)
+    tol = TOL_BF16 if mode == "bf16" and d in (64, 128) else TOL
     for name in ["o", "dq", "dk", "dv"]:
         e = maxrel(ar.get(gpu, name), ar.get(cpu, name))
         assert e <= tol, f"{name}: {e:.3g}"
@@ -496,26 +512,33 @@ def test_attention_tiled(hip, orc, backend, B, S, H, d, seg, relaxed):
         assert e <= tol, f"stats[{col}]: {e:.3g}"
 
 
-@pytest.mark.parametrize("scale", [2.0, 3.0, 6.0, 12.0])
+def _bf16_valued(x):
+    """x rounded to the nearest bf16 (ties to even), kept as f32."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("scale", [1.0, 2.0, 3.0, 6.0, 12.0])
 @pytest.mark.parametrize("d", [64, 128])
-def test_relaxed_attention_on_peaked_rows(hip, orc, backend, scale, d):
+@pytest.mark.parametrize("mode", ["relaxed", "bf16"])
+def test_relaxed_attention_on_peaked_rows(hip, orc, backend, scale, d, mode):
     """Scores of standard deviation `scale` (the BASELINE inputs give 1):
-    rows put more and more weight on one key, so dP - delta cancels and the
-    bf16 operands' rounding shows.  The relaxed dQ forms K^T (p dP) and
-    delta K^T p and subtracts, so its terms round relative to |dP| + |delta|
-    rather than |dP - delta|.
-    Measured on MI355X: every output holds 2e-2 up to scale 2; beyond it dK
-    and dV (which take dP - delta directly) pass 2e-2 first (scale 3: dK
-    2.2e-2, scale 12: 8e-2), the two-pass and one-pass dQ alike (scale 6:
-    1.3e-2 / 1.7e-2).  Asserted: the full bar at scale 2, and at every scale
-    the one-pass dQ is never the weakest of the gradients."""
+    rows put more and more weight on one key, so dP - delta cancels.
+    relaxed: kFlagRelaxed's own grant, f32 products with reordered sums
+    (instruction.h:384-390), held to 1e-4 at every scale.
+    bf16: the bf16-operand kernels on bf16-valued inputs (the models trained
+    in bf16 activations that switch them on), held to the bf16 bar 2e-2 on
+    every output at every scale."""
     from tests.plan_ops import ins
     B, S, H = 2, 300, 2
     r = rng(int(scale * 10) + d)
     shape = (B * S, H * d)
+    cast = _bf16_valued if mode == "bf16" else (lambda x: x)
     ar = Arena()
-    rq = ar.add("q", (r.standard_normal(shape) * scale).astype(np.float32))
-    rk, rv, rdo = (ar.add(n, r.standard_normal(shape).astype(np.float32)) for n in ("k", "v", "do"))
+    rq = ar.add("q", cast((r.standard_normal(shape) * scale).astype(np.float32)))
+    rk, rv, rdo = (ar.add(n, cast(r.standard_normal(shape).astype(np.float32)))
+                   for n in ("k", "v", "do"))
     o, st = ar.empty("o", shape), ar.empty("stats", (B * H * S, 4))
     dq, dk, dv = ar.empty("dq", shape), ar.empty("dk", shape), ar.empty("dv", shape)
     geo = (B << 48) | (S << 32) | (H << 16) | d
@@ -523,24 +546,28 @@ def test_relaxed_attention_on_peaked_rows(hip, orc, backend, scale, d):
             ins(48, [rq, rk, rv, rdo], [st, dq, geo], flags=32),
             ins(49, [rq, rk, rv, rdo], [st, dk, geo], flags=32),
             ins(50, [rq, rk, rv, rdo], [st, dv, geo], flags=32)]
-    cpu, gpu = execute(hip, orc, backend, ar, prog)
+    backend.SetAttentionBf16(mode == "bf16")
+    try:
+        cpu, gpu = execute(hip, orc, backend, ar, prog)
+    finally:
+        backend.SetAttentionBf16(False)
     errs = {name: maxrel(ar.get(gpu, name), ar.get(cpu, name)) for name in ["o", "dq", "dk", "dv"]}
     errs["delta"] = maxrel(ar.get(gpu, "stats")[:, 2], ar.get(cpu, "stats")[:, 2])
-    print(f"peaked scale={scale} d={d}: " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()))
-    if scale <= 2.0:
-        for name, e in errs.items():
-            assert e <= TOL_BF16, f"{name}: {e:.3g}"
-    assert errs["dq"] <= max(errs["dk"], errs["dv"], TOL_BF16), errs
+    print(f"peaked {mode} scale={scale} d={d}: " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()))
+    bar = TOL_BF16 if mode == "bf16" else 1e-4
+    for name, e in errs.items():
+        assert e <= bar, f"{name}: {e:.3g}"
 
 
 @pytest.mark.parametrize("B,S,H,d,seg", [(2, 67, 2, 64, False), (1, 512, 2, 64, True),
                                          (2, 300, 2, 64, False)])
 @pytest.mark.parametrize("order", ["dk_dv", "dv_dk"])
-def test_attention_backward_pair_fuses_bitwise(hip, orc, backend, B, S, H, d, seg, order):
+def test_attention_backward_pair_fuses_bitwise(hip, orc, backend, bf16_attention, B, S, H, d, seg,
+                                               order):
     """Adjacent relaxed kAttnDKTiled / kAttnDVTiled of one attention run as
-    one pass when a range shows the backend the program (ExecuteRange): the
-    arena bytes are those of the two instructions run one by one, and the
-    pass is counted as a fused dispatch."""
+    one pass on the bf16 kernels when a range shows the backend the program
+    (ExecuteRange): the arena bytes are those of the two instructions run
+    one by one, and the pass is counted as a fused dispatch."""
     from tests.plan_ops import ins
     r = rng(B * 7 + S + d)
     shape = (B * S, H * d)
@@ -577,7 +604,8 @@ def test_attention_backward_pair_fuses_bitwise(hip, orc, backend, B, S, H, d, se
         assert e <= TOL_BF16, f"{name}: {e:.3g}"
 
 
-def test_attention_backward_pair_refuses_to_fuse_over_a_reused_buffer(hip, orc, backend):
+def test_attention_backward_pair_refuses_to_fuse_over_a_reused_buffer(hip, orc, backend,
+                                                                      bf16_attention):
     """dV written over v, which only the dK before it reads: legal in the
     separate order, a race in one pass.  The range runs the two apart."""
     from tests.plan_ops import ins
@@ -1024,6 +1052,48 @@ def test_w8a8_bit_exact(hip, orc, torch_cuda, M, N, K):
     torch.cuda.synchronize()
     assert bits_equal(acc.cpu().numpy(), acc_c), "int32 accumulators (large kernels)"
     assert bits_equal(C.cpu().numpy(), C_c), "dequantized output (large kernels)"
+    ctx.close()
+
+
+@pytest.mark.parametrize("M", [4096, 32])
+def test_w8a8_at_the_bench_shapes(hip, orc, torch_cuda, M):
+    """BASELINE configs[1] itself under the built-in policy: M = 4096 (the
+    direct-to-LDS 256 x 256 kernel the bench times) and M = 32 (the decode
+    shape's skinny kernel), K = N = 4096.  Quantized operands, the int32
+    accumulators and C against the oracle bit for bit on 64 sampled rows
+    (every row at M = 32), all N columns."""
+    torch = torch_cuda
+    N = K = 4096
+    print(f"w8a8 bench shape M={M} N={N} K={K}", flush=True)
+    r = rng(M + 1)
+    X = r.standard_normal((M, K)).astype(np.float32)
+    W = (r.standard_normal((K, N)) * 0.02).astype(np.float32)
+    rows = np.arange(M) if M <= 64 else np.sort(r.choice(M, 64, replace=False))
+    rows[-1] = M - 1  # the last row of the last tile
+    QA_c, sa_c = orc.quantize_rows(X[rows])
+    QW_c, sw_c = orc.quantize_cols(W)
+    acc_c, C_c = orc.gemm_w8a8(QA_c, sa_c, QW_c, sw_c)
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    dX, dW = torch.from_numpy(X).cuda(), torch.from_numpy(W).cuda()
+    QA = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    sa = torch.empty(M, dtype=torch.float32, device="cuda")
+    QWt = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    sw = torch.empty(N, dtype=torch.float32, device="cuda")
+    C = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    acc = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    ctx.call("seeai_w8a8_quantize_rows", dX.data_ptr(), QA.data_ptr(), sa.data_ptr(), M, K)
+    ctx.call("seeai_w8a8_pack_weights", dW.data_ptr(), QWt.data_ptr(), sw.data_ptr(), K, N)
+    ctx.call("seeai_w8a8_gemm", QA.data_ptr(), sa.data_ptr(), QWt.data_ptr(), sw.data_ptr(),
+             C.data_ptr(), acc.data_ptr(), M, N, K)
+    torch.cuda.synchronize()
+    idx = torch.from_numpy(rows).cuda()
+    assert bits_equal(QA[idx].cpu().numpy(), QA_c) and bits_equal(sa[idx].cpu().numpy(), sa_c)
+    assert bits_equal(QWt.cpu().numpy(), np.ascontiguousarray(QW_c.T))
+    assert bits_equal(sw.cpu().numpy(), sw_c)
+    assert bits_equal(acc[idx].cpu().numpy(), acc_c), "int32 accumulators"
+    assert bits_equal(C[idx].cpu().numpy(), C_c), "dequantized output"
+    assert not torch.isnan(C).any().item(), "every output written"
     ctx.close()
 
 
