@@ -285,24 +285,105 @@ def main():
     return 0
 
 
+def host_threads():
+    """The host threads this process may use, capped at the 16 a one-GPU
+    box grants (its OMP_NUM_THREADS)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    cap = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(n, cap, 16))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(M, N, K):
-    """The oracle's W8A8 (quantize + int32 GEMM + dequant) on a row sample."""
+    """The reported CPU baseline: the oracle (the repository's C restatement
+    of the reference executor, bit-matched to it) on this host.  The W8A8
+    step (quantize + int32 GEMM + dequant) on a row sample at all threads
+    and at one; the config-1 train step; a config-3 slice at full widths.
+    Each measurement is a median of repeats after a warm-up.  The oracle's
+    chunks are the reference's ParallelFor chunks, so every thread count
+    computes the same bits."""
     import numpy as np
     from oracle.oracle import oracle
     orc = oracle()
-    rows = 1024
+    threads = host_threads()
     r = np.random.default_rng(1)
-    X = r.standard_normal((rows, K)).astype(np.float32)
+
+    def median_s(fn, reps):
+        fn()  # warm
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    out = {"kind": "port", "cores": threads, "host_threads_available": os.cpu_count(),
+           "cpu_model": cpu_model()}
+    # W8A8: weights packed once, outside the step, as on the GPU.
     W = (r.standard_normal((K, N)) * 0.02).astype(np.float32)
-    QW, sw = orc.quantize_cols(W)  # weights are packed once, outside the step
-    t0 = time.perf_counter()
-    QA, sa = orc.quantize_rows(X)
-    orc.gemm_w8a8(QA, sa, QW, sw)
-    dt = time.perf_counter() - t0
-    return {"value": round(2.0 * rows * N * K / dt / 1e12, 5), "unit": "TOPS", "cores": 1,
-            "kind": "port",
-            "sample": f"{rows} of the {M} activation rows (quantize + int32 GEMM + dequant "
-                      f"against all {N}x{K} weights), {dt:.2f} s on one host core"}
+    QW, sw = orc.quantize_cols(W)
+    w8 = {}
+    for th, rows, reps in [(threads, 1024, 3), (1, 256, 1)]:
+        X = r.standard_normal((rows, K)).astype(np.float32)
+        orc.set_threads(th)
+
+        def step(X=X):
+            QA, sa = orc.quantize_rows(X)
+            orc.gemm_w8a8(QA, sa, QW, sw)
+        dt = median_s(step, reps)
+        w8[th] = (2.0 * rows * N * K / dt / 1e12, rows, dt)
+    out.update({"value": round(w8[threads][0], 4), "unit": "TOPS",
+                "sample": f"W8A8 step on {w8[threads][1]} of the {M} activation rows (quantize + "
+                          f"int32 GEMM + dequant against all {N}x{K} weights), median of 3, "
+                          f"{threads} threads; CPU {out['cpu_model']}",
+                "one_thread": {"value": round(w8[1][0], 4), "unit": "TOPS",
+                               "sample": f"{w8[1][1]} rows, {w8[1][2]:.2f} s"}})
+    # Train steps through the oracle's instruction interpreter (the CPU
+    # executor's arithmetic and order).
+    from tests.engine_oracle import OracleEngine
+    pw = importlib.import_module("see-ai_amd.planwriter")
+    hip = importlib.import_module("see-ai_amd.hip")
+    steps = {}
+    img = pw.mlp_lora(hip.plan_self_hash)
+    x, y = pw.normal(1, (32, 256)), pw.uniform_ints(2, 32, 256)
+    for th in (threads, 1):
+        orc.set_threads(th)
+        eng = OracleEngine(orc, img.blob)
+        dt = median_s(lambda: eng.train_step(x, y), 5)
+        steps[f"c1_{th}t"] = {"ms_per_step": round(dt * 1e3, 3), "rows_s": round(32 / dt, 1),
+                              "threads": th}
+    # configs[3] at full widths, one block and one sequence (the whole step
+    # is 12 blocks x 8 sequences of 1024): tokens/s of the slice, all threads
+    # at S 1024, one thread at S 256.
+    for th, seq, reps in ((threads, 1024, 2), (1, 256, 1)):
+        cfg = dict(vocab=32000, dim=768, heads=12, ffn=3072, layers=1, seq=seq, batch=1, rank=8)
+        img = pw.decoder_lora(hip.plan_self_hash, relaxed=False, **cfg)
+        t = pw.uniform_ints(9, seq + 1, 32000)
+        xb, yb = t[:seq].copy().view(np.float32), t[1:].copy()
+        orc.set_threads(th)
+        eng = OracleEngine(orc, img.blob)
+        dt = median_s(lambda: eng.train_step(xb, yb), reps)
+        steps[f"c4_slice_{th}t"] = {
+            "s_per_step": round(dt, 3), "tokens_s": round(seq / dt, 1), "threads": th,
+            "sample": f"configs[3] widths (d768, 12 heads, FFN 3072, vocab 32000), 1 block, "
+                      f"B1 x S{seq}, exact family"}
+        del eng, img
+    orc.set_threads(1)
+    out["train_steps"] = steps
+    return out
 
 
 def extras(ctx, torch, hip):

@@ -65,11 +65,12 @@ typedef struct {
   orc_chunk_fn fn;
   void* ctx;
   size_t n, grain, count;
-  size_t next; /* the next chunk to take */
+  size_t next;   /* the next chunk to take */
+  int seats;     /* pool workers that may join this job */
+  int joined;    /* pool workers that tried to */
 } OrcWork;
 
-static void* orc_worker(void* arg) {
-  OrcWork* w = (OrcWork*)arg;
+static void orc_run_chunks(OrcWork* w) {
   for (;;) {
     const size_t c = __atomic_fetch_add(&w->next, 1, __ATOMIC_RELAXED);
     if (c >= w->count) break;
@@ -77,31 +78,71 @@ static void* orc_worker(void* arg) {
     const size_t e = b + w->grain < w->n ? b + w->grain : w->n;
     w->fn(w->ctx, b, e, c);
   }
+}
+
+/* A persistent pool (the reference keeps one too, parallel_for.h): workers
+ * sleep on `go`, each job is published with a generation number, and the
+ * caller works beside them and waits on `done` until every worker that
+ * woke for the job has left it. */
+static struct {
+  pthread_mutex_t mu;
+  pthread_cond_t go, done;
+  int workers;
+  unsigned long gen;
+  OrcWork* job;
+  int busy; /* workers still inside the current job */
+} g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER,
+            0, 0, NULL, 0};
+
+/* arg: the generation current when the worker was created; the job
+ * published right after it (generation + 1) is its first. */
+static void* orc_pool_worker(void* arg) {
+  unsigned long seen = (unsigned long)(uintptr_t)arg;
+  pthread_mutex_lock(&g_pool.mu);
+  for (;;) {
+    while (g_pool.gen == seen) pthread_cond_wait(&g_pool.go, &g_pool.mu);
+    seen = g_pool.gen;
+    OrcWork* w = g_pool.job;
+    pthread_mutex_unlock(&g_pool.mu);
+    if (__atomic_fetch_add(&w->joined, 1, __ATOMIC_RELAXED) < w->seats) orc_run_chunks(w);
+    pthread_mutex_lock(&g_pool.mu);
+    if (--g_pool.busy == 0) pthread_cond_signal(&g_pool.done);
+  }
   return NULL;
 }
 
-/* Runs fn over [0, n) in chunks of orc_chunk_grain(n, grain); returns the
- * chunk count. */
+/* Runs fn over [0, n) in chunks of orc_chunk_grain(n, grain) on the caller
+ * and up to orc_threads() - 1 pool workers; returns the chunk count.  Not
+ * reentrant: one job at a time (the oracle runs one instruction at a time). */
 static size_t orc_parallel(size_t n, size_t grain, orc_chunk_fn fn, void* ctx) {
   if (n == 0) return 0;
-  OrcWork w = {fn, ctx, n, orc_chunk_grain(n, grain), 0, 0};
+  OrcWork w = {fn, ctx, n, orc_chunk_grain(n, grain), 0, 0, 0, 0};
   w.count = (n + w.grain - 1) / w.grain;
   int t = orc_threads();
   if ((size_t)t > w.count) t = (int)w.count;
   if (t <= 1) {
-    orc_worker(&w);
+    orc_run_chunks(&w);
     return w.count;
   }
-  pthread_t ids[256];
-  if (t > 256) t = 256;
-  int started = 0;
-  for (; started < t - 1; ++started)
-    if (pthread_create(&ids[started], NULL, orc_worker, &w) != 0) break;
-  orc_worker(&w);
-  for (int i = 0; i < started; ++i) pthread_join(ids[i], NULL);
+  pthread_mutex_lock(&g_pool.mu);
+  while (g_pool.workers < t - 1 && g_pool.workers < 255) {
+    pthread_t id;
+    if (pthread_create(&id, NULL, orc_pool_worker, (void*)(uintptr_t)g_pool.gen) != 0) break;
+    pthread_detach(id);
+    ++g_pool.workers;
+  }
+  w.seats = t - 1;
+  g_pool.job = &w;
+  g_pool.busy = g_pool.workers;
+  ++g_pool.gen;
+  pthread_cond_broadcast(&g_pool.go);
+  pthread_mutex_unlock(&g_pool.mu);
+  orc_run_chunks(&w);
+  pthread_mutex_lock(&g_pool.mu);
+  while (g_pool.busy > 0) pthread_cond_wait(&g_pool.done, &g_pool.mu);
+  pthread_mutex_unlock(&g_pool.mu);
   return w.count;
 }
-
 /* kernel_policy.h:122-136: the shared activation expressions. */
 static const float kGeluC = 0.7978845608028654f;
 static const float kGeluA = 0.044715f;
