@@ -200,6 +200,25 @@ int seeai_attn_fwd(seeai_ctx* ctx, int dtype, const float* d_q,
                    const float* d_k, const float* d_v, float* d_o,
                    float* d_stats, uint64_t B, uint64_t S, uint64_t H,
                    uint64_t d, const int32_t* d_starts);
+/* The tiled forward on bf16 operands held in HBM as bf16 ([B*S, H*64],
+ * head width 64): O (f32) and the stats row as seeai_attn_fwd.  Staged
+ * straight into LDS, 32 queries per wave; results within the bf16 bar of
+ * the exact family on the same (bf16-valued) inputs. */
+int seeai_attn_fwd_bf16(seeai_ctx* ctx, const uint16_t* d_q, const uint16_t* d_k,
+                        const uint16_t* d_v, float* d_o, float* d_stats, uint64_t B,
+                        uint64_t S, uint64_t H, uint64_t d, const int32_t* d_starts);
+/* dQ and the stats row's delta, then dK and dV, on the same bf16 operands
+ * (dout bf16 too) and the forward's stats rows: AttnDQTiled and the fused
+ * AttnDKTiled + AttnDVTiled pair (attention.cc:494-590) with bf16 in HBM.
+ * dQ, dK, dV are f32 [B*S, H*64]; in seeai_attn_dkdv_bf16 one of d_dk, d_dv
+ * may be NULL. */
+int seeai_attn_dq_bf16(seeai_ctx* ctx, const uint16_t* d_q, const uint16_t* d_k,
+                       const uint16_t* d_v, const uint16_t* d_dout, float* d_stats,
+                       float* d_dq, uint64_t B, uint64_t S, uint64_t H, uint64_t d);
+int seeai_attn_dkdv_bf16(seeai_ctx* ctx, const uint16_t* d_q, const uint16_t* d_k,
+                         const uint16_t* d_v, const uint16_t* d_dout, const float* d_stats,
+                         float* d_dk, float* d_dv, uint64_t B, uint64_t S, uint64_t H,
+                         uint64_t d);
 int seeai_attn_dq(seeai_ctx* ctx, int dtype, const float* d_q,
                   const float* d_k, const float* d_v, const float* d_dout,
                   float* d_stats, float* d_dq, uint64_t B, uint64_t S,

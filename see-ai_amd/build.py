@@ -10,7 +10,7 @@ Flags:
                       keeps the compiler from forming packed-f32 VALU ops
                       (this pool's rule; the host pass warns it does not know
                       the feature, which is harmless)
-  -mllvm -amdgpu-mfma-vgpr-form  (k_flash.hip only)
+  -mllvm -amdgpu-mfma-vgpr-form  (k_flash.hip, k_attn16.hip)
                       MFMA accumulators in VGPRs: the attention kernels run
                       VALU softmax on every score tile, and AGPR-resident
                       tiles cost a copy per element each way
@@ -40,7 +40,8 @@ COMMON = [
 ]
 
 
-PER_FILE = {"k_flash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+PER_FILE = {"k_flash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+            "k_attn16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 # The host layer above the C ABI (plan reader, backend, engine): C++20,

@@ -1446,6 +1446,38 @@ int seeai_attn_fwd(seeai_ctx* c, int dtype, const float* q, const float* k, cons
   SEEAI_TRY(c, LaunchAttnFwdTiled(dtype, q, k, v, o, stats, B, S, H, d, starts, c->stream), "attn_fwd");
   return SEEAI_OK;
 }
+int seeai_attn_fwd_bf16(seeai_ctx* c, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        float* o, float* stats, uint64_t B, uint64_t S, uint64_t H, uint64_t d,
+                        const int32_t* starts) {
+  if (!c) return SEEAI_INVALID;
+  if (!Attn16Fits(B, S, H, d))
+    return Fail(c, SEEAI_INVALID, "attn_fwd_bf16: head width %llu (64 only) or slice too large",
+                static_cast<unsigned long long>(d));
+  SEEAI_TRY(c, LaunchAttn16Fwd(q, k, v, o, stats, B, S, H, starts, c->stream), "attn_fwd_bf16");
+  return SEEAI_OK;
+}
+int seeai_attn_dq_bf16(seeai_ctx* c, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                       const uint16_t* dout, float* stats, float* dq, uint64_t B, uint64_t S,
+                       uint64_t H, uint64_t d) {
+  if (!c) return SEEAI_INVALID;
+  if (!Attn16Fits(B, S, H, d))
+    return Fail(c, SEEAI_INVALID, "attn_dq_bf16: head width %llu (64 only) or slice too large",
+                static_cast<unsigned long long>(d));
+  SEEAI_TRY(c, LaunchAttn16DQ(q, k, v, dout, stats, dq, B, S, H, c->stream), "attn_dq_bf16");
+  return SEEAI_OK;
+}
+int seeai_attn_dkdv_bf16(seeai_ctx* c, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         const uint16_t* dout, const float* stats, float* dk, float* dv,
+                         uint64_t B, uint64_t S, uint64_t H, uint64_t d) {
+  if (!c) return SEEAI_INVALID;
+  if (!Attn16Fits(B, S, H, d) || (!dk && !dv))
+    return Fail(c, SEEAI_INVALID,
+                "attn_dkdv_bf16: head width %llu (64 only), slice too large or no output",
+                static_cast<unsigned long long>(d));
+  SEEAI_TRY(c, LaunchAttn16DKDV(q, k, v, dout, stats, dk, dv, B, S, H, c->stream),
+            "attn_dkdv_bf16");
+  return SEEAI_OK;
+}
 int seeai_attn_dq(seeai_ctx* c, int dtype, const float* q, const float* k, const float* v,
                   const float* dout, float* stats, float* dq, uint64_t B, uint64_t S, uint64_t H,
                   uint64_t d) {

@@ -328,6 +328,17 @@ hipError_t LaunchAttnDKDVFused(const float* q, const float* k, const float* v, c
 // LaunchFlashDKDV one or both of dk, dv are non-null; both only where
 // FlashFusedDKDV(d).
 bool FlashFits(size_t B, size_t S, size_t H, size_t d);
+// Head width 64 on bf16 operands in HBM (k_attn16.hip).
+bool Attn16Fits(size_t B, size_t S, size_t H, size_t d);
+hipError_t LaunchAttn16Fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, float* o,
+                           float* stats, size_t B, size_t S, size_t H, const int32_t* starts,
+                           hipStream_t s);
+hipError_t LaunchAttn16DQ(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                          const uint16_t* dout, float* stats, float* dq, size_t B, size_t S,
+                          size_t H, hipStream_t s);
+hipError_t LaunchAttn16DKDV(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            const uint16_t* dout, const float* stats, float* dk, float* dv,
+                            size_t B, size_t S, size_t H, hipStream_t s);
 bool FlashFusedDKDV(size_t d);
 hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float* o, float* stats,
                           size_t B, size_t S, size_t H, size_t d, const int32_t* starts,

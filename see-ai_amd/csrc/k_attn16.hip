@@ -1,0 +1,753 @@
+// k_attn16.hip -- causal attention at head width 64 on bf16 operands held in
+// HBM as bf16: forward, dQ and dK / dV over the tiled family's stats-row
+// contract (instruction.h:174-190, 234-259), for the models that train in
+// bf16 activations (BASELINE configs[2] bf16, [3], [4]).
+//
+// Staging.  Every tile that enters a product is a 64-row block of one
+// (b, h) slice -- 64 rows x 64 dims of bf16 -- copied from HBM straight into
+// LDS by buffer_load ... lds (no registers, no conversion).  A tile is two
+// halves (dims 0-31, 32-63) of 64-byte rows; chunk c (16 bytes) of row r
+// sits at physical chunk (c + r / 4) mod 4, which keeps the MFMA fragment
+// reads free of bank conflicts (the W8A8 kernel's measured rotation).  Rows
+// past the sequence end read as zeros through the buffer range check.
+//
+// Products.  v_mfma_f32_32x32x16_bf16 with the scores formed transposed
+// (S^T = K Q^T): the accumulator layout -- lane (g = lane / 32, c = lane %
+// 32) holding rows 8q + 4g + e of column c -- is then the B operand of the
+// next product, so probabilities never leave registers.  Operands whose
+// reduction index runs down a tile's rows (V^T in O^T = V^T P^T, K^T in
+// dQ^T = K^T dS^T, Q^T and dO^T in dK^T / dV^T) are read with gfx950's
+// ds_read_b64_tr_b16, which hands each lane one column of a 4 x 16 block
+// gathered from its 16-lane group: no transposed copies.
+//
+// Every output element has one writer; no atomics; the reductions run in a
+// fixed order, so results repeat bit for bit.
+#include "common.h"
+
+namespace seeai {
+namespace {
+
+constexpr int kD = 64;          // head width
+constexpr int kBlkRows = 64;    // rows of a staged tile
+constexpr int kTile = kBlkRows * kD * 2;  // bytes of one staged tile (8 KiB)
+constexpr int kHalf = kTile / 2;          // one 64-byte-row half
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit format, range-checked
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void* LdsPtr;
+typedef __attribute__((address_space(3))) bf16x4* LdsBf16x4;
+
+__device__ __forceinline__ float Exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ v16f Mfma(const bf16x8& a, const bf16x8& b, const v16f& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ int Phys(int row, int chunk) { return (chunk + row / 4) & 3; }
+
+// s_waitcnt vmcnt(n), the other counters left alone.
+template <int n>
+__device__ __forceinline__ void WaitVm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+// The (b, h) slice of a [B*S, H*64] bf16 tensor as a buffer resource whose
+// first record is row `row0`; rows at or past S are out of range (zeros).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t SliceRsrc(const uint16_t* slice, int ld, int S,
+                                                            int row0) {
+  const int rows = S - row0;
+  const int bytes = rows > 0 ? ((rows - 1) * ld + kD) * 2 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(slice) +
+                                               static_cast<size_t>(row0) * ld,
+                                           0, Uniform(bytes), kRsrcWord3);
+}
+
+// One wave-load of a tile: 16 rows x 64 bytes of one half, lane l filling
+// row r0 + l / 4, physical chunk l % 4.  `u` = half * 4 + row group.
+__device__ __forceinline__ int TileLoadOffset(int u, int lane, int ld) {
+  const int half = u / 4, row = (u % 4) * 16 + lane / 4;
+  const int c = (lane % 4 - row / 4) & 3;
+  return row * ld * 2 + half * 64 + c * 16;
+}
+__device__ __forceinline__ void TileLoad(__amdgpu_buffer_rsrc_t rs, uint8_t* tile, int u,
+                                         int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LdsPtr)(tile + (u / 4) * kHalf + (u % 4) * 1024),
+                                           16, voff, 0, 0, 0);
+}
+
+// Per-lane byte offsets of the two fragment kinds within a tile.  The
+// swizzle's phase repeats every 16 rows, so a fragment 16 k rows further
+// down (or 32 rows, for the row kind) is the same offset plus a constant:
+// the offsets are computed once and the rest folds into the read's
+// immediate.
+struct FragOffsets {
+  int row[2];  // row kind, k-step parity 0 / 1
+  int col[2];  // column kind, lo / hi quads
+};
+__device__ __forceinline__ FragOffsets MakeFragOffsets(int lane) {
+  FragOffsets f;
+  const int r = lane % 32, g = lane / 32;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) f.row[p] = r * 64 + Phys(r, 2 * p + g) * 16;
+  const int grp = lane / 16, j = lane % 16;
+  const int row = 4 * (grp / 2) + j / 4;
+  const int byte = 32 * (grp % 2) + 8 * (j % 4);  // within the 64-byte half row
+  const int chunk = byte / 16, in = byte % 16;
+  f.col[0] = row * 64 + Phys(row, chunk) * 16 + in;
+  f.col[1] = (row + 8) * 64 + Phys(row + 8, chunk) * 16 + in;
+  return f;
+}
+
+// A fragment with the reduction along the tile's columns: lane (g, c) gets
+// row `row0 + c` dims 16 s + 8 g .. + 8 (k-step s of the 64 dims); row0 a
+// multiple of 32.
+__device__ __forceinline__ bf16x8 RowFrag(const uint8_t* tile, const FragOffsets& f, int row0,
+                                          int s) {
+  return *reinterpret_cast<const bf16x8*>(tile + (s / 2) * kHalf + row0 * 64 + f.row[s % 2]);
+}
+
+// A fragment with the reduction down the tile's rows: lane (g, c) gets
+// column `32 dt + c` at rows k0 + 4 g + {0..3} (elements 0-3) and
+// k0 + 8 + 4 g + {0..3} (elements 4-7) -- the k order PackTile gives the
+// register operand it meets; k0 a multiple of 16.  Two transpose reads of
+// 4 rows x 16 columns per 16-lane group: lane 16 G + j points at row
+// k0 + 4 (G / 2) + j / 4, columns 32 dt + 16 (G % 2) + 4 (j % 4) .. + 4, and
+// receives column 32 dt + 16 (G % 2) + j of the group's four rows.
+__device__ __forceinline__ bf16x8 ColFrag(const uint8_t* tile, const FragOffsets& f, int dt,
+                                          int k0) {
+  const uint8_t* base = tile + dt * kHalf + k0 * 64;
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LdsBf16x4)(base + f.col[0]));
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LdsBf16x4)(base + f.col[1]));
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// A 32 x 32 score tile's 16 values in this lane (rows 8q + 4g + e in
+// w[4q + e]) as the two B operands of a 16-row-step product over those rows:
+// out[h] holds rows 16h + 4g + {0..3} and 16h + 8 + 4g + {0..3}.
+__device__ __forceinline__ void PackTile(const float* w, bf16x8* out) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    out[h] = bf16x8{static_cast<__bf16>(w[8 * h + 0]), static_cast<__bf16>(w[8 * h + 1]),
+                    static_cast<__bf16>(w[8 * h + 2]), static_cast<__bf16>(w[8 * h + 3]),
+                    static_cast<__bf16>(w[8 * h + 4]), static_cast<__bf16>(w[8 * h + 5]),
+                    static_cast<__bf16>(w[8 * h + 6]), static_cast<__bf16>(w[8 * h + 7])};
+}
+
+// Lane (g, c)'s 8 dims 16 s + 8 g .. + 8 of one bf16 row, from HBM.
+__device__ __forceinline__ bf16x8 OwnedFrag(const uint16_t* row, int s, int lane) {
+  return *reinterpret_cast<const bf16x8*>(row + 16 * s + 8 * (lane / 32));
+}
+
+__device__ __forceinline__ float SwapMax(float v) { return fmaxf(v, __shfl_xor(v, 32, kWave)); }
+__device__ __forceinline__ float SwapSum(float v) { return v + __shfl_xor(v, 32, kWave); }
+__device__ __forceinline__ int WaveMaxI(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
+  return __builtin_amdgcn_readfirstlane(v);
+}
+__device__ __forceinline__ int WaveMinI(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
+  return __builtin_amdgcn_readfirstlane(v);
+}
+// all ones when a < 0 or b < 0
+__device__ __forceinline__ int Outside(int a, int b) { return (a | b) >> 31; }
+__device__ __forceinline__ float OrNegInf(float x, int bad) {
+  return __int_as_float((__float_as_int(x) & ~bad) | (static_cast<int>(0xff800000u) & bad));
+}
+__device__ __forceinline__ float OrZero(float x, int bad) { return __int_as_float(__float_as_int(x) & ~bad); }
+// Row r (0..15) of a lane's accumulator within its 32-row tile, less 4 g.
+__device__ __forceinline__ constexpr int RowConst(int r) { return 8 * (r / 4) + (r % 4); }
+
+// Work unit: (bh, rank), rank 0 the heaviest of the nb row blocks of one
+// (b, h); consecutive workgroup ids go to the 8 XCDs in turn, so ids are
+// regrouped to give each XCD whole (b, h) slices, heavy blocks first.
+__device__ __forceinline__ void UnitOf(int nb, int& bh, int& rank) {
+  const int w = blockIdx.x, total = gridDim.x;
+  const int t = total % 8 == 0 ? (w % 8) * (total / 8) + w / 8 : w;
+  bh = t / nb;
+  rank = t % nb;
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  A workgroup of kFwdWaves waves owns kFwdWaves * 32 * QT queries
+// of one (b, h); each wave QT 32-query tiles, so every K and V fragment read
+// from LDS feeds QT MFMAs.  The launch takes QT = 1, four waves, four
+// workgroups per CU: occupancy, which hides the softmax behind the other
+// waves' products, measured ahead of fragment reuse.  Keys stream in 64-row
+// blocks, kFwdStages buffers of K and V in flight.  The scores arrive as q.k; t = q.k * log2(e)/sqrt(d) - m_use
+// (one FMA) is the base-2 exponent of the weight.  m_use moves only when a
+// key tile's maximum passes it by more than 2^8, or on the first tile a
+// query sees; the true maximum is kept beside it and the stats row (m, 1/l)
+// is stated against it.  l sums the bf16-rounded weights that enter P V.
+// ---------------------------------------------------------------------------
+constexpr float kLazy = 8.0f;
+
+template <int QT, int kFwdStages, int kFwdWaves, int kMinBlocks>
+__global__ void __launch_bounds__(kFwdWaves * kWave, kMinBlocks)
+Attn16Fwd(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+          const uint16_t* __restrict__ v, float* __restrict__ o, float* __restrict__ stats, int S,
+          int H, const int32_t* __restrict__ starts) {
+  constexpr int kFwdRows = kFwdWaves * 32 * QT;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kFwdStages * 2 * kTile];
+  __shared__ int wave_lo[kFwdWaves];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / 32, c = lane % 32;
+  const int nq = (S + kFwdRows - 1) / kFwdRows;
+  int bh, rank;
+  UnitOf(nq, bh, rank);
+  const int qblk = nq - 1 - rank;
+  const int b = bh / H, h = bh % H;
+  const int ld = H * kD;
+  const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * kD;
+  const int qw = qblk * kFwdRows + wave * 32 * QT;  // this wave's first query
+  int iq[QT], jstart[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    iq[t] = qw + 32 * t + c;
+    const int ic = min(iq[t], S - 1);
+    int s0 = 0;
+    if (starts) {
+      const int v0 = starts[static_cast<size_t>(b) * S + ic];
+      s0 = v0 <= 0 ? 0 : min(v0, ic);
+    }
+    jstart[t] = s0;
+  }
+  int js_lo = jstart[0], js_hi = jstart[0];
+#pragma unroll
+  for (int t = 1; t < QT; ++t) js_lo = min(js_lo, jstart[t]), js_hi = max(js_hi, jstart[t]);
+  const int w_lo = WaveMinI(js_lo);
+  const int w_hi_start = WaveMaxI(js_hi);
+  if (lane == 0) wave_lo[wave] = w_lo;
+  __syncthreads();
+  int lo = wave_lo[0];
+#pragma unroll
+  for (int w = 1; w < kFwdWaves; ++w) lo = min(lo, wave_lo[w]);
+  const int blk_lo = Uniform(lo) / kBlkRows;
+  const int q_hi = min(qblk * kFwdRows + kFwdRows - 1, S - 1);
+  const int nblk = q_hi / kBlkRows + 1 - blk_lo;
+
+  bf16x8 qf[QT][4];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const uint16_t* row = q + base + static_cast<size_t>(min(iq[t], S - 1)) * ld;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[t][s] = OwnedFrag(row, s, lane);
+  }
+  const float scl = kLog2e * 0.125f;  // log2(e) / sqrt(64)
+
+  // Loads: per stage 16 wave-loads (K then V, 2 halves x 4 row groups); wave
+  // w takes u = kFwdWaves j + w.
+  constexpr int kLoadsPerWave = 16 / kFwdWaves;
+  int voff[kLoadsPerWave];
+#pragma unroll
+  for (int j = 0; j < kLoadsPerWave; ++j)
+    voff[j] = TileLoadOffset((kFwdWaves * j + wave) % 8, lane, ld);
+  auto issue = [&](int jb, int buf) {
+    const int j0 = (blk_lo + jb) * kBlkRows;
+    const __amdgpu_buffer_rsrc_t rk = SliceRsrc(k + base, ld, S, j0);
+    const __amdgpu_buffer_rsrc_t rv = SliceRsrc(v + base, ld, S, j0);
+    uint8_t* st = smem + buf * 2 * kTile;
+#pragma unroll
+    for (int j = 0; j < kLoadsPerWave; ++j) {
+      const int u = kFwdWaves * j + wave;
+      if (u < 8)
+        TileLoad(rk, st, u, voff[j]);
+      else
+        TileLoad(rv, st + kTile, u - 8, voff[j]);
+    }
+  };
+
+  const FragOffsets fo = MakeFragOffsets(lane);
+  v16f oacc[2][QT] = {};  // [dt][t]
+  float m_use[QT], m_true[QT], l[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) m_use[t] = 0.0f, m_true[t] = -INFINITY, l[t] = 0.0f;
+  const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+
+  // A 32-key tile kt of the block in buffer `st`: its scores (S^T = K Q^T,
+  // eight MFMAs), their softmax (VALU), and O^T += V^T P^T (eight MFMAs).
+  // The loop below orders them so the next tile's score MFMAs are in
+  // flight while this tile's softmax runs, and this tile's accumulation
+  // while the next tile's softmax runs.
+  auto key_tile = [&](auto masked, const uint8_t* kt_tile, const uint8_t* vt_tile, int kt,
+                      int jt) {
+    constexpr bool kMask = decltype(masked)::value;
+    v16f sc[QT] = {};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const bf16x8 kf = RowFrag(kt_tile, fo, 32 * kt, s);
+#pragma unroll
+      for (int t = 0; t < QT; ++t) sc[t] = Mfma(kf, qf[t][s], sc[t]);
+    }
+    bf16x8 pb[QT][2];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      float bmax = -INFINITY;
+      const int hi_rel = iq[t] - jt - 4 * g;
+      const int lo_rel = jstart[t] - jt - 4 * g;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = __builtin_fmaf(sc[t][r], scl, -m_use[t]);
+        if constexpr (kMask)  // keep key jt + row in [jstart, i]
+          x = OrNegInf(x, Outside(hi_rel - RowConst(r), RowConst(r) - lo_rel));
+        sc[t][r] = x;
+        bmax = fmaxf(bmax, x);
+      }
+      bmax = SwapMax(bmax);  // relative to m_use
+      const bool first = m_true[t] == -INFINITY;
+      if (bmax != -INFINITY) m_true[t] = fmaxf(m_true[t], m_use[t] + bmax);
+      const bool need = first ? bmax != -INFINITY : bmax > kLazy;
+      if (__any(need)) {
+        const float shift = need ? bmax : 0.0f;
+        const float alpha = first ? 0.0f : Exp2(-shift);
+        m_use[t] += shift;
+        l[t] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) oacc[dt][t] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[t][r] -= shift;
+      }
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = Exp2(sc[t][r]);
+      PackTile(p, pb[t]);
+      float psum = 0.0f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          psum = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pb[t][hh][2 * e], pb[t][hh][2 * e + 1]},
+                                                 ones, psum, false);
+      l[t] += SwapSum(psum);
+    }
+    // O^T += V^T P^T over the tile's 32 keys (two 16-key steps).
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const bf16x8 vf = ColFrag(vt_tile, fo, dt, 32 * kt + 16 * hh);
+#pragma unroll
+        for (int t = 0; t < QT; ++t) oacc[dt][t] = Mfma(vf, pb[t][hh], oacc[dt][t]);
+      }
+  };
+
+  // Prologue: kStages - 1 blocks in flight (past the last, the last repeats:
+  // in bounds, into a buffer no later block reads).
+  const int last = nblk - 1;
+#pragma unroll
+  for (int s = 0; s < kFwdStages - 1; ++s) issue(min(s, last), s);
+  const int qmin = qw, qmax = qw + 32 * QT - 1;
+  for (int jb = 0; jb < nblk; ++jb) {
+    WaitVm<(kFwdStages - 2) * kLoadsPerWave>();  // this block's loads have landed
+    __syncthreads();                 // ... in every wave, and block jb - 1's buffer is free
+    issue(min(jb + kFwdStages - 1, last), (jb + kFwdStages - 1) % kFwdStages);
+    const uint8_t* st = smem + (jb % kFwdStages) * 2 * kTile;
+    const int j0 = (blk_lo + jb) * kBlkRows;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int jt = j0 + 32 * kt;
+      if (jt > qmax) continue;  // keys wholly after this wave's queries
+      if (jt + 31 <= qmin && jt >= w_hi_start)
+        key_tile(std::false_type{}, st, st + kTile, kt, jt);
+      else
+        key_tile(std::true_type{}, st, st + kTile, kt, jt);
+    }
+  }
+  WaitVm<0>();  // the repeated tail loads have landed before the workgroup ends
+
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int i = iq[t];
+    if (i >= S) continue;
+    const float inv = 1.0f / l[t];
+    float* orow = o + base + static_cast<size_t>(i) * ld;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq)
+        *reinterpret_cast<float4*>(orow + dt * 32 + 8 * qq + 4 * g) =
+            make_float4(oacc[dt][t][4 * qq] * inv, oacc[dt][t][4 * qq + 1] * inv,
+                        oacc[dt][t][4 * qq + 2] * inv, oacc[dt][t][4 * qq + 3] * inv);
+    if (g == 0) {
+      float* sr = stats + (static_cast<size_t>(bh) * S + i) * 4;
+      sr[0] = m_true[t] * kLn2;
+      sr[1] = inv * Exp2(m_true[t] - m_use[t]);
+      sr[2] = 0.0f;
+      sr[3] = static_cast<float>(jstart[t]);
+    }
+  }
+}
+
+// Row offset of the base-2 exponent: p = 2^(s c - mm) with c = log2(e)/8
+// and mm = m log2(e) + log2(l), from the stats row (m, 1/l).
+__device__ __forceinline__ float RowOffset(float m, float inv) { return m * kLog2e - log2f(inv); }
+
+// Stats start column: the document start stored as a float (instruction.h:
+// 246-250), clamped to the row.
+__device__ __forceinline__ int StatsStart(float stored, int i) {
+  if (!(stored > 0.0f)) return 0;
+  const float cap = static_cast<float>(i);
+  return stored >= cap ? i : static_cast<int>(stored);
+}
+
+// ---------------------------------------------------------------------------
+// dQ and the stats row's delta = sum_j p dP, in one walk over K / V: with
+// dS = p (dP - delta) linear in delta,
+//   dQ^T = K^T (p dP)^T - delta K^T p^T,
+// and delta accumulates beside the two products (four per tile -- S^T,
+// dP^T and the two accumulations -- one exponential per score).  Four waves
+// of 32 queries; K and V blocks staged as in the forward, K^T read by
+// transpose reads.  dQ is scaled by 1/sqrt(d) once, at the end.
+// ---------------------------------------------------------------------------
+constexpr int kBwdWaves = 4;
+constexpr int kBwdRows = kBwdWaves * 32;
+
+template <int kMinBlocks>
+__global__ void __launch_bounds__(kBwdWaves * kWave, kMinBlocks)
+Attn16DQ(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+         const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
+         float* __restrict__ stats, float* __restrict__ dq, int S, int H) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * kTile];
+  __shared__ int wave_lo[kBwdWaves];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / 32;
+  const int nq = (S + kBwdRows - 1) / kBwdRows;
+  int bh, rank;
+  UnitOf(nq, bh, rank);
+  const int qblk = nq - 1 - rank;
+  const int b = bh / H, h = bh % H;
+  const int ld = H * kD;
+  const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * kD;
+  const int qw = qblk * kBwdRows + wave * 32;
+  const int i = qw + lane % 32;
+  const int ic = min(i, S - 1);
+  float* st = stats + (static_cast<size_t>(bh) * S + ic) * 4;
+  const float4 st4 = *reinterpret_cast<const float4*>(st);
+  const float mm = RowOffset(st4.x, st4.y);
+  const int jstart = StatsStart(st4.w, ic);
+  const int w_hi_start = WaveMaxI(jstart);
+  if (lane == 0) wave_lo[wave] = WaveMinI(jstart);
+  __syncthreads();
+  int lo = wave_lo[0];
+#pragma unroll
+  for (int w = 1; w < kBwdWaves; ++w) lo = min(lo, wave_lo[w]);
+  const int blk_lo = Uniform(lo) / kBlkRows;
+  const int q_hi = min(qblk * kBwdRows + kBwdRows - 1, S - 1);
+  const int nblk = q_hi / kBlkRows + 1 - blk_lo;
+  const float scl = kLog2e * 0.125f;
+
+  bf16x8 qf[4], df[4];
+  {
+    const uint16_t* qrow = q + base + static_cast<size_t>(ic) * ld;
+    const uint16_t* drow = dout + base + static_cast<size_t>(ic) * ld;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = OwnedFrag(qrow, s, lane), df[s] = OwnedFrag(drow, s, lane);
+  }
+  int voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) voff[j] = TileLoadOffset((4 * j + wave) % 8, lane, ld);
+  auto issue = [&](int jb, int buf) {
+    const int j0 = (blk_lo + jb) * kBlkRows;
+    const __amdgpu_buffer_rsrc_t rk = SliceRsrc(k + base, ld, S, j0);
+    const __amdgpu_buffer_rsrc_t rv = SliceRsrc(v + base, ld, S, j0);
+    uint8_t* sb = smem + buf * 2 * kTile;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int u = 4 * j + wave;
+      if (u < 8)
+        TileLoad(rk, sb, u, voff[j]);
+      else
+        TileLoad(rv, sb + kTile, u - 8, voff[j]);
+    }
+  };
+  const FragOffsets fo = MakeFragOffsets(lane);
+  v16f acc[2] = {}, acc_p[2] = {};  // [dt]
+  float delta = 0.0f;
+
+  auto key_tile = [&](auto masked, const uint8_t* ktile, const uint8_t* vtile, int kt, int jt) {
+    constexpr bool kMask = decltype(masked)::value;
+    v16f sc = {}, dp = {};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      sc = Mfma(RowFrag(ktile, fo, 32 * kt, s), qf[s], sc);
+      dp = Mfma(RowFrag(vtile, fo, 32 * kt, s), df[s], dp);
+    }
+    const int hi_rel = i - jt - 4 * g, lo_rel = jstart - jt - 4 * g;
+    float w[16], p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float e = Exp2(__builtin_fmaf(sc[r], scl, -mm));
+      if constexpr (kMask)  // keep key jt + row in [jstart, i]
+        e = OrZero(e, Outside(hi_rel - RowConst(r), RowConst(r) - lo_rel));
+      delta = __builtin_fmaf(dp[r], e, delta);
+      w[r] = e * dp[r];
+      p[r] = e;
+    }
+    bf16x8 wb[2], pb[2];
+    PackTile(w, wb);
+    PackTile(p, pb);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const bf16x8 kf = ColFrag(ktile, fo, dt, 32 * kt + 16 * hh);
+        acc[dt] = Mfma(kf, wb[hh], acc[dt]);
+        acc_p[dt] = Mfma(kf, pb[hh], acc_p[dt]);
+      }
+  };
+
+  issue(0, 0);
+  const int qmin = qw, qmax = qw + 31;
+  for (int jb = 0; jb < nblk; ++jb) {
+    WaitVm<0>();
+    __syncthreads();
+    if (jb + 1 < nblk) issue(jb + 1, (jb + 1) & 1);
+    const uint8_t* sb = smem + (jb & 1) * 2 * kTile;
+    const int j0 = (blk_lo + jb) * kBlkRows;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int jt = j0 + 32 * kt;
+      if (jt > qmax) continue;
+      if (jt + 31 <= qmin && jt >= w_hi_start)
+        key_tile(std::false_type{}, sb, sb + kTile, kt, jt);
+      else
+        key_tile(std::true_type{}, sb, sb + kTile, kt, jt);
+    }
+  }
+  delta = SwapSum(delta);
+  if (i >= S) return;
+  const float isd = 0.125f;
+  float* drow = dq + base + static_cast<size_t>(i) * ld;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+    const v16f r = acc[dt] - delta * acc_p[dt];
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+      *reinterpret_cast<float4*>(drow + dt * 32 + 8 * qq + 4 * g) =
+          make_float4(r[4 * qq] * isd, r[4 * qq + 1] * isd, r[4 * qq + 2] * isd,
+                      r[4 * qq + 3] * isd);
+  }
+  if (g == 0) st[2] = delta;
+}
+
+// ---------------------------------------------------------------------------
+// dK and dV: four waves of 32 keys walking the query blocks from the
+// diagonal.  S = Q K^T and dP = dO V^T are formed query-major (Q and dO
+// tiles as the row operand, K and V held in registers), so the score
+// accumulator's layout is the k operand of dV^T = dO^T P and
+// dK^T = Q^T dS, whose dO^T and Q^T come by transpose reads.  Per query
+// row the exponent offset -mm and -delta come from a row-terms array
+// staged beside the tiles; four products per tile, one exponential per
+// score.  dK is scaled by 1/sqrt(d) once, at the end.
+// ---------------------------------------------------------------------------
+template <int kMinBlocks>
+__global__ void __launch_bounds__(kBwdWaves * kWave, kMinBlocks)
+Attn16DKDV(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+           const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
+           const float* __restrict__ stats, float* __restrict__ out_k,
+           float* __restrict__ out_v, int S, int H) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * kTile];
+  // Per streamed query row: -mm, -delta (float2) and the document start.
+  __shared__ __attribute__((aligned(16))) float2 Srow[2][kBlkRows];
+  __shared__ int Sst[2][kBlkRows];
+  __shared__ int Smax[2];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / 32;
+  const int nk = (S + kBwdRows - 1) / kBwdRows;
+  int bh, kblk;
+  UnitOf(nk, bh, kblk);  // rank 0 = the first keys, the longest columns
+  const int b = bh / H, h = bh % H;
+  const int ld = H * kD;
+  const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * kD;
+  const int jw = kblk * kBwdRows + wave * 32;
+  const int j = jw + lane % 32;
+  const int jc = min(j, S - 1);
+  const float scl = kLog2e * 0.125f;
+  const float4* st_bh = reinterpret_cast<const float4*>(stats) + static_cast<size_t>(bh) * S;
+
+  bf16x8 kf[4], vf[4];
+  {
+    const uint16_t* krow = k + base + static_cast<size_t>(jc) * ld;
+    const uint16_t* vrow = v + base + static_cast<size_t>(jc) * ld;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kf[s] = OwnedFrag(krow, s, lane), vf[s] = OwnedFrag(vrow, s, lane);
+  }
+  const int blk_first = (kblk * kBwdRows) / kBlkRows;
+  const int nblk = (S + kBlkRows - 1) / kBlkRows - blk_first;
+  int voff[4];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) voff[jj] = TileLoadOffset((4 * jj + wave) % 8, lane, ld);
+  auto issue = [&](int ib, int buf) {
+    const int r0 = (blk_first + ib) * kBlkRows;
+    const __amdgpu_buffer_rsrc_t rq = SliceRsrc(q + base, ld, S, r0);
+    const __amdgpu_buffer_rsrc_t rd = SliceRsrc(dout + base, ld, S, r0);
+    uint8_t* sb = smem + buf * 2 * kTile;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int u = 4 * jj + wave;
+      if (u < 8)
+        TileLoad(rq, sb, u, voff[jj]);
+      else
+        TileLoad(rd, sb + kTile, u - 8, voff[jj]);
+    }
+  };
+  // The row terms of block ib, by wave 0 (64 queries): fetched from HBM one
+  // block ahead of their store into LDS, so the load's latency hides behind
+  // a block's products.
+  float4 pend = {};
+  auto fetch = [&](int ib) {
+    const int iq = (blk_first + ib) * kBlkRows + lane;
+    if (iq < S) pend = st_bh[iq];
+  };
+  auto put = [&](int ib, int buf) {
+    const int iq = (blk_first + ib) * kBlkRows + lane;
+    int start = 0;
+    if (iq < S) {
+      Srow[buf][lane] = make_float2(-RowOffset(pend.x, pend.y), -pend.z);
+      start = StatsStart(pend.w, iq);
+    } else {
+      Srow[buf][lane] = make_float2(-INFINITY, 0.0f);  // weight 0 past the sequence end
+    }
+    Sst[buf][lane] = start;
+    const int mx = WaveMaxI(start);
+    if (lane == 0) Smax[buf] = mx;
+  };
+  // This lane's 16 per-row values of tile qt (rows 8q + 4g + e).
+  auto rows16 = [&](int buf, int qt, float* mmv, float* dlv) {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const float4 a = *reinterpret_cast<const float4*>(&Srow[buf][qt * 32 + 8 * q4 + 4 * g]);
+      const float4 bb = *reinterpret_cast<const float4*>(&Srow[buf][qt * 32 + 8 * q4 + 4 * g + 2]);
+      mmv[4 * q4] = a.x, dlv[4 * q4] = a.y, mmv[4 * q4 + 1] = a.z, dlv[4 * q4 + 1] = a.w;
+      mmv[4 * q4 + 2] = bb.x, dlv[4 * q4 + 2] = bb.y, mmv[4 * q4 + 3] = bb.z, dlv[4 * q4 + 3] = bb.w;
+    }
+  };
+  const FragOffsets fo = MakeFragOffsets(lane);
+  v16f acc_k[2] = {}, acc_v[2] = {};  // [dt]
+
+  auto query_tile = [&](auto masked, const uint8_t* qtile, const uint8_t* dtile, int buf, int qt,
+                        int r0) {
+    constexpr bool kMask = decltype(masked)::value;
+    v16f sc = {}, dp = {};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      sc = Mfma(RowFrag(qtile, fo, 32 * qt, s), kf[s], sc);
+      dp = Mfma(RowFrag(dtile, fo, 32 * qt, s), vf[s], dp);
+    }
+    float mmv[16], dlv[16];
+    rows16(buf, qt, mmv, dlv);
+    const int lo_rel = r0 + 32 * qt + 4 * g - j;  // query row minus this lane's key
+    float w[16], p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float e = Exp2(__builtin_fmaf(sc[r], scl, mmv[r]));
+      if constexpr (kMask) {  // keep query row >= j and its start <= j
+        const int il = qt * 32 + RowConst(r) + 4 * g;
+        e = OrZero(e, Outside(lo_rel + RowConst(r), j - Sst[buf][il]));
+      }
+      p[r] = e;
+      w[r] = e * (dp[r] + dlv[r]);
+    }
+    bf16x8 wb[2], pb[2];
+    PackTile(w, wb);
+    PackTile(p, pb);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        acc_k[dt] = Mfma(ColFrag(qtile, fo, dt, 32 * qt + 16 * hh), wb[hh], acc_k[dt]);
+        acc_v[dt] = Mfma(ColFrag(dtile, fo, dt, 32 * qt + 16 * hh), pb[hh], acc_v[dt]);
+      }
+  };
+
+  issue(0, 0);
+  if (wave == 0) {
+    fetch(0);
+    put(0, 0);
+    if (1 < nblk) fetch(1);
+  }
+  for (int ib = 0; ib < nblk; ++ib) {
+    const int buf = ib & 1;
+    WaitVm<0>();
+    __syncthreads();
+    if (ib + 1 < nblk) {
+      issue(ib + 1, buf ^ 1);
+      if (wave == 0) {
+        put(ib + 1, buf ^ 1);
+        if (ib + 2 < nblk) fetch(ib + 2);
+      }
+    }
+    const uint8_t* sb = smem + buf * 2 * kTile;
+    const int r0 = (blk_first + ib) * kBlkRows;
+    const int smax = Uniform(Smax[buf]);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int rt = r0 + 32 * qt;
+      if (rt + 31 < jw) continue;  // queries wholly before this wave's keys
+      if (rt >= jw + 31 && rt + 32 <= S && smax <= jw)
+        query_tile(std::false_type{}, sb, sb + kTile, buf, qt, r0);
+      else
+        query_tile(std::true_type{}, sb, sb + kTile, buf, qt, r0);
+    }
+  }
+  if (j >= S) return;
+  const float isd = 0.125f;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const size_t at = base + static_cast<size_t>(j) * ld + dt * 32 + 8 * qq + 4 * g;
+      if (out_k)
+        *reinterpret_cast<float4*>(out_k + at) =
+            make_float4(acc_k[dt][4 * qq] * isd, acc_k[dt][4 * qq + 1] * isd,
+                        acc_k[dt][4 * qq + 2] * isd, acc_k[dt][4 * qq + 3] * isd);
+      if (out_v)
+        *reinterpret_cast<float4*>(out_v + at) =
+            make_float4(acc_v[dt][4 * qq], acc_v[dt][4 * qq + 1], acc_v[dt][4 * qq + 2],
+                        acc_v[dt][4 * qq + 3]);
+    }
+}
+
+}  // namespace
+
+bool Attn16Fits(size_t B, size_t S, size_t H, size_t d) {
+  return d == kD && S > 0 && (S - 1) * H * kD * 2 + kD * 2 < (size_t{1} << 31) &&
+         (S + 127) / 128 * B * H < (size_t{1} << 31);
+}
+
+hipError_t LaunchAttn16Fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, float* o,
+                           float* stats, size_t B, size_t S, size_t H, const int32_t* starts,
+                           hipStream_t s) {
+  if (B * H * S == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((S + 127) / 128 * B * H));
+  hipLaunchKernelGGL((Attn16Fwd<1, 2, 4, 4>), grid, dim3(256), 0, s, q, k, v, o, stats,
+                     static_cast<int>(S), static_cast<int>(H), starts);
+  return hipGetLastError();
+}
+
+hipError_t LaunchAttn16DQ(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                          const uint16_t* dout, float* stats, float* dq, size_t B, size_t S,
+                          size_t H, hipStream_t s) {
+  if (B * H * S == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((S + kBwdRows - 1) / kBwdRows * B * H));
+  hipLaunchKernelGGL(Attn16DQ<2>, grid, dim3(kBwdWaves * kWave), 0, s, q, k, v, dout, stats, dq,
+                     static_cast<int>(S), static_cast<int>(H));
+  return hipGetLastError();
+}
+
+hipError_t LaunchAttn16DKDV(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            const uint16_t* dout, const float* stats, float* dk, float* dv,
+                            size_t B, size_t S, size_t H, hipStream_t s) {
+  if (B * H * S == 0) return hipSuccess;
+  if (!dk && !dv) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>((S + kBwdRows - 1) / kBwdRows * B * H));
+  hipLaunchKernelGGL(Attn16DKDV<2>, grid, dim3(kBwdWaves * kWave), 0, s, q, k, v, dout, stats,
+                     dk, dv, static_cast<int>(S), static_cast<int>(H));
+  return hipGetLastError();
+}
+
+}  // namespace seeai

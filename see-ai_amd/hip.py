@@ -103,6 +103,9 @@ EXPORTS = {
     "seeai_w8a8_pack_weights": (_I, [_P, _P, _P, _P, _U64, _U64]),
     "seeai_w8a8_gemm": (_I, [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64]),
     "seeai_attn_fwd": (_I, [_P, _I, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64, _P]),
+    "seeai_attn_fwd_bf16": (_I, [_P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64, _P]),
+    "seeai_attn_dq_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
+    "seeai_attn_dkdv_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
     "seeai_attn_dq": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
     "seeai_attn_dk": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
     "seeai_attn_dv": (_I, [_P, _I, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),

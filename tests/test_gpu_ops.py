@@ -559,6 +559,102 @@ def test_relaxed_attention_on_peaked_rows(hip, orc, backend, scale, d, mode):
         assert e <= bar, f"{name}: {e:.3g}"
 
 
+ATTN16_SHAPES = [(1, 1, 1), (2, 67, 2), (1, 256, 1), (1, 512, 2), (2, 300, 2), (1, 1024, 3),
+                 (1, 2048, 2)]
+
+
+def _bf16_bits(x):
+    """The bf16 bit patterns of bf16-valued f32 data."""
+    return (np.ascontiguousarray(x, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("B,S,H", ATTN16_SHAPES)
+@pytest.mark.parametrize("seg", [False, True])
+def test_attention_bf16_storage_forward(hip, orc, torch_cuda, B, S, H, seg):
+    """The forward on bf16 operands held as bf16 (head width 64, 32 queries
+    per wave, direct-to-LDS staging, transpose reads for V^T) against the
+    oracle on the same bf16-valued inputs: O and the stats row within the
+    bf16 bar, the document starts exactly."""
+    torch = torch_cuda
+    d = 64
+    r = rng(B * 100 + S + H + 3 * seg)
+    shape = (B * S, H * d)
+    q, k, v = (_bf16_valued(r.standard_normal(shape).astype(np.float32)) for _ in range(3))
+    starts = None
+    if seg:
+        toks = r.integers(0, 4, B * S).astype(np.int32)
+        starts = orc.segment_starts(toks, B, S, 3)
+    o_c, st_c = orc.attn_fwd_tiled(q, k, v, B, S, H, d, starts=starts)
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    dq, dk, dv = (torch.from_numpy(_bf16_bits(x).view(np.int16)).cuda() for x in (q, k, v))
+    o = torch.full(shape, float("nan"), dtype=torch.float32, device="cuda")
+    st = torch.full((B * H * S, 4), float("nan"), dtype=torch.float32, device="cuda")
+    dstarts = torch.from_numpy(starts).cuda() if seg else None
+    ctx.call("seeai_attn_fwd_bf16", dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), o.data_ptr(),
+             st.data_ptr(), B, S, H, d, dstarts.data_ptr() if seg else None)
+    torch.cuda.synchronize()
+    og, sg = o.cpu().numpy(), st.cpu().numpy()
+    e = maxrel(og, o_c)
+    assert e <= TOL_BF16, f"o: {e:.3g}"
+    assert bits_equal(sg[:, 3], st_c[:, 3]), "document starts"
+    for col in (0, 1):
+        e = maxrel(sg[:, col], st_c[:, col])
+        assert e <= TOL_BF16, f"stats[{col}]: {e:.3g}"
+    ctx.close()
+
+
+@pytest.mark.parametrize("B,S,H", ATTN16_SHAPES)
+@pytest.mark.parametrize("seg", [False, True])
+def test_attention_bf16_storage_backward(hip, orc, torch_cuda, B, S, H, seg):
+    """dQ (with the stats row's delta) and dK / dV on bf16 operands held as
+    bf16, from the bf16 forward's stats rows, against the oracle's tiled
+    backward on the same bf16-valued inputs and its own stats: within the
+    bf16 bar.  dK / dV with one output absent are bitwise the pair's."""
+    torch = torch_cuda
+    d = 64
+    r = rng(B * 300 + S + H + 5 * seg)
+    shape = (B * S, H * d)
+    q, k, v, do = (_bf16_valued(r.standard_normal(shape).astype(np.float32)) for _ in range(4))
+    starts = None
+    if seg:
+        toks = r.integers(0, 4, B * S).astype(np.int32)
+        starts = orc.segment_starts(toks, B, S, 3)
+    _, st_c = orc.attn_fwd_tiled(q, k, v, B, S, H, d, starts=starts)
+    dq_c, st_c = orc.attn_dq_tiled(q, k, v, do, st_c, B, S, H, d)
+    dk_c = orc.attn_dk_tiled(q, k, v, do, st_c, B, S, H, d)
+    dv_c = orc.attn_dv_tiled(q, k, do, st_c, B, S, H, d)
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    gq, gk, gv, gdo = (torch.from_numpy(_bf16_bits(x).view(np.int16)).cuda() for x in (q, k, v, do))
+    nan = lambda sh: torch.full(sh, float("nan"), dtype=torch.float32, device="cuda")  # noqa: E731
+    o, st = nan(shape), nan((B * H * S, 4))
+    dq, dk, dv, dk1, dv1 = (nan(shape) for _ in range(5))
+    dstarts = torch.from_numpy(starts).cuda() if seg else None
+    P = lambda t: t.data_ptr()  # noqa: E731
+    ctx.call("seeai_attn_fwd_bf16", P(gq), P(gk), P(gv), P(o), P(st), B, S, H, d,
+             P(dstarts) if seg else None)
+    ctx.call("seeai_attn_dq_bf16", P(gq), P(gk), P(gv), P(gdo), P(st), P(dq), B, S, H, d)
+    ctx.call("seeai_attn_dkdv_bf16", P(gq), P(gk), P(gv), P(gdo), P(st), P(dk), P(dv), B, S, H, d)
+    ctx.call("seeai_attn_dkdv_bf16", P(gq), P(gk), P(gv), P(gdo), P(st), P(dk1), None, B, S, H, d)
+    ctx.call("seeai_attn_dkdv_bf16", P(gq), P(gk), P(gv), P(gdo), P(st), None, P(dv1), B, S, H, d)
+    torch.cuda.synchronize()
+    sg = st.cpu().numpy()
+    for name, got, want in (("dq", dq, dq_c), ("dk", dk, dk_c), ("dv", dv, dv_c)):
+        e = maxrel(got.cpu().numpy(), want)
+        assert e <= TOL_BF16, f"{name}: {e:.3g}"
+    e = maxrel(sg[:, 2], st_c[:, 2])
+    assert e <= TOL_BF16, f"delta: {e:.3g}"
+    assert bits_equal(sg[:, 3], st_c[:, 3]), "document starts"
+    assert torch.equal(dk.view(torch.int32), dk1.view(torch.int32))
+    assert torch.equal(dv.view(torch.int32), dv1.view(torch.int32))
+    with pytest.raises(hip.BackendError):
+        ctx.call("seeai_attn_dkdv_bf16", P(gq), P(gk), P(gv), P(gdo), P(st), None, None, B, S, H, d)
+    with pytest.raises(hip.BackendError):
+        ctx.call("seeai_attn_dq_bf16", P(gq), P(gk), P(gv), P(gdo), P(st), P(dq), B, S, H, 128)
+    ctx.close()
+
+
 @pytest.mark.parametrize("B,S,H,d,seg", [(2, 67, 2, 64, False), (1, 512, 2, 64, True),
                                          (2, 300, 2, 64, False)])
 @pytest.mark.parametrize("order", ["dk_dv", "dv_dk"])
