@@ -140,10 +140,25 @@ def attention_step(ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d, parts=No
             ctx.call("seeai_attn_dv", dt, P(q), P(k), P(do), P(st), P(dv), B, S, H, d)
 
 
+def attention_step_bf16(ctx, q, k, v, do, o, st, dq, dk, dv, B, S, H, d, parts=None):
+    """One causal attention fwd + bwd on bf16 operands held in HBM as bf16
+    (what a model trained in bf16 activations holds): the forward, dQ with
+    the stats delta, and the fused dK / dV pass."""
+    P = lambda t: t.data_ptr()
+    parts = parts or ("fwd", "dq", "dkdv")
+    if "fwd" in parts:
+        ctx.call("seeai_attn_fwd_bf16", P(q), P(k), P(v), P(o), P(st), B, S, H, d, None)
+    if "dq" in parts:
+        ctx.call("seeai_attn_dq_bf16", P(q), P(k), P(v), P(do), P(st), P(dq), B, S, H, d)
+    if "dkdv" in parts:
+        ctx.call("seeai_attn_dkdv_bf16", P(q), P(k), P(v), P(do), P(st), P(dk), P(dv), B, S, H, d)
+
+
 def attn_probe():
-    """BASELINE configs[2] once per family for the profilers: causal
-    attention fwd + dQ + dK + dV at B16 H16 S2048 d64, relaxed (bf16) three
-    times, exact (f32) once."""
+    """BASELINE configs[2] per path for the profilers: causal attention fwd +
+    dQ + dK + dV at B16 H16 S2048 d64 -- on bf16 operands held as bf16 three
+    times, on f32 operands through the relaxed bf16 kernels once, exact (f32)
+    once."""
     import torch
     hip = importlib.import_module("see-ai_amd.hip")
     ctx = hip.Context(0)
@@ -153,12 +168,15 @@ def attn_probe():
     q, k, v, do = (torch.randn((B * S, H * d), device="cuda", generator=g) for _ in range(4))
     o, st = torch.empty_like(q), torch.empty((B * H * S, 4), device="cuda")
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
-    for dt, reps in [(1, 3), (0, 1)]:
-        for _ in range(reps):
-            attention_step(ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d)
+    qb, kb, vb, dob = (x.to(torch.bfloat16) for x in (q, k, v, do))
+    for _ in range(3):
+        attention_step_bf16(ctx, qb, kb, vb, dob, o, st, dq, dk, dv, B, S, H, d)
+    for dt in (1, 0):
+        attention_step(ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d)
     torch.cuda.synchronize()
     ctx.close()
-    print("attention probe: B16 H16 S2048 d64 causal, 3 x bf16 fwd+bwd, 1 x f32 fwd+bwd", flush=True)
+    print("attention probe: B16 H16 S2048 d64 causal, 3 x bf16-held fwd+bwd, 1 x relaxed bf16 on "
+          "f32 operands, 1 x f32 fwd+bwd", flush=True)
     return 0
 
 
@@ -421,7 +439,21 @@ def extras(ctx, torch, hip):
     q, k, v, do = (torch.randn((B * S, H * d), device="cuda") for _ in range(4))
     o, st = torch.empty_like(q), torch.empty((B * H * S, 4), device="cuda")
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
-    for dt, name in [(1, "attention_bf16"), (0, "attention_f32")]:
+    # bf16 operands held as bf16 (the models trained in bf16 activations)
+    qb, kb, vb, dob = (x.to(torch.bfloat16) for x in (q, k, v, do))
+    args_ = (ctx, qb, kb, vb, dob, o, st, dq, dk, dv, B, S, H, d)
+    ms = timed(lambda: attention_step_bf16(*args_), 5, 1)
+    tf = flops / ms / 1e9
+    out["attention_bf16"] = {
+        "ms_fwd_bwd": round(ms, 3), "TFLOP_s": round(tf, 1),
+        "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4),
+        "config": "B16 H16 S2048 d64 causal, Q/K/V/dO bf16 in HBM",
+        "ms_parts": {part: round(timed(lambda part=part: attention_step_bf16(*args_, parts=(part,)),
+                                       5, 1), 4) for part in ("fwd", "dq", "dkdv")}}
+    del qb, kb, vb, dob
+    # f32 operands: the relaxed family on the bf16 kernels (rounding while
+    # staging), and the exact family
+    for dt, name in [(1, "attention_bf16_f32_operands"), (0, "attention_f32")]:
         args_ = (ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d)
         ms = timed(lambda: attention_step(*args_), 3 if dt else 1, 1)
         tf = flops / ms / 1e9

@@ -54,6 +54,60 @@ __device__ __forceinline__ void WaitVm() {
   __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
 }
 
+// f(integral_constant<I>) for I = 0 .. N-1, unrolled.
+template <int I, int N>
+struct Unroll {
+  template <class F>
+  __device__ __forceinline__ static void Run(F&& f) {
+    if constexpr (I < N) {
+      f(std::integral_constant<int, I>{});
+      Unroll<I + 1, N>::Run(f);
+    }
+  }
+};
+
+// The stage ring of a kernel: kStages buffers of one K-and-V (or Q-and-dO)
+// block, each a separate LDS object named at compile time (stage ids are
+// template constants after unrolling), so the compiler can tell a fragment
+// read of one stage from the DMA into another and does not make the read
+// wait for that DMA.
+#define SEEAI_STAGE_RING(kStages)                                                          \
+  static_assert(kStages >= 2 && kStages <= 4, "2 to 4 stages");                            \
+  __shared__ __attribute__((aligned(1024))) uint8_t stage_0[2 * kTile];                    \
+  __shared__ __attribute__((aligned(1024))) uint8_t stage_1[2 * kTile];                    \
+  __shared__ __attribute__((aligned(1024))) uint8_t stage_2[kStages > 2 ? 2 * kTile : 1];  \
+  __shared__ __attribute__((aligned(1024))) uint8_t stage_3[kStages > 3 ? 2 * kTile : 1];  \
+  auto stage = [&](auto id) -> uint8_t* {                                                  \
+    constexpr int kId = decltype(id)::value % kStages;                                     \
+    if constexpr (kId == 0) return stage_0;                                                \
+    else if constexpr (kId == 1) return stage_1;                                           \
+    else if constexpr (kId == 2) return stage_2;                                           \
+    else return stage_3;                                                                   \
+  }
+
+// Runs blocks 0 .. nblk-1 through the ring: block jb computes from stage
+// jb % kStages while blocks jb + 1 .. jb + kStages - 1 land in the others.
+// issue(jb, stage) starts block jb's loads (kLoads per wave); step(jb, stage)
+// computes it.  Past the last block the last is loaded again into a stage
+// no later block reads, so every wait counts the same number of loads.
+template <int kStages, int kLoads, class Issue, class Step, class Stage>
+__device__ __forceinline__ void RunRing(int nblk, Issue&& issue, Step&& step, Stage&& stage) {
+  const int last = nblk - 1;
+  Unroll<0, kStages - 1>::Run([&](auto id) { issue(min(decltype(id)::value, last), stage(id)); });
+  for (int jb0 = 0; jb0 < nblk; jb0 += kStages) {
+    Unroll<0, kStages>::Run([&](auto id) {
+      constexpr int kId = decltype(id)::value;
+      const int jb = jb0 + kId;
+      if (jb >= nblk) return;
+      WaitVm<(kStages - 2) * kLoads>();  // block jb's loads have landed
+      __syncthreads();  // ... in every wave, and block jb - 1's stage is free
+      issue(min(jb + kStages - 1, last), stage(std::integral_constant<int, kId + kStages - 1>{}));
+      step(jb, static_cast<const uint8_t*>(stage(id)));
+    });
+  }
+  WaitVm<0>();  // no load into LDS outlives the workgroup
+}
+
 // The (b, h) slice of a [B*S, H*64] bf16 tensor as a buffer resource whose
 // first record is row `row0`; rows at or past S are out of range (zeros).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t SliceRsrc(const uint16_t* slice, int ld, int S,
@@ -141,8 +195,19 @@ __device__ __forceinline__ bf16x8 OwnedFrag(const uint16_t* row, int s, int lane
   return *reinterpret_cast<const bf16x8*>(row + 16 * s + 8 * (lane / 32));
 }
 
-__device__ __forceinline__ float SwapMax(float v) { return fmaxf(v, __shfl_xor(v, 32, kWave)); }
-__device__ __forceinline__ float SwapSum(float v) { return v + __shfl_xor(v, 32, kWave); }
+// Lanes c and c + 32 combined by v_permlane32_swap (no LDS round trip): the
+// swap of v with itself leaves lanes c's value in .x and lane c + 32's in .y
+// of both lanes, so the sum is formed in the same order in both.
+__device__ __forceinline__ float SwapMax(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float SwapSum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 __device__ __forceinline__ int WaveMaxI(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
@@ -173,28 +238,36 @@ __device__ __forceinline__ void UnitOf(int nb, int& bh, int& rank) {
 }
 
 // ---------------------------------------------------------------------------
-// Forward.  A workgroup of kFwdWaves waves owns kFwdWaves * 32 * QT queries
-// of one (b, h); each wave QT 32-query tiles, so every K and V fragment read
-// from LDS feeds QT MFMAs.  The launch takes QT = 1, four waves, four
-// workgroups per CU: occupancy, which hides the softmax behind the other
-// waves' products, measured ahead of fragment reuse.  Keys stream in 64-row
-// blocks, kFwdStages buffers of K and V in flight.  The scores arrive as q.k; t = q.k * log2(e)/sqrt(d) - m_use
-// (one FMA) is the base-2 exponent of the weight.  m_use moves only when a
-// key tile's maximum passes it by more than 2^8, or on the first tile a
-// query sees; the true maximum is kept beside it and the stats row (m, 1/l)
-// is stated against it.  l sums the bf16-rounded weights that enter P V.
+// Forward.  A workgroup of kFwdWaves waves owns kFwdWaves * 32 queries of one
+// (b, h), 32 per wave.  Keys stream in 64-row blocks through two stage
+// buffers.  The scores arrive as q.k; x = q.k * log2(e)/sqrt(d) - m_use (one
+// FMA) is the base-2 exponent of the weight.
+//
+// Lazy offset.  Lane (g, c) holds 16 of query c's scores per tile, lane
+// (1 - g, c) the other 16, and both must weigh against the same m_use.  Each
+// half tracks its own maximum; m_use moves only when some half's tile
+// maximum passes it by more than 2^8, or on the first tile a half sees --
+// rare events, in which the pair first agrees on its maximum by one lane
+// swap.  The common tile therefore has no cross-lane traffic: l and the true
+// maximum are per half until the end.  The stats row (m, 1/l) is stated
+// against the true maximum; l sums the bf16-rounded weights that enter P V.
+//
+// Every tile runs one body; on the diagonal (and at document starts) a
+// uniform branch masks the exponents, so the accumulators keep their
+// registers across the branch.
 // ---------------------------------------------------------------------------
 constexpr float kLazy = 8.0f;
 
-template <int QT, int kFwdStages, int kFwdWaves, int kMinBlocks>
+template <int kFwdWaves, int kStages, int kMinBlocks>
 __global__ void __launch_bounds__(kFwdWaves * kWave, kMinBlocks)
 Attn16Fwd(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
           const uint16_t* __restrict__ v, float* __restrict__ o, float* __restrict__ stats, int S,
           int H, const int32_t* __restrict__ starts) {
-  constexpr int kFwdRows = kFwdWaves * 32 * QT;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kFwdStages * 2 * kTile];
+  constexpr int kFwdRows = kFwdWaves * 32;
+  SEEAI_STAGE_RING(kStages);
   __shared__ int wave_lo[kFwdWaves];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane / 32, c = lane % 32;
   const int nq = (S + kFwdRows - 1) / kFwdRows;
   int bh, rank;
@@ -203,25 +276,16 @@ Attn16Fwd(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   const int b = bh / H, h = bh % H;
   const int ld = H * kD;
   const size_t base = static_cast<size_t>(b) * S * ld + static_cast<size_t>(h) * kD;
-  const int qw = qblk * kFwdRows + wave * 32 * QT;  // this wave's first query
-  int iq[QT], jstart[QT];
-#pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    iq[t] = qw + 32 * t + c;
-    const int ic = min(iq[t], S - 1);
-    int s0 = 0;
-    if (starts) {
-      const int v0 = starts[static_cast<size_t>(b) * S + ic];
-      s0 = v0 <= 0 ? 0 : min(v0, ic);
-    }
-    jstart[t] = s0;
+  const int qw = qblk * kFwdRows + wave * 32;  // this wave's first query
+  const int i = qw + c;
+  const int ic = min(i, S - 1);
+  int jstart = 0;
+  if (starts) {
+    const int v0 = starts[static_cast<size_t>(b) * S + ic];
+    jstart = v0 <= 0 ? 0 : min(v0, ic);
   }
-  int js_lo = jstart[0], js_hi = jstart[0];
-#pragma unroll
-  for (int t = 1; t < QT; ++t) js_lo = min(js_lo, jstart[t]), js_hi = max(js_hi, jstart[t]);
-  const int w_lo = WaveMinI(js_lo);
-  const int w_hi_start = WaveMaxI(js_hi);
-  if (lane == 0) wave_lo[wave] = w_lo;
+  const int w_hi_start = WaveMaxI(jstart);
+  if (lane == 0) wave_lo[wave] = WaveMinI(jstart);
   __syncthreads();
   int lo = wave_lo[0];
 #pragma unroll
@@ -230,27 +294,26 @@ Attn16Fwd(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   const int q_hi = min(qblk * kFwdRows + kFwdRows - 1, S - 1);
   const int nblk = q_hi / kBlkRows + 1 - blk_lo;
 
-  bf16x8 qf[QT][4];
+  bf16x8 qf[4];
+  {
+    const uint16_t* row = q + base + static_cast<size_t>(ic) * ld;
 #pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    const uint16_t* row = q + base + static_cast<size_t>(min(iq[t], S - 1)) * ld;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qf[t][s] = OwnedFrag(row, s, lane);
+    for (int s = 0; s < 4; ++s) qf[s] = OwnedFrag(row, s, lane);
   }
   const float scl = kLog2e * 0.125f;  // log2(e) / sqrt(64)
 
   // Loads: per stage 16 wave-loads (K then V, 2 halves x 4 row groups); wave
   // w takes u = kFwdWaves j + w.
   constexpr int kLoadsPerWave = 16 / kFwdWaves;
+  static_assert(kLoadsPerWave * kFwdWaves == 16, "16 wave-loads per block");
   int voff[kLoadsPerWave];
 #pragma unroll
   for (int j = 0; j < kLoadsPerWave; ++j)
     voff[j] = TileLoadOffset((kFwdWaves * j + wave) % 8, lane, ld);
-  auto issue = [&](int jb, int buf) {
+  auto issue = [&](int jb, uint8_t* st) {
     const int j0 = (blk_lo + jb) * kBlkRows;
     const __amdgpu_buffer_rsrc_t rk = SliceRsrc(k + base, ld, S, j0);
     const __amdgpu_buffer_rsrc_t rv = SliceRsrc(v + base, ld, S, j0);
-    uint8_t* st = smem + buf * 2 * kTile;
 #pragma unroll
     for (int j = 0; j < kLoadsPerWave; ++j) {
       const int u = kFwdWaves * j + wave;
@@ -262,123 +325,98 @@ Attn16Fwd(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   };
 
   const FragOffsets fo = MakeFragOffsets(lane);
-  v16f oacc[2][QT] = {};  // [dt][t]
-  float m_use[QT], m_true[QT], l[QT];
-#pragma unroll
-  for (int t = 0; t < QT; ++t) m_use[t] = 0.0f, m_true[t] = -INFINITY, l[t] = 0.0f;
+  v16f oacc[2] = {};  // [dt]
+  float m_use = 0.0f, m_half = -INFINITY, l_half = 0.0f;
+  float thr = -INFINITY;  // a half's tile maximum above this moves m_use: -inf until it sees a score
+
   const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
-  // A 32-key tile kt of the block in buffer `st`: its scores (S^T = K Q^T,
-  // eight MFMAs), their softmax (VALU), and O^T += V^T P^T (eight MFMAs).
-  // The loop below orders them so the next tile's score MFMAs are in
-  // flight while this tile's softmax runs, and this tile's accumulation
-  // while the next tile's softmax runs.
-  auto key_tile = [&](auto masked, const uint8_t* kt_tile, const uint8_t* vt_tile, int kt,
-                      int jt) {
-    constexpr bool kMask = decltype(masked)::value;
-    v16f sc[QT] = {};
+  // A 32-key tile kt of a staged block: S^T = K Q^T (four MFMAs) ...
+  auto scores = [&](const uint8_t* kt_tile, int kt) {
+    v16f sc = {};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bf16x8 kf = RowFrag(kt_tile, fo, 32 * kt, s);
+    for (int s = 0; s < 4; ++s) sc = Mfma(RowFrag(kt_tile, fo, 32 * kt, s), qf[s], sc);
+    return sc;
+  };
+  // ... the softmax weights (VALU) and O^T += V^T P^T (four MFMAs).
+  auto weigh = [&](const v16f& sc, bool masked, const uint8_t* vt_tile, int kt, int jt) {
+    float x[16];
 #pragma unroll
-      for (int t = 0; t < QT; ++t) sc[t] = Mfma(kf, qf[t][s], sc[t]);
+    for (int r = 0; r < 16; ++r) x[r] = __builtin_fmaf(sc[r], scl, -m_use);
+    if (masked) {  // keep key jt + row in [jstart, i]
+      const int hi_rel = i - jt - 4 * g, lo_rel = jstart - jt - 4 * g;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        x[r] = OrNegInf(x[r], Outside(hi_rel - RowConst(r), RowConst(r) - lo_rel));
     }
-    bf16x8 pb[QT][2];
+    float hmax = x[0];
 #pragma unroll
-    for (int t = 0; t < QT; ++t) {
-      float bmax = -INFINITY;
-      const int hi_rel = iq[t] - jt - 4 * g;
-      const int lo_rel = jstart[t] - jt - 4 * g;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = __builtin_fmaf(sc[t][r], scl, -m_use[t]);
-        if constexpr (kMask)  // keep key jt + row in [jstart, i]
-          x = OrNegInf(x, Outside(hi_rel - RowConst(r), RowConst(r) - lo_rel));
-        sc[t][r] = x;
-        bmax = fmaxf(bmax, x);
-      }
-      bmax = SwapMax(bmax);  // relative to m_use
-      const bool first = m_true[t] == -INFINITY;
-      if (bmax != -INFINITY) m_true[t] = fmaxf(m_true[t], m_use[t] + bmax);
+    for (int r = 1; r < 16; ++r) hmax = fmaxf(hmax, x[r]);  // relative to m_use
+    const float m_prev = m_half;
+    m_half = fmaxf(m_half, m_use + hmax);
+    if (__any(hmax > thr)) {
+      const float bmax = SwapMax(hmax);
+      const bool first = SwapMax(m_prev) == -INFINITY;
       const bool need = first ? bmax != -INFINITY : bmax > kLazy;
-      if (__any(need)) {
-        const float shift = need ? bmax : 0.0f;
-        const float alpha = first ? 0.0f : Exp2(-shift);
-        m_use[t] += shift;
-        l[t] *= alpha;
+      const float shift = need ? bmax : 0.0f;
+      const float alpha = first ? 0.0f : Exp2(-shift);
+      m_use += shift;
+      l_half *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) oacc[dt][t] *= alpha;
+      for (int dt = 0; dt < 2; ++dt) oacc[dt] *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sc[t][r] -= shift;
-      }
-      float p[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = Exp2(sc[t][r]);
-      PackTile(p, pb[t]);
-      float psum = 0.0f;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          psum = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pb[t][hh][2 * e], pb[t][hh][2 * e + 1]},
-                                                 ones, psum, false);
-      l[t] += SwapSum(psum);
+      for (int r = 0; r < 16; ++r) x[r] -= shift;
+      thr = m_half == -INFINITY ? -INFINITY : kLazy;
     }
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = Exp2(x[r]);
+    bf16x8 pb[2];
+    PackTile(p, pb);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        l_half = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pb[hh][2 * e], pb[hh][2 * e + 1]}, ones,
+                                                 l_half, false);
     // O^T += V^T P^T over the tile's 32 keys (two 16-key steps).
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        const bf16x8 vf = ColFrag(vt_tile, fo, dt, 32 * kt + 16 * hh);
-#pragma unroll
-        for (int t = 0; t < QT; ++t) oacc[dt][t] = Mfma(vf, pb[t][hh], oacc[dt][t]);
-      }
+      for (int dt = 0; dt < 2; ++dt)
+        oacc[dt] = Mfma(ColFrag(vt_tile, fo, dt, 32 * kt + 16 * hh), pb[hh], oacc[dt]);
   };
 
-  // Prologue: kStages - 1 blocks in flight (past the last, the last repeats:
-  // in bounds, into a buffer no later block reads).
-  const int last = nblk - 1;
-#pragma unroll
-  for (int s = 0; s < kFwdStages - 1; ++s) issue(min(s, last), s);
-  const int qmin = qw, qmax = qw + 32 * QT - 1;
-  for (int jb = 0; jb < nblk; ++jb) {
-    WaitVm<(kFwdStages - 2) * kLoadsPerWave>();  // this block's loads have landed
-    __syncthreads();                 // ... in every wave, and block jb - 1's buffer is free
-    issue(min(jb + kFwdStages - 1, last), (jb + kFwdStages - 1) % kFwdStages);
-    const uint8_t* st = smem + (jb % kFwdStages) * 2 * kTile;
+  const int qmin = qw, qmax = qw + 31;
+  auto step = [&](int jb, const uint8_t* cur) {
     const int j0 = (blk_lo + jb) * kBlkRows;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       const int jt = j0 + 32 * kt;
       if (jt > qmax) continue;  // keys wholly after this wave's queries
-      if (jt + 31 <= qmin && jt >= w_hi_start)
-        key_tile(std::false_type{}, st, st + kTile, kt, jt);
-      else
-        key_tile(std::true_type{}, st, st + kTile, kt, jt);
+      weigh(scores(cur, kt), !(jt + 31 <= qmin && jt >= w_hi_start), cur + kTile, kt, jt);
     }
-  }
-  WaitVm<0>();  // the repeated tail loads have landed before the workgroup ends
+  };
+  RunRing<kStages, kLoadsPerWave>(nblk, issue, step, stage);
 
+  const float l = SwapSum(l_half);
+  const float m_true = SwapMax(m_half);
+  if (i >= S) return;
+  const float inv = 1.0f / l;
+  float* orow = o + base + static_cast<size_t>(i) * ld;
 #pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    const int i = iq[t];
-    if (i >= S) continue;
-    const float inv = 1.0f / l[t];
-    float* orow = o + base + static_cast<size_t>(i) * ld;
+  for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq)
-        *reinterpret_cast<float4*>(orow + dt * 32 + 8 * qq + 4 * g) =
-            make_float4(oacc[dt][t][4 * qq] * inv, oacc[dt][t][4 * qq + 1] * inv,
-                        oacc[dt][t][4 * qq + 2] * inv, oacc[dt][t][4 * qq + 3] * inv);
-    if (g == 0) {
-      float* sr = stats + (static_cast<size_t>(bh) * S + i) * 4;
-      sr[0] = m_true[t] * kLn2;
-      sr[1] = inv * Exp2(m_true[t] - m_use[t]);
-      sr[2] = 0.0f;
-      sr[3] = static_cast<float>(jstart[t]);
-    }
+    for (int qq = 0; qq < 4; ++qq)
+      *reinterpret_cast<float4*>(orow + dt * 32 + 8 * qq + 4 * g) =
+          make_float4(oacc[dt][4 * qq] * inv, oacc[dt][4 * qq + 1] * inv,
+                      oacc[dt][4 * qq + 2] * inv, oacc[dt][4 * qq + 3] * inv);
+  if (g == 0) {
+    float* sr = stats + (static_cast<size_t>(bh) * S + i) * 4;
+    sr[0] = m_true * kLn2;
+    sr[1] = inv * Exp2(m_true - m_use);
+    sr[2] = 0.0f;
+    sr[3] = static_cast<float>(jstart);
   }
 }
 
@@ -406,14 +444,15 @@ __device__ __forceinline__ int StatsStart(float stored, int i) {
 constexpr int kBwdWaves = 4;
 constexpr int kBwdRows = kBwdWaves * 32;
 
-template <int kMinBlocks>
+template <int kStages, int kMinBlocks>
 __global__ void __launch_bounds__(kBwdWaves * kWave, kMinBlocks)
 Attn16DQ(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
          const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
          float* __restrict__ stats, float* __restrict__ dq, int S, int H) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * kTile];
+  SEEAI_STAGE_RING(kStages);
   __shared__ int wave_lo[kBwdWaves];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane / 32;
   const int nq = (S + kBwdRows - 1) / kBwdRows;
   int bh, rank;
@@ -450,11 +489,10 @@ Attn16DQ(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   int voff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) voff[j] = TileLoadOffset((4 * j + wave) % 8, lane, ld);
-  auto issue = [&](int jb, int buf) {
+  auto issue = [&](int jb, uint8_t* sb) {
     const int j0 = (blk_lo + jb) * kBlkRows;
     const __amdgpu_buffer_rsrc_t rk = SliceRsrc(k + base, ld, S, j0);
     const __amdgpu_buffer_rsrc_t rv = SliceRsrc(v + base, ld, S, j0);
-    uint8_t* sb = smem + buf * 2 * kTile;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int u = 4 * j + wave;
@@ -468,24 +506,32 @@ Attn16DQ(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   v16f acc[2] = {}, acc_p[2] = {};  // [dt]
   float delta = 0.0f;
 
-  auto key_tile = [&](auto masked, const uint8_t* ktile, const uint8_t* vtile, int kt, int jt) {
-    constexpr bool kMask = decltype(masked)::value;
-    v16f sc = {}, dp = {};
+  // A 32-key tile kt: S^T = K Q^T and dP^T = V dO^T (eight MFMAs) ...
+  auto front = [&](const uint8_t* ktile, const uint8_t* vtile, int kt, v16f& sc, v16f& dp) {
+    sc = v16f{};
+    dp = v16f{};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       sc = Mfma(RowFrag(ktile, fo, 32 * kt, s), qf[s], sc);
       dp = Mfma(RowFrag(vtile, fo, 32 * kt, s), df[s], dp);
     }
-    const int hi_rel = i - jt - 4 * g, lo_rel = jstart - jt - 4 * g;
+  };
+  // ... the weights (VALU) and the two accumulations (eight MFMAs).
+  auto back = [&](const v16f& sc, const v16f& dp, bool masked, const uint8_t* ktile, int kt,
+                  int jt) {
     float w[16], p[16];
 #pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = Exp2(__builtin_fmaf(sc[r], scl, -mm));
+    if (masked) {  // keep key jt + row in [jstart, i]
+      const int hi_rel = i - jt - 4 * g, lo_rel = jstart - jt - 4 * g;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        p[r] = OrZero(p[r], Outside(hi_rel - RowConst(r), RowConst(r) - lo_rel));
+    }
+#pragma unroll
     for (int r = 0; r < 16; ++r) {
-      float e = Exp2(__builtin_fmaf(sc[r], scl, -mm));
-      if constexpr (kMask)  // keep key jt + row in [jstart, i]
-        e = OrZero(e, Outside(hi_rel - RowConst(r), RowConst(r) - lo_rel));
-      delta = __builtin_fmaf(dp[r], e, delta);
-      w[r] = e * dp[r];
-      p[r] = e;
+      delta = __builtin_fmaf(dp[r], p[r], delta);
+      w[r] = p[r] * dp[r];
     }
     bf16x8 wb[2], pb[2];
     PackTile(w, wb);
@@ -500,24 +546,19 @@ Attn16DQ(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
       }
   };
 
-  issue(0, 0);
   const int qmin = qw, qmax = qw + 31;
-  for (int jb = 0; jb < nblk; ++jb) {
-    WaitVm<0>();
-    __syncthreads();
-    if (jb + 1 < nblk) issue(jb + 1, (jb + 1) & 1);
-    const uint8_t* sb = smem + (jb & 1) * 2 * kTile;
+  auto step = [&](int jb, const uint8_t* cur) {
     const int j0 = (blk_lo + jb) * kBlkRows;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       const int jt = j0 + 32 * kt;
       if (jt > qmax) continue;
-      if (jt + 31 <= qmin && jt >= w_hi_start)
-        key_tile(std::false_type{}, sb, sb + kTile, kt, jt);
-      else
-        key_tile(std::true_type{}, sb, sb + kTile, kt, jt);
+      v16f sc, dp;
+      front(cur, cur + kTile, kt, sc, dp);
+      back(sc, dp, !(jt + 31 <= qmin && jt >= w_hi_start), cur, kt, jt);
     }
-  }
+  };
+  RunRing<kStages, 4>(nblk, issue, step, stage);
   delta = SwapSum(delta);
   if (i >= S) return;
   const float isd = 0.125f;
@@ -544,18 +585,22 @@ Attn16DQ(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
 // staged beside the tiles; four products per tile, one exponential per
 // score.  dK is scaled by 1/sqrt(d) once, at the end.
 // ---------------------------------------------------------------------------
-template <int kMinBlocks>
+template <int kStages, int kMinBlocks>
 __global__ void __launch_bounds__(kBwdWaves * kWave, kMinBlocks)
 Attn16DKDV(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
            const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
            const float* __restrict__ stats, float* __restrict__ out_k,
            float* __restrict__ out_v, int S, int H) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * kTile];
-  // Per streamed query row: -mm, -delta (float2) and the document start.
-  __shared__ __attribute__((aligned(16))) float2 Srow[2][kBlkRows];
+  SEEAI_STAGE_RING(kStages);
+  // Per streamed query row: -mm, -delta and the document start.  Rows are
+  // contiguous, so a lane's 16 rows of a tile (8q + 4g + e) are four 16-byte
+  // reads in accumulator order.
+  __shared__ __attribute__((aligned(16))) float Smm[2][kBlkRows];
+  __shared__ __attribute__((aligned(16))) float Sdl[2][kBlkRows];
   __shared__ int Sst[2][kBlkRows];
   __shared__ int Smax[2];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane / 32;
   const int nk = (S + kBwdRows - 1) / kBwdRows;
   int bh, kblk;
@@ -581,11 +626,10 @@ Attn16DKDV(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   int voff[4];
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) voff[jj] = TileLoadOffset((4 * jj + wave) % 8, lane, ld);
-  auto issue = [&](int ib, int buf) {
+  auto issue = [&](int ib, uint8_t* sb) {
     const int r0 = (blk_first + ib) * kBlkRows;
     const __amdgpu_buffer_rsrc_t rq = SliceRsrc(q + base, ld, S, r0);
     const __amdgpu_buffer_rsrc_t rd = SliceRsrc(dout + base, ld, S, r0);
-    uint8_t* sb = smem + buf * 2 * kTile;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int u = 4 * jj + wave;
@@ -607,51 +651,61 @@ Attn16DKDV(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const int iq = (blk_first + ib) * kBlkRows + lane;
     int start = 0;
     if (iq < S) {
-      Srow[buf][lane] = make_float2(-RowOffset(pend.x, pend.y), -pend.z);
+      Smm[buf][lane] = -RowOffset(pend.x, pend.y);
+      Sdl[buf][lane] = -pend.z;
       start = StatsStart(pend.w, iq);
     } else {
-      Srow[buf][lane] = make_float2(-INFINITY, 0.0f);  // weight 0 past the sequence end
+      Smm[buf][lane] = -INFINITY;  // weight 0 past the sequence end
+      Sdl[buf][lane] = 0.0f;
     }
     Sst[buf][lane] = start;
     const int mx = WaveMaxI(start);
     if (lane == 0) Smax[buf] = mx;
   };
   // This lane's 16 per-row values of tile qt (rows 8q + 4g + e).
-  auto rows16 = [&](int buf, int qt, float* mmv, float* dlv) {
+  // A lane's 16 values of one row-term array for tile qt, in accumulator
+  // order.
+  auto rows16 = [&](const float* terms, int qt) {
+    v16f r;
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const float4 a = *reinterpret_cast<const float4*>(&Srow[buf][qt * 32 + 8 * q4 + 4 * g]);
-      const float4 bb = *reinterpret_cast<const float4*>(&Srow[buf][qt * 32 + 8 * q4 + 4 * g + 2]);
-      mmv[4 * q4] = a.x, dlv[4 * q4] = a.y, mmv[4 * q4 + 1] = a.z, dlv[4 * q4 + 1] = a.w;
-      mmv[4 * q4 + 2] = bb.x, dlv[4 * q4 + 2] = bb.y, mmv[4 * q4 + 3] = bb.z, dlv[4 * q4 + 3] = bb.w;
+      const float4 a = *reinterpret_cast<const float4*>(terms + qt * 32 + 8 * q4 + 4 * g);
+      r[4 * q4] = a.x, r[4 * q4 + 1] = a.y, r[4 * q4 + 2] = a.z, r[4 * q4 + 3] = a.w;
     }
+    return r;
   };
   const FragOffsets fo = MakeFragOffsets(lane);
   v16f acc_k[2] = {}, acc_v[2] = {};  // [dt]
 
-  auto query_tile = [&](auto masked, const uint8_t* qtile, const uint8_t* dtile, int buf, int qt,
-                        int r0) {
-    constexpr bool kMask = decltype(masked)::value;
-    v16f sc = {}, dp = {};
+  // A 32-query tile qt: S = Q K^T and dP = dO V^T (eight MFMAs) ...
+  // dP starts at -delta, so the product arrives as dP - delta.
+  auto front = [&](const uint8_t* qtile, const uint8_t* dtile, int buf, int qt, v16f& sc,
+                   v16f& dp) {
+    sc = v16f{};
+    dp = rows16(Sdl[buf], qt);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       sc = Mfma(RowFrag(qtile, fo, 32 * qt, s), kf[s], sc);
       dp = Mfma(RowFrag(dtile, fo, 32 * qt, s), vf[s], dp);
     }
-    float mmv[16], dlv[16];
-    rows16(buf, qt, mmv, dlv);
-    const int lo_rel = r0 + 32 * qt + 4 * g - j;  // query row minus this lane's key
+  };
+  // ... the weights (VALU) and dK^T += Q^T dS, dV^T += dO^T P (eight MFMAs).
+  auto back = [&](const v16f& sc, const v16f& dp, bool masked, const uint8_t* qtile,
+                  const uint8_t* dtile, int buf, int qt, int r0) {
+    const v16f mmv = rows16(Smm[buf], qt);
     float w[16], p[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float e = Exp2(__builtin_fmaf(sc[r], scl, mmv[r]));
-      if constexpr (kMask) {  // keep query row >= j and its start <= j
+    for (int r = 0; r < 16; ++r) p[r] = Exp2(__builtin_fmaf(sc[r], scl, mmv[r]));
+    if (masked) {  // keep query row >= j and its start <= j
+      const int lo_rel = r0 + 32 * qt + 4 * g - j;  // query row minus this lane's key
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
         const int il = qt * 32 + RowConst(r) + 4 * g;
-        e = OrZero(e, Outside(lo_rel + RowConst(r), j - Sst[buf][il]));
+        p[r] = OrZero(p[r], Outside(lo_rel + RowConst(r), j - Sst[buf][il]));
       }
-      p[r] = e;
-      w[r] = e * (dp[r] + dlv[r]);
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) w[r] = p[r] * dp[r];
     bf16x8 wb[2], pb[2];
     PackTile(w, wb);
     PackTile(p, pb);
@@ -664,36 +718,32 @@ Attn16DKDV(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
       }
   };
 
-  issue(0, 0);
+  // Row terms run one block ahead of the tiles (two LDS buffers, by
+  // parity): block ib's are stored during block ib - 1, from a load issued
+  // during block ib - 2.
   if (wave == 0) {
     fetch(0);
     put(0, 0);
     if (1 < nblk) fetch(1);
   }
-  for (int ib = 0; ib < nblk; ++ib) {
+  auto step = [&](int ib, const uint8_t* cur) {
     const int buf = ib & 1;
-    WaitVm<0>();
-    __syncthreads();
-    if (ib + 1 < nblk) {
-      issue(ib + 1, buf ^ 1);
-      if (wave == 0) {
-        put(ib + 1, buf ^ 1);
-        if (ib + 2 < nblk) fetch(ib + 2);
-      }
+    if (wave == 0 && ib + 1 < nblk) {
+      put(ib + 1, buf ^ 1);
+      if (ib + 2 < nblk) fetch(ib + 2);
     }
-    const uint8_t* sb = smem + buf * 2 * kTile;
     const int r0 = (blk_first + ib) * kBlkRows;
     const int smax = Uniform(Smax[buf]);
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const int rt = r0 + 32 * qt;
       if (rt + 31 < jw) continue;  // queries wholly before this wave's keys
-      if (rt >= jw + 31 && rt + 32 <= S && smax <= jw)
-        query_tile(std::false_type{}, sb, sb + kTile, buf, qt, r0);
-      else
-        query_tile(std::true_type{}, sb, sb + kTile, buf, qt, r0);
+      v16f sc, dp;
+      front(cur, cur + kTile, buf, qt, sc, dp);
+      back(sc, dp, !(rt >= jw + 31 && rt + 32 <= S && smax <= jw), cur, cur + kTile, buf, qt, r0);
     }
-  }
+  };
+  RunRing<kStages, 4>(nblk, issue, step, stage);
   if (j >= S) return;
   const float isd = 0.125f;
 #pragma unroll
@@ -723,8 +773,10 @@ hipError_t LaunchAttn16Fwd(const uint16_t* q, const uint16_t* k, const uint16_t*
                            float* stats, size_t B, size_t S, size_t H, const int32_t* starts,
                            hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
+  // Four waves, two stages, four workgroups per CU (measured against 3-4
+  // stages and 8-wave workgroups at B16 H16 S2048).
   const dim3 grid(static_cast<unsigned>((S + 127) / 128 * B * H));
-  hipLaunchKernelGGL((Attn16Fwd<1, 2, 4, 4>), grid, dim3(256), 0, s, q, k, v, o, stats,
+  hipLaunchKernelGGL((Attn16Fwd<4, 2, 4>), grid, dim3(256), 0, s, q, k, v, o, stats,
                      static_cast<int>(S), static_cast<int>(H), starts);
   return hipGetLastError();
 }
@@ -734,8 +786,9 @@ hipError_t LaunchAttn16DQ(const uint16_t* q, const uint16_t* k, const uint16_t* 
                           size_t H, hipStream_t s) {
   if (B * H * S == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((S + kBwdRows - 1) / kBwdRows * B * H));
-  hipLaunchKernelGGL(Attn16DQ<2>, grid, dim3(kBwdWaves * kWave), 0, s, q, k, v, dout, stats, dq,
-                     static_cast<int>(S), static_cast<int>(H));
+  // Three stages, three workgroups per CU (160 VGPRs, 48 KiB of LDS each).
+  hipLaunchKernelGGL((Attn16DQ<3, 3>), grid, dim3(kBwdWaves * kWave), 0, s, q, k, v, dout, stats,
+                     dq, static_cast<int>(S), static_cast<int>(H));
   return hipGetLastError();
 }
 
@@ -745,8 +798,9 @@ hipError_t LaunchAttn16DKDV(const uint16_t* q, const uint16_t* k, const uint16_t
   if (B * H * S == 0) return hipSuccess;
   if (!dk && !dv) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>((S + kBwdRows - 1) / kBwdRows * B * H));
-  hipLaunchKernelGGL(Attn16DKDV<2>, grid, dim3(kBwdWaves * kWave), 0, s, q, k, v, dout, stats,
-                     dk, dv, static_cast<int>(S), static_cast<int>(H));
+  // Two stages, two workgroups per CU (about 200 VGPRs).
+  hipLaunchKernelGGL((Attn16DKDV<2, 2>), grid, dim3(kBwdWaves * kWave), 0, s, q, k, v, dout,
+                     stats, dk, dv, static_cast<int>(S), static_cast<int>(H));
   return hipGetLastError();
 }
 
