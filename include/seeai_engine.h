@@ -48,6 +48,13 @@ int seeai_engine_train_step(seeai_engine* engine, const float* inputs, const voi
 /* The train program again on the batch already staged, no host-to-device
  * copy: the device-resident step. */
 int seeai_engine_train_resident(seeai_engine* engine, float* loss);
+/* Optimizer steps over `batches` consecutive batches (max(1,
+ * grad_accum_steps) per step) with the reference's BatchPipeline overlap
+ * (runtime/pipeline/batch_pipeline.h:13-57): a feeder thread checks and
+ * uploads the next batch while the current step runs.  Bit-identical to
+ * seeai_engine_train_step once per step; one loss per step in `losses`. */
+int seeai_engine_train_steps(seeai_engine* engine, const float* inputs, const void* labels,
+                             uint64_t batches, float* losses);
 int seeai_engine_evaluate(seeai_engine* engine, const float* input, const void* labels,
                           float* loss);
 /* The eval program with its accuracy tally (update_engine.cc:437-565): the

@@ -89,6 +89,24 @@ int seeai_upload(seeai_ctx* ctx, uint64_t arena_offset, const void* src,
                  uint64_t bytes);
 int seeai_download(seeai_ctx* ctx, uint64_t arena_offset, void* dst,
                    uint64_t bytes);
+/* The device side of the feeder (BatchPipeline, runtime/pipeline/
+ * batch_pipeline.h:13-57): a batch is staged while the current step runs --
+ * copied into pinned host memory and uploaded on the feeder's own stream
+ * (default priority) into device staging -- and seeai_feeder_next moves the
+ * oldest staged batch into the arena's I/O slots on the context's stream,
+ * ordered after its upload by an event (update_engine.cc:853-856).  At most
+ * two batches are staged ahead (status 2 on a third).  seeai_feeder_stage
+ * touches only the feeder's own stream and buffers, so the engine's feeder
+ * thread may call it while the context's thread enqueues steps;
+ * seeai_feeder_next belongs to the context's thread.  Staging buffers are
+ * reused only after the arena copy that read them has run on the device. */
+typedef struct seeai_feeder seeai_feeder;
+int seeai_feeder_create(seeai_ctx* ctx, uint64_t input_bytes, uint64_t label_bytes,
+                        seeai_feeder** out);
+void seeai_feeder_destroy(seeai_feeder* feeder);
+const char* seeai_feeder_last_error(const seeai_feeder* feeder);
+int seeai_feeder_stage(seeai_feeder* feeder, const void* input, const void* labels);
+int seeai_feeder_next(seeai_feeder* feeder, uint64_t input_offset, uint64_t label_offset);
 /* The device arena's base (for callers that place tensors themselves). */
 void* seeai_arena(seeai_ctx* ctx);
 uint64_t seeai_arena_bytes(const seeai_ctx* ctx);

@@ -909,6 +909,137 @@ int seeai_download(seeai_ctx* c, uint64_t off, void* dst, uint64_t bytes) {
   return SEEAI_OK;
 }
 
+struct seeai_feeder {
+  seeai_ctx* ctx = nullptr;
+  int device = 0;
+  hipStream_t stream = nullptr;  // the uploads, at the default priority
+  uint64_t input_bytes = 0, label_bytes = 0;
+  uint8_t* pinned[2] = {nullptr, nullptr};  // hipHostMalloc
+  uint8_t* staged[2] = {nullptr, nullptr};  // device
+  hipEvent_t uploaded[2] = {nullptr, nullptr};
+  hipEvent_t consumed[2] = {nullptr, nullptr};  // the arena copy that read the slot
+  bool upload_recorded[2] = {false, false};
+  bool consume_recorded[2] = {false, false};
+  int head = 0, tail = 0, count = 0;  // next slot to stage, next to hand over, staged
+  std::mutex mu;
+  std::string error;
+};
+
+namespace {
+int FeederFail(seeai_feeder* f, int status, const char* what, hipError_t e) {
+  f->error = std::string("feeder: ") + what + ": " + hipGetErrorString(e);
+  return status;
+}
+}  // namespace
+
+int seeai_feeder_create(seeai_ctx* c, uint64_t input_bytes, uint64_t label_bytes,
+                        seeai_feeder** out) {
+  if (!c || !out || input_bytes == 0) return Fail(c, SEEAI_INVALID, "feeder_create: no input slot");
+  *out = nullptr;
+  auto* f = new seeai_feeder;
+  f->ctx = c;
+  f->device = c->device;
+  f->input_bytes = input_bytes;
+  f->label_bytes = label_bytes;
+  const uint64_t bytes = input_bytes + label_bytes;
+  hipError_t e = hipSetDevice(c->device);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&f->stream, hipStreamNonBlocking);
+  for (int s = 0; s < 2 && e == hipSuccess; ++s) {
+    e = hipHostMalloc(reinterpret_cast<void**>(&f->pinned[s]), bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&f->staged[s]), bytes);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&f->uploaded[s], hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&f->consumed[s], hipEventDisableTiming);
+  }
+  if (e != hipSuccess) {
+    seeai_feeder_destroy(f);
+    return Fail(c, SEEAI_HIP_ERROR, "feeder_create: %s", hipGetErrorString(e));
+  }
+  *out = f;
+  return SEEAI_OK;
+}
+
+void seeai_feeder_destroy(seeai_feeder* f) {
+  if (!f) return;
+  (void)hipSetDevice(f->device);
+  if (f->stream) (void)hipStreamSynchronize(f->stream);
+  if (f->ctx && f->ctx->stream) (void)hipStreamSynchronize(f->ctx->stream);
+  for (int s = 0; s < 2; ++s) {
+    if (f->uploaded[s]) (void)hipEventDestroy(f->uploaded[s]);
+    if (f->consumed[s]) (void)hipEventDestroy(f->consumed[s]);
+    if (f->staged[s]) (void)hipFree(f->staged[s]);
+    if (f->pinned[s]) (void)hipHostFree(f->pinned[s]);
+  }
+  if (f->stream) (void)hipStreamDestroy(f->stream);
+  delete f;
+}
+
+const char* seeai_feeder_last_error(const seeai_feeder* f) {
+  return f ? f->error.c_str() : "no feeder";
+}
+
+int seeai_feeder_stage(seeai_feeder* f, const void* input, const void* labels) {
+  if (!f || !input || (f->label_bytes && !labels)) return SEEAI_INVALID;
+  int slot;
+  bool consumed;
+  {
+    std::lock_guard<std::mutex> lock(f->mu);
+    if (f->count == 2) {
+      f->error = "feeder: two batches are already staged";
+      return SEEAI_INVALID;
+    }
+    slot = f->head;
+    consumed = f->consume_recorded[slot];
+  }
+  hipError_t e = hipSetDevice(f->device);
+  if (e != hipSuccess) return FeederFail(f, SEEAI_HIP_ERROR, "set device", e);
+  // The pinned slot's previous upload has left it before it is refilled.
+  if (f->upload_recorded[slot] && (e = hipEventSynchronize(f->uploaded[slot])) != hipSuccess)
+    return FeederFail(f, SEEAI_HIP_ERROR, "upload wait", e);
+  std::memcpy(f->pinned[slot], input, f->input_bytes);
+  if (f->label_bytes) std::memcpy(f->pinned[slot] + f->input_bytes, labels, f->label_bytes);
+  // The device slot is refilled after the arena copy that read it.
+  if (consumed && (e = hipStreamWaitEvent(f->stream, f->consumed[slot], 0)) != hipSuccess)
+    return FeederFail(f, SEEAI_HIP_ERROR, "consume wait", e);
+  if ((e = hipMemcpyAsync(f->staged[slot], f->pinned[slot], f->input_bytes + f->label_bytes,
+                          hipMemcpyHostToDevice, f->stream)) != hipSuccess)
+    return FeederFail(f, SEEAI_HIP_ERROR, "upload", e);
+  if ((e = hipEventRecord(f->uploaded[slot], f->stream)) != hipSuccess)
+    return FeederFail(f, SEEAI_HIP_ERROR, "upload event", e);
+  f->upload_recorded[slot] = true;
+  std::lock_guard<std::mutex> lock(f->mu);
+  f->head ^= 1;
+  ++f->count;
+  return SEEAI_OK;
+}
+
+int seeai_feeder_next(seeai_feeder* f, uint64_t input_off, uint64_t label_off) {
+  if (!f) return SEEAI_INVALID;
+  seeai_ctx* c = f->ctx;
+  if (!c->arena || input_off + f->input_bytes > c->arena_bytes ||
+      (f->label_bytes && label_off + f->label_bytes > c->arena_bytes))
+    return Fail(c, SEEAI_INVALID, "feeder_next: I/O slot outside the arena");
+  int slot;
+  {
+    std::lock_guard<std::mutex> lock(f->mu);
+    if (f->count == 0) return Fail(c, SEEAI_INVALID, "feeder_next: no batch staged");
+    slot = f->tail;
+  }
+  SEEAI_TRY(c, hipStreamWaitEvent(c->stream, f->uploaded[slot], 0), "feeder_next wait");
+  SEEAI_TRY(c, hipMemcpyAsync(c->arena + input_off, f->staged[slot], f->input_bytes,
+                              hipMemcpyDeviceToDevice, c->stream), "feeder_next input");
+  if (f->label_bytes)
+    SEEAI_TRY(c, hipMemcpyAsync(c->arena + label_off, f->staged[slot] + f->input_bytes,
+                                f->label_bytes, hipMemcpyDeviceToDevice, c->stream),
+              "feeder_next labels");
+  SEEAI_TRY(c, hipEventRecord(f->consumed[slot], c->stream), "feeder_next event");
+  c->cvt_key.at = nullptr;  // the arena changed outside the program
+  std::lock_guard<std::mutex> lock(f->mu);
+  f->consume_recorded[slot] = true;
+  f->tail ^= 1;
+  --f->count;
+  return SEEAI_OK;
+}
+
 void* seeai_arena(seeai_ctx* c) { return c ? c->arena : nullptr; }
 uint64_t seeai_arena_bytes(const seeai_ctx* c) { return c ? c->arena_bytes : 0; }
 

@@ -569,7 +569,7 @@ GemmI8DmaKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[slot][i], fb[slot][j], acc[i][j],
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[slot][j], fa[slot][i], acc[i][j],
                                                           0, 0, 0);
   };
   // The next k-step's TM + TN LDS reads spread one per MFMA from the start
@@ -619,74 +619,46 @@ GemmI8DmaKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
   mfmas(0);
   interleave();
   mfmas(1);
-  WaitVm<0>();  // the repeated loads have landed before LDS is reused
-  __syncthreads();  // every wave is done with the stage buffers: reuse them for staging
+  WaitVm<0>();  // the repeated loads have landed before the workgroup ends
 
-  if (acc_out) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-          const int n = n0 + wn + j * 32 + lr;
-          if (m < M && n < N) acc_out[static_cast<size_t>(m) * N + n] = acc[i][j][r];
-        }
-  }
-  // Dequant epilogue through this wave's 32 x WN slice of LDS, 32 rows at a
-  // time, so C leaves in row-contiguous 16-byte stores.
-  constexpr int SLD = WN + 4;
-  static_assert(kWaves * 32 * SLD * 4 <= kStages * kStage, "staging fits in LDS");
-  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
-  const bool vec_out = (N % 4) == 0;
-  float swv[TN];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = n0 + wn + j * 32 + lr;
-    swv[j] = n < N ? sw[n] : 0.0f;
-  }
+  // The products are C^T tiles (W fragments as the A operand): lane (h, lr)
+  // holds columns n = 32 j + 8 q + 4 h + e, e < 4, of row m = 32 i + lr --
+  // four consecutive floats of one C row, stored as 16 bytes straight from
+  // registers.
+  const bool vec_out = (N % 4) == 0 && ((reinterpret_cast<uintptr_t>(C) |
+                                         reinterpret_cast<uintptr_t>(sw) |
+                                         reinterpret_cast<uintptr_t>(acc_out)) & 15) == 0;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int mb = m0 + wm + i * 32;
+    const int m = m0 + wm + i * 32 + lr;
+    if (m >= M) continue;
+    const float s_a = sa[m];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int m4 = mb + 8 * q + 4 * h;
-      float sav[4];
-      if (m4 + 3 < M && (M % 4) == 0) {
-        const float4 v = *reinterpret_cast<const float4*>(sa + m4);
-        sav[0] = v.x, sav[1] = v.y, sav[2] = v.z, sav[3] = v.w;
-      } else {
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sav[e] = m4 + e < M ? sa[m4 + e] : 0.0f;
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn + j * 32 + 8 * q + 4 * h;
+        const size_t at = static_cast<size_t>(m) * N + n;
+        const v16i& a = acc[i][j];
+        if (vec_out && n + 3 < N) {
+          const float4 s4 = *reinterpret_cast<const float4*>(sw + n);
+          *reinterpret_cast<float4*>(C + at) =
+              make_float4((static_cast<float>(a[4 * q]) * s_a) * s4.x,
+                          (static_cast<float>(a[4 * q + 1]) * s_a) * s4.y,
+                          (static_cast<float>(a[4 * q + 2]) * s_a) * s4.z,
+                          (static_cast<float>(a[4 * q + 3]) * s_a) * s4.w);
+          if (acc_out)
+            *reinterpret_cast<int4*>(acc_out + at) =
+                make_int4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (n + e >= N) continue;
+            C[at + e] = (static_cast<float>(a[4 * q + e]) * s_a) * sw[n + e];
+            if (acc_out) acc_out[at + e] = a[4 * q + e];
+          }
+        }
       }
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          stage[(8 * q + 4 * h + e) * SLD + j * 32 + lr] =
-              (static_cast<float>(acc[i][j][4 * q + e]) * sav[e]) * swv[j];
-    }
-    __builtin_amdgcn_wave_barrier();
-    constexpr int kVecRow = WN / 4;  // float4 per staged row
-#pragma unroll
-    for (int t = 0; t < 32 * kVecRow / kWave; ++t) {
-      const int idx = lane + t * kWave;
-      const int row = idx / kVecRow, c4 = idx % kVecRow;
-      const int m = mb + row, n = n0 + wn + c4 * 4;
-      const float4 v = *reinterpret_cast<const float4*>(stage + row * SLD + c4 * 4);
-      if (m >= M) continue;
-      float* dst = C + static_cast<size_t>(m) * N + n;
-      if (vec_out && n + 3 < N) {
-        *reinterpret_cast<float4*>(dst) = v;
-      } else {
-        if (n < N) dst[0] = v.x;
-        if (n + 1 < N) dst[1] = v.y;
-        if (n + 2 < N) dst[2] = v.z;
-        if (n + 3 < N) dst[3] = v.w;
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
   }
 }
 

@@ -15,6 +15,7 @@ not been built raises ``ImportError`` -- there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes as C
+import importlib
 import os
 import struct
 
@@ -82,6 +83,11 @@ EXPORTS = {
     "seeai_bind": (_I, [_P, _U64, _P, _U64]),
     "seeai_bind_source": (_I, [_P, _P, _U64]),
     "seeai_upload": (_I, [_P, _U64, _P, _U64]),
+    "seeai_feeder_create": (_I, [_P, _U64, _U64, _P]),
+    "seeai_feeder_destroy": (None, [_P]),
+    "seeai_feeder_last_error": (C.c_char_p, [_P]),
+    "seeai_feeder_stage": (_I, [_P, _P, _P]),
+    "seeai_feeder_next": (_I, [_P, _U64, _U64]),
     "seeai_download": (_I, [_P, _U64, _P, _U64]),
     "seeai_arena": (_P, [_P]),
     "seeai_arena_bytes": (_U64, [_P]),
@@ -127,6 +133,7 @@ ENGINE_EXPORTS = {
     "seeai_engine_header": (_I, [_P, _P]),
     "seeai_engine_train_step": (_I, [_P, _P, _P, C.POINTER(_F)]),
     "seeai_engine_train_resident": (_I, [_P, C.POINTER(_F)]),
+    "seeai_engine_train_steps": (_I, [_P, _P, _P, _U64, _P]),
     "seeai_engine_evaluate": (_I, [_P, _P, _P, C.POINTER(_F)]),
     "seeai_engine_evaluate_metrics": (_I, [_P, _P, _P, C.POINTER(_F), C.POINTER(_U64),
                                           C.POINTER(_U64)]),
@@ -411,6 +418,23 @@ class Engine:
         self._check(_lib.seeai_engine_train_step(
             self.h, x.ctypes.data, None if lab is None else lab.ctypes.data, C.byref(loss)))
         return loss.value
+
+    def train_steps(self, inputs, labels=None):
+        """Optimizer steps over consecutive batches (inputs[b], labels[b]),
+        the next batch's upload overlapping the current step; returns one
+        loss per step."""
+        import numpy as np
+        x = np.ascontiguousarray(inputs, np.float32)
+        lab = None if labels is None else np.ascontiguousarray(labels)
+        batches = x.shape[0]
+        pw = importlib.import_module("see-ai_amd.planwriter")
+        fields = dict(zip(pw.HEADER_NAMES, struct.unpack(pw.HEADER_FORMAT, self.header())))
+        micro = max(1, fields["grad_accum_steps"])
+        losses = np.zeros(batches // micro, np.float32)
+        self._check(_lib.seeai_engine_train_steps(
+            self.h, x.ctypes.data, None if lab is None else lab.ctypes.data, batches,
+            losses.ctypes.data))
+        return losses
 
     def train_resident(self) -> float:
         loss = _F(0.0)

@@ -96,6 +96,12 @@ int seeai_engine_train_step(seeai_engine* e, const float* inputs, const void* la
   return Report(e, r);
 }
 
+int seeai_engine_train_steps(seeai_engine* e, const float* inputs, const void* labels,
+                             uint64_t batches, float* losses) {
+  if (!e || !inputs || !losses) return SEEAI_INVALID;
+  return Report(e, e->engine->TrainSteps(inputs, labels, batches, losses));
+}
+
 int seeai_engine_train_resident(seeai_engine* e, float* loss) {
   if (!e) return SEEAI_INVALID;
   auto r = e->engine->TrainStepResident();

@@ -2,8 +2,12 @@
 #include "engine.h"
 
 #include <cmath>
+#include <condition_variable>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
 
 #include "seeai_hip.h"
 
@@ -87,6 +91,7 @@ Result<std::unique_ptr<PlanEngine>> PlanEngine::Load(std::span<const uint8_t> bl
 }
 
 PlanEngine::~PlanEngine() {
+  seeai_feeder_destroy(feeder_);  // before the context it copies into
   backend_.reset();  // the backend's views die before the memory they view
   std::free(arena_);
 }
@@ -106,9 +111,8 @@ float PlanEngine::EffectiveLr() const {
   return floor + (base - floor) * 0.5f * (1.0f + std::cos(kPi * t));
 }
 
-Result<void> PlanEngine::Stage(const float* input, const void* labels) {
+Result<void> PlanEngine::CheckBatch(const float* input, const void* labels) const {
   const PlanHeader& h = plan_.header;
-  const uint64_t in_off = RefOffset(h.input_ref), in_bytes = h.input_floats * sizeof(float);
   if (h.input_kind == 1) {
     // The feeder's token contract: every id indexes an embedding row.
     const auto* tok = reinterpret_cast<const int32_t*>(input);
@@ -117,8 +121,6 @@ Result<void> PlanEngine::Stage(const float* input, const void* labels) {
         return Fail("token " + std::to_string(tok[i]) + " at position " + std::to_string(i) +
                     " is outside the plan's " + std::to_string(vocab_bound_) + "-token vocabulary");
   }
-  std::memcpy(arena_ + in_off, input, in_bytes);
-  if (auto r = backend_->SyncToDevice(in_off, in_bytes); !r) return r;
   if (h.label_kind == 0) return {};
   if (!labels) return Fail("this plan trains on labels: none were staged");
   if (h.label_kind == 1) {
@@ -132,6 +134,16 @@ Result<void> PlanEngine::Stage(const float* input, const void* labels) {
         return Fail("label " + std::to_string(lab[i]) + " at position " + std::to_string(i) +
                     " is outside the plan's " + std::to_string(num_classes_) + " classes");
   }
+  return {};
+}
+
+Result<void> PlanEngine::Stage(const float* input, const void* labels) {
+  const PlanHeader& h = plan_.header;
+  if (auto r = CheckBatch(input, labels); !r) return r;
+  const uint64_t in_off = RefOffset(h.input_ref), in_bytes = h.input_floats * sizeof(float);
+  std::memcpy(arena_ + in_off, input, in_bytes);
+  if (auto r = backend_->SyncToDevice(in_off, in_bytes); !r) return r;
+  if (h.label_kind == 0) return {};
   const uint64_t lab_off = RefOffset(h.label_ref);
   std::memcpy(arena_ + lab_off, labels, h.label_bytes);
   return backend_->SyncToDevice(lab_off, h.label_bytes);
@@ -180,6 +192,11 @@ Result<float> PlanEngine::Loss() {
 Result<float> PlanEngine::TrainStep(const float* inputs, const void* labels) {
   const PlanHeader& h = plan_.header;
   const uint64_t micro = h.grad_accum_steps > 1 ? h.grad_accum_steps : 1;
+  // A refused batch refuses the step before it runs: no timestep is spent.
+  for (uint64_t g = 0; g < micro; ++g) {
+    const auto* lab = labels ? static_cast<const uint8_t*>(labels) + g * h.label_bytes : nullptr;
+    if (auto r = CheckBatch(inputs + g * h.input_floats, lab); !r) return Fail(r.error());
+  }
   ++step_;  // the 1-indexed timestep of this optimizer step
   double loss_sum = 0.0;
   for (uint64_t g = 0; g < micro; ++g) {
@@ -193,6 +210,96 @@ Result<float> PlanEngine::TrainStep(const float* inputs, const void* labels) {
   if (!plan_.step.empty())
     if (auto r = ExecuteRange(plan_.step, 0, plan_.step.size()); !r) return Fail(r.error());
   return static_cast<float>(loss_sum / static_cast<double>(micro));
+}
+
+Result<void> PlanEngine::TrainSteps(const float* inputs, const void* labels, uint64_t batches,
+                                    float* losses) {
+  const PlanHeader& h = plan_.header;
+  const uint64_t micro = h.grad_accum_steps > 1 ? h.grad_accum_steps : 1;
+  if (!inputs || !losses || batches == 0 || batches % micro != 0)
+    return Fail("train_steps takes a whole number of optimizer steps' batches (" +
+                std::to_string(micro) + " per step)");
+  if (h.label_kind != 0 && !labels) return Fail("this plan trains on labels: none were staged");
+  const uint64_t in_bytes = h.input_floats * sizeof(float);
+  const uint64_t lab_bytes = h.label_kind != 0 ? h.label_bytes : 0;
+  const uint64_t in_off = RefOffset(h.input_ref), lab_off = lab_bytes ? RefOffset(h.label_ref) : 0;
+  seeai_ctx* ctx = backend_->context();
+  if (!feeder_ && seeai_feeder_create(ctx, in_bytes, lab_bytes, &feeder_) != SEEAI_OK)
+    return Fail(std::string("backend 'hip' failed to create the feeder: ") + seeai_last_error(ctx));
+
+  // The feeder thread stays at most two batches ahead of the steps (the
+  // device feeder's two slots); `taken` counts batches moved into the slots.
+  std::mutex mu;
+  std::condition_variable cv;
+  uint64_t staged = 0, taken = 0;
+  bool stop = false;
+  std::string feeder_error;
+  std::thread feeder([&] {
+    for (uint64_t b = 0; b < batches; ++b) {
+      {
+        std::unique_lock<std::mutex> lk(mu);
+        cv.wait(lk, [&] { return stop || staged - taken < 2; });
+        if (stop) return;
+      }
+      const float* in = inputs + b * h.input_floats;
+      const void* lab = lab_bytes ? static_cast<const uint8_t*>(labels) + b * h.label_bytes : nullptr;
+      std::string err;
+      if (auto r = CheckBatch(in, lab); !r)
+        err = r.error();
+      else if (seeai_feeder_stage(feeder_, in, lab) != SEEAI_OK)
+        err = seeai_feeder_last_error(feeder_);
+      std::lock_guard<std::mutex> lk(mu);
+      if (!err.empty()) {
+        feeder_error = "batch " + std::to_string(b) + ": " + err;
+        stop = true;
+        cv.notify_all();
+        return;
+      }
+      ++staged;
+      cv.notify_all();
+    }
+  });
+  // Every exit joins the feeder (batch_pipeline.h's destructor contract).
+  auto finish = [&](Result<void> r) -> Result<void> {
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      stop = true;
+    }
+    cv.notify_all();
+    feeder.join();
+    return r;
+  };
+  for (uint64_t s = 0; s < batches / micro; ++s) {
+    double loss_sum = 0.0;
+    for (uint64_t g = 0; g < micro; ++g) {
+      bool starved;
+      std::string why;
+      {
+        std::unique_lock<std::mutex> lk(mu);
+        cv.wait(lk, [&] { return stop || staged > taken; });
+        starved = staged == taken;
+        why = feeder_error;
+      }
+      if (starved) return finish(Fail(why));  // finish takes the lock itself
+      if (g == 0) ++step_;  // the 1-indexed timestep of this optimizer step
+      if (seeai_feeder_next(feeder_, in_off, lab_off) != SEEAI_OK)
+        return finish(Fail(std::string("backend 'hip' failed to feed the batch: ") +
+                           seeai_last_error(ctx)));
+      {
+        std::lock_guard<std::mutex> lk(mu);
+        ++taken;
+      }
+      cv.notify_all();
+      if (auto r = ExecuteRange(plan_.train, 0, plan_.train.size()); !r) return finish(Fail(r.error()));
+      auto loss = Loss();
+      if (!loss) return finish(Fail(loss.error()));
+      loss_sum += *loss;
+    }
+    if (!plan_.step.empty())
+      if (auto r = ExecuteRange(plan_.step, 0, plan_.step.size()); !r) return finish(Fail(r.error()));
+    losses[s] = static_cast<float>(loss_sum / static_cast<double>(micro));
+  }
+  return finish({});
 }
 
 Result<float> PlanEngine::TrainStepResident() {

@@ -15,6 +15,8 @@
 #include "plan.h"
 #include "result.h"
 
+struct seeai_feeder;
+
 namespace seeai::host {
 
 class PlanEngine {
@@ -44,6 +46,17 @@ class PlanEngine {
   // that many batches of input_floats floats, `labels` as many batches of
   // label_bytes.  Returns the micro-batches' mean loss.
   Result<float> TrainStep(const float* inputs, const void* labels);
+  // Optimizer steps over `batches` consecutive batches (each step takes
+  // max(1, grad_accum_steps) of them), fed as the reference's BatchPipeline
+  // feeds them (runtime/pipeline/batch_pipeline.h:13-57): a feeder thread
+  // checks and stages batch b + 1 -- pinned copy, upload on the feeder's
+  // own stream -- while the step on batch b runs, and each step begins by
+  // moving its staged batch into the I/O slots behind the upload's event.
+  // The batches and their order are TrainStep's, so the results are bit
+  // for bit those of calling TrainStep once per step.  One loss per step
+  // lands in `losses`.  The host mirror's I/O slots are not refreshed.
+  Result<void> TrainSteps(const float* inputs, const void* labels, uint64_t batches,
+                          float* losses);
   // Runs the train program again on the batch already staged (the bench's
   // device-resident step: no host-to-device copy inside the step).
   Result<float> TrainStepResident();
@@ -77,6 +90,8 @@ class PlanEngine {
  private:
   PlanEngine() = default;
   Result<void> Stage(const float* input, const void* labels);
+  // The feeder's token and label contracts on one batch.
+  Result<void> CheckBatch(const float* input, const void* labels) const;
   Result<void> ExecuteRange(const std::vector<Instruction>& program, size_t begin, size_t end);
   Result<float> Loss();
 
@@ -96,6 +111,7 @@ class PlanEngine {
   uint64_t eval_probs_off_ = 0, eval_rows_ = 0, eval_cols_ = 0;
   bool eval_probs_ = false;
   uint64_t source_bytes_ = 0;     // bytes of the bound source model
+  seeai_feeder* feeder_ = nullptr;  // TrainSteps' device staging, made on first use
 };
 
 }  // namespace seeai::host

@@ -111,6 +111,7 @@ def test_label_outside_the_classes_is_refused(hip, torch_cuda, c1):
         eng.train_step(x, y)
     assert err.value.status == hip.INVALID
     assert "label 256 at position 5" in str(err.value)
+    assert eng.step == 0  # the refused step spent no timestep
     eng.close()
 
 
