@@ -165,6 +165,9 @@ typedef struct seeai_tile_policy {
                                      conversion (default 8, <= 64) */
   uint32_t exact_longk_first;     /* exact skinny long-K GEMM: 1 the two-pass form before the
                                      chain kernel (default), 2 the chain kernel first */
+  uint32_t relaxed_tile_192;      /* relaxed bf16 GEMM below the 256x256 threshold: 1 128x192
+                                     tiles where they take fewer CU rounds per unit of work than
+                                     128x128, 2 never (default), 3 always (N >= 192) */
 } seeai_tile_policy;
 /* NULL restores the defaults; an out-of-range field is status 2 and leaves
  * the policy in force unchanged. */

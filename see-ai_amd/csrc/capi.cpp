@@ -1390,6 +1390,9 @@ int seeai_configure(seeai_ctx* c, const seeai_tile_policy* p) {
     if (p->exact_longk_first > 2)
       return Fail(c, SEEAI_INVALID, "tile policy: exact_longk_first %u is not 1 or 2",
                   p->exact_longk_first);
+    if (p->relaxed_tile_192 > 3)
+      return Fail(c, SEEAI_INVALID, "tile policy: relaxed_tile_192 %u is not 1, 2 or 3",
+                  p->relaxed_tile_192);
     if (p->relaxed_min_fill_256 > 100)
       return Fail(c, SEEAI_INVALID, "tile policy: relaxed_min_fill_256 %u exceeds 100 percent",
                   p->relaxed_min_fill_256);
@@ -1407,6 +1410,7 @@ int seeai_configure(seeai_ctx* c, const seeai_tile_policy* p) {
     if (p->relaxed_nt_dma_min_k) t.relaxed_nt_dma_min_k = p->relaxed_nt_dma_min_k;
     if (p->convert_wgs_per_cu) t.convert_wgs_per_cu = static_cast<int>(p->convert_wgs_per_cu);
     if (p->exact_longk_first) t.exact_longk_first = static_cast<int>(p->exact_longk_first);
+    if (p->relaxed_tile_192) t.relaxed_tile_192 = static_cast<int>(p->relaxed_tile_192);
   }
   c->policy = t;
   return SEEAI_OK;
@@ -1422,6 +1426,7 @@ int seeai_policy(const seeai_ctx* c, seeai_tile_policy* out) {
   out->relaxed_nt_dma_min_k = static_cast<uint32_t>(c->policy.relaxed_nt_dma_min_k);
   out->convert_wgs_per_cu = static_cast<uint32_t>(c->policy.convert_wgs_per_cu);
   out->exact_longk_first = static_cast<uint32_t>(c->policy.exact_longk_first);
+  out->relaxed_tile_192 = static_cast<uint32_t>(c->policy.relaxed_tile_192);
   return SEEAI_OK;
 }
 

@@ -222,6 +222,10 @@ struct TilePolicy {
   int convert_wgs_per_cu = 8;          // workgroups per CU of the activation conversion
   int exact_longk_first = 1;           // exact skinny long-K GEMM: 1 the two-pass workspace
                                        // form before the chain kernel, 2 the chain kernel first
+  int relaxed_tile_192 = 2;            // relaxed bf16 GEMM below 256 x 256: 1 128 x 192 tiles
+                                       // when they take fewer CU rounds per unit of work,
+                                       // 2 never (default: measured slower on the decoder's
+                                       // 8192 x 768 products), 3 always (N >= 192)
 };
 
 struct GemmArgs {

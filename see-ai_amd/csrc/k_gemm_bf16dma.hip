@@ -255,13 +255,19 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
   const float* __restrict__ bias = g.bias;
   float* __restrict__ C = g.C;
   constexpr int kVecRow = WN / 4;
-  static_assert(kWave % kVecRow == 0, "a lane keeps one column quad through the epilogue");
+  // A lane keeps one column quad through the epilogue: kRowsPerPass rows of
+  // kVecRow quads per pass (lanes past them idle where kVecRow does not
+  // divide the wave).
+  constexpr int kRowsPerPass = kWave / kVecRow;
+  static_assert(kRowsPerPass >= 1 && 32 % kRowsPerPass == 0, "epilogue passes cover 32 rows");
+  const int c4 = lane % kVecRow, row0 = lane / kVecRow;
+  const bool epi_lane = lane < kRowsPerPass * kVecRow;
   // Low-rank epilogue: this lane's four columns of the rank operand, every k,
   // in registers for the whole epilogue (its column quad never changes).
   float lb[4][kLowRankMaxK];
   const int lr_r = kLR ? g.lr_k : 0;
   if constexpr (kLR != 0) {
-    const int nl = n0 + wn + (lane % kVecRow) * 4;
+    const int nl = n0 + wn + c4 * 4;
 #pragma unroll
     for (int k = 0; k < kLowRankMaxK; ++k) {
       float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -289,11 +295,10 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
         for (int e = 0; e < 4; ++e) stage[(8 * q + 4 * h + e) * SLD + j * 32 + lr] = acc[i][j][4 * q + e];
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int t = 0; t < 32 * kVecRow / kWave; ++t) {
-      const int idx = lane + t * kWave;
-      const int row = idx / kVecRow, c4 = idx % kVecRow;
+    for (int t = 0; t < 32 / kRowsPerPass; ++t) {
+      const int row = row0 + t * kRowsPerPass;
       const int m = mb + row, n = n0 + wn + c4 * 4;
-      if (m >= M || n >= N) continue;
+      if (!epi_lane || m >= M || n >= N) continue;
       float v[4];
       const float4 s4 = *reinterpret_cast<const float4*>(stage + row * SLD + c4 * 4);
       v[0] = s4.x, v[1] = s4.y, v[2] = s4.z, v[3] = s4.w;
@@ -535,6 +540,19 @@ hipError_t LaunchGemmBf16Dma(const void* A, const void* W, const GemmArgs& a, hi
   const size_t rounds = (t256 + cus - 1) / cus;
   const bool full = 100 * t256 >= static_cast<size_t>(fill) * rounds * cus;
   if (t256 >= min256 && full) return Launch<256, 256, 2, 4, 4>(Ab, Wb, Kp, a, s);
+  // Below that, 128 x 128; the policy can take 128 x 192 (four waves of
+  // 64 x 96, three stages) where it needs fewer rounds of tiles over the CUs
+  // per unit of work (8192 x 768: 256 tiles instead of 384) -- measured
+  // slower there on MI355X (one wave per SIMD against two workgroups of
+  // 128 x 128 per CU), so not by default.
+  const size_t t128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+  const size_t t192 = ((a.M + 127) / 128) * ((a.N + 191) / 192);
+  const size_t r128 = (t128 + 2 * cus - 1) / (2 * cus), r192 = (t192 + 2 * cus - 1) / (2 * cus);
+  const size_t c128 = std::max<size_t>(1, (t128 + cus - 1) / cus) * 2,
+               c192 = std::max<size_t>(1, (t192 + cus - 1) / cus) * 3;  // CU-rounds x tile area / 8192
+  const int mode = a.policy ? a.policy->relaxed_tile_192 : 2;
+  if (a.N >= 192 && (mode == 3 || (mode == 1 && (c192 < c128 || (c192 == c128 && r192 <= r128)))))
+    return Launch<128, 192, 2, 2, 3>(Ab, Wb, Kp, a, s);
   return Launch<128, 128, 2, 2, 4>(Ab, Wb, Kp, a, s);
 }
 

@@ -67,7 +67,7 @@ class TilePolicy(C.Structure):
                 ("quantize_waves_per_cu", C.c_uint32), ("relaxed_min_tiles_256", C.c_uint32),
                 ("relaxed_min_fill_256", C.c_uint32), ("relaxed_nt_dma_min_k", C.c_uint32),
                 ("convert_wgs_per_cu", C.c_uint32),
-                ("exact_longk_first", C.c_uint32)]
+                ("exact_longk_first", C.c_uint32), ("relaxed_tile_192", C.c_uint32)]
 
 
 # Every exported symbol with its ctypes signature: the header, one to one.

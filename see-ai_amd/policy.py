@@ -50,6 +50,9 @@ FIELDS = {
     "exact_longk_first": (1, ("choice", 1, 2),
                           "exact skinny long-K GEMM: 1 two-pass workspace form first, "
                           "2 chain kernel first"),
+    "relaxed_tile_192": (2, ("choice", 1, 2, 3),
+                         "relaxed bf16 GEMM below 256x256: 1 128x192 tiles where they take fewer "
+                         "CU rounds per unit of work, 2 never, 3 always (N >= 192)"),
 }
 DEFAULTS = {k: v[0] for k, v in FIELDS.items()}
 

@@ -48,6 +48,7 @@ ARMS = {
     "relaxed_nt_dma_min_k": [512, 768, 1024, 4096],
     "convert_wgs_per_cu": [2, 4, 8, 16, 32],
     "exact_longk_first": [1, 2],
+    "relaxed_tile_192": [1, 2, 3],
 }
 
 
@@ -155,7 +156,7 @@ class Bench:
                     return (lambda: ctx.call("seeai_w8a8_quantize_rows", X.data_ptr(), Q.data_ptr(),
                                              s.data_ptr(), rows, cols), 5.0 * rows * cols, keep)
                 yield f"quantize {rows}x{cols}", setup
-        elif field in ("relaxed_min_tiles_256", "relaxed_min_fill_256"):
+        elif field in ("relaxed_min_tiles_256", "relaxed_min_fill_256", "relaxed_tile_192"):
             # The decoder steps' relaxed frozen-weight products (q8, column
             # scales, weights in rodata) -- NN forward and NT dX shapes, the
             # vocabulary head among them.

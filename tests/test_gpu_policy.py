@@ -91,8 +91,8 @@ def test_quantizer_wave_counts_are_bitwise_equal(hip, ctx, torch_cuda, rows, col
 
 @pytest.mark.parametrize("nt", [0, 1])
 def test_relaxed_tile_arms_are_bitwise_equal(hip, torch_cuda, nt):
-    """The relaxed frozen-weight product on 256 x 256 and on 128 x 128 tiles
-    (K >= 1024: NT takes the direct-to-LDS kernel from there)."""
+    """The relaxed frozen-weight product on 256 x 256, 128 x 192 and 128 x 128
+    tiles (K >= 1024: NT takes the direct-to-LDS kernel from there)."""
     M, N, K = 640, 768, 1024
     r = rng(11 + nt)
     A = r.standard_normal((M, K)).astype(np.float32)
@@ -108,6 +108,8 @@ def test_relaxed_tile_arms_are_bitwise_equal(hip, torch_cuda, nt):
     outs = []
     for arm in ({"relaxed_min_tiles_256": 1}, {"relaxed_min_tiles_256": 1 << 30}, None,
                 {"relaxed_min_tiles_256": 1, "relaxed_min_fill_256": 100},
+                {"relaxed_min_tiles_256": 1 << 30, "relaxed_tile_192": 2},
+                {"relaxed_min_tiles_256": 1 << 30, "relaxed_tile_192": 3},
                 {"convert_wgs_per_cu": 1}, {"convert_wgs_per_cu": 64}):
         be = hip.HipBackend(0)
         be.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
