@@ -54,20 +54,32 @@ def parse():
                         "(the counter calibration: a copy's known bytes)")
     p.add_argument("--attn-probe", action="store_true",
                    help="for rocprofv3 runs: BASELINE configs[2] attention fwd+bwd, bf16 x3, f32 x1")
-    p.add_argument("--lora-probe", nargs="?", const="c4", choices=["c4", "c5"],
+    p.add_argument("--lora-probe", nargs="?", const="c4", choices=["c1", "c4", "c5"],
                    help="for rocprofv3 runs: BASELINE configs[3] (c4) or configs[4] (c5) decoder "
                         "LoRA plan, one staged step then resident steps (relaxed family)")
     return p.parse_args()
 
 
 def lora_probe(which: str):
-    """BASELINE configs[3] (c4) or configs[4] (c5) through the plan engine
-    for the profilers: build the decoder LoRA plan, one staged step, then
-    resident steps (five for c4, two for c5)."""
+    """BASELINE configs[0] (c1), configs[3] (c4) or configs[4] (c5) through
+    the plan engine for the profilers: build the LoRA plan, one staged step,
+    then resident steps (200 for c1, five for c4, two for c5)."""
     import numpy as np
     import torch
     hip = importlib.import_module("see-ai_amd.hip")
     pw = importlib.import_module("see-ai_amd.planwriter")
+    if which == "c1":
+        eng = hip.Engine(pw.mlp_lora(hip.plan_self_hash).blob)
+        eng.train_step(pw.normal(1, (32, 256)), pw.uniform_ints(2, 32, 256))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(200):
+            loss = eng.train_resident()
+        dt = (time.perf_counter() - t0) / 200
+        eng.close()
+        print(f"lora probe: LoRA MLP (c1), 200 resident steps, {dt * 1e6:.1f} us/step, "
+              f"loss {loss:.5f}", flush=True)
+        return 0
     if which == "c5":
         img, T, n = pw.decoder_q8_lora(hip.plan_self_hash, relaxed=True), 4 * 2048, 2
     else:
