@@ -294,6 +294,7 @@ int GemmBf16Dma(seeai_ctx* c, GemmArgs& a, const char* what) {
   const size_t need = a.M * Bf16DmaKp(a.K) * 2;
   if (!ConvertedAlready(c, a)) {
     if (need > c->cvt_bytes) {  // grow after draining the stream
+      c->cvt_key.at = nullptr;
       SEEAI_TRY(c, hipStreamSynchronize(c->stream), "conversion buffer drain");
       if (c->cvt) SEEAI_TRY(c, hipFree(c->cvt), "conversion buffer free");
       c->cvt = nullptr;
@@ -1348,9 +1349,57 @@ int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params
   return rc;
 }
 
+namespace {
+// A range's workspaces at their largest before its first instruction runs:
+// the exact family's reduction scratch, the relaxed products' conversion
+// buffer and their weights' bf16 shadows are sized (and the shadows made)
+// here, so no instruction of the range drains the stream to allocate.
+int PresizeWorkspaces(seeai_ctx* c, const uint8_t* prog, uint64_t begin, uint64_t end) {
+  size_t scratch = 0, cvt = 0;
+  for (uint64_t i = begin; i < end; ++i) {
+    Instruction ins;
+    std::memcpy(&ins, prog + i * sizeof(Instruction), sizeof ins);
+    if (ins.opcode == 11 || ins.opcode == 51)  // softmax-xent forward (+masked): row partials
+      scratch = std::max(scratch, XEntFwdScratchBytes(ins.out[0]));
+    GemmArgs a{};
+    if (!DecodeGemm(c, ins, &a)) continue;
+    a.relaxed = (ins.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
+    a.policy = &c->policy;
+    if (a.relaxed && c->allow_dma && Bf16DmaFits(a) && Immutable(c, a.B)) {
+      cvt = std::max(cvt, static_cast<size_t>(a.M * Bf16DmaKp(a.K) * 2));
+      const auto key = std::make_tuple(a.B, a.layout, a.b_kind, static_cast<uint64_t>(a.N),
+                                       static_cast<uint64_t>(a.K));
+      if (c->shadows.find(key) == c->shadows.end()) {
+        void* shadow = nullptr;
+        SEEAI_TRY(c, hipMalloc(&shadow, a.N * Bf16DmaKp(a.K) * 2), "weight shadow alloc");
+        c->shadows[key] = shadow;
+        SEEAI_TRY(c, LaunchWeightShadow(a, shadow, c->stream), "weight shadow");
+      }
+    } else if (!a.relaxed) {
+      scratch = std::max(scratch, GemmExactScratchBytes(a));
+    }
+  }
+  {  // at least the initial size: the norm and clip partials take 8 KiB
+    void* ws;
+    if (int rc = Scratch(c, std::max(scratch, kInitialScratch), &ws)) return rc;
+  }
+  if (cvt > c->cvt_bytes) {
+    SEEAI_TRY(c, hipStreamSynchronize(c->stream), "conversion buffer drain");
+    if (c->cvt) SEEAI_TRY(c, hipFree(c->cvt), "conversion buffer free");
+    c->cvt = nullptr;
+    c->cvt_bytes = 0;
+    SEEAI_TRY(c, hipMalloc(&c->cvt, cvt), "conversion buffer alloc");
+    c->cvt_bytes = cvt;
+  }
+  return SEEAI_OK;
+}
+}  // namespace
+
 int seeai_begin_range(seeai_ctx* c, const void* program, uint64_t count, uint64_t begin,
                       uint64_t end) {
   if (!c || (!program && count) || begin > end || end > count) return SEEAI_INVALID;
+  if (c->arena)
+    if (int rc = PresizeWorkspaces(c, static_cast<const uint8_t*>(program), begin, end)) return rc;
   c->prog_hash = ProgramHash(static_cast<const uint8_t*>(program), count);
   c->prog = static_cast<const uint8_t*>(program);
   c->prog_count = count;

@@ -325,6 +325,37 @@ __global__ void __launch_bounds__(kThreads) GemmPanelKernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// NT over few outputs (the small-batch plans' dX and dt products): the
+// reference's eight chains per output (lane l adds the products of k = l
+// mod 8 in k order) each get a lane of their own, 32 outputs per workgroup,
+// reading A's and B's rows straight from memory (the eight lanes of an
+// output read eight consecutive words); the eight chains then add in lane
+// order, alpha multiplies, the epilogue follows -- the panel kernel's
+// expression, spread over 8 x more lanes.
+// ---------------------------------------------------------------------------
+template <int kBKind>
+__global__ void __launch_bounds__(kThreads) GemmNTLanesKernel(GemmArgs g) {
+  __shared__ float part[kThreads];
+  const int tid = threadIdx.x, l = tid % 8;
+  const size_t o = static_cast<size_t>(blockIdx.x) * (kThreads / 8) + tid / 8;
+  const size_t MN = g.M * g.N;
+  const bool live = o < MN;
+  const size_t m = live ? o / g.N : 0, n = live ? o % g.N : 0;
+  float chain = 0.0f;
+  if (live)
+    for (size_t k = l; k < g.K; k += 8)
+      chain = Add(chain, Mul(LoadA<1>(g, m, k), LoadB<1, kBKind>(g.B, g.N, g.K, n, k, g.b_col_scale)));
+  part[tid] = chain;
+  __syncthreads();
+  if (!live || l != 0) return;
+  float c = part[tid];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) c = Add(c, part[tid + j]);
+  c = Mul(g.alpha_dot, c);
+  g.C[m * g.N + n] = Epilogue(g, m, n, c);
+}
+
+// ---------------------------------------------------------------------------
 // Rank-r products (K <= 32, f32 B, N % 4 == 0: the LoRA site's s (t B) + C
 // and dt A^T + dX, wide outputs over a tiny reduction).  The output and the
 // addend are the traffic, so a lane owns four consecutive outputs of one
@@ -1133,9 +1164,41 @@ hipError_t LaunchChain(const GemmArgs& a, hipStream_t s) {
 
 bool LongK(const GemmArgs& a) { return a.layout != 1 && a.M * a.N <= 16384 && a.K >= 1024; }
 
+// Short reductions over few outputs (the small-batch plans' products, e.g.
+// 32 x 8 over K = 512): the panel kernel would give the whole GEMM a handful
+// of workgroups, each lane running its output's chain alone; the two-pass
+// workspace form spreads the quads over the machine and folds them in k
+// order -- the same quads, the same order, the same bits.
+bool ShortKQuads(const GemmArgs& a) {
+  if (a.layout == 1 || a.K < 128 || a.K > static_cast<size_t>(kPanelK) || a.M * a.N > 16384)
+    return false;
+  return ((a.M + 15) / 16) * ((a.N + 15) / 16) < 128;
+}
+
+// NT over few outputs and a short K: one lane per chain (GemmNTLanesKernel)
+// where the panel kernel would leave most CUs idle.
+bool NTLanes(const GemmArgs& a) {
+  if (a.layout != 1 || a.K < 64 || a.K > static_cast<size_t>(kPanelK) || a.M * a.N > 16384)
+    return false;
+  return ((a.M + 15) / 16) * ((a.N + 15) / 16) < 128;
+}
+
 // Where both apply, the two-pass workspace form runs before the chain
 // kernel unless the tile policy puts the chain kernel first.
 bool LongKFirst(const GemmArgs& a) { return !a.policy || a.policy->exact_longk_first != 2; }
+
+// The two-pass workspace form: every quad sum in parallel, then each
+// output's quads added in k order.
+template <int kLayout, int kBKind>
+hipError_t LaunchQuadsFold(const GemmArgs& a, hipStream_t s) {
+  const unsigned quads4 = static_cast<unsigned>((a.K / 4 + 3) / 4);
+  const unsigned ob = static_cast<unsigned>((a.M * a.N + kThreads - 1) / kThreads);
+  const dim3 g1(ob, quads4 < 1024 ? quads4 : 1024);
+  hipLaunchKernelGGL((LongKQuadsKernel<kLayout, kBKind>), g1, dim3(kThreads), 0, s, a, quads4);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  hipLaunchKernelGGL((LongKFoldKernel<kLayout, kBKind>), dim3(ob), dim3(kThreads), 0, s, a, quads4);
+  return hipGetLastError();
+}
 
 template <int kLayout, int kBKind>
 hipError_t Run(const GemmArgs& a, hipStream_t s) {
@@ -1144,6 +1207,15 @@ hipError_t Run(const GemmArgs& a, hipStream_t s) {
                     static_cast<unsigned>((a.M + kRankRows - 1) / kRankRows));
     hipLaunchKernelGGL((GemmRankKernel<kLayout>), grid, dim3(kThreads), 0, s, a);
     return hipGetLastError();
+  }
+  if constexpr (kLayout != 1) {
+    if (ShortKQuads(a) && a.scratch) return LaunchQuadsFold<kLayout, kBKind>(a, s);
+  } else {
+    if (NTLanes(a)) {
+      const unsigned grid = static_cast<unsigned>((a.M * a.N + kThreads / 8 - 1) / (kThreads / 8));
+      hipLaunchKernelGGL((GemmNTLanesKernel<kBKind>), dim3(grid), dim3(kThreads), 0, s, a);
+      return hipGetLastError();
+    }
   }
   if (a.K <= static_cast<size_t>(kPanelK) && a.K > 0 && (a.M + 15) / 16 <= 65535) {
     const dim3 grid(static_cast<unsigned>((a.N + 15) / 16), static_cast<unsigned>((a.M + 15) / 16));
@@ -1159,15 +1231,7 @@ hipError_t Run(const GemmArgs& a, hipStream_t s) {
     return LaunchChain<kLayout, kBKind, 16, 16>(a, s);
   }
   if constexpr (kLayout != 1) {
-    if (LongK(a) && a.scratch) {
-      const unsigned quads4 = static_cast<unsigned>((a.K / 4 + 3) / 4);
-      const unsigned ob = static_cast<unsigned>((a.M * a.N + kThreads - 1) / kThreads);
-      const dim3 g1(ob, quads4 < 1024 ? quads4 : 1024);
-      hipLaunchKernelGGL((LongKQuadsKernel<kLayout, kBKind>), g1, dim3(kThreads), 0, s, a, quads4);
-      if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-      hipLaunchKernelGGL((LongKFoldKernel<kLayout, kBKind>), dim3(ob), dim3(kThreads), 0, s, a, quads4);
-      return hipGetLastError();
-    }
+    if (LongK(a) && a.scratch) return LaunchQuadsFold<kLayout, kBKind>(a, s);
     if (LongK(a)) {
       int lb = 0;
       while (lb < 5 && (size_t{2} << lb) <= a.N) ++lb;  // BNo = 2^lb <= min(N, 32)
@@ -1204,7 +1268,7 @@ hipError_t LaunchGemmExact(const GemmArgs& a, hipStream_t s) {
 }
 
 size_t GemmExactScratchBytes(const GemmArgs& a) {
-  if (!LongK(a)) return 0;
+  if (!LongK(a) && !ShortKQuads(a)) return 0;
   return a.M * a.N * ((a.K / 4 + 3) / 4) * 4 * sizeof(float);
 }
 

@@ -30,6 +30,9 @@ PARAMS = (1e-3, 0.9, 0.999, 1e-8, 0.01, 3)  # lr, beta1, beta2, eps, wd, step
 GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 257, 63),
                (131, 517, 203), (8, 1100, 300), (2, 700, 900), (257, 33, 64), (66, 131, 65),
                (32, 512, 256), (32, 8, 256), (32, 512, 8), (8, 256, 32), (512, 8, 32),
+               # few outputs over a short K: the two-pass quads and fold, NT one lane
+               # per chain (K % 4 and K % 8 tails)
+               (32, 8, 512), (32, 256, 512), (48, 40, 130), (40, 24, 77),
                # the decoder steps' long reductions: LoRA dA / dB over 8192 tokens
                (768, 8, 8192), (8, 768, 8192),
                # few outputs over long K: the chain kernel (one output per lane),
@@ -220,7 +223,7 @@ def test_relaxed_q8_gemms_on_bf16_mfma(hip, orc, backend, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(3, 5, 7), (67, 129, 66), (131, 517, 203), (32, 512, 256),
-                                   (2, 700, 900)])
+                                   (2, 700, 900), (32, 8, 512)])
 def test_gemm_narrow_weights(hip, orc, backend, M, N, K):
     r = rng(M + 100 * N + K)
     A = r.standard_normal((M, K)).astype(np.float32)
