@@ -412,6 +412,7 @@ def cpu_baseline(M, N, K):
                       f"B1 x S{seq}, exact family"}
         del eng, img
     orc.set_threads(1)
+    orc.pool_stop()  # the host threads end here, before the GPU extras
     out["train_steps"] = steps
     return out
 

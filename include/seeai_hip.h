@@ -160,7 +160,7 @@ typedef struct seeai_tile_policy {
   uint32_t relaxed_min_fill_256;  /* ... and when their last round over the CUs is at least
                                      this percent full (<= 100) */
   uint32_t relaxed_nt_dma_min_k;  /* relaxed NT on rodata weights: the direct-to-LDS kernel from
-                                     this K, the register-staged one below (default 1024) */
+                                     this K, the register-staged one below (default 768) */
   uint32_t convert_wgs_per_cu;    /* workgroups per CU of the relaxed GEMMs' activation
                                      conversion (default 8, <= 64) */
   uint32_t exact_longk_first;     /* exact skinny long-K GEMM: 1 the two-pass form before the

@@ -91,8 +91,9 @@ static struct {
   unsigned long gen;
   OrcWork* job;
   int busy; /* workers still inside the current job */
+  int quit; /* set by orc_pool_stop: the next generation ends the workers */
 } g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER,
-            0, 0, NULL, 0};
+            0, 0, NULL, 0, 0};
 
 /* arg: the generation current when the worker was created; the job
  * published right after it (generation + 1) is its first. */
@@ -102,6 +103,11 @@ static void* orc_pool_worker(void* arg) {
   for (;;) {
     while (g_pool.gen == seen) pthread_cond_wait(&g_pool.go, &g_pool.mu);
     seen = g_pool.gen;
+    if (g_pool.quit) {
+      if (--g_pool.workers == 0) pthread_cond_signal(&g_pool.done);
+      pthread_mutex_unlock(&g_pool.mu);
+      return NULL;
+    }
     OrcWork* w = g_pool.job;
     pthread_mutex_unlock(&g_pool.mu);
     if (__atomic_fetch_add(&w->joined, 1, __ATOMIC_RELAXED) < w->seats) orc_run_chunks(w);
@@ -142,6 +148,20 @@ static size_t orc_parallel(size_t n, size_t grain, orc_chunk_fn fn, void* ctx) {
   while (g_pool.busy > 0) pthread_cond_wait(&g_pool.done, &g_pool.mu);
   pthread_mutex_unlock(&g_pool.mu);
   return w.count;
+}
+
+/* Ends every pool worker and waits until each has left its loop; the next
+ * orc_parallel starts a fresh pool. */
+void orc_pool_stop(void) {
+  pthread_mutex_lock(&g_pool.mu);
+  if (g_pool.workers > 0) {
+    g_pool.quit = 1;
+    ++g_pool.gen;
+    pthread_cond_broadcast(&g_pool.go);
+    while (g_pool.workers > 0) pthread_cond_wait(&g_pool.done, &g_pool.mu);
+    g_pool.quit = 0;
+  }
+  pthread_mutex_unlock(&g_pool.mu);
 }
 /* kernel_policy.h:122-136: the shared activation expressions. */
 static const float kGeluC = 0.7978845608028654f;

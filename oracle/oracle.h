@@ -180,6 +180,8 @@ uint64_t orc_plan_self_hash(const uint8_t* plan, size_t size, size_t hash_offset
  * spread over n threads; 0 or less means 1.  The default is
  * SEEAI_ORACLE_THREADS, else 1. */
 void orc_set_threads(int n);
+/* Ends the worker pool's threads (a later threaded call starts new ones). */
+void orc_pool_stop(void);
 int orc_threads(void);
 
 /* --- Instruction interpreter (runtime/executor/cpu_backend.cc:260-646) --- */

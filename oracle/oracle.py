@@ -98,6 +98,7 @@ ORACLE_ONLY = {
     "execute_src": (_I, [_P, _P, _P, _P, _P]),
     "set_threads": (None, [_I]),
     "threads": (_I, []),
+    "pool_stop": (None, []),
     "chunk_grain": (_Z, [_Z, _Z]),
     "chunk_count": (_Z, [_Z, _Z]),
 }
@@ -501,6 +502,10 @@ class Kernels:
 
     def threads(self) -> int:
         return int(self._fn("threads")())
+
+    def pool_stop(self):
+        """Ends the worker threads; a later threaded call starts new ones."""
+        self._fn("pool_stop")()
 
     def argmax_tally(self, probs, labels):
         """(hits, judged rows) over rows whose label is not -1

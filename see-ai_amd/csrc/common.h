@@ -217,7 +217,7 @@ struct TilePolicy {
   size_t relaxed_min_tiles_256 = 256;  // relaxed bf16 GEMM: 256 x 256 tiles from this many
   int relaxed_min_fill_256 = 0;        // ... and when their last round of tiles over
                                        // the CUs is at least this percent full
-  size_t relaxed_nt_dma_min_k = 1024;  // relaxed NT: the direct-to-LDS kernel from this K
+  size_t relaxed_nt_dma_min_k = 768;   // relaxed NT: the direct-to-LDS kernel from this K
                                        // (below it the register-staged bf16 kernel)
   int convert_wgs_per_cu = 8;          // workgroups per CU of the activation conversion
   int exact_longk_first = 1;           // exact skinny long-K GEMM: 1 the two-pass workspace

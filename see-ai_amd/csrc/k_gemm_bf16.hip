@@ -16,7 +16,9 @@
 // into registers while the current step multiplies, and one barrier
 // separates steps.  NN's B is [K, N] in memory: a lane loads a 4 x 4 block
 // (four k rows, four n) and transposes it in registers.  The epilogue is the
-// exact family's: alpha, addend, bias, activation.
+// exact family's (column scale, alpha, addend, accumulate, bias,
+// activation) on four consecutive columns of a row per lane, stored as one
+// 16-byte write.
 #include "common.h"
 
 namespace seeai {
@@ -200,32 +202,62 @@ __global__ void __launch_bounds__(kThreads) GemmBf16Kernel(GemmArgs g) {
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
     }
     if (s + 1 < steps) store(buf ^ 1);
     __syncthreads();
   }
 
-  // Epilogue: acc[i][j] element r is C row wm + 32i + 8(r/4) + 4(lane/32)
-  // + r%4, column wn + 32j + lane%32 (the 32x32 accumulator layout).
+  // Epilogue: with the B fragment as the MFMA's first operand, acc[i][j]
+  // element 4q + e is C row wm + 32i + lane%32, column wn + 32j + 8q +
+  // 4(lane/32) + e: four consecutive columns of one row per (i, j, q).
+  const bool vec = N % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(g.C) | reinterpret_cast<uintptr_t>(g.addend)) & 15) == 0;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const size_t m = m0 + wm + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-        const size_t n = n0 + wn + j * 32 + c32;
+      for (int q = 0; q < 4; ++q) {
+        const size_t m = m0 + wm + i * 32 + c32;
+        const size_t n = n0 + wn + j * 32 + 8 * q + 4 * (lane / 32);
         if (m >= M || n >= N) continue;
-        float v = acc[i][j][r];
-        if (kBKind == 1 && g.b_col_scale) v = v * g.b_col_scale[n];
-        if (g.alpha_dot != 1.0f) v = g.alpha_dot * v;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[i][j][4 * q + e];
+          if (n + e >= N) continue;
+          if (kBKind == 1 && g.b_col_scale) v[e] = v[e] * g.b_col_scale[n + e];
+          if (g.alpha_dot != 1.0f) v[e] = g.alpha_dot * v[e];
+        }
         const size_t o = m * N + n;
-        if (g.addend) v = g.addend[o] + v;
-        if (g.accumulate) v = g.C[o] + v;
-        if (g.bias) v = v + g.bias[n];
-        if (g.act) v = ActExpr(g.act, v);
-        g.C[o] = v;
+        if (vec) {
+          if (g.addend) {
+            const float4 a4 = *reinterpret_cast<const float4*>(g.addend + o);
+            v[0] = a4.x + v[0], v[1] = a4.y + v[1], v[2] = a4.z + v[2], v[3] = a4.w + v[3];
+          }
+          if (g.accumulate) {
+            const float4 c4 = *reinterpret_cast<const float4*>(g.C + o);
+            v[0] = c4.x + v[0], v[1] = c4.y + v[1], v[2] = c4.z + v[2], v[3] = c4.w + v[3];
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (g.bias) v[e] = v[e] + g.bias[n + e];
+            if (g.act) v[e] = ActExpr(g.act, v[e]);
+          }
+          *reinterpret_cast<float4*>(g.C + o) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (n + e >= N) continue;
+            float x = v[e];
+            if (g.addend) x = g.addend[o + e] + x;
+            if (g.accumulate) x = g.C[o + e] + x;
+            if (g.bias) x = x + g.bias[n + e];
+            if (g.act) x = ActExpr(g.act, x);
+            g.C[o + e] = x;
+          }
+        }
       }
 }
 

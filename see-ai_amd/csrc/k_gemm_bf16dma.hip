@@ -19,9 +19,12 @@
 //     multiplied, one barrier per stage.  LDS rows are 64 bytes, four 16-byte
 //     chunks; chunk c of row r sits at physical chunk (c + r/4) mod 4, which
 //     keeps the fragment reads (lane l: row l % 32, chunk 2ks + l / 32) free
-//     of bank conflicts.  The epilogue (NN column scale, alpha, addend,
-//     accumulate, bias, activation -- the exact family's order) runs on rows
-//     staged through LDS so C leaves in row-contiguous 16-byte stores.
+//     of bank conflicts.  The W fragment is the MFMA's first operand, so a
+//     lane's accumulators hold four consecutive columns of one row; the
+//     epilogue (NN column scale, alpha, addend, accumulate, bias, activation
+//     -- the exact family's order) runs on them in registers and C leaves in
+//     16-byte stores.  With the low-rank term, or rows whose length is not a
+//     multiple of four, the rows pass through LDS instead.
 // Rows past M or N read as zeros through the buffer range check; Kp is K
 // rounded up to 32.
 #include <algorithm>
@@ -192,7 +195,7 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j],
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[slot][j], fa[slot][i], acc[i][j],
                                                             0, 0, 0);
   };
   // The next k-step's TM + TN LDS reads spread one per MFMA; after the
@@ -241,10 +244,80 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
   mfmas(0);
   interleave();
   mfmas(1);
-  WaitVm<0>();
+  WaitVm<0>();  // the repeated loads past the last stage have landed
+
+  // Accumulator element 4q + e of block (i, j) is C[m][n] at
+  // m = m0 + wm + 32 i + lane % 32, n = n0 + wn + 32 j + 8 q + 4 (lane / 32) + e.
+  if constexpr (kLR == 0) {
+    const bool vec4 = (g.N % 4) == 0 &&
+                      ((reinterpret_cast<uintptr_t>(g.C) | reinterpret_cast<uintptr_t>(g.addend) |
+                        reinterpret_cast<uintptr_t>(g.b_col_scale) |
+                        reinterpret_cast<uintptr_t>(g.bias)) & 15) == 0;
+    // The plain product (the frozen projections): nothing but the stores.
+    if (vec4 && !g.b_col_scale && g.alpha_dot == 1.0f && !g.addend && !g.accumulate && !g.bias &&
+        !g.act) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + wm + i * 32 + lr;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = n0 + wn + j * 32 + 8 * q + 4 * h;
+            if (m < M && n < N)
+              *reinterpret_cast<float4*>(g.C + static_cast<size_t>(m) * N + n) = make_float4(
+                  acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          }
+      }
+      return;
+    }
+    if (vec4) {  // the general epilogue on one column quad at a time
+      const float alpha = g.alpha_dot;
+      const float* __restrict__ cs = g.b_col_scale;
+      const float* __restrict__ add = g.addend;
+      const float* __restrict__ bias = g.bias;
+      float* __restrict__ C = g.C;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + wm + i * 32 + lr;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = n0 + wn + j * 32 + 8 * q + 4 * h;
+            if (m < M && n < N) {
+              const size_t o = static_cast<size_t>(m) * N + n;
+              float x0 = acc[i][j][4 * q], x1 = acc[i][j][4 * q + 1], x2 = acc[i][j][4 * q + 2],
+                    x3 = acc[i][j][4 * q + 3];
+              if (cs) {
+                const float4 s4 = *reinterpret_cast<const float4*>(cs + n);
+                x0 = x0 * s4.x, x1 = x1 * s4.y, x2 = x2 * s4.z, x3 = x3 * s4.w;
+              }
+              if (alpha != 1.0f) x0 = alpha * x0, x1 = alpha * x1, x2 = alpha * x2, x3 = alpha * x3;
+              if (add) {
+                const float4 a4 = *reinterpret_cast<const float4*>(add + o);
+                x0 = a4.x + x0, x1 = a4.y + x1, x2 = a4.z + x2, x3 = a4.w + x3;
+              }
+              if (g.accumulate) {
+                const float4 c4v = *reinterpret_cast<const float4*>(C + o);
+                x0 = c4v.x + x0, x1 = c4v.y + x1, x2 = c4v.z + x2, x3 = c4v.w + x3;
+              }
+              if (bias) {
+                const float4 b4 = *reinterpret_cast<const float4*>(bias + n);
+                x0 = x0 + b4.x, x1 = x1 + b4.y, x2 = x2 + b4.z, x3 = x3 + b4.w;
+              }
+              *reinterpret_cast<float4*>(C + o) = make_float4(ActF(g.act, x0), ActF(g.act, x1),
+                                                              ActF(g.act, x2), ActF(g.act, x3));
+            }
+          }
+      }
+      return;
+    }
+  }
   __syncthreads();  // every wave is done with the stage buffers: reuse them for staging
 
-  // Epilogue through this wave's 32 x WN slice of LDS, 32 rows at a time.
+  // The staged epilogue: this wave's 32 x WN slice of LDS, 32 rows at a
+  // time, so a lane keeps one column quad (and its rank-operand values).
   constexpr int SLD = WN + 4;
   static_assert(kWaves * 32 * SLD * 4 <= kStages * kStage, "staging fits in LDS");
   float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SLD;
@@ -292,7 +365,7 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) stage[(8 * q + 4 * h + e) * SLD + j * 32 + lr] = acc[i][j][4 * q + e];
+        for (int e = 0; e < 4; ++e) stage[lr * SLD + j * 32 + 8 * q + 4 * h + e] = acc[i][j][4 * q + e];
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int t = 0; t < 32 / kRowsPerPass; ++t) {
@@ -466,9 +539,9 @@ bool Bf16DmaFits(const GemmArgs& a) {
   if (!a.relaxed || a.layout > 1 || a.b_kind > 2) return false;
   if (a.M < 128 || a.N < 128 || a.K < 64) return false;
   // NT below the tile policy's relaxed_nt_dma_min_k runs the
-  // register-staged kernel (the conversion pass can cost more than it saves
-  // at short K: 8192 x 768 x 768 and 8192 x 3072 x 768).
-  if (a.layout == 1 && a.K < (a.policy ? a.policy->relaxed_nt_dma_min_k : 1024)) return false;
+  // register-staged kernel (at short K the conversion pass can cost more
+  // than it saves).
+  if (a.layout == 1 && a.K < (a.policy ? a.policy->relaxed_nt_dma_min_k : 768)) return false;
   const size_t Kp = Bf16DmaKp(a.K);
   // 32-bit buffer offsets within a tile and int tile indices.
   if (Kp * 2 * 256 >= (size_t{1} << 31) || a.M >= (size_t{1} << 30) || a.N >= (size_t{1} << 30))

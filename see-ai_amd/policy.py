@@ -43,7 +43,7 @@ FIELDS = {
     "relaxed_min_fill_256": (0, ("range", 0, 100),
                              "relaxed bf16 GEMM: 256x256 tiles only when their last round over "
                              "the CUs is at least this percent full"),
-    "relaxed_nt_dma_min_k": (1024, ("range", 64, 1 << 30),
+    "relaxed_nt_dma_min_k": (768, ("range", 64, 1 << 30),
                              "relaxed NT on rodata weights: the direct-to-LDS kernel from this K"),
     "convert_wgs_per_cu": (8, ("range", 1, 64),
                            "workgroups per CU of the relaxed GEMMs' activation conversion"),

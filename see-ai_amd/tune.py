@@ -45,7 +45,7 @@ ARMS = {
     "quantize_waves_per_cu": [4, 8, 16, 32],
     "relaxed_min_tiles_256": [1, 128, 256, 1 << 30],
     "relaxed_min_fill_256": [0, 50, 80, 95],
-    "relaxed_nt_dma_min_k": [512, 768, 1024, 4096],
+    "relaxed_nt_dma_min_k": [256, 512, 768, 1024, 4096],
     "convert_wgs_per_cu": [2, 4, 8, 16, 32],
     "exact_longk_first": [1, 2],
     "relaxed_tile_192": [1, 2, 3],

@@ -169,7 +169,7 @@ def test_relaxed_nt_kernel_arms_are_bitwise_equal(hip, torch_cuda, kind):
         word = ins(2, [a, w, o], [M, N, K], flags=1 << 5, imm=f32_bits(0.37))
     arena, ro = ar.images()
     outs = []
-    for arm in ({"relaxed_nt_dma_min_k": 512}, None):
+    for arm in ({"relaxed_nt_dma_min_k": 512}, {"relaxed_nt_dma_min_k": 1024}):
         be = hip.HipBackend(0)
         be.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
         be.Configure(arm)
