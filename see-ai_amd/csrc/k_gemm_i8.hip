@@ -664,54 +664,73 @@ GemmI8DmaKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
 
 // --- the small-M GEMM (decode-like) ---------------------------------------------
 
-template <int MT>  // 16-row MFMA tiles covering M <= 16 * MT
-__global__ void __launch_bounds__(kThreads)
+// A workgroup per 16 kNT output columns; its kW waves each reduce one
+// contiguous K / kW slice (a 16-wave workgroup keeps 64 KB of the weight
+// stream in flight per CU), each activation fragment serving kNT weight
+// tiles; the int32 partials add exactly in any order.
+template <int MT, int kW, int kNT>  // M <= 16 MT rows; kW waves; 16 kNT columns
+__global__ void __launch_bounds__(kW * kWave)
 GemmI8SkinnyKernel(const int8_t* __restrict__ QA, const float* __restrict__ sa,
                    const int8_t* __restrict__ QW, const float* __restrict__ sw,
                    float* __restrict__ C, int32_t* __restrict__ acc_out, int M, int N, int K) {
-  __shared__ v4i part[4][MT][kWave];
+  constexpr int kTiles = MT * kNT;
+  static_assert(kTiles <= kW, "a reducing wave per tile");
+  __shared__ v4i part[kW][kTiles][kWave];
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
-  const int n0 = blockIdx.x * 16;
-  const int kq = K / 4;  // each wave reduces one contiguous quarter of K
+  const int n0 = blockIdx.x * 16 * kNT;
+  const int kq = K / kW;  // each wave reduces one contiguous slice of K
   const int kb = wave * kq, ke = kb + kq;
-  const int col = n0 + lane % 16;
   const int kl = (lane / 16) * 16;
-  const int8_t* wrow = QW + static_cast<size_t>(col < N ? col : 0) * K;
-  v4i acc[MT];
+  const int8_t* wrow[kNT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = v4i{0, 0, 0, 0};
+  for (int c = 0; c < kNT; ++c) {
+    const int col = n0 + c * 16 + lane % 16;
+    wrow[c] = QW + static_cast<size_t>(col < N ? col : 0) * K;
+  }
+  v4i acc[MT][kNT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int c = 0; c < kNT; ++c) acc[t][c] = v4i{0, 0, 0, 0};
 #pragma unroll 4
   for (int k = kb; k < ke; k += 64) {
-    const v4i b = col < N ? *reinterpret_cast<const v4i*>(wrow + k + kl) : v4i{0, 0, 0, 0};
+    v4i b[kNT];
+#pragma unroll
+    for (int c = 0; c < kNT; ++c)
+      b[c] = n0 + c * 16 + lane % 16 < N ? *reinterpret_cast<const v4i*>(wrow[c] + k + kl)
+                                         : v4i{0, 0, 0, 0};
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       const int m = t * 16 + lane % 16;
       const v4i a = m < M ? *reinterpret_cast<const v4i*>(QA + static_cast<size_t>(m) * K + k + kl)
                           : v4i{0, 0, 0, 0};
-      acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
+#pragma unroll
+      for (int c = 0; c < kNT; ++c)
+        acc[t][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[c], acc[t][c], 0, 0, 0);
     }
   }
 #pragma unroll
-  for (int t = 0; t < MT; ++t) part[wave][t][lane] = acc[t];
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int c = 0; c < kNT; ++c) part[wave][t * kNT + c][lane] = acc[t][c];
   __syncthreads();
-  if (wave != 0) return;
-  // Integer sums: exact in any order; wave order for good measure.
+  if (wave >= kTiles) return;
+  // Wave w sums tile w over the K slices (integers: exact in any order).
+  const int t = wave / kNT, c = wave % kNT;
+  v4i sum = part[0][wave][lane];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    v4i s = part[0][t][lane];
+  for (int w = 1; w < kW; ++w) sum += part[w][wave][lane];
+  const int col = n0 + c * 16 + lane % 16;
+  if (col >= N) return;
+  const float swn = sw[col];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) s += part[w][t][lane];
-    if (col >= N) continue;
-    const float swn = sw[col];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = t * 16 + (lane / 16) * 4 + r;  // lane holds rows 4*(lane/16)+r
-      if (m >= M) continue;
-      const size_t o = static_cast<size_t>(m) * N + col;
-      if (acc_out) acc_out[o] = s[r];
-      C[o] = (static_cast<float>(s[r]) * sa[m]) * swn;
-    }
+  for (int r = 0; r < 4; ++r) {
+    const int m = t * 16 + (lane / 16) * 4 + r;  // lane holds rows 4*(lane/16)+r
+    if (m >= M) continue;
+    const size_t o = static_cast<size_t>(m) * N + col;
+    if (acc_out) acc_out[o] = sum[r];
+    C[o] = (static_cast<float>(sum[r]) * sa[m]) * swn;
   }
 }
 
@@ -794,13 +813,23 @@ hipError_t LaunchGemmW8A8(const int8_t* QA, const float* sa, const int8_t* QWt, 
                       N < (1u << 30) && K < (1u << 30) && M * K < (1ull << 31) &&
                       N * K < (1ull << 31);
   if (vec_ok && M <= 64 && K % 256 == 0) {
-    const dim3 grid(static_cast<unsigned>((N + 15) / 16));
-    if (M <= 32)
-      hipLaunchKernelGGL(GemmI8SkinnyKernel<2>, grid, dim3(kThreads), 0, s, QA, sa, QWt, sw, C, acc,
-                         static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
-    else
-      hipLaunchKernelGGL(GemmI8SkinnyKernel<4>, grid, dim3(kThreads), 0, s, QA, sa, QWt, sw, C, acc,
-                         static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+    const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+    const auto grid = [&](int cols) { return dim3(static_cast<unsigned>((N + cols - 1) / cols)); };
+    if (K % (64 * 16) == 0) {  // 16 waves of 64-deep steps (two column tiles per
+                               // fragment measured slower at 32 x 4096 x 4096)
+      if (M <= 32)
+        hipLaunchKernelGGL((GemmI8SkinnyKernel<2, 16, 1>), grid(16), dim3(16 * kWave), 0, s, QA, sa,
+                           QWt, sw, C, acc, m, n, k);
+      else
+        hipLaunchKernelGGL((GemmI8SkinnyKernel<4, 16, 1>), grid(16), dim3(16 * kWave), 0, s, QA, sa,
+                           QWt, sw, C, acc, m, n, k);
+    } else if (M <= 32) {
+      hipLaunchKernelGGL((GemmI8SkinnyKernel<2, 4, 1>), grid(16), dim3(4 * kWave), 0, s, QA, sa, QWt,
+                         sw, C, acc, m, n, k);
+    } else {
+      hipLaunchKernelGGL((GemmI8SkinnyKernel<4, 4, 1>), grid(16), dim3(4 * kWave), 0, s, QA, sa, QWt,
+                         sw, C, acc, m, n, k);
+    }
     return hipGetLastError();
   }
   if (vec_ok) {

@@ -34,7 +34,7 @@ GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 
                # per chain (K % 4 and K % 8 tails)
                (32, 8, 512), (32, 256, 512), (48, 40, 130), (40, 24, 77),
                # the decoder steps' long reductions: LoRA dA / dB over 8192 tokens
-               (768, 8, 8192), (8, 768, 8192),
+               (768, 8, 8192), (8, 768, 8192), (24, 16, 1027),
                # few outputs over long K: the chain kernel (one output per lane),
                # ragged chunks and a K % 4 tail
                (1040, 16, 2050), (8200, 8, 600), (16, 1030, 1000), (300, 8, 520), (40, 16, 1300),
