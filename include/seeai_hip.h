@@ -132,6 +132,30 @@ int seeai_execute_range(seeai_ctx* ctx, const void* instructions,
 int seeai_begin_range(seeai_ctx* ctx, const void* program, uint64_t count,
                       uint64_t begin, uint64_t end);
 int seeai_end_range(seeai_ctx* ctx);
+/* A whole range, as seeai_begin_range + seeai_execute of each of
+ * [begin, end) + seeai_end_range would run it (the engine's ExecuteRange,
+ * update_engine.cc:345-351), with the same bits.  No counterpart in the
+ * reference (its CPU executor runs each instruction): for callers that run
+ * the same range step after step.  The first run of a range runs
+ * instruction by instruction (it sizes the workspaces and makes the weight
+ * shadows); the second is captured as a HIP graph and the graph launched;
+ * later runs launch the graph again, one launch per range, the step's
+ * optimizer values (lr and the bias corrections of `params`) copied to the
+ * device ahead of it.  Any bind, setting, policy or workspace change drops
+ * the captured graphs; a range whose capture fails runs instruction by
+ * instruction from then on.  The program's bytes must not change while a
+ * graph of it is kept (they are hashed at every call).  A failure reports
+ * the failing instruction's index in *failed_at. */
+int seeai_run_range(seeai_ctx* ctx, const void* program, uint64_t count, uint64_t begin,
+                    uint64_t end, const seeai_step_params* params, uint64_t* failed_at);
+/* Graph replay in seeai_run_range (default 0: every range runs instruction
+ * by instruction; SEEAI_GRAPHS=1 in the environment starts a context with
+ * it on).  Measured on MI355X, replay runs the decoder and MLP ranges no
+ * faster: the GPU's per-dispatch cost, not the host's launches, sets their
+ * pace. */
+int seeai_set_graph_replay(seeai_ctx* ctx, int on);
+/* Ranges seeai_run_range has run as one graph launch so far. */
+uint64_t seeai_graph_launches(const seeai_ctx* ctx);
 /* Whether adjacent instructions may fuse (default 1), and how many fused
  * dispatches ran (ExecutorBackend::fused_dispatches, backend.h:165). */
 int seeai_set_fusion(seeai_ctx* ctx, int allow);
@@ -144,6 +168,13 @@ uint64_t seeai_dropped_stores(const seeai_ctx* ctx);
 /* Waits for the stream; reports a refusal raised on the device since the
  * last flush (non-finite clip norm: nothing it guarded was written). */
 int seeai_flush(seeai_ctx* ctx);
+/* seeai_flush with `bytes` of the arena at `arena_offset` read back into
+ * `dst` in the same drain (one stream synchronisation for the step's
+ * refusal check and its loss).  No counterpart in the reference: its
+ * engine flushes and then syncs the loss to the host
+ * (update_engine.cc:345-360); this is both for a caller that runs a step
+ * per batch. */
+int seeai_flush_download(seeai_ctx* ctx, uint64_t arena_offset, void* dst, uint64_t bytes);
 
 /* --- Kernel geometry: ExecutorBackend::Configure (backend.h:117) -------- */
 /* The gfx950 member of the reference's schema-1 kernel-policy table

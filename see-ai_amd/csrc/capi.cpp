@@ -111,7 +111,8 @@ struct seeai_ctx {
   uint64_t rodata_bytes = 0;
   uint8_t* source = nullptr;
   uint64_t source_bytes = 0;
-  uint8_t* small = nullptr;  // [0] refusal word, [64] scale slot, [128] two u64 counts
+  uint8_t* small = nullptr;  // [0] refusal word, [64] scale slot, [128] two u64 counts,
+                             // [256] the optimizer's step values for replayed graphs
   int* host_flag = nullptr;  // pinned
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
@@ -125,9 +126,9 @@ struct seeai_ctx {
   const uint8_t* prog = nullptr;
   uint64_t prog_count = 0, range_end = 0;
   // Instructions of the range already run by a fused dispatch, in the order
-  // the engine will present them (at most two: a LoRA site's t product and
-  // rank-r product).
-  const uint8_t* done[2] = {nullptr, nullptr};
+  // the engine will present them (a LoRA site's t product and rank-r
+  // product; the rest of a run of AdamW steps).
+  const uint8_t* done[kAdamWMulti] = {};
   int ndone = 0;
   int allow_fusion = 1;
   int allow_dma = 1;  // relaxed frozen-weight GEMMs on the bf16 shadow path
@@ -159,11 +160,37 @@ struct seeai_ctx {
   // bf16 copies [N, Kp] of frozen weights for the relaxed GEMMs, keyed by
   // (weight, layout, kind, N, K); valid until the next bind.
   std::map<std::tuple<const void*, int, int, uint64_t, uint64_t>, void*> shadows;
+  // Whole ranges captured as HIP graphs (seeai_run_range) and replayed when
+  // the same range of the same program runs again with nothing it depends
+  // on changed since the capture: every binding, setting or workspace change
+  // drops them (DropGraphs, which also advances graph_gen).
+  struct RangeGraph {
+    const uint8_t* prog = nullptr;
+    uint64_t count = 0, begin = 0, end = 0, hash = 0, gen = 0;
+    int runs = 0;             // eager runs so far (the first sizes the workspaces)
+    bool ungraphable = false;  // its capture failed: always eager
+    hipGraphExec_t exec = nullptr;
+    uint64_t relaxed = 0, fused = 0, dropped = 0;  // counter increments per run
+  };
+  std::vector<RangeGraph> graphs;
+  // Off by default: on MI355X the replay measured no faster than the
+  // launches it replaces (the GPU's own per-dispatch cost sets the pace of
+  // these ranges, not the host's launches).
+  int graph_replay = 0;
+  uint64_t graph_gen = 0;
+  uint64_t graph_launches = 0;
+  bool capturing = false;           // the optimizer reads hyper() instead of arguments
+  float* host_hyper = nullptr;      // pinned: the step's {lr, inv_bc1, inv_bc2}
+  hipEvent_t hyper_copied = nullptr;
+  // Captures record on a stream of their own: the context's stream keeps
+  // serving other threads' event waits (the feeder's) while one is recorded.
+  hipStream_t capture_stream = nullptr;
   std::string err;
 
   int* flag() { return reinterpret_cast<int*>(small); }
   float* scale_slot() { return reinterpret_cast<float*>(small + 64); }
   uint64_t* counts() { return reinterpret_cast<uint64_t*>(small + 128); }
+  float* hyper() { return reinterpret_cast<float*>(small + 256); }
 };
 
 namespace {
@@ -189,10 +216,22 @@ int Hip(seeai_ctx* c, hipError_t e, const char* what) {
     if (seeai_rc_ != SEEAI_OK) return seeai_rc_;           \
   } while (0)
 
+// Destroys the captured range graphs (after the stream drains: one may be
+// running) and advances the generation every capture is checked against.
+void DropGraphs(seeai_ctx* c) {
+  ++c->graph_gen;
+  if (c->graphs.empty()) return;
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  for (auto& g : c->graphs)
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  c->graphs.clear();
+}
+
 // Scratch for reductions; grown (after draining the stream) when an op
 // needs more than it holds.
 int Scratch(seeai_ctx* c, size_t bytes, void** out) {
   if (bytes > c->scratch_bytes) {
+    DropGraphs(c);
     SEEAI_TRY(c, hipStreamSynchronize(c->stream), "scratch drain");
     if (c->scratch) SEEAI_TRY(c, hipFree(c->scratch), "scratch free");
     c->scratch = nullptr;
@@ -219,11 +258,19 @@ struct Ptrs {
   int32_t* i32(uint64_t ref) const { return reinterpret_cast<int32_t*>(at(ref)); }
 };
 
+// The step's optimizer values {lr, 1 / (1 - beta1^t), 1 / (1 - beta2^t)}
+// (optimizer.cc:115-118, evaluated on the host with the reference's powf).
+void StepHyper(const seeai_step_params& P, float out[3]) {
+  out[0] = P.lr;
+  out[1] = 1.0f / (1.0f - std::pow(P.beta1, static_cast<float>(P.step)));
+  out[2] = 1.0f / (1.0f - std::pow(P.beta2, static_cast<float>(P.step)));
+}
+
 int AdamWLaunch(seeai_ctx* c, float* p, const float* g, float* m, float* v, uint64_t n,
                 const seeai_step_params& P, float clip) {
-  // optimizer.cc:115-118, evaluated on the host with the reference's powf.
-  const float inv_bc1 = 1.0f / (1.0f - std::pow(P.beta1, static_cast<float>(P.step)));
-  const float inv_bc2 = 1.0f / (1.0f - std::pow(P.beta2, static_cast<float>(P.step)));
+  float hy[3];
+  StepHyper(P, hy);
+  const float inv_bc1 = hy[1], inv_bc2 = hy[2];
   const float* scale = nullptr;
   if (clip > 0.0f) {
     void* ws;
@@ -234,12 +281,13 @@ int AdamWLaunch(seeai_ctx* c, float* p, const float* g, float* m, float* v, uint
   }
   SEEAI_TRY(c,
             LaunchAdamW(p, g, m, v, n, P.lr, P.beta1, P.beta2, P.eps, P.weight_decay, inv_bc1,
-                        inv_bc2, scale, c->flag(), c->stream),
+                        inv_bc2, scale, c->flag(), c->stream, c->capturing ? c->hyper() : nullptr),
             "adamw");
   return SEEAI_OK;
 }
 
 void DropShadows(seeai_ctx* c) {
+  DropGraphs(c);
   for (auto& kv : c->shadows) (void)hipFree(kv.second);
   c->shadows.clear();
 }
@@ -295,6 +343,7 @@ int GemmBf16Dma(seeai_ctx* c, GemmArgs& a, const char* what) {
   if (!ConvertedAlready(c, a)) {
     if (need > c->cvt_bytes) {  // grow after draining the stream
       c->cvt_key.at = nullptr;
+      DropGraphs(c);
       SEEAI_TRY(c, hipStreamSynchronize(c->stream), "conversion buffer drain");
       if (c->cvt) SEEAI_TRY(c, hipFree(c->cvt), "conversion buffer free");
       c->cvt = nullptr;
@@ -573,7 +622,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       }
       SEEAI_TRY(c,
                 LaunchSgd(R.f(ins.in[0]), R.f(ins.in[1]), ins.out[0], P.lr, P.weight_decay, scale,
-                          c->flag(), s),
+                          c->flag(), s, c->capturing ? c->hyper() : nullptr),
                 "sgd");
       return SEEAI_OK;
     }
@@ -800,6 +849,13 @@ int seeai_create(int device, seeai_ctx** out) {
   if (rc == SEEAI_OK) rc = Hip(c, hipMalloc(&c->small, kSmallBytes), "small alloc");
   if (rc == SEEAI_OK) rc = Hip(c, hipMemset(c->small, 0, kSmallBytes), "small clear");
   if (rc == SEEAI_OK) rc = Hip(c, hipHostMalloc(reinterpret_cast<void**>(&c->host_flag), 64), "pinned");
+  if (rc == SEEAI_OK)
+    rc = Hip(c, hipHostMalloc(reinterpret_cast<void**>(&c->host_hyper), 64), "pinned step values");
+  if (rc == SEEAI_OK)
+    rc = Hip(c, hipEventCreateWithFlags(&c->hyper_copied, hipEventDisableTiming), "event");
+  // SEEAI_GRAPHS=1: ranges replayed from captured graphs from the start
+  // (seeai_set_graph_replay for a caller that sets it itself).
+  if (const char* e = std::getenv("SEEAI_GRAPHS"); e && e[0] == '1') c->graph_replay = 1;
   if (rc != SEEAI_OK) {
     seeai_destroy(c);
     return rc;
@@ -813,6 +869,7 @@ void seeai_destroy(seeai_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
+  DropGraphs(c);
   if (c->arena) (void)hipFree(c->arena);
   if (c->rodata) (void)hipFree(c->rodata);
   if (c->source) (void)hipFree(c->source);
@@ -821,6 +878,9 @@ void seeai_destroy(seeai_ctx* c) {
   DropShadows(c);
   if (c->small) (void)hipFree(c->small);
   if (c->host_flag) (void)hipHostFree(c->host_flag);
+  if (c->hyper_copied) (void)hipEventDestroy(c->hyper_copied);
+  if (c->capture_stream) (void)hipStreamDestroy(c->capture_stream);
+  if (c->host_hyper) (void)hipHostFree(c->host_hyper);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
 }
@@ -835,18 +895,21 @@ int seeai_set_stream(seeai_ctx* c, void* stream) {
 void* seeai_get_stream(seeai_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
 int seeai_set_relaxed(seeai_ctx* c, int allow) {
   if (!c) return SEEAI_INVALID;
+  DropGraphs(c);
   c->allow_relaxed = allow ? 1 : 0;
   return SEEAI_OK;
 }
 uint64_t seeai_relaxed_executions(const seeai_ctx* c) { return c ? c->relaxed : 0; }
 int seeai_set_attention_bf16(seeai_ctx* c, int on) {
   if (!c) return SEEAI_INVALID;
+  DropGraphs(c);
   c->attn_bf16 = on ? 1 : 0;
   return SEEAI_OK;
 }
 
 int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t rodata_bytes) {
   if (!c) return SEEAI_INVALID;
+  DropGraphs(c);
   c->cvt_key.at = nullptr;
   c->dead_prog = nullptr;  // dead-store decisions name the old binding's pointers
   const uint64_t bytes = (arena_bytes + kArenaAlignment - 1) / kArenaAlignment * kArenaAlignment;
@@ -877,6 +940,7 @@ int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t 
 
 int seeai_bind_source(seeai_ctx* c, const void* data, uint64_t bytes) {
   if (!c) return SEEAI_INVALID;
+  DropGraphs(c);
   c->cvt_key.at = nullptr;
   c->dead_prog = nullptr;
   SEEAI_TRY(c, hipStreamSynchronize(c->stream), "bind_source drain");
@@ -1245,6 +1309,53 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
 // standalone kernels' expressions; every output is still written.  Refused
 // when the element counts differ or any output overlaps another operand.
 // Returns -1 when the instructions do not fuse.
+int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at);
+
+// A run of adjacent kAdamWStep instructions without a fused clip (the end of
+// every train program: one per adapter tensor) as one launch: each
+// element's update is AdamWKernel's, so the bits are the separate launches'.
+// Refused when any tensor's p, m or v overlaps another operand of the run.
+int TryFuseAdamW(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
+                 const seeai_step_params& P) {
+  if (!c->allow_fusion || ins.opcode != 18 || !c->prog || at < c->prog ||
+      at >= c->prog + c->prog_count * 64 || (at - c->prog) % 64 != 0)
+    return -1;
+  const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
+  const Ptrs R{c};
+  AdamWTable tab{};
+  std::vector<std::pair<const uint8_t*, uint64_t>> writes, reads;
+  for (uint64_t j = idx; j < c->range_end && tab.count < kAdamWMulti; ++j) {
+    Instruction x;
+    std::memcpy(&x, c->prog + j * 64, sizeof x);
+    if (x.opcode != 18 || BitsToF32(x.out[1]) > 0.0f || x.out[0] == 0) break;
+    const uint64_t nb = x.out[0] * 4;
+    const uint8_t* ops[4] = {R.at(x.in[0]), R.at(x.in[1]), R.at(x.in[2]), R.at(x.in[3])};
+    bool clash = false;
+    for (int w : {0, 2, 3}) {
+      for (const auto& o : writes) clash |= Overlap(ops[w], nb, o.first, o.second);
+      for (const auto& o : reads) clash |= Overlap(ops[w], nb, o.first, o.second);
+    }
+    for (const auto& o : writes) clash |= Overlap(ops[1], nb, o.first, o.second);
+    for (int a = 0; a < 4; ++a)
+      for (int b = a + 1; b < 4; ++b) clash |= Overlap(ops[a], nb, ops[b], nb);
+    if (clash) break;
+    for (int w : {0, 2, 3}) writes.push_back({ops[w], nb});
+    reads.push_back({ops[1], nb});
+    tab.t[tab.count++] = {R.f(x.in[0]), R.f(x.in[1]), R.f(x.in[2]), R.f(x.in[3]), x.out[0]};
+  }
+  if (tab.count < 2) return -1;
+  float hy[3];
+  StepHyper(P, hy);
+  SEEAI_TRY(c,
+            LaunchAdamWMulti(tab, hy[0], P.beta1, P.beta2, P.eps, P.weight_decay, hy[1], hy[2],
+                             c->flag(), c->stream, c->capturing ? c->hyper() : nullptr),
+            "adamw");
+  for (int i = 1; i < tab.count; ++i) c->done[i - 1] = at + 64 * i;
+  c->ndone = tab.count - 1;
+  c->fused += tab.count - 1;
+  return SEEAI_OK;
+}
+
 int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   if (!c->allow_fusion || !c->prog || at < c->prog || at >= c->prog + c->prog_count * 64 ||
       (at - c->prog) % 64 != 0)
@@ -1328,7 +1439,7 @@ int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params
   if (!c || !instruction) return SEEAI_INVALID;
   const auto* at = static_cast<const uint8_t*>(instruction);
   if (c->ndone > 0 && at == c->done[0]) {  // ran with an earlier instruction
-    c->done[0] = c->done[1];
+    for (int i = 1; i < c->ndone; ++i) c->done[i - 1] = c->done[i];
     --c->ndone;
     return SEEAI_OK;
   }
@@ -1342,6 +1453,7 @@ int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params
                         (at - c->prog) % 64 == 0;
   c->cur_at = in_range ? at : nullptr;
   int rc = TryFuseLowRank(c, ins, at, P);
+  if (rc < 0) rc = TryFuseAdamW(c, ins, at, P);
   if (rc < 0) rc = TryFuseAttnBwd(c, ins, at);
   if (rc < 0) rc = TryFuseElementwise(c, ins, at);
   if (rc < 0) rc = ExecuteOne(c, ins, P);
@@ -1384,6 +1496,7 @@ int PresizeWorkspaces(seeai_ctx* c, const uint8_t* prog, uint64_t begin, uint64_
     if (int rc = Scratch(c, std::max(scratch, kInitialScratch), &ws)) return rc;
   }
   if (cvt > c->cvt_bytes) {
+    DropGraphs(c);
     SEEAI_TRY(c, hipStreamSynchronize(c->stream), "conversion buffer drain");
     if (c->cvt) SEEAI_TRY(c, hipFree(c->cvt), "conversion buffer free");
     c->cvt = nullptr;
@@ -1420,6 +1533,7 @@ int seeai_end_range(seeai_ctx* c) {
 
 int seeai_set_fusion(seeai_ctx* c, int allow) {
   if (!c) return SEEAI_INVALID;
+  DropGraphs(c);
   c->allow_fusion = allow ? 1 : 0;
   return SEEAI_OK;
 }
@@ -1461,6 +1575,7 @@ int seeai_configure(seeai_ctx* c, const seeai_tile_policy* p) {
     if (p->exact_longk_first) t.exact_longk_first = static_cast<int>(p->exact_longk_first);
     if (p->relaxed_tile_192) t.relaxed_tile_192 = static_cast<int>(p->relaxed_tile_192);
   }
+  DropGraphs(c);
   c->policy = t;
   return SEEAI_OK;
 }
@@ -1511,6 +1626,120 @@ int seeai_execute_range(seeai_ctx* c, const void* instructions, uint64_t count,
   return SEEAI_OK;
 }
 
+int seeai_set_graph_replay(seeai_ctx* c, int on) {
+  if (!c) return SEEAI_INVALID;
+  DropGraphs(c);
+  c->graph_replay = on ? 1 : 0;
+  return SEEAI_OK;
+}
+
+int seeai_run_range(seeai_ctx* c, const void* program, uint64_t count, uint64_t begin,
+                    uint64_t end, const seeai_step_params* params, uint64_t* failed_at) {
+  if (!c || (!program && count) || begin > end || end > count) return SEEAI_INVALID;
+  const auto* base = static_cast<const uint8_t*>(program);
+  auto eager = [&]() -> int {
+    if (int rc = seeai_begin_range(c, program, count, begin, end)) return rc;
+    for (uint64_t i = begin; i < end; ++i) {
+      if (int rc = seeai_execute(c, base + i * 64, params)) {
+        if (failed_at) *failed_at = i;
+        seeai_end_range(c);
+        return rc;
+      }
+    }
+    seeai_end_range(c);
+    return SEEAI_OK;
+  };
+  if (!c->graph_replay || begin == end || !c->arena) return eager();
+  const uint64_t hash = ProgramHash(base, count);
+  // The entry of this range (found again after anything that may have
+  // dropped the list: a workspace growth clears it).
+  auto find = [&]() -> seeai_ctx::RangeGraph* {
+    for (auto& g : c->graphs)
+      if (g.prog == base && g.count == count && g.begin == begin && g.end == end && g.hash == hash)
+        return &g;
+    return nullptr;
+  };
+  seeai_ctx::RangeGraph* e = find();
+  if (!e) {
+    if (c->graphs.size() >= 8) {  // a few ranges per plan: keep the newest
+      if (c->graphs.front().exec) {
+        SEEAI_TRY(c, hipStreamSynchronize(c->stream), "graph retire");
+        (void)hipGraphExecDestroy(c->graphs.front().exec);
+      }
+      c->graphs.erase(c->graphs.begin());
+    }
+    c->graphs.push_back({});
+    e = &c->graphs.back();
+    e->prog = base, e->count = count, e->begin = begin, e->end = end, e->hash = hash;
+    e->gen = c->graph_gen;
+  }
+  if (e->ungraphable) return eager();
+  if (!e->exec) {
+    if (e->runs == 0) {  // eager first: makes the shadows, sizes the workspaces
+      const uint64_t gen = c->graph_gen;
+      const int rc = eager();
+      if (auto* g = find(); g && rc == SEEAI_OK && c->graph_gen == gen) g->runs = 1;
+      return rc;
+    }
+    // Capture: the range's launches recorded, not run (nothing in it waits
+    // on the host or allocates once its first run has sized everything).
+    const uint64_t gen = c->graph_gen;
+    if (int rc = seeai_begin_range(c, program, count, begin, end)) return rc;
+    if (c->graph_gen != gen) {  // the range start grew a workspace: run it as it is
+      seeai_end_range(c);
+      return eager();
+    }
+    const uint64_t relaxed0 = c->relaxed, fused0 = c->fused, dropped0 = c->dropped_stores;
+    int rc = SEEAI_OK;
+    if (!c->capture_stream)
+      rc = Hip(c, hipStreamCreateWithFlags(&c->capture_stream, hipStreamNonBlocking), "capture stream");
+    const hipStream_t stream = c->stream;
+    if (rc == SEEAI_OK)
+      rc = Hip(c, hipStreamBeginCapture(c->capture_stream, hipStreamCaptureModeThreadLocal), "capture");
+    const bool began = rc == SEEAI_OK;
+    c->stream = c->capture_stream;  // every launch of the range records into the capture
+    c->capturing = true;
+    for (uint64_t i = begin; rc == SEEAI_OK && i < end; ++i) rc = seeai_execute(c, base + i * 64, params);
+    c->capturing = false;
+    hipGraph_t graph = nullptr;
+    hipError_t ec = began ? hipStreamEndCapture(c->capture_stream, &graph) : hipErrorUnknown;
+    c->stream = stream;
+    seeai_end_range(c);
+    const uint64_t d_relaxed = c->relaxed - relaxed0, d_fused = c->fused - fused0,
+                   d_dropped = c->dropped_stores - dropped0;
+    c->relaxed = relaxed0, c->fused = fused0, c->dropped_stores = dropped0;  // nothing ran yet
+    hipGraphExec_t exec = nullptr;
+    if (rc == SEEAI_OK && ec == hipSuccess && graph && c->graph_gen == gen)
+      ec = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    else
+      ec = hipErrorUnknown;
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();  // a refused capture leaves nothing to report
+    e = find();
+    if (ec != hipSuccess || !exec || !e) {
+      if (exec) (void)hipGraphExecDestroy(exec);
+      if (e) e->ungraphable = true;  // instruction by instruction, now and from here on
+      return eager();
+    }
+    e->exec = exec;
+    e->relaxed = d_relaxed, e->fused = d_fused, e->dropped = d_dropped;
+  }
+  // Replay: the step's optimizer values land in hyper() first.
+  float hy[3] = {0.0f, 0.0f, 0.0f};
+  if (params) StepHyper(*params, hy);
+  SEEAI_TRY(c, hipEventSynchronize(c->hyper_copied), "step values");  // the last copy has read them
+  std::memcpy(c->host_hyper, hy, sizeof hy);
+  SEEAI_TRY(c, hipMemcpyAsync(c->hyper(), c->host_hyper, sizeof hy, hipMemcpyHostToDevice, c->stream),
+            "step values");
+  SEEAI_TRY(c, hipEventRecord(c->hyper_copied, c->stream), "step values");
+  SEEAI_TRY(c, hipGraphLaunch(e->exec, c->stream), "graph launch");
+  c->relaxed += e->relaxed, c->fused += e->fused, c->dropped_stores += e->dropped;
+  ++c->graph_launches;
+  return SEEAI_OK;
+}
+
+uint64_t seeai_graph_launches(const seeai_ctx* c) { return c ? c->graph_launches : 0; }
+
 int seeai_attn_dkdv(seeai_ctx* c, const float* q, const float* k, const float* v,
                     const float* dout, const float* stats, float* dk, float* dv, uint64_t B,
                     uint64_t S, uint64_t H, uint64_t d) {
@@ -1520,6 +1749,23 @@ int seeai_attn_dkdv(seeai_ctx* c, const float* q, const float* k, const float* v
                                   "operands and slices under 2 GiB");
   SEEAI_TRY(c, LaunchAttnDKDVFused(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
             "attn_dkdv");
+  return SEEAI_OK;
+}
+
+int seeai_flush_download(seeai_ctx* c, uint64_t off, void* dst, uint64_t bytes) {
+  if (!c || !c->arena || off + bytes > c->arena_bytes || (bytes && !dst))
+    return Fail(c, SEEAI_INVALID, "flush_download: extent outside the arena");
+  SEEAI_TRY(c, hipMemcpyAsync(c->host_flag, c->flag(), sizeof(int), hipMemcpyDeviceToHost, c->stream),
+            "flush flag");
+  if (bytes)
+    SEEAI_TRY(c, hipMemcpyAsync(dst, c->arena + off, bytes, hipMemcpyDeviceToHost, c->stream),
+              "flush download");
+  SEEAI_TRY(c, hipStreamSynchronize(c->stream), "flush");
+  if (*c->host_flag) {
+    SEEAI_TRY(c, hipMemsetAsync(c->flag(), 0, sizeof(int), c->stream), "flush reset");
+    SEEAI_TRY(c, hipStreamSynchronize(c->stream), "flush reset sync");
+    return Fail(c, SEEAI_REFUSED, "%s", kNonFiniteNormRefusal);
+  }
   return SEEAI_OK;
 }
 

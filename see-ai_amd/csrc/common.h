@@ -199,11 +199,32 @@ hipError_t LaunchGlobalClipFactor(const float* acc, float max_norm, float* scale
                                   hipStream_t s);
 hipError_t LaunchScaleByFactor(float* g, size_t n, const float* scale, const int* flag,
                                hipStream_t s);
+// hyper: null, or device memory holding {lr, inv_bc1, inv_bc2} that take the
+// place of the arguments (a replayed graph reads each step's values there).
 hipError_t LaunchAdamW(float* p, const float* g, float* m, float* v, size_t n, float lr,
                        float beta1, float beta2, float eps, float wd, float inv_bc1,
-                       float inv_bc2, const float* scale, const int* flag, hipStream_t s);
+                       float inv_bc2, const float* scale, const int* flag, hipStream_t s,
+                       const float* hyper = nullptr);
 hipError_t LaunchSgd(float* p, const float* g, size_t n, float lr, float wd, const float* scale,
-                     const int* flag, hipStream_t s);
+                     const int* flag, hipStream_t s, const float* hyper = nullptr);
+// Up to kAdamWMulti tensors' AdamW steps (no clip) in one launch, each
+// element's update AdamWKernel's.
+constexpr int kAdamWMulti = 16;
+struct AdamWTensor {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  size_t n;
+};
+struct AdamWTable {
+  AdamWTensor t[kAdamWMulti];
+  int first[kAdamWMulti + 1];  // first workgroup of each tensor (set by the launcher)
+  int count;
+};
+hipError_t LaunchAdamWMulti(const AdamWTable& tab, float lr, float beta1, float beta2, float eps,
+                            float wd, float inv_bc1, float inv_bc2, const int* flag, hipStream_t s,
+                            const float* hyper = nullptr);
 
 // fp32-output GEMM family on MFMA (k_gemm_f32.hip).
 // Kernel-geometry choices (the C ABI's seeai_tile_policy): each field picks

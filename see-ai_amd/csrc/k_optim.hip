@@ -90,34 +90,62 @@ ScaleByFactorKernel(float* __restrict__ g, size_t n, const float* __restrict__ s
 }
 
 // optimizer.cc:104-132, per element.
+__device__ __forceinline__ void AdamWElement(float* __restrict__ p, const float* __restrict__ g,
+                                             float* __restrict__ m, float* __restrict__ v, size_t i,
+                                             float s, float lr, float beta1, float beta2, float eps,
+                                             float wd, float inv_bc1, float inv_bc2) {
+  const float om_b1 = 1.0f - beta1;
+  const float om_b2 = 1.0f - beta2;
+  const float gi = g[i] * s;
+  const float mi = beta1 * m[i] + om_b1 * gi;
+  const float vi = beta2 * v[i] + om_b2 * gi * gi;
+  m[i] = mi;
+  v[i] = vi;
+  const float m_hat = mi * inv_bc1;
+  const float v_hat = vi * inv_bc2;
+  const float pi = p[i];
+  p[i] = pi - lr * (m_hat / (sqrtf(v_hat) + eps) + wd * pi);
+}
+
 __global__ void __launch_bounds__(kThreads)
 AdamWKernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
             float* __restrict__ v, size_t n, float lr, float beta1, float beta2, float eps,
             float wd, float inv_bc1, float inv_bc2, const float* __restrict__ scale_p,
-            const int* __restrict__ flag) {
+            const int* __restrict__ flag, const float* __restrict__ hyper) {
   if (*flag) return;
+  if (hyper) lr = hyper[0], inv_bc1 = hyper[1], inv_bc2 = hyper[2];
   const float s = scale_p ? *scale_p : 1.0f;
-  const float om_b1 = 1.0f - beta1;
-  const float om_b2 = 1.0f - beta2;
   const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
-  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
-    const float gi = g[i] * s;
-    const float mi = beta1 * m[i] + om_b1 * gi;
-    const float vi = beta2 * v[i] + om_b2 * gi * gi;
-    m[i] = mi;
-    v[i] = vi;
-    const float m_hat = mi * inv_bc1;
-    const float v_hat = vi * inv_bc2;
-    const float pi = p[i];
-    p[i] = pi - lr * (m_hat / (sqrtf(v_hat) + eps) + wd * pi);
-  }
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
+    AdamWElement(p, g, m, v, i, s, lr, beta1, beta2, eps, wd, inv_bc1, inv_bc2);
+}
+
+// Adjacent kAdamWStep instructions of a range (no clip) as one launch: the
+// workgroups of tensor t are blocks [first[t], first[t + 1]) of the grid,
+// each running the per-element update of AdamWKernel on its slice.
+__global__ void __launch_bounds__(kThreads)
+AdamWMultiKernel(AdamWTable tab, float lr, float beta1, float beta2, float eps, float wd,
+                 float inv_bc1, float inv_bc2, const int* __restrict__ flag,
+                 const float* __restrict__ hyper) {
+  if (*flag) return;
+  if (hyper) lr = hyper[0], inv_bc1 = hyper[1], inv_bc2 = hyper[2];
+  int t = 0;
+  while (t + 1 < tab.count && static_cast<int>(blockIdx.x) >= tab.first[t + 1]) ++t;
+  const AdamWTensor& x = tab.t[t];
+  const size_t blocks = static_cast<size_t>(tab.first[t + 1] - tab.first[t]);
+  const size_t stride = blocks * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x - tab.first[t]) * kThreads + threadIdx.x; i < x.n;
+       i += stride)
+    AdamWElement(x.p, x.g, x.m, x.v, i, 1.0f, lr, beta1, beta2, eps, wd, inv_bc1, inv_bc2);
 }
 
 // optimizer.cc:91-102
 __global__ void __launch_bounds__(kThreads)
 SgdKernel(float* __restrict__ p, const float* __restrict__ g, size_t n, float lr, float wd,
-          const float* __restrict__ scale_p, const int* __restrict__ flag) {
+          const float* __restrict__ scale_p, const int* __restrict__ flag,
+          const float* __restrict__ hyper) {
   if (*flag) return;
+  if (hyper) lr = hyper[0];
   const float s = scale_p ? *scale_p : 1.0f;
   const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
   for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
@@ -166,18 +194,35 @@ hipError_t LaunchScaleByFactor(float* g, size_t n, const float* scale, const int
 
 hipError_t LaunchAdamW(float* p, const float* g, float* m, float* v, size_t n, float lr,
                        float beta1, float beta2, float eps, float wd, float inv_bc1,
-                       float inv_bc2, const float* scale, const int* flag, hipStream_t s) {
+                       float inv_bc2, const float* scale, const int* flag, hipStream_t s,
+                       const float* hyper) {
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(AdamWKernel, dim3(GridFor(n, kThreads, 4096)), dim3(kThreads), 0, s, p, g, m,
-                     v, n, lr, beta1, beta2, eps, wd, inv_bc1, inv_bc2, scale, flag);
+                     v, n, lr, beta1, beta2, eps, wd, inv_bc1, inv_bc2, scale, flag, hyper);
+  return hipGetLastError();
+}
+
+hipError_t LaunchAdamWMulti(const AdamWTable& tab, float lr, float beta1, float beta2, float eps,
+                            float wd, float inv_bc1, float inv_bc2, const int* flag, hipStream_t s,
+                            const float* hyper) {
+  if (tab.count <= 0 || tab.count > kAdamWMulti) return hipErrorInvalidValue;
+  AdamWTable t = tab;
+  int blocks = 0;
+  for (int i = 0; i < t.count; ++i) {
+    t.first[i] = blocks;
+    blocks += static_cast<int>(GridFor(t.t[i].n ? t.t[i].n : 1, kThreads, 4096));
+  }
+  t.first[t.count] = blocks;
+  hipLaunchKernelGGL(AdamWMultiKernel, dim3(blocks), dim3(kThreads), 0, s, t, lr, beta1, beta2,
+                     eps, wd, inv_bc1, inv_bc2, flag, hyper);
   return hipGetLastError();
 }
 
 hipError_t LaunchSgd(float* p, const float* g, size_t n, float lr, float wd, const float* scale,
-                     const int* flag, hipStream_t s) {
+                     const int* flag, hipStream_t s, const float* hyper) {
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(SgdKernel, dim3(GridFor(n, kThreads, 4096)), dim3(kThreads), 0, s, p, g, n, lr,
-                     wd, scale, flag);
+                     wd, scale, flag, hyper);
   return hipGetLastError();
 }
 

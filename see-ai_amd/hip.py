@@ -95,10 +95,14 @@ EXPORTS = {
     "seeai_execute_range": (_I, [_P, _P, _U64, _P, C.POINTER(_U64)]),
     "seeai_begin_range": (_I, [_P, _P, _U64, _U64, _U64]),
     "seeai_end_range": (_I, [_P]),
+    "seeai_run_range": (_I, [_P, _P, _U64, _U64, _U64, _P, C.POINTER(_U64)]),
+    "seeai_set_graph_replay": (_I, [_P, _I]),
+    "seeai_graph_launches": (_U64, [_P]),
     "seeai_set_fusion": (_I, [_P, _I]),
     "seeai_fused_dispatches": (_U64, [_P]),
     "seeai_dropped_stores": (_U64, [_P]),
     "seeai_flush": (_I, [_P]),
+    "seeai_flush_download": (_I, [_P, _U64, _P, _U64]),
     "seeai_configure": (_I, [_P, C.POINTER(TilePolicy)]),
     "seeai_policy": (_I, [_P, C.POINTER(TilePolicy)]),
     "seeai_device_key": (_I, [_I, C.c_char_p, _U64]),
@@ -521,6 +525,18 @@ class Engine:
     def configure(self, policy=None):
         """The backend's kernel geometry (HipBackend.Configure)."""
         _configure(_lib.seeai_engine_context(self.h), policy)
+
+    def set_graph_replay(self, on: bool):
+        """seeai_set_graph_replay on the engine's context: ranges replayed
+        from captured HIP graphs from their second run (True) or run
+        instruction by instruction (False, the default)."""
+        rc = _lib.seeai_set_graph_replay(_lib.seeai_engine_context(self.h), int(bool(on)))
+        if rc != OK:
+            raise BackendError(rc, "set_graph_replay")
+
+    @property
+    def graph_launches(self) -> int:
+        return int(_lib.seeai_graph_launches(_lib.seeai_engine_context(self.h)))
 
     def policy(self) -> dict:
         return _policy_of(_lib.seeai_engine_context(self.h))

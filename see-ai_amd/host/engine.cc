@@ -150,20 +150,27 @@ Result<void> PlanEngine::Stage(const float* input, const void* labels) {
 }
 
 Result<void> PlanEngine::ExecuteRange(const std::vector<Instruction>& program, size_t begin,
-                                      size_t end) {
+                                      size_t end, float* loss_after) {
   const PlanHeader& h = plan_.header;
   if (source_required_ > source_bytes_)
     return Fail("this plan reads the source model: bind it with BindSource before running");
   const StepParams params{EffectiveLr(), h.beta1, h.beta2, h.eps, h.weight_decay, step_};
-  backend_->BeginRange(std::span<const Instruction>(program), begin, end);
-  for (size_t idx = begin; idx < end; ++idx)
-    if (auto r = backend_->Execute(program[idx], params); !r) {
-      backend_->EndRange();
-      return Fail(std::string("backend '") + backend_->name() + "' failed at instruction " +
-                  std::to_string(idx) + ": " + r.error());
-    }
+  // BeginRange, Execute of each instruction, EndRange -- replayed as one
+  // graph launch once the range has run before (HipBackend::RunRange).
+  size_t idx = begin;
+  if (auto r = backend_->RunRange(std::span<const Instruction>(program), begin, end, params, &idx);
+      !r)
+    return Fail(std::string("backend '") + backend_->name() + "' failed at instruction " +
+                std::to_string(idx) + ": " + r.error());
+  if (loss_after) {  // the loss synced to the host in the flush's own drain
+    const uint64_t off = RefOffset(plan_.header.loss_ref);
+    if (auto flushed = backend_->FlushSyncToHost(off, sizeof(float)); !flushed)
+      return Fail(std::string("backend '") + backend_->name() + "' failed to complete: " +
+                  flushed.error());
+    std::memcpy(loss_after, arena_ + off, sizeof(float));
+    return {};
+  }
   auto flushed = backend_->Flush();
-  backend_->EndRange();
   if (!flushed)
     return Fail(std::string("backend '") + backend_->name() + "' failed to complete: " +
                 flushed.error());
@@ -202,10 +209,9 @@ Result<float> PlanEngine::TrainStep(const float* inputs, const void* labels) {
   for (uint64_t g = 0; g < micro; ++g) {
     const auto* lab = labels ? static_cast<const uint8_t*>(labels) + g * h.label_bytes : nullptr;
     if (auto r = Stage(inputs + g * h.input_floats, lab); !r) return Fail(r.error());
-    if (auto r = ExecuteRange(plan_.train, 0, plan_.train.size()); !r) return Fail(r.error());
-    auto loss = Loss();
-    if (!loss) return loss;
-    loss_sum += *loss;
+    float loss = 0.0f;
+    if (auto r = ExecuteRange(plan_.train, 0, plan_.train.size(), &loss); !r) return Fail(r.error());
+    loss_sum += loss;
   }
   if (!plan_.step.empty())
     if (auto r = ExecuteRange(plan_.step, 0, plan_.step.size()); !r) return Fail(r.error());
@@ -290,10 +296,10 @@ Result<void> PlanEngine::TrainSteps(const float* inputs, const void* labels, uin
         ++taken;
       }
       cv.notify_all();
-      if (auto r = ExecuteRange(plan_.train, 0, plan_.train.size()); !r) return finish(Fail(r.error()));
-      auto loss = Loss();
-      if (!loss) return finish(Fail(loss.error()));
-      loss_sum += *loss;
+      float loss = 0.0f;
+      if (auto r = ExecuteRange(plan_.train, 0, plan_.train.size(), &loss); !r)
+        return finish(Fail(r.error()));
+      loss_sum += loss;
     }
     if (!plan_.step.empty())
       if (auto r = ExecuteRange(plan_.step, 0, plan_.step.size()); !r) return finish(Fail(r.error()));
@@ -306,8 +312,9 @@ Result<float> PlanEngine::TrainStepResident() {
   if (plan_.header.grad_accum_steps > 1)
     return Fail("a resident step replays one staged batch; this plan accumulates micro-batches");
   ++step_;
-  if (auto r = ExecuteRange(plan_.train, 0, plan_.train.size()); !r) return Fail(r.error());
-  return Loss();
+  float loss = 0.0f;
+  if (auto r = ExecuteRange(plan_.train, 0, plan_.train.size(), &loss); !r) return Fail(r.error());
+  return loss;
 }
 
 Result<PlanEngine::EvalMetrics> PlanEngine::EvaluateMetrics(const float* input,

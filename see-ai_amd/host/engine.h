@@ -92,7 +92,10 @@ class PlanEngine {
   Result<void> Stage(const float* input, const void* labels);
   // The feeder's token and label contracts on one batch.
   Result<void> CheckBatch(const float* input, const void* labels) const;
-  Result<void> ExecuteRange(const std::vector<Instruction>& program, size_t begin, size_t end);
+  // Runs [begin, end) of a program and drains the stream; with loss_after,
+  // the plan's loss is read back in the same drain.
+  Result<void> ExecuteRange(const std::vector<Instruction>& program, size_t begin, size_t end,
+                            float* loss_after = nullptr);
   Result<float> Loss();
 
   std::vector<uint8_t> blob_;

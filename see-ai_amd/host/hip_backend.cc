@@ -62,9 +62,24 @@ void HipBackend::BeginRange(std::span<const Instruction> program, size_t begin, 
 
 void HipBackend::EndRange() { (void)seeai_end_range(ctx_); }
 
+Result<void> HipBackend::RunRange(std::span<const Instruction> program, size_t begin, size_t end,
+                                  const StepParams& p, size_t* failed_at) {
+  const seeai_step_params sp{p.lr, p.beta1, p.beta2, p.eps, p.weight_decay, 0, p.step};
+  uint64_t at = begin;
+  auto r = Check(seeai_run_range(ctx_, program.data(), program.size(), begin, end, &sp, &at));
+  if (failed_at) *failed_at = static_cast<size_t>(at);
+  return r;
+}
+
 uint64_t HipBackend::fused_dispatches() const { return seeai_fused_dispatches(ctx_); }
 
 Result<void> HipBackend::Flush() { return Check(seeai_flush(ctx_)); }
+
+Result<void> HipBackend::FlushSyncToHost(uint64_t offset, uint64_t bytes) {
+  if (!host_ || offset > host_bytes_ || bytes > host_bytes_ - offset)
+    return Fail("hip backend: sync range outside the bound arena");
+  return Check(seeai_flush_download(ctx_, offset, host_ + offset, bytes));
+}
 
 uint64_t HipBackend::relaxed_executions() const { return seeai_relaxed_executions(ctx_); }
 

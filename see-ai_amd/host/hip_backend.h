@@ -61,8 +61,16 @@ class HipBackend {
   // attention run as one dispatch.
   void BeginRange(std::span<const Instruction> program, size_t begin, size_t end);
   void EndRange();
+  // The range [begin, end) as BeginRange + Execute each + EndRange, replayed
+  // from a captured HIP graph from its second run (seeai_run_range); on
+  // failure *failed_at names the instruction.
+  Result<void> RunRange(std::span<const Instruction> program, size_t begin, size_t end,
+                        const StepParams& params, size_t* failed_at);
   // backend.h:147: drains the stream; reports a refused optimizer step.
   Result<void> Flush();
+  // Flush with `bytes` of the arena at `offset` synced to the host in the
+  // same drain (seeai_flush_download).
+  Result<void> FlushSyncToHost(uint64_t offset, uint64_t bytes);
   uint64_t relaxed_executions() const;
   uint64_t fused_dispatches() const;
   void SetRelaxed(bool allow);

@@ -228,6 +228,10 @@ def test_decoder_fused_backward_is_bitwise_the_separate_passes(hip, torch_cuda):
 
 
 TINY_Q8 = dict(vocab=96, dim=128, heads=2, ffn=352, layers=2, seq=64, batch=2, rank=16)
+# The train program ends in one kAdamWStep per adapter tensor (A and B at four
+# sites per block); runs of up to 16 adjacent steps fuse into one launch.
+Q8_ADAMW = TINY_Q8["layers"] * 4 * 2
+Q8_ADAMW_FUSED = Q8_ADAMW - (Q8_ADAMW + 15) // 16
 
 
 def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch_cuda):
@@ -252,8 +256,9 @@ def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch
         fused.append(eng.fused_dispatches())
         dropped.append(eng.dropped_stores())
         eng.close()
-    # per step and block: 4 LoRA forwards, the dK / dV pair, 2 SwiGLU chains
-    assert fused[0] == 3 * TINY_Q8["layers"] * 7 and fused[1] == 0
+    # per step and block: 4 LoRA forwards, the dK / dV pair, 2 SwiGLU chains;
+    # per step the AdamW runs
+    assert fused[0] == 3 * (TINY_Q8["layers"] * 7 + Q8_ADAMW_FUSED) and fused[1] == 0
     # the base values no later instruction reads (30 here): same bits without them
     assert dropped[0] > 0 and dropped[1] == 0
     assert curves[0].tobytes() == curves[1].tobytes()
@@ -293,7 +298,7 @@ def test_q8_decoder_training_matches_the_oracle(hip, orc, torch_cuda, relaxed):
     # elementwise chains fuse in the exact family too.  Relaxed attention
     # runs f32 products here, so its dK / dV pair stays two dispatches.
     per_block = 6 if relaxed else 2
-    assert eng.fused_dispatches() == TINY_Q8["layers"] * 6 * per_block
+    assert eng.fused_dispatches() == 6 * (TINY_Q8["layers"] * per_block + Q8_ADAMW_FUSED)
     eng.close()
 
 
