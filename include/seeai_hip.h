@@ -165,6 +165,13 @@ uint64_t seeai_fused_dispatches(const seeai_ctx* ctx);
  * any read or never touches again (metal_backend.mm:1281-1313).
  * SEEAI_KEEP_DEAD_STORES=1 at seeai_create keeps every store. */
 uint64_t seeai_dropped_stores(const seeai_ctx* ctx);
+/* How many relaxed products' bf16 activation copies their producers wrote
+ * as they stored (within a range, with fusion on: the SwiGLU passes, GELU
+ * forward / backward and the softmax-xent backward, when the next
+ * instruction is a relaxed frozen-weight product on the direct-to-LDS
+ * path reading their output; the product then skips its conversion pass,
+ * and the producer skips its f32 store where nothing else reads it). */
+uint64_t seeai_fused_conversions(const seeai_ctx* ctx);
 /* Waits for the stream; reports a refusal raised on the device since the
  * last flush (non-finite clip norm: nothing it guarded was written). */
 int seeai_flush(seeai_ctx* ctx);

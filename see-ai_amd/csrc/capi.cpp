@@ -134,7 +134,9 @@ struct seeai_ctx {
   int allow_dma = 1;  // relaxed frozen-weight GEMMs on the bf16 shadow path
   int allow_lowrank = 1;  // LoRA sites folded into the frozen product's epilogue
   int allow_dead_store_drop = 1;  // fused passes skip stores the range overwrites unread
+  int allow_sinks = 1;  // producers write the next relaxed product's bf16 activation
   uint64_t dropped_stores = 0;
+  uint64_t sinks = 0;  // conversions fused into their producers
   // The program `dead` was decided for: its address, length and a hash of
   // its words (a caller may present another program of the same length at
   // the same address, e.g. a temporary buffer freed and reallocated).
@@ -170,7 +172,7 @@ struct seeai_ctx {
     int runs = 0;             // eager runs so far (the first sizes the workspaces)
     bool ungraphable = false;  // its capture failed: always eager
     hipGraphExec_t exec = nullptr;
-    uint64_t relaxed = 0, fused = 0, dropped = 0;  // counter increments per run
+    uint64_t relaxed = 0, fused = 0, dropped = 0, sinks = 0;  // counter increments per run
   };
   std::vector<RangeGraph> graphs;
   // Off by default: on MI355X the replay measured no faster than the
@@ -527,6 +529,13 @@ const char* DecodeGemm(seeai_ctx* c, const Instruction& ins, GemmArgs* out) {
   return what;
 }
 
+bool PlanSink(seeai_ctx* c, uint64_t last, uint64_t writer, const float* out, uint64_t n,
+              Bf16Sink* sink, GemmArgs* ga);
+void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a);
+// The index of the instruction being executed within its range's program
+// (c->cur_at set).
+uint64_t CurIndex(const seeai_ctx* c) { return static_cast<uint64_t>(c->cur_at - c->prog) / 64; }
+
 int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P) {
   if (!c->arena) return Fail(c, SEEAI_INVALID, "execute: no arena is bound");
   const Ptrs R{c};
@@ -566,19 +575,35 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
     case 7:   // ReluFwd
     case 22:  // GeluFwd
     case 24:  // SiluFwd
-      SEEAI_TRY(c,
-                LaunchUnary(ins.opcode == 7 ? 1 : ins.opcode == 22 ? 2 : 3, R.f(ins.in[0]),
-                            R.f(ins.in[1]), ins.out[0], 1.0f, s),
+    {
+      const int kind = ins.opcode == 7 ? 1 : ins.opcode == 22 ? 2 : 3;
+      Bf16Sink sink;
+      GemmArgs ga{};
+      const bool sunk = c->cur_at && ElementwiseSinkFits(kind, ins.out[0], R.f(ins.in[0]), nullptr,
+                                                         R.f(ins.in[1])) &&
+                        PlanSink(c, CurIndex(c), CurIndex(c), R.f(ins.in[1]), ins.out[0], &sink, &ga);
+      SEEAI_TRY(c, LaunchUnary(kind, R.f(ins.in[0]), R.f(ins.in[1]), ins.out[0], 1.0f, s, sink),
                 "act.fwd");
+      if (sunk) SinkDone(c, CurIndex(c), ga);
       return SEEAI_OK;
+    }
     case 8:   // ReluBwd
     case 23:  // GeluBwd
     case 25:  // SiluBwd
+    {
+      const int kind = ins.opcode == 8 ? 1 : ins.opcode == 23 ? 2 : 3;
+      Bf16Sink sink;
+      GemmArgs ga{};
+      const bool sunk = c->cur_at && ElementwiseSinkFits(kind, ins.out[0], R.f(ins.in[0]),
+                                                         R.f(ins.in[1]), R.f(ins.in[2])) &&
+                        PlanSink(c, CurIndex(c), CurIndex(c), R.f(ins.in[2]), ins.out[0], &sink, &ga);
       SEEAI_TRY(c,
-                LaunchBinaryBwd(ins.opcode == 8 ? 1 : ins.opcode == 23 ? 2 : 3, R.f(ins.in[0]),
-                                R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s),
+                LaunchBinaryBwd(kind, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s,
+                                sink),
                 "act.bwd");
+      if (sunk) SinkDone(c, CurIndex(c), ga);
       return SEEAI_OK;
+    }
     case 9:  // kScale
       SEEAI_TRY(c,
                 LaunchUnary(4, R.f(ins.in[0]), R.f(ins.in[1]), ins.out[0], BitsToF32(ins.in[2]), s),
@@ -602,10 +627,16 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
     case 52: {  // SoftmaxXEntBwd (+masked)
       void* ws;
       if (int rc = Scratch(c, 64, &ws)) return rc;
+      Bf16Sink sink;
+      GemmArgs ga{};
+      const bool sunk = c->cur_at && XEntBwdSinkFits(R.f(ins.in[0]), R.f(ins.in[3]), ins.out[1]) &&
+                        PlanSink(c, CurIndex(c), CurIndex(c), R.f(ins.in[3]),
+                                 ins.out[0] * ins.out[1], &sink, &ga);
       SEEAI_TRY(c,
                 LaunchXEntBwd(R.f(ins.in[0]), R.i32(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
-                              ins.out[0], ins.out[1], ins.opcode == 52, ws, s),
+                              ins.out[0], ins.out[1], ins.opcode == 52, ws, s, sink),
                 "softmax_xent.bwd");
+      if (sunk) SinkDone(c, CurIndex(c), ga);
       return SEEAI_OK;
     }
     case 17: {  // kSgdStep
@@ -840,6 +871,9 @@ int seeai_create(int device, seeai_ctx** out) {
   // same-session control of the dead-store scan).
   if (const char* e = std::getenv("SEEAI_KEEP_DEAD_STORES"); e && e[0] == '1')
     c->allow_dead_store_drop = 0;
+  // SEEAI_UNFUSED_CONVERSIONS=1: every relaxed product converts its own
+  // activation (the same-session control of the producers' bf16 copies).
+  if (const char* e = std::getenv("SEEAI_UNFUSED_CONVERSIONS"); e && e[0] == '1') c->allow_sinks = 0;
   // SEEAI_ATTENTION_BF16=1: relaxed attention on bf16 operands from the
   // start (seeai_set_attention_bf16 for a caller that sets it itself).
   if (const char* e = std::getenv("SEEAI_ATTENTION_BF16"); e && e[0] == '1') c->attn_bf16 = 1;
@@ -1214,6 +1248,42 @@ bool DeadStore(seeai_ctx* c, uint64_t at_idx, uint64_t from, const Extent& E) {
   return v != 0;
 }
 
+// Conversion fused into a producer: when the instruction after index `last`
+// is a relaxed frozen-weight product on the direct-to-LDS path whose
+// activation is the producer's output `out` (n floats, K a multiple of 32),
+// `sink` writes that product's bf16 copy into the conversion workspace as
+// the producer stores, and the f32 store is dropped where nothing after the
+// product reads `out` (the dead-store rule, decided for instruction
+// `writer`).  *ga: the product's arguments, for SinkDone.
+bool PlanSink(seeai_ctx* c, uint64_t last, uint64_t writer, const float* out, uint64_t n,
+              Bf16Sink* sink, GemmArgs* ga) {
+  if (!c->allow_fusion || !c->allow_sinks || !c->prog || last + 1 >= c->range_end) return false;
+  Instruction nx;
+  std::memcpy(&nx, c->prog + (last + 1) * 64, sizeof nx);
+  GemmArgs a{};
+  if (!DecodeGemm(c, nx, &a)) return false;
+  a.relaxed = (nx.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
+  a.policy = &c->policy;
+  if (!a.relaxed || !c->allow_dma || !Bf16DmaFits(a) || !Immutable(c, a.B)) return false;
+  if (a.A != out || a.M * a.K != n || a.K % 32 != 0 || a.M * a.K * 2 > c->cvt_bytes) return false;
+  if (reinterpret_cast<uintptr_t>(a.a_k_scale) & 15) return false;
+  sink->out = static_cast<uint16_t*>(c->cvt);
+  sink->ks = a.a_k_scale;
+  sink->alpha = a.alpha_a;
+  sink->K = static_cast<uint32_t>(a.K);
+  sink->store_f32 =
+      DeadStore(c, writer, last + 2, Extent{reinterpret_cast<const uint8_t*>(out), n * 4}) ? 0 : 1;
+  *ga = a;
+  return true;
+}
+
+// After a producer ran with its sink: the workspace holds the next
+// product's A' (its ConvertedAlready finds it, nothing between them).
+void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a) {
+  c->cvt_key = {a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->prog + last * 64};
+  ++c->sinks;
+}
+
 // Range-level fusion of a LoRA site (the seam's whole-program visibility,
 // backend.h:139-142; the reference's Metal backend folds the same pair,
 // metal_kernels.h:290-358, docs/runtime.md:119).  A relaxed frozen-weight
@@ -1387,7 +1457,11 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
     const float *x = R.f(ins.in[0]), *u = R.f(n1.in[0] == ins.in[1] ? n1.in[1] : n1.in[0]);
     float *y = R.f(ins.in[1]), *h = R.f(n1.in[2]);
     if (!clear({y, h}, {x, u})) return -1;
-    SEEAI_TRY(c, LaunchSiluMul(x, u, y, h, n, c->stream), "silu_mul");
+    Bf16Sink sink;
+    GemmArgs ga{};
+    const bool sunk = SwigluFits(n, {x, u, y, h}) && PlanSink(c, idx + 1, idx + 1, h, n, &sink, &ga);
+    SEEAI_TRY(c, LaunchSiluMul(x, u, y, h, n, c->stream, sink), "silu_mul");
+    if (sunk) SinkDone(c, idx + 1, ga);
     c->done[0] = at + 64;
     c->ndone = 1;
     ++c->fused;
@@ -1407,7 +1481,13 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
     float* o1_store = o1;
     if (DeadStore(c, idx, idx + 3, Extent{reinterpret_cast<const uint8_t*>(o1), nb}))
       o1_store = nullptr;
-    SEEAI_TRY(c, LaunchSwigluBwd(a1, b1, o1_store, a2, b2, o2, x, dx, n, c->stream), "swiglu_bwd");
+    Bf16Sink sink;
+    GemmArgs ga{};
+    const bool sunk = SwigluFits(n, {a1, b1, o1, a2, b2, o2, x, dx}) &&
+                      PlanSink(c, idx + 2, idx + 2, dx, n, &sink, &ga);
+    SEEAI_TRY(c, LaunchSwigluBwd(a1, b1, o1_store, a2, b2, o2, x, dx, n, c->stream, sink),
+              "swiglu_bwd");
+    if (sunk) SinkDone(c, idx + 2, ga);
     c->done[0] = at + 64;
     c->done[1] = at + 128;
     c->ndone = 2;
@@ -1540,6 +1620,7 @@ int seeai_set_fusion(seeai_ctx* c, int allow) {
 
 uint64_t seeai_fused_dispatches(const seeai_ctx* c) { return c ? c->fused : 0; }
 uint64_t seeai_dropped_stores(const seeai_ctx* c) { return c ? c->dropped_stores : 0; }
+uint64_t seeai_fused_conversions(const seeai_ctx* c) { return c ? c->sinks : 0; }
 
 int seeai_configure(seeai_ctx* c, const seeai_tile_policy* p) {
   if (!c) return SEEAI_INVALID;
@@ -1689,7 +1770,8 @@ int seeai_run_range(seeai_ctx* c, const void* program, uint64_t count, uint64_t 
       seeai_end_range(c);
       return eager();
     }
-    const uint64_t relaxed0 = c->relaxed, fused0 = c->fused, dropped0 = c->dropped_stores;
+    const uint64_t relaxed0 = c->relaxed, fused0 = c->fused, dropped0 = c->dropped_stores,
+                   sinks0 = c->sinks;
     int rc = SEEAI_OK;
     if (!c->capture_stream)
       rc = Hip(c, hipStreamCreateWithFlags(&c->capture_stream, hipStreamNonBlocking), "capture stream");
@@ -1706,8 +1788,9 @@ int seeai_run_range(seeai_ctx* c, const void* program, uint64_t count, uint64_t 
     c->stream = stream;
     seeai_end_range(c);
     const uint64_t d_relaxed = c->relaxed - relaxed0, d_fused = c->fused - fused0,
-                   d_dropped = c->dropped_stores - dropped0;
+                   d_dropped = c->dropped_stores - dropped0, d_sinks = c->sinks - sinks0;
     c->relaxed = relaxed0, c->fused = fused0, c->dropped_stores = dropped0;  // nothing ran yet
+    c->sinks = sinks0;
     hipGraphExec_t exec = nullptr;
     if (rc == SEEAI_OK && ec == hipSuccess && graph && c->graph_gen == gen)
       ec = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
@@ -1722,7 +1805,7 @@ int seeai_run_range(seeai_ctx* c, const void* program, uint64_t count, uint64_t 
       return eager();
     }
     e->exec = exec;
-    e->relaxed = d_relaxed, e->fused = d_fused, e->dropped = d_dropped;
+    e->relaxed = d_relaxed, e->fused = d_fused, e->dropped = d_dropped, e->sinks = d_sinks;
   }
   // Replay: the step's optimizer values land in hyper() first.
   float hy[3] = {0.0f, 0.0f, 0.0f};
@@ -1734,6 +1817,7 @@ int seeai_run_range(seeai_ctx* c, const void* program, uint64_t count, uint64_t 
   SEEAI_TRY(c, hipEventRecord(c->hyper_copied, c->stream), "step values");
   SEEAI_TRY(c, hipGraphLaunch(e->exec, c->stream), "graph launch");
   c->relaxed += e->relaxed, c->fused += e->fused, c->dropped_stores += e->dropped;
+  c->sinks += e->sinks;
   ++c->graph_launches;
   return SEEAI_OK;
 }

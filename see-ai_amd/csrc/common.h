@@ -8,6 +8,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <initializer_list>
 
 namespace seeai {
 
@@ -142,14 +143,44 @@ inline unsigned GridFor(size_t n, unsigned threads, unsigned cap = 65536u) {
 // device memory the caller owns; each launcher documents the bytes it needs.
 // ---------------------------------------------------------------------------
 
+// A producer's output as the next relaxed GEMM would round it into its
+// bf16 workspace (ConvertFlatKernel's expression: RNE(alpha * (v * ks[k])),
+// k = flat index mod K, K a multiple of 32, ks 16-byte aligned), written by
+// the producer itself so the GEMM skips its conversion pass; store_f32 = 0
+// drops the f32 output where nothing else reads it.  out null: no copy.
+struct Bf16Sink {
+  uint16_t* out = nullptr;
+  const float* ks = nullptr;
+  float alpha = 1.0f;
+  uint32_t K = 0;
+  int store_f32 = 1;
+};
+// Elements i .. i + 3 (i a multiple of 4) of a sink.
+__device__ __forceinline__ void SinkStore4(const Bf16Sink& s, size_t i, float4 v) {
+  float x[4] = {v.x, v.y, v.z, v.w};
+  if (s.ks) {
+    const float4 sc = *reinterpret_cast<const float4*>(s.ks + i % s.K);
+    x[0] = x[0] * sc.x, x[1] = x[1] * sc.y, x[2] = x[2] * sc.z, x[3] = x[3] * sc.w;
+  }
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  bf16x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = static_cast<__bf16>(s.alpha != 1.0f ? s.alpha * x[e] : x[e]);
+  *reinterpret_cast<bf16x4_t*>(s.out + i) = o;
+}
+
 // Elementwise family (k_elementwise.hip).
 hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hipStream_t s);
 hipError_t LaunchMulEW(const float* x, const float* y, float* out, size_t n, hipStream_t s);
 hipError_t LaunchAddBias(const float* x, const float* b, float* out, size_t rows, size_t cols,
                          hipStream_t s);
-hipError_t LaunchUnary(int kind, const float* x, float* out, size_t n, float alpha, hipStream_t s);
+// A sink (GELU only: kind 2) takes the output's bf16 copy.
+hipError_t LaunchUnary(int kind, const float* x, float* out, size_t n, float alpha, hipStream_t s,
+                       const Bf16Sink& sink = Bf16Sink{});
 hipError_t LaunchBinaryBwd(int kind, const float* dy, const float* x, float* dx, size_t n,
-                           hipStream_t s);
+                           hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
+// Whether LaunchUnary / LaunchBinaryBwd can feed a sink for this call.
+bool ElementwiseSinkFits(int kind, size_t n, const void* a, const void* b, const void* out);
 hipError_t LaunchReduceRows(const float* dy, float* db, size_t rows, size_t cols, hipStream_t s);
 hipError_t LaunchFill(float* dst, float value, size_t n, hipStream_t s);
 hipError_t LaunchCopy(const float* src, float* dst, size_t n, hipStream_t s);
@@ -187,7 +218,9 @@ hipError_t LaunchXEntFwd(const float* logits, const int32_t* labels, float* loss
                          size_t N, size_t C, int masked, void* ws, hipStream_t s);
 hipError_t LaunchXEntBwd(const float* probs, const int32_t* labels, const float* seed,
                          float* dlogits, size_t N, size_t C, int masked, void* ws,
-                         hipStream_t s);
+                         hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
+// Whether the backward's row kernel can feed a sink (float4 rows).
+bool XEntBwdSinkFits(const float* probs, const float* dlogits, size_t C);
 
 // Optimizer family (k_optim.hip).  `flag` is the device refusal word that
 // every parameter-writing kernel honours; `scale` a device float slot.
@@ -313,11 +346,14 @@ int DeviceCUs();
 // operand).  Forward: y = SiLU(x), h = y * u.  Backward: o1 = a1 * b1,
 // o2 = a2 * b2, dx = SiluBwd(o1, x), o1 not stored when null (a dead store).
 // The standalone kernels' expressions.
+// A sink takes h's (forward) or dx's (backward) bf16 copy; the float4
+// kernels only (n % 4 == 0, 16-byte aligned operands: SwigluFits).
 hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, size_t n,
-                         hipStream_t s);
+                         hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
 hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const float* a2,
                            const float* b2, float* o2, const float* x, float* dx, size_t n,
-                           hipStream_t s);
+                           hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
+bool SwigluFits(size_t n, std::initializer_list<const void*> ptrs);
 
 // W8A8 (k_gemm_i8.hip).
 hipError_t LaunchQuantizeRows(const float* X, int8_t* Q, float* scale, size_t rows, size_t cols,

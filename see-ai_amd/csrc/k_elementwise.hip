@@ -372,13 +372,15 @@ ArgmaxTallyKernel(const float* __restrict__ probs, const int32_t* __restrict__ l
 
 __global__ void __launch_bounds__(kThreads)
 SiluMul4(const float4* __restrict__ x, const float4* __restrict__ u, float4* __restrict__ y,
-         float4* __restrict__ h, size_t n4) {
+         float4* __restrict__ h, size_t n4, Bf16Sink sink) {
   const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
   for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
     const float4 a = x[i], b = u[i];
     const float4 g = make_float4(SiluExpr(a.x), SiluExpr(a.y), SiluExpr(a.z), SiluExpr(a.w));
     y[i] = g;
-    h[i] = make_float4(g.x * b.x, g.y * b.y, g.z * b.z, g.w * b.w);
+    const float4 hv = make_float4(g.x * b.x, g.y * b.y, g.z * b.z, g.w * b.w);
+    if (sink.store_f32) h[i] = hv;
+    if (sink.out) SinkStore4(sink, 4 * i, hv);
   }
 }
 
@@ -387,15 +389,52 @@ template <bool kStoreO1>
 __global__ void __launch_bounds__(kThreads)
 SwigluBwd4(const float4* __restrict__ a1, const float4* __restrict__ b1, float4* __restrict__ o1,
            const float4* __restrict__ a2, const float4* __restrict__ b2, float4* __restrict__ o2,
-           const float4* __restrict__ x, float4* __restrict__ dx, size_t n4) {
+           const float4* __restrict__ x, float4* __restrict__ dx, size_t n4, Bf16Sink sink) {
   const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
   for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
     const float4 p = a1[i], q = b1[i], r = a2[i], t = b2[i], v = x[i];
     const float4 m1 = make_float4(p.x * q.x, p.y * q.y, p.z * q.z, p.w * q.w);
     if constexpr (kStoreO1) o1[i] = m1;
     o2[i] = make_float4(r.x * t.x, r.y * t.y, r.z * t.z, r.w * t.w);
-    dx[i] = make_float4(SiluBwdExpr(m1.x, v.x), SiluBwdExpr(m1.y, v.y), SiluBwdExpr(m1.z, v.z),
-                        SiluBwdExpr(m1.w, v.w));
+    const float4 d = make_float4(SiluBwdExpr(m1.x, v.x), SiluBwdExpr(m1.y, v.y),
+                                 SiluBwdExpr(m1.z, v.z), SiluBwdExpr(m1.w, v.w));
+    if (sink.store_f32) dx[i] = d;
+    if (sink.out) SinkStore4(sink, 4 * i, d);
+  }
+}
+
+// GELU forward and backward (activation.cc's expressions, as the Map forms
+// of LaunchUnary / LaunchBinaryBwd compute them) over float4, with a sink.
+__device__ __forceinline__ float GeluBwdElem(float dy, float v) {
+  const float kC = 0.7978845608028654f, kA = 0.044715f;
+  const float u = kC * (v + kA * v * v * v);
+  const float t = tanhf(u);
+  const float omt2 = 1.0f - t * t;
+  const float tail = omt2 == 0.0f ? 0.0f : 0.5f * v * omt2 * (kC * (1.0f + 3.0f * kA * v * v));
+  return dy * (0.5f * (1.0f + t) + tail);
+}
+
+__global__ void __launch_bounds__(kThreads)
+GeluFwd4(const float4* __restrict__ x, float4* __restrict__ out, size_t n4, Bf16Sink sink) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
+    const float4 a = x[i];
+    const float4 g = make_float4(GeluExpr(a.x), GeluExpr(a.y), GeluExpr(a.z), GeluExpr(a.w));
+    if (sink.store_f32) out[i] = g;
+    if (sink.out) SinkStore4(sink, 4 * i, g);
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+GeluBwd4(const float4* __restrict__ dy, const float4* __restrict__ x, float4* __restrict__ dx,
+         size_t n4, Bf16Sink sink) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
+    const float4 d = dy[i], v = x[i];
+    const float4 r = make_float4(GeluBwdElem(d.x, v.x), GeluBwdElem(d.y, v.y), GeluBwdElem(d.z, v.z),
+                                 GeluBwdElem(d.w, v.w));
+    if (sink.store_f32) dx[i] = r;
+    if (sink.out) SinkStore4(sink, 4 * i, r);
   }
 }
 
@@ -411,15 +450,23 @@ hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hip
   }
   return Map(n, s, [=] __device__(size_t i) { out[i] = x[i] + y[i]; });
 }
+bool SwigluFits(size_t n, std::initializer_list<const void*> ptrs) {
+  if (n % 4 != 0) return false;
+  for (const void* p : ptrs)
+    if (!Aligned16(p)) return false;
+  return true;
+}
+
 hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, size_t n,
-                         hipStream_t s) {
-  if (n % 4 == 0 && Aligned16(x) && Aligned16(u) && Aligned16(y) && Aligned16(h)) {
+                         hipStream_t s, const Bf16Sink& sink) {
+  if (SwigluFits(n, {x, u, y, h})) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(SiluMul4, dim3(GridFor(n / 4, kThreads, 8192)), dim3(kThreads), 0, s,
                        reinterpret_cast<const float4*>(x), reinterpret_cast<const float4*>(u),
-                       reinterpret_cast<float4*>(y), reinterpret_cast<float4*>(h), n / 4);
+                       reinterpret_cast<float4*>(y), reinterpret_cast<float4*>(h), n / 4, sink);
     return hipGetLastError();
   }
+  if (sink.out || !sink.store_f32) return hipErrorInvalidValue;
   return Map(n, s, [=] __device__(size_t i) {
     const float g = SiluExpr(x[i]);
     y[i] = g;
@@ -428,21 +475,21 @@ hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, siz
 }
 hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const float* a2,
                            const float* b2, float* o2, const float* x, float* dx, size_t n,
-                           hipStream_t s) {
-  if (n % 4 == 0 && Aligned16(a1) && Aligned16(b1) && Aligned16(o1) && Aligned16(a2) &&
-      Aligned16(b2) && Aligned16(o2) && Aligned16(x) && Aligned16(dx)) {
+                           hipStream_t s, const Bf16Sink& sink) {
+  if (SwigluFits(n, {a1, b1, o1, a2, b2, o2, x, dx})) {
     if (n == 0) return hipSuccess;
     const auto c4 = [](const float* p) { return reinterpret_cast<const float4*>(p); };
     const auto m4 = [](float* p) { return reinterpret_cast<float4*>(p); };
     const dim3 grid(GridFor(n / 4, kThreads, 8192));
     if (o1)
       hipLaunchKernelGGL(SwigluBwd4<true>, grid, dim3(kThreads), 0, s, c4(a1), c4(b1), m4(o1),
-                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4);
+                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4, sink);
     else
       hipLaunchKernelGGL(SwigluBwd4<false>, grid, dim3(kThreads), 0, s, c4(a1), c4(b1), m4(o1),
-                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4);
+                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4, sink);
     return hipGetLastError();
   }
+  if (sink.out || !sink.store_f32) return hipErrorInvalidValue;
   return Map(n, s, [=] __device__(size_t i) {
     const float m1 = a1[i] * b1[i];
     if (o1) o1[i] = m1;
@@ -458,7 +505,19 @@ hipError_t LaunchAddBias(const float* x, const float* b, float* out, size_t rows
   return Map(rows * cols, s, [=] __device__(size_t i) { out[i] = x[i] + b[i % cols]; });
 }
 // kind: 1 relu, 2 gelu, 3 silu, 4 scale (out = alpha * x).
-hipError_t LaunchUnary(int kind, const float* x, float* out, size_t n, float alpha, hipStream_t s) {
+bool ElementwiseSinkFits(int kind, size_t n, const void* a, const void* b, const void* out) {
+  return kind == 2 && n > 0 && n % 4 == 0 && Aligned16(a) && (!b || Aligned16(b)) && Aligned16(out);
+}
+
+hipError_t LaunchUnary(int kind, const float* x, float* out, size_t n, float alpha, hipStream_t s,
+                       const Bf16Sink& sink) {
+  if (kind == 2 && ElementwiseSinkFits(2, n, x, nullptr, out)) {
+    hipLaunchKernelGGL(GeluFwd4, dim3(GridFor(n / 4, kThreads, 8192)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const float4*>(x), reinterpret_cast<float4*>(out), n / 4,
+                       sink);
+    return hipGetLastError();
+  }
+  if (sink.out || !sink.store_f32) return hipErrorInvalidValue;
   switch (kind) {
     case 1: return Map(n, s, [=] __device__(size_t i) { out[i] = ReluExpr(x[i]); });
     case 2: return Map(n, s, [=] __device__(size_t i) { out[i] = GeluExpr(x[i]); });
@@ -468,7 +527,14 @@ hipError_t LaunchUnary(int kind, const float* x, float* out, size_t n, float alp
 }
 // kind: 1 relu, 2 gelu, 3 silu backward (activation.cc:28-75).
 hipError_t LaunchBinaryBwd(int kind, const float* dy, const float* x, float* dx, size_t n,
-                           hipStream_t s) {
+                           hipStream_t s, const Bf16Sink& sink) {
+  if (kind == 2 && ElementwiseSinkFits(2, n, dy, x, dx)) {
+    hipLaunchKernelGGL(GeluBwd4, dim3(GridFor(n / 4, kThreads, 8192)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const float4*>(dy), reinterpret_cast<const float4*>(x),
+                       reinterpret_cast<float4*>(dx), n / 4, sink);
+    return hipGetLastError();
+  }
+  if (sink.out || !sink.store_f32) return hipErrorInvalidValue;
   switch (kind) {
     case 1:
       return Map(n, s, [=] __device__(size_t i) { dx[i] = x[i] > 0.0f ? dy[i] : 0.0f; });

@@ -18,7 +18,7 @@ namespace {
 constexpr int kMaxThreads = 256;
 
 // Rows of 16-byte multiples move as float4 with two running maxima per lane.
-__device__ __forceinline__ bool Vec4Rows(const void* p, size_t C) {
+__host__ __device__ __forceinline__ bool Vec4Rows(const void* p, size_t C) {
   return C % 4 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
 
@@ -210,9 +210,9 @@ XEntScaleKernel(const int32_t* __restrict__ labels, const float* __restrict__ se
 __global__ void __launch_bounds__(256)
 XEntBwdKernel(const float* __restrict__ probs, const int32_t* __restrict__ labels,
               const float* __restrict__ scale_p, float* __restrict__ dl, size_t N, size_t C,
-              int masked) {
+              int masked, Bf16Sink sink) {
   const float scale = *scale_p;
-  const bool vec = Vec4Rows(probs, C) && Vec4Rows(dl, C);
+  const bool vec = Vec4Rows(probs, C) && Vec4Rows(dl, C);  // always, with a sink
   for (size_t r = blockIdx.x; r < N; r += gridDim.x) {
     const int32_t lab = labels[r];
     const float* pr = probs + r * C;
@@ -235,7 +235,8 @@ XEntBwdKernel(const float* __restrict__ probs, const int32_t* __restrict__ label
             else v.w -= scale;
           }
         }
-        d4[c] = v;
+        if (sink.store_f32) d4[c] = v;
+        if (sink.out) SinkStore4(sink, r * C + 4 * c, v);
       }
     } else {
       for (size_t c = threadIdx.x; c < C; c += 256) {
@@ -270,14 +271,19 @@ hipError_t LaunchXEntFwd(const float* logits, const int32_t* labels, float* loss
   return hipGetLastError();
 }
 
+bool XEntBwdSinkFits(const float* probs, const float* dlogits, size_t C) {
+  return C > 0 && Vec4Rows(probs, C) && Vec4Rows(dlogits, C);
+}
+
 hipError_t LaunchXEntBwd(const float* probs, const int32_t* labels, const float* seed,
                          float* dlogits, size_t N, size_t C, int masked, void* ws,
-                         hipStream_t s) {
+                         hipStream_t s, const Bf16Sink& sink) {
   if (N == 0) return hipSuccess;
+  if ((sink.out || !sink.store_f32) && !XEntBwdSinkFits(probs, dlogits, C)) return hipErrorInvalidValue;
   float* scale = static_cast<float*>(ws);
   hipLaunchKernelGGL(XEntScaleKernel, dim3(1), dim3(1024), 0, s, labels, seed, scale, N, masked);
   hipLaunchKernelGGL(XEntBwdKernel, dim3(static_cast<unsigned>(N < 65536 ? N : 65536)), dim3(256), 0,
-                     s, probs, labels, scale, dlogits, N, C, masked);
+                     s, probs, labels, scale, dlogits, N, C, masked, sink);
   return hipGetLastError();
 }
 

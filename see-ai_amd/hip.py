@@ -101,6 +101,7 @@ EXPORTS = {
     "seeai_set_fusion": (_I, [_P, _I]),
     "seeai_fused_dispatches": (_U64, [_P]),
     "seeai_dropped_stores": (_U64, [_P]),
+    "seeai_fused_conversions": (_U64, [_P]),
     "seeai_flush": (_I, [_P]),
     "seeai_flush_download": (_I, [_P, _U64, _P, _U64]),
     "seeai_configure": (_I, [_P, C.POINTER(TilePolicy)]),
@@ -521,6 +522,9 @@ class Engine:
 
     def dropped_stores(self) -> int:
         return int(_lib.seeai_dropped_stores(_lib.seeai_engine_context(self.h)))
+
+    def fused_conversions(self) -> int:
+        return int(_lib.seeai_fused_conversions(_lib.seeai_engine_context(self.h)))
 
     def configure(self, policy=None):
         """The backend's kernel geometry (HipBackend.Configure)."""

@@ -442,3 +442,39 @@ def test_c4_width_slice_step_tensors_match_the_oracle(hip, orc, torch_cuda, rela
     bad = {n: e for n, e in errs.items() if not e <= bar}
     assert not bad, bad
     eng.close()
+
+
+@pytest.mark.parametrize("plan", ["c4", "c5"])
+def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda, plan):
+    """A producer followed by a relaxed frozen-weight product on the
+    direct-to-LDS path writes the product's bf16 activation as it stores
+    (GELU forward / backward, the SwiGLU passes, the softmax-xent backward)
+    and drops its f32 store where nothing else reads it; the product skips
+    its conversion pass.  With the NT products on the direct-to-LDS kernel
+    at these small K (relaxed_nt_dma_min_k 64), three steps with fusion on
+    and off give the same losses and persistent bytes."""
+    print(f"engine: fused conversions, tiny {plan}", flush=True)
+    curves, states, sinks = [], [], []
+    for allow in (True, False):
+        if plan == "c4":
+            img = pw.decoder_lora(hip.plan_self_hash, relaxed=True, **TINY)
+            T = TINY["batch"] * TINY["seq"]
+            vocab = TINY["vocab"]
+        else:
+            img = pw.decoder_q8_lora(hip.plan_self_hash, relaxed=True, **TINY_Q8)
+            T = TINY_Q8["batch"] * TINY_Q8["seq"]
+            vocab = TINY_Q8["vocab"]
+        eng = hip.Engine(img.blob)
+        eng.configure({"relaxed_nt_dma_min_k": 64})
+        eng.set_fusion(allow)
+        curve = []
+        for s in range(3):
+            t = pw.uniform_ints(7300 + s, T + 1, vocab)
+            curve.append(eng.train_step(t[:T].copy().view(np.float32), t[1:].copy()))
+        curves.append(np.array(curve, np.float32))
+        states.append(eng.read(0, img.header["persistent_size"]))
+        sinks.append(eng.fused_conversions())
+        eng.close()
+    assert sinks[0] > 0 and sinks[1] == 0
+    assert curves[0].tobytes() == curves[1].tobytes()
+    assert states[0] == states[1]
