@@ -560,9 +560,17 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       a.relaxed = Relaxed(c, ins);
       return Gemm(c, a, what);
     }
-    case 5:
-      SEEAI_TRY(c, LaunchAddEW(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s), "add");
+    case 5: {
+      Bf16Sink sink;
+      GemmArgs ga{};
+      const bool sunk = c->cur_at &&
+                        NormSinkFits(ins.out[0], {R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2])}) &&
+                        PlanSink(c, CurIndex(c), CurIndex(c), R.f(ins.in[2]), ins.out[0], &sink, &ga);
+      SEEAI_TRY(c, LaunchAddEW(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s, sink),
+                "add");
+      if (sunk) SinkDone(c, CurIndex(c), ga);
       return SEEAI_OK;
+    }
     case 21:
       SEEAI_TRY(c, LaunchMulEW(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), ins.out[0], s), "mul");
       return SEEAI_OK;
@@ -696,30 +704,42 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       SEEAI_TRY(c, LaunchAccumulate(R.f(ins.in[0]), R.f(ins.in[1]), ins.out[0], s), "accumulate");
       return SEEAI_OK;
     case 26:
-      SEEAI_TRY(c,
-                LaunchLayerNormFwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
-                                   R.f(ins.out[1]), R.f(ins.out[2]), hi0, lo0, norm_eps, s),
-                "layernorm.fwd");
-      return SEEAI_OK;
     case 27:
-      SEEAI_TRY(c,
-                LaunchLayerNormBwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.out[0]),
-                                   R.f(ins.out[1]), R.f(ins.in[3]), ins.out[2] >> 32,
-                                   ins.out[2] & 0xFFFFFFFFu, s),
-                "layernorm.bwd");
-      return SEEAI_OK;
     case 31:
-      SEEAI_TRY(c,
-                LaunchRmsNormFwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
-                                 hi0, lo0, norm_eps, s),
-                "rmsnorm.fwd");
+    case 32: {  // LayerNorm / RMSNorm forward and backward
+      const uint64_t shape = ins.opcode == 27 ? ins.out[2] : ins.opcode == 32 ? ins.out[1] : ins.out[0];
+      const uint64_t rows = shape >> 32, cols = shape & 0xFFFFFFFFu;
+      // The row-shaped output: y (forward) or dx (backward).
+      const float* out = R.f(ins.opcode == 31 ? ins.in[2] : ins.in[3]);
+      Bf16Sink sink;
+      GemmArgs ga{};
+      const bool sunk =
+          c->cur_at &&
+          NormSinkFits(cols, {R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3])}) &&
+          PlanSink(c, CurIndex(c), CurIndex(c), out, rows * cols, &sink, &ga);
+      if (ins.opcode == 26)
+        SEEAI_TRY(c,
+                  LaunchLayerNormFwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                                     R.f(ins.out[1]), R.f(ins.out[2]), rows, cols, norm_eps, s, sink),
+                  "layernorm.fwd");
+      else if (ins.opcode == 27)
+        SEEAI_TRY(c,
+                  LaunchLayerNormBwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.out[0]),
+                                     R.f(ins.out[1]), R.f(ins.in[3]), rows, cols, s, sink),
+                  "layernorm.bwd");
+      else if (ins.opcode == 31)
+        SEEAI_TRY(c,
+                  LaunchRmsNormFwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
+                                   rows, cols, norm_eps, s, sink),
+                  "rmsnorm.fwd");
+      else
+        SEEAI_TRY(c,
+                  LaunchRmsNormBwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.out[0]),
+                                   R.f(ins.in[3]), rows, cols, s, sink),
+                  "rmsnorm.bwd");
+      if (sunk) SinkDone(c, CurIndex(c), ga);
       return SEEAI_OK;
-    case 32:
-      SEEAI_TRY(c,
-                LaunchRmsNormBwd(R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.out[0]),
-                                 R.f(ins.in[3]), ins.out[1] >> 32, ins.out[1] & 0xFFFFFFFFu, s),
-                "rmsnorm.bwd");
-      return SEEAI_OK;
+    }
     case 33:
     case 34: {  // RopeFwd / RopeBwd (v12 table in in[2])
       const uint64_t d = ins.out[1] & 0xFFFFFFFFu;
@@ -1208,14 +1228,18 @@ bool OverwritesWhatItWrites(uint16_t op) {
   }
 }
 
-// Whether the store of E made by the instruction before index `from` is
+// Whether the store of E made by instruction `writer` (before `from`) is
 // dead, under the reference's rule for a LoRA site's base value
 // (metal_backend.mm:1281-1313): over the whole program, not the range, the
 // first instruction at or after `from` to touch E writes all of it, reads
 // none of it and overwrites what it writes, or no instruction touches it.
-// An instruction whose extents are not modelled keeps the store.
-bool DeadFrom(seeai_ctx* c, uint64_t from, const Extent& E) {
-  for (uint64_t k = from; k < c->prog_count; ++k) {
+// The program runs again at the next step, so the scan wraps round to the
+// start and ends at the writer: a value that only the next step's earlier
+// instructions read keeps its store.  An instruction whose extents are not
+// modelled keeps the store.
+bool DeadFrom(seeai_ctx* c, uint64_t writer, uint64_t from, const Extent& E) {
+  for (uint64_t i = from; i < c->prog_count + writer + 1; ++i) {
+    const uint64_t k = i < c->prog_count ? i : i - c->prog_count;
     Instruction ins;
     std::memcpy(&ins, c->prog + k * 64, sizeof ins);
     Touch t[16];
@@ -1243,7 +1267,7 @@ bool DeadStore(seeai_ctx* c, uint64_t at_idx, uint64_t from, const Extent& E) {
     c->dead.assign(c->prog_count, -1);
   }
   int8_t& v = c->dead[at_idx];
-  if (v < 0) v = DeadFrom(c, from, E) ? 1 : 0;
+  if (v < 0) v = DeadFrom(c, at_idx, from, E) ? 1 : 0;
   if (v) ++c->dropped_stores;
   return v != 0;
 }

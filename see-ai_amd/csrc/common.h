@@ -170,7 +170,12 @@ __device__ __forceinline__ void SinkStore4(const Bf16Sink& s, size_t i, float4 v
 }
 
 // Elementwise family (k_elementwise.hip).
-hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hipStream_t s);
+hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hipStream_t s,
+                       const Bf16Sink& sink = Bf16Sink{});
+// Whether rows of `cols` floats (a multiple of 4; the non-null operands
+// 16-byte aligned) go out as float4 stores and so can feed a sink: the
+// normalisations' rows, and the residual add as one row of n.
+bool NormSinkFits(size_t cols, std::initializer_list<const void*> ptrs);
 hipError_t LaunchMulEW(const float* x, const float* y, float* out, size_t n, hipStream_t s);
 hipError_t LaunchAddBias(const float* x, const float* b, float* out, size_t rows, size_t cols,
                          hipStream_t s);
@@ -191,14 +196,16 @@ hipError_t LaunchFusedMap(const float* x, const float* o1, const float* o2, floa
                           uint64_t stages, float imm0, float imm1, hipStream_t s);
 hipError_t LaunchLayerNormFwd(const float* x, const float* g, const float* b, float* y,
                               float* mean, float* rstd, size_t rows, size_t cols, float eps,
-                              hipStream_t s);
+                              hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
 hipError_t LaunchLayerNormBwd(const float* dy, const float* x, const float* g,
                               const float* mean, const float* rstd, float* dx, size_t rows,
-                              size_t cols, hipStream_t s);
+                              size_t cols, hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
 hipError_t LaunchRmsNormFwd(const float* x, const float* g, float* y, float* rstd, size_t rows,
-                            size_t cols, float eps, hipStream_t s);
+                            size_t cols, float eps, hipStream_t s,
+                            const Bf16Sink& sink = Bf16Sink{});
 hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, const float* rstd,
-                            float* dx, size_t rows, size_t cols, hipStream_t s);
+                            float* dx, size_t rows, size_t cols, hipStream_t s,
+                            const Bf16Sink& sink = Bf16Sink{});
 hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
                       float step, const float* table, int backward, hipStream_t s);
 hipError_t LaunchRopeTable(float* table, size_t S, size_t d, float step, hipStream_t s);

@@ -36,11 +36,30 @@ hipError_t Map(size_t n, hipStream_t s, F f) {
 // elementwise.cc:16-27 / 38-48 as 4-wide vectors when n and the pointers
 // allow (the same per-element expression; vectors only widen the access).
 __global__ void __launch_bounds__(kThreads)
-AddEW4(const float4* __restrict__ x, const float4* __restrict__ y, float4* __restrict__ o, size_t n4) {
+AddEW4(const float4* __restrict__ x, const float4* __restrict__ y, float4* __restrict__ o, size_t n4,
+       Bf16Sink sink) {
   const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
   for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
     const float4 a = x[i], b = y[i];
-    o[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    const float4 v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    if (sink.store_f32) o[i] = v;
+    if (sink.out) SinkStore4(sink, 4 * i, v);
+  }
+}
+
+// A normalisation's output row: float4 where the row allows it (the same
+// per-element expression), with the sink; element by element otherwise.
+template <class F>
+__device__ __forceinline__ void NormRowOut(float* __restrict__ yr, size_t row0, size_t cols, bool vec,
+                                           const Bf16Sink& sink, F&& elem) {
+  if (vec) {
+    for (size_t c = threadIdx.x * 4; c < cols; c += kThreads * 4) {
+      const float4 v = make_float4(elem(c), elem(c + 1), elem(c + 2), elem(c + 3));
+      if (sink.store_f32) *reinterpret_cast<float4*>(yr + c) = v;
+      if (sink.out) SinkStore4(sink, row0 + c, v);
+    }
+  } else {
+    for (size_t c = threadIdx.x; c < cols; c += kThreads) yr[c] = elem(c);
   }
 }
 
@@ -103,7 +122,7 @@ EmbedKernel(const int32_t* __restrict__ tokens, const float* __restrict__ table,
 __global__ void __launch_bounds__(kThreads)
 LayerNormFwdKernel(const float* __restrict__ x, const float* __restrict__ g,
                    const float* __restrict__ b, float* __restrict__ y, float* __restrict__ mean,
-                   float* __restrict__ rstd, size_t cols, float eps) {
+                   float* __restrict__ rstd, size_t cols, float eps, int vec, Bf16Sink sink) {
   __shared__ double red[kThreads / kWave];
   const size_t r = blockIdx.x;
   const float* xr = x + r * cols;
@@ -122,15 +141,16 @@ LayerNormFwdKernel(const float* __restrict__ x, const float* __restrict__ g,
     mean[r] = mu;
     rstd[r] = rs;
   }
-  float* yr = y + r * cols;
-  for (size_t c = threadIdx.x; c < cols; c += kThreads) yr[c] = (xr[c] - mu) * rs * g[c] + b[c];
+  NormRowOut(y + r * cols, r * cols, cols, vec, sink,
+             [&](size_t c) { return (xr[c] - mu) * rs * g[c] + b[c]; });
 }
 
 // LayerNorm backward (normalization.cc:47-78).
 __global__ void __launch_bounds__(kThreads)
 LayerNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
                    const float* __restrict__ g, const float* __restrict__ mean,
-                   const float* __restrict__ rstd, float* __restrict__ dx, size_t cols) {
+                   const float* __restrict__ rstd, float* __restrict__ dx, size_t cols, int vec,
+                   Bf16Sink sink) {
   __shared__ double red[kThreads / kWave];
   const size_t r = blockIdx.x;
   const float* dyr = dy + r * cols;
@@ -148,18 +168,17 @@ LayerNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
   const float inv_d = 1.0f / static_cast<float>(cols);
   const float mg = static_cast<float>(sg) * inv_d;
   const float mgx = static_cast<float>(sgx) * inv_d;
-  float* dxr = dx + r * cols;
-  for (size_t c = threadIdx.x; c < cols; c += kThreads) {
+  NormRowOut(dx + r * cols, r * cols, cols, vec, sink, [&](size_t c) {
     const float xhat = (xr[c] - mu) * rs;
     const float gg = dyr[c] * g[c];
-    dxr[c] = rs * (gg - mg - xhat * mgx);
-  }
+    return rs * (gg - mg - xhat * mgx);
+  });
 }
 
 // RMSNorm forward / backward (normalization.cc:80-113).
 __global__ void __launch_bounds__(kThreads)
 RmsNormFwdKernel(const float* __restrict__ x, const float* __restrict__ g, float* __restrict__ y,
-                 float* __restrict__ rstd, size_t cols, float eps) {
+                 float* __restrict__ rstd, size_t cols, float eps, int vec, Bf16Sink sink) {
   __shared__ double red[kThreads / kWave];
   const size_t r = blockIdx.x;
   const float* xr = x + r * cols;
@@ -168,14 +187,13 @@ RmsNormFwdKernel(const float* __restrict__ x, const float* __restrict__ g, float
   ss = BlockSumD<kThreads>(ss, red);
   const float rs = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + eps);
   if (threadIdx.x == 0) rstd[r] = rs;
-  float* yr = y + r * cols;
-  for (size_t c = threadIdx.x; c < cols; c += kThreads) yr[c] = xr[c] * rs * g[c];
+  NormRowOut(y + r * cols, r * cols, cols, vec, sink, [&](size_t c) { return xr[c] * rs * g[c]; });
 }
 
 __global__ void __launch_bounds__(kThreads)
 RmsNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
                  const float* __restrict__ g, const float* __restrict__ rstd,
-                 float* __restrict__ dx, size_t cols) {
+                 float* __restrict__ dx, size_t cols, int vec, Bf16Sink sink) {
   __shared__ double red[kThreads / kWave];
   const size_t r = blockIdx.x;
   const float* dyr = dy + r * cols;
@@ -187,9 +205,8 @@ RmsNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
   sgx = BlockSumD<kThreads>(sgx, red);
   const float inv_d = 1.0f / static_cast<float>(cols);
   const float mgx = static_cast<float>(sgx) * inv_d;
-  float* dxr = dx + r * cols;
-  for (size_t c = threadIdx.x; c < cols; c += kThreads)
-    dxr[c] = rs * (dyr[c] * g[c] - xr[c] * rs * rs * mgx);
+  NormRowOut(dx + r * cols, r * cols, cols, vec, sink,
+             [&](size_t c) { return rs * (dyr[c] * g[c] - xr[c] * rs * rs * mgx); });
 }
 
 // RoPE (attention.cc:103-174): one lane per interleaved pair (c, c+1) of a
@@ -440,14 +457,16 @@ GeluBwd4(const float4* __restrict__ dy, const float4* __restrict__ x, float4* __
 
 }  // namespace
 
-hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hipStream_t s) {
+hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hipStream_t s,
+                       const Bf16Sink& sink) {
   if (n % 4 == 0 && Aligned16(x) && Aligned16(y) && Aligned16(out)) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(AddEW4, dim3(GridFor(n / 4, kThreads, 8192)), dim3(kThreads), 0, s,
                        reinterpret_cast<const float4*>(x), reinterpret_cast<const float4*>(y),
-                       reinterpret_cast<float4*>(out), n / 4);
+                       reinterpret_cast<float4*>(out), n / 4, sink);
     return hipGetLastError();
   }
+  if (sink.out || !sink.store_f32) return hipErrorInvalidValue;
   return Map(n, s, [=] __device__(size_t i) { out[i] = x[i] + y[i]; });
 }
 bool SwigluFits(size_t n, std::initializer_list<const void*> ptrs) {
@@ -589,34 +608,49 @@ hipError_t LaunchFusedMap(const float* x, const float* o1, const float* o2, floa
                      o2, out, n, p, imm0, imm1);
   return hipGetLastError();
 }
+bool NormSinkFits(size_t cols, std::initializer_list<const void*> ptrs) {
+  if (cols == 0 || cols % 4 != 0) return false;
+  for (const void* p : ptrs)
+    if (p && !Aligned16(p)) return false;
+  return true;
+}
 hipError_t LaunchLayerNormFwd(const float* x, const float* g, const float* b, float* y,
                               float* mean, float* rstd, size_t rows, size_t cols, float eps,
-                              hipStream_t s) {
+                              hipStream_t s, const Bf16Sink& sink) {
   if (rows == 0) return hipSuccess;
+  const int vec = NormSinkFits(cols, {x, g, b, y});
+  if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(LayerNormFwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s,
-                     x, g, b, y, mean, rstd, cols, eps);
+                     x, g, b, y, mean, rstd, cols, eps, vec, sink);
   return hipGetLastError();
 }
 hipError_t LaunchLayerNormBwd(const float* dy, const float* x, const float* g,
                               const float* mean, const float* rstd, float* dx, size_t rows,
-                              size_t cols, hipStream_t s) {
+                              size_t cols, hipStream_t s, const Bf16Sink& sink) {
   if (rows == 0) return hipSuccess;
+  const int vec = NormSinkFits(cols, {dy, x, g, dx});
+  if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(LayerNormBwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s,
-                     dy, x, g, mean, rstd, dx, cols);
+                     dy, x, g, mean, rstd, dx, cols, vec, sink);
   return hipGetLastError();
 }
 hipError_t LaunchRmsNormFwd(const float* x, const float* g, float* y, float* rstd, size_t rows,
-                            size_t cols, float eps, hipStream_t s) {
+                            size_t cols, float eps, hipStream_t s, const Bf16Sink& sink) {
   if (rows == 0) return hipSuccess;
+  const int vec = NormSinkFits(cols, {x, g, y});
+  if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(RmsNormFwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, x,
-                     g, y, rstd, cols, eps);
+                     g, y, rstd, cols, eps, vec, sink);
   return hipGetLastError();
 }
 hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, const float* rstd,
-                            float* dx, size_t rows, size_t cols, hipStream_t s) {
+                            float* dx, size_t rows, size_t cols, hipStream_t s,
+                            const Bf16Sink& sink) {
   if (rows == 0) return hipSuccess;
+  const int vec = NormSinkFits(cols, {dy, x, g, dx});
+  if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(RmsNormBwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, dy,
-                     x, g, rstd, dx, cols);
+                     x, g, rstd, dx, cols, vec, sink);
   return hipGetLastError();
 }
 hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,

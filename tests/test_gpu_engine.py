@@ -444,11 +444,22 @@ def test_c4_width_slice_step_tensors_match_the_oracle(hip, orc, torch_cuda, rela
     eng.close()
 
 
+# Producers that feed a relaxed direct-to-LDS product in one training step of
+# the two-block tiny decoders.  c4: LayerNorm forward ahead of Q and of the
+# FFN up product (2 + 2), GELU forward (2), the softmax-xent backward (1),
+# the final LayerNorm backward (1), GELU backward (2), the residual-gradient
+# adds ahead of Wo^T (2) and of the block below's Wd^T (1).  c5 the same with
+# RMSNorm and the SwiGLU passes in place of GELU.  The final norm does not
+# fuse: the head's N = 96 is below the direct-to-LDS kernel's 128.
+SINKS_PER_STEP = {"c4": 13, "c5": 13}
+
+
 @pytest.mark.parametrize("plan", ["c4", "c5"])
 def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda, plan):
     """A producer followed by a relaxed frozen-weight product on the
     direct-to-LDS path writes the product's bf16 activation as it stores
-    (GELU forward / backward, the SwiGLU passes, the softmax-xent backward)
+    (GELU forward / backward, the SwiGLU passes, the softmax-xent backward,
+    LayerNorm / RMSNorm forward and backward, the residual-gradient adds)
     and drops its f32 store where nothing else reads it; the product skips
     its conversion pass.  With the NT products on the direct-to-LDS kernel
     at these small K (relaxed_nt_dma_min_k 64), three steps with fusion on
@@ -471,10 +482,16 @@ def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda
         for s in range(3):
             t = pw.uniform_ints(7300 + s, T + 1, vocab)
             curve.append(eng.train_step(t[:T].copy().view(np.float32), t[1:].copy()))
+            if s == 0:
+                first = eng.fused_conversions()
         curves.append(np.array(curve, np.float32))
         states.append(eng.read(0, img.header["persistent_size"]))
-        sinks.append(eng.fused_conversions())
+        sinks.append(eng.fused_conversions() - first)
         eng.close()
-    assert sinks[0] > 0 and sinks[1] == 0
+    # The first step grows the conversion workspace as it goes (a producer
+    # ahead of the first product that needs the room does not fuse); steps
+    # two and three fuse every one.
+    print(f"  {sinks[0]} conversions fused over steps 2-3", flush=True)
+    assert sinks[0] == 2 * SINKS_PER_STEP[plan] and sinks[1] == 0
     assert curves[0].tobytes() == curves[1].tobytes()
     assert states[0] == states[1]
