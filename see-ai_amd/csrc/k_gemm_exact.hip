@@ -957,27 +957,38 @@ __global__ void __launch_bounds__(kThreads) GemmFoldKernel(GemmArgs g) {
   g.C[mf * N + nf] = Epilogue(g, mf, nf, c);
 }
 
-// The fold kernel with 16-byte staging: TN with f32 operands, 16-byte
-// aligned, M a multiple of BMo and N of BNo (both >= 4), K * M and K * N
-// below 2^31; a BMo x BNo block of outputs per workgroup, K in chunks of
-// kKc.  A chunk row contributes BMo / 4 float4 of A (A[k][m0 ...]) and
-// BNo / 4 of B, read with one 32-bit offset each and transposed into the
-// k-contiguous LDS rows as they are stored.  Each lane forms the quads of a
-// 2 x 2 block of outputs (two A and two B reads give four quads), and the
-// lanes below BMo x BNo fold them in k order, sixteen LDS reads in flight
-// ahead of the adds -- GemmFoldKernel's chains, with a quarter of its
-// instructions for staging and half its operand reads.
-template <int BMo, int BNo, int kKc>
-__global__ void __launch_bounds__(kThreads) GemmFoldVecKernel(GemmArgs g) {
-  static_assert(BMo >= 4 && BNo >= 4, "whole float4 row segments");
-  constexpr int kOut = BMo * BNo, kQc = kKc / 4, kLd = kKc + 4;
-  constexpr int kAv = kKc * BMo / 4 / kThreads, kBv = kKc * BNo / 4 / kThreads;
-  static_assert(kAv * kThreads * 4 == kKc * BMo && kBv * kThreads * 4 == kKc * BNo,
-                "every chunk float4 has a lane");
-  __shared__ __attribute__((aligned(16))) float As[BMo][kLd];
-  __shared__ __attribute__((aligned(16))) float Bs[BNo][kLd];
-  __shared__ float Q[kQc][kOut + 1];
+// The fold kernel with its waves split by role (TN, f32 operands 16-byte
+// aligned, M % BMo == N % BNo == 0, K * M and K * N below 2^31, no q8
+// k-scale): the chain of each output is a strict sequence of adds, so one
+// wave does nothing but fold -- kF outputs per lane, their chains
+// interleaved -- while the other kW - 1 waves load, stage and form the
+// quads.  Operands and quads are double-buffered, one barrier per interval:
+// in interval i the producers form chunk i's quads (QM x QN output blocks
+// per task, written k-contiguous per output, Q[o][j]) and stage chunk i + 1
+// from a ring of kD register slots that runs kD chunks ahead, while the
+// folder adds chunk i - 1's quads, reading four of them per 16-byte read.
+// A and B are staged in rounds of their own (whole wave-uniform loads, the
+// last round's spare lanes re-reading the last element), and the steady
+// state issues its loads unconditionally -- with the folder's loop apart
+// from the producers' there is no join in it, so each store waits for its
+// own slot's loads and no more; the last intervals wait for every load.
+// Rows past K are clamped reads: they meet only quads past K / 4, which are
+// never folded.  The sums are GemmFoldKernel's, operation for operation.
+template <int BMo, int BNo, int kKc, int kD, int QM, int QN, int kW, int kF>
+__global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
+  constexpr int kOut = BMo * BNo, kQc = kKc / 4, kLd = kKc + 4, kQLd = kQc + 4;
+  static_assert(kOut == 64 * kF || (kF == 1 && kOut < 64), "kF outputs per folder lane");
+  constexpr int kP = 64 * (kW - 1);  // producer lanes
+  constexpr int kAf = kKc * BMo / 4, kBf = kKc * BNo / 4;  // float4 per chunk
+  constexpr int kRA = (kAf + kP - 1) / kP, kRB = (kBf + kP - 1) / kP;
+  constexpr int kBlkN = BNo / QN, kBlk = (BMo / QM) * kBlkN, kTasks = kBlk * kQc;
+  constexpr int kT = (kTasks + kP - 1) / kP;
+  static_assert(BMo % QM == 0 && BNo % QN == 0 && QM % 4 == 0 && QN % 4 == 0, "whole blocks");
+  __shared__ __attribute__((aligned(16))) float As[2][BMo][kLd];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BNo][kLd];
+  __shared__ __attribute__((aligned(16))) float Q[2][kOut][kQLd];
   const int tid = threadIdx.x;
+  const int p = tid - 64;
   const unsigned M = static_cast<unsigned>(g.M), N = static_cast<unsigned>(g.N),
                  K = static_cast<unsigned>(g.K);
   const unsigned total = gridDim.x * gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
@@ -985,121 +996,167 @@ __global__ void __launch_bounds__(kThreads) GemmFoldVecKernel(GemmArgs g) {
   const unsigned m0 = (t / gridDim.x) * BMo, n0 = (t % gridDim.x) * BNo;
   const float* __restrict__ A = g.A;
   const float* __restrict__ B = static_cast<const float*>(g.B);
-  float4 ra[kAv], rb[kBv];
-  auto load = [&](unsigned k0) {  // rows past K re-read row K - 1 (zeroed at the store)
+  float4 ra[kD][kRA], rb[kD][kRB];
+  auto load = [&](int s, unsigned k0) {
 #pragma unroll
-    for (int r = 0; r < kAv; ++r) {
-      const int f = tid + r * kThreads, kk = f / (BMo / 4), c4 = f % (BMo / 4);
-      const unsigned k = min(k0 + kk, K - 1);
-      ra[r] = *reinterpret_cast<const float4*>(A + k * M + m0 + 4 * c4);
+    for (int r = 0; r < kRA; ++r) {
+      const int f = min(p + r * kP, kAf - 1), kk = f / (BMo / 4), c4 = f % (BMo / 4);
+      ra[s][r] = *reinterpret_cast<const float4*>(A + min(k0 + kk, K - 1) * M + m0 + 4 * c4);
     }
 #pragma unroll
-    for (int r = 0; r < kBv; ++r) {
-      const int f = tid + r * kThreads, kk = f / (BNo / 4), c4 = f % (BNo / 4);
-      const unsigned k = min(k0 + kk, K - 1);
-      rb[r] = *reinterpret_cast<const float4*>(B + k * N + n0 + 4 * c4);
+    for (int r = 0; r < kRB; ++r) {
+      const int f = min(p + r * kP, kBf - 1), kk = f / (BNo / 4), c4 = f % (BNo / 4);
+      rb[s][r] = *reinterpret_cast<const float4*>(B + min(k0 + kk, K - 1) * N + n0 + 4 * c4);
     }
   };
-  auto store = [&](unsigned k0) {
+  auto store = [&](int s, int buf) {  // transposed into k-contiguous rows, alpha applied
 #pragma unroll
-    for (int r = 0; r < kAv; ++r) {
-      const int f = tid + r * kThreads, kk = f / (BMo / 4), c4 = f % (BMo / 4);
-      float4 v = ra[r];
+    for (int r = 0; r < kRA; ++r) {
+      const int f = min(p + r * kP, kAf - 1), kk = f / (BMo / 4), c4 = f % (BMo / 4);
+      float4 v = ra[s][r];
       if (g.alpha_a != 1.0f)
         v = make_float4(Mul(g.alpha_a, v.x), Mul(g.alpha_a, v.y), Mul(g.alpha_a, v.z),
                         Mul(g.alpha_a, v.w));
-      if (k0 + kk >= K) v = make_float4(0.f, 0.f, 0.f, 0.f);
-      As[4 * c4 + 0][kk] = v.x;
-      As[4 * c4 + 1][kk] = v.y;
-      As[4 * c4 + 2][kk] = v.z;
-      As[4 * c4 + 3][kk] = v.w;
+      As[buf][4 * c4 + 0][kk] = v.x;
+      As[buf][4 * c4 + 1][kk] = v.y;
+      As[buf][4 * c4 + 2][kk] = v.z;
+      As[buf][4 * c4 + 3][kk] = v.w;
     }
 #pragma unroll
-    for (int r = 0; r < kBv; ++r) {
-      const int f = tid + r * kThreads, kk = f / (BNo / 4), c4 = f % (BNo / 4);
-      float4 v = rb[r];
-      if (k0 + kk >= K) v = make_float4(0.f, 0.f, 0.f, 0.f);
-      Bs[4 * c4 + 0][kk] = v.x;
-      Bs[4 * c4 + 1][kk] = v.y;
-      Bs[4 * c4 + 2][kk] = v.z;
-      Bs[4 * c4 + 3][kk] = v.w;
+    for (int r = 0; r < kRB; ++r) {
+      const int f = min(p + r * kP, kBf - 1), kk = f / (BNo / 4), c4 = f % (BNo / 4);
+      const float4 v = rb[s][r];
+      Bs[buf][4 * c4 + 0][kk] = v.x;
+      Bs[buf][4 * c4 + 1][kk] = v.y;
+      Bs[buf][4 * c4 + 2][kk] = v.z;
+      Bs[buf][4 * c4 + 3][kk] = v.w;
     }
   };
-  const int o = tid % kOut;  // the output this lane folds (lanes below kOut)
-  const int mo = o / BNo, no = o % BNo;
-  const unsigned mf = m0 + mo, nf = n0 + no;
-  const bool folds = tid < kOut;  // M % BMo == N % BNo == 0: every output exists
-  float c = (folds && g.accumulate) ? g.C[static_cast<size_t>(mf) * N + nf] : 0.0f;
+  auto quads_of = [&](int buf, int nq) {
+#pragma unroll
+    for (int r = 0; r < kT; ++r) {
+      const int task = p + r * kP;
+      if (task >= kTasks) continue;
+      const int qb = task % kBlk, j = task / kBlk;
+      if (j >= nq) continue;
+      const int bm = qb / kBlkN, bn = qb % kBlkN;
+      float4 a[QM], b[QN];
+#pragma unroll
+      for (int u = 0; u < QM; ++u) a[u] = *reinterpret_cast<const float4*>(&As[buf][QM * bm + u][4 * j]);
+#pragma unroll
+      for (int v = 0; v < QN; ++v) b[v] = *reinterpret_cast<const float4*>(&Bs[buf][QN * bn + v][4 * j]);
+#pragma unroll
+      for (int u = 0; u < QM; ++u)
+#pragma unroll
+        for (int v = 0; v < QN; ++v)
+          Q[buf][(QM * bm + u) * BNo + QN * bn + v][j] =
+              Add(Add(Add(Mul(a[u].x, b[v].x), Mul(a[u].y, b[v].y)), Mul(a[u].z, b[v].z)),
+                  Mul(a[u].w, b[v].w));
+    }
+  };
   const unsigned quads = K / 4;
   const unsigned chunks = (quads + kQc - 1) / kQc;
-  load(0);
-  for (unsigned ch = 0; ch < chunks; ++ch) {
-    const unsigned k0 = ch * kKc;
-    __syncthreads();
-    if (ch + 1 == chunks) WaitVmAll();
-    store(k0);
-    __syncthreads();
-    if (ch + 1 < chunks) load(k0 + kKc);
-    const int nq = static_cast<int>(min(quads - ch * kQc, static_cast<unsigned>(kQc)));
-    // Quads in 2 x 2 output blocks: a lane reads two A rows and two B rows
-    // of quad j (four 16-byte reads) and forms the four outputs' quads.
-    // Block qb covers outputs (2 bm + u, 2 bn + v).
-    {
-      constexpr int kBlk = kOut / 4, kBlkN = BNo / 2, kQSlots = kThreads / kBlk;
-      static_assert(kThreads % kBlk == 0 && kQc % kQSlots == 0, "whole quad steps");
-      const int qb = tid % kBlk, qs = tid / kBlk;
-      const int bm = qb / kBlkN, bn = qb % kBlkN;
-      auto quad4 = [&](int j) {
-        const float4 a0 = *reinterpret_cast<const float4*>(&As[2 * bm][4 * j]);
-        const float4 a1 = *reinterpret_cast<const float4*>(&As[2 * bm + 1][4 * j]);
-        const float4 b0 = *reinterpret_cast<const float4*>(&Bs[2 * bn][4 * j]);
-        const float4 b1 = *reinterpret_cast<const float4*>(&Bs[2 * bn + 1][4 * j]);
-        const auto q = [](float4 a, float4 b) {
-          return Add(Add(Add(Mul(a.x, b.x), Mul(a.y, b.y)), Mul(a.z, b.z)), Mul(a.w, b.w));
-        };
-        Q[j][(2 * bm) * BNo + 2 * bn] = q(a0, b0);
-        Q[j][(2 * bm) * BNo + 2 * bn + 1] = q(a0, b1);
-        Q[j][(2 * bm + 1) * BNo + 2 * bn] = q(a1, b0);
-        Q[j][(2 * bm + 1) * BNo + 2 * bn + 1] = q(a1, b1);
-      };
-      if (nq == kQc) {
+  auto nq_of = [&](unsigned i) { return static_cast<int>(min(quads - i * kQc, static_cast<unsigned>(kQc))); };
+  const int fo = min(tid, kOut - 1);  // a folder lane's first output (lanes past kOut idle)
+  float c[kF];
 #pragma unroll
-        for (int j = qs; j < kQc; j += kQSlots) quad4(j);
-      } else {
-        for (int j = qs; j < nq; j += kQSlots) quad4(j);
+  for (int e = 0; e < kF; ++e) {
+    const int o = min(fo + 64 * e, kOut - 1);
+    c[e] = (tid < kOut && g.accumulate) ? g.C[static_cast<size_t>(m0 + o / BNo) * N + n0 + o % BNo] : 0.0f;
+  }
+  auto fold = [&](int buf, int nq) {
+    if (nq == kQc) {
+      constexpr int kH = kF == 1 ? kQc / 4 : kQc / 8;  // 16-byte reads per batch per output
+      static_assert((kQc / 4) % kH == 0, "whole batches");
+#pragma unroll
+      for (int h = 0; h < kQc / 4; h += kH) {
+        float4 q[kF][kH];
+#pragma unroll
+        for (int e = 0; e < kF; ++e)
+#pragma unroll
+          for (int i = 0; i < kH; ++i) q[e][i] = *reinterpret_cast<const float4*>(&Q[buf][fo + 64 * e][4 * (h + i)]);
+        __builtin_amdgcn_sched_barrier(0);  // every read of the batch in flight before the adds
+#pragma unroll
+        for (int i = 0; i < kH; ++i)
+#pragma unroll
+          for (int e = 0; e < kF; ++e) {
+            c[e] = Add(c[e], q[e][i].x);
+            c[e] = Add(c[e], q[e][i].y);
+            c[e] = Add(c[e], q[e][i].z);
+            c[e] = Add(c[e], q[e][i].w);
+          }
+      }
+    } else {
+      for (int j = 0; j < nq; ++j)
+#pragma unroll
+        for (int e = 0; e < kF; ++e) c[e] = Add(c[e], Q[buf][fo + 64 * e][j]);
+    }
+  };
+  if (chunks <= static_cast<unsigned>(kD) + 1) {  // a few chunks: one at a time
+    for (unsigned i = 0; i < chunks; ++i) {
+      if (tid >= 64) {
+        load(0, i * kKc);
+        WaitVmAll();
+        store(0, 0);
+      }
+      __syncthreads();
+      if (tid >= 64) quads_of(0, nq_of(i));
+      __syncthreads();
+      if (tid < 64) fold(0, nq_of(i));
+      __syncthreads();
+    }
+  } else if (tid < 64) {
+    __syncthreads();
+    for (unsigned i = 0; i <= chunks; ++i) {
+      if (i >= 1) fold((i - 1) & 1, nq_of(i - 1));
+      __syncthreads();
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < kD; ++s) load(s, s * kKc);
+    WaitVmAll();
+    store(0, 0);
+    load(0, kD * kKc);
+    __syncthreads();
+    // Interval i: chunk i's quads; chunk i + 1 stored from ring slot
+    // (i + 1) % kD, which then takes chunk i + 1 + kD.
+    const unsigned nmain = (chunks - kD - 1) / kD * kD;
+    for (unsigned i0 = 0; i0 < nmain; i0 += kD) {
+#pragma unroll
+      for (int u = 0; u < kD; ++u) {
+        const unsigned i = i0 + u;
+        quads_of(i & 1, kQc);
+        const int nx = (u + 1) % kD;
+        store(nx, (i + 1) & 1);
+        load(nx, (i + 1 + kD) * kKc);
+        __syncthreads();
       }
     }
-    __syncthreads();
-    if (folds) {
-      if (nq == kQc) {
-        // Quads read sixteen at a time into registers, the next sixteen in
-        // flight while these are added in order: the chain waits on LDS once.
-        static_assert(kQc % 32 == 0, "whole pairs of sixteen");
-        float qa[16], qb[16];
+    for (unsigned i = nmain; i <= chunks; ++i) {
+      if (i < chunks) quads_of(i & 1, nq_of(i));
+      if (i + 1 < chunks) {
+        WaitVmAll();
+        const unsigned slot = (i + 1) % kD;
 #pragma unroll
-        for (int u = 0; u < 16; ++u) qa[u] = Q[u][o];
-#pragma unroll
-        for (int j = 0; j < kQc; j += 32) {
-#pragma unroll
-          for (int u = 0; u < 16; ++u) qb[u] = Q[j + 16 + u][o];
-#pragma unroll
-          for (int u = 0; u < 16; ++u) c = Add(c, qa[u]);
-          if (j + 32 < kQc) {
-#pragma unroll
-            for (int u = 0; u < 16; ++u) qa[u] = Q[j + 32 + u][o];
+        for (int u = 0; u < kD; ++u)
+          if (slot == static_cast<unsigned>(u)) {
+            store(u, (i + 1) & 1);
+            if (i + 1 + kD < chunks) load(u, (i + 1 + kD) * kKc);
           }
-#pragma unroll
-          for (int u = 0; u < 16; ++u) c = Add(c, qb[u]);
-        }
-      } else {
-        for (int j = 0; j < nq; ++j) c = Add(c, Q[j][o]);
       }
+      __syncthreads();
     }
   }
-  if (!folds) return;
-  for (unsigned k = quads * 4; k < K; ++k)  // the K % 4 tail, one term at a time
-    c = Add(c, Mul(LoadA<2>(g, mf, k), B[static_cast<size_t>(k) * N + nf]));
-  g.C[static_cast<size_t>(mf) * N + nf] = Epilogue(g, mf, nf, c);
+  if (tid >= kOut || tid >= 64) return;
+#pragma unroll
+  for (int e = 0; e < kF; ++e) {
+    const int o = tid + 64 * e;
+    const unsigned mf = m0 + o / BNo, nf = n0 + o % BNo;
+    float v = c[e];
+    for (unsigned k = quads * 4; k < K; ++k)  // the K % 4 tail, one term at a time
+      v = Add(v, Mul(LoadA<2>(g, mf, k), B[static_cast<size_t>(k) * N + nf]));
+    g.C[static_cast<size_t>(mf) * N + nf] = Epilogue(g, mf, nf, v);
+  }
 }
 
 // The fold kernel for TN with f32 B over K >= 1024 when the outputs fill at
@@ -1116,20 +1173,21 @@ hipError_t LaunchFold(const GemmArgs& a, hipStream_t s) {
   int bno = 2;
   while (bno < 16 && static_cast<size_t>(bno) < a.N) bno *= 2;
   const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  // 16-byte staging over 256-deep chunks: 4 x 16 output blocks where that
-  // still gives at least 512 workgroups, else 4 x 8 (half the LDS, twice the
-  // workgroups: C4's 768 x 8 and 8 x 768 gradients run 33 us against 44).
   if (kLayout == 2 && a.M % 4 == 0 && a.N % 8 == 0 && a.K * a.M < (size_t{1} << 31) &&
       a.K * a.N < (size_t{1} << 31) && al16(a.A) && al16(a.B) && !a.a_k_scale) {
-    if (a.N % 16 == 0 && a.M * a.N >= 512 * 64) {
-      const dim3 grid(static_cast<unsigned>(a.N / 16), static_cast<unsigned>(a.M / 4));
+    // Role-split folds: 8 x 16 blocks (two outputs per folder lane) where
+    // they still fill the machine, else 4 x 8 (C5's 2048 x 16 and 16 x 2048
+    // gradients run 38 us against 55; C4's 768 x 8 and 8 x 768 20 us
+    // against 33).
+    if (a.M % 8 == 0 && a.N % 16 == 0 && (a.M / 8) * (a.N / 16) >= 256) {
+      const dim3 grid(static_cast<unsigned>(a.N / 16), static_cast<unsigned>(a.M / 8));
       if (grid.y > 65535) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((GemmFoldVecKernel<4, 16, 256>), grid, dim3(kThreads), 0, s, a);
-    } else {
-      const dim3 grid(static_cast<unsigned>(a.N / 8), static_cast<unsigned>(a.M / 4));
-      if (grid.y > 65535) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((GemmFoldVecKernel<4, 8, 256>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((GemmFoldSplitKernel<8, 16, 256, 2, 4, 4, 8, 2>), grid, dim3(512), 0, s, a);
+      return hipGetLastError();
     }
+    const dim3 grid(static_cast<unsigned>(a.N / 8), static_cast<unsigned>(a.M / 4));
+    if (grid.y > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((GemmFoldSplitKernel<4, 8, 512, 2, 4, 4, 5, 1>), grid, dim3(320), 0, s, a);
     return hipGetLastError();
   }
   const size_t bmo = kFoldOut / bno;
