@@ -143,7 +143,7 @@ struct seeai_ctx {
   const uint8_t* dead_prog = nullptr;
   uint64_t dead_hash = 0;
   uint64_t prog_hash = 0;  // of the range's program, taken at begin_range
-  std::vector<int8_t> dead;  // per instruction: -1 undecided, 0 kept, 1 dropped
+  std::vector<int8_t> dead;  // per instruction and asking site: -1 undecided, 0 kept, 1 dropped
   TilePolicy policy;  // kernel geometry (seeai_configure)
   // The relaxed GEMMs' bf16 copy of their activations, and what it holds:
   // a later relaxed GEMM of the same range that rounds the same bytes the
@@ -1257,16 +1257,21 @@ bool DeadFrom(seeai_ctx* c, uint64_t writer, uint64_t from, const Extent& E) {
   return true;
 }
 
-// DeadFrom, decided once per program and instruction: the answer depends on
-// the program's words and the binding alone (dropped at bind).
-bool DeadStore(seeai_ctx* c, uint64_t at_idx, uint64_t from, const Extent& E) {
+// DeadFrom, decided once per program, instruction and asking site (each
+// site asks one question of an instruction: 0 the producers' sinks and the
+// elementwise chains, 1 the low-rank fold, 2 the residual add behind a
+// GEMM, 3 the residual add behind a normalisation's gradient): the answer
+// depends on the program's words and the binding alone (dropped at bind).
+constexpr int kDeadSites = 4;
+bool DeadStore(seeai_ctx* c, uint64_t at_idx, uint64_t from, const Extent& E, int site = 0) {
   if (!c->allow_dead_store_drop) return false;
-  if (c->dead_prog != c->prog || c->dead.size() != c->prog_count || c->dead_hash != c->prog_hash) {
+  if (c->dead_prog != c->prog || c->dead.size() != c->prog_count * kDeadSites ||
+      c->dead_hash != c->prog_hash) {
     c->dead_prog = c->prog;
     c->dead_hash = c->prog_hash;
-    c->dead.assign(c->prog_count, -1);
+    c->dead.assign(c->prog_count * kDeadSites, -1);
   }
-  int8_t& v = c->dead[at_idx];
+  int8_t& v = c->dead[at_idx * kDeadSites + site];
   if (v < 0) v = DeadFrom(c, at_idx, from, E) ? 1 : 0;
   if (v) ++c->dropped_stores;
   return v != 0;
@@ -1379,7 +1384,36 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
         return -1;
       // C's store is dropped where the rest of the range overwrites C
       // before anything reads it.
-      if (DeadStore(c, idx, j + 1, out_a)) a.lr_store_c = 0;
+      if (DeadStore(c, idx, j + 1, out_a, 1)) a.lr_store_c = 0;
+      // A residual add of C' next (kAddEW, C' on one side, C' read by
+      // nothing after it) joins the epilogue: the add's output takes
+      // R + C' in C''s place.  Its output may be R itself, or C when C's
+      // store is dropped; it misses everything else the pass reads.
+      bool res_add = false;
+      if (j + 1 < c->range_end) {
+        Instruction ad;
+        std::memcpy(&ad, c->prog + (j + 1) * 64, sizeof ad);
+        const Ptrs R{c};
+        if (ad.opcode == 5 && ad.out[0] == a.M * a.N &&
+            (R.f(ad.in[0]) == b.C) != (R.f(ad.in[1]) == b.C)) {
+          const float* res = R.f(ad.in[0]) == b.C ? R.f(ad.in[1]) : R.f(ad.in[0]);
+          float* aout = R.f(ad.in[2]);
+          const uint64_t nb = a.M * a.N * 4;
+          const Extent e_res{reinterpret_cast<const uint8_t*>(res), nb};
+          const Extent e_out{reinterpret_cast<const uint8_t*>(aout), nb};
+          const bool clear =
+              !Hits(e_out, reads_a, na) && !Hits(e_out, &t_b, 1) && !Hits(e_out, &r_b, 1) &&
+              !Hits(e_res, &out_b, 1) && (aout == res || !Hits(e_out, &e_res, 1)) &&
+              (!a.lr_store_c || (!Hits(e_out, &out_a, 1) && !Hits(e_res, &out_a, 1)));
+          GemmArgs t = a;
+          t.lr_res = res;
+          t.lr_out = aout;
+          if (clear && Bf16DmaLowRankFits(t) && DeadStore(c, j, j + 2, out_b, 2)) {
+            a = t;
+            res_add = true;
+          }
+        }
+      }
       if (gap) {
         if (int rc = ExecuteOne(c, mid, P)) return rc;
       }
@@ -1388,6 +1422,7 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
       c->ndone = 0;
       if (gap) c->done[c->ndone++] = c->prog + (idx + 1) * 64;
       c->done[c->ndone++] = c->prog + j * 64;
+      if (res_add) c->done[c->ndone++] = c->prog + (j + 1) * 64;
       ++c->fused;
       return SEEAI_OK;
     }
@@ -1521,6 +1556,104 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
   return -1;
 }
 
+// The residual add behind a product: a GEMM with no addend, accumulate,
+// bias or activation whose C the next instruction, kAddEW, adds to another
+// operand X (either side; IEEE addition commutes) runs with X as its addend
+// and the add's output as C -- the epilogue's X + dot is the add's X + C,
+// the same rounding -- when C is read by nothing after the add (the
+// dead-store rule) and the add's output misses everything the product
+// reads (it may be X itself).  One pass instead of two over M x N floats.
+int TryFuseAddend(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
+  if (!c->allow_fusion || !c->prog || at < c->prog || at >= c->prog + c->prog_count * 64 ||
+      (at - c->prog) % 64 != 0)
+    return -1;
+  const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
+  if (idx + 1 >= c->range_end) return -1;
+  Instruction nx;
+  std::memcpy(&nx, c->prog + (idx + 1) * 64, sizeof nx);
+  if (nx.opcode != 5) return -1;
+  GemmArgs a{};
+  const char* what = DecodeGemm(c, ins, &a);
+  if (!what || a.addend || a.accumulate || a.bias || a.act || a.M * a.N != nx.out[0]) return -1;
+  const Ptrs R{c};
+  const float *x0 = R.f(nx.in[0]), *x1 = R.f(nx.in[1]);
+  float* out = R.f(nx.in[2]);
+  if ((x0 == a.C) == (x1 == a.C)) return -1;  // C on exactly one side
+  const float* X = x0 == a.C ? x1 : x0;
+  const uint64_t nb = a.M * a.N * 4;
+  const Extent e_out{reinterpret_cast<const uint8_t*>(out), nb};
+  const Extent e_x{reinterpret_cast<const uint8_t*>(X), nb};
+  const Extent e_c = GemmWrites(a);
+  Extent reads[8];
+  const int nr = GemmReads(a, reads);
+  if (Hits(e_out, reads, nr) || Hits(e_c, &e_x, 1) || (out != X && Hits(e_out, &e_x, 1)))
+    return -1;
+  if (!DeadStore(c, idx, idx + 2, e_c, 2)) return -1;
+  a.relaxed = Relaxed(c, ins);
+  a.addend = X;
+  a.C = out;
+  if (int rc = Gemm(c, a, what)) return rc;
+  c->done[0] = at + 64;
+  c->ndone = 1;
+  ++c->fused;
+  return SEEAI_OK;
+}
+
+// The residual add behind a normalisation's gradient: LayerNorm / RMSNorm
+// backward writing dx, then kAddEW of dx and a residual gradient R, runs as
+// one pass writing R + dx into the add's output (with the add's conversion
+// sink when a relaxed product follows), when dx is read by nothing after
+// the add and the add's output misses the normalisation's inputs (it may
+// be R itself).
+int TryFuseNormAdd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
+  if (!c->allow_fusion || !c->prog || (ins.opcode != 27 && ins.opcode != 32) || at < c->prog ||
+      at >= c->prog + c->prog_count * 64 || (at - c->prog) % 64 != 0)
+    return -1;
+  const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
+  if (idx + 1 >= c->range_end) return -1;
+  Instruction nx;
+  std::memcpy(&nx, c->prog + (idx + 1) * 64, sizeof nx);
+  if (nx.opcode != 5) return -1;
+  const Ptrs R{c};
+  const bool ln = ins.opcode == 27;
+  const uint64_t shape = ln ? ins.out[2] : ins.out[1];
+  const uint64_t rows = shape >> 32, cols = shape & 0xFFFFFFFFu, n = rows * cols;
+  const float *dy = R.f(ins.in[0]), *x = R.f(ins.in[1]), *g = R.f(ins.in[2]);
+  const float* mean = ln ? R.f(ins.out[0]) : nullptr;
+  const float* rstd = R.f(ln ? ins.out[1] : ins.out[0]);
+  const float* dx = R.f(ins.in[3]);
+  const float *x0 = R.f(nx.in[0]), *x1 = R.f(nx.in[1]);
+  float* out = R.f(nx.in[2]);
+  if (n == 0 || nx.out[0] != n || (x0 == dx) == (x1 == dx)) return -1;
+  const float* res = x0 == dx ? x1 : x0;
+  const uint64_t nb = n * 4;
+  const auto ext = [](const void* p, uint64_t bytes) {
+    return Extent{static_cast<const uint8_t*>(p), bytes};
+  };
+  const Extent reads[] = {ext(dy, nb), ext(x, nb), ext(g, cols * 4), ext(rstd, rows * 4),
+                          ext(mean ? mean : rstd, rows * 4)};
+  const Extent e_out = ext(out, nb), e_dx = ext(dx, nb), e_res = ext(res, nb);
+  if (Hits(e_out, reads, 5) || Hits(e_dx, &e_res, 1) || (out != res && Hits(e_out, &e_res, 1)) ||
+      Hits(e_res, reads, 2))
+    return -1;
+  if (!NormSinkFits(cols, {dy, x, g, out, res})) return -1;
+  if (!DeadStore(c, idx, idx + 2, e_dx, 3)) return -1;
+  Bf16Sink sink;
+  GemmArgs ga{};
+  const bool sunk = PlanSink(c, idx + 1, idx + 1, out, n, &sink, &ga);
+  if (ln)
+    SEEAI_TRY(c, LaunchLayerNormBwd(dy, x, g, mean, rstd, out, rows, cols, c->stream, sink, res),
+              "layernorm.bwd+add");
+  else
+    SEEAI_TRY(c, LaunchRmsNormBwd(dy, x, g, rstd, out, rows, cols, c->stream, sink, res),
+              "rmsnorm.bwd+add");
+  if (sunk) SinkDone(c, idx + 1, ga);
+  c->done[0] = at + 64;
+  c->ndone = 1;
+  ++c->fused;
+  return SEEAI_OK;
+}
+
 // A 64-bit hash of a program's words (FNV-1a over 8-byte words, then a
 // final avalanche): what the per-program dead-store decisions are keyed on
 // besides the program's address and length.
@@ -1560,6 +1693,8 @@ int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params
   if (rc < 0) rc = TryFuseAdamW(c, ins, at, P);
   if (rc < 0) rc = TryFuseAttnBwd(c, ins, at);
   if (rc < 0) rc = TryFuseElementwise(c, ins, at);
+  if (rc < 0) rc = TryFuseNormAdd(c, ins, at);
+  if (rc < 0) rc = TryFuseAddend(c, ins, at);
   if (rc < 0) rc = ExecuteOne(c, ins, P);
   c->cur_at = nullptr;
   return rc;

@@ -197,15 +197,18 @@ hipError_t LaunchFusedMap(const float* x, const float* o1, const float* o2, floa
 hipError_t LaunchLayerNormFwd(const float* x, const float* g, const float* b, float* y,
                               float* mean, float* rstd, size_t rows, size_t cols, float eps,
                               hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
+// With res, dx = res + the normalisation's gradient (a residual add fused
+// behind it; dx may be res itself).
 hipError_t LaunchLayerNormBwd(const float* dy, const float* x, const float* g,
                               const float* mean, const float* rstd, float* dx, size_t rows,
-                              size_t cols, hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
+                              size_t cols, hipStream_t s, const Bf16Sink& sink = Bf16Sink{},
+                              const float* res = nullptr);
 hipError_t LaunchRmsNormFwd(const float* x, const float* g, float* y, float* rstd, size_t rows,
                             size_t cols, float eps, hipStream_t s,
                             const Bf16Sink& sink = Bf16Sink{});
 hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, const float* rstd,
                             float* dx, size_t rows, size_t cols, hipStream_t s,
-                            const Bf16Sink& sink = Bf16Sink{});
+                            const Bf16Sink& sink = Bf16Sink{}, const float* res = nullptr);
 hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
                       float step, const float* table, int backward, hipStream_t s);
 hipError_t LaunchRopeTable(float* table, size_t S, size_t d, float step, hipStream_t s);
@@ -321,6 +324,9 @@ struct GemmArgs {
   int lr_k;            // 1..kLowRankMaxK
   int lr_store_c;      // also store C
   float lr_alpha;
+  // A residual add behind the site: lr_out = lr_res + (C + dot), the add's
+  // operand order immaterial (IEEE addition commutes); null: none.
+  const float* lr_res;
 };
 constexpr int kLowRankMaxK = 16;
 // Relaxed -> MFMA (k_gemm_f32.hip); otherwise the reference's order.

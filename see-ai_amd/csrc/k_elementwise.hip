@@ -49,17 +49,23 @@ AddEW4(const float4* __restrict__ x, const float4* __restrict__ y, float4* __res
 
 // A normalisation's output row: float4 where the row allows it (the same
 // per-element expression), with the sink; element by element otherwise.
+// With a residual row rr, the row stored is rr + the element (a residual
+// add fused behind the normalisation).
 template <class F>
-__device__ __forceinline__ void NormRowOut(float* __restrict__ yr, size_t row0, size_t cols, bool vec,
-                                           const Bf16Sink& sink, F&& elem) {
+__device__ __forceinline__ void NormRowOut(float* yr, size_t row0, size_t cols, bool vec,
+                                           const Bf16Sink& sink, const float* rr, F&& elem) {
   if (vec) {
     for (size_t c = threadIdx.x * 4; c < cols; c += kThreads * 4) {
-      const float4 v = make_float4(elem(c), elem(c + 1), elem(c + 2), elem(c + 3));
+      float4 v = make_float4(elem(c), elem(c + 1), elem(c + 2), elem(c + 3));
+      if (rr) {
+        const float4 r = *reinterpret_cast<const float4*>(rr + c);
+        v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
+      }
       if (sink.store_f32) *reinterpret_cast<float4*>(yr + c) = v;
       if (sink.out) SinkStore4(sink, row0 + c, v);
     }
   } else {
-    for (size_t c = threadIdx.x; c < cols; c += kThreads) yr[c] = elem(c);
+    for (size_t c = threadIdx.x; c < cols; c += kThreads) yr[c] = rr ? rr[c] + elem(c) : elem(c);
   }
 }
 
@@ -141,7 +147,7 @@ LayerNormFwdKernel(const float* __restrict__ x, const float* __restrict__ g,
     mean[r] = mu;
     rstd[r] = rs;
   }
-  NormRowOut(y + r * cols, r * cols, cols, vec, sink,
+  NormRowOut(y + r * cols, r * cols, cols, vec, sink, nullptr,
              [&](size_t c) { return (xr[c] - mu) * rs * g[c] + b[c]; });
 }
 
@@ -149,8 +155,8 @@ LayerNormFwdKernel(const float* __restrict__ x, const float* __restrict__ g,
 __global__ void __launch_bounds__(kThreads)
 LayerNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
                    const float* __restrict__ g, const float* __restrict__ mean,
-                   const float* __restrict__ rstd, float* __restrict__ dx, size_t cols, int vec,
-                   Bf16Sink sink) {
+                   const float* __restrict__ rstd, float* dx, size_t cols, int vec,
+                   Bf16Sink sink, const float* res) {
   __shared__ double red[kThreads / kWave];
   const size_t r = blockIdx.x;
   const float* dyr = dy + r * cols;
@@ -168,7 +174,7 @@ LayerNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
   const float inv_d = 1.0f / static_cast<float>(cols);
   const float mg = static_cast<float>(sg) * inv_d;
   const float mgx = static_cast<float>(sgx) * inv_d;
-  NormRowOut(dx + r * cols, r * cols, cols, vec, sink, [&](size_t c) {
+  NormRowOut(dx + r * cols, r * cols, cols, vec, sink, res ? res + r * cols : nullptr, [&](size_t c) {
     const float xhat = (xr[c] - mu) * rs;
     const float gg = dyr[c] * g[c];
     return rs * (gg - mg - xhat * mgx);
@@ -187,13 +193,14 @@ RmsNormFwdKernel(const float* __restrict__ x, const float* __restrict__ g, float
   ss = BlockSumD<kThreads>(ss, red);
   const float rs = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + eps);
   if (threadIdx.x == 0) rstd[r] = rs;
-  NormRowOut(y + r * cols, r * cols, cols, vec, sink, [&](size_t c) { return xr[c] * rs * g[c]; });
+  NormRowOut(y + r * cols, r * cols, cols, vec, sink, nullptr,
+             [&](size_t c) { return xr[c] * rs * g[c]; });
 }
 
 __global__ void __launch_bounds__(kThreads)
 RmsNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
                  const float* __restrict__ g, const float* __restrict__ rstd,
-                 float* __restrict__ dx, size_t cols, int vec, Bf16Sink sink) {
+                 float* dx, size_t cols, int vec, Bf16Sink sink, const float* res) {
   __shared__ double red[kThreads / kWave];
   const size_t r = blockIdx.x;
   const float* dyr = dy + r * cols;
@@ -205,7 +212,7 @@ RmsNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
   sgx = BlockSumD<kThreads>(sgx, red);
   const float inv_d = 1.0f / static_cast<float>(cols);
   const float mgx = static_cast<float>(sgx) * inv_d;
-  NormRowOut(dx + r * cols, r * cols, cols, vec, sink,
+  NormRowOut(dx + r * cols, r * cols, cols, vec, sink, res ? res + r * cols : nullptr,
              [&](size_t c) { return rs * (dyr[c] * g[c] - xr[c] * rs * rs * mgx); });
 }
 
@@ -626,12 +633,12 @@ hipError_t LaunchLayerNormFwd(const float* x, const float* g, const float* b, fl
 }
 hipError_t LaunchLayerNormBwd(const float* dy, const float* x, const float* g,
                               const float* mean, const float* rstd, float* dx, size_t rows,
-                              size_t cols, hipStream_t s, const Bf16Sink& sink) {
+                              size_t cols, hipStream_t s, const Bf16Sink& sink, const float* res) {
   if (rows == 0) return hipSuccess;
-  const int vec = NormSinkFits(cols, {dy, x, g, dx});
+  const int vec = NormSinkFits(cols, {dy, x, g, dx, res});
   if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(LayerNormBwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s,
-                     dy, x, g, mean, rstd, dx, cols, vec, sink);
+                     dy, x, g, mean, rstd, dx, cols, vec, sink, res);
   return hipGetLastError();
 }
 hipError_t LaunchRmsNormFwd(const float* x, const float* g, float* y, float* rstd, size_t rows,
@@ -645,12 +652,12 @@ hipError_t LaunchRmsNormFwd(const float* x, const float* g, float* y, float* rst
 }
 hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, const float* rstd,
                             float* dx, size_t rows, size_t cols, hipStream_t s,
-                            const Bf16Sink& sink) {
+                            const Bf16Sink& sink, const float* res) {
   if (rows == 0) return hipSuccess;
-  const int vec = NormSinkFits(cols, {dy, x, g, dx});
+  const int vec = NormSinkFits(cols, {dy, x, g, dx, res});
   if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(RmsNormBwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, dy,
-                     x, g, rstd, dx, cols, vec, sink);
+                     x, g, rstd, dx, cols, vec, sink, res);
   return hipGetLastError();
 }
 hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,

@@ -403,6 +403,11 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           o4[e] = AddRn(v[e], LowRankDot<kLR - 1>(t, lb[e], lr_r, g.lr_alpha));
+        if (g.lr_res) {
+          const float4 r4 = *reinterpret_cast<const float4*>(g.lr_res + o);
+          o4[0] = AddRn(r4.x, o4[0]), o4[1] = AddRn(r4.y, o4[1]);
+          o4[2] = AddRn(r4.z, o4[2]), o4[3] = AddRn(r4.w, o4[3]);
+        }
         *reinterpret_cast<float4*>(g.lr_out + o) = make_float4(o4[0], o4[1], o4[2], o4[3]);
       } else if (vec) {
         *reinterpret_cast<float4*>(C + o) = make_float4(v[0], v[1], v[2], v[3]);
@@ -553,7 +558,8 @@ bool Bf16DmaLowRankFits(const GemmArgs& a) {
   const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   return a.lr_out && a.lr_t && a.lr_b && a.lr_layout >= 0 && a.lr_layout <= 1 && a.lr_k >= 1 &&
          a.lr_k <= kLowRankMaxK && a.lr_k % 4 == 0 && a.N % 4 == 0 && !a.accumulate &&
-         al16(a.lr_t) && al16(a.lr_out) && al16(a.C) && (a.lr_layout == 1 || al16(a.lr_b));
+         al16(a.lr_t) && al16(a.lr_out) && al16(a.C) && (a.lr_layout == 1 || al16(a.lr_b)) &&
+         al16(a.lr_res);
 }
 
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,

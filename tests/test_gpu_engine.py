@@ -232,6 +232,12 @@ TINY_Q8 = dict(vocab=96, dim=128, heads=2, ffn=352, layers=2, seq=64, batch=2, r
 # sites per block); runs of up to 16 adjacent steps fuse into one launch.
 Q8_ADAMW = TINY_Q8["layers"] * 4 * 2
 Q8_ADAMW_FUSED = Q8_ADAMW - (Q8_ADAMW + 15) // 16
+# Residual adds that run inside their producer, per step: in every block the
+# FFN-down product's (x2 = x1 + down), the FFN input gradient's sum (the up
+# product's dX plus the gate product's) and the post-attention residual
+# gradient behind RMSNorm's backward; below the first block, the block
+# input's residual gradient behind the other RMSNorm backward.
+Q8_RESIDUAL_ADDS = TINY_Q8["layers"] * 3 + TINY_Q8["layers"] - 1
 
 
 def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch_cuda):
@@ -257,8 +263,9 @@ def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch
         dropped.append(eng.dropped_stores())
         eng.close()
     # per step and block: 4 LoRA forwards, the dK / dV pair, 2 SwiGLU chains;
-    # per step the AdamW runs
-    assert fused[0] == 3 * (TINY_Q8["layers"] * 7 + Q8_ADAMW_FUSED) and fused[1] == 0
+    # per step the residual adds and the AdamW runs
+    assert fused[0] == 3 * (TINY_Q8["layers"] * 7 + Q8_RESIDUAL_ADDS + Q8_ADAMW_FUSED)
+    assert fused[1] == 0
     # the base values no later instruction reads (30 here): same bits without them
     assert dropped[0] > 0 and dropped[1] == 0
     assert curves[0].tobytes() == curves[1].tobytes()
@@ -298,7 +305,8 @@ def test_q8_decoder_training_matches_the_oracle(hip, orc, torch_cuda, relaxed):
     # elementwise chains fuse in the exact family too.  Relaxed attention
     # runs f32 products here, so its dK / dV pair stays two dispatches.
     per_block = 6 if relaxed else 2
-    assert eng.fused_dispatches() == 6 * (TINY_Q8["layers"] * per_block + Q8_ADAMW_FUSED)
+    assert eng.fused_dispatches() == 6 * (TINY_Q8["layers"] * per_block + Q8_RESIDUAL_ADDS +
+                                          Q8_ADAMW_FUSED)
     eng.close()
 
 
@@ -461,7 +469,8 @@ def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda
     (GELU forward / backward, the SwiGLU passes, the softmax-xent backward,
     LayerNorm / RMSNorm forward and backward, the residual-gradient adds)
     and drops its f32 store where nothing else reads it; the product skips
-    its conversion pass.  With the NT products on the direct-to-LDS kernel
+    its conversion pass.  The residual adds run inside their producers
+    (a product's epilogue, a normalisation's backward) in the same run.  With the NT products on the direct-to-LDS kernel
     at these small K (relaxed_nt_dma_min_k 64), three steps with fusion on
     and off give the same losses and persistent bytes."""
     print(f"engine: fused conversions, tiny {plan}", flush=True)

@@ -1069,6 +1069,83 @@ def test_swiglu_chain_refuses_to_fuse_over_an_input(hip, orc, backend):
     assert ranged.tobytes() == apart.tobytes()
 
 
+@pytest.mark.parametrize("producer", ["gemm", "gemm_relaxed", "lora_site", "rmsnorm_bwd",
+                                      "layernorm_bwd"])
+@pytest.mark.parametrize("form", ["res_first", "res_second", "in_place", "read_later"])
+def test_residual_adds_run_inside_their_producers(hip, orc, backend, producer, form):
+    """kAddEW of a producer's output and a residual R, with the output read by
+    nothing after the add, runs inside the producer: a GEMM takes R as its
+    addend and writes the add's output; a normalisation's backward writes
+    R + dx.  Bitwise the instructions one by one (the producer's own output
+    keeps its old bytes), one fused dispatch; R on either side of the add,
+    the add written over R; with the output read again, the two run apart."""
+    from tests.plan_ops import ins
+    rows, cols = 256, 256
+    n = rows * cols
+    r = rng(len(producer) * 31 + len(form))
+    ar = Arena()
+    res = ar.add("R", r.standard_normal((rows, cols)).astype(np.float32))
+    out = res if form == "in_place" else ar.empty("out", (rows, cols))
+    prod = ar.empty("P", (rows, cols))
+    dead_too = []
+    if producer == "lora_site":
+        # the frozen q8 product with the rank-r term folded in (its base
+        # value read by nothing else), then the add of the site's output
+        rx, cs_flag = 1 << 5, 1 << 4
+        K, rank = 256, 16
+        x = ar.add("x", r.standard_normal((rows, K)).astype(np.float32))
+        A = ar.add("A", (r.standard_normal((K, rank)) * 0.02).astype(np.float32))
+        B = ar.add("B", (r.standard_normal((rank, cols)) * 0.02).astype(np.float32))
+        w = ar.add("W", r.integers(-127, 128, (K, cols)).astype(np.int8), rodata=True)
+        ws = ar.add("Ws", r.uniform(1e-3, 5e-2, cols).astype(np.float32), rodata=True)
+        c0, t = ar.empty("C0", (rows, cols)), ar.empty("t", (rows, rank))
+        prog = [ins(29, [x, w, c0, ws], [rows, cols, K], flags=rx | cs_flag),
+                ins(1, [x, A, t], [rows, rank, K]),
+                ins(1, [t, B, prod, c0], [rows, cols, rank], flags=1 << 3, imm=f32_bits(2.0))]
+        dead_too = ["C0"]
+    elif producer.startswith("gemm"):
+        K = 128
+        x = ar.add("x", r.standard_normal((rows, K)).astype(np.float32))
+        # relaxed: a read-only weight, so the product takes the direct-to-LDS kernel
+        w = ar.add("W", (r.standard_normal((K, cols)) * 0.1).astype(np.float32),
+                   rodata=producer == "gemm_relaxed")
+        flags = (1 << 5) if producer == "gemm_relaxed" else 0
+        prog = [ins(1, [x, w, prod], [rows, cols, K], flags=flags)]
+    else:
+        x = ar.add("x", r.standard_normal((rows, cols)).astype(np.float32))
+        dy = ar.add("dy", r.standard_normal((rows, cols)).astype(np.float32))
+        g = ar.add("g", r.uniform(0.5, 1.5, cols).astype(np.float32))
+        y, rstd = ar.empty("y", (rows, cols)), ar.empty("rstd", (rows,))
+        shape = (rows << 32) | cols
+        if producer == "rmsnorm_bwd":
+            prog = [ins(31, [x, g, y, rstd], [shape]), ins(32, [dy, x, g, prod], [rstd, shape])]
+        else:
+            b = ar.add("b", r.standard_normal(cols).astype(np.float32))
+            mean = ar.empty("mean", (rows,))
+            prog = [ins(26, [x, g, b, y], [shape, mean, rstd]),
+                    ins(27, [dy, x, g, prod], [mean, rstd, shape])]
+    prog.append(ins(5, [prod, res, out] if form == "res_second" else [res, prod, out], [n]))
+    if form == "read_later":
+        prog += _readers(ar, ["P"])
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before = backend.fused_dispatches()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    fused = form != "read_later"
+    # the site folds either way; the add joins it unless P is read again
+    assert backend.fused_dispatches() - before == int(fused or producer == "lora_site")
+    dead = (["P"] if fused else []) + dead_too
+    diff = np.flatnonzero(ranged != _restored(apart, ar, dead, arena))
+    assert diff.size == 0, f"{diff.size} bytes differ from byte {diff[:1]}"
+    name = "R" if form == "in_place" else "out"
+    e = maxrel(ar.get(ranged, name), ar.get(cpu, name))
+    relaxed = producer in ("gemm_relaxed", "lora_site")
+    assert e <= (TOL_BF16 if relaxed else TOL), f"{name}: {e:.3g}"
+
+
 def test_attn_dkdv_entry_point_matches_the_separate_passes(hip, torch_cuda):
     import torch
     B, S, H, d = 2, 384, 3, 64
