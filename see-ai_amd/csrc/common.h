@@ -324,8 +324,8 @@ struct GemmArgs {
   int lr_k;            // 1..kLowRankMaxK
   int lr_store_c;      // also store C
   float lr_alpha;
-  // A residual add behind the site: lr_out = lr_res + (C + dot), the add's
-  // operand order immaterial (IEEE addition commutes); null: none.
+  // A residual add behind the site (NT sites): lr_out = lr_res + (C + dot),
+  // the add's operand order immaterial (IEEE addition commutes); null: none.
   const float* lr_res;
 };
 constexpr int kLowRankMaxK = 16;

@@ -403,7 +403,9 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           o4[e] = AddRn(v[e], LowRankDot<kLR - 1>(t, lb[e], lr_r, g.lr_alpha));
-        if (g.lr_res) {
+        // (NT sites only: in the NN instance the extra operand pushes the
+        // 256 x 256 tile into scratch.)
+        if (kLR == 2 && g.lr_res) {
           const float4 r4 = *reinterpret_cast<const float4*>(g.lr_res + o);
           o4[0] = AddRn(r4.x, o4[0]), o4[1] = AddRn(r4.y, o4[1]);
           o4[2] = AddRn(r4.z, o4[2]), o4[3] = AddRn(r4.w, o4[3]);

@@ -1089,20 +1089,20 @@ def test_residual_adds_run_inside_their_producers(hip, orc, backend, producer, f
     prod = ar.empty("P", (rows, cols))
     dead_too = []
     if producer == "lora_site":
-        # the frozen q8 product with the rank-r term folded in (its base
-        # value read by nothing else), then the add of the site's output
+        # a LoRA site's input gradient -- the frozen q8 NT product with the
+        # rank-r term folded in, its base value read by nothing else -- then
+        # the add of the site's output
         rx, cs_flag = 1 << 5, 1 << 4
-        K, rank = 256, 16
-        x = ar.add("x", r.standard_normal((rows, K)).astype(np.float32))
-        A = ar.add("A", (r.standard_normal((K, rank)) * 0.02).astype(np.float32))
-        B = ar.add("B", (r.standard_normal((rank, cols)) * 0.02).astype(np.float32))
-        w = ar.add("W", r.integers(-127, 128, (K, cols)).astype(np.int8), rodata=True)
-        ws = ar.add("Ws", r.uniform(1e-3, 5e-2, cols).astype(np.float32), rodata=True)
-        c0, t = ar.empty("C0", (rows, cols)), ar.empty("t", (rows, rank))
-        prog = [ins(29, [x, w, c0, ws], [rows, cols, K], flags=rx | cs_flag),
-                ins(1, [x, A, t], [rows, rank, K]),
-                ins(1, [t, B, prod, c0], [rows, cols, rank], flags=1 << 3, imm=f32_bits(2.0))]
-        dead_too = ["C0"]
+        K, rank = 768, 16
+        dC = ar.add("dC", r.standard_normal((rows, K)).astype(np.float32))
+        dt = ar.add("dt", r.standard_normal((rows, rank)).astype(np.float32))
+        A = ar.add("A", (r.standard_normal((cols, rank)) * 0.02).astype(np.float32))
+        w = ar.add("W", r.integers(-127, 128, (cols, K)).astype(np.int8), rodata=True)
+        ws = ar.add("Ws", r.uniform(1e-3, 5e-2, K).astype(np.float32), rodata=True)
+        p1 = ar.empty("P1", (rows, cols))
+        prog = [ins(30, [dC, w, p1, ws], [rows, cols, K], flags=rx | cs_flag),
+                ins(2, [dt, A, prod, p1], [rows, cols, rank], flags=1 << 3)]
+        dead_too = ["P1"]
     elif producer.startswith("gemm"):
         K = 128
         x = ar.add("x", r.standard_normal((rows, K)).astype(np.float32))
