@@ -216,6 +216,194 @@ RmsNormBwdKernel(const float* __restrict__ dy, const float* __restrict__ x,
              [&](size_t c) { return rs * (dyr[c] * g[c] - xr[c] * rs * rs * mgx); });
 }
 
+// The normalisations with a row per wave (rows of at most 256 kV floats,
+// a multiple of 4, 16-byte aligned operands): lane l holds float4 l + 64 j
+// of its row in registers, so the row is read once; the double sums are
+// wave reductions (the same sums as the block kernels above, in another
+// association -- f32 stats within an ulp of them), and the outputs are the
+// block kernels' per-element expressions, with the sink and the residual.
+template <int kV>
+__device__ __forceinline__ void LoadRow4(const float* __restrict__ p, int lane, size_t cols,
+                                         float4 (&v)[kV]) {
+#pragma unroll
+  for (int j = 0; j < kV; ++j) {
+    const size_t c = 4 * static_cast<size_t>(lane + kWave * j);
+    v[j] = c < cols ? *reinterpret_cast<const float4*>(p + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+template <int kV, class F>
+__device__ __forceinline__ void StoreRow4(float* yr, size_t row0, size_t cols, int lane,
+                                          const Bf16Sink& sink, const float* rr, F&& elem) {
+#pragma unroll
+  for (int j = 0; j < kV; ++j) {
+    const size_t c = 4 * static_cast<size_t>(lane + kWave * j);
+    if (c >= cols) continue;
+    float4 v = make_float4(elem(j, 0), elem(j, 1), elem(j, 2), elem(j, 3));
+    if (rr) {
+      const float4 r = *reinterpret_cast<const float4*>(rr + c);
+      v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
+    }
+    if (sink.store_f32) *reinterpret_cast<float4*>(yr + c) = v;
+    if (sink.out) SinkStore4(sink, row0 + c, v);
+  }
+}
+
+__device__ __forceinline__ float Comp(const float4& v, int e) {
+  return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
+
+template <int kV>
+__global__ void __launch_bounds__(kThreads)
+LayerNormFwdRows(const float* __restrict__ x, const float* __restrict__ g,
+                 const float* __restrict__ b, float* __restrict__ y, float* __restrict__ mean,
+                 float* __restrict__ rstd, size_t rows, size_t cols, float eps, Bf16Sink sink) {
+  const int lane = threadIdx.x % kWave;
+  const size_t r = static_cast<size_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
+  if (r >= rows) return;
+  float4 xv[kV];
+  LoadRow4<kV>(x + r * cols, lane, cols, xv);
+  double sum = 0.0;
+#pragma unroll
+  for (int j = 0; j < kV; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum += Comp(xv[j], e);
+  sum = WaveSumD(sum);
+  const float mu = static_cast<float>(sum / static_cast<double>(cols));
+  double var = 0.0;
+#pragma unroll
+  for (int j = 0; j < kV; ++j) {
+    if (4 * static_cast<size_t>(lane + kWave * j) >= cols) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const double d = static_cast<double>(Comp(xv[j], e)) - mu;
+      var += d * d;
+    }
+  }
+  var = WaveSumD(var);
+  const float rs = 1.0f / sqrtf(static_cast<float>(var / static_cast<double>(cols)) + eps);
+  if (lane == 0) {
+    mean[r] = mu;
+    rstd[r] = rs;
+  }
+  StoreRow4<kV>(y + r * cols, r * cols, cols, lane, sink, nullptr, [&](int j, int e) {
+    const size_t c = 4 * static_cast<size_t>(lane + kWave * j) + e;
+    return (Comp(xv[j], e) - mu) * rs * g[c] + b[c];
+  });
+}
+
+template <int kV>
+__global__ void __launch_bounds__(kThreads)
+LayerNormBwdRows(const float* __restrict__ dy, const float* __restrict__ x,
+                 const float* __restrict__ g, const float* __restrict__ mean,
+                 const float* __restrict__ rstd, float* dx, size_t rows, size_t cols,
+                 Bf16Sink sink, const float* res) {
+  const int lane = threadIdx.x % kWave;
+  const size_t r = static_cast<size_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
+  if (r >= rows) return;
+  float4 xv[kV], dv[kV];
+  LoadRow4<kV>(x + r * cols, lane, cols, xv);
+  LoadRow4<kV>(dy + r * cols, lane, cols, dv);
+  const float mu = mean[r], rs = rstd[r];
+  double sg = 0.0, sgx = 0.0;
+#pragma unroll
+  for (int j = 0; j < kV; ++j) {
+    const size_t c0 = 4 * static_cast<size_t>(lane + kWave * j);
+    if (c0 >= cols) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float xhat = (Comp(xv[j], e) - mu) * rs;
+      const float gg = Comp(dv[j], e) * g[c0 + e];
+      sg += gg;
+      sgx += static_cast<double>(gg) * xhat;
+    }
+  }
+  sg = WaveSumD(sg);
+  sgx = WaveSumD(sgx);
+  const float inv_d = 1.0f / static_cast<float>(cols);
+  const float mg = static_cast<float>(sg) * inv_d;
+  const float mgx = static_cast<float>(sgx) * inv_d;
+  StoreRow4<kV>(dx + r * cols, r * cols, cols, lane, sink, res ? res + r * cols : nullptr,
+                [&](int j, int e) {
+                  const size_t c = 4 * static_cast<size_t>(lane + kWave * j) + e;
+                  const float xhat = (Comp(xv[j], e) - mu) * rs;
+                  const float gg = Comp(dv[j], e) * g[c];
+                  return rs * (gg - mg - xhat * mgx);
+                });
+}
+
+template <int kV>
+__global__ void __launch_bounds__(kThreads)
+RmsNormFwdRows(const float* __restrict__ x, const float* __restrict__ g, float* __restrict__ y,
+               float* __restrict__ rstd, size_t rows, size_t cols, float eps, Bf16Sink sink) {
+  const int lane = threadIdx.x % kWave;
+  const size_t r = static_cast<size_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
+  if (r >= rows) return;
+  float4 xv[kV];
+  LoadRow4<kV>(x + r * cols, lane, cols, xv);
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < kV; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += static_cast<double>(Comp(xv[j], e)) * Comp(xv[j], e);
+  ss = WaveSumD(ss);
+  const float rs = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + eps);
+  if (lane == 0) rstd[r] = rs;
+  StoreRow4<kV>(y + r * cols, r * cols, cols, lane, sink, nullptr, [&](int j, int e) {
+    const size_t c = 4 * static_cast<size_t>(lane + kWave * j) + e;
+    return Comp(xv[j], e) * rs * g[c];
+  });
+}
+
+template <int kV>
+__global__ void __launch_bounds__(kThreads)
+RmsNormBwdRows(const float* __restrict__ dy, const float* __restrict__ x,
+               const float* __restrict__ g, const float* __restrict__ rstd, float* dx,
+               size_t rows, size_t cols, Bf16Sink sink, const float* res) {
+  const int lane = threadIdx.x % kWave;
+  const size_t r = static_cast<size_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
+  if (r >= rows) return;
+  float4 xv[kV], dv[kV];
+  LoadRow4<kV>(x + r * cols, lane, cols, xv);
+  LoadRow4<kV>(dy + r * cols, lane, cols, dv);
+  const float rs = rstd[r];
+  double sgx = 0.0;
+#pragma unroll
+  for (int j = 0; j < kV; ++j) {
+    const size_t c0 = 4 * static_cast<size_t>(lane + kWave * j);
+    if (c0 >= cols) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      sgx += static_cast<double>(Comp(dv[j], e) * g[c0 + e]) * Comp(xv[j], e);
+  }
+  sgx = WaveSumD(sgx);
+  const float inv_d = 1.0f / static_cast<float>(cols);
+  const float mgx = static_cast<float>(sgx) * inv_d;
+  StoreRow4<kV>(dx + r * cols, r * cols, cols, lane, sink, res ? res + r * cols : nullptr,
+                [&](int j, int e) {
+                  const size_t c = 4 * static_cast<size_t>(lane + kWave * j) + e;
+                  return rs * (Comp(dv[j], e) * g[c] - Comp(xv[j], e) * rs * rs * mgx);
+                });
+}
+
+// The float4 slots per lane for a row of `cols` (0: the row kernels do not
+// take it -- over 4096 floats).
+int RowSlots(size_t cols) {
+  for (int v : {1, 2, 3, 4, 8, 16})
+    if (static_cast<size_t>(v) * 256 >= cols) return v;
+  return 0;
+}
+
+#define SEEAI_ROWS_SWITCH(KERNEL, ...)                                                        \
+  switch (RowSlots(cols)) {                                                                  \
+    case 1: hipLaunchKernelGGL((KERNEL<1>), grid, dim3(kThreads), 0, s, __VA_ARGS__); break;  \
+    case 2: hipLaunchKernelGGL((KERNEL<2>), grid, dim3(kThreads), 0, s, __VA_ARGS__); break;  \
+    case 3: hipLaunchKernelGGL((KERNEL<3>), grid, dim3(kThreads), 0, s, __VA_ARGS__); break;  \
+    case 4: hipLaunchKernelGGL((KERNEL<4>), grid, dim3(kThreads), 0, s, __VA_ARGS__); break;  \
+    case 8: hipLaunchKernelGGL((KERNEL<8>), grid, dim3(kThreads), 0, s, __VA_ARGS__); break;  \
+    default: hipLaunchKernelGGL((KERNEL<16>), grid, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+  }
+
 // RoPE (attention.cc:103-174): one lane per interleaved pair (c, c+1) of a
 // (b, s, h) head segment, so a wave moves 512 contiguous bytes in and out
 // (float2 where the operands are 8-byte aligned).  The rotation is the
@@ -627,6 +815,11 @@ hipError_t LaunchLayerNormFwd(const float* x, const float* g, const float* b, fl
   if (rows == 0) return hipSuccess;
   const int vec = NormSinkFits(cols, {x, g, b, y});
   if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
+  if (vec && RowSlots(cols) > 0) {
+    const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+    SEEAI_ROWS_SWITCH(LayerNormFwdRows, x, g, b, y, mean, rstd, rows, cols, eps, sink)
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(LayerNormFwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s,
                      x, g, b, y, mean, rstd, cols, eps, vec, sink);
   return hipGetLastError();
@@ -637,6 +830,11 @@ hipError_t LaunchLayerNormBwd(const float* dy, const float* x, const float* g,
   if (rows == 0) return hipSuccess;
   const int vec = NormSinkFits(cols, {dy, x, g, dx, res});
   if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
+  if (vec && RowSlots(cols) > 0) {
+    const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+    SEEAI_ROWS_SWITCH(LayerNormBwdRows, dy, x, g, mean, rstd, dx, rows, cols, sink, res)
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(LayerNormBwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s,
                      dy, x, g, mean, rstd, dx, cols, vec, sink, res);
   return hipGetLastError();
@@ -646,6 +844,11 @@ hipError_t LaunchRmsNormFwd(const float* x, const float* g, float* y, float* rst
   if (rows == 0) return hipSuccess;
   const int vec = NormSinkFits(cols, {x, g, y});
   if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
+  if (vec && RowSlots(cols) > 0) {
+    const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+    SEEAI_ROWS_SWITCH(RmsNormFwdRows, x, g, y, rstd, rows, cols, eps, sink)
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(RmsNormFwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, x,
                      g, y, rstd, cols, eps, vec, sink);
   return hipGetLastError();
@@ -656,6 +859,11 @@ hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, con
   if (rows == 0) return hipSuccess;
   const int vec = NormSinkFits(cols, {dy, x, g, dx, res});
   if (!vec && (sink.out || !sink.store_f32)) return hipErrorInvalidValue;
+  if (vec && RowSlots(cols) > 0) {
+    const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+    SEEAI_ROWS_SWITCH(RmsNormBwdRows, dy, x, g, rstd, dx, rows, cols, sink, res)
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(RmsNormBwdKernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, dy,
                      x, g, rstd, dx, cols, vec, sink, res);
   return hipGetLastError();

@@ -320,7 +320,10 @@ def test_elementwise_family(hip, orc, backend):
         assert e <= TOL, f"{name}: {e:.3g}"
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 1), (37, 300), (64, 768), (9, 2048)])
+# (1, 1) and (3, 4100) take the block-per-row kernels; the rest a row per
+# wave at 2, 3, 4, 8 and 16 float4 per lane (37 rows: a partial workgroup)
+@pytest.mark.parametrize("rows,cols", [(1, 1), (37, 300), (64, 768), (6, 1000), (9, 2048),
+                                       (5, 4096), (3, 4100)])
 def test_norms(hip, orc, backend, rows, cols):
     from tests.plan_ops import ins
     r = rng(rows * cols)
