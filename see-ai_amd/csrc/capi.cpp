@@ -1655,6 +1655,64 @@ int TryFuseNormAdd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   return SEEAI_OK;
 }
 
+// The loss at the turn of a train program: softmax-xent forward, the fill of
+// its seed, softmax-xent backward over the same probabilities and labels
+// (plain or masked).  The fill runs first (it touches nothing the forward
+// reads or writes), then one pass forms the probabilities and, from them,
+// the gradient -- the backward's expression on the same f32 values, with
+// its conversion sink -- storing the probabilities only where something
+// after the backward reads them.  One read of the logits and no read of
+// the probabilities instead of a write and a read.
+int TryFuseXEnt(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
+                const seeai_step_params& P) {
+  if (!c->allow_fusion || !c->prog || (ins.opcode != 11 && ins.opcode != 51) || at < c->prog ||
+      at >= c->prog + c->prog_count * 64 || (at - c->prog) % 64 != 0)
+    return -1;
+  const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
+  if (idx + 2 >= c->range_end) return -1;
+  Instruction f, b;
+  std::memcpy(&f, c->prog + (idx + 1) * 64, sizeof f);
+  std::memcpy(&b, c->prog + (idx + 2) * 64, sizeof b);
+  if (f.opcode != 19 || b.opcode != ins.opcode + 1 || b.in[0] != ins.in[3] ||
+      b.in[1] != ins.in[1] || b.out[0] != ins.out[0] || b.out[1] != ins.out[1])
+    return -1;
+  const Ptrs R{c};
+  const uint64_t N = ins.out[0], C = ins.out[1];
+  const float* logits = R.f(ins.in[0]);
+  const int32_t* labels = R.i32(ins.in[1]);
+  float *loss = R.f(ins.in[2]), *probs = R.f(ins.in[3]);
+  const float* seed = R.f(b.in[2]);
+  float* dl = R.f(b.in[3]);
+  const auto ext = [](const void* p, uint64_t bytes) {
+    return Extent{static_cast<const uint8_t*>(p), bytes};
+  };
+  const Extent fwd[] = {ext(logits, N * C * 4), ext(labels, N * 4), ext(loss, 4),
+                        ext(probs, N * C * 4)};
+  const Extent e_fill = ext(R.f(f.in[0]), f.out[0] * 4), e_dl = ext(dl, N * C * 4),
+               e_seed = ext(seed, 4);
+  if (Hits(e_fill, fwd, 4) || Hits(e_dl, fwd, 4) || Hits(e_dl, &e_seed, 1) ||
+      Hits(e_seed, fwd + 2, 2))
+    return -1;
+  float* keep = DeadStore(c, idx, idx + 3, fwd[3]) ? nullptr : probs;
+  if (!XEntFusedFits(logits, keep, dl, C)) return -1;
+  void* ws;
+  if (int rc = Scratch(c, XEntFwdScratchBytes(N), &ws)) return rc;
+  if (int rc = ExecuteOne(c, f, P)) return rc;
+  Bf16Sink sink;
+  GemmArgs ga{};
+  const bool sunk = PlanSink(c, idx + 2, idx + 2, dl, N * C, &sink, &ga);
+  SEEAI_TRY(c,
+            LaunchXEntFwdBwd(logits, labels, loss, keep, seed, dl, N, C, ins.opcode == 51, ws,
+                             c->stream, sink),
+            "softmax_xent.fwd+bwd");
+  if (sunk) SinkDone(c, idx + 2, ga);
+  c->done[0] = at + 64;
+  c->done[1] = at + 128;
+  c->ndone = 2;
+  ++c->fused;
+  return SEEAI_OK;
+}
+
 // A 64-bit hash of a program's words (FNV-1a over 8-byte words, then a
 // final avalanche): what the per-program dead-store decisions are keyed on
 // besides the program's address and length.
@@ -1695,6 +1753,7 @@ int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params
   if (rc < 0) rc = TryFuseAttnBwd(c, ins, at);
   if (rc < 0) rc = TryFuseElementwise(c, ins, at);
   if (rc < 0) rc = TryFuseNormAdd(c, ins, at);
+  if (rc < 0) rc = TryFuseXEnt(c, ins, at, P);
   if (rc < 0) rc = TryFuseAddend(c, ins, at);
   if (rc < 0) rc = ExecuteOne(c, ins, P);
   c->cur_at = nullptr;

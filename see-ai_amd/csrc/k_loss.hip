@@ -132,16 +132,48 @@ XEntSerialSumKernel(const float* __restrict__ logits, const float* __restrict__ 
 // --- pass 3: probabilities and the label term ----------------------------------
 constexpr int kProbThreads = 256;
 
+// With kBwd (the backward fused behind the forward, every row 16-byte
+// aligned): each probability also becomes its gradient, scale * p minus
+// scale at the label (zero on a masked row) -- XEntBwdKernel's expression on
+// the same f32 p -- stored with the sink; probs is stored only where given.
+template <bool kBwd>
 __global__ void __launch_bounds__(kProbThreads)
 XEntProbsKernel(const float* __restrict__ logits, const int32_t* __restrict__ labels,
                 const float* __restrict__ row_max, const float* __restrict__ row_sum,
-                float* __restrict__ probs, double* __restrict__ row_loss, size_t C, int masked) {
+                float* __restrict__ probs, double* __restrict__ row_loss, size_t C, int masked,
+                const float* __restrict__ scale_p, float* __restrict__ dl, Bf16Sink sink) {
   const size_t r = blockIdx.x;
   const float* x = logits + r * C;
   float* p = probs + r * C;
   const float mx = row_max[r];
   const float inv_sum = 1.0f / row_sum[r];  // loss.cc:30
-  if (Vec4Rows(logits, C) && Vec4Rows(probs, C)) {
+  if constexpr (kBwd) {
+    const float scale = *scale_p;
+    const int32_t lab = labels[r];
+    const bool zero = masked && lab < 0;
+    const size_t lc = static_cast<size_t>(lab);
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float4* d4 = reinterpret_cast<float4*>(dl + r * C);
+    for (size_t c = threadIdx.x; c < C / 4; c += kProbThreads) {
+      const float4 v = x4[c];
+      const float4 q = make_float4(expf(v.x - mx) * inv_sum, expf(v.y - mx) * inv_sum,
+                                   expf(v.z - mx) * inv_sum, expf(v.w - mx) * inv_sum);
+      if (probs) reinterpret_cast<float4*>(p)[c] = q;
+      float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (!zero) {
+        g = make_float4(scale * q.x, scale * q.y, scale * q.z, scale * q.w);
+        if (lc / 4 == c) {
+          const size_t l = lc % 4;
+          if (l == 0) g.x -= scale;
+          else if (l == 1) g.y -= scale;
+          else if (l == 2) g.z -= scale;
+          else g.w -= scale;
+        }
+      }
+      if (sink.store_f32) d4[c] = g;
+      if (sink.out) SinkStore4(sink, r * C + 4 * c, g);
+    }
+  } else if (Vec4Rows(logits, C) && Vec4Rows(probs, C)) {
     const float4* x4 = reinterpret_cast<const float4*>(x);
     float4* p4 = reinterpret_cast<float4*>(p);
     for (size_t c = threadIdx.x; c < C / 4; c += kProbThreads) {
@@ -265,8 +297,32 @@ hipError_t LaunchXEntFwd(const float* logits, const int32_t* labels, float* loss
   hipLaunchKernelGGL(XEntRowMaxKernel, dim3(rows), dim3(kMaxThreads), 0, s, logits, row_max, C);
   hipLaunchKernelGGL(XEntSerialSumKernel, dim3(static_cast<unsigned>((N + kSumRows - 1) / kSumRows)),
                      dim3(kSumThreads), 0, s, logits, row_max, row_sum, N, C);
-  hipLaunchKernelGGL(XEntProbsKernel, dim3(rows), dim3(kProbThreads), 0, s, logits, labels, row_max,
-                     row_sum, probs, row_loss, C, masked);
+  hipLaunchKernelGGL((XEntProbsKernel<false>), dim3(rows), dim3(kProbThreads), 0, s, logits, labels,
+                     row_max, row_sum, probs, row_loss, C, masked, nullptr, nullptr, Bf16Sink{});
+  hipLaunchKernelGGL(XEntFinishKernel, dim3(1), dim3(1024), 0, s, row_loss, labels, loss, N, masked);
+  return hipGetLastError();
+}
+
+bool XEntFusedFits(const float* logits, const float* probs, const float* dlogits, size_t C) {
+  return C > 0 && Vec4Rows(logits, C) && (!probs || Vec4Rows(probs, C)) && Vec4Rows(dlogits, C);
+}
+
+hipError_t LaunchXEntFwdBwd(const float* logits, const int32_t* labels, float* loss, float* probs,
+                            const float* seed, float* dlogits, size_t N, size_t C, int masked,
+                            void* ws, hipStream_t s, const Bf16Sink& sink) {
+  if (N == 0) return hipSuccess;
+  if (!XEntFusedFits(logits, probs, dlogits, C)) return hipErrorInvalidValue;
+  double* row_loss = static_cast<double*>(ws);
+  float* row_max = reinterpret_cast<float*>(row_loss + N);
+  float* row_sum = row_max + N;
+  float* scale = row_sum + N;  // in the scratch's spare tail
+  const unsigned rows = static_cast<unsigned>(N);
+  hipLaunchKernelGGL(XEntScaleKernel, dim3(1), dim3(1024), 0, s, labels, seed, scale, N, masked);
+  hipLaunchKernelGGL(XEntRowMaxKernel, dim3(rows), dim3(kMaxThreads), 0, s, logits, row_max, C);
+  hipLaunchKernelGGL(XEntSerialSumKernel, dim3(static_cast<unsigned>((N + kSumRows - 1) / kSumRows)),
+                     dim3(kSumThreads), 0, s, logits, row_max, row_sum, N, C);
+  hipLaunchKernelGGL((XEntProbsKernel<true>), dim3(rows), dim3(kProbThreads), 0, s, logits, labels,
+                     row_max, row_sum, probs, row_loss, C, masked, scale, dlogits, sink);
   hipLaunchKernelGGL(XEntFinishKernel, dim3(1), dim3(1024), 0, s, row_loss, labels, loss, N, masked);
   return hipGetLastError();
 }

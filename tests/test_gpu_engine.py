@@ -238,6 +238,8 @@ Q8_ADAMW_FUSED = Q8_ADAMW - (Q8_ADAMW + 15) // 16
 # gradient behind RMSNorm's backward; below the first block, the block
 # input's residual gradient behind the other RMSNorm backward.
 Q8_RESIDUAL_ADDS = TINY_Q8["layers"] * 3 + TINY_Q8["layers"] - 1
+# ... and the loss: softmax-xent forward, its seed's fill and backward as one.
+Q8_XENT = 1
 
 
 def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch_cuda):
@@ -264,7 +266,7 @@ def test_q8_decoder_folded_lora_sites_are_bitwise_the_separate_passes(hip, torch
         eng.close()
     # per step and block: 4 LoRA forwards, the dK / dV pair, 2 SwiGLU chains;
     # per step the residual adds and the AdamW runs
-    assert fused[0] == 3 * (TINY_Q8["layers"] * 7 + Q8_RESIDUAL_ADDS + Q8_ADAMW_FUSED)
+    assert fused[0] == 3 * (TINY_Q8["layers"] * 7 + Q8_RESIDUAL_ADDS + Q8_XENT + Q8_ADAMW_FUSED)
     assert fused[1] == 0
     # the base values no later instruction reads (30 here): same bits without them
     assert dropped[0] > 0 and dropped[1] == 0
@@ -306,7 +308,7 @@ def test_q8_decoder_training_matches_the_oracle(hip, orc, torch_cuda, relaxed):
     # runs f32 products here, so its dK / dV pair stays two dispatches.
     per_block = 6 if relaxed else 2
     assert eng.fused_dispatches() == 6 * (TINY_Q8["layers"] * per_block + Q8_RESIDUAL_ADDS +
-                                          Q8_ADAMW_FUSED)
+                                          Q8_XENT + Q8_ADAMW_FUSED)
     eng.close()
 
 

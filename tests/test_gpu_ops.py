@@ -396,6 +396,46 @@ def test_xent(hip, orc, backend, N, C, masked):
         assert e <= TOL, f"{name}: {e:.3g}"
 
 
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("read_later", [False, True])
+def test_xent_forward_fill_backward_fuse_bitwise(hip, orc, backend, masked, read_later):
+    """The train program's loss turn -- softmax-xent forward, the fill of its
+    seed, softmax-xent backward -- runs in a range as the fill and one pass
+    that forms the probabilities and their gradient: bitwise the three run
+    one by one, one fused dispatch; the probabilities stay unstored unless
+    something after the backward reads them."""
+    from tests.plan_ops import ins
+    N, C = 96, 1000
+    r = rng(31 + masked)
+    logits = (r.standard_normal((N, C)) * 3).astype(np.float32)
+    labels = r.integers(0, C, N).astype(np.int32)
+    if masked:
+        labels[::3] = -1
+    ar = Arena()
+    rl, ry = ar.add("logits", logits), ar.add("labels", labels)
+    loss, probs = ar.empty("loss", (1,)), ar.empty("probs", (N, C))
+    seed, dl = ar.empty("seed", (1,)), ar.empty("dl", (N, C))
+    fwd, bwd = (51, 52) if masked else (11, 12)
+    prog = [ins(fwd, [rl, ry, loss, probs], [N, C]), ins(19, [seed, f32_bits(0.5)], [1]),
+            ins(bwd, [probs, ry, seed, dl], [N, C])]
+    if read_later:
+        prog += _readers(ar, ["probs"])
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before = backend.fused_dispatches()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.fused_dispatches() - before == 1
+    dead = [] if read_later else ["probs"]
+    diff = np.flatnonzero(ranged != _restored(apart, ar, dead, arena))
+    assert diff.size == 0, f"{diff.size} bytes differ from byte {diff[:1]}"
+    for name in ["loss", "dl"] + (["probs"] if read_later else []):
+        e = maxrel(ar.get(ranged, name), ar.get(cpu, name))
+        assert e <= TOL, f"{name}: {e:.3g}"
+
+
 # --- optimizer -----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("n", [1, 2048, 100003])
