@@ -160,17 +160,22 @@ uint64_t seeai_graph_launches(const seeai_ctx* ctx);
  * dispatches ran (ExecutorBackend::fused_dispatches, backend.h:165). */
 int seeai_set_fusion(seeai_ctx* ctx, int allow);
 uint64_t seeai_fused_dispatches(const seeai_ctx* ctx);
-/* How many stores fused passes skipped as dead: a LoRA site's base value,
- * or the SwiGLU backward's dh*up product, that the program overwrites before
- * any read or never touches again (metal_backend.mm:1281-1313).
- * SEEAI_KEEP_DEAD_STORES=1 at seeai_create keeps every store. */
+/* How many stores fused passes skipped as dead: a value the program, run
+ * again from its start, overwrites before any read or never touches again
+ * (the rule metal_backend.mm:1281-1313 applies to a LoRA site's base
+ * value): the base value, the SwiGLU backward's dh*up product, a
+ * producer's f32 output whose only reader converts it to bf16, the output
+ * of a producer whose residual add ran inside it, unread probabilities.
+ * Such a slot keeps its old bytes; a caller that downloads intermediates
+ * sets SEEAI_KEEP_DEAD_STORES=1 at seeai_create to keep every store. */
 uint64_t seeai_dropped_stores(const seeai_ctx* ctx);
 /* How many relaxed products' bf16 activation copies their producers wrote
  * as they stored (within a range, with fusion on: the SwiGLU passes, GELU
- * forward / backward and the softmax-xent backward, when the next
- * instruction is a relaxed frozen-weight product on the direct-to-LDS
- * path reading their output; the product then skips its conversion pass,
- * and the producer skips its f32 store where nothing else reads it). */
+ * forward / backward, the softmax-xent backward, LayerNorm / RMSNorm
+ * forward and backward and the residual adds, when the next instruction is
+ * a relaxed frozen-weight product on the direct-to-LDS path reading their
+ * output; the product then skips its conversion pass, and the producer
+ * skips its f32 store where nothing else reads it). */
 uint64_t seeai_fused_conversions(const seeai_ctx* ctx);
 /* Waits for the stream; reports a refusal raised on the device since the
  * last flush (non-finite clip norm: nothing it guarded was written). */
