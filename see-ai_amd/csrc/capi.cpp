@@ -1658,7 +1658,8 @@ int TryFuseNormAdd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
 // The loss at the turn of a train program: softmax-xent forward, the fill of
 // its seed, softmax-xent backward over the same probabilities and labels
 // (plain or masked).  The fill runs first (it touches nothing the forward
-// reads or writes), then one pass forms the probabilities and, from them,
+// reads or writes; a few rows run the whole turn in one workgroup), then
+// one pass forms the probabilities and, from them,
 // the gradient -- the backward's expression on the same f32 values, with
 // its conversion sink -- storing the probabilities only where something
 // after the backward reads them.  One read of the logits and no read of
@@ -1697,13 +1698,13 @@ int TryFuseXEnt(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
   if (!XEntFusedFits(logits, keep, dl, C)) return -1;
   void* ws;
   if (int rc = Scratch(c, XEntFwdScratchBytes(N), &ws)) return rc;
-  if (int rc = ExecuteOne(c, f, P)) return rc;
   Bf16Sink sink;
   GemmArgs ga{};
   const bool sunk = PlanSink(c, idx + 2, idx + 2, dl, N * C, &sink, &ga);
   SEEAI_TRY(c,
-            LaunchXEntFwdBwd(logits, labels, loss, keep, seed, dl, N, C, ins.opcode == 51, ws,
-                             c->stream, sink),
+            LaunchXEntFwdBwd(logits, labels, loss, keep, R.f(f.in[0]), f.out[0],
+                             BitsToF32(f.in[1]), seed, dl, N, C, ins.opcode == 51, ws, c->stream,
+                             sink),
             "softmax_xent.fwd+bwd");
   if (sunk) SinkDone(c, idx + 2, ga);
   c->done[0] = at + 64;

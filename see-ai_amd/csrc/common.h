@@ -229,13 +229,15 @@ hipError_t LaunchXEntFwd(const float* logits, const int32_t* labels, float* loss
 hipError_t LaunchXEntBwd(const float* probs, const int32_t* labels, const float* seed,
                          float* dlogits, size_t N, size_t C, int masked, void* ws,
                          hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
-// The forward and the backward as one: probabilities (stored where probs is
+// The forward, the fill of the backward's seed (fill_n floats of fill_v at
+// fill_dst) and the backward as one: probabilities (stored where probs is
 // given) and their gradients in one pass (scale from seed as the backward
-// forms it); rows 16-byte aligned.
+// forms it); rows 16-byte aligned.  A few rows run in one workgroup.
 bool XEntFusedFits(const float* logits, const float* probs, const float* dlogits, size_t C);
 hipError_t LaunchXEntFwdBwd(const float* logits, const int32_t* labels, float* loss, float* probs,
-                            const float* seed, float* dlogits, size_t N, size_t C, int masked,
-                            void* ws, hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
+                            float* fill_dst, uint64_t fill_n, float fill_v, const float* seed,
+                            float* dlogits, size_t N, size_t C, int masked, void* ws,
+                            hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
 // Whether the backward's row kernel can feed a sink (float4 rows).
 bool XEntBwdSinkFits(const float* probs, const float* dlogits, size_t C);
 

@@ -283,6 +283,118 @@ XEntBwdKernel(const float* __restrict__ probs, const int32_t* __restrict__ label
   }
 }
 
+// The whole loss turn for a few rows (N <= 1024, N x C <= kSmallFloats, rows
+// 16-byte aligned) in one workgroup: the seed's fill, the row max, the
+// exps into LDS, the exp-sum chain of each row in column order, the
+// probabilities and their gradient, the loss -- every value the
+// multi-kernel path's expression in its association (the chain's
+// sum += e, the probability e * (1 / sum), XEntFinishKernel's tree over the
+// row terms), so the bits are the same.  Small plans run the turn in one
+// dispatch instead of six.
+constexpr int kSmallThreads = 1024;
+constexpr size_t kSmallFloats = 16384;
+__global__ void __launch_bounds__(kSmallThreads)
+XEntSmallKernel(const float* __restrict__ logits, const int32_t* __restrict__ labels,
+                float* __restrict__ loss, float* __restrict__ probs, float* fill_dst,
+                uint64_t fill_n, float fill_v, const float* seed, float* __restrict__ dl,
+                size_t N, size_t C, int masked, Bf16Sink sink) {
+  __shared__ __attribute__((aligned(16))) float e[kSmallFloats];
+  __shared__ float smax[kSmallThreads], sinv[kSmallThreads];
+  __shared__ double rloss[kSmallThreads];
+  __shared__ double red[kSmallThreads / kWave];
+  __shared__ float sscale;
+  constexpr int kWaves = kSmallThreads / kWave;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  for (uint64_t i = tid; i < fill_n; i += kSmallThreads) fill_dst[i] = fill_v;
+  for (size_t r = wave; r < N; r += kWaves) {  // row max, a wave per row
+    const float4* x4 = reinterpret_cast<const float4*>(logits + r * C);
+    float mx = NAN, mx2 = NAN;
+    for (size_t c = lane; c < C / 4; c += kWave) {
+      const float4 v = x4[c];
+      mx = fmaxf(mx, fmaxf(v.x, v.y));
+      mx2 = fmaxf(mx2, fmaxf(v.z, v.w));
+    }
+    mx = WaveMaxF(fmaxf(mx, mx2));
+    if (lane == 0) smax[r] = mx;
+  }
+  __syncthreads();
+  for (size_t i = tid; i < N * C / 4; i += kSmallThreads) {  // the exps
+    const float4 v = reinterpret_cast<const float4*>(logits)[i];
+    const float mx = smax[4 * i / C];
+    reinterpret_cast<float4*>(e)[i] =
+        make_float4(expf(v.x - mx), expf(v.y - mx), expf(v.z - mx), expf(v.w - mx));
+  }
+  __syncthreads();
+  if (static_cast<size_t>(tid) < N) {  // each row's chain in column order
+    const float* er = e + static_cast<size_t>(tid) * C;
+    float sum = 0.0f;
+    for (size_t c = 0; c < C; ++c) sum += er[c];
+    sinv[tid] = 1.0f / sum;  // loss.cc:30
+  }
+  double t = 0.0;
+  if (masked)
+    for (size_t r = tid; r < N; r += kSmallThreads) t += labels[r] >= 0 ? 1.0 : 0.0;
+  t = BlockSumD<kSmallThreads>(t, red);  // also orders the fill and the chains before what follows
+  if (tid == 0) {
+    if (masked) {
+      const uint64_t T = static_cast<uint64_t>(t);
+      sscale = T ? *seed / static_cast<float>(T) : 0.0f;
+    } else {
+      sscale = *seed / static_cast<float>(N);
+    }
+  }
+  __syncthreads();
+  const float scale = sscale;
+  for (size_t r = wave; r < N; r += kWaves) {  // probabilities, gradient, the row's term
+    const float inv_sum = sinv[r];
+    const int32_t lab = labels[r];
+    const bool zero = masked && lab < 0;
+    const size_t lc = static_cast<size_t>(lab);
+    const float4* e4 = reinterpret_cast<const float4*>(e + r * C);
+    for (size_t c = lane; c < C / 4; c += kWave) {
+      const float4 v = e4[c];
+      const float4 q = make_float4(v.x * inv_sum, v.y * inv_sum, v.z * inv_sum, v.w * inv_sum);
+      if (probs) reinterpret_cast<float4*>(probs + r * C)[c] = q;
+      float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (!zero) {
+        g = make_float4(scale * q.x, scale * q.y, scale * q.z, scale * q.w);
+        if (lc / 4 == c) {
+          const size_t l = lc % 4;
+          if (l == 0) g.x -= scale;
+          else if (l == 1) g.y -= scale;
+          else if (l == 2) g.z -= scale;
+          else g.w -= scale;
+        }
+      }
+      if (sink.store_f32) reinterpret_cast<float4*>(dl + r * C)[c] = g;
+      if (sink.out) SinkStore4(sink, r * C + 4 * c, g);
+    }
+    if (lane == 0) {
+      double term = 0.0;
+      if (!zero) {
+        const float pl = e[r * C + lc] * inv_sum;
+        const double safe = pl != pl ? static_cast<double>(pl) : static_cast<double>(fmaxf(pl, 1e-12f));
+        term = -log(safe);
+      }
+      rloss[r] = term;
+    }
+  }
+  __syncthreads();
+  double total = 0.0, targets = 0.0;
+  for (size_t r = tid; r < N; r += kSmallThreads) {
+    total += rloss[r];
+    if (!masked || labels[r] >= 0) targets += 1.0;
+  }
+  total = BlockSumD<kSmallThreads>(total, red);
+  targets = BlockSumD<kSmallThreads>(targets, red);
+  if (tid == 0) {
+    if (masked)
+      *loss = targets > 0.0 ? static_cast<float>(total / targets) : 0.0f;
+    else
+      *loss = static_cast<float>(total / static_cast<double>(N));
+  }
+}
+
 }  // namespace
 
 size_t XEntFwdScratchBytes(size_t N) { return N * (8 + 4 + 4) + 256; }
@@ -308,10 +420,17 @@ bool XEntFusedFits(const float* logits, const float* probs, const float* dlogits
 }
 
 hipError_t LaunchXEntFwdBwd(const float* logits, const int32_t* labels, float* loss, float* probs,
-                            const float* seed, float* dlogits, size_t N, size_t C, int masked,
-                            void* ws, hipStream_t s, const Bf16Sink& sink) {
+                            float* fill_dst, uint64_t fill_n, float fill_v, const float* seed,
+                            float* dlogits, size_t N, size_t C, int masked, void* ws,
+                            hipStream_t s, const Bf16Sink& sink) {
   if (N == 0) return hipSuccess;
   if (!XEntFusedFits(logits, probs, dlogits, C)) return hipErrorInvalidValue;
+  if (N <= static_cast<size_t>(kSmallThreads) && N * C <= kSmallFloats) {
+    hipLaunchKernelGGL(XEntSmallKernel, dim3(1), dim3(kSmallThreads), 0, s, logits, labels, loss,
+                       probs, fill_dst, fill_n, fill_v, seed, dlogits, N, C, masked, sink);
+    return hipGetLastError();
+  }
+  if (hipError_t e = LaunchFill(fill_dst, fill_v, fill_n, s); e != hipSuccess) return e;
   double* row_loss = static_cast<double*>(ws);
   float* row_max = reinterpret_cast<float*>(row_loss + N);
   float* row_sum = row_max + N;

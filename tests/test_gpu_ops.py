@@ -398,14 +398,15 @@ def test_xent(hip, orc, backend, N, C, masked):
 
 @pytest.mark.parametrize("masked", [False, True])
 @pytest.mark.parametrize("read_later", [False, True])
-def test_xent_forward_fill_backward_fuse_bitwise(hip, orc, backend, masked, read_later):
+@pytest.mark.parametrize("N,C", [(96, 1000), (32, 256), (1024, 16), (5, 3276)])
+def test_xent_forward_fill_backward_fuse_bitwise(hip, orc, backend, masked, read_later, N, C):
     """The train program's loss turn -- softmax-xent forward, the fill of its
     seed, softmax-xent backward -- runs in a range as the fill and one pass
-    that forms the probabilities and their gradient: bitwise the three run
-    one by one, one fused dispatch; the probabilities stay unstored unless
-    something after the backward reads them."""
+    that forms the probabilities and their gradient (a few rows: the whole
+    turn in one workgroup): bitwise the three run one by one, one fused
+    dispatch; the probabilities stay unstored unless something after the
+    backward reads them."""
     from tests.plan_ops import ins
-    N, C = 96, 1000
     r = rng(31 + masked)
     logits = (r.standard_normal((N, C)) * 3).astype(np.float32)
     labels = r.integers(0, C, N).astype(np.int32)
