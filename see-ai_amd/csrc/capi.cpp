@@ -1557,13 +1557,16 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
   return -1;
 }
 
-// The residual add behind a product: a GEMM with no addend, accumulate,
-// bias or activation whose C the next instruction, kAddEW, adds to another
-// operand X (either side; IEEE addition commutes) runs with X as its addend
-// and the add's output as C -- the epilogue's X + dot is the add's X + C,
-// the same rounding -- when C is read by nothing after the add (the
+// The add behind a product: a GEMM with no addend, accumulate, bias or
+// activation whose C the next instruction, kAddEW, adds to another operand
+// X (either side; IEEE addition commutes) runs with X as its addend and the
+// add's output as C -- the epilogue's X + dot is the add's X + C, the same
+// rounding; and a GEMM with no bias, accumulate or activation (an addend
+// allowed) whose C the next instruction, kAddBias, offsets by a bias row
+// runs with that bias -- the epilogue adds it after the addend, as the
+// instruction would.  Either when C is read by nothing after the add (the
 // dead-store rule) and the add's output misses everything the product
-// reads (it may be X itself).  One pass instead of two over M x N floats.
+// reads (it may be X, or C, itself).  One pass instead of two over M x N.
 int TryFuseAddend(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   if (!c->allow_fusion || !c->prog || at < c->prog || at >= c->prog + c->prog_count * 64 ||
       (at - c->prog) % 64 != 0)
@@ -1572,11 +1575,34 @@ int TryFuseAddend(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   if (idx + 1 >= c->range_end) return -1;
   Instruction nx;
   std::memcpy(&nx, c->prog + (idx + 1) * 64, sizeof nx);
-  if (nx.opcode != 5) return -1;
+  if (nx.opcode != 5 && nx.opcode != 6) return -1;
   GemmArgs a{};
   const char* what = DecodeGemm(c, ins, &a);
-  if (!what || a.addend || a.accumulate || a.bias || a.act || a.M * a.N != nx.out[0]) return -1;
+  if (!what || a.accumulate || a.bias || a.act) return -1;
   const Ptrs R{c};
+  if (nx.opcode == 6) {  // kAddBias [x, b, out], [rows, cols]
+    float* out = R.f(nx.in[2]);
+    const float* bias = R.f(nx.in[1]);
+    if (R.f(nx.in[0]) != a.C || nx.out[0] != a.M || nx.out[1] != a.N) return -1;
+    const Extent e_out{reinterpret_cast<const uint8_t*>(out), a.M * a.N * 4};
+    const Extent e_b{reinterpret_cast<const uint8_t*>(bias), a.N * 4};
+    const Extent e_c = GemmWrites(a);
+    Extent reads[8];
+    const int nr = GemmReads(a, reads);
+    if (Hits(e_out, reads, nr) || Hits(e_out, &e_b, 1) || Hits(e_c, &e_b, 1) ||
+        (out != a.C && Hits(e_out, &e_c, 1)))
+      return -1;
+    if (!DeadStore(c, idx, idx + 2, e_c, 2)) return -1;
+    a.relaxed = Relaxed(c, ins);
+    a.bias = bias;
+    a.C = out;
+    if (int rc = Gemm(c, a, what)) return rc;
+    c->done[0] = at + 64;
+    c->ndone = 1;
+    ++c->fused;
+    return SEEAI_OK;
+  }
+  if (a.addend || a.M * a.N != nx.out[0]) return -1;
   const float *x0 = R.f(nx.in[0]), *x1 = R.f(nx.in[1]);
   float* out = R.f(nx.in[2]);
   if ((x0 == a.C) == (x1 == a.C)) return -1;  // C on exactly one side

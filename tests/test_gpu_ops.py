@@ -1113,6 +1113,48 @@ def test_swiglu_chain_refuses_to_fuse_over_an_input(hip, orc, backend):
     assert ranged.tobytes() == apart.tobytes()
 
 
+@pytest.mark.parametrize("relaxed", [False, True])
+@pytest.mark.parametrize("form", ["addend", "plain", "in_place", "read_later"])
+def test_bias_add_runs_in_the_product_epilogue(hip, orc, backend, relaxed, form):
+    """kAddBias of a product's C (C read by nothing after it) runs as the
+    product's epilogue bias, after its addend as the instruction would add
+    it: bitwise the two run one by one, one fused dispatch; written over C
+    itself too; with C read again, apart."""
+    from tests.plan_ops import ins
+    M, N, K = 64, 256, 96
+    r = rng(len(form) * 7 + relaxed)
+    ar = Arena()
+    x = ar.add("x", r.standard_normal((M, K)).astype(np.float32))
+    w = ar.add("W", (r.standard_normal((K, N)) * 0.1).astype(np.float32))
+    d = ar.add("D", r.standard_normal((M, N)).astype(np.float32))
+    b = ar.add("b", r.standard_normal(N).astype(np.float32))
+    c = ar.empty("C", (M, N))
+    out = c if form == "in_place" else ar.empty("out", (M, N))
+    flags = (1 << 5) if relaxed else 0
+    if form == "addend":
+        prog = [ins(1, [x, w, c, d], [M, N, K], flags=flags | (1 << 3), imm=f32_bits(2.0))]
+    else:
+        prog = [ins(1, [x, w, c], [M, N, K], flags=flags)]
+    prog.append(ins(6, [c, b, out], [M, N]))
+    if form == "read_later":
+        prog += _readers(ar, ["C"])
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before = backend.fused_dispatches()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    fused = form != "read_later"
+    assert backend.fused_dispatches() - before == int(fused)
+    dead = ["C"] if fused and form != "in_place" else []
+    diff = np.flatnonzero(ranged != _restored(apart, ar, dead, arena))
+    assert diff.size == 0, f"{diff.size} bytes differ from byte {diff[:1]}"
+    name = "C" if form == "in_place" else "out"
+    e = maxrel(ar.get(ranged, name), ar.get(cpu, name))
+    assert e <= (TOL_BF16 if relaxed else TOL), f"{name}: {e:.3g}"
+
+
 @pytest.mark.parametrize("producer", ["gemm", "gemm_relaxed", "lora_site", "rmsnorm_bwd",
                                       "layernorm_bwd"])
 @pytest.mark.parametrize("form", ["res_first", "res_second", "in_place", "read_later"])
