@@ -45,7 +45,9 @@ GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 
                # TN with the folder wave apart: 4 x 8 blocks over two chunks, 8 x 16
                # blocks (two chains per folder lane) over a K % 4 tail and a ring
                # that runs its steady state before the last intervals
-               (32, 64, 1024), (128, 256, 1030), (136, 256, 2051), (256, 128, 3000)]
+               (32, 64, 1024), (128, 256, 1030), (136, 256, 2051), (256, 128, 3000),
+               # NN chains two to a lane (rows mi and mi + 16), ragged M, N and K
+               (8200, 12, 1030)]
 
 
 @pytest.fixture(scope="module")
