@@ -150,6 +150,17 @@ struct seeai_ctx {
   // same way reuses it when every instruction between wrote elsewhere.
   void* cvt = nullptr;
   size_t cvt_bytes = 0;
+  // bf16 copies of relaxed attention's operands (q, k, v, dO: four slots of
+  // B·S·H·64) for the bf16-operand kernels, and what they hold: the sources
+  // and the instruction that converted them.
+  void* a16 = nullptr;
+  size_t a16_bytes = 0;
+  struct A16Key {
+    const float* src[4];
+    uint64_t n;
+    const uint8_t* at;
+  } a16_key{};
+  int attn16_plans = 1;  // SEEAI_ATTN16_PLANS=0: the f32-operand kernels
   struct {
     const float* A = nullptr;
     uint64_t M = 0, K = 0;
@@ -398,6 +409,74 @@ bool Overlap(const uint8_t* a, uint64_t na, const uint8_t* b, uint64_t nb) {
   return a < b + nb && b < a + na;
 }
 
+// One operand's byte extent and whether the instruction writes it (a
+// read-modify-write operand is one write extent, as the reference's
+// validator describes it, plan_validator.cc:365-745): what the dead-store
+// scan and the attention copies below ask of an instruction.
+struct Touch {
+  const uint8_t* p;
+  uint64_t n;
+  bool write;
+};
+bool TouchExtents(seeai_ctx* c, const Instruction& ins, Touch* out, int* n);
+
+// Relaxed bf16 attention with head width 64 runs the bf16-operand kernels
+// (k_attn16.hip) on bf16 copies of its f32 operands: rounding them once per
+// instruction (or once for a dQ and the dK / dV right after it) costs less
+// than the f32-operand kernels' rounding as they stage.  The kernels round
+// the same values to bf16 (RNE), so the relaxed grant is unchanged.
+bool Attn16Plan(const seeai_ctx* c, uint64_t B, uint64_t S, uint64_t H, uint64_t d) {
+  return c->attn16_plans && c->attn_bf16 && c->allow_relaxed && Attn16Fits(B, S, H, d) &&
+         (H * d) % 32 == 0;
+}
+
+// The bf16 copies of the operands `need` marks (bit i: slot i = q, k, v,
+// dO), each [B·S, H·64]: converted here, or kept from the instruction just
+// before when it converted the same sources and wrote none of them.
+int Attn16Operands(seeai_ctx* c, const float* const src[4], unsigned need, uint64_t rows,
+                   uint64_t cols, uint16_t* out[4]) {
+  const uint64_t n = rows * cols;
+  const size_t bytes = 4 * n * 2;
+  if (bytes > c->a16_bytes) {
+    c->a16_key.at = nullptr;
+    DropGraphs(c);
+    SEEAI_TRY(c, hipStreamSynchronize(c->stream), "attention copies drain");
+    if (c->a16) SEEAI_TRY(c, hipFree(c->a16), "attention copies free");
+    c->a16 = nullptr;
+    c->a16_bytes = 0;
+    SEEAI_TRY(c, hipMalloc(&c->a16, bytes), "attention copies alloc");
+    c->a16_bytes = bytes;
+  }
+  bool keep = c->cur_at && c->a16_key.at && c->a16_key.at + 64 == c->cur_at && c->a16_key.n == n;
+  if (keep) {  // the previous instruction must not have written a kept source
+    Instruction prev;
+    std::memcpy(&prev, c->a16_key.at, sizeof prev);
+    Touch t[16];
+    int nt = 0;
+    keep = TouchExtents(c, prev, t, &nt);
+    for (int i = 0; keep && i < nt; ++i)
+      for (int j = 0; j < 4; ++j)
+        if (t[i].write && src[j] &&
+            Overlap(t[i].p, t[i].n, reinterpret_cast<const uint8_t*>(src[j]), n * 4))
+          keep = false;
+  }
+  for (int i = 0; i < 4; ++i) {
+    out[i] = static_cast<uint16_t*>(c->a16) + static_cast<size_t>(i) * n;
+    if (!(need & (1u << i))) continue;
+    if (keep && c->a16_key.src[i] == src[i]) continue;
+    SEEAI_TRY(c,
+              LaunchConvertRowsBf16(src[i], rows, cols, 1.0f, nullptr, out[i],
+                                    c->policy.convert_wgs_per_cu, c->stream),
+              "attention operand to bf16");
+  }
+  for (int i = 0; i < 4; ++i)
+    if (need & (1u << i)) c->a16_key.src[i] = src[i];
+    else if (!keep) c->a16_key.src[i] = nullptr;
+  c->a16_key.n = n;
+  c->a16_key.at = c->cur_at;
+  return SEEAI_OK;
+}
+
 // Range-level fusion of the attention backward (the seam's whole-program
 // visibility, backend.h:139-142; the reference's Metal backend fuses the
 // low-rank pair the same way, metal_backend.mm:1155-1340).  kAttnDKTiled and
@@ -442,8 +521,17 @@ int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
     if (Overlap(o, act, reinterpret_cast<const uint8_t*>(stats), st)) return -1;
   RelaxedAttention(c, ins);
   RelaxedAttention(c, nx);
-  SEEAI_TRY(c, LaunchAttnDKDVFused(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
-            "attn.dkdv_fused");
+  if (Attn16Plan(c, B, S, H, d)) {
+    const float* src[4] = {q, k, v, dout};
+    uint16_t* b16[4];
+    if (int rc = Attn16Operands(c, src, 15u, B * S, H * d, b16)) return rc;
+    SEEAI_TRY(c,
+              LaunchAttn16DKDV(b16[0], b16[1], b16[2], b16[3], stats, dk, dv, B, S, H, c->stream),
+              "attn.dkdv_bf16");
+  } else {
+    SEEAI_TRY(c, LaunchAttnDKDVFused(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
+              "attn.dkdv_fused");
+  }
   c->done[0] = at + 64;
   c->ndone = 1;
   ++c->fused;
@@ -836,6 +924,16 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
         starts = R.i32(ins.out[2]);
       }
       const int dt = RelaxedAttention(c, ins);
+      if (dt == 1 && Attn16Plan(c, B, S, H, d)) {
+        const float* src[4] = {R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), nullptr};
+        uint16_t* b16[4];
+        if (int rc = Attn16Operands(c, src, 7u, B * S, H * d, b16)) return rc;
+        SEEAI_TRY(c,
+                  LaunchAttn16Fwd(b16[0], b16[1], b16[2], R.f(ins.in[3]), R.f(ins.out[0]), B, S,
+                                  H, starts, s),
+                  "attn.fwd_bf16");
+        return SEEAI_OK;
+      }
       SEEAI_TRY(c,
                 LaunchAttnFwdTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]),
                                    R.f(ins.in[3]), R.f(ins.out[0]), B, S, H, d, starts, s),
@@ -848,6 +946,23 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       const uint64_t g = ins.out[2];
       const uint64_t B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
       const int dt = RelaxedAttention(c, ins);
+      // The bf16-operand kernels read v for dV too (it forms dP): a dV
+      // instruction without a v operand keeps the f32-operand kernel.
+      if (dt == 1 && Attn16Plan(c, B, S, H, d) && (ins.opcode != 50 || ins.in[2] != kNullRef)) {
+        const float* src[4] = {R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3])};
+        uint16_t* b16[4];
+        if (int rc = Attn16Operands(c, src, 15u, B * S, H * d, b16)) return rc;
+        hipError_t e;
+        if (ins.opcode == 48)
+          e = LaunchAttn16DQ(b16[0], b16[1], b16[2], b16[3], R.f(ins.out[0]), R.f(ins.out[1]), B,
+                             S, H, s);
+        else
+          e = LaunchAttn16DKDV(b16[0], b16[1], b16[2], b16[3], R.f(ins.out[0]),
+                               ins.opcode == 49 ? R.f(ins.out[1]) : nullptr,
+                               ins.opcode == 50 ? R.f(ins.out[1]) : nullptr, B, S, H, s);
+        SEEAI_TRY(c, e, "attn.bwd_bf16");
+        return SEEAI_OK;
+      }
       hipError_t e;
       if (ins.opcode == 48)
         e = LaunchAttnDQTiled(dt, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3]),
@@ -897,6 +1012,9 @@ int seeai_create(int device, seeai_ctx** out) {
   // SEEAI_ATTENTION_BF16=1: relaxed attention on bf16 operands from the
   // start (seeai_set_attention_bf16 for a caller that sets it itself).
   if (const char* e = std::getenv("SEEAI_ATTENTION_BF16"); e && e[0] == '1') c->attn_bf16 = 1;
+  // SEEAI_ATTN16_PLANS=0: relaxed bf16 attention on the f32-operand kernels
+  // (the same-session control of the bf16 copies).
+  if (const char* e = std::getenv("SEEAI_ATTN16_PLANS"); e && e[0] == '0') c->attn16_plans = 0;
   int rc = Hip(c, hipSetDevice(device), "set device");
   if (rc == SEEAI_OK) rc = Hip(c, NoAllocScratchInit(device), "no-allocation workspace address");
   if (rc == SEEAI_OK) rc = Hip(c, hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "stream");
@@ -929,6 +1047,7 @@ void seeai_destroy(seeai_ctx* c) {
   if (c->source) (void)hipFree(c->source);
   if (c->scratch) (void)hipFree(c->scratch);
   if (c->cvt) (void)hipFree(c->cvt);
+  if (c->a16) (void)hipFree(c->a16);
   DropShadows(c);
   if (c->small) (void)hipFree(c->small);
   if (c->host_flag) (void)hipHostFree(c->host_flag);
@@ -1191,16 +1310,8 @@ bool Hits(const Extent& x, const Extent* set, int n) {
   return false;
 }
 
-// --- Dead-store scan ----------------------------------------------------------
-// One operand's byte extent and whether the instruction writes it (a
-// read-modify-write operand is one write extent, as the reference's
-// validator describes it, plan_validator.cc:365-745).
-struct Touch {
-  const uint8_t* p;
-  uint64_t n;
-  bool write;
-};
 
+// --- Dead-store scan ----------------------------------------------------------
 // Every operand extent of an instruction (the validator's roles and sizes,
 // plan_validator.cc:368-745, as operands.h states them), resolved to device
 // addresses.  False for opcodes not modelled there.
