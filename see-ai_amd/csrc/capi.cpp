@@ -161,6 +161,18 @@ struct seeai_ctx {
     const uint8_t* at;
   } a16_key{};
   int attn16_plans = 1;  // SEEAI_ATTN16_PLANS=0: the f32-operand kernels
+  // The forward's bf16 copies of q, k, v, one buffer per source triple, kept
+  // for the backward of the same range run: `idx` is the converting
+  // instruction, `epoch` the range run it belongs to, `clean_to` how far the
+  // scan for writes into the sources has reached.
+  struct A16Saved {
+    const float* src[3];
+    uint64_t n;
+    uint64_t idx, clean_to, epoch;
+    void* buf;
+  };
+  std::vector<A16Saved> a16_saved;
+  uint64_t a16_epoch = 1;
   struct {
     const float* A = nullptr;
     uint64_t M = 0, K = 0;
@@ -231,6 +243,21 @@ int Hip(seeai_ctx* c, hipError_t e, const char* what) {
 
 // Destroys the captured range graphs (after the stream drains: one may be
 // running) and advances the generation every capture is checked against.
+// The arena may have changed outside the program (or the program itself):
+// no bf16 copy made earlier may be taken for current.
+void ForgetCopies(seeai_ctx* c) {
+  c->cvt_key.at = nullptr;
+  c->a16_key.at = nullptr;
+  ++c->a16_epoch;
+}
+
+// The forward's saved attention copies (they name the binding's pointers).
+void DropSavedCopies(seeai_ctx* c) {
+  for (auto& sv : c->a16_saved)
+    if (sv.buf) (void)hipFree(sv.buf);
+  c->a16_saved.clear();
+}
+
 void DropGraphs(seeai_ctx* c) {
   ++c->graph_gen;
   if (c->graphs.empty()) return;
@@ -488,6 +515,65 @@ int Attn16Operands(seeai_ctx* c, const float* const src[4], unsigned need, uint6
 // (the two run apart) when either output overlaps the other or anything the
 // pass reads: the separate order may legally reuse a buffer the first
 // instruction alone still reads.  Returns -1 when the pair does not fuse.
+// The saved forward copies of (q, k, v) over n floats each, or null.
+seeai_ctx::A16Saved* SavedCopies(seeai_ctx* c, const float* q, const float* k, const float* v,
+                                 uint64_t n) {
+  for (auto& sv : c->a16_saved)
+    if (sv.src[0] == q && sv.src[1] == k && sv.src[2] == v && sv.n == n) return &sv;
+  return nullptr;
+}
+
+// A buffer for the forward's copies of (q, k, v) (made ahead of a range by
+// PresizeWorkspaces, so none is allocated inside one).
+int MakeSavedCopies(seeai_ctx* c, const float* q, const float* k, const float* v, uint64_t n) {
+  if (SavedCopies(c, q, k, v, n)) return SEEAI_OK;
+  void* buf = nullptr;
+  SEEAI_TRY(c, hipMalloc(&buf, 3 * n * 2), "attention forward copies alloc");
+  c->a16_saved.push_back({{q, k, v}, n, 0, 0, 0, buf});
+  return SEEAI_OK;
+}
+
+// Whether the saved copies still match their sources at the current
+// instruction: made in this range run, and no instruction since has written
+// into a source (each instruction between scanned once).
+bool SavedCurrent(seeai_ctx* c, seeai_ctx::A16Saved* sv) {
+  if (!sv || sv->epoch != c->a16_epoch || !c->cur_at || !c->prog) return false;
+  const uint64_t cur = static_cast<uint64_t>(c->cur_at - c->prog) / 64;
+  if (cur <= sv->idx) return false;
+  for (uint64_t i = std::max(sv->clean_to, sv->idx + 1); i < cur; ++i) {
+    Instruction ins;
+    std::memcpy(&ins, c->prog + i * 64, sizeof ins);
+    Touch t[16];
+    int nt = 0;
+    bool ok = TouchExtents(c, ins, t, &nt);
+    for (int j = 0; ok && j < nt; ++j)
+      for (int s = 0; s < 3; ++s)
+        if (t[j].write &&
+            Overlap(t[j].p, t[j].n, reinterpret_cast<const uint8_t*>(sv->src[s]), sv->n * 4))
+          ok = false;
+    if (!ok) {
+      sv->epoch = 0;
+      return false;
+    }
+    sv->clean_to = i + 1;
+  }
+  return true;
+}
+
+// The operands of a backward instruction: q, k, v from the forward's saved
+// copies where they are current, else converted with dO.
+int Attn16BwdOperands(seeai_ctx* c, const float* const src[4], uint64_t rows, uint64_t cols,
+                      uint16_t* out[4]) {
+  seeai_ctx::A16Saved* sv = SavedCopies(c, src[0], src[1], src[2], rows * cols);
+  if (SavedCurrent(c, sv)) {
+    if (int rc = Attn16Operands(c, src, 8u, rows, cols, out)) return rc;
+    for (int i = 0; i < 3; ++i)
+      out[i] = static_cast<uint16_t*>(sv->buf) + static_cast<size_t>(i) * rows * cols;
+    return SEEAI_OK;
+  }
+  return Attn16Operands(c, src, 15u, rows, cols, out);
+}
+
 int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   if (!c->allow_fusion || !c->allow_relaxed || !c->attn_bf16 || !c->prog || at < c->prog ||
       at >= c->prog + c->prog_count * 64 || (at - c->prog) % 64 != 0)
@@ -524,7 +610,7 @@ int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   if (Attn16Plan(c, B, S, H, d)) {
     const float* src[4] = {q, k, v, dout};
     uint16_t* b16[4];
-    if (int rc = Attn16Operands(c, src, 15u, B * S, H * d, b16)) return rc;
+    if (int rc = Attn16BwdOperands(c, src, B * S, H * d, b16)) return rc;
     SEEAI_TRY(c,
               LaunchAttn16DKDV(b16[0], b16[1], b16[2], b16[3], stats, dk, dv, B, S, H, c->stream),
               "attn.dkdv_bf16");
@@ -927,7 +1013,22 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       if (dt == 1 && Attn16Plan(c, B, S, H, d)) {
         const float* src[4] = {R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), nullptr};
         uint16_t* b16[4];
-        if (int rc = Attn16Operands(c, src, 7u, B * S, H * d, b16)) return rc;
+        const uint64_t n = B * S * H * d;
+        seeai_ctx::A16Saved* sv = c->cur_at ? SavedCopies(c, src[0], src[1], src[2], n) : nullptr;
+        if (sv) {  // into the copies the backward of this range run may take
+          for (int i = 0; i < 3; ++i) {
+            b16[i] = static_cast<uint16_t*>(sv->buf) + static_cast<size_t>(i) * n;
+            SEEAI_TRY(c,
+                      LaunchConvertRowsBf16(src[i], B * S, H * d, 1.0f, nullptr, b16[i],
+                                            c->policy.convert_wgs_per_cu, s),
+                      "attention operand to bf16");
+          }
+          sv->idx = static_cast<uint64_t>(c->cur_at - c->prog) / 64;
+          sv->clean_to = sv->idx + 1;
+          sv->epoch = c->a16_epoch;
+        } else if (int rc = Attn16Operands(c, src, 7u, B * S, H * d, b16)) {
+          return rc;
+        }
         SEEAI_TRY(c,
                   LaunchAttn16Fwd(b16[0], b16[1], b16[2], R.f(ins.in[3]), R.f(ins.out[0]), B, S,
                                   H, starts, s),
@@ -951,7 +1052,7 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       if (dt == 1 && Attn16Plan(c, B, S, H, d) && (ins.opcode != 50 || ins.in[2] != kNullRef)) {
         const float* src[4] = {R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]), R.f(ins.in[3])};
         uint16_t* b16[4];
-        if (int rc = Attn16Operands(c, src, 15u, B * S, H * d, b16)) return rc;
+        if (int rc = Attn16BwdOperands(c, src, B * S, H * d, b16)) return rc;
         hipError_t e;
         if (ins.opcode == 48)
           e = LaunchAttn16DQ(b16[0], b16[1], b16[2], b16[3], R.f(ins.out[0]), R.f(ins.out[1]), B,
@@ -1048,6 +1149,7 @@ void seeai_destroy(seeai_ctx* c) {
   if (c->scratch) (void)hipFree(c->scratch);
   if (c->cvt) (void)hipFree(c->cvt);
   if (c->a16) (void)hipFree(c->a16);
+  DropSavedCopies(c);
   DropShadows(c);
   if (c->small) (void)hipFree(c->small);
   if (c->host_flag) (void)hipHostFree(c->host_flag);
@@ -1083,7 +1185,7 @@ int seeai_set_attention_bf16(seeai_ctx* c, int on) {
 int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t rodata_bytes) {
   if (!c) return SEEAI_INVALID;
   DropGraphs(c);
-  c->cvt_key.at = nullptr;
+  ForgetCopies(c);
   c->dead_prog = nullptr;  // dead-store decisions name the old binding's pointers
   const uint64_t bytes = (arena_bytes + kArenaAlignment - 1) / kArenaAlignment * kArenaAlignment;
   uint8_t* arena = nullptr;
@@ -1102,6 +1204,7 @@ int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t 
     return Hip(c, e, "bind");
   }
   DropShadows(c);  // made from the old rodata
+  DropSavedCopies(c);  // of the old arena's activations
   if (c->arena) (void)hipFree(c->arena);
   if (c->rodata) (void)hipFree(c->rodata);
   c->arena = arena;
@@ -1114,7 +1217,7 @@ int seeai_bind(seeai_ctx* c, uint64_t arena_bytes, const void* rodata, uint64_t 
 int seeai_bind_source(seeai_ctx* c, const void* data, uint64_t bytes) {
   if (!c) return SEEAI_INVALID;
   DropGraphs(c);
-  c->cvt_key.at = nullptr;
+  ForgetCopies(c);
   c->dead_prog = nullptr;
   SEEAI_TRY(c, hipStreamSynchronize(c->stream), "bind_source drain");
   DropShadows(c);  // some may be of the old source image
@@ -1131,7 +1234,7 @@ int seeai_bind_source(seeai_ctx* c, const void* data, uint64_t bytes) {
 int seeai_upload(seeai_ctx* c, uint64_t off, const void* src, uint64_t bytes) {
   if (!c || !c->arena || off + bytes > c->arena_bytes) return Fail(c, SEEAI_INVALID, "upload: extent outside the arena");
   if (!bytes) return SEEAI_OK;
-  c->cvt_key.at = nullptr;  // the arena changed outside the program
+  ForgetCopies(c);  // the arena changed outside the program
   SEEAI_TRY(c, hipMemcpyAsync(c->arena + off, src, bytes, hipMemcpyHostToDevice, c->stream), "upload");
   // The source buffer is the caller's pageable memory: complete the copy
   // before returning so the caller may reuse it at once.
@@ -1270,7 +1373,7 @@ int seeai_feeder_next(seeai_feeder* f, uint64_t input_off, uint64_t label_off) {
                                 f->label_bytes, hipMemcpyDeviceToDevice, c->stream),
               "feeder_next labels");
   SEEAI_TRY(c, hipEventRecord(f->consumed[slot], c->stream), "feeder_next event");
-  c->cvt_key.at = nullptr;  // the arena changed outside the program
+  ForgetCopies(c);  // the arena changed outside the program
   std::lock_guard<std::mutex> lock(f->mu);
   f->consume_recorded[slot] = true;
   f->tail ^= 1;
@@ -1910,6 +2013,22 @@ int PresizeWorkspaces(seeai_ctx* c, const uint8_t* prog, uint64_t begin, uint64_
     std::memcpy(&ins, prog + i * sizeof(Instruction), sizeof ins);
     if (ins.opcode == 11 || ins.opcode == 51)  // softmax-xent forward (+masked): row partials
       scratch = std::max(scratch, XEntFwdScratchBytes(ins.out[0]));
+    if ((ins.opcode == 47 || ins.opcode == 57) && (ins.flags & kFlagRelaxed)) {
+      uint64_t B, S, H, d;
+      if (ins.opcode == 47) {
+        B = ins.out[1] >> 32, S = ins.out[1] & 0xFFFFFFFFu, H = ins.out[2] >> 32,
+        d = ins.out[2] & 0xFFFFFFFFu;
+      } else {
+        const uint64_t g = ins.out[1];
+        B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
+      }
+      if (Attn16Plan(c, B, S, H, d)) {
+        const Ptrs R{c};
+        if (int rc = MakeSavedCopies(c, R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2]),
+                                     B * S * H * d))
+          return rc;
+      }
+    }
     GemmArgs a{};
     if (!DecodeGemm(c, ins, &a)) continue;
     a.relaxed = (ins.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
@@ -1955,7 +2074,7 @@ int seeai_begin_range(seeai_ctx* c, const void* program, uint64_t count, uint64_
   c->prog_count = count;
   c->range_end = end;
   c->ndone = 0;
-  c->cvt_key.at = nullptr;
+  ForgetCopies(c);
   return SEEAI_OK;
 }
 
@@ -1964,7 +2083,7 @@ int seeai_end_range(seeai_ctx* c) {
   c->prog = nullptr;
   c->prog_count = c->range_end = 0;
   c->ndone = 0;
-  c->cvt_key.at = nullptr;
+  ForgetCopies(c);
   return SEEAI_OK;
 }
 
