@@ -232,16 +232,19 @@ __device__ __forceinline__ void LoadRow4(const float* __restrict__ p, int lane, 
   }
 }
 
+// With `has_res`, rv holds the residual row (loaded with the row's operands,
+// so its latency hides behind the sums).
 template <int kV, class F>
 __device__ __forceinline__ void StoreRow4(float* yr, size_t row0, size_t cols, int lane,
-                                          const Bf16Sink& sink, const float* rr, F&& elem) {
+                                          const Bf16Sink& sink, bool has_res,
+                                          const float4 (&rv)[kV], F&& elem) {
 #pragma unroll
   for (int j = 0; j < kV; ++j) {
     const size_t c = 4 * static_cast<size_t>(lane + kWave * j);
     if (c >= cols) continue;
     float4 v = make_float4(elem(j, 0), elem(j, 1), elem(j, 2), elem(j, 3));
-    if (rr) {
-      const float4 r = *reinterpret_cast<const float4*>(rr + c);
+    if (has_res) {
+      const float4 r = rv[j];
       v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
     }
     if (sink.store_f32) *reinterpret_cast<float4*>(yr + c) = v;
@@ -286,7 +289,7 @@ LayerNormFwdRows(const float* __restrict__ x, const float* __restrict__ g,
     mean[r] = mu;
     rstd[r] = rs;
   }
-  StoreRow4<kV>(y + r * cols, r * cols, cols, lane, sink, nullptr, [&](int j, int e) {
+  StoreRow4<kV>(y + r * cols, r * cols, cols, lane, sink, false, xv, [&](int j, int e) {
     const size_t c = 4 * static_cast<size_t>(lane + kWave * j) + e;
     return (Comp(xv[j], e) - mu) * rs * g[c] + b[c];
   });
@@ -301,9 +304,10 @@ LayerNormBwdRows(const float* __restrict__ dy, const float* __restrict__ x,
   const int lane = threadIdx.x % kWave;
   const size_t r = static_cast<size_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
   if (r >= rows) return;
-  float4 xv[kV], dv[kV];
+  float4 xv[kV], dv[kV], rv[kV];
   LoadRow4<kV>(x + r * cols, lane, cols, xv);
   LoadRow4<kV>(dy + r * cols, lane, cols, dv);
+  if (res) LoadRow4<kV>(res + r * cols, lane, cols, rv);
   const float mu = mean[r], rs = rstd[r];
   double sg = 0.0, sgx = 0.0;
 #pragma unroll
@@ -323,7 +327,7 @@ LayerNormBwdRows(const float* __restrict__ dy, const float* __restrict__ x,
   const float inv_d = 1.0f / static_cast<float>(cols);
   const float mg = static_cast<float>(sg) * inv_d;
   const float mgx = static_cast<float>(sgx) * inv_d;
-  StoreRow4<kV>(dx + r * cols, r * cols, cols, lane, sink, res ? res + r * cols : nullptr,
+  StoreRow4<kV>(dx + r * cols, r * cols, cols, lane, sink, res != nullptr, rv,
                 [&](int j, int e) {
                   const size_t c = 4 * static_cast<size_t>(lane + kWave * j) + e;
                   const float xhat = (Comp(xv[j], e) - mu) * rs;
@@ -349,7 +353,7 @@ RmsNormFwdRows(const float* __restrict__ x, const float* __restrict__ g, float* 
   ss = WaveSumD(ss);
   const float rs = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + eps);
   if (lane == 0) rstd[r] = rs;
-  StoreRow4<kV>(y + r * cols, r * cols, cols, lane, sink, nullptr, [&](int j, int e) {
+  StoreRow4<kV>(y + r * cols, r * cols, cols, lane, sink, false, xv, [&](int j, int e) {
     const size_t c = 4 * static_cast<size_t>(lane + kWave * j) + e;
     return Comp(xv[j], e) * rs * g[c];
   });
@@ -363,9 +367,10 @@ RmsNormBwdRows(const float* __restrict__ dy, const float* __restrict__ x,
   const int lane = threadIdx.x % kWave;
   const size_t r = static_cast<size_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
   if (r >= rows) return;
-  float4 xv[kV], dv[kV];
+  float4 xv[kV], dv[kV], rv[kV];
   LoadRow4<kV>(x + r * cols, lane, cols, xv);
   LoadRow4<kV>(dy + r * cols, lane, cols, dv);
+  if (res) LoadRow4<kV>(res + r * cols, lane, cols, rv);
   const float rs = rstd[r];
   double sgx = 0.0;
 #pragma unroll
@@ -379,7 +384,7 @@ RmsNormBwdRows(const float* __restrict__ dy, const float* __restrict__ x,
   sgx = WaveSumD(sgx);
   const float inv_d = 1.0f / static_cast<float>(cols);
   const float mgx = static_cast<float>(sgx) * inv_d;
-  StoreRow4<kV>(dx + r * cols, r * cols, cols, lane, sink, res ? res + r * cols : nullptr,
+  StoreRow4<kV>(dx + r * cols, r * cols, cols, lane, sink, res != nullptr, rv,
                 [&](int j, int e) {
                   const size_t c = 4 * static_cast<size_t>(lane + kWave * j) + e;
                   return rs * (Comp(dv[j], e) * g[c] - Comp(xv[j], e) * rs * rs * mgx);
