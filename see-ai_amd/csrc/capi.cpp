@@ -1029,10 +1029,17 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
         } else if (int rc = Attn16Operands(c, src, 7u, B * S, H * d, b16)) {
           return rc;
         }
+        // The output's bf16 copy for the relaxed product reading it next.
+        Bf16Sink sink;
+        GemmArgs ga{};
+        const bool sunk = c->cur_at && NormSinkFits(H * d, {R.f(ins.in[3])}) &&
+                          PlanSink(c, CurIndex(c), CurIndex(c), R.f(ins.in[3]), B * S * H * d,
+                                   &sink, &ga);
         SEEAI_TRY(c,
                   LaunchAttn16Fwd(b16[0], b16[1], b16[2], R.f(ins.in[3]), R.f(ins.out[0]), B, S,
-                                  H, starts, s),
+                                  H, starts, s, sink),
                   "attn.fwd_bf16");
+        if (sunk) SinkDone(c, CurIndex(c), ga);
         return SEEAI_OK;
       }
       SEEAI_TRY(c,

@@ -413,9 +413,11 @@ hipError_t LaunchAttnDKDVFused(const float* q, const float* k, const float* v, c
 bool FlashFits(size_t B, size_t S, size_t H, size_t d);
 // Head width 64 on bf16 operands in HBM (k_attn16.hip).
 bool Attn16Fits(size_t B, size_t S, size_t H, size_t d);
+// sink: the output's bf16 copy for the relaxed product after it (the
+// attention output o is [B·S, H·64], the product's A).
 hipError_t LaunchAttn16Fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, float* o,
                            float* stats, size_t B, size_t S, size_t H, const int32_t* starts,
-                           hipStream_t s);
+                           hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
 hipError_t LaunchAttn16DQ(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                           const uint16_t* dout, float* stats, float* dq, size_t B, size_t S,
                           size_t H, hipStream_t s);

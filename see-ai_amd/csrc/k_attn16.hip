@@ -262,7 +262,7 @@ template <int kFwdWaves, int kStages, int kMinBlocks>
 __global__ void __launch_bounds__(kFwdWaves * kWave, kMinBlocks)
 Attn16Fwd(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
           const uint16_t* __restrict__ v, float* __restrict__ o, float* __restrict__ stats, int S,
-          int H, const int32_t* __restrict__ starts) {
+          int H, const int32_t* __restrict__ starts, Bf16Sink sink) {
   constexpr int kFwdRows = kFwdWaves * 32;
   SEEAI_STAGE_RING(kStages);
   __shared__ int wave_lo[kFwdWaves];
@@ -403,14 +403,18 @@ Attn16Fwd(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   const float m_true = SwapMax(m_half);
   if (i >= S) return;
   const float inv = 1.0f / l;
-  float* orow = o + base + static_cast<size_t>(i) * ld;
+  const size_t orow0 = base + static_cast<size_t>(i) * ld;
+  float* orow = o + orow0;
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq)
-      *reinterpret_cast<float4*>(orow + dt * 32 + 8 * qq + 4 * g) =
-          make_float4(oacc[dt][4 * qq] * inv, oacc[dt][4 * qq + 1] * inv,
-                      oacc[dt][4 * qq + 2] * inv, oacc[dt][4 * qq + 3] * inv);
+    for (int qq = 0; qq < 4; ++qq) {
+      const float4 ov = make_float4(oacc[dt][4 * qq] * inv, oacc[dt][4 * qq + 1] * inv,
+                                    oacc[dt][4 * qq + 2] * inv, oacc[dt][4 * qq + 3] * inv);
+      const int col = dt * 32 + 8 * qq + 4 * g;
+      if (sink.store_f32) *reinterpret_cast<float4*>(orow + col) = ov;
+      if (sink.out) SinkStore4(sink, orow0 + col, ov);  // the next product's bf16 A'
+    }
   if (g == 0) {
     float* sr = stats + (static_cast<size_t>(bh) * S + i) * 4;
     sr[0] = m_true * kLn2;
@@ -771,13 +775,13 @@ bool Attn16Fits(size_t B, size_t S, size_t H, size_t d) {
 
 hipError_t LaunchAttn16Fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, float* o,
                            float* stats, size_t B, size_t S, size_t H, const int32_t* starts,
-                           hipStream_t s) {
+                           hipStream_t s, const Bf16Sink& sink) {
   if (B * H * S == 0) return hipSuccess;
   // Four waves, two stages, four workgroups per CU (measured against 3-4
   // stages and 8-wave workgroups at B16 H16 S2048).
   const dim3 grid(static_cast<unsigned>((S + 127) / 128 * B * H));
   hipLaunchKernelGGL((Attn16Fwd<4, 2, 4>), grid, dim3(256), 0, s, q, k, v, o, stats,
-                     static_cast<int>(S), static_cast<int>(H), starts);
+                     static_cast<int>(S), static_cast<int>(H), starts, sink);
   return hipGetLastError();
 }
 

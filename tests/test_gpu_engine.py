@@ -462,10 +462,14 @@ def test_c4_width_slice_step_tensors_match_the_oracle(hip, orc, torch_cuda, rela
 # RMSNorm and the SwiGLU passes in place of GELU.  The final norm does not
 # fuse: the head's N = 96 is below the direct-to-LDS kernel's 128.
 SINKS_PER_STEP = {"c4": 13, "c5": 13}
+# With attention on bf16 copies, the attention forward also writes the
+# O product's activation: one more per block.
+ATTN_SINKS_PER_STEP = 2
 
 
+@pytest.mark.parametrize("attn16", [False, True])
 @pytest.mark.parametrize("plan", ["c4", "c5"])
-def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda, plan):
+def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda, plan, attn16):
     """A producer followed by a relaxed frozen-weight product on the
     direct-to-LDS path writes the product's bf16 activation as it stores
     (GELU forward / backward, the SwiGLU passes, the softmax-xent backward,
@@ -474,8 +478,9 @@ def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda
     its conversion pass.  The residual adds run inside their producers
     (a product's epilogue, a normalisation's backward) in the same run.  With the NT products on the direct-to-LDS kernel
     at these small K (relaxed_nt_dma_min_k 64), three steps with fusion on
-    and off give the same losses and persistent bytes."""
-    print(f"engine: fused conversions, tiny {plan}", flush=True)
+    and off give the same losses and persistent bytes; with attention on
+    bf16 copies the attention forward is one of the producers."""
+    print(f"engine: fused conversions, tiny {plan}, attention bf16 {attn16}", flush=True)
     curves, states, sinks = [], [], []
     for allow in (True, False):
         if plan == "c4":
@@ -488,6 +493,7 @@ def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda
             vocab = TINY_Q8["vocab"]
         eng = hip.Engine(img.blob)
         eng.configure({"relaxed_nt_dma_min_k": 64})
+        eng.set_attention_bf16(attn16)
         eng.set_fusion(allow)
         curve = []
         for s in range(3):
@@ -503,6 +509,7 @@ def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda
     # ahead of the first product that needs the room does not fuse); steps
     # two and three fuse every one.
     print(f"  {sinks[0]} conversions fused over steps 2-3", flush=True)
-    assert sinks[0] == 2 * SINKS_PER_STEP[plan] and sinks[1] == 0
+    assert sinks[0] == 2 * (SINKS_PER_STEP[plan] + (ATTN_SINKS_PER_STEP if attn16 else 0))
+    assert sinks[1] == 0
     assert curves[0].tobytes() == curves[1].tobytes()
     assert states[0] == states[1]
