@@ -173,6 +173,12 @@ struct seeai_ctx {
   };
   std::vector<A16Saved> a16_saved;
   uint64_t a16_epoch = 1;
+  // Operand copies a RoPE forward wrote into the saved copies of the
+  // attention forward at instruction `at` (slot 0 q, 1 k), in this epoch.
+  struct {
+    const float* src = nullptr;
+    uint64_t at = 0, epoch = 0;
+  } a16_pre[2];
   struct {
     const float* A = nullptr;
     uint64_t M = 0, K = 0;
@@ -341,6 +347,7 @@ bool Immutable(const seeai_ctx* c, const void* p) {
 
 const char* DecodeGemm(seeai_ctx* c, const Instruction& ins, GemmArgs* out);
 bool Overlap(const uint8_t* a, uint64_t na, const uint8_t* b, uint64_t nb);
+uint64_t CurIndex(const seeai_ctx* c);
 
 // Whether the conversion buffer already holds this GEMM's A' (range
 // fusion): the same A, shape, alpha and k-scale converted by an earlier
@@ -558,6 +565,53 @@ bool SavedCurrent(seeai_ctx* c, seeai_ctx::A16Saved* sv) {
     sv->clean_to = i + 1;
   }
   return true;
+}
+
+// A RoPE forward whose output y is the q or k operand of a bf16-copy
+// attention forward at most two instructions on (the instruction between,
+// the other RoPE, writes neither y nor the copies) writes y's bf16 copy into
+// that attention's saved copies as it stores y; the attention then skips
+// that operand's conversion.  Returns the copy's slot, or null.
+uint16_t* RopeAttnCopy(seeai_ctx* c, const float* x, const float* y, uint64_t B, uint64_t S,
+                       uint64_t H, uint64_t d, const float* table) {
+  if (!c->allow_fusion || !c->allow_sinks || !c->cur_at || !c->prog ||
+      !RopeRowsFits(x, y, B, S, H, d, table))
+    return nullptr;
+  const uint64_t at = CurIndex(c), n = B * S * H * d;
+  for (uint64_t a = at + 1; a <= at + 2 && a < c->range_end; ++a) {
+    Instruction ins;
+    std::memcpy(&ins, c->prog + a * 64, sizeof ins);
+    if (ins.opcode != 47 && ins.opcode != 57) {
+      Touch t[16];
+      int nt = 0;
+      if (!TouchExtents(c, ins, t, &nt)) return nullptr;
+      for (int j = 0; j < nt; ++j)
+        if (t[j].write && Overlap(t[j].p, t[j].n, reinterpret_cast<const uint8_t*>(y), n * 4))
+          return nullptr;
+      continue;
+    }
+    uint64_t aB, aS, aH, ad;
+    if (ins.opcode == 47) {
+      aB = ins.out[1] >> 32, aS = ins.out[1] & 0xFFFFFFFFu, aH = ins.out[2] >> 32,
+      ad = ins.out[2] & 0xFFFFFFFFu;
+    } else {
+      const uint64_t g = ins.out[1];
+      aB = g >> 48, aS = (g >> 32) & 0xFFFF, aH = (g >> 16) & 0xFFFF, ad = g & 0xFFFF;
+    }
+    if (aB * aS * aH * ad != n || RelaxedAttention(c, ins) != 1 || !Attn16Plan(c, aB, aS, aH, ad))
+      return nullptr;
+    Ptrs R{c};
+    const float* src[3] = {R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2])};
+    seeai_ctx::A16Saved* sv = SavedCopies(c, src[0], src[1], src[2], n);
+    if (!sv) return nullptr;
+    const int slot = src[0] == y ? 0 : src[1] == y ? 1 : -1;
+    if (slot < 0) return nullptr;
+    c->a16_pre[slot].src = y;
+    c->a16_pre[slot].at = a;
+    c->a16_pre[slot].epoch = c->a16_epoch;
+    return static_cast<uint16_t*>(sv->buf) + static_cast<size_t>(slot) * n;
+  }
+  return nullptr;
 }
 
 // The operands of a backward instruction: q, k, v from the forward's saved
@@ -919,9 +973,13 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       const uint64_t d = ins.out[1] & 0xFFFFFFFFu;
       const float base = BitsToF32(ins.out[2]);
       const float step = std::pow(base, -2.0f / static_cast<float>(d));  // attention.cc:123
+      uint16_t* y16 = ins.opcode == 33
+                          ? RopeAttnCopy(c, R.f(ins.in[0]), R.f(ins.in[1]), hi0, lo0,
+                                         ins.out[1] >> 32, d, R.fo(ins.in[2]))
+                          : nullptr;
       SEEAI_TRY(c,
                 LaunchRope(R.f(ins.in[0]), R.f(ins.in[1]), hi0, lo0, ins.out[1] >> 32, d, step,
-                           R.fo(ins.in[2]), ins.opcode == 34, s),
+                           R.fo(ins.in[2]), ins.opcode == 34, s, y16),
                 "rope");
       return SEEAI_OK;
     }
@@ -1018,6 +1076,12 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
         if (sv) {  // into the copies the backward of this range run may take
           for (int i = 0; i < 3; ++i) {
             b16[i] = static_cast<uint16_t*>(sv->buf) + static_cast<size_t>(i) * n;
+            if (i < 2 && c->a16_pre[i].src == src[i] && c->a16_pre[i].at == CurIndex(c) &&
+                c->a16_pre[i].epoch == c->a16_epoch) {
+              c->a16_pre[i].src = nullptr;  // written by the RoPE forward just before
+              ++c->sinks;
+              continue;
+            }
             SEEAI_TRY(c,
                       LaunchConvertRowsBf16(src[i], B * S, H * d, 1.0f, nullptr, b16[i],
                                             c->policy.convert_wgs_per_cu, s),

@@ -471,7 +471,8 @@ RopeKernel(const float* __restrict__ x, float* __restrict__ y, size_t B, size_t 
 // expressions as RopeKernel.  d % 4 == 0, x, y and the table 16-byte aligned.
 __global__ void __launch_bounds__(kThreads)
 RopeRowsKernel(const float* __restrict__ x, float* __restrict__ y, unsigned rows, unsigned S,
-               unsigned width, unsigned d, const float* __restrict__ table, int backward) {
+               unsigned width, unsigned d, const float* __restrict__ table, int backward,
+               uint16_t* __restrict__ y16) {
   for (unsigned r = blockIdx.y; r < rows; r += gridDim.y) {
     const unsigned s = r % S;
     const float* __restrict__ trow = table + static_cast<size_t>(s) * d;  // d/2 pairs x 2
@@ -494,6 +495,12 @@ RopeRowsKernel(const float* __restrict__ x, float* __restrict__ y, unsigned rows
         o.w = v.z * t.w + v.w * t.z;
       }
       *reinterpret_cast<float4*>(y + base + c) = o;
+      if (y16) {  // the attention's bf16 copy of y, rounded to nearest even
+        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+        const bf16x4_t h = {static_cast<__bf16>(o.x), static_cast<__bf16>(o.y),
+                            static_cast<__bf16>(o.z), static_cast<__bf16>(o.w)};
+        *reinterpret_cast<bf16x4_t*>(y16 + base + c) = h;
+      }
     }
   }
 }
@@ -873,21 +880,28 @@ hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, con
                      x, g, rstd, dx, cols, vec, sink, res);
   return hipGetLastError();
 }
-hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
-                      float step, const float* table, int backward, hipStream_t s) {
-  const size_t n = B * S * H * (d / 2);
-  if (n == 0) return hipSuccess;
+bool RopeRowsFits(const float* x, const float* y, size_t B, size_t S, size_t H, size_t d,
+                  const float* table) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
                        reinterpret_cast<uintptr_t>(table);
-  if (table && d % 4 == 0 && (al & 15) == 0 && B * S < (size_t{1} << 31) &&
-      H * d < (size_t{1} << 31)) {
+  return table && d % 4 == 0 && (al & 15) == 0 && B * S < (size_t{1} << 31) &&
+         H * d < (size_t{1} << 31);
+}
+
+hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
+                      float step, const float* table, int backward, hipStream_t s, uint16_t* y16) {
+  const size_t n = B * S * H * (d / 2);
+  if (n == 0) return hipSuccess;
+  if (RopeRowsFits(x, y, B, S, H, d, table)) {
     const unsigned width = static_cast<unsigned>(H * d), rows = static_cast<unsigned>(B * S);
     const unsigned gx = static_cast<unsigned>(std::min<size_t>((width / 4 + kThreads - 1) / kThreads, 64));
     const dim3 grid(gx, std::min(rows, 65535u));
     hipLaunchKernelGGL(RopeRowsKernel, grid, dim3(kThreads), 0, s, x, y, rows,
-                       static_cast<unsigned>(S), width, static_cast<unsigned>(d), table, backward);
+                       static_cast<unsigned>(S), width, static_cast<unsigned>(d), table, backward,
+                       y16);
     return hipGetLastError();
   }
+  if (y16) return hipErrorInvalidValue;  // the bf16 copy rides on the row kernel only
   const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 7) == 0;
   if (vec)
     hipLaunchKernelGGL(RopeKernel<true>, dim3(GridFor(n, kThreads)), dim3(kThreads), 0, s, x, y, B,
