@@ -172,6 +172,7 @@ struct seeai_ctx {
     void* buf;
   };
   std::vector<A16Saved> a16_saved;
+  uint64_t a16_saved_cap = uint64_t{4} << 30;  // bytes over every saved triple
   uint64_t a16_epoch = 1;
   // Operand copies a RoPE forward wrote into the saved copies of the
   // attention forward at instruction `at` (slot 0 q, 1 k), in this epoch.
@@ -433,8 +434,11 @@ int Relaxed(seeai_ctx* c, const Instruction& ins) {
 // with the sums reordered, at head widths up to 64) runs the f32 MFMA
 // family unless the backend is switched to bf16 attention; only the bf16
 // kernels are a relaxed execution.
+bool IsRelaxedAttention(const seeai_ctx* c, const Instruction& ins) {
+  return (ins.flags & kFlagRelaxed) && c->allow_relaxed && c->attn_bf16;
+}
 int RelaxedAttention(seeai_ctx* c, const Instruction& ins) {
-  const int r = (ins.flags & kFlagRelaxed) && c->allow_relaxed && c->attn_bf16 ? 1 : 0;
+  const int r = IsRelaxedAttention(c, ins) ? 1 : 0;
   c->relaxed += r;
   return r;
 }
@@ -531,9 +535,17 @@ seeai_ctx::A16Saved* SavedCopies(seeai_ctx* c, const float* q, const float* k, c
 }
 
 // A buffer for the forward's copies of (q, k, v) (made ahead of a range by
-// PresizeWorkspaces, so none is allocated inside one).
+// PresizeWorkspaces, so none is allocated inside one): 6 bytes per element
+// of q, one buffer per distinct source triple (a decoder keeps one per
+// layer, every forward-to-backward interval of a step overlapping the
+// others), kept until the next bind.  The buffers together stay within
+// c->a16_saved_cap bytes; a triple past the cap keeps no copies and its
+// backward converts q, k and v again, as a separate range would.
 int MakeSavedCopies(seeai_ctx* c, const float* q, const float* k, const float* v, uint64_t n) {
   if (SavedCopies(c, q, k, v, n)) return SEEAI_OK;
+  uint64_t held = 0;
+  for (const auto& sv : c->a16_saved) held += 3 * sv.n * 2;
+  if (held + 3 * n * 2 > c->a16_saved_cap) return SEEAI_OK;
   void* buf = nullptr;
   SEEAI_TRY(c, hipMalloc(&buf, 3 * n * 2), "attention forward copies alloc");
   c->a16_saved.push_back({{q, k, v}, n, 0, 0, 0, buf});
@@ -598,7 +610,7 @@ uint16_t* RopeAttnCopy(seeai_ctx* c, const float* x, const float* y, uint64_t B,
       const uint64_t g = ins.out[1];
       aB = g >> 48, aS = (g >> 32) & 0xFFFF, aH = (g >> 16) & 0xFFFF, ad = g & 0xFFFF;
     }
-    if (aB * aS * aH * ad != n || RelaxedAttention(c, ins) != 1 || !Attn16Plan(c, aB, aS, aH, ad))
+    if (aB * aS * aH * ad != n || !IsRelaxedAttention(c, ins) || !Attn16Plan(c, aB, aS, aH, ad))
       return nullptr;
     Ptrs R{c};
     const float* src[3] = {R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2])};
@@ -1187,6 +1199,10 @@ int seeai_create(int device, seeai_ctx** out) {
   // SEEAI_ATTN16_PLANS=0: relaxed bf16 attention on the f32-operand kernels
   // (the same-session control of the bf16 copies).
   if (const char* e = std::getenv("SEEAI_ATTN16_PLANS"); e && e[0] == '0') c->attn16_plans = 0;
+  // SEEAI_ATTN_SAVED_MB: the cap on the forward's saved bf16 copies of q,
+  // k and v (4096 MiB by default: C5's 16 layers take 1.6 GB).
+  if (const char* e = std::getenv("SEEAI_ATTN_SAVED_MB"))
+    c->a16_saved_cap = std::strtoull(e, nullptr, 10) << 20;
   int rc = Hip(c, hipSetDevice(device), "set device");
   if (rc == SEEAI_OK) rc = Hip(c, NoAllocScratchInit(device), "no-allocation workspace address");
   if (rc == SEEAI_OK) rc = Hip(c, hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "stream");

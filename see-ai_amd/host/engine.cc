@@ -250,10 +250,7 @@ Result<void> PlanEngine::TrainSteps(const float* inputs, const void* labels, uin
       const float* in = inputs + b * h.input_floats;
       const void* lab = lab_bytes ? static_cast<const uint8_t*>(labels) + b * h.label_bytes : nullptr;
       std::string err;
-      if (auto r = CheckBatch(in, lab); !r)
-        err = r.error();
-      else if (seeai_feeder_stage(feeder_, in, lab) != SEEAI_OK)
-        err = seeai_feeder_last_error(feeder_);
+      if (seeai_feeder_stage(feeder_, in, lab) != SEEAI_OK) err = seeai_feeder_last_error(feeder_);
       std::lock_guard<std::mutex> lk(mu);
       if (!err.empty()) {
         feeder_error = "batch " + std::to_string(b) + ": " + err;
@@ -276,6 +273,15 @@ Result<void> PlanEngine::TrainSteps(const float* inputs, const void* labels, uin
     return r;
   };
   for (uint64_t s = 0; s < batches / micro; ++s) {
+    // As TrainStep: every micro-batch of the step is checked before the
+    // step's timestep is spent, so a refusal leaves the engine where the
+    // previous step left it (the feeder only stages).
+    for (uint64_t g = 0; g < micro; ++g) {
+      const uint64_t b = s * micro + g;
+      const void* lab = lab_bytes ? static_cast<const uint8_t*>(labels) + b * h.label_bytes : nullptr;
+      if (auto r = CheckBatch(inputs + b * h.input_floats, lab); !r)
+        return finish(Fail("batch " + std::to_string(b) + ": " + r.error()));
+    }
     double loss_sum = 0.0;
     for (uint64_t g = 0; g < micro; ++g) {
       bool starved;

@@ -40,6 +40,7 @@ ADD_BIAS, RELU_FWD, RELU_BWD = 6, 7, 8
 XENT_FWD, XENT_BWD = 11, 12
 ADAMW = 18
 FILL = 19
+ACCUMULATE = 42
 FLAG_ADDEND = 1 << 3          # kFlagGemmAddend
 
 # PlanHeader field order and widths (schema.h:296-384); packed, little-endian.
@@ -240,13 +241,14 @@ class PlanImage:
 
 
 def assemble(header: dict, train: list, eval_: list, merge: list, emit: list,
-             persist_init: bytes, rodata: bytes, self_hash) -> bytes:
+             persist_init: bytes, rodata: bytes, self_hash, step: list = ()) -> bytes:
     """Lays the sections out after the header and seals the plan.
-    `self_hash(blob) -> int` is PlanSelfHash with the hash field zeroed."""
+    `self_hash(blob) -> int` is PlanSelfHash with the hash field zeroed;
+    `step` is the step program of a plan that accumulates micro-batches."""
     h = dict(header)
     parts = [(b"".join(train), 64), (b"".join(eval_), 64), (b"".join(merge), 64),
              (b"".join(struct.pack("<3Q", *e) for e in emit), 64), (persist_init, 64),
-             (rodata, 4096)]
+             (rodata, 4096), (b"".join(step), 64)]
     offs, end = [], 320
     for payload, align in parts:
         end = (end + align - 1) // align * align
@@ -268,6 +270,8 @@ def assemble(header: dict, train: list, eval_: list, merge: list, emit: list,
     h["persist_init_size"] = len(persist_init)
     h["rodata_offset"] = offs[5]
     h["rodata_size"] = len(rodata)
+    h["step_instr_offset"] = offs[6] if step else 0
+    h["step_instr_count"] = len(step)
     h["plan_hash"] = 0
     out[0:320] = pack_header(h)
     h["plan_hash"] = self_hash(out)
@@ -279,13 +283,20 @@ def assemble(header: dict, train: list, eval_: list, merge: list, emit: list,
 
 def mlp_lora(self_hash, batch: int = 32, din: int = 256, hidden: int = 512, dout: int = 256,
              rank: int = 8, alpha: float = 16.0, lr: float = 1e-3, weight_decay: float = 0.01,
-             seed: int = 20261201, default_steps: int = 100) -> PlanImage:
+             seed: int = 20261201, default_steps: int = 100, grad_accum: int = 1) -> PlanImage:
     """MLP din -> hidden (ReLU) -> dout with AddBias and
     LoRA (rank, alpha) on both MatMuls, softmax-xent over dout classes,
     AdamW.  Base weights and biases N(0, 0.02); LoRA A N(0, 0.02), B = 0.
 
     The train program is the reference's 25 instructions, eval its first
-    10, merge the 4-instruction delta program (fill, GemmAccNN per site)."""
+    10, merge the 4-instruction delta program (fill, GemmAccNN per site).
+
+    grad_accum = G > 1 lowers gradient accumulation as the reference's
+    optimizer pass does (compiler/analysis/optimization/optimizer.cc:22-108,
+    update_compiler.cc:845-864): the loss seed is 1/G, each adapter's
+    gradient folds into a persistent zero-initialised accumulator
+    (kAccumulate) at the end of the train (grad) program, and the step
+    program runs each AdamW step on the accumulator, then zeroes it."""
     s = alpha / rank
     arrays = {
         "W1": normal(seed + 1, (din, hidden), 0.02), "b1": normal(seed + 2, (hidden,), 0.02),
@@ -304,6 +315,9 @@ def mlp_lora(self_hash, batch: int = 32, din: int = 256, hidden: int = 512, dout
         ar.alloc("m_" + n, arrays[n].nbytes, align=4)
     for n in params:                                   # then second moments
         ar.alloc("v_" + n, arrays[n].nbytes, align=4)
+    if grad_accum > 1:                                 # then the accumulators
+        for n in params:
+            ar.alloc("acc_" + n, arrays[n].nbytes, align=4)
     persistent = ar.size
     ar.alloc("X", batch * din * 4, align=4)            # I/O slots
     ar.alloc("labels", batch * 4, align=4)
@@ -333,7 +347,7 @@ def mlp_lora(self_hash, batch: int = 32, din: int = 256, hidden: int = 512, dout
             flags=FLAG_ADDEND, imm=sb),
         ins(ADD_BIAS, [R("Z2b"), RO("b2"), R("logits")], [batch, dout]),
         ins(XENT_FWD, [R("logits"), R("labels"), R("loss"), R("probs")], [batch, dout]),
-        ins(FILL, [R("seed"), f32_bits(1.0)], [1]),
+        ins(FILL, [R("seed"), f32_bits(1.0 / grad_accum)], [1]),
         ins(XENT_BWD, [R("probs"), R("labels"), R("seed"), R("dZ")], [batch, dout]),
         ins(GEMM_NT, [R("dZ"), R("B2"), R("dt2")], [batch, rank, dout], imm=sb),
         ins(GEMM_TN, [R("t2"), R("dZ"), R("dB2")], [rank, dout, batch], imm=sb),
@@ -346,9 +360,19 @@ def mlp_lora(self_hash, batch: int = 32, din: int = 256, hidden: int = 512, dout
         ins(GEMM_TN, [R("t1"), R("dH"), R("dB1")], [rank, hidden, batch], imm=sb),
         ins(GEMM_TN, [R("X"), R("dt1"), R("dA1")], [din, rank, batch]),
     ]
-    for p, g in [("A1", "dA1"), ("B1", "dB1"), ("A2", "dA2"), ("B2", "dB2")]:
-        train.append(ins(ADAMW, [R(p), R(g), R("m_" + p), R("v_" + p)],
-                         [arrays[p].size, 0]))
+    step = []
+    grads = [("A1", "dA1"), ("B1", "dB1"), ("A2", "dA2"), ("B2", "dB2")]
+    if grad_accum > 1:
+        for p, g in grads:
+            train.append(ins(ACCUMULATE, [R("acc_" + p), R(g)], [arrays[p].size]))
+        for p, _ in grads:
+            step += [ins(ADAMW, [R(p), R("acc_" + p), R("m_" + p), R("v_" + p)],
+                         [arrays[p].size, 0]),
+                     ins(FILL, [R("acc_" + p), 0], [arrays[p].size])]
+    else:
+        for p, g in grads:
+            train.append(ins(ADAMW, [R(p), R(g), R("m_" + p), R("v_" + p)],
+                             [arrays[p].size, 0]))
     eval_ = train[:10]
     merge = [
         ins(FILL, [R("D1"), 0], [din * hidden]),
@@ -374,8 +398,9 @@ def mlp_lora(self_hash, batch: int = 32, din: int = 256, hidden: int = 512, dout
         input_ref=R("X"), input_floats=batch * din, label_ref=R("labels"), label_bytes=batch * 4,
         label_kind=1, optimizer_kind=1, loss_ref=R("loss"), lr=lr, beta1=0.9, beta2=0.999,
         eps=1e-8, weight_decay=weight_decay, batch=batch, default_steps=default_steps,
-        step_instr_offset=0, step_instr_count=0)
-    blob = assemble(header, train, eval_, merge, emit, bytes(persist), bytes(rodata), self_hash)
+        step_instr_offset=0, step_instr_count=0, grad_accum_steps=grad_accum if grad_accum > 1 else 0)
+    blob = assemble(header, train, eval_, merge, emit, bytes(persist), bytes(rodata), self_hash,
+                    step=step)
     return PlanImage(blob=blob, header=parse_header(blob), arena=dict(ar.names),
                      rodata=dict(ro.names), train=train, eval=eval_, merge=merge, arrays=arrays)
 

@@ -50,6 +50,8 @@ class OracleEngine:
         self.train = section(h["train_instr_offset"], h["train_instr_count"])
         self.eval = section(h["eval_instr_offset"], h["eval_instr_count"])
         self.merge = section(h["merge_instr_offset"], h["merge_instr_count"])
+        self.step_program = section(h["step_instr_offset"], h["step_instr_count"])
+        self.micro = h["grad_accum_steps"] if h["grad_accum_steps"] > 1 else 1
         self.step = 0
         self.horizon = 0
 
@@ -78,10 +80,23 @@ class OracleEngine:
         return struct.unpack("<f", self.arena[o:o + 4].tobytes())[0]
 
     def train_step(self, x, labels) -> float:
+        """One optimizer step: `x` / `labels` hold the step's micro-batches
+        back to back (update_engine.cc:840-870); the mean of their losses."""
         self.step += 1
-        self._stage(x, labels)
-        self._run(self.train)
-        return self.loss()
+        if self.micro == 1:
+            self._stage(x, labels)
+            self._run(self.train)
+            return self.loss()
+        h = self.h
+        xs = np.ascontiguousarray(x, np.float32).reshape(self.micro, -1)
+        ls = np.ascontiguousarray(labels).view(np.uint8).reshape(self.micro, -1)
+        total = 0.0
+        for g in range(self.micro):
+            self._stage(xs[g][:h["input_floats"]], ls[g])
+            self._run(self.train)
+            total += self.loss()
+        self._run(self.step_program)
+        return float(np.float32(total / self.micro))
 
     def evaluate(self, x, labels) -> float:
         self._stage(x, labels)

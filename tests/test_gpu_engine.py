@@ -327,14 +327,16 @@ def test_token_outside_the_vocabulary_is_refused(hip, torch_cuda):
 
 def _plant_b(img, eng, twin, seed):
     """Nonzero B adapters (B = 0 at init would leave every dA at zero), the
-    same bytes in the engine and its twin."""
+    same bytes in the engine and its twin (either may be None)."""
     r = np.random.default_rng(seed)
     for name in img.arrays:
         if ".B" in name:
             off, nb = img.arena[name]
             val = (r.standard_normal(img.arrays[name].shape) * 0.05).astype(np.float32)
-            eng.write(off, val.tobytes())
-            twin.arena[off:off + nb] = val.view(np.uint8).ravel()
+            if eng is not None:
+                eng.write(off, val.tobytes())
+            if twin is not None:
+                twin.arena[off:off + nb] = val.view(np.uint8).ravel()
 
 
 def _step_tensor_errors(img, eng, twin):
@@ -355,103 +357,226 @@ def _step_tensor_errors(img, eng, twin):
     return errs
 
 
-@pytest.mark.parametrize("which", ["c4", "c5"])
-@pytest.mark.parametrize("relaxed", [False, True])
-def test_decoder_step_tensors_match_the_oracle(hip, orc, torch_cuda, which, relaxed):
-    """One step of the small decoder plans with B planted nonzero, fusion
-    off so every instruction stores its output: every activation, gradient
-    and scratch tensor of the arena against the oracle's, per tensor --
-    exact family 1e-5, relaxed family (bf16 frozen-weight products) 2e-2 --
-    the north star's bars, before AdamW's sign amplification can act."""
-    make, cfg = (pw.decoder_lora, TINY) if which == "c4" else (pw.decoder_q8_lora, TINY_Q8)
-    img = make(hip.plan_self_hash, relaxed=relaxed, **cfg)
-    eng, twin = hip.Engine(img.blob), OracleEngine(orc, img.blob)
-    eng.set_fusion(False)
-    _plant_b(img, eng, twin, 77)
-    T = cfg["batch"] * cfg["seq"]
-    t = pw.uniform_ints(7300, T + 1, cfg["vocab"])
-    x, y = t[:T].copy(), t[1:].copy()
-    lg, lc = eng.train_step(x.view(np.float32), y), twin.train_step(x.view(np.float32), y)
+# The modes a decoder step is compared in.  "exact": the exact family, fusion
+# off.  "relaxed": the relaxed family with fusion off, so every instruction
+# stores its output, attention on f32 products.  "bench": what bench.py
+# times -- the relaxed family, attention on bf16 copies (the forward's copies
+# kept for the backward, RoPE writing them), every range fusion on -- with
+# SEEAI_KEEP_DEAD_STORES=1, so each tensor the fused passes compute is still
+# stored and compared (storing it or not never changes a value).
+STEP_MODES = ["exact", "relaxed", "bench"]
+ATTN_OPS = {47, 48, 49, 50, 57}
+
+
+def _mode_engine(hip, blob, mode):
+    import os
+    keep = os.environ.get("SEEAI_KEEP_DEAD_STORES")
+    if mode == "bench":
+        os.environ["SEEAI_KEEP_DEAD_STORES"] = "1"  # read when the context is made
+    try:
+        eng = hip.Engine(blob)
+    finally:
+        if keep is None:
+            os.environ.pop("SEEAI_KEEP_DEAD_STORES", None)
+        else:
+            os.environ["SEEAI_KEEP_DEAD_STORES"] = keep
+    eng.set_fusion(mode == "bench")
+    eng.set_attention_bf16(mode == "bench")
+    return eng
+
+
+_TWINS: dict = {}
+
+
+def _oracle_step(orc, key, img, plant_seed, tokens, threads=1):
+    """One oracle train step of `img` with B planted from `plant_seed`,
+    cached per key: the oracle runs the exact family whatever the plan's
+    relaxed flags, so the exact and relaxed plans (same layout) share it."""
+    if key in _TWINS:
+        twin, loss, arena_map = _TWINS[key]
+        assert arena_map == img.arena
+        return twin, loss
+    _TWINS.clear()  # one big twin at a time
+    twin = OracleEngine(orc, img.blob)
+    _plant_b(img, None, twin, plant_seed)
+    x, y = tokens
+    orc.set_threads(threads)
+    try:
+        loss = twin.train_step(x.view(np.float32), y)
+    finally:
+        orc.set_threads(1)
+    _TWINS[key] = (twin, loss, dict(img.arena))
+    return twin, loss
+
+
+def _compare_step(hip, orc, img, mode, key, plant_seed, tokens, threads=1):
+    eng = _mode_engine(hip, img.blob, mode)
+    _plant_b(img, eng, None, plant_seed)
+    x, y = tokens
+    relaxed0 = eng.relaxed_executions()
+    lg = eng.train_step(x.view(np.float32), y)
+    twin, lc = _oracle_step(orc, key, img, plant_seed, tokens, threads)
     errs = _step_tensor_errors(img, eng, twin)
     worst = sorted(errs.items(), key=lambda kv: -kv[1])[:6]
-    print(f"{which} relaxed={relaxed}: loss {lg} vs {lc}; worst " +
-          ", ".join(f"{n} {e:.2e}" for n, e in worst))
-    bar = 2e-2 if relaxed else TOL
+    print(f"{key} {mode}: loss {lg} vs {lc}; fused {eng.fused_dispatches()}; worst " +
+          ", ".join(f"{n} {e:.2e}" for n, e in worst), flush=True)
+    bar = TOL if mode == "exact" else 2e-2
     assert abs(lg - lc) <= bar * abs(lc)
     bad = {n: e for n, e in errs.items() if not e <= bar}
     assert not bad, bad
+    # Relaxed attention counts as a relaxed execution only on the bf16
+    # kernels (bench mode); the f32-product family is exact arithmetic.
+    n_relaxed = sum(1 for w in img.train
+                    if struct.unpack_from("<H", w, 2)[0] & (1 << 5)
+                    and (mode == "bench" or struct.unpack_from("<H", w)[0] not in ATTN_OPS))
+    assert eng.relaxed_executions() - relaxed0 == (0 if mode == "exact" else n_relaxed)
+    if mode == "bench":
+        assert eng.fused_dispatches() > 0
     eng.close()
 
 
 @pytest.mark.parametrize("which", ["c4", "c5"])
-def test_relaxed_adapters_after_steps_match_the_oracle(hip, orc, torch_cuda, which):
-    """The relaxed plans' adapters after four AdamW steps, B planted, against
-    the exact twin: per tensor, the relative L2 error ||gpu - cpu|| / ||cpu||
-    within the bf16 bar 2e-2.
-
-    Per element the bar cannot hold, whatever the kernels: AdamW's update is
-    lr * m / (sqrt(v) + eps), about lr * sign(g) in the first steps, so a
-    gradient element at the bf16 noise floor that changes sign moves its
-    parameter by 2 lr per step.  Four steps at lr 1e-3 against adapters of
-    magnitude ~0.1 give a per-tensor max-rel near 3e-2 from single elements
-    (measured on MI355X: 3.2e-2 and 3.4e-2), printed here beside the L2
-    measure that is asserted."""
+@pytest.mark.parametrize("mode", STEP_MODES)
+def test_decoder_step_tensors_match_the_oracle(hip, orc, torch_cuda, which, mode):
+    """One step of the small decoder plans with B planted nonzero: every
+    activation, gradient and scratch tensor of the arena against the
+    oracle's, per tensor -- exact family 1e-5, relaxed family 2e-2 -- the
+    north star's bars, before AdamW's sign amplification can act; in the
+    exact mode, in the relaxed mode with every instruction apart, and in the
+    configuration the bench times; each relaxed instruction counted once."""
     make, cfg = (pw.decoder_lora, TINY) if which == "c4" else (pw.decoder_q8_lora, TINY_Q8)
-    img = make(hip.plan_self_hash, relaxed=True, **cfg)
-    eng, twin = hip.Engine(img.blob), OracleEngine(orc, img.blob)
+    img = make(hip.plan_self_hash, relaxed=mode != "exact", **cfg)
+    T = cfg["batch"] * cfg["seq"]
+    t = pw.uniform_ints(7300, T + 1, cfg["vocab"])
+    _compare_step(hip, orc, img, mode, f"tiny-{which}", 77, (t[:T].copy(), t[1:].copy()))
+
+
+def _adamw_pairs(img):
+    """(parameter, gradient) arena names of the train program's AdamW steps."""
+    inv = {off: n for n, (off, nb) in img.arena.items()}
+    out = []
+    for w in img.train:
+        if struct.unpack_from("<H", w)[0] == 18:
+            p, g = struct.unpack_from("<2Q", w, 8)
+            out.append((inv[p], inv[g]))
+    return out
+
+
+def _f64(reader, img, name):
+    off, nb = img.arena[name]
+    return np.frombuffer(reader.read(off, nb), np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("which", ["c4", "c5"])
+@pytest.mark.parametrize("mode", ["exact", "bench"])
+def test_adapters_after_steps_match_the_oracle(hip, orc, torch_cuda, which, mode):
+    """The updated adapters over four AdamW steps (B planted) against the
+    exact twin, and where their error comes from.
+
+    At every step the engine's update is bitwise the reference AdamW
+    (optimizer.cc:104-132, the oracle's restatement) applied to the engine's
+    own gradient and state: the optimizer adds no error of its own.  At the
+    first step those gradients are within the family's bar of the twin's
+    (exact 1e-5, relaxed 2e-2).  What the update then does to them is
+    AdamW's: its step is lr m / (sqrt(v) + eps), about lr g / (|g| + eps) at
+    step one, so a gradient element near eps moves its parameter by a
+    sizeable fraction of lr for a tiny change of g, and one whose sign
+    changes (relaxed: an element at the bf16 noise floor) by 2 lr.  So the
+    per-tensor max-rel of the parameters after a step is not the gradients'
+    bar: it is printed, held under a regression ceiling (exact 1e-4, relaxed
+    5e-2), the relative L2 error under the bar; relaxed, every gradient sign
+    change sits below 2e-2 max|g| of its tensor and every parameter element
+    outside the bar after four steps had one."""
+    make, cfg = (pw.decoder_lora, TINY) if which == "c4" else (pw.decoder_q8_lora, TINY_Q8)
+    img = make(hip.plan_self_hash, relaxed=mode != "exact", **cfg)
+    eng, twin = _mode_engine(hip, img.blob, mode), OracleEngine(orc, img.blob)
     _plant_b(img, eng, twin, 78)
     T = cfg["batch"] * cfg["seq"]
+    h = img.header
+    moments = {}
+    for w in img.train:
+        if struct.unpack_from("<H", w)[0] == 18:
+            refs = struct.unpack_from("<4Q", w, 8)
+            inv = {off: n for n, (off, nb) in img.arena.items()}
+            moments[inv[refs[0]]] = (inv[refs[1]], inv[refs[2]], inv[refs[3]])
+    flipped = {p: np.zeros(img.arena[p][1] // 4, bool) for p in moments}
+    bar = TOL if mode == "exact" else 2e-2
+    f32 = lambda reader, name: _f64(reader, img, name).astype(np.float32)  # noqa: E731
+    first = {}
     for s in range(4):
+        before = {p: (f32(eng, p), f32(eng, m), f32(eng, v)) for p, (_, m, v) in moments.items()}
         t = pw.uniform_ints(7400 + s, T + 1, cfg["vocab"])
         eng.train_step(t[:T].copy().view(np.float32), t[1:].copy())
         twin.train_step(t[:T].copy().view(np.float32), t[1:].copy())
-    l2, mx = {}, {}
-    for name in img.arrays:
-        if ".A" in name or ".B" in name:
-            off, nb = img.arena[name]
-            g = np.frombuffer(eng.read(off, nb), np.float32).astype(np.float64)
-            c = np.frombuffer(twin.read(off, nb), np.float32).astype(np.float64)
-            l2[name] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
-            mx[name] = maxrel(g, c)
-    print(f"{which} adapters after 4 steps: L2 max {max(l2.values()):.2e}, "
-          f"per-element max-rel max {max(mx.values()):.2e}")
-    bad = {n: e for n, e in l2.items() if not e <= 2e-2}
-    assert not bad, bad
+        for p, (g, m, v) in moments.items():
+            ok, p1, m1, v1 = orc.adamw_step(before[p][0], f32(eng, g), before[p][1], before[p][2],
+                                            h["lr"], h["beta1"], h["beta2"], h["eps"],
+                                            h["weight_decay"], s + 1)
+            assert ok
+            assert p1.tobytes() == f32(eng, p).tobytes(), f"step {s + 1} {p}: not AdamW(g)"
+            assert m1.tobytes() == f32(eng, m).tobytes() and v1.tobytes() == f32(eng, v).tobytes()
+            gg, gc = _f64(eng, img, g), _f64(twin, img, g)
+            if s == 0:
+                first[p] = (maxrel(gg, gc), maxrel(_f64(eng, img, p), _f64(twin, img, p)))
+            flip = np.sign(gg) != np.sign(gc)
+            if mode != "exact":
+                assert np.all(np.abs(gc[flip]) <= bar * np.max(np.abs(gc))), \
+                    f"step {s + 1} {g}: a sign change above the noise floor"
+            flipped[p] |= flip
+    l2, mx, outside = {}, {}, 0
+    for p in moments:
+        g, c = _f64(eng, img, p), _f64(twin, img, p)
+        l2[p] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
+        mx[p] = maxrel(g, c)
+        out = np.abs(g - c) > bar * np.max(np.abs(c))
+        outside += int(out.sum())
+        if mode != "exact":
+            assert np.all(flipped[p][out]), f"{p}: an element outside the bar with no sign change"
+    print(f"{which} {mode}: step 1 gradients max-rel {max(e for e, _ in first.values()):.2e}, "
+          f"adapters {max(e for _, e in first.values()):.2e}; after 4 steps adapters L2 "
+          f"{max(l2.values()):.2e}, max-rel {max(mx.values()):.2e}, {outside} elements outside "
+          f"{bar:g}, {sum(int(f.sum()) for f in flipped.values())} gradient sign changes",
+          flush=True)
+    assert max(e for e, _ in first.values()) <= bar
+    assert max(l2.values()) <= bar
+    assert max(mx.values()) <= (1e-4 if mode == "exact" else 5e-2)
     eng.close()
 
 
 C4_WIDE = dict(vocab=32000, dim=768, heads=12, ffn=3072, layers=1, seq=1024, batch=1, rank=8)
 
 
-@pytest.mark.parametrize("relaxed", [False, True])
-def test_c4_width_slice_step_tensors_match_the_oracle(hip, orc, torch_cuda, relaxed):
+@pytest.mark.parametrize("mode", STEP_MODES)
+def test_c4_width_slice_step_tensors_match_the_oracle(hip, orc, torch_cuda, mode):
     """BASELINE configs[3] at its real widths -- d 768, 12 heads, FFN 3072,
     vocab 32000, S 1024 -- one block, one sequence: every arena tensor after
-    one step, per tensor, at the bars above (the oracle threaded; its bits
-    do not depend on the thread count)."""
+    one step, per tensor, at the bars above, in the three modes (the oracle
+    threaded; its bits do not depend on the thread count)."""
     import os
-    print(f"engine: C4-width slice {C4_WIDE}, relaxed={relaxed}", flush=True)
-    img = pw.decoder_lora(hip.plan_self_hash, relaxed=relaxed, **C4_WIDE)
-    eng, twin = hip.Engine(img.blob), OracleEngine(orc, img.blob)
-    eng.set_fusion(False)
-    _plant_b(img, eng, twin, 79)
+    print(f"engine: C4-width slice {C4_WIDE}, {mode}", flush=True)
+    img = pw.decoder_lora(hip.plan_self_hash, relaxed=mode != "exact", **C4_WIDE)
     t = pw.uniform_ints(7500, 1025, 32000)
-    x, y = t[:1024].copy(), t[1:].copy()
-    lg = eng.train_step(x.view(np.float32), y)
-    orc.set_threads(min(16, os.cpu_count() or 1))
-    try:
-        lc = twin.train_step(x.view(np.float32), y)
-    finally:
-        orc.set_threads(1)
-    errs = _step_tensor_errors(img, eng, twin)
-    worst = sorted(errs.items(), key=lambda kv: -kv[1])[:6]
-    print(f"C4 width relaxed={relaxed}: loss {lg} vs {lc}; worst " +
-          ", ".join(f"{n} {e:.2e}" for n, e in worst))
-    bar = 2e-2 if relaxed else TOL
-    assert abs(lg - lc) <= bar * abs(lc)
-    bad = {n: e for n, e in errs.items() if not e <= bar}
-    assert not bad, bad
-    eng.close()
+    _compare_step(hip, orc, img, mode, "c4-width", 79, (t[:1024].copy(), t[1:].copy()),
+                  threads=min(16, os.cpu_count() or 1))
+
+
+C5_WIDE = dict(vocab=32000, dim=2048, heads=32, ffn=5632, layers=1, seq=2048, batch=1, rank=16)
+
+
+@pytest.mark.parametrize("mode", STEP_MODES)
+def test_c5_width_slice_step_tensors_match_the_oracle(hip, orc, torch_cuda, mode):
+    """BASELINE configs[4] at its real widths -- d 2048, 32 heads, SiLU-gated
+    FFN 5632, RMSNorm, the frozen int8 base with per-column scales, LoRA r16
+    on Q / K / V / O, vocab 32000, S 2048 -- one block, one sequence (the
+    reference's q8 system test, update_system_test.cc:827, at model widths):
+    every arena tensor after one step, per tensor, at the bars above, in the
+    three modes, against the threaded oracle."""
+    import os
+    print(f"engine: C5-width slice {C5_WIDE}, {mode}", flush=True)
+    img = pw.decoder_q8_lora(hip.plan_self_hash, relaxed=mode != "exact", **C5_WIDE)
+    t = pw.uniform_ints(7600, 2049, 32000)
+    _compare_step(hip, orc, img, mode, "c5-width", 80, (t[:2048].copy(), t[1:].copy()),
+                  threads=min(16, os.cpu_count() or 1))
 
 
 # Producers that feed a relaxed direct-to-LDS product in one training step of
@@ -515,3 +640,33 @@ def test_conversions_fused_into_producers_are_bitwise_the_passes(hip, torch_cuda
     assert sinks[1] == 0
     assert curves[0].tobytes() == curves[1].tobytes()
     assert states[0] == states[1]
+
+
+def test_saved_attention_copies_under_a_cap_keep_the_bits(hip, torch_cuda):
+    """The forward's bf16 copies of q, k and v kept for the backward are a
+    cost, never a value: with the cap at zero (SEEAI_ATTN_SAVED_MB=0, no
+    triple saved, every backward converting again) three steps of the tiny
+    decoders on bf16 copies give the losses and persistent bytes of the
+    default, which saves one triple per layer."""
+    import os
+    for make, cfg in ((pw.decoder_lora, TINY), (pw.decoder_q8_lora, TINY_Q8)):
+        T = cfg["batch"] * cfg["seq"]
+        curves, states = [], []
+        for cap in (None, "0"):
+            img = make(hip.plan_self_hash, relaxed=True, **cfg)
+            if cap is not None:
+                os.environ["SEEAI_ATTN_SAVED_MB"] = cap
+            try:
+                eng = hip.Engine(img.blob)
+            finally:
+                os.environ.pop("SEEAI_ATTN_SAVED_MB", None)
+            eng.set_attention_bf16(True)
+            curve = []
+            for s in range(3):
+                t = pw.uniform_ints(7700 + s, T + 1, cfg["vocab"])
+                curve.append(eng.train_step(t[:T].copy().view(np.float32), t[1:].copy()))
+            curves.append(np.array(curve, np.float32))
+            states.append(eng.read(0, img.header["persistent_size"]))
+            eng.close()
+        assert curves[0].tobytes() == curves[1].tobytes()
+        assert states[0] == states[1]

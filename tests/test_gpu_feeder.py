@@ -89,6 +89,70 @@ def test_feeder_stops_at_a_refused_batch(hip, torch_cuda):
     ref.close()
 
 
+def test_accumulating_plan_through_the_feeder(hip, orc, torch_cuda):
+    """A plan that accumulates G = 2 micro-batches per optimizer step (the
+    reference's grad / step program split, optimizer.cc:22-108): the
+    pipelined steps are bitwise the serial ones and within 1e-5 of the
+    oracle twin; a refused micro-batch refuses its whole step before the
+    step's timestep is spent -- the engine is where the step before left it,
+    as TrainStep leaves it (update_engine.cc:840-870) -- and it trains on."""
+    from tests.engine_oracle import OracleEngine
+    print("feeder: config-1 plan with two micro-batches per step", flush=True)
+    img = pw.mlp_lora(hip.plan_self_hash, grad_accum=2)
+    n = img.header["persistent_size"]
+    batches = [c1_batch(s) for s in range(8)]
+    a, b = _serial_and_pipelined_accum(hip, img.blob, batches, n)
+    twin = OracleEngine(orc, img.blob)
+    for s in range(4):
+        xs = np.stack([batches[2 * s][0], batches[2 * s + 1][0]])
+        ys = np.stack([batches[2 * s][1], batches[2 * s + 1][1]])
+        twin.train_step(xs, ys)
+    g = np.frombuffer(a.read(0, n), np.float32).astype(np.float64)
+    c = np.frombuffer(twin.read(0, n), np.float32).astype(np.float64)
+    for name in ("A1", "B1", "A2", "B2"):
+        off, nb = img.arena[name]
+        sl = slice(off // 4, (off + nb) // 4)
+        e = float(np.max(np.abs(g[sl] - c[sl])) / np.max(np.abs(c[sl])))
+        assert e <= 1e-5, f"{name}: {e:.3g}"
+    a.close()
+    b.close()
+    # Micro-batch 1 of step 2 (batch 3) breaks the label contract.
+    bad_y = batches[3][1].copy()
+    bad_y[5] = 256
+    bad = list(batches)
+    bad[3] = (batches[3][0], bad_y)
+    eng, ref = hip.Engine(img.blob), hip.Engine(img.blob)
+    with pytest.raises(hip.BackendError, match="batch 3: label 256"):
+        eng.train_steps(np.stack([x for x, _ in bad]), np.stack([y for _, y in bad]))
+    ref.train_step(np.stack([batches[0][0], batches[1][0]]),
+                   np.stack([batches[0][1], batches[1][1]]))
+    assert eng.step == 1 == ref.step
+    assert eng.read(0, n) == ref.read(0, n)
+    with pytest.raises(hip.BackendError, match="label 256"):
+        ref.train_step(np.stack([batches[2][0], batches[3][0]]), np.stack([batches[2][1], bad_y]))
+    assert ref.step == 1 and eng.read(0, n) == ref.read(0, n)
+    xs = np.stack([batches[2][0], batches[3][0]])
+    ys = np.stack([batches[2][1], batches[3][1]])
+    assert eng.train_step(xs, ys) == ref.train_step(xs, ys)
+    assert eng.read(0, n) == ref.read(0, n)
+    eng.close()
+    ref.close()
+
+
+def _serial_and_pipelined_accum(hip, blob, batches, persistent):
+    """Serial TrainStep over pairs of micro-batches against TrainSteps over
+    the same batches in order: losses and persistent bytes equal."""
+    a, b = hip.Engine(blob), hip.Engine(blob)
+    xs, ys = zip(*batches)
+    serial = np.array([a.train_step(np.stack(xs[i:i + 2]), np.stack(ys[i:i + 2]))
+                       for i in range(0, len(batches), 2)], np.float32)
+    piped = b.train_steps(np.stack(xs), np.stack(ys))
+    assert a.step == b.step == len(batches) // 2
+    assert serial.tobytes() == piped.tobytes(), f"losses {serial} vs {piped}"
+    assert a.read(0, persistent) == b.read(0, persistent)
+    return a, b
+
+
 def test_device_feeder_holds_two_batches(hip, torch_cuda):
     """The C ABI's two staging slots: a third stage before a hand-over and a
     hand-over with nothing staged are refused; handed-over batches land in

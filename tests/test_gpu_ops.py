@@ -709,6 +709,82 @@ def test_attention_bf16_storage_backward(hip, orc, torch_cuda, B, S, H, seg):
     ctx.close()
 
 
+C3_GRID = (16, 2048, 16, 64)  # B, S, H, d
+
+
+@pytest.mark.parametrize("mode", ["f32", "relaxed", "bf16"])
+def test_attention_at_the_configs2_grid(hip, orc, torch_cuda, mode):
+    """BASELINE configs[2] at its full grid -- B16 H16 S2048 d64, Q, K, V,
+    dO ~ N(0,1), every (b, h) unit of the 256 in one launch per pass -- the
+    reference's check of attention at model shape (metal_backend_test.cc:875).
+    f32: the exact family (seeai_attn_* dtype 0); relaxed: the relaxed
+    family on f32 operands (dtype 1); bf16: operands held as bf16 in HBM.
+    Three (b, h) units -- the first, one between, the last -- against the
+    oracle's tiled family on that unit alone (its rows depend on nothing
+    else), O, dQ, dK, dV and the stats rows at 1e-5 (f32) or 2e-2; the
+    whole tensors finite; and row 0 of every sequence, which attends to
+    itself alone, gives O = V there (exactly; within bf16 rounding on the
+    relaxed family's bf16-rounded V)."""
+    torch = torch_cuda
+    B, S, H, d = C3_GRID
+    print(f"attention configs[2] grid {C3_GRID}, {mode}", flush=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2024)
+    shape = (B * S, H * d)
+    q, k, v, do = (torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+                   for _ in range(4))
+    if mode == "bf16":
+        q16, k16, v16, do16 = (t.to(torch.bfloat16) for t in (q, k, v, do))
+        q, k, v, do = (t.float() for t in (q16, k16, v16, do16))
+    nan = lambda sh: torch.full(sh, float("nan"), dtype=torch.float32, device="cuda")  # noqa: E731
+    o, st, dq, dk, dv = nan(shape), nan((B * H * S, 4)), nan(shape), nan(shape), nan(shape)
+    P = lambda t: t.data_ptr()  # noqa: E731
+    ctx = hip.Context(0)
+    ctx.use_torch_stream()
+    if mode == "bf16":
+        ctx.call("seeai_attn_fwd_bf16", P(q16), P(k16), P(v16), P(o), P(st), B, S, H, d, None)
+        ctx.call("seeai_attn_dq_bf16", P(q16), P(k16), P(v16), P(do16), P(st), P(dq), B, S, H, d)
+        ctx.call("seeai_attn_dkdv_bf16", P(q16), P(k16), P(v16), P(do16), P(st), P(dk), P(dv),
+                 B, S, H, d)
+    else:
+        dt = 0 if mode == "f32" else 1
+        ctx.call("seeai_attn_fwd", dt, P(q), P(k), P(v), P(o), P(st), B, S, H, d, None)
+        ctx.call("seeai_attn_dq", dt, P(q), P(k), P(v), P(do), P(st), P(dq), B, S, H, d)
+        if dt == 1:
+            ctx.call("seeai_attn_dkdv", P(q), P(k), P(v), P(do), P(st), P(dk), P(dv), B, S, H, d)
+        else:
+            ctx.call("seeai_attn_dk", dt, P(q), P(k), P(v), P(do), P(st), P(dk), B, S, H, d)
+            ctx.call("seeai_attn_dv", dt, P(q), P(k), P(do), P(st), P(dv), B, S, H, d)
+    torch.cuda.synchronize()
+    ctx.close()
+    for name, t in (("o", o), ("stats", st), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert bool(torch.isfinite(t).all()), f"{name}: not finite"
+    first = torch.arange(B, device="cuda") * S
+    o0, v0 = o[first], v[first]
+    if mode == "relaxed":
+        assert bool((torch.abs(o0 - v0) <= 2.0 ** -8 * torch.abs(v0)).all()), "row 0: O != V"
+    else:
+        assert torch.equal(o0, v0), "row 0: O != V"
+    tol = TOL if mode == "f32" else TOL_BF16
+    host = {n: t.cpu().numpy() for n, t in (("q", q), ("k", k), ("v", v), ("do", do),
+                                            ("o", o), ("dq", dq), ("dk", dk), ("dv", dv))}
+    stats = st.cpu().numpy().reshape(B, H, S, 4)
+    for b, h in [(0, 0), (7, 9), (B - 1, H - 1)]:
+        rows, cols = slice(b * S, (b + 1) * S), slice(h * d, (h + 1) * d)
+        uq, uk, uv, udo = (np.ascontiguousarray(host[n][rows, cols]) for n in ("q", "k", "v", "do"))
+        o_c, st_c = orc.attn_fwd_tiled(uq, uk, uv, 1, S, 1, d)
+        dq_c, st_c = orc.attn_dq_tiled(uq, uk, uv, udo, st_c, 1, S, 1, d)
+        want = {"o": o_c, "dq": dq_c, "dk": orc.attn_dk_tiled(uq, uk, uv, udo, st_c, 1, S, 1, d),
+                "dv": orc.attn_dv_tiled(uq, uk, udo, st_c, 1, S, 1, d)}
+        for name, w in want.items():
+            e = maxrel(host[name][rows, cols], w)
+            assert e <= tol, f"unit ({b},{h}) {name}: {e:.3g}"
+        for col in range(3):
+            e = maxrel(stats[b, h, :, col], st_c[:, col])
+            assert e <= tol, f"unit ({b},{h}) stats[{col}]: {e:.3g}"
+        assert np.all(stats[b, h, :, 3] == 0.0)
+
+
 @pytest.mark.parametrize("B,S,H,d,seg", [(2, 67, 2, 64, False), (1, 512, 2, 64, True),
                                          (2, 300, 2, 64, False)])
 @pytest.mark.parametrize("order", ["dk_dv", "dv_dk"])
@@ -783,6 +859,69 @@ def test_attention_backward_pair_refuses_to_fuse_over_a_reused_buffer(hip, orc, 
     assert ranged.tobytes() == apart.tobytes()
     e = maxrel(ar.get(ranged, "v"), ar.get(cpu, "v"))
     assert e <= TOL_BF16, f"dv over v: {e:.3g}"
+
+
+def _attn_copies_program(ar, r, B, S, H, d, case):
+    """Relaxed tiled attention (forward, dQ, dK, dV) in one range with
+    instructions that write its sources around the forward: the cases the
+    bf16 copies of q, k and v must notice."""
+    from tests.plan_ops import ins
+    shape = (B * S, H * d)
+    rq, rk, rv, rdo, rx, rx2 = (ar.add(n, r.standard_normal(shape).astype(np.float32))
+                                for n in ("q", "k", "v", "do", "x", "x2"))
+    o, st = ar.empty("o", shape), ar.empty("stats", (B * H * S, 4))
+    dq, dk, dv = ar.empty("dq", shape), ar.empty("dk", shape), ar.empty("dv", shape)
+    tab = ar.empty("table", (S, d // 2, 2))
+    geo = (B << 48) | (S << 32) | (H << 16) | d
+    bs, hd, base = (B << 32) | S, (H << 32) | d, f32_bits(10000.0)
+    fwd = ins(47, [rq, rk, rv, o], [st, bs, hd], flags=32)
+    bwd = [ins(48, [rq, rk, rv, rdo], [st, dq, geo], flags=32),
+           ins(49, [rq, rk, rv, rdo], [st, dk, geo], flags=32),
+           ins(50, [rq, rk, rv, rdo], [st, dv, geo], flags=32)]
+    table = ins(45, [tab], [(S << 32) | d, base])
+    rope_q = ins(33, [rx, rq, tab], [bs, hd, base])
+    rope_k = ins(33, [rx2, rk, tab], [bs, hd, base])
+    if case == "copy_into_q":  # q rewritten between the forward and the backward
+        return [fwd, ins(20, [rx, rq], [B * S * H * d])] + bwd
+    if case == "rope_into_k":  # k rewritten by a RoPE forward there
+        return [table, fwd, ins(33, [rx2, rk, tab], [bs, hd, base])] + bwd
+    if case == "rope_then_write_y":  # the RoPE output rewritten before the forward reads it
+        return [table, rope_q, ins(20, [rx2, rq], [B * S * H * d]), fwd] + bwd
+    assert case == "rope_feeds_the_copies"  # the RoPE forwards write the forward's copies
+    return [table, rope_q, rope_k, fwd] + bwd
+
+
+@pytest.mark.parametrize("case", ["copy_into_q", "rope_into_k", "rope_then_write_y",
+                                  "rope_feeds_the_copies"])
+def test_attention_copies_follow_sources_written_in_the_range(hip, orc, backend, bf16_attention,
+                                                              case):
+    """With attention on bf16 copies, the forward's copies of q, k and v
+    serve the backward of the same range run only while no instruction since
+    has written a source, and a RoPE forward writes its output's copy for the
+    attention only when nothing between writes that output.  A source
+    rewritten after the forward (a kCopy into q, a RoPE forward into k), or
+    the RoPE output rewritten before the forward reads it, must make the
+    range convert again: the ranged run is bitwise the instructions run one
+    by one (each its own range, so every operand converted afresh), within
+    the relaxed bar of the oracle, and counts each relaxed instruction once."""
+    B, S, H, d = 2, 200, 2, 64
+    r = rng(hash(case) % 1000)
+    ar = Arena()
+    prog = _attn_copies_program(ar, r, B, S, H, d, case)
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    relaxed_before = backend.relaxed_executions()
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    n_relaxed = sum(1 for w in prog if struct.unpack_from("<H", w, 2)[0] & 32)
+    assert backend.relaxed_executions() - relaxed_before == n_relaxed
+    for name in ["o", "stats", "dq", "dk", "dv", "q", "k"]:
+        assert bits_equal(ar.get(ranged, name), ar.get(apart, name)), name
+    for name in ["o", "dq", "dk", "dv"]:
+        e = maxrel(ar.get(ranged, name), ar.get(cpu, name))
+        assert e <= TOL_BF16, f"{name}: {e:.3g}"
 
 
 def _lora_site_program(ar, r, kind, M, Din, Dout, rank, t_over_c0=False):

@@ -256,3 +256,31 @@ def test_argmax_tally_skips_unlabelled_rows(orc):
     keep = labels >= 0
     assert judged == int(keep.sum())
     assert hits == int((np.argmax(probs, axis=1)[keep] == labels[keep]).sum())
+
+
+def test_accumulating_plan_steps_as_the_single_batch_plan(orc):
+    """Gradient accumulation (optimizer.cc:22-108): with G = 2 micro-batches
+    that are the same batch, the seed 1/2 halves every gradient exactly (a
+    power of two through linear kernels), the accumulator folds the two
+    halves back to the whole gradient, and the step program's AdamW then
+    moves the adapters exactly as the single-batch plan's does: the
+    persistent parameters and moments bitwise, the loss the same."""
+    import importlib
+    hip = importlib.import_module("see-ai_amd.hip")
+    one = pw.mlp_lora(hip.plan_self_hash)
+    two = pw.mlp_lora(hip.plan_self_hash, grad_accum=2)
+    assert hip.plan_check(two.blob) == ""
+    assert two.header["grad_accum_steps"] == 2 and two.header["step_instr_count"] == 8
+    e1, e2 = OracleEngine(orc, one.blob), OracleEngine(orc, two.blob)
+    for step in range(3):
+        x, y = pw.normal(60 + step, (32, 256)), pw.uniform_ints(70 + step, 32, 256)
+        l1 = e1.train_step(x, y)
+        l2 = e2.train_step(np.stack([x, x]), np.stack([y, y]))
+        assert np.float32(l1) == np.float32(l2)
+    for name in ("A1", "B1", "A2", "B2"):
+        for prefix in ("", "m_", "v_"):
+            off1, nb = one.arena[prefix + name]
+            off2, _ = two.arena[prefix + name]
+            assert e1.read(off1, nb) == e2.read(off2, nb), prefix + name
+        off, nb = two.arena["acc_" + name]
+        assert not np.any(np.frombuffer(e2.read(off, nb), np.float32)), "accumulator zeroed"
