@@ -135,9 +135,9 @@ def pmc_probe():
 
 def attention_step(ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d, parts=None):
     """One causal attention fwd + bwd as a plan runs it: forward, dQ, then
-    dK and dV -- one fused pass in the relaxed family (an adjacent dK / dV
-    pair fuses in a range), two passes in the exact family.  `parts` picks a
-    subset ("fwd", "dq", "dkdv") for per-kernel timing."""
+    dK and dV as one fused pass (an adjacent dK / dV pair fuses in a range,
+    in the relaxed and the exact family).  `parts` picks a subset ("fwd",
+    "dq", "dkdv") for per-kernel timing."""
     P = lambda t: t.data_ptr()
     parts = parts or ("fwd", "dq", "dkdv")
     if "fwd" in parts:
@@ -145,11 +145,8 @@ def attention_step(ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d, parts=No
     if "dq" in parts:
         ctx.call("seeai_attn_dq", dt, P(q), P(k), P(v), P(do), P(st), P(dq), B, S, H, d)
     if "dkdv" in parts:
-        if dt:
-            ctx.call("seeai_attn_dkdv", P(q), P(k), P(v), P(do), P(st), P(dk), P(dv), B, S, H, d)
-        else:
-            ctx.call("seeai_attn_dk", dt, P(q), P(k), P(v), P(do), P(st), P(dk), B, S, H, d)
-            ctx.call("seeai_attn_dv", dt, P(q), P(k), P(do), P(st), P(dv), B, S, H, d)
+        ctx.call("seeai_attn_dkdv" if dt else "seeai_attn_dkdv_f32", P(q), P(k), P(v), P(do),
+                 P(st), P(dk), P(dv), B, S, H, d)
 
 
 def attention_step_bf16(ctx, q, k, v, do, o, st, dq, dk, dv, B, S, H, d, parts=None):
@@ -468,15 +465,14 @@ def extras(ctx, torch, hip):
     # staging), and the exact family
     for dt, name in [(1, "attention_bf16_f32_operands"), (0, "attention_f32")]:
         args_ = (ctx, dt, q, k, v, do, o, st, dq, dk, dv, B, S, H, d)
-        ms = timed(lambda: attention_step(*args_), 3 if dt else 1, 1)
+        ms = timed(lambda: attention_step(*args_), 3, 1)
         tf = flops / ms / 1e9
         peak = PEAK_BF16_TFLOPS if dt else PEAK_FP32_TFLOPS
         out[name] = {"ms_fwd_bwd": round(ms, 3), "TFLOP_s": round(tf, 1),
                      "mfma_frac": round(tf / peak, 4), "config": "B16 H16 S2048 d64 causal"}
-        if dt:
-            out[name]["ms_parts"] = {
-                part: round(timed(lambda part=part: attention_step(*args_, parts=(part,)), 5, 1), 4)
-                for part in ("fwd", "dq", "dkdv")}
+        out[name]["ms_parts"] = {
+            part: round(timed(lambda part=part: attention_step(*args_, parts=(part,)), 3, 1), 4)
+            for part in ("fwd", "dq", "dkdv")}
     del q, k, v, do, o, st, dq, dk, dv
 
     # Softmax cross-entropy fwd at the decoders' 8192 x 32000 logits.

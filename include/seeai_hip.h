@@ -302,6 +302,14 @@ int seeai_attn_dkdv(seeai_ctx* ctx, const float* d_q, const float* d_k,
                     const float* d_v, const float* d_dout,
                     const float* d_stats, float* d_dk, float* d_dv,
                     uint64_t B, uint64_t S, uint64_t H, uint64_t d);
+/* AttnDKTiled + AttnDVTiled (attention.cc:537-590) in one exact-family pass
+ * (f32 MFMA): what an adjacent exact pair runs in a range, each output the
+ * bits of its own pass (seeai_attn_dk / seeai_attn_dv).  d = 64 or 128,
+ * 16-byte aligned operands, both outputs; status 2 otherwise. */
+int seeai_attn_dkdv_f32(seeai_ctx* ctx, const float* d_q, const float* d_k,
+                        const float* d_v, const float* d_dout,
+                        const float* d_stats, float* d_dk, float* d_dv,
+                        uint64_t B, uint64_t S, uint64_t H, uint64_t d);
 
 /* SoftmaxXEntFwd / Bwd and the masked pair (loss.cc:35-126). */
 int seeai_xent_fwd(seeai_ctx* ctx, const float* d_logits,

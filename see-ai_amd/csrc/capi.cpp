@@ -641,15 +641,18 @@ int Attn16BwdOperands(seeai_ctx* c, const float* const src[4], uint64_t rows, ui
 }
 
 int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
-  if (!c->allow_fusion || !c->allow_relaxed || !c->attn_bf16 || !c->prog || at < c->prog ||
-      at >= c->prog + c->prog_count * 64 || (at - c->prog) % 64 != 0)
+  if (!c->allow_fusion || !c->prog || at < c->prog || at >= c->prog + c->prog_count * 64 ||
+      (at - c->prog) % 64 != 0)
     return -1;
   const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
   if (idx + 1 >= c->range_end) return -1;
   Instruction nx;
   std::memcpy(&nx, at + 64, sizeof nx);
   if (ins.opcode + nx.opcode != 49 + 50 || (ins.opcode != 49 && ins.opcode != 50)) return -1;
-  if (!(ins.flags & kFlagRelaxed) || !(nx.flags & kFlagRelaxed)) return -1;
+  // Both on the relaxed bf16 kernels, or both in the exact family (which
+  // relaxed instructions run when attention is not on bf16).
+  const bool relaxed = IsRelaxedAttention(c, ins);
+  if (relaxed != IsRelaxedAttention(c, nx)) return -1;
   if (ins.in[0] != nx.in[0] || ins.in[1] != nx.in[1] || ins.in[3] != nx.in[3] ||
       ins.out[0] != nx.out[0] || ins.out[2] != nx.out[2])
     return -1;
@@ -661,7 +664,9 @@ int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   const float *q = R.f(dki.in[0]), *k = R.f(dki.in[1]), *v = R.f(dki.in[2]), *dout = R.f(dki.in[3]);
   const float* stats = R.f(dki.out[0]);
   float *dk = R.f(dki.out[1]), *dv = R.f(dvi.out[1]);
-  if (!AttnDKDVFusable(q, k, v, dout, dk, dv, B, S, H, d)) return -1;
+  if (relaxed ? !AttnDKDVFusable(q, k, v, dout, dk, dv, B, S, H, d)
+              : !AttnDKDVExactFusable(q, k, v, dout, stats, dk, dv, B, S, H, d))
+    return -1;
   const uint64_t act = B * S * H * d * 4, st = B * H * S * 16;
   const auto* o1 = reinterpret_cast<const uint8_t*>(dk);
   const auto* o2 = reinterpret_cast<const uint8_t*>(dv);
@@ -673,7 +678,10 @@ int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
     if (Overlap(o, act, reinterpret_cast<const uint8_t*>(stats), st)) return -1;
   RelaxedAttention(c, ins);
   RelaxedAttention(c, nx);
-  if (Attn16Plan(c, B, S, H, d)) {
+  if (!relaxed) {
+    SEEAI_TRY(c, LaunchAttnDKDVExact(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
+              "attn.dkdv_exact");
+  } else if (Attn16Plan(c, B, S, H, d)) {
     const float* src[4] = {q, k, v, dout};
     uint16_t* b16[4];
     if (int rc = Attn16BwdOperands(c, src, B * S, H * d, b16)) return rc;
@@ -2574,6 +2582,17 @@ int seeai_attn_dv(seeai_ctx* c, int dtype, const float* q, const float* k, const
                   const float* stats, float* dv, uint64_t B, uint64_t S, uint64_t H, uint64_t d) {
   if (!c || dtype < 0 || dtype > 1) return Fail(c, SEEAI_INVALID, "attn_dv: dtype is 0 or 1");
   SEEAI_TRY(c, LaunchAttnDVTiled(dtype, q, k, dout, stats, dv, B, S, H, d, c->stream), "attn_dv");
+  return SEEAI_OK;
+}
+int seeai_attn_dkdv_f32(seeai_ctx* c, const float* q, const float* k, const float* v,
+                        const float* dout, const float* stats, float* dk, float* dv, uint64_t B,
+                        uint64_t S, uint64_t H, uint64_t d) {
+  if (!c) return SEEAI_INVALID;
+  if (!dk || !dv || !AttnDKDVExactFusable(q, k, v, dout, stats, dk, dv, B, S, H, d))
+    return Fail(c, SEEAI_INVALID, "attn_dkdv_f32: the exact pass takes d = 64 or 128 with "
+                                  "16-byte aligned operands and both outputs");
+  SEEAI_TRY(c, LaunchAttnDKDVExact(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
+            "attn_dkdv_f32");
   return SEEAI_OK;
 }
 

@@ -404,6 +404,28 @@ hipError_t LaunchAttnDKTiled(int dtype, const float* q, const float* k, const fl
 hipError_t LaunchAttnDVTiled(int dtype, const float* q, const float* k, const float* dout,
                              const float* stats, float* dv, size_t B, size_t S, size_t H,
                              size_t d, hipStream_t s);
+// The exact family on f32 operands for head widths 64 and 128, staged
+// through LDS (k_attn32.hip).  In LaunchAttn32DKDV one or both of dk, dv are
+// non-null; each output has the same bits either way.
+bool Attn32Fits(size_t B, size_t S, size_t H, size_t d, std::initializer_list<const void*> ptrs);
+hipError_t LaunchAttn32Fwd(const float* q, const float* k, const float* v, float* o, float* stats,
+                           size_t B, size_t S, size_t H, size_t d, const int32_t* starts,
+                           hipStream_t s);
+hipError_t LaunchAttn32DQ(const float* q, const float* k, const float* v, const float* dout,
+                          float* stats, float* dq, size_t B, size_t S, size_t H, size_t d,
+                          hipStream_t s);
+hipError_t LaunchAttn32DKDV(const float* q, const float* k, const float* v, const float* dout,
+                            const float* stats, float* dk, float* dv, size_t B, size_t S, size_t H,
+                            size_t d, hipStream_t s);
+// dK and dV of the exact family in one pass (k_attention.hip): Fusable says
+// whether the pass takes the shape; otherwise Launch returns
+// hipErrorNotSupported and launches nothing.
+bool AttnDKDVExactFusable(const float* q, const float* k, const float* v, const float* dout,
+                          const float* stats, const float* dk, const float* dv, size_t B, size_t S,
+                          size_t H, size_t d);
+hipError_t LaunchAttnDKDVExact(const float* q, const float* k, const float* v, const float* dout,
+                               const float* stats, float* dk, float* dv, size_t B, size_t S,
+                               size_t H, size_t d, hipStream_t s);
 // dK and dV in one pass (relaxed family; k_attention.hip).  Fusable says
 // whether the fused launch takes the shape; otherwise it returns
 // hipErrorNotSupported and launches nothing.

@@ -121,6 +121,7 @@ EXPORTS = {
     "seeai_attn_dk": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
     "seeai_attn_dv": (_I, [_P, _I, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
     "seeai_attn_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
+    "seeai_attn_dkdv_f32": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _U64]),
     "seeai_xent_fwd": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _I]),
     "seeai_xent_fwd_noalloc": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _I]),
     "seeai_xent_bwd": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _I]),

@@ -755,6 +755,13 @@ def test_attention_at_the_configs2_grid(hip, orc, torch_cuda, mode):
         else:
             ctx.call("seeai_attn_dk", dt, P(q), P(k), P(v), P(do), P(st), P(dk), B, S, H, d)
             ctx.call("seeai_attn_dv", dt, P(q), P(k), P(do), P(st), P(dv), B, S, H, d)
+            dk2, dv2 = nan(shape), nan(shape)
+            ctx.call("seeai_attn_dkdv_f32", P(q), P(k), P(v), P(do), P(st), P(dk2), P(dv2),
+                     B, S, H, d)
+            torch.cuda.synchronize()
+            assert torch.equal(dk.view(torch.int32), dk2.view(torch.int32)), "fused dK"
+            assert torch.equal(dv.view(torch.int32), dv2.view(torch.int32)), "fused dV"
+            del dk2, dv2
     torch.cuda.synchronize()
     ctx.close()
     for name, t in (("o", o), ("stats", st), ("dq", dq), ("dk", dk), ("dv", dv)):
@@ -786,14 +793,26 @@ def test_attention_at_the_configs2_grid(hip, orc, torch_cuda, mode):
 
 
 @pytest.mark.parametrize("B,S,H,d,seg", [(2, 67, 2, 64, False), (1, 512, 2, 64, True),
-                                         (2, 300, 2, 64, False)])
+                                         (2, 300, 2, 64, False), (1, 200, 2, 128, True)])
 @pytest.mark.parametrize("order", ["dk_dv", "dv_dk"])
-def test_attention_backward_pair_fuses_bitwise(hip, orc, backend, bf16_attention, B, S, H, d, seg,
-                                               order):
-    """Adjacent relaxed kAttnDKTiled / kAttnDVTiled of one attention run as
-    one pass on the bf16 kernels when a range shows the backend the program
-    (ExecuteRange): the arena bytes are those of the two instructions run
-    one by one, and the pass is counted as a fused dispatch."""
+@pytest.mark.parametrize("family", ["bf16", "exact"])
+def test_attention_backward_pair_fuses_bitwise(hip, orc, backend, B, S, H, d, seg, order, family):
+    """Adjacent kAttnDKTiled / kAttnDVTiled of one attention run as one pass
+    when a range shows the backend the program (ExecuteRange) -- relaxed on
+    the bf16 kernels, or exact (no flag) on the f32 kernels: the arena bytes
+    are those of the two instructions run one by one, and the pass is
+    counted as a fused dispatch."""
+    from tests.plan_ops import ins
+    if family == "bf16" and d != 64:
+        pytest.skip("the relaxed pair fuses at head width 64")
+    backend.SetAttentionBf16(family == "bf16")
+    try:
+        _attention_pair(hip, orc, backend, B, S, H, d, seg, order, 32 if family == "bf16" else 0)
+    finally:
+        backend.SetAttentionBf16(False)
+
+
+def _attention_pair(hip, orc, backend, B, S, H, d, seg, order, flags):
     from tests.plan_ops import ins
     r = rng(B * 7 + S + d)
     shape = (B * S, H * d)
@@ -806,12 +825,12 @@ def test_attention_backward_pair_fuses_bitwise(hip, orc, backend, bf16_attention
     prog = []
     if seg:
         rt, rs = ar.add("toks", r.integers(0, 4, B * S).astype(np.int32)), ar.empty("starts", (B * S,), np.int32)
-        prog += [ins(55, [rt, rs], [(B << 32) | S, 3]), ins(57, [rq, rk, rv, o], [st, geo, rs], flags=32)]
+        prog += [ins(55, [rt, rs], [(B << 32) | S, 3]), ins(57, [rq, rk, rv, o], [st, geo, rs], flags=flags)]
     else:
-        prog.append(ins(47, [rq, rk, rv, o], [st, (B << 32) | S, (H << 32) | d], flags=32))
-    pair = [ins(49, [rq, rk, rv, rdo], [st, dk, geo], flags=32),
-            ins(50, [rq, rk, rv, rdo], [st, dv, geo], flags=32)]
-    prog += [ins(48, [rq, rk, rv, rdo], [st, dq, geo], flags=32)] + (
+        prog.append(ins(47, [rq, rk, rv, o], [st, (B << 32) | S, (H << 32) | d], flags=flags))
+    pair = [ins(49, [rq, rk, rv, rdo], [st, dk, geo], flags=flags),
+            ins(50, [rq, rk, rv, rdo], [st, dv, geo], flags=flags)]
+    prog += [ins(48, [rq, rk, rv, rdo], [st, dq, geo], flags=flags)] + (
         pair if order == "dk_dv" else pair[::-1])
     cpu, apart = execute(hip, orc, backend, ar, prog)
     before = backend.fused_dispatches()
@@ -822,12 +841,13 @@ def test_attention_backward_pair_fuses_bitwise(hip, orc, backend, bf16_attention
     backend.Flush()
     fused = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
     assert backend.fused_dispatches() - before == 1
-    assert backend.relaxed_executions() - relaxed_before == len(prog) - (1 if seg else 0)
+    n_relaxed = len(prog) - (1 if seg else 0) if flags else 0
+    assert backend.relaxed_executions() - relaxed_before == n_relaxed
     for name in ["dk", "dv", "dq", "o", "stats"]:
         assert bits_equal(ar.get(fused, name), ar.get(apart, name)), name
     for name in ["dk", "dv"]:
         e = maxrel(ar.get(fused, name), ar.get(cpu, name))
-        assert e <= TOL_BF16, f"{name}: {e:.3g}"
+        assert e <= (TOL_BF16 if flags else TOL), f"{name}: {e:.3g}"
 
 
 def test_attention_backward_pair_refuses_to_fuse_over_a_reused_buffer(hip, orc, backend,
