@@ -336,9 +336,11 @@ def cpu_model():
 
 def cpu_baseline(M, N, K):
     """The reported CPU baseline: the oracle (the repository's C restatement
-    of the reference executor, bit-matched to it) on this host.  The W8A8
-    step (quantize + int32 GEMM + dequant) on a row sample at all threads
-    and at one; the config-1 train step; a config-3 slice at full widths.
+    of the reference executor, bit-matched to it) on this host, for all five
+    configs: the W8A8 step (quantize + int32 GEMM + dequant, configs[1]) on
+    a row sample; the config-1 train step; one-block slices of configs[3]
+    and configs[4] at full widths; configs[2]'s attention on sampled (b, h)
+    units -- each at all threads and at one, on the same workload.
     Each measurement is a median of repeats after a warm-up.  The oracle's
     chunks are the reference's ParallelFor chunks, so every thread count
     computes the same bits."""
@@ -348,8 +350,9 @@ def cpu_baseline(M, N, K):
     threads = host_threads()
     r = np.random.default_rng(1)
 
-    def median_s(fn, reps):
-        fn()  # warm
+    def median_s(fn, reps, warm=True):
+        if warm:
+            fn()
         ts = []
         for _ in range(reps):
             t0 = time.perf_counter()
@@ -392,22 +395,55 @@ def cpu_baseline(M, N, K):
         dt = median_s(lambda: eng.train_step(x, y), 5)
         steps[f"c1_{th}t"] = {"ms_per_step": round(dt * 1e3, 3), "rows_s": round(32 / dt, 1),
                               "threads": th}
-    # configs[3] at full widths, one block and one sequence (the whole step
-    # is 12 blocks x 8 sequences of 1024): tokens/s of the slice, all threads
-    # at S 1024, one thread at S 256.
-    for th, seq, reps in ((threads, 1024, 2), (1, 256, 1)):
-        cfg = dict(vocab=32000, dim=768, heads=12, ffn=3072, layers=1, seq=seq, batch=1, rank=8)
-        img = pw.decoder_lora(hip.plan_self_hash, relaxed=False, **cfg)
+    # configs[3] and configs[4] at full widths, one block and one sequence
+    # (the whole steps are 12 blocks x 8 sequences of 1024 and 16 blocks x 4
+    # sequences of 2048): tokens/s of the slice, all threads and one thread
+    # on the same slice.
+    slices = [("c4_slice", pw.decoder_lora,
+               dict(vocab=32000, dim=768, heads=12, ffn=3072, layers=1, seq=512, batch=1, rank=8),
+               "configs[3] widths (d768, 12 heads, FFN 3072, vocab 32000), 1 block"),
+              ("c5_slice", pw.decoder_q8_lora,
+               dict(vocab=32000, dim=2048, heads=32, ffn=5632, layers=1, seq=128, batch=1,
+                    rank=16),
+               "configs[4] widths (d2048, 32 heads, SiLU-gated FFN 5632, int8 base, vocab "
+               "32000), 1 block")]
+    for key, make, cfg, what in slices:
+        seq = cfg["seq"]
+        img = make(hip.plan_self_hash, relaxed=False, **cfg)
         t = pw.uniform_ints(9, seq + 1, 32000)
         xb, yb = t[:seq].copy().view(np.float32), t[1:].copy()
+        for th in (threads, 1):
+            orc.set_threads(th)
+            eng = OracleEngine(orc, img.blob)
+            # the one-thread run follows the warm all-threads one on the same plan
+            dt = median_s(lambda: eng.train_step(xb, yb), 2 if th > 1 else 1, warm=th > 1)
+            steps[f"{key}_{th}t"] = {"s_per_step": round(dt, 3), "tokens_s": round(seq / dt, 1),
+                                     "threads": th,
+                                     "sample": f"{what}, B1 x S{seq}, exact family"}
+            del eng
+        del img
+    # causal attention fwd + bwd (the tiled family: forward, dQ,
+    # dK, dV) on (b, h) units of the B16 H16 S2048 d64 grid -- every unit is
+    # the same work -- scaled to the 256 units of the grid.
+    S2, d2 = 2048, 64
+    att = {}
+    for th, units in ((threads, 4), (1, 1)):
         orc.set_threads(th)
-        eng = OracleEngine(orc, img.blob)
-        dt = median_s(lambda: eng.train_step(xb, yb), reps)
-        steps[f"c4_slice_{th}t"] = {
-            "s_per_step": round(dt, 3), "tokens_s": round(seq / dt, 1), "threads": th,
-            "sample": f"configs[3] widths (d768, 12 heads, FFN 3072, vocab 32000), 1 block, "
-                      f"B1 x S{seq}, exact family"}
-        del eng, img
+        q2, k2, v2, do2 = (r.standard_normal((S2, units * d2)).astype(np.float32)
+                           for _ in range(4))
+
+        def attn_step():
+            _, st = orc.attn_fwd_tiled(q2, k2, v2, 1, S2, units, d2)
+            _, st = orc.attn_dq_tiled(q2, k2, v2, do2, st, 1, S2, units, d2)
+            orc.attn_dk_tiled(q2, k2, v2, do2, st, 1, S2, units, d2)
+            orc.attn_dv_tiled(q2, k2, do2, st, 1, S2, units, d2)
+        dt = median_s(attn_step, 1, warm=th > 1) * 256 / units
+        att[th] = {"ms_fwd_bwd": round(dt * 1e3, 1), "TFLOP_s": round(412518187008 / dt / 1e12, 5),
+                   "threads": th,
+                   "sample": f"{units} of the 256 (b, h) units of B16 H16 S2048 d64, scaled x "
+                             f"{256 // units}"}
+    steps["attention_c3_all_threads"] = att[threads]
+    steps["attention_c3_1t"] = att[1]
     orc.set_threads(1)
     orc.pool_stop()  # the host threads end here, before the GPU extras
     out["train_steps"] = steps

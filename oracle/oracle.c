@@ -66,8 +66,6 @@ typedef struct {
   void* ctx;
   size_t n, grain, count;
   size_t next;   /* the next chunk to take */
-  int seats;     /* pool workers that may join this job */
-  int joined;    /* pool workers that tried to */
 } OrcWork;
 
 static void orc_run_chunks(OrcWork* w) {
@@ -80,37 +78,40 @@ static void orc_run_chunks(OrcWork* w) {
   }
 }
 
-/* A persistent pool (the reference keeps one too, parallel_for.h): workers
- * sleep on `go`, each job is published with a generation number, and the
- * caller works beside them and waits on `done` until every worker that
- * woke for the job has left it. */
+/* A persistent pool (the reference keeps one too, parallel_for.h): worker i
+ * sleeps until its own generation word moves, so a job wakes exactly the
+ * workers it seats (seats < workers leaves the rest asleep); the caller works
+ * beside them and waits on `done` until every seated worker has left the
+ * job. */
+enum { kMaxWorkers = 255 };
 static struct {
   pthread_mutex_t mu;
-  pthread_cond_t go, done;
+  pthread_cond_t done;
+  pthread_cond_t go[kMaxWorkers];
+  unsigned long gen[kMaxWorkers]; /* worker i's job generation */
   int workers;
-  unsigned long gen;
   OrcWork* job;
-  int busy; /* workers still inside the current job */
-  int quit; /* set by orc_pool_stop: the next generation ends the workers */
-} g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER,
-            0, 0, NULL, 0, 0};
+  int busy; /* seated workers still inside the current job */
+  int quit; /* set by orc_pool_stop: the next wake ends the worker */
+} g_pool = {.mu = PTHREAD_MUTEX_INITIALIZER, .done = PTHREAD_COND_INITIALIZER};
 
-/* arg: the generation current when the worker was created; the job
- * published right after it (generation + 1) is its first. */
+/* Worker i starts at generation 0 (its creator zeroed gen[i] and seats it
+ * in the job being published, which moves gen[i] to 1). */
 static void* orc_pool_worker(void* arg) {
-  unsigned long seen = (unsigned long)(uintptr_t)arg;
+  const int i = (int)(uintptr_t)arg;
+  unsigned long seen = 0;
   pthread_mutex_lock(&g_pool.mu);
   for (;;) {
-    while (g_pool.gen == seen) pthread_cond_wait(&g_pool.go, &g_pool.mu);
-    seen = g_pool.gen;
+    while (g_pool.gen[i] == seen) pthread_cond_wait(&g_pool.go[i], &g_pool.mu);
+    seen = g_pool.gen[i];
     if (g_pool.quit) {
-      if (--g_pool.workers == 0) pthread_cond_signal(&g_pool.done);
+      if (--g_pool.busy == 0) pthread_cond_signal(&g_pool.done);
       pthread_mutex_unlock(&g_pool.mu);
       return NULL;
     }
     OrcWork* w = g_pool.job;
     pthread_mutex_unlock(&g_pool.mu);
-    if (__atomic_fetch_add(&w->joined, 1, __ATOMIC_RELAXED) < w->seats) orc_run_chunks(w);
+    orc_run_chunks(w);
     pthread_mutex_lock(&g_pool.mu);
     if (--g_pool.busy == 0) pthread_cond_signal(&g_pool.done);
   }
@@ -119,35 +120,55 @@ static void* orc_pool_worker(void* arg) {
 
 /* Runs fn over [0, n) in chunks of orc_chunk_grain(n, grain) on the caller
  * and up to orc_threads() - 1 pool workers; returns the chunk count.  Not
- * reentrant: one job at a time (the oracle runs one instruction at a time). */
-static size_t orc_parallel(size_t n, size_t grain, orc_chunk_fn fn, void* ctx) {
+ * reentrant: one job at a time (the oracle runs one instruction at a time).
+ * `unit_cost` (operations per unit, 0 = unknown) caps the threads at one
+ * per kThreadWork operations, so a small job stays on the calling thread as
+ * the reference's small tensors do (kernel_policy.h:36-40: grains chosen so
+ * small tensors never leave the calling thread); the chunks, and so the
+ * bits, do not depend on it. */
+enum { kThreadWork = 1 << 22 };
+static size_t orc_parallel_cost(size_t n, size_t grain, size_t unit_cost, orc_chunk_fn fn,
+                                void* ctx) {
   if (n == 0) return 0;
-  OrcWork w = {fn, ctx, n, orc_chunk_grain(n, grain), 0, 0, 0, 0};
+  OrcWork w = {fn, ctx, n, orc_chunk_grain(n, grain), 0, 0};
   w.count = (n + w.grain - 1) / w.grain;
   int t = orc_threads();
   if ((size_t)t > w.count) t = (int)w.count;
+  if (unit_cost > 0) {
+    const double work = (double)n * (double)unit_cost;
+    const double cap = work / kThreadWork;
+    if (cap < (double)t) t = cap < 1.0 ? 1 : (int)cap;
+  }
   if (t <= 1) {
     orc_run_chunks(&w);
     return w.count;
   }
   pthread_mutex_lock(&g_pool.mu);
-  while (g_pool.workers < t - 1 && g_pool.workers < 255) {
+  while (g_pool.workers < t - 1 && g_pool.workers < kMaxWorkers) {
+    const int i = g_pool.workers;
+    pthread_cond_init(&g_pool.go[i], NULL);
+    g_pool.gen[i] = 0;
     pthread_t id;
-    if (pthread_create(&id, NULL, orc_pool_worker, (void*)(uintptr_t)g_pool.gen) != 0) break;
+    if (pthread_create(&id, NULL, orc_pool_worker, (void*)(uintptr_t)i) != 0) break;
     pthread_detach(id);
     ++g_pool.workers;
   }
-  w.seats = t - 1;
+  const int seats = t - 1 < g_pool.workers ? t - 1 : g_pool.workers;
   g_pool.job = &w;
-  g_pool.busy = g_pool.workers;
-  ++g_pool.gen;
-  pthread_cond_broadcast(&g_pool.go);
+  g_pool.busy = seats;
+  for (int i = 0; i < seats; ++i) {
+    ++g_pool.gen[i];
+    pthread_cond_signal(&g_pool.go[i]);
+  }
   pthread_mutex_unlock(&g_pool.mu);
   orc_run_chunks(&w);
   pthread_mutex_lock(&g_pool.mu);
   while (g_pool.busy > 0) pthread_cond_wait(&g_pool.done, &g_pool.mu);
   pthread_mutex_unlock(&g_pool.mu);
   return w.count;
+}
+static size_t orc_parallel(size_t n, size_t grain, orc_chunk_fn fn, void* ctx) {
+  return orc_parallel_cost(n, grain, 0, fn, ctx);
 }
 
 /* Ends every pool worker and waits until each has left its loop; the next
@@ -156,9 +177,14 @@ void orc_pool_stop(void) {
   pthread_mutex_lock(&g_pool.mu);
   if (g_pool.workers > 0) {
     g_pool.quit = 1;
-    ++g_pool.gen;
-    pthread_cond_broadcast(&g_pool.go);
-    while (g_pool.workers > 0) pthread_cond_wait(&g_pool.done, &g_pool.mu);
+    g_pool.busy = g_pool.workers;
+    for (int i = 0; i < g_pool.workers; ++i) {
+      ++g_pool.gen[i];
+      pthread_cond_signal(&g_pool.go[i]);
+    }
+    while (g_pool.busy > 0) pthread_cond_wait(&g_pool.done, &g_pool.mu);
+    for (int i = 0; i < g_pool.workers; ++i) pthread_cond_destroy(&g_pool.go[i]);
+    g_pool.workers = 0;
     g_pool.quit = 0;
   }
   pthread_mutex_unlock(&g_pool.mu);
@@ -269,7 +295,7 @@ static void nn_core(const float* A, const void* B, int b_kind,
                     size_t K, float alpha, int a_transposed, int accumulate) {
   const float* Bf = widen(B, b_kind, col_scale, K, N, 1);
   NnArgs g = {A, Bf, C, M, N, K, alpha, a_transposed, accumulate};
-  orc_parallel(M, 1, nn_rows, &g);
+  orc_parallel_cost(M, 1, N * K, nn_rows, &g);
   if (Bf != B) free((void*)Bf);
 }
 
@@ -308,7 +334,7 @@ static void nt_core(const float* A, const void* B, int b_kind, float* C,
                     size_t M, size_t N, size_t K, float alpha) {
   const float* Bf = widen(B, b_kind, NULL, N, K, 0);
   NtArgs g = {A, Bf, C, N, K, alpha};
-  orc_parallel(M, 1, nt_rows, &g);
+  orc_parallel_cost(M, 1, N * K, nt_rows, &g);
   if (Bf != B) free((void*)Bf);
 }
 
@@ -903,7 +929,7 @@ void orc_attn_fwd_tiled(const float* q, const float* k, const float* v,
                         float* o, float* stats, size_t B, size_t S, size_t H,
                         size_t d, const int32_t* starts) {
   AttnArgs a = {q, k, v, NULL, o, stats, NULL, starts, B, S, H, d};
-  orc_parallel(B * H * S, 1, attn_fwd_units, &a);
+  orc_parallel_cost(B * H * S, 1, S * d, attn_fwd_units, &a);
 }
 /* attention.cc:495-535 */
 static void attn_dq_units(void* ctx, size_t u0, size_t u1, size_t chunk) {
@@ -946,7 +972,7 @@ void orc_attn_dq_tiled(const float* q, const float* k, const float* v,
                        const float* dout, float* stats, float* dq, size_t B,
                        size_t S, size_t H, size_t d) {
   AttnArgs a = {q, k, v, dout, NULL, stats, dq, NULL, B, S, H, d};
-  orc_parallel(B * H * S, 1, attn_dq_units, &a);
+  orc_parallel_cost(B * H * S, 1, S * d, attn_dq_units, &a);
 }
 /* attention.cc:537-563 */
 static void attn_dk_units(void* ctx, size_t u0, size_t u1, size_t chunk) {
@@ -979,7 +1005,7 @@ void orc_attn_dk_tiled(const float* q, const float* k, const float* v,
                        const float* dout, const float* stats, float* dk,
                        size_t B, size_t S, size_t H, size_t d) {
   AttnArgs a = {q, k, v, dout, NULL, (float*)stats, dk, NULL, B, S, H, d};
-  orc_parallel(B * H * S, 1, attn_dk_units, &a);
+  orc_parallel_cost(B * H * S, 1, S * d, attn_dk_units, &a);
 }
 /* attention.cc:565-590 */
 static void attn_dv_units(void* ctx, size_t u0, size_t u1, size_t chunk) {
@@ -1009,7 +1035,7 @@ void orc_attn_dv_tiled(const float* q, const float* k, const float* dout,
                        const float* stats, float* dv, size_t B, size_t S,
                        size_t H, size_t d) {
   AttnArgs a = {q, k, NULL, dout, NULL, (float*)stats, dv, NULL, B, S, H, d};
-  orc_parallel(B * H * S, 1, attn_dv_units, &a);
+  orc_parallel_cost(B * H * S, 1, S * d, attn_dv_units, &a);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1061,7 +1087,7 @@ void orc_xent_fwd(const float* logits, const int32_t* labels, float* loss,
                   float* probs, size_t N, size_t C) {
   XentArgs* a = (XentArgs*)calloc(1, sizeof(XentArgs));
   a->logits = logits, a->labels = labels, a->probs = probs, a->C = C, a->masked = 0;
-  const size_t chunks = orc_parallel(N, row_grain(C, kGrainMath), xent_chunk, a);
+  const size_t chunks = orc_parallel_cost(N, row_grain(C, kGrainMath), 8 * C, xent_chunk, a);
   double total = 0.0;
   for (size_t c = 0; c < chunks; ++c) total += a->part[c];  /* chunk order */
   free(a);
@@ -1081,7 +1107,7 @@ void orc_xent_masked_fwd(const float* logits, const int32_t* labels,
                          float* loss, float* probs, size_t N, size_t C) {
   XentArgs* a = (XentArgs*)calloc(1, sizeof(XentArgs));
   a->logits = logits, a->labels = labels, a->probs = probs, a->C = C, a->masked = 1;
-  const size_t chunks = orc_parallel(N, row_grain(C, kGrainMath), xent_chunk, a);
+  const size_t chunks = orc_parallel_cost(N, row_grain(C, kGrainMath), 8 * C, xent_chunk, a);
   double total = 0.0;
   uint64_t T = 0;
   for (size_t c = 0; c < chunks; ++c) {  /* chunk order */
