@@ -28,12 +28,25 @@ XEntRowMaxKernel(const float* __restrict__ logits, float* __restrict__ row_max, 
   const float* x = logits + static_cast<size_t>(blockIdx.x) * C;
   float mx = NAN, mx2 = NAN;  // the identity of fmax
   if (Vec4Rows(logits, C)) {
+    // Four 16-byte loads in flight per lane (a 32k-column row is 31 per
+    // lane), each into its own running maximum.
     const float4* x4 = reinterpret_cast<const float4*>(x);
-    for (size_t c = threadIdx.x; c < C / 4; c += kMaxThreads) {
+    const size_t n4 = C / 4;
+    float m4[4] = {NAN, NAN, NAN, NAN};
+    size_t c = threadIdx.x;
+    for (; c + 3 * kMaxThreads < n4; c += 4 * kMaxThreads) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = x4[c + u * kMaxThreads];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) m4[u] = fmaxf(m4[u], fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
+    }
+    for (; c < n4; c += kMaxThreads) {
       const float4 v = x4[c];
       mx = fmaxf(mx, fmaxf(v.x, v.y));
       mx2 = fmaxf(mx2, fmaxf(v.z, v.w));
     }
+    mx = fmaxf(mx, fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
   } else {
     for (size_t c = threadIdx.x; c < C; c += kMaxThreads) mx = fmaxf(mx, x[c]);
   }
@@ -49,6 +62,16 @@ XEntRowMaxKernel(const float* __restrict__ logits, float* __restrict__ row_max, 
 // of wave 0 adds row r's previous tile in column order, sixteen LDS values
 // read ahead of its adds.  The chain wave does nothing else, so a tile
 // costs the longer of its 224 dependent adds and the producers' exps.
+// The exps that feed the chain: 2^(x log2 e) on the hardware's exp2 (two
+// instructions where the libm expf takes about fifteen).  The rounding of
+// x log2 e moves a term by at most |x| 1e-7 of itself (below 2e-6 down to
+// x = -30, where a term is 1e-13 of the row's largest one), so the chain's
+// sum stays within 1e-6 of expf's; the probabilities themselves are still
+// expf(x - max) times 1/sum (pass 3).
+__device__ __forceinline__ float SumExp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
 constexpr int kSumThreads = 512;
 constexpr int kSumRows = 32;
 constexpr int kTileCols = 224;                      // 56 float4 per row
@@ -88,11 +111,11 @@ XEntSerialSumKernel(const float* __restrict__ logits, const float* __restrict__ 
       const size_t row = r0 + r, c = k * kTileCols + 4 * c4;
       float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (full[i]) {
-        e[0] = expf(v[i].x - mx[i]), e[1] = expf(v[i].y - mx[i]);
-        e[2] = expf(v[i].z - mx[i]), e[3] = expf(v[i].w - mx[i]);
+        e[0] = SumExp(v[i].x - mx[i]), e[1] = SumExp(v[i].y - mx[i]);
+        e[2] = SumExp(v[i].z - mx[i]), e[3] = SumExp(v[i].w - mx[i]);
       } else if (row < N) {
         for (int u = 0; u < 4; ++u)
-          if (c + u < C) e[u] = expf(logits[row * C + c + u] - mx[i]);
+          if (c + u < C) e[u] = SumExp(logits[row * C + c + u] - mx[i]);
       }
       *reinterpret_cast<float4*>(&tile[buf][r][4 * c4]) = make_float4(e[0], e[1], e[2], e[3]);
     }
@@ -325,10 +348,11 @@ XEntSmallKernel(const float* __restrict__ logits, const int32_t* __restrict__ la
         make_float4(expf(v.x - mx), expf(v.y - mx), expf(v.z - mx), expf(v.w - mx));
   }
   __syncthreads();
-  if (static_cast<size_t>(tid) < N) {  // each row's chain in column order
-    const float* er = e + static_cast<size_t>(tid) * C;
+  if (static_cast<size_t>(tid) < N) {  // each row's chain in column order, on pass 2's exps
+    const float* xr = logits + static_cast<size_t>(tid) * C;
+    const float mx = smax[tid];
     float sum = 0.0f;
-    for (size_t c = 0; c < C; ++c) sum += er[c];
+    for (size_t c = 0; c < C; ++c) sum += SumExp(xr[c] - mx);
     sinv[tid] = 1.0f / sum;  // loss.cc:30
   }
   double t = 0.0;
