@@ -76,20 +76,20 @@ __device__ __forceinline__ float AddRn(float a, float b) { return __fadd_rn(a, b
 
 // The low-rank term of one output: the rank-r product's exact chain over
 // the row's t values and the column's rank-operand values (GemmArgs).
+// NN: `t` holds the row's t values already multiplied by alpha (each
+// (alpha t) rounded once, as the reference folds alpha into A), shared by
+// the row's columns; NT: the raw t, alpha applied to the finished dot.
 template <int kLayout>
 __device__ __forceinline__ float LowRankDot(const float (&t)[kLowRankMaxK],
                                             const float (&b)[kLowRankMaxK], int r, float alpha) {
   if constexpr (kLayout == 0) {  // quads of (alpha t) b from k = 0 (r % 4 == 0: no tail)
+    (void)alpha;
     float c = 0.0f;
 #pragma unroll
     for (int k = 0; k < kLowRankMaxK; k += 4) {
-      if (k < r) {
-        float a[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) a[u] = alpha != 1.0f ? MulRn(alpha, t[k + u]) : t[k + u];
-        c = AddRn(c, AddRn(AddRn(AddRn(MulRn(a[0], b[k]), MulRn(a[1], b[k + 1])),
-                                 MulRn(a[2], b[k + 2])), MulRn(a[3], b[k + 3])));
-      }
+      if (k < r)
+        c = AddRn(c, AddRn(AddRn(AddRn(MulRn(t[k], b[k]), MulRn(t[k + 1], b[k + 1])),
+                                 MulRn(t[k + 2], b[k + 2])), MulRn(t[k + 3], b[k + 3])));
     }
     return c;
   } else {  // eight lanes by k mod 8, added in lane order, then alpha
@@ -363,9 +363,10 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) stage[lr * SLD + j * 32 + 8 * q + 4 * h + e] = acc[i][j][4 * q + e];
+      for (int j = 0; j < TN; ++j)  // four consecutive columns: one 16-byte write
+        *reinterpret_cast<float4*>(stage + lr * SLD + j * 32 + 8 * q + 4 * h) =
+            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                        acc[i][j][4 * q + 3]);
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int t = 0; t < 32 / kRowsPerPass; ++t) {
@@ -398,6 +399,10 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
           float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
           if (k < lr_r) q = *reinterpret_cast<const float4*>(tr + k);
           t[k] = q.x, t[k + 1] = q.y, t[k + 2] = q.z, t[k + 3] = q.w;
+        }
+        if (kLR == 1 && g.lr_alpha != 1.0f) {  // alpha into t once per row, not per column
+#pragma unroll
+          for (int k = 0; k < kLowRankMaxK; ++k) t[k] = MulRn(g.lr_alpha, t[k]);
         }
         float o4[4];
 #pragma unroll
