@@ -24,10 +24,15 @@
 //     epilogue (NN column scale, alpha, addend, accumulate, bias, activation
 //     -- the exact family's order) runs on them in registers and C leaves in
 //     16-byte stores.  With the low-rank term, or rows whose length is not a
-//     multiple of four, the rows pass through LDS instead.
+//     multiple of four, the rows pass through LDS instead; the low-rank
+//     term's t rows for the whole tile are staged in LDS once, and at rank 8
+//     or 16 behind a plain epilogue (column scale and alpha only) the rank
+//     is a compile-time constant, so each row pass is straight-line code of
+//     four independent chains.
 // Rows past M or N read as zeros through the buffer range check; Kp is K
 // rounded up to 32.
 #include <algorithm>
+#include <type_traits>
 #include <cstdint>
 
 #include "common.h"
@@ -339,23 +344,113 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
   // in registers for the whole epilogue (its column quad never changes).
   float lb[4][kLowRankMaxK];
   const int lr_r = kLR ? g.lr_k : 0;
+  // The tile's t rows [BM][kLowRankMaxK] in LDS past the staging slices
+  // (NN: already alpha t, each product rounded once), zero past r and M.
+  constexpr int kTOff = kWaves * 32 * SLD;
+  static_assert((kTOff + BM * kLowRankMaxK) * 4 <= kStages * kStage, "t block fits in LDS");
+  float* tl = reinterpret_cast<float*>(smem) + kTOff;
   if constexpr (kLR != 0) {
+    for (int e = tid; e < BM * (kLowRankMaxK / 4); e += kWaves * kWave) {
+      const int rr = e / (kLowRankMaxK / 4), k = (e % (kLowRankMaxK / 4)) * 4;
+      float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (k < lr_r && m0 + rr < M)
+        q = *reinterpret_cast<const float4*>(g.lr_t + static_cast<size_t>(m0 + rr) * lr_r + k);
+      if (kLR == 1 && g.lr_alpha != 1.0f)
+        q = make_float4(MulRn(g.lr_alpha, q.x), MulRn(g.lr_alpha, q.y), MulRn(g.lr_alpha, q.z),
+                        MulRn(g.lr_alpha, q.w));
+      *reinterpret_cast<float4*>(tl + rr * kLowRankMaxK + k) = q;
+    }
     const int nl = n0 + wn + c4 * 4;
+    const bool b16 = (reinterpret_cast<uintptr_t>(g.lr_b) & 15) == 0;
 #pragma unroll
-    for (int k = 0; k < kLowRankMaxK; ++k) {
-      float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (k < lr_r && nl < N) {
-        if constexpr (kLR == 1) {
+    for (int k = 0; k < kLowRankMaxK; ++k) lb[0][k] = lb[1][k] = lb[2][k] = lb[3][k] = 0.0f;
+    if constexpr (kLR == 1) {
+#pragma unroll
+      for (int k = 0; k < kLowRankMaxK; ++k) {
+        float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k < lr_r && nl < N)
           b = *reinterpret_cast<const float4*>(g.lr_b + static_cast<size_t>(k) * N + nl);
-        } else {
-          b.x = g.lr_b[static_cast<size_t>(nl) * lr_r + k];
-          b.y = g.lr_b[static_cast<size_t>(nl + 1) * lr_r + k];
-          b.z = g.lr_b[static_cast<size_t>(nl + 2) * lr_r + k];
-          b.w = g.lr_b[static_cast<size_t>(nl + 3) * lr_r + k];
+        lb[0][k] = b.x, lb[1][k] = b.y, lb[2][k] = b.z, lb[3][k] = b.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int k = 0; k < kLowRankMaxK; k += 4) {
+          if (k < lr_r && nl < N) {
+            const float* src = g.lr_b + static_cast<size_t>(nl + e) * lr_r + k;
+            float4 b;
+            if (b16) b = *reinterpret_cast<const float4*>(src);
+            else b = make_float4(src[0], src[1], src[2], src[3]);
+            lb[e][k] = b.x, lb[e][k + 1] = b.y, lb[e][k + 2] = b.z, lb[e][k + 3] = b.w;
+          }
+        }
+    }
+    __syncthreads();
+  }
+  if constexpr (kLR != 0) {
+    // Rank 8 or 16 with nothing but the column scale and alpha before the
+    // low-rank term: the rank is a constant, so each pass is one block of
+    // four independent chains.
+    const bool plain = !add && !g.accumulate && !bias && !g.act;
+    auto fast = [&](auto rq_tag) {
+      constexpr int RQ = decltype(rq_tag)::value;
+      float csq[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) csq[e] = 1.0f;
+      {
+        const int n = n0 + wn + c4 * 4;
+        if (cs && n < N) {
+          const float4 c4v = *reinterpret_cast<const float4*>(cs + n);
+          csq[0] = c4v.x, csq[1] = c4v.y, csq[2] = c4v.z, csq[3] = c4v.w;
         }
       }
-      lb[0][k] = b.x, lb[1][k] = b.y, lb[2][k] = b.z, lb[3][k] = b.w;
-    }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int mb = m0 + wm + i * 32;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            *reinterpret_cast<float4*>(stage + lr * SLD + j * 32 + 8 * q + 4 * h) =
+                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                            acc[i][j][4 * q + 3]);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int tt = 0; tt < 32 / kRowsPerPass; ++tt) {
+          const int row = row0 + tt * kRowsPerPass;
+          const int m = mb + row, n = n0 + wn + c4 * 4;
+          if (!epi_lane || m >= M || n >= N) continue;
+          const float4 s4 = *reinterpret_cast<const float4*>(stage + row * SLD + c4 * 4);
+          float v[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = alpha * (v[e] * csq[e]);  // x 1.0f is exact
+          const size_t o = static_cast<size_t>(m) * N + n;
+          if (g.lr_store_c) *reinterpret_cast<float4*>(C + o) = make_float4(v[0], v[1], v[2], v[3]);
+          float t[kLowRankMaxK];
+          const float* trow = tl + (m - m0) * kLowRankMaxK;
+#pragma unroll
+          for (int k = 0; k < kLowRankMaxK; k += 4) {
+            float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k < 4 * RQ) q = *reinterpret_cast<const float4*>(trow + k);
+            t[k] = q.x, t[k + 1] = q.y, t[k + 2] = q.z, t[k + 3] = q.w;
+          }
+          float o4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o4[e] = AddRn(v[e], LowRankDot<kLR - 1>(t, lb[e], 4 * RQ, g.lr_alpha));
+          if (kLR == 2 && g.lr_res) {
+            const float4 r4 = *reinterpret_cast<const float4*>(g.lr_res + o);
+            o4[0] = AddRn(r4.x, o4[0]), o4[1] = AddRn(r4.y, o4[1]);
+            o4[2] = AddRn(r4.z, o4[2]), o4[3] = AddRn(r4.w, o4[3]);
+          }
+          *reinterpret_cast<float4*>(g.lr_out + o) = make_float4(o4[0], o4[1], o4[2], o4[3]);
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+    };
+    if (plain && lr_r == 16) return fast(std::integral_constant<int, 4>{});
+    if (plain && lr_r == 8) return fast(std::integral_constant<int, 2>{});
   }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -393,16 +488,11 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
         // N % 4 == 0 here: the whole quad is in range.
         if (g.lr_store_c) *reinterpret_cast<float4*>(C + o) = make_float4(v[0], v[1], v[2], v[3]);
         float t[kLowRankMaxK];
-        const float* __restrict__ tr = g.lr_t + static_cast<size_t>(m) * lr_r;
+        const float* trow = tl + (m - m0) * kLowRankMaxK;
 #pragma unroll
         for (int k = 0; k < kLowRankMaxK; k += 4) {
-          float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (k < lr_r) q = *reinterpret_cast<const float4*>(tr + k);
+          const float4 q = *reinterpret_cast<const float4*>(trow + k);
           t[k] = q.x, t[k + 1] = q.y, t[k + 2] = q.z, t[k + 3] = q.w;
-        }
-        if (kLR == 1 && g.lr_alpha != 1.0f) {  // alpha into t once per row, not per column
-#pragma unroll
-          for (int k = 0; k < kLowRankMaxK; ++k) t[k] = MulRn(g.lr_alpha, t[k]);
         }
         float o4[4];
 #pragma unroll

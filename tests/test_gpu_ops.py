@@ -1000,7 +1000,9 @@ def _readers(ar, names):
 @pytest.mark.parametrize("kind", ["q8", "f32"])
 @pytest.mark.parametrize("M,Din,Dout,rank,read_later", [
     (512, 1024, 1024, 16, False), (512, 1024, 1024, 16, True), (300, 1024, 2048, 8, False),
-    (2048, 2048, 1280, 16, True)])
+    (2048, 2048, 1280, 16, True), (256, 1024, 1024, 4, False), (384, 1024, 1024, 12, True),
+    # one 256 x 256 tile per CU, the C5 site shape
+    (8192, 2048, 2048, 16, False)])
 def test_lora_site_folds_into_the_frozen_product_bitwise(hip, orc, backend, kind, M, Din, Dout,
                                                          rank, read_later):
     """With the range visible, each LoRA site runs as one dispatch: the
