@@ -298,7 +298,7 @@ def main():
             "kernel_ms": round(gemm_ms, 5),
             "traffic": load_traffic("w8a8_4096"),
         },
-        "quantize": {"kernel": "QuantizeRowsWaveKernel<16>", "ms": round(quant_ms, 5),
+        "quantize": {"kernel": "QuantizeRowsBlockKernel<4>", "ms": round(quant_ms, 5),
                      "bytes": quant_bytes, "GB_s": round(quant_bytes / quant_ms / 1e6, 1),
                      "hbm_frac": round(quant_bytes / quant_ms / 1e6 / PEAK_HBM_GBS, 4)},
     }

@@ -198,7 +198,9 @@ typedef struct seeai_tile_policy {
   uint32_t w8a8_large_kernel;     /* 1 direct-to-LDS 256x256 (default), 2 register-staged 256x256,
                                      3 register-staged 128x128 */
   uint32_t w8a8_large_min;        /* M and N from which it applies (default 4096) */
-  uint32_t quantize_waves_per_cu; /* waves per CU walking the quantizer's rows (default 32, <= 32) */
+  uint32_t quantize_waves_per_cu; /* waves per CU walking the quantizer's rows of at most 1024
+                                     or more than 8192 floats (default 32, <= 32); rows in
+                                     between take a workgroup of four waves each */
   uint32_t relaxed_min_tiles_256; /* relaxed bf16 GEMM: 256x256 tiles from this many (default 256) */
   uint32_t relaxed_min_fill_256;  /* ... and when their last round over the CUs is at least
                                      this percent full (<= 100) */

@@ -291,7 +291,9 @@ struct TilePolicy {
   int w8a8_large_kernel = 1;           // 1 direct-to-LDS 256 x 256, 2 register-staged 256 x 256,
                                        // 3 register-staged 128 x 128
   size_t w8a8_large_min = 4096;        // M and N from which w8a8_large_kernel applies
-  int quantize_waves_per_cu = 32;      // waves per CU walking the rows of the quantizer
+  int quantize_waves_per_cu = 32;      // waves per CU walking the quantizer's rows of at most
+                                       // 1024 or more than 8192 floats (rows in between take
+                                       // a workgroup of four waves each)
   size_t relaxed_min_tiles_256 = 256;  // relaxed bf16 GEMM: 256 x 256 tiles from this many
   int relaxed_min_fill_256 = 0;        // ... and when their last round of tiles over
                                        // the CUs is at least this percent full

@@ -37,7 +37,8 @@ FIELDS = {
                           "2 register-staged 256x256, 3 register-staged 128x128"),
     "w8a8_large_min": (4096, ("range", 1, 1 << 30), "M and N from which w8a8_large_kernel applies"),
     "quantize_waves_per_cu": (32, ("range", 1, 32),
-                              "waves per CU walking the activation quantizer's rows"),
+                              "waves per CU walking the activation quantizer's rows of at most "
+                              "1024 or more than 8192 floats (rows in between: four waves each)"),
     "relaxed_min_tiles_256": (256, ("range", 1, 1 << 30),
                               "relaxed bf16 GEMM: 256x256 tiles once the grid has this many"),
     "relaxed_min_fill_256": (0, ("range", 0, 100),

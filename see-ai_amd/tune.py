@@ -144,7 +144,7 @@ class Bench:
             yield from self.fixtures_w8a8([(1024, 1024, 4096), (2048, 2048, 4096),
                                            (2048, 4096, 4096)])
         elif field == "quantize_waves_per_cu":
-            shapes = [(4096, 4096), (8192, 2048), (8192, 768)]
+            shapes = [(8192, 768), (4096, 1024), (1024, 16384)]
             if self.quick:
                 shapes = shapes[:1]
             for rows, cols in shapes:

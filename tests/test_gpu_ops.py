@@ -1532,8 +1532,9 @@ def test_w8a8_at_the_bench_shapes(hip, orc, torch_cuda, M):
 def test_w8a8_quantizer_on_half_level_quotients(hip, orc, torch_cuda, cols):
     """Every element's quotient x / scale sits within a few ulps of a half
     integer, where round-half-away decides the level; the levels and scales
-    must still be the oracle's bit for bit (the wave-per-row quantizer takes
-    the true division there, the reciprocal elsewhere)."""
+    must still be the oracle's bit for bit (both quantizers -- a wave per row
+    at 1024 columns, four waves per row at 2052 to 4100 -- take the true
+    division there, the reciprocal elsewhere)."""
     torch = torch_cuda
     rows = 96
     r = rng(cols)
