@@ -32,6 +32,7 @@
 // Rows past M or N read as zeros through the buffer range check; Kp is K
 // rounded up to 32.
 #include <algorithm>
+#include <numeric>
 #include <type_traits>
 #include <cstdint>
 
@@ -554,14 +555,28 @@ ConvertRowsKernel(const float* __restrict__ A, size_t K, size_t Kp, float alpha,
 // of a few workgroups per CU; each lane keeps four groups (eight 16-byte
 // loads) in flight per trip.  The k-scale index is the flat index mod K
 // (32-bit: fewer than 2^32 groups), its eight values two 16-byte loads.
-template <bool kScale>
+// kFixedK: the grid's stride is a multiple of K / 8, so a lane's groups all
+// share one k-scale group, loaded once (8192 x 5632 on MI355X: 50 -> 42 us;
+// the per-group index division and loads dominated).
+template <bool kScale, bool kFixedK = false>
 __global__ void __launch_bounds__(kCvtThreads)
 ConvertFlatKernel(const float* __restrict__ A, unsigned groups, unsigned kgroups, float alpha,
                   const float* __restrict__ ks, __bf16* __restrict__ out) {
   const unsigned stride = gridDim.x * kCvtThreads;
+  float fixed_sc[8];
+  if constexpr (kScale && kFixedK) {
+    const float4* k4 =
+        reinterpret_cast<const float4*>(ks + ((blockIdx.x * kCvtThreads + threadIdx.x) % kgroups) * 8);
+    const float4 s0 = k4[0], s1 = k4[1];
+    fixed_sc[0] = s0.x, fixed_sc[1] = s0.y, fixed_sc[2] = s0.z, fixed_sc[3] = s0.w;
+    fixed_sc[4] = s1.x, fixed_sc[5] = s1.y, fixed_sc[6] = s1.z, fixed_sc[7] = s1.w;
+  }
   auto convert = [&](unsigned gi, float4 a, float4 b) {
     float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    if constexpr (kScale) {
+    if constexpr (kScale && kFixedK) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = x[e] * fixed_sc[e];
+    } else if constexpr (kScale) {
       const float4* k4 = reinterpret_cast<const float4*>(ks + (gi % kgroups) * 8);
       const float4 s0 = k4[0], s1 = k4[1];
       const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
@@ -670,7 +685,14 @@ hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha
         std::min<size_t>((groups + 4 * kCvtThreads - 1) / (4 * kCvtThreads),
                          static_cast<size_t>(DeviceCUs()) * (wgs_per_cu > 0 ? wgs_per_cu : 8)));
     const unsigned g = static_cast<unsigned>(groups), kg = static_cast<unsigned>(K / 8);
-    if (kscale)
+    // A grid whose stride (grid x 256 groups) is a multiple of K / 8 keeps
+    // each lane on one k-scale group: the largest such grid not above the
+    // default, where one exists.
+    const unsigned period = kg / std::gcd(static_cast<unsigned>(kCvtThreads), kg);
+    if (kscale && period <= grid)
+      hipLaunchKernelGGL((ConvertFlatKernel<true, true>), dim3(grid / period * period),
+                         dim3(kCvtThreads), 0, s, A, g, kg, alpha, kscale, static_cast<__bf16*>(out));
+    else if (kscale)
       hipLaunchKernelGGL((ConvertFlatKernel<true>), dim3(grid), dim3(kCvtThreads), 0, s, A, g, kg,
                          alpha, kscale, static_cast<__bf16*>(out));
     else

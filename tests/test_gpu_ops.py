@@ -39,7 +39,7 @@ GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 
                # ragged chunks and a K % 4 tail
                (1040, 16, 2050), (8200, 8, 600), (16, 1030, 1000), (300, 8, 520), (40, 16, 1300),
                # rank-r products: wide outputs over K <= 32 (four outputs per lane)
-               (67, 1100, 16), (130, 512, 8), (100, 260, 13),
+               (67, 1100, 16), (130, 512, 8), (100, 260, 13), (96, 256, 32), (70, 512, 21),
                # TN over long K: quads formed by four lanes per output, folded in order
                (300, 3, 1100), (100, 1, 1030),
                # TN with the folder wave apart: 4 x 8 blocks over two chunks, 8 x 16
