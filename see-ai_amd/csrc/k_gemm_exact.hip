@@ -974,9 +974,17 @@ __global__ void __launch_bounds__(kThreads) GemmFoldKernel(GemmArgs g) {
 // own slot's loads and no more; the last intervals wait for every load.
 // Rows past K are clamped reads: they meet only quads past K / 4, which are
 // never folded.  The sums are GemmFoldKernel's, operation for operation.
+//
+// LDS layout (64 banks of 4 bytes): a wave's transposed stores put lanes f
+// at (row 4 (f % W) + t, column f / W), W = BMo / 4 or BNo / 4, so the row
+// stride is padded to 8 (mod 16) floats for W = 2 and 4 (mod 16) otherwise,
+// which spreads the W row groups over disjoint banks; a producer task takes
+// the quad index fastest, so a wave's quad writes and operand reads walk
+// consecutive columns of one block (conflict-free whatever the strides).
 template <int BMo, int BNo, int kKc, int kD, int QM, int QN, int kW, int kF>
 __global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
-  constexpr int kOut = BMo * BNo, kQc = kKc / 4, kLd = kKc + 4, kQLd = kQc + 4;
+  constexpr int kOut = BMo * BNo, kQc = kKc / 4, kQLd = kQc + 4;
+  constexpr int kLdA = kKc + (BMo / 4 == 2 ? 8 : 4), kLdB = kKc + (BNo / 4 == 2 ? 8 : 4);
   static_assert(kOut == 64 * kF || (kF == 1 && kOut < 64), "kF outputs per folder lane");
   constexpr int kP = 64 * (kW - 1);  // producer lanes
   constexpr int kAf = kKc * BMo / 4, kBf = kKc * BNo / 4;  // float4 per chunk
@@ -984,8 +992,8 @@ __global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
   constexpr int kBlkN = BNo / QN, kBlk = (BMo / QM) * kBlkN, kTasks = kBlk * kQc;
   constexpr int kT = (kTasks + kP - 1) / kP;
   static_assert(BMo % QM == 0 && BNo % QN == 0 && QM % 4 == 0 && QN % 4 == 0, "whole blocks");
-  __shared__ __attribute__((aligned(16))) float As[2][BMo][kLd];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BNo][kLd];
+  __shared__ __attribute__((aligned(16))) float As[2][BMo][kLdA];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BNo][kLdB];
   __shared__ __attribute__((aligned(16))) float Q[2][kOut][kQLd];
   const int tid = threadIdx.x;
   const int p = tid - 64;
@@ -1009,9 +1017,13 @@ __global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
       rb[s][r] = *reinterpret_cast<const float4*>(B + min(k0 + kk, K - 1) * N + n0 + 4 * c4);
     }
   };
-  auto store = [&](int s, int buf) {  // transposed into k-contiguous rows, alpha applied
+  // Transposed into k-contiguous rows, alpha applied; the spare lanes of a
+  // last round (their loads re-read the last element) store nothing, so no
+  // two lanes of a store meet at one address.
+  auto store = [&](int s, int buf) {
 #pragma unroll
     for (int r = 0; r < kRA; ++r) {
+      if (kRA * kP > kAf && p + r * kP >= kAf) continue;
       const int f = min(p + r * kP, kAf - 1), kk = f / (BMo / 4), c4 = f % (BMo / 4);
       float4 v = ra[s][r];
       if (g.alpha_a != 1.0f)
@@ -1024,6 +1036,7 @@ __global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
     }
 #pragma unroll
     for (int r = 0; r < kRB; ++r) {
+      if (kRB * kP > kBf && p + r * kP >= kBf) continue;
       const int f = min(p + r * kP, kBf - 1), kk = f / (BNo / 4), c4 = f % (BNo / 4);
       const float4 v = rb[s][r];
       Bs[buf][4 * c4 + 0][kk] = v.x;
@@ -1037,7 +1050,7 @@ __global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
     for (int r = 0; r < kT; ++r) {
       const int task = p + r * kP;
       if (task >= kTasks) continue;
-      const int qb = task % kBlk, j = task / kBlk;
+      const int j = task % kQc, qb = task / kQc;
       if (j >= nq) continue;
       const int bm = qb / kBlkN, bn = qb % kBlkN;
       float4 a[QM], b[QN];
