@@ -493,6 +493,24 @@ def extras(ctx, torch, hip):
                        "ms_one_matrix_cache_resident": round(ms_resident, 5)}
     del QWs
 
+    # A reference point, not this build's code: the vendor library's int8
+    # GEMM (hipBLASLt, through torch._int_mm) on the same box and shapes,
+    # int32 output with no quantize and no dequant, the weight passed
+    # K-contiguous as W8A8 packs it.
+    ref = {}
+    for (m, n, kk) in [(4096, 4096, 4096), (32, 4096, 4096)]:
+        a = torch.randint(-127, 128, (m, kk), dtype=torch.int8, device="cuda")
+        wt = torch.randint(-127, 128, (n, kk), dtype=torch.int8, device="cuda")
+        try:
+            ms_v = timed(lambda: torch._int_mm(a, wt.t()), 50, 5)
+            ref[f"{m}x{n}x{kk}"] = {"ms": round(ms_v, 5),
+                                    "TOPS": round(2 * m * n * kk / ms_v / 1e9, 1)}
+        except RuntimeError as e:  # a build of torch without the int8 path
+            ref[f"{m}x{n}x{kk}"] = {"error": str(e)[:120]}
+        del a, wt
+    out["w8a8_vendor_reference"] = dict(
+        ref, note="hipBLASLt int8 GEMM via torch._int_mm: int32 output, no quantize or dequant")
+
     # Causal attention fwd+bwd, BASELINE config 3 (B16 H16 S2048 d64).
     B, S, H, d = 16, 2048, 16, 64
     flops = 412518187008.0  # causal-exact fwd + bwd
