@@ -957,9 +957,10 @@ __global__ void __launch_bounds__(kThreads) GemmFoldKernel(GemmArgs g) {
   g.C[mf * N + nf] = Epilogue(g, mf, nf, c);
 }
 
-// The fold kernel with its waves split by role (TN, f32 operands 16-byte
-// aligned, M % BMo == N % BNo == 0, K * M and K * N below 2^31, no q8
-// k-scale): the chain of each output is a strict sequence of adds, so one
+// The fold kernel with its waves split by role (TN or NN, f32 operands
+// 16-byte aligned, M % BMo == N % BNo == 0, K * M and K * N below 2^31, NN
+// with K % 4 == 0, no q8 k-scale): the chain of each output is a strict
+// sequence of adds, so one
 // wave does nothing but fold -- kF outputs per lane, their chains
 // interleaved -- while the other kW - 1 waves load, stage and form the
 // quads.  Operands and quads are double-buffered, one barrier per interval:
@@ -975,16 +976,21 @@ __global__ void __launch_bounds__(kThreads) GemmFoldKernel(GemmArgs g) {
 // Rows past K are clamped reads: they meet only quads past K / 4, which are
 // never folded.  The sums are GemmFoldKernel's, operation for operation.
 //
+// A is staged k-contiguous per output row: TN's A [K, M] transposed on the
+// way in, NN's A [M, K] as it lies (16-byte row segments).
+//
 // LDS layout (64 banks of 4 bytes): a wave's transposed stores put lanes f
 // at (row 4 (f % W) + t, column f / W), W = BMo / 4 or BNo / 4, so the row
 // stride is padded to 8 (mod 16) floats for W = 2 and 4 (mod 16) otherwise,
 // which spreads the W row groups over disjoint banks; a producer task takes
 // the quad index fastest, so a wave's quad writes and operand reads walk
 // consecutive columns of one block (conflict-free whatever the strides).
-template <int BMo, int BNo, int kKc, int kD, int QM, int QN, int kW, int kF>
+template <int kLayout, int BMo, int BNo, int kKc, int kD, int QM, int QN, int kW, int kF>
 __global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
+  static_assert(kLayout == 0 || kLayout == 2, "NN or TN");
+  constexpr bool kTN = kLayout == 2;
   constexpr int kOut = BMo * BNo, kQc = kKc / 4, kQLd = kQc + 4;
-  constexpr int kLdA = kKc + (BMo / 4 == 2 ? 8 : 4), kLdB = kKc + (BNo / 4 == 2 ? 8 : 4);
+  constexpr int kLdA = kKc + (kTN && BMo / 4 == 2 ? 8 : 4), kLdB = kKc + (BNo / 4 == 2 ? 8 : 4);
   static_assert(kOut == 64 * kF || (kF == 1 && kOut < 64), "kF outputs per folder lane");
   constexpr int kP = 64 * (kW - 1);  // producer lanes
   constexpr int kAf = kKc * BMo / 4, kBf = kKc * BNo / 4;  // float4 per chunk
@@ -1008,8 +1014,15 @@ __global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
   auto load = [&](int s, unsigned k0) {
 #pragma unroll
     for (int r = 0; r < kRA; ++r) {
-      const int f = min(p + r * kP, kAf - 1), kk = f / (BMo / 4), c4 = f % (BMo / 4);
-      ra[s][r] = *reinterpret_cast<const float4*>(A + min(k0 + kk, K - 1) * M + m0 + 4 * c4);
+      const int f = min(p + r * kP, kAf - 1);
+      if constexpr (kTN) {  // A [K, M]: four consecutive m at one k
+        const int kk = f / (BMo / 4), c4 = f % (BMo / 4);
+        ra[s][r] = *reinterpret_cast<const float4*>(A + min(k0 + kk, K - 1) * M + m0 + 4 * c4);
+      } else {              // A [M, K]: four consecutive k of one row
+        const int mm = f / (kKc / 4), c4 = f % (kKc / 4);
+        ra[s][r] = *reinterpret_cast<const float4*>(A + static_cast<size_t>(m0 + mm) * K +
+                                                    min(k0 + 4 * c4, K - 4));
+      }
     }
 #pragma unroll
     for (int r = 0; r < kRB; ++r) {
@@ -1024,15 +1037,21 @@ __global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
 #pragma unroll
     for (int r = 0; r < kRA; ++r) {
       if (kRA * kP > kAf && p + r * kP >= kAf) continue;
-      const int f = min(p + r * kP, kAf - 1), kk = f / (BMo / 4), c4 = f % (BMo / 4);
+      const int f = min(p + r * kP, kAf - 1);
       float4 v = ra[s][r];
       if (g.alpha_a != 1.0f)
         v = make_float4(Mul(g.alpha_a, v.x), Mul(g.alpha_a, v.y), Mul(g.alpha_a, v.z),
                         Mul(g.alpha_a, v.w));
-      As[buf][4 * c4 + 0][kk] = v.x;
-      As[buf][4 * c4 + 1][kk] = v.y;
-      As[buf][4 * c4 + 2][kk] = v.z;
-      As[buf][4 * c4 + 3][kk] = v.w;
+      if constexpr (kTN) {
+        const int kk = f / (BMo / 4), c4 = f % (BMo / 4);
+        As[buf][4 * c4 + 0][kk] = v.x;
+        As[buf][4 * c4 + 1][kk] = v.y;
+        As[buf][4 * c4 + 2][kk] = v.z;
+        As[buf][4 * c4 + 3][kk] = v.w;
+      } else {
+        const int mm = f / (kKc / 4), c4 = f % (kKc / 4);
+        *reinterpret_cast<float4*>(&As[buf][mm][4 * c4]) = v;
+      }
     }
 #pragma unroll
     for (int r = 0; r < kRB; ++r) {
@@ -1175,8 +1194,14 @@ __global__ void __launch_bounds__(64 * kW) GemmFoldSplitKernel(GemmArgs g) {
 // The fold kernel for TN with f32 B over K >= 1024 when the outputs fill at
 // most a few thousand workgroups (NN over these shapes measured faster on
 // the chain kernel).
+// TN from K = 1024 (the adapter gradients); NN from K = 1024 past the
+// two-pass form's output count (the LoRA products t = X A; C5's
+// 8192 x 16 x 2048: 49.2 -> 44.2 us against the chain kernel, while C4's
+// 8192 x 8 x 768 measured 19.6 on the chain kernel against 31.2 here): up to
+// 2^18 outputs, each one reduction chain.
 bool Fold(const GemmArgs& a) {
-  return a.layout == 2 && a.b_kind == 0 && a.K >= 1024 && a.M * a.N <= (size_t{1} << 18);
+  if (a.b_kind != 0 || a.M * a.N > (size_t{1} << 18) || a.K < 1024) return false;
+  return a.layout == 2 || (a.layout == 0 && a.M * a.N > 16384);
 }
 
 template <int kLayout>
@@ -1186,8 +1211,9 @@ hipError_t LaunchFold(const GemmArgs& a, hipStream_t s) {
   int bno = 2;
   while (bno < 16 && static_cast<size_t>(bno) < a.N) bno *= 2;
   const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  if (kLayout == 2 && a.M % 4 == 0 && a.N % 8 == 0 && a.K * a.M < (size_t{1} << 31) &&
-      a.K * a.N < (size_t{1} << 31) && al16(a.A) && al16(a.B) && !a.a_k_scale) {
+  if (a.M % 4 == 0 && a.N % 8 == 0 && a.K * a.M < (size_t{1} << 31) &&
+      a.K * a.N < (size_t{1} << 31) && al16(a.A) && al16(a.B) && !a.a_k_scale &&
+      (kLayout == 2 || a.K % 4 == 0)) {
     // Role-split folds: 8 x 16 blocks (two outputs per folder lane) where
     // they still fill the machine, else 4 x 8 (C5's 2048 x 16 and 16 x 2048
     // gradients run 38 us against 55; C4's 768 x 8 and 8 x 768 20 us
@@ -1195,12 +1221,14 @@ hipError_t LaunchFold(const GemmArgs& a, hipStream_t s) {
     if (a.M % 8 == 0 && a.N % 16 == 0 && (a.M / 8) * (a.N / 16) >= 256) {
       const dim3 grid(static_cast<unsigned>(a.N / 16), static_cast<unsigned>(a.M / 8));
       if (grid.y > 65535) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((GemmFoldSplitKernel<8, 16, 256, 2, 4, 4, 8, 2>), grid, dim3(512), 0, s, a);
+      hipLaunchKernelGGL((GemmFoldSplitKernel<kLayout, 8, 16, 256, 2, 4, 4, 8, 2>), grid, dim3(512),
+                         0, s, a);
       return hipGetLastError();
     }
     const dim3 grid(static_cast<unsigned>(a.N / 8), static_cast<unsigned>(a.M / 4));
     if (grid.y > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((GemmFoldSplitKernel<4, 8, 512, 2, 4, 4, 5, 1>), grid, dim3(320), 0, s, a);
+    hipLaunchKernelGGL((GemmFoldSplitKernel<kLayout, 4, 8, 512, 2, 4, 4, 5, 1>), grid, dim3(320), 0,
+                       s, a);
     return hipGetLastError();
   }
   const size_t bmo = kFoldOut / bno;
@@ -1294,7 +1322,7 @@ hipError_t Run(const GemmArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((GemmPanelKernel<kLayout, kBKind>), grid, dim3(kThreads), lds, s, a);
     return hipGetLastError();
   }
-  if constexpr (kLayout == 2 && kBKind == 0)
+  if constexpr (kLayout != 1 && kBKind == 0)
     if (Fold(a)) return LaunchFold<kLayout>(a, s);
   if (Chain(a) && !(kLayout != 1 && LongK(a) && a.scratch && LongKFirst(a))) {
     if (a.N <= 8) return LaunchChain<kLayout, kBKind, 32, 8>(a, s);

@@ -40,6 +40,10 @@ GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 
                (1040, 16, 2050), (8200, 8, 600), (16, 1030, 1000), (300, 8, 520), (40, 16, 1300),
                # rank-r products: wide outputs over K <= 32 (four outputs per lane)
                (67, 1100, 16), (130, 512, 8), (100, 260, 13), (96, 256, 32), (70, 512, 21),
+               # the LoRA products t = X A on the role-split fold (NN): 8 x 16 blocks over
+               # a K % 256 tail, 4 x 8 blocks over a partial 512-deep chunk; C4's
+               # 8192 x 8 x 768 on the chain kernel
+               (2048, 16, 2056), (4096, 8, 1300), (8192, 8, 768),
                # TN over long K: quads formed by four lanes per output, folded in order
                (300, 3, 1100), (100, 1, 1030),
                # TN with the folder wave apart: 4 x 8 blocks over two chunks, 8 x 16
@@ -911,8 +915,10 @@ def _attn_copies_program(ar, r, B, S, H, d, case):
     return [table, rope_q, rope_k, fwd] + bwd
 
 
-@pytest.mark.parametrize("case", ["copy_into_q", "rope_into_k", "rope_then_write_y",
-                                  "rope_feeds_the_copies"])
+ATTN_COPY_CASES = ["copy_into_q", "rope_into_k", "rope_then_write_y", "rope_feeds_the_copies"]
+
+
+@pytest.mark.parametrize("case", ATTN_COPY_CASES)
 def test_attention_copies_follow_sources_written_in_the_range(hip, orc, backend, bf16_attention,
                                                               case):
     """With attention on bf16 copies, the forward's copies of q, k and v
@@ -925,7 +931,7 @@ def test_attention_copies_follow_sources_written_in_the_range(hip, orc, backend,
     by one (each its own range, so every operand converted afresh), within
     the relaxed bar of the oracle, and counts each relaxed instruction once."""
     B, S, H, d = 2, 200, 2, 64
-    r = rng(hash(case) % 1000)
+    r = rng(ATTN_COPY_CASES.index(case) + 11)  # a fixed seed per case
     ar = Arena()
     prog = _attn_copies_program(ar, r, B, S, H, d, case)
     cpu, apart = execute(hip, orc, backend, ar, prog)
@@ -1183,7 +1189,10 @@ def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
     assert ranged.tobytes() == _restored(apart, ar, ["P1"], arena).tobytes()
 
 
-@pytest.mark.parametrize("between", ["gemm_elsewhere", "gemm_into_x", "add_into_x"])
+RECONVERT_CASES = ["gemm_elsewhere", "gemm_into_x", "add_into_x"]
+
+
+@pytest.mark.parametrize("between", RECONVERT_CASES)
 def test_relaxed_gemms_reconvert_after_their_activation_changes(hip, orc, backend, between):
     """Relaxed GEMMs of a range that round the same activation the same way
     share one bf16 conversion.  Anything between them that writes into the
@@ -1191,7 +1200,7 @@ def test_relaxed_gemms_reconvert_after_their_activation_changes(hip, orc, backen
     again: the range's bytes are those of the instructions run one by one."""
     from tests.plan_ops import ins
     M, K, N = 512, 1024, 768
-    r = rng(hash(between) % 1000)
+    r = rng(RECONVERT_CASES.index(between) + 21)  # a fixed seed per case
     ar = Arena()
     x = ar.add("x", r.standard_normal((M, K)).astype(np.float32))
     y = ar.add("y", r.standard_normal((M, 64)).astype(np.float32))
