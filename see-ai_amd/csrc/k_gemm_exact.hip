@@ -1214,14 +1214,16 @@ hipError_t LaunchFold(const GemmArgs& a, hipStream_t s) {
   if (a.M % 4 == 0 && a.N % 8 == 0 && a.K * a.M < (size_t{1} << 31) &&
       a.K * a.N < (size_t{1} << 31) && al16(a.A) && al16(a.B) && !a.a_k_scale &&
       (kLayout == 2 || a.K % 4 == 0)) {
-    // Role-split folds: 8 x 16 blocks (two outputs per folder lane) where
-    // they still fill the machine, else 4 x 8 (C5's 2048 x 16 and 16 x 2048
-    // gradients run 38 us against 55; C4's 768 x 8 and 8 x 768 20 us
-    // against 33).
+    // Role-split folds: 8 x 16 blocks (two outputs per folder lane, eight
+    // producer waves: the 512 tasks of a chunk in one round; seven took two
+    // rounds, the second 1/7 busy -- C5's 2048 x 16 and 16 x 2048 gradients
+    // 38.0 / 35.1 -> 35.6 / 32.8 us, its 8192 x 16 x 2048 t 44.2 -> 39.1) where
+    // they still fill the machine, else 4 x 8 with four producer waves (C4's
+    // 768 x 8 and 8 x 768 20 us against 33 on the one-pass fold).
     if (a.M % 8 == 0 && a.N % 16 == 0 && (a.M / 8) * (a.N / 16) >= 256) {
       const dim3 grid(static_cast<unsigned>(a.N / 16), static_cast<unsigned>(a.M / 8));
       if (grid.y > 65535) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((GemmFoldSplitKernel<kLayout, 8, 16, 256, 2, 4, 4, 8, 2>), grid, dim3(512),
+      hipLaunchKernelGGL((GemmFoldSplitKernel<kLayout, 8, 16, 256, 2, 4, 4, 9, 2>), grid, dim3(576),
                          0, s, a);
       return hipGetLastError();
     }
