@@ -150,6 +150,11 @@ struct seeai_ctx {
   // same way reuses it when every instruction between wrote elsewhere.
   void* cvt = nullptr;
   size_t cvt_bytes = 0;
+  // A second copy slot, filled only by a producer's second conversion sink
+  // (two outputs of one pass, each the activation of one of the two relaxed
+  // products after it), the same size as the first.
+  void* cvt2 = nullptr;
+  size_t cvt2_bytes = 0;
   // bf16 copies of relaxed attention's operands (q, k, v, dO: four slots of
   // B·S·H·64) for the bf16-operand kernels, and what they hold: the sources
   // and the instruction that converted them.
@@ -180,13 +185,13 @@ struct seeai_ctx {
     const float* src = nullptr;
     uint64_t at = 0, epoch = 0;
   } a16_pre[2];
-  struct {
+  struct CvtKey {
     const float* A = nullptr;
     uint64_t M = 0, K = 0;
     float alpha = 0.0f;
     const float* ks = nullptr;
     const uint8_t* at = nullptr;  // the converting instruction in the range; null: none
-  } cvt_key;
+  } cvt_key, cvt2_key;
   const uint8_t* cur_at = nullptr;  // the instruction being executed, when in the range
   uint64_t fused = 0;
   // bf16 copies [N, Kp] of frozen weights for the relaxed GEMMs, keyed by
@@ -254,6 +259,7 @@ int Hip(seeai_ctx* c, hipError_t e, const char* what) {
 // no bf16 copy made earlier may be taken for current.
 void ForgetCopies(seeai_ctx* c) {
   c->cvt_key.at = nullptr;
+  c->cvt2_key.at = nullptr;
   c->a16_key.at = nullptr;
   ++c->a16_epoch;
 }
@@ -356,8 +362,7 @@ uint64_t CurIndex(const seeai_ctx* c);
 // whose output misses A.  Anything else -- another opcode between, a write
 // into A, a copy of the instruction word run outside the range -- converts
 // again.
-bool ConvertedAlready(seeai_ctx* c, const GemmArgs& a) {
-  const auto& k = c->cvt_key;
+bool ConvertedAlready(seeai_ctx* c, const GemmArgs& a, const seeai_ctx::CvtKey& k) {
   if (!c->allow_fusion || !c->cur_at || !k.at || k.at >= c->cur_at || k.A != a.A || k.M != a.M ||
       k.K != a.K || k.alpha != a.alpha_a || k.ks != a.a_k_scale)
     return false;
@@ -388,7 +393,12 @@ int GemmBf16Dma(seeai_ctx* c, GemmArgs& a, const char* what) {
     SEEAI_TRY(c, LaunchWeightShadow(a, shadow, c->stream), "weight shadow");
   }
   const size_t need = a.M * Bf16DmaKp(a.K) * 2;
-  if (!ConvertedAlready(c, a)) {
+  // A copy a second conversion sink left in the second slot.
+  if (c->cvt2 && ConvertedAlready(c, a, c->cvt2_key)) {
+    SEEAI_TRY(c, LaunchGemmBf16Dma(c->cvt2, shadow, a, c->stream), what);
+    return SEEAI_OK;
+  }
+  if (!ConvertedAlready(c, a, c->cvt_key)) {
     if (need > c->cvt_bytes) {  // grow after draining the stream
       c->cvt_key.at = nullptr;
       DropGraphs(c);
@@ -778,8 +788,8 @@ const char* DecodeGemm(seeai_ctx* c, const Instruction& ins, GemmArgs* out) {
 }
 
 bool PlanSink(seeai_ctx* c, uint64_t last, uint64_t writer, const float* out, uint64_t n,
-              Bf16Sink* sink, GemmArgs* ga);
-void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a);
+              Bf16Sink* sink, GemmArgs* ga, int slot = 1, int site = 0);
+void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a, int slot = 1);
 // The index of the instruction being executed within its range's program
 // (c->cur_at set).
 uint64_t CurIndex(const seeai_ctx* c) { return static_cast<uint64_t>(c->cur_at - c->prog) / 64; }
@@ -1243,6 +1253,7 @@ void seeai_destroy(seeai_ctx* c) {
   if (c->source) (void)hipFree(c->source);
   if (c->scratch) (void)hipFree(c->scratch);
   if (c->cvt) (void)hipFree(c->cvt);
+  if (c->cvt2) (void)hipFree(c->cvt2);
   if (c->a16) (void)hipFree(c->a16);
   DropSavedCopies(c);
   DropShadows(c);
@@ -1592,33 +1603,54 @@ bool DeadStore(seeai_ctx* c, uint64_t at_idx, uint64_t from, const Extent& E, in
 // `sink` writes that product's bf16 copy into the conversion workspace as
 // the producer stores, and the f32 store is dropped where nothing after the
 // product reads `out` (the dead-store rule, decided for instruction
-// `writer`).  *ga: the product's arguments, for SinkDone.
+// `writer`, memoised under `site`).  Slot 2 (a producer's second sink): the
+// product is the one after the next, into the second workspace, and the
+// instruction between is a GEMM that neither reads nor writes `out` (so the
+// dead-store question starts after the product, and ConvertedAlready finds
+// the copy when the product runs).  *ga: the product's arguments,
+// for SinkDone.
 bool PlanSink(seeai_ctx* c, uint64_t last, uint64_t writer, const float* out, uint64_t n,
-              Bf16Sink* sink, GemmArgs* ga) {
-  if (!c->allow_fusion || !c->allow_sinks || !c->prog || last + 1 >= c->range_end) return false;
+              Bf16Sink* sink, GemmArgs* ga, int slot, int site) {
+  const uint64_t at = last + static_cast<uint64_t>(slot);
+  if (!c->allow_fusion || !c->allow_sinks || !c->prog || at >= c->range_end) return false;
+  if (slot == 2) {  // the product between: a GEMM clear of `out` (no read, no write)
+    Instruction mid;
+    std::memcpy(&mid, c->prog + (last + 1) * 64, sizeof mid);
+    GemmArgs m{};
+    Touch t[16];
+    int nt = 0;
+    if (!DecodeGemm(c, mid, &m) || !TouchExtents(c, mid, t, &nt)) return false;
+    for (int i = 0; i < nt; ++i)
+      if (Overlap(t[i].p, t[i].n, reinterpret_cast<const uint8_t*>(out), n * 4)) return false;
+  }
   Instruction nx;
-  std::memcpy(&nx, c->prog + (last + 1) * 64, sizeof nx);
+  std::memcpy(&nx, c->prog + at * 64, sizeof nx);
   GemmArgs a{};
   if (!DecodeGemm(c, nx, &a)) return false;
   a.relaxed = (nx.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
   a.policy = &c->policy;
   if (!a.relaxed || !c->allow_dma || !Bf16DmaFits(a) || !Immutable(c, a.B)) return false;
-  if (a.A != out || a.M * a.K != n || a.K % 32 != 0 || a.M * a.K * 2 > c->cvt_bytes) return false;
+  const size_t cap = slot == 2 ? c->cvt2_bytes : c->cvt_bytes;
+  if (a.A != out || a.M * a.K != n || a.K % 32 != 0 || a.M * a.K * 2 > cap) return false;
   if (reinterpret_cast<uintptr_t>(a.a_k_scale) & 15) return false;
-  sink->out = static_cast<uint16_t*>(c->cvt);
+  sink->out = static_cast<uint16_t*>(slot == 2 ? c->cvt2 : c->cvt);
   sink->ks = a.a_k_scale;
   sink->alpha = a.alpha_a;
   sink->K = static_cast<uint32_t>(a.K);
-  sink->store_f32 =
-      DeadStore(c, writer, last + 2, Extent{reinterpret_cast<const uint8_t*>(out), n * 4}) ? 0 : 1;
+  sink->store_f32 = DeadStore(c, writer, at + 1,
+                              Extent{reinterpret_cast<const uint8_t*>(out), n * 4}, site)
+                        ? 0
+                        : 1;
   *ga = a;
   return true;
 }
 
-// After a producer ran with its sink: the workspace holds the next
-// product's A' (its ConvertedAlready finds it, nothing between them).
-void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a) {
-  c->cvt_key = {a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->prog + last * 64};
+// After a producer ran with its sink: the workspace holds the product's A'
+// (its ConvertedAlready finds it; slot 2's product has the GEMM PlanSink
+// checked between them).
+void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a, int slot) {
+  (slot == 2 ? c->cvt2_key : c->cvt_key) =
+      seeai_ctx::CvtKey{a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->prog + last * 64};
   ++c->sinks;
 }
 
@@ -1850,13 +1882,19 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
     float* o1_store = o1;
     if (DeadStore(c, idx, idx + 3, Extent{reinterpret_cast<const uint8_t*>(o1), nb}))
       o1_store = nullptr;
-    Bf16Sink sink;
-    GemmArgs ga{};
-    const bool sunk = SwigluFits(n, {a1, b1, o1, a2, b2, o2, x, dx}) &&
-                      PlanSink(c, idx + 2, idx + 2, dx, n, &sink, &ga);
-    SEEAI_TRY(c, LaunchSwigluBwd(a1, b1, o1_store, a2, b2, o2, x, dx, n, c->stream, sink),
+    // dx feeds the product right after the pass; the other product (o2)
+    // commonly feeds the one after that: each takes a sink of its own.
+    Bf16Sink sink, sink2;
+    GemmArgs ga{}, ga2{};
+    const bool fits = SwigluFits(n, {a1, b1, o1, a2, b2, o2, x, dx});
+    const bool sunk = fits && PlanSink(c, idx + 2, idx + 2, dx, n, &sink, &ga);
+    const bool sunk2 = sunk && PlanSink(c, idx + 2, idx + (first ? 1 : 0), o2, n, &sink2, &ga2, 2, 1);
+    SEEAI_TRY(c,
+              LaunchSwigluBwd(a1, b1, o1_store, a2, b2, o2, x, dx, n, c->stream, sink,
+                              sunk2 ? sink2 : Bf16Sink{}),
               "swiglu_bwd");
     if (sunk) SinkDone(c, idx + 2, ga);
+    if (sunk2) SinkDone(c, idx + 2, ga2, 2);
     c->done[0] = at + 64;
     c->done[1] = at + 128;
     c->ndone = 2;
@@ -2155,6 +2193,16 @@ int PresizeWorkspaces(seeai_ctx* c, const uint8_t* prog, uint64_t begin, uint64_
     SEEAI_TRY(c, hipMalloc(&c->cvt, cvt), "conversion buffer alloc");
     c->cvt_bytes = cvt;
   }
+  if (cvt > c->cvt2_bytes) {
+    DropGraphs(c);
+    SEEAI_TRY(c, hipStreamSynchronize(c->stream), "conversion buffer drain");
+    c->cvt2_key.at = nullptr;
+    if (c->cvt2) SEEAI_TRY(c, hipFree(c->cvt2), "conversion buffer free");
+    c->cvt2 = nullptr;
+    c->cvt2_bytes = 0;
+    SEEAI_TRY(c, hipMalloc(&c->cvt2, cvt), "conversion buffer alloc");
+    c->cvt2_bytes = cvt;
+  }
   return SEEAI_OK;
 }
 }  // namespace
@@ -2266,7 +2314,7 @@ int seeai_execute_range(seeai_ctx* c, const void* instructions, uint64_t count,
                         const seeai_step_params* params, uint64_t* failed_at) {
   if (!c || (!instructions && count)) return SEEAI_INVALID;
   const auto* base = static_cast<const uint8_t*>(instructions);
-  seeai_begin_range(c, instructions, count, 0, count);
+  if (int rc = seeai_begin_range(c, instructions, count, 0, count)) return rc;
   for (uint64_t i = 0; i < count; ++i) {
     if (int rc = seeai_execute(c, base + i * 64, params)) {
       if (failed_at) *failed_at = i;

@@ -609,17 +609,22 @@ SiluMul4(const float4* __restrict__ x, const float4* __restrict__ u, float4* __r
 }
 
 // kStoreO1 false: the first product is dead after the pass and is not stored.
+// `sink` takes dx's bf16 copy, `sink2` the second product's (each with its
+// f32 store kept or dropped on its own).
 template <bool kStoreO1>
 __global__ void __launch_bounds__(kThreads)
 SwigluBwd4(const float4* __restrict__ a1, const float4* __restrict__ b1, float4* __restrict__ o1,
            const float4* __restrict__ a2, const float4* __restrict__ b2, float4* __restrict__ o2,
-           const float4* __restrict__ x, float4* __restrict__ dx, size_t n4, Bf16Sink sink) {
+           const float4* __restrict__ x, float4* __restrict__ dx, size_t n4, Bf16Sink sink,
+           Bf16Sink sink2) {
   const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
   for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
     const float4 p = a1[i], q = b1[i], r = a2[i], t = b2[i], v = x[i];
     const float4 m1 = make_float4(p.x * q.x, p.y * q.y, p.z * q.z, p.w * q.w);
     if constexpr (kStoreO1) o1[i] = m1;
-    o2[i] = make_float4(r.x * t.x, r.y * t.y, r.z * t.z, r.w * t.w);
+    const float4 m2 = make_float4(r.x * t.x, r.y * t.y, r.z * t.z, r.w * t.w);
+    if (sink2.store_f32) o2[i] = m2;
+    if (sink2.out) SinkStore4(sink2, 4 * i, m2);
     const float4 d = make_float4(SiluBwdExpr(m1.x, v.x), SiluBwdExpr(m1.y, v.y),
                                  SiluBwdExpr(m1.z, v.z), SiluBwdExpr(m1.w, v.w));
     if (sink.store_f32) dx[i] = d;
@@ -701,7 +706,7 @@ hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, siz
 }
 hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const float* a2,
                            const float* b2, float* o2, const float* x, float* dx, size_t n,
-                           hipStream_t s, const Bf16Sink& sink) {
+                           hipStream_t s, const Bf16Sink& sink, const Bf16Sink& sink2) {
   if (SwigluFits(n, {a1, b1, o1, a2, b2, o2, x, dx})) {
     if (n == 0) return hipSuccess;
     const auto c4 = [](const float* p) { return reinterpret_cast<const float4*>(p); };
@@ -709,13 +714,13 @@ hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const fl
     const dim3 grid(GridFor(n / 4, kThreads, 8192));
     if (o1)
       hipLaunchKernelGGL(SwigluBwd4<true>, grid, dim3(kThreads), 0, s, c4(a1), c4(b1), m4(o1),
-                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4, sink);
+                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4, sink, sink2);
     else
       hipLaunchKernelGGL(SwigluBwd4<false>, grid, dim3(kThreads), 0, s, c4(a1), c4(b1), m4(o1),
-                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4, sink);
+                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4, sink, sink2);
     return hipGetLastError();
   }
-  if (sink.out || !sink.store_f32) return hipErrorInvalidValue;
+  if (sink.out || !sink.store_f32 || sink2.out || !sink2.store_f32) return hipErrorInvalidValue;
   return Map(n, s, [=] __device__(size_t i) {
     const float m1 = a1[i] * b1[i];
     if (o1) o1[i] = m1;

@@ -326,6 +326,9 @@ class HipBackend:
     def dropped_stores(self) -> int:
         return int(_lib.seeai_dropped_stores(self.ctx.h))
 
+    def fused_conversions(self) -> int:
+        return int(_lib.seeai_fused_conversions(self.ctx.h))
+
     def SetFusion(self, allow: bool):
         self.ctx.call("seeai_set_fusion", int(bool(allow)))
 

@@ -1263,6 +1263,57 @@ def test_swiglu_chains_fuse_bitwise(hip, orc, backend, n, order, read_later):
         assert e <= TOL, f"{name}: {e:.3g}"
 
 
+SWIGLU_SINK_CASES = ["plain", "dup_read_later", "products_swapped", "first_writes_dup"]
+
+
+@pytest.mark.parametrize("case", SWIGLU_SINK_CASES)
+def test_swiglu_backward_writes_both_products_copies(hip, orc, backend, case):
+    """SwiGLU's backward pass (dsg = dh * u, dup = dh * y, dg = SiluBwd(dsg,
+    g)) ahead of its two relaxed q8 NT products -- dg Wg^T, then dup Wu^T --
+    writes the bf16 copies both products read as it stores, and drops the f32
+    stores nothing reads: the products skip their conversion passes.  The
+    range's bytes are those of the instructions one by one (dropped stores
+    put back).  dup read after the products keeps its store; with the
+    products in the other order neither copy is written; a first product
+    writing into dup leaves the second to convert what it finds there."""
+    from tests.plan_ops import ins
+    M, F, D = 256, 1024, 512
+    r = rng(SWIGLU_SINK_CASES.index(case) + 41)  # a fixed seed per case
+    ar = Arena()
+    n = M * F
+    g, u, dh, y = (ar.add(k, r.standard_normal(n).astype(np.float32)) for k in ("g", "u", "dh", "y"))
+    dsg, dup, dg = (ar.empty(k, (n,)) for k in ("dsg", "dup", "dg"))
+    wg = ar.add("Wg", r.integers(-127, 128, (D, F)).astype(np.int8), rodata=True)
+    wu = ar.add("Wu", r.integers(-127, 128, (D, F)).astype(np.int8), rodata=True)
+    kg = ar.add("kg", r.uniform(1e-3, 5e-2, F).astype(np.float32), rodata=True)
+    ku = ar.add("ku", r.uniform(1e-3, 5e-2, F).astype(np.float32), rodata=True)
+    xg, xu = ar.empty("xg", (M, D)), ar.empty("xu", (M, D))
+    rx = (1 << 5) | (1 << 4)
+    first = ins(30, [dg, wg, dup if case == "first_writes_dup" else xg, kg], [M, D, F], flags=rx)
+    second = ins(30, [dup, wu, xu, ku], [M, D, F], flags=rx)
+    products = [second, first] if case == "products_swapped" else [first, second]
+    prog = [ins(21, [dh, u, dsg], [n]), ins(21, [dh, y, dup], [n]), ins(25, [dsg, g, dg], [n])]
+    prog += products
+    if case == "dup_read_later":
+        prog += _readers(ar, ["dup"])
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    convs, drops = backend.fused_conversions(), backend.dropped_stores()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    sinks = {"plain": 2, "dup_read_later": 2, "products_swapped": 0, "first_writes_dup": 1}[case]
+    dead = {"plain": ["dsg", "dg", "dup"], "dup_read_later": ["dsg", "dg"],
+            "products_swapped": ["dsg"], "first_writes_dup": ["dsg", "dg"]}[case]
+    assert backend.fused_conversions() - convs == sinks
+    assert backend.dropped_stores() - drops == len(dead)
+    assert ranged.tobytes() == _restored(apart, ar, dead, arena).tobytes()
+    for name in ("dup" if case == "first_writes_dup" else "xg", "xu"):
+        e = maxrel(ar.get(ranged, name), ar.get(cpu, name))
+        assert e <= TOL_BF16, f"{name}: {e:.3g}"
+
+
 def test_swiglu_chain_refuses_to_fuse_over_an_input(hip, orc, backend):
     """h written over u, which the product reads: one pass would still be
     right element by element, but the rule is simple -- an output touching an
