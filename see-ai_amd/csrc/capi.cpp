@@ -1727,8 +1727,9 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
       // before anything reads it.
       if (DeadStore(c, idx, j + 1, out_a, 1)) a.lr_store_c = 0;
       // A residual add of C' next (kAddEW, C' on one side, C' read by
-      // nothing after it; NT sites, the dX chains) joins the epilogue: the
-      // add's output takes R + C' in C''s place.  Its output may be R
+      // nothing after it: the dX chains on NT sites, the forward's residual
+      // behind an NN site of rank 8 or 16 with a plain epilogue) joins the
+      // epilogue: the add's output takes R + C' in C''s place.  Its output may be R
       // itself, or C when C's store is dropped; it misses everything else
       // the pass reads.
       bool res_add = false;
@@ -1736,7 +1737,7 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
         Instruction ad;
         std::memcpy(&ad, c->prog + (j + 1) * 64, sizeof ad);
         const Ptrs R{c};
-        if (ad.opcode == 5 && ad.out[0] == a.M * a.N && b.layout == 1 &&
+        if (ad.opcode == 5 && ad.out[0] == a.M * a.N &&
             (R.f(ad.in[0]) == b.C) != (R.f(ad.in[1]) == b.C)) {
           const float* res = R.f(ad.in[0]) == b.C ? R.f(ad.in[1]) : R.f(ad.in[0]);
           float* aout = R.f(ad.in[2]);

@@ -392,7 +392,8 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
   if constexpr (kLR != 0) {
     // Rank 8 or 16 with nothing but the column scale and alpha before the
     // low-rank term: the rank is a constant, so each pass is one block of
-    // four independent chains.
+    // four independent chains; a residual behind the site (NN or NT) adds
+    // last.
     const bool plain = !add && !g.accumulate && !bias && !g.act;
     auto fast = [&](auto rq_tag) {
       constexpr int RQ = decltype(rq_tag)::value;
@@ -405,6 +406,22 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
           const float4 c4v = *reinterpret_cast<const float4*>(cs + n);
           csq[0] = c4v.x, csq[1] = c4v.y, csq[2] = c4v.z, csq[3] = c4v.w;
         }
+      }
+      // The residual, kResAhead quads in flight ahead of their use in the
+      // lane's sequence of (pass, row) steps (each element read before this
+      // lane writes it, also where the output is the residual itself).
+      constexpr int kSteps = 32 / kRowsPerPass, kResAhead = 4;
+      float4 rr[kResAhead];
+      auto res_load = [&](int s) {
+        const int m = m0 + wm + (s / kSteps) * 32 + row0 + (s % kSteps) * kRowsPerPass;
+        const int n = n0 + wn + c4 * 4;
+        return epi_lane && m < M && n < N && s < TM * kSteps
+                   ? *reinterpret_cast<const float4*>(g.lr_res + static_cast<size_t>(m) * N + n)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+      };
+      if (g.lr_res) {
+#pragma unroll
+        for (int s = 0; s < kResAhead; ++s) rr[s] = res_load(s);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
@@ -440,8 +457,10 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             o4[e] = AddRn(v[e], LowRankDot<kLR - 1>(t, lb[e], 4 * RQ, g.lr_alpha));
-          if (kLR == 2 && g.lr_res) {
-            const float4 r4 = *reinterpret_cast<const float4*>(g.lr_res + o);
+          if (g.lr_res) {
+            const int s = i * kSteps + tt;
+            const float4 r4 = rr[s % kResAhead];
+            if (s + kResAhead < TM * kSteps) rr[s % kResAhead] = res_load(s + kResAhead);
             o4[0] = AddRn(r4.x, o4[0]), o4[1] = AddRn(r4.y, o4[1]);
             o4[2] = AddRn(r4.z, o4[2]), o4[3] = AddRn(r4.w, o4[3]);
           }
@@ -499,8 +518,9 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           o4[e] = AddRn(v[e], LowRankDot<kLR - 1>(t, lb[e], lr_r, g.lr_alpha));
-        // (NT sites only: in the NN instance the extra operand pushes the
-        // 256 x 256 tile into scratch.)
+        // (NT sites only here: in the NN instance the extra operand pushes
+        // the general pass's 256 x 256 tile into scratch; NN sites with a
+        // residual take the constant-rank pass above.)
         if (kLR == 2 && g.lr_res) {
           const float4 r4 = *reinterpret_cast<const float4*>(g.lr_res + o);
           o4[0] = AddRn(r4.x, o4[0]), o4[1] = AddRn(r4.y, o4[1]);
@@ -671,7 +691,12 @@ bool Bf16DmaLowRankFits(const GemmArgs& a) {
   return a.lr_out && a.lr_t && a.lr_b && a.lr_layout >= 0 && a.lr_layout <= 1 && a.lr_k >= 1 &&
          a.lr_k <= kLowRankMaxK && a.lr_k % 4 == 0 && a.N % 4 == 0 && !a.accumulate &&
          al16(a.lr_t) && al16(a.lr_out) && al16(a.C) && (a.lr_layout == 1 || al16(a.lr_b)) &&
-         al16(a.lr_res);
+         al16(a.lr_res) &&
+         // A residual on an NN site rides the constant-rank pass only (rank 8
+         // or 16 with no addend, bias or activation); the general pass adds
+         // it on NT sites alone.
+         (!a.lr_res || a.lr_layout == 1 ||
+          ((a.lr_k == 8 || a.lr_k == 16) && !a.addend && !a.bias && !a.act));
 }
 
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,

@@ -1378,16 +1378,19 @@ def test_bias_add_runs_in_the_product_epilogue(hip, orc, backend, relaxed, form)
     assert e <= (TOL_BF16 if relaxed else TOL), f"{name}: {e:.3g}"
 
 
-@pytest.mark.parametrize("producer", ["gemm", "gemm_relaxed", "lora_site", "rmsnorm_bwd",
-                                      "layernorm_bwd"])
+@pytest.mark.parametrize("producer", ["gemm", "gemm_relaxed", "lora_site", "lora_site_nn",
+                                      "lora_site_nn_r12", "rmsnorm_bwd", "layernorm_bwd"])
 @pytest.mark.parametrize("form", ["res_first", "res_second", "in_place", "read_later"])
 def test_residual_adds_run_inside_their_producers(hip, orc, backend, producer, form):
     """kAddEW of a producer's output and a residual R, with the output read by
     nothing after the add, runs inside the producer: a GEMM takes R as its
     addend and writes the add's output; a normalisation's backward writes
-    R + dx.  Bitwise the instructions one by one (the producer's own output
-    keeps its old bytes), one fused dispatch; R on either side of the add,
-    the add written over R; with the output read again, the two run apart."""
+    R + dx; a LoRA site (the dX chain's NT form, the forward's NN form at
+    rank 16) adds R last in its epilogue.  Bitwise the instructions one by
+    one (the producer's own output keeps its old bytes), one fused dispatch;
+    R on either side of the add, the add written over R; with the output read
+    again, the two run apart -- as an NN site of rank 12 always does (its
+    general epilogue takes no residual)."""
     from tests.plan_ops import ins
     rows, cols = 256, 256
     n = rows * cols
@@ -1411,6 +1414,20 @@ def test_residual_adds_run_inside_their_producers(hip, orc, backend, producer, f
         p1 = ar.empty("P1", (rows, cols))
         prog = [ins(30, [dC, w, p1, ws], [rows, cols, K], flags=rx | cs_flag),
                 ins(2, [dt, A, prod, p1], [rows, cols, rank], flags=1 << 3)]
+        dead_too = ["P1"]
+    elif producer.startswith("lora_site_nn"):
+        # the forward's O site: the frozen q8 NN product, the exact rank-r
+        # NN term t B added to it, then the residual
+        rx, cs_flag = 1 << 5, 1 << 4
+        K, rank = 768, 12 if producer.endswith("r12") else 16
+        X = ar.add("X", r.standard_normal((rows, K)).astype(np.float32))
+        t = ar.add("t", r.standard_normal((rows, rank)).astype(np.float32))
+        B = ar.add("B", (r.standard_normal((rank, cols)) * 0.02).astype(np.float32))
+        w = ar.add("W", r.integers(-127, 128, (K, cols)).astype(np.int8), rodata=True)
+        ws = ar.add("Ws", r.uniform(1e-3, 5e-2, cols).astype(np.float32), rodata=True)
+        p1 = ar.empty("P1", (rows, cols))
+        prog = [ins(29, [X, w, p1, ws], [rows, cols, K], flags=rx | cs_flag),
+                ins(1, [t, B, prod, p1], [rows, cols, rank], flags=1 << 3)]
         dead_too = ["P1"]
     elif producer.startswith("gemm"):
         K = 128
@@ -1443,15 +1460,15 @@ def test_residual_adds_run_inside_their_producers(hip, orc, backend, producer, f
     backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
     backend.Flush()
     ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
-    fused = form != "read_later"
+    fused = form != "read_later" and producer != "lora_site_nn_r12"
     # the site folds either way; the add joins it unless P is read again
-    assert backend.fused_dispatches() - before == int(fused or producer == "lora_site")
+    assert backend.fused_dispatches() - before == int(fused or producer.startswith("lora_site"))
     dead = (["P"] if fused else []) + dead_too
     diff = np.flatnonzero(ranged != _restored(apart, ar, dead, arena))
     assert diff.size == 0, f"{diff.size} bytes differ from byte {diff[:1]}"
     name = "R" if form == "in_place" else "out"
     e = maxrel(ar.get(ranged, name), ar.get(cpu, name))
-    relaxed = producer in ("gemm_relaxed", "lora_site")
+    relaxed = producer == "gemm_relaxed" or producer.startswith("lora_site")
     assert e <= (TOL_BF16 if relaxed else TOL), f"{name}: {e:.3g}"
 
 
