@@ -1658,10 +1658,11 @@ void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a, int slot) {
 // backend.h:139-142; the reference's Metal backend folds the same pair,
 // metal_kernels.h:290-358, docs/runtime.md:119).  A relaxed frozen-weight
 // product writing C on the direct-to-LDS kernel, followed -- next, or after
-// one exact GEMM (the site's t = x A) that neither touches C nor writes what
-// the product reads -- by an exact rank-r GEMM (NN or NT, r <= 16, no bias or
-// activation) whose addend is C, runs as one dispatch: the in-between GEMM
-// first, then the frozen product with the rank-r term in its epilogue, which
+// up to three exact GEMMs (the site's t = x A; on a backward site its dt, dB
+// and dA) that neither touch C nor write what the product reads -- by an
+// exact rank-r GEMM (NN or NT, r <= 16, no bias or activation) whose addend
+// is C, runs as one dispatch: the in-between GEMMs first, in their order,
+// then the frozen product with the rank-r term in its epilogue, which
 // forms C as before, stores it, and writes C' = C + the rank-r product in the
 // rank-r instruction's own chain.  The arena holds the bytes of the separate
 // dispatches.  Refused (each runs at its place) when an output overlaps
@@ -1682,7 +1683,9 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
   Extent reads_a[8];
   const int na = GemmReads(a, reads_a);
   const Extent out_a = GemmWrites(a);
-  for (uint64_t gap = 0; gap <= 1; ++gap) {
+  constexpr uint64_t kMaxGap = 3;
+  Instruction mids[kMaxGap];
+  for (uint64_t gap = 0; gap <= kMaxGap; ++gap) {
     const uint64_t j = idx + 1 + gap;
     if (j >= c->range_end) return -1;
     Instruction nj;
@@ -1693,19 +1696,6 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
       GemmArgs b{};
       DecodeGemm(c, nj, &b);
       if (b.M != a.M || b.N != a.N || b.bias) return -1;
-      Instruction mid{};
-      GemmArgs m{};
-      if (gap) {  // the in-between instruction: an exact GEMM clear of the product
-        std::memcpy(&mid, c->prog + (idx + 1) * 64, sizeof mid);
-        if (!DecodeGemm(c, mid, &m) || ((mid.flags & kFlagRelaxed) && c->allow_relaxed))
-          return -1;
-        Extent reads_m[8];
-        const int nm = GemmReads(m, reads_m);
-        const Extent out_m = GemmWrites(m);
-        if (Hits(out_m, reads_a, na) || Overlap(out_m.p, out_m.n, out_a.p, out_a.n) ||
-            Hits(out_a, reads_m, nm))
-          return -1;
-      }
       a.lr_t = b.A;
       a.lr_b = static_cast<const float*>(b.B);
       a.lr_out = b.C;
@@ -1757,18 +1747,30 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
           }
         }
       }
-      if (gap) {
-        if (int rc = ExecuteOne(c, mid, P)) return rc;
-      }
+      for (uint64_t g = 0; g < gap; ++g)
+        if (int rc = ExecuteOne(c, mids[g], P)) return rc;
       Relaxed(c, ins);
       if (int rc = GemmBf16Dma(c, a, "gemm.low_rank")) return rc;
       c->ndone = 0;
-      if (gap) c->done[c->ndone++] = c->prog + (idx + 1) * 64;
+      for (uint64_t g = 0; g < gap; ++g) c->done[c->ndone++] = c->prog + (idx + 1 + g) * 64;
       c->done[c->ndone++] = c->prog + j * 64;
       if (res_add) c->done[c->ndone++] = c->prog + (j + 1) * 64;
       ++c->fused;
       return SEEAI_OK;
     }
+    // Not the rank-r GEMM: it may sit between the two as an exact GEMM that
+    // writes nothing the product reads or writes and reads nothing the
+    // product writes (it then runs first).
+    if (gap == kMaxGap) return -1;
+    GemmArgs m{};
+    if (!DecodeGemm(c, nj, &m) || ((nj.flags & kFlagRelaxed) && c->allow_relaxed)) return -1;
+    Extent reads_m[8];
+    const int nm = GemmReads(m, reads_m);
+    const Extent out_m = GemmWrites(m);
+    if (Hits(out_m, reads_a, na) || Overlap(out_m.p, out_m.n, out_a.p, out_a.n) ||
+        Hits(out_a, reads_m, nm))
+      return -1;
+    mids[gap] = nj;
   }
   return -1;
 }

@@ -1189,6 +1189,64 @@ def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
     assert ranged.tobytes() == _restored(apart, ar, ["P1"], arena).tobytes()
 
 
+GAP_CASES = ["grads_between", "one_between", "mid_reads_c", "mid_writes_dc", "four_between"]
+
+
+@pytest.mark.parametrize("case", GAP_CASES)
+def test_lora_dx_site_folds_over_the_adapter_gradients(hip, orc, backend, case):
+    """An input-gradient site as the plan writer lowers the O projection's:
+    the frozen q8 NT product P1 = dC W^T, then the adapter GEMMs dt = dC B^T,
+    dB = t^T dC and dA = x^T dt, then P2 = P1 + dt A^T.  The three exact
+    GEMMs run first and the product folds with the rank-r term (one fused
+    dispatch, P1 dropped): bitwise the instructions one by one.  Refused --
+    every instruction at its place -- when an in-between GEMM reads P1 (it
+    would read it before the product writes it), writes dC (the product's
+    operand), or when four GEMMs sit between."""
+    from tests.plan_ops import ins
+    M, D, r_ = 512, 1024, 16
+    r = rng(GAP_CASES.index(case) + 61)  # a fixed seed per case
+    rx, cs_flag = 1 << 5, 1 << 4
+    ar = Arena()
+    dC = ar.add("dC", r.standard_normal((M, D)).astype(np.float32))
+    x = ar.add("x", r.standard_normal((M, D)).astype(np.float32))
+    t = ar.add("t", r.standard_normal((M, r_)).astype(np.float32))
+    A = ar.add("A", (r.standard_normal((D, r_)) * 0.02).astype(np.float32))
+    B = ar.add("B", (r.standard_normal((r_, D)) * 0.02).astype(np.float32))
+    w = ar.add("W", r.integers(-127, 128, (D, D)).astype(np.int8), rodata=True)
+    ws = ar.add("Ws", r.uniform(1e-3, 5e-2, D).astype(np.float32), rodata=True)
+    p1, p2 = ar.empty("P1", (M, D)), ar.empty("P2", (M, D))
+    dt, dB, dA = ar.empty("dt", (M, r_)), ar.empty("dB", (r_, D)), ar.empty("dA", (D, r_))
+    dt2 = ar.empty("dt2", (M, r_))
+    mids = [ins(2, [dC, B, dt], [M, r_, D]),
+            ins(3, [p1 if case == "mid_reads_c" else t, dC, dB], [r_, D, M]),
+            ins(3, [x, dt, dA], [D, r_, M])]
+    if case == "one_between":
+        mids = mids[:1]
+    elif case == "mid_writes_dc":
+        mids[1] = ins(1, [t, B, dC], [M, D, r_])
+    elif case == "four_between":
+        mids.append(ins(2, [dC, B, dt2], [M, r_, D]))
+    prog = ([ins(30, [dC, w, p1, ws], [M, D, D], flags=rx | cs_flag)] + mids +
+            [ins(2, [dt, A, p2, p1], [M, D, r_], flags=1 << 3)])
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    before = backend.fused_dispatches()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    folds = case in ("grads_between", "one_between")
+    assert backend.fused_dispatches() - before == int(folds)
+    dead = ["P1"] if folds else []
+    assert ranged.tobytes() == _restored(apart, ar, dead, arena).tobytes()
+    e = maxrel(ar.get(ranged, "P2"), ar.get(cpu, "P2"))
+    assert e <= TOL_BF16, f"P2: {e:.3g}"
+    # the exact adapter GEMMs against the oracle (dB reads the relaxed P1
+    # where the case makes it)
+    for name in ("dt", "dA") + (() if case == "mid_reads_c" else ("dB",)):
+        assert bits_equal(ar.get(ranged, name), ar.get(cpu, name)), name
+
+
 RECONVERT_CASES = ["gemm_elsewhere", "gemm_into_x", "add_into_x"]
 
 
