@@ -179,12 +179,14 @@ struct seeai_ctx {
   std::vector<A16Saved> a16_saved;
   uint64_t a16_saved_cap = uint64_t{4} << 30;  // bytes over every saved triple
   uint64_t a16_epoch = 1;
-  // Operand copies a RoPE forward wrote into the saved copies of the
-  // attention forward at instruction `at` (slot 0 q, 1 k), in this epoch.
+  // Operand copies a producer wrote for the attention at instruction `at`,
+  // in this epoch: a RoPE forward's q or k (slots 0, 1) and a LoRA site's v
+  // (slot 2) into the forward's saved copies, a LoRA site's dO (slot 3) into
+  // the operand buffer's dO slot.
   struct {
     const float* src = nullptr;
     uint64_t at = 0, epoch = 0;
-  } a16_pre[2];
+  } a16_pre[4];
   struct CvtKey {
     const float* A = nullptr;
     uint64_t M = 0, K = 0;
@@ -512,6 +514,12 @@ int Attn16Operands(seeai_ctx* c, const float* const src[4], unsigned need, uint6
     out[i] = static_cast<uint16_t*>(c->a16) + static_cast<size_t>(i) * n;
     if (!(need & (1u << i))) continue;
     if (keep && c->a16_key.src[i] == src[i]) continue;
+    if (i == 3 && c->cur_at && c->a16_pre[3].src == src[3] && c->a16_pre[3].at == CurIndex(c) &&
+        c->a16_pre[3].epoch == c->a16_epoch) {
+      c->a16_pre[3].src = nullptr;  // written by the LoRA site just before
+      ++c->sinks;
+      continue;
+    }
     SEEAI_TRY(c,
               LaunchConvertRowsBf16(src[i], rows, cols, 1.0f, nullptr, out[i],
                                     c->policy.convert_wgs_per_cu, c->stream),
@@ -632,6 +640,64 @@ uint16_t* RopeAttnCopy(seeai_ctx* c, const float* x, const float* y, uint64_t B,
     c->a16_pre[slot].at = a;
     c->a16_pre[slot].epoch = c->a16_epoch;
     return static_cast<uint16_t*>(sv->buf) + static_cast<size_t>(slot) * n;
+  }
+  return nullptr;
+}
+
+// A LoRA site's output y (n floats, the fused pass's last instruction at
+// `last`) read by a bf16-copy attention: as v by a forward within three
+// instructions (those between write neither y nor the copies -- the RoPE
+// forwards, which write the q and k slots), or as dO by a backward right
+// after.  The site's epilogue then writes y's bf16 copy where that attention
+// takes it: the forward's saved copies (slot 2), the operand buffer's dO
+// slot (slot 3).  Returns the copy's address with *slot and the attention's
+// index *at, or null.
+uint16_t* PlanAttnCopy(seeai_ctx* c, uint64_t last, const float* y, uint64_t n, int* slot,
+                       uint64_t* at) {
+  if (!c->allow_fusion || !c->allow_sinks || !c->prog) return nullptr;
+  const Ptrs R{c};
+  for (uint64_t f = last + 1; f <= last + 3 && f < c->range_end; ++f) {
+    Instruction ins;
+    std::memcpy(&ins, c->prog + f * 64, sizeof ins);
+    if (ins.opcode == 47 || ins.opcode == 57) {
+      uint64_t aB, aS, aH, ad;
+      if (ins.opcode == 47) {
+        aB = ins.out[1] >> 32, aS = ins.out[1] & 0xFFFFFFFFu, aH = ins.out[2] >> 32,
+        ad = ins.out[2] & 0xFFFFFFFFu;
+      } else {
+        const uint64_t g = ins.out[1];
+        aB = g >> 48, aS = (g >> 32) & 0xFFFF, aH = (g >> 16) & 0xFFFF, ad = g & 0xFFFF;
+      }
+      if (aB * aS * aH * ad != n || !IsRelaxedAttention(c, ins) || !Attn16Plan(c, aB, aS, aH, ad))
+        return nullptr;
+      const float* src[3] = {R.f(ins.in[0]), R.f(ins.in[1]), R.f(ins.in[2])};
+      if (src[2] != y || src[0] == y || src[1] == y) return nullptr;
+      seeai_ctx::A16Saved* sv = SavedCopies(c, src[0], src[1], src[2], n);
+      if (!sv) return nullptr;
+      *slot = 2;
+      *at = f;
+      return static_cast<uint16_t*>(sv->buf) + 2 * static_cast<size_t>(n);
+    }
+    if (f == last + 1 && (ins.opcode == 48 || ins.opcode == 49 || ins.opcode == 50)) {
+      const uint64_t g = ins.out[2];
+      const uint64_t B = g >> 48, S = (g >> 32) & 0xFFFF, H = (g >> 16) & 0xFFFF, d = g & 0xFFFF;
+      if (B * S * H * d != n || !IsRelaxedAttention(c, ins) || !Attn16Plan(c, B, S, H, d) ||
+          (ins.opcode == 50 && ins.in[2] == kNullRef))
+        return nullptr;
+      if (R.f(ins.in[3]) != y || R.f(ins.in[0]) == y || R.f(ins.in[1]) == y ||
+          R.f(ins.in[2]) == y)
+        return nullptr;
+      if (!c->a16 || c->a16_bytes < 4 * n * 2) return nullptr;  // sized by an earlier run
+      *slot = 3;
+      *at = f;
+      return static_cast<uint16_t*>(c->a16) + 3 * static_cast<size_t>(n);
+    }
+    Touch t[16];
+    int nt = 0;
+    if (!TouchExtents(c, ins, t, &nt)) return nullptr;
+    for (int j = 0; j < nt; ++j)
+      if (t[j].write && Overlap(t[j].p, t[j].n, reinterpret_cast<const uint8_t*>(y), n * 4))
+        return nullptr;
   }
   return nullptr;
 }
@@ -1106,9 +1172,9 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
         if (sv) {  // into the copies the backward of this range run may take
           for (int i = 0; i < 3; ++i) {
             b16[i] = static_cast<uint16_t*>(sv->buf) + static_cast<size_t>(i) * n;
-            if (i < 2 && c->a16_pre[i].src == src[i] && c->a16_pre[i].at == CurIndex(c) &&
+            if (c->a16_pre[i].src == src[i] && c->a16_pre[i].at == CurIndex(c) &&
                 c->a16_pre[i].epoch == c->a16_epoch) {
-              c->a16_pre[i].src = nullptr;  // written by the RoPE forward just before
+              c->a16_pre[i].src = nullptr;  // written by a RoPE forward or a LoRA site before
               ++c->sinks;
               continue;
             }
@@ -1747,10 +1813,25 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
           }
         }
       }
+      // The site's output read next by a bf16-copy attention: its copy is
+      // written in the epilogue (the constant-rank pass only).
+      int pre_slot = -1;
+      uint64_t pre_at = 0;
+      {
+        GemmArgs t = a;
+        t.lr_sink = PlanAttnCopy(c, res_add ? j + 1 : j, a.lr_out, a.M * a.N, &pre_slot, &pre_at);
+        if (t.lr_sink && Bf16DmaLowRankFits(t)) a = t;
+        else pre_slot = -1;
+      }
       for (uint64_t g = 0; g < gap; ++g)
         if (int rc = ExecuteOne(c, mids[g], P)) return rc;
       Relaxed(c, ins);
       if (int rc = GemmBf16Dma(c, a, "gemm.low_rank")) return rc;
+      if (pre_slot >= 0) {
+        c->a16_pre[pre_slot].src = a.lr_out;
+        c->a16_pre[pre_slot].at = pre_at;
+        c->a16_pre[pre_slot].epoch = c->a16_epoch;
+      }
       c->ndone = 0;
       for (uint64_t g = 0; g < gap; ++g) c->done[c->ndone++] = c->prog + (idx + 1 + g) * 64;
       c->done[c->ndone++] = c->prog + j * 64;

@@ -168,6 +168,13 @@ __device__ __forceinline__ void SinkStore4(const Bf16Sink& s, size_t i, float4 v
   for (int e = 0; e < 4; ++e) o[e] = static_cast<__bf16>(s.alpha != 1.0f ? s.alpha * x[e] : x[e]);
   *reinterpret_cast<bf16x4_t*>(s.out + i) = o;
 }
+// Four floats rounded to bf16 (nearest even) in one 8-byte store.
+__device__ __forceinline__ void StoreBf16x4(uint16_t* dst, const float v[4]) {
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  const bf16x4_t o = {static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1]),
+                      static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
+  *reinterpret_cast<bf16x4_t*>(dst) = o;
+}
 
 // Elementwise family (k_elementwise.hip).
 hipError_t LaunchAddEW(const float* x, const float* y, float* out, size_t n, hipStream_t s,
@@ -343,6 +350,9 @@ struct GemmArgs {
   // A residual add behind the site (NT sites): lr_out = lr_res + (C + dot),
   // the add's operand order immaterial (IEEE addition commutes); null: none.
   const float* lr_res;
+  // lr_out's bf16 copy (round to nearest even, same [M, N] layout) for the
+  // attention that reads it next; null: none.
+  uint16_t* lr_sink;
 };
 constexpr int kLowRankMaxK = 16;
 // Relaxed -> MFMA (k_gemm_f32.hip); otherwise the reference's order.

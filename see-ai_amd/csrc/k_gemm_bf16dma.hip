@@ -410,7 +410,7 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
       // The residual, kResAhead quads in flight ahead of their use in the
       // lane's sequence of (pass, row) steps (each element read before this
       // lane writes it, also where the output is the residual itself).
-      constexpr int kSteps = 32 / kRowsPerPass, kResAhead = 4;
+      constexpr int kSteps = 32 / kRowsPerPass, kResAhead = kLR == 1 ? 4 : 2;
       float4 rr[kResAhead];
       auto res_load = [&](int s) {
         const int m = m0 + wm + (s / kSteps) * 32 + row0 + (s % kSteps) * kRowsPerPass;
@@ -465,6 +465,7 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
             o4[2] = AddRn(r4.z, o4[2]), o4[3] = AddRn(r4.w, o4[3]);
           }
           *reinterpret_cast<float4*>(g.lr_out + o) = make_float4(o4[0], o4[1], o4[2], o4[3]);
+          if (g.lr_sink) StoreBf16x4(g.lr_sink + o, o4);
         }
         __builtin_amdgcn_wave_barrier();
       }
@@ -686,17 +687,24 @@ bool Bf16DmaFits(const GemmArgs& a) {
   return ((a.M + 127) / 128) * ((a.N + 127) / 128) < (size_t{1} << 31);
 }
 
+// The epilogue's constant-rank pass: rank 8 or 16 behind nothing but the
+// column scale and alpha.
+bool LowRankConstPass(const GemmArgs& a) {
+  return (a.lr_k == 8 || a.lr_k == 16) && !a.addend && !a.bias && !a.act && !a.accumulate;
+}
+
 bool Bf16DmaLowRankFits(const GemmArgs& a) {
   const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   return a.lr_out && a.lr_t && a.lr_b && a.lr_layout >= 0 && a.lr_layout <= 1 && a.lr_k >= 1 &&
          a.lr_k <= kLowRankMaxK && a.lr_k % 4 == 0 && a.N % 4 == 0 && !a.accumulate &&
          al16(a.lr_t) && al16(a.lr_out) && al16(a.C) && (a.lr_layout == 1 || al16(a.lr_b)) &&
-         al16(a.lr_res) &&
+         al16(a.lr_res) && (reinterpret_cast<uintptr_t>(a.lr_sink) & 7) == 0 &&
          // A residual on an NN site rides the constant-rank pass only (rank 8
-         // or 16 with no addend, bias or activation); the general pass adds
-         // it on NT sites alone.
-         (!a.lr_res || a.lr_layout == 1 ||
-          ((a.lr_k == 8 || a.lr_k == 16) && !a.addend && !a.bias && !a.act));
+         // or 16 with no addend, bias or activation), the general pass adds
+         // it on NT sites alone; the bf16 copy of the output rides the
+         // constant-rank pass only.
+         (!a.lr_res || a.lr_layout == 1 || LowRankConstPass(a)) &&
+         (!a.lr_sink || LowRankConstPass(a));
 }
 
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,
