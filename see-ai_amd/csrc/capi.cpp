@@ -150,11 +150,14 @@ struct seeai_ctx {
   // same way reuses it when every instruction between wrote elsewhere.
   void* cvt = nullptr;
   size_t cvt_bytes = 0;
-  // A second copy slot, filled only by a producer's second conversion sink
-  // (two outputs of one pass, each the activation of one of the two relaxed
-  // products after it), the same size as the first.
-  void* cvt2 = nullptr;
-  size_t cvt2_bytes = 0;
+  // More copy slots, the size of the first, filled only by conversion sinks:
+  // slot 0 by a producer's second sink (two outputs of one pass, each the
+  // activation of one of the two relaxed products after it), slots 1 .. 3 in
+  // turn by sinks whose product comes later in the range (FarSink).
+  static constexpr int kXSlots = 4;
+  void* xcvt[kXSlots] = {};
+  size_t xcvt_bytes = 0;
+  int far_next = 0;
   // bf16 copies of relaxed attention's operands (q, k, v, dO: four slots of
   // B·S·H·64) for the bf16-operand kernels, and what they hold: the sources
   // and the instruction that converted them.
@@ -193,7 +196,7 @@ struct seeai_ctx {
     float alpha = 0.0f;
     const float* ks = nullptr;
     const uint8_t* at = nullptr;  // the converting instruction in the range; null: none
-  } cvt_key, cvt2_key;
+  } cvt_key, xcvt_key[kXSlots];
   const uint8_t* cur_at = nullptr;  // the instruction being executed, when in the range
   uint64_t fused = 0;
   // bf16 copies [N, Kp] of frozen weights for the relaxed GEMMs, keyed by
@@ -261,7 +264,7 @@ int Hip(seeai_ctx* c, hipError_t e, const char* what) {
 // no bf16 copy made earlier may be taken for current.
 void ForgetCopies(seeai_ctx* c) {
   c->cvt_key.at = nullptr;
-  c->cvt2_key.at = nullptr;
+  for (auto& k : c->xcvt_key) k.at = nullptr;
   c->a16_key.at = nullptr;
   ++c->a16_epoch;
 }
@@ -395,11 +398,12 @@ int GemmBf16Dma(seeai_ctx* c, GemmArgs& a, const char* what) {
     SEEAI_TRY(c, LaunchWeightShadow(a, shadow, c->stream), "weight shadow");
   }
   const size_t need = a.M * Bf16DmaKp(a.K) * 2;
-  // A copy a second conversion sink left in the second slot.
-  if (c->cvt2 && ConvertedAlready(c, a, c->cvt2_key)) {
-    SEEAI_TRY(c, LaunchGemmBf16Dma(c->cvt2, shadow, a, c->stream), what);
-    return SEEAI_OK;
-  }
+  // A copy a conversion sink left in one of the other slots.
+  for (int s = 0; s < seeai_ctx::kXSlots; ++s)
+    if (c->xcvt[s] && ConvertedAlready(c, a, c->xcvt_key[s])) {
+      SEEAI_TRY(c, LaunchGemmBf16Dma(c->xcvt[s], shadow, a, c->stream), what);
+      return SEEAI_OK;
+    }
   if (!ConvertedAlready(c, a, c->cvt_key)) {
     if (need > c->cvt_bytes) {  // grow after draining the stream
       c->cvt_key.at = nullptr;
@@ -856,6 +860,9 @@ const char* DecodeGemm(seeai_ctx* c, const Instruction& ins, GemmArgs* out) {
 bool PlanSink(seeai_ctx* c, uint64_t last, uint64_t writer, const float* out, uint64_t n,
               Bf16Sink* sink, GemmArgs* ga, int slot = 1, int site = 0);
 void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a, int slot = 1);
+bool PlanFarSink(seeai_ctx* c, uint64_t last, const float* out, uint64_t n, Bf16Sink* sink,
+                 GemmArgs* ga, int* xslot, uint64_t* key_at);
+void FarSinkDone(seeai_ctx* c, uint64_t key_at, const GemmArgs& a, int xslot);
 // The index of the instruction being executed within its range's program
 // (c->cur_at set).
 uint64_t CurIndex(const seeai_ctx* c) { return static_cast<uint64_t>(c->cur_at - c->prog) / 64; }
@@ -1069,14 +1076,28 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       const uint64_t d = ins.out[1] & 0xFFFFFFFFu;
       const float base = BitsToF32(ins.out[2]);
       const float step = std::pow(base, -2.0f / static_cast<float>(d));  // attention.cc:123
-      uint16_t* y16 = ins.opcode == 33
-                          ? RopeAttnCopy(c, R.f(ins.in[0]), R.f(ins.in[1]), hi0, lo0,
-                                         ins.out[1] >> 32, d, R.fo(ins.in[2]))
-                          : nullptr;
+      // The forward writes the bf16-copy attention's copy of its output; the
+      // backward the bf16 copy of the relaxed product that takes its output
+      // later (the input-gradient product of a q / k site, past the
+      // adapter GEMMs).
+      Bf16Sink sink;
+      GemmArgs ga{};
+      int xslot = -1;
+      uint64_t key_at = 0;
+      const uint64_t rows = hi0 * lo0, width = (ins.out[1] >> 32) * d;
+      if (ins.opcode == 33) {
+        sink.out = RopeAttnCopy(c, R.f(ins.in[0]), R.f(ins.in[1]), hi0, lo0, ins.out[1] >> 32, d,
+                                R.fo(ins.in[2]));
+        sink.K = static_cast<uint32_t>(width);
+      } else if (c->cur_at && RopeRowsFits(R.f(ins.in[0]), R.f(ins.in[1]), hi0, lo0,
+                                            ins.out[1] >> 32, d, R.fo(ins.in[2]))) {
+        PlanFarSink(c, CurIndex(c), R.f(ins.in[1]), rows * width, &sink, &ga, &xslot, &key_at);
+      }
       SEEAI_TRY(c,
                 LaunchRope(R.f(ins.in[0]), R.f(ins.in[1]), hi0, lo0, ins.out[1] >> 32, d, step,
-                           R.fo(ins.in[2]), ins.opcode == 34, s, y16),
+                           R.fo(ins.in[2]), ins.opcode == 34, s, sink),
                 "rope");
+      if (xslot >= 0) FarSinkDone(c, key_at, ga, xslot);
       return SEEAI_OK;
     }
     case 45: {  // RopeTable
@@ -1319,7 +1340,8 @@ void seeai_destroy(seeai_ctx* c) {
   if (c->source) (void)hipFree(c->source);
   if (c->scratch) (void)hipFree(c->scratch);
   if (c->cvt) (void)hipFree(c->cvt);
-  if (c->cvt2) (void)hipFree(c->cvt2);
+  for (void* p : c->xcvt)
+    if (p) (void)hipFree(p);
   if (c->a16) (void)hipFree(c->a16);
   DropSavedCopies(c);
   DropShadows(c);
@@ -1696,10 +1718,10 @@ bool PlanSink(seeai_ctx* c, uint64_t last, uint64_t writer, const float* out, ui
   a.relaxed = (nx.flags & kFlagRelaxed) && c->allow_relaxed ? 1 : 0;
   a.policy = &c->policy;
   if (!a.relaxed || !c->allow_dma || !Bf16DmaFits(a) || !Immutable(c, a.B)) return false;
-  const size_t cap = slot == 2 ? c->cvt2_bytes : c->cvt_bytes;
+  const size_t cap = slot == 2 ? c->xcvt_bytes : c->cvt_bytes;
   if (a.A != out || a.M * a.K != n || a.K % 32 != 0 || a.M * a.K * 2 > cap) return false;
   if (reinterpret_cast<uintptr_t>(a.a_k_scale) & 15) return false;
-  sink->out = static_cast<uint16_t*>(slot == 2 ? c->cvt2 : c->cvt);
+  sink->out = static_cast<uint16_t*>(slot == 2 ? c->xcvt[0] : c->cvt);
   sink->ks = a.a_k_scale;
   sink->alpha = a.alpha_a;
   sink->K = static_cast<uint32_t>(a.K);
@@ -1715,8 +1737,64 @@ bool PlanSink(seeai_ctx* c, uint64_t last, uint64_t writer, const float* out, ui
 // (its ConvertedAlready finds it; slot 2's product has the GEMM PlanSink
 // checked between them).
 void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a, int slot) {
-  (slot == 2 ? c->cvt2_key : c->cvt_key) =
+  (slot == 2 ? c->xcvt_key[0] : c->cvt_key) =
       seeai_ctx::CvtKey{a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->prog + last * 64};
+  ++c->sinks;
+}
+
+// A sink whose product comes later in the range: the first relaxed
+// frozen-weight product on the direct-to-LDS path that takes the producer's
+// output `out` (producer at index `last`) as its activation, within
+// kFarWindow instructions, no instruction before it writing into `out`
+// (those that read `out` -- exact GEMMs taking it as an operand -- read the
+// f32 store, which is always kept).  The copy goes to extra slots 1 .. 3 in
+// turn (a slot taken again before its product runs only costs that product
+// its own conversion: its key no longer matches).  *key_at: the last
+// instruction before the product that is not a GEMM, from where
+// ConvertedAlready walks the GEMMs to the product; *ga: the product's
+// arguments.
+bool PlanFarSink(seeai_ctx* c, uint64_t last, const float* out, uint64_t n, Bf16Sink* sink,
+                 GemmArgs* ga, int* xslot, uint64_t* key_at) {
+  constexpr uint64_t kFarWindow = 16;
+  if (!c->allow_fusion || !c->allow_sinks || !c->prog || !c->xcvt[1]) return false;
+  const auto* o = reinterpret_cast<const uint8_t*>(out);
+  uint64_t free_at = last;
+  for (uint64_t f = last + 1; f < c->range_end && f <= last + kFarWindow; ++f) {
+    Instruction ins;
+    std::memcpy(&ins, c->prog + f * 64, sizeof ins);
+    GemmArgs a{};
+    const bool gemm = DecodeGemm(c, ins, &a) != nullptr;
+    if (gemm && a.A == out && (ins.flags & kFlagRelaxed)) {
+      a.relaxed = c->allow_relaxed ? 1 : 0;
+      a.policy = &c->policy;
+      if (!a.relaxed || !c->allow_dma || !Bf16DmaFits(a) || !Immutable(c, a.B)) return false;
+      if (a.M * a.K != n || a.K % 32 != 0 || a.M * a.K * 2 > c->xcvt_bytes) return false;
+      if (reinterpret_cast<uintptr_t>(a.a_k_scale) & 15) return false;
+      const int s = 1 + c->far_next;
+      c->far_next = (c->far_next + 1) % (seeai_ctx::kXSlots - 1);
+      sink->out = static_cast<uint16_t*>(c->xcvt[s]);
+      sink->ks = a.a_k_scale;
+      sink->alpha = a.alpha_a;
+      sink->K = static_cast<uint32_t>(a.K);
+      sink->store_f32 = 1;
+      *ga = a;
+      *xslot = s;
+      *key_at = free_at;
+      return true;
+    }
+    Touch t[16];
+    int nt = 0;
+    if (!TouchExtents(c, ins, t, &nt)) return false;
+    for (int i = 0; i < nt; ++i)
+      if (t[i].write && Overlap(t[i].p, t[i].n, o, n * 4)) return false;
+    if (!gemm) free_at = f;
+  }
+  return false;
+}
+
+void FarSinkDone(seeai_ctx* c, uint64_t key_at, const GemmArgs& a, int xslot) {
+  c->xcvt_key[xslot] =
+      seeai_ctx::CvtKey{a.A, a.M, a.K, a.alpha_a, a.a_k_scale, c->prog + key_at * 64};
   ++c->sinks;
 }
 
@@ -1744,6 +1822,7 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
   GemmArgs a{};
   if (!DecodeGemm(c, ins, &a)) return -1;
   a.relaxed = 1;
+  a.policy = &c->policy;  // the same kernel choice the product makes alone
   if (a.accumulate || !Bf16DmaFits(a) || !Immutable(c, a.B)) return -1;
   const uint64_t idx = static_cast<uint64_t>(at - c->prog) / 64;
   Extent reads_a[8];
@@ -2277,15 +2356,18 @@ int PresizeWorkspaces(seeai_ctx* c, const uint8_t* prog, uint64_t begin, uint64_
     SEEAI_TRY(c, hipMalloc(&c->cvt, cvt), "conversion buffer alloc");
     c->cvt_bytes = cvt;
   }
-  if (cvt > c->cvt2_bytes) {
+  if (cvt > c->xcvt_bytes) {
     DropGraphs(c);
     SEEAI_TRY(c, hipStreamSynchronize(c->stream), "conversion buffer drain");
-    c->cvt2_key.at = nullptr;
-    if (c->cvt2) SEEAI_TRY(c, hipFree(c->cvt2), "conversion buffer free");
-    c->cvt2 = nullptr;
-    c->cvt2_bytes = 0;
-    SEEAI_TRY(c, hipMalloc(&c->cvt2, cvt), "conversion buffer alloc");
-    c->cvt2_bytes = cvt;
+    c->xcvt_bytes = 0;
+    for (int s = 0; s < seeai_ctx::kXSlots; ++s) {
+      c->xcvt_key[s].at = nullptr;
+      if (c->xcvt[s]) SEEAI_TRY(c, hipFree(c->xcvt[s]), "conversion buffer free");
+      c->xcvt[s] = nullptr;
+    }
+    for (int s = 0; s < seeai_ctx::kXSlots; ++s)
+      SEEAI_TRY(c, hipMalloc(&c->xcvt[s], cvt), "conversion buffer alloc");
+    c->xcvt_bytes = cvt;
   }
   return SEEAI_OK;
 }

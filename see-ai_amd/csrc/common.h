@@ -216,13 +216,13 @@ hipError_t LaunchRmsNormFwd(const float* x, const float* g, float* y, float* rst
 hipError_t LaunchRmsNormBwd(const float* dy, const float* x, const float* g, const float* rstd,
                             float* dx, size_t rows, size_t cols, hipStream_t s,
                             const Bf16Sink& sink = Bf16Sink{}, const float* res = nullptr);
-// y16: also y's bf16 copy (round to nearest even), on the row kernel only
-// (RopeRowsFits).
+// sink: also a bf16 copy of y (with the sink's scales; the attention's copy
+// is plain round to nearest even), on the row kernel only (RopeRowsFits).
 bool RopeRowsFits(const float* x, const float* y, size_t B, size_t S, size_t H, size_t d,
                   const float* table);
 hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
                       float step, const float* table, int backward, hipStream_t s,
-                      uint16_t* y16 = nullptr);
+                      const Bf16Sink& sink = Bf16Sink{});
 hipError_t LaunchRopeTable(float* table, size_t S, size_t d, float step, hipStream_t s);
 hipError_t LaunchSegmentStarts(const int32_t* tokens, int32_t* starts, size_t B, size_t S,
                                int32_t eos, hipStream_t s);

@@ -472,7 +472,7 @@ RopeKernel(const float* __restrict__ x, float* __restrict__ y, size_t B, size_t 
 __global__ void __launch_bounds__(kThreads)
 RopeRowsKernel(const float* __restrict__ x, float* __restrict__ y, unsigned rows, unsigned S,
                unsigned width, unsigned d, const float* __restrict__ table, int backward,
-               uint16_t* __restrict__ y16) {
+               Bf16Sink sink) {
   for (unsigned r = blockIdx.y; r < rows; r += gridDim.y) {
     const unsigned s = r % S;
     const float* __restrict__ trow = table + static_cast<size_t>(s) * d;  // d/2 pairs x 2
@@ -494,13 +494,9 @@ RopeRowsKernel(const float* __restrict__ x, float* __restrict__ y, unsigned rows
         o.z = v.z * t.z - v.w * t.w;
         o.w = v.z * t.w + v.w * t.z;
       }
-      *reinterpret_cast<float4*>(y + base + c) = o;
-      if (y16) {  // the attention's bf16 copy of y, rounded to nearest even
-        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-        const bf16x4_t h = {static_cast<__bf16>(o.x), static_cast<__bf16>(o.y),
-                            static_cast<__bf16>(o.z), static_cast<__bf16>(o.w)};
-        *reinterpret_cast<bf16x4_t*>(y16 + base + c) = h;
-      }
+      if (sink.store_f32) *reinterpret_cast<float4*>(y + base + c) = o;
+      // y's bf16 copy: the attention's (plain), or a product's (its scales)
+      if (sink.out) SinkStore4(sink, base + c, o);
     }
   }
 }
@@ -894,7 +890,8 @@ bool RopeRowsFits(const float* x, const float* y, size_t B, size_t S, size_t H, 
 }
 
 hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
-                      float step, const float* table, int backward, hipStream_t s, uint16_t* y16) {
+                      float step, const float* table, int backward, hipStream_t s,
+                      const Bf16Sink& sink) {
   const size_t n = B * S * H * (d / 2);
   if (n == 0) return hipSuccess;
   if (RopeRowsFits(x, y, B, S, H, d, table)) {
@@ -903,10 +900,10 @@ hipError_t LaunchRope(const float* x, float* y, size_t B, size_t S, size_t H, si
     const dim3 grid(gx, std::min(rows, 65535u));
     hipLaunchKernelGGL(RopeRowsKernel, grid, dim3(kThreads), 0, s, x, y, rows,
                        static_cast<unsigned>(S), width, static_cast<unsigned>(d), table, backward,
-                       y16);
+                       sink);
     return hipGetLastError();
   }
-  if (y16) return hipErrorInvalidValue;  // the bf16 copy rides on the row kernel only
+  if (sink.out || !sink.store_f32) return hipErrorInvalidValue;  // the row kernel's only
   const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 7) == 0;
   if (vec)
     hipLaunchKernelGGL(RopeKernel<true>, dim3(GridFor(n, kThreads)), dim3(kThreads), 0, s, x, y, B,

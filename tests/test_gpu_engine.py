@@ -640,11 +640,13 @@ def test_c5_width_slice_step_tensors_match_the_oracle(hip, orc, torch_cuda, mode
 # the two-block tiny decoders.  c4: LayerNorm forward ahead of Q and of the
 # FFN up product (2 + 2), GELU forward (2), the softmax-xent backward (1),
 # the final LayerNorm backward (1), GELU backward (2), the residual-gradient
-# adds ahead of Wo^T (2) and of the block below's Wd^T (1).  c5 the same with
-# RMSNorm and the SwiGLU passes in place of GELU, the SwiGLU backward writing
-# the copies of both its products (2 more).  The final norm does not fuse:
-# the head's N = 96 is below the direct-to-LDS kernel's 128.
-SINKS_PER_STEP = {"c4": 13, "c5": 15}
+# adds ahead of Wo^T (2) and of the block below's Wd^T (1), and the upper
+# block's RoPE backwards of q and k for the input-gradient products past the
+# adapter GEMMs (2; the lower block has no input-gradient products).  c5 the
+# same with RMSNorm and the SwiGLU passes in place of GELU, the SwiGLU
+# backward writing the copies of both its products (2 more).  The final norm
+# does not fuse: the head's N = 96 is below the direct-to-LDS kernel's 128.
+SINKS_PER_STEP = {"c4": 15, "c5": 17}
 # With attention on bf16 copies, per block: the attention forward writes the
 # O product's activation, the RoPE forwards of q and k write the attention's
 # own copies of them, and the V site's low-rank pass writes v's; in c5 the O

@@ -1247,6 +1247,67 @@ def test_lora_dx_site_folds_over_the_adapter_gradients(hip, orc, backend, case):
         assert bits_equal(ar.get(ranged, name), ar.get(cpu, name)), name
 
 
+FAR_CASES = ["gemms_between", "copy_between", "writer_between", "five_pending"]
+
+
+@pytest.mark.parametrize("case", FAR_CASES)
+def test_rope_backward_writes_a_later_products_copy(hip, orc, backend, case):
+    """A RoPE backward whose output dq the adapter GEMMs read first and a
+    relaxed q8 NT product takes later (a q / k site's input gradient) writes
+    that product's bf16 activation as it stores dq: the product skips its
+    conversion, the range is bitwise the instructions one by one.  An
+    instruction between that writes into dq refuses it (that instruction, an
+    add right before the product, then writes the copy itself); with five such
+    copies pending the three slots are taken again before some products run,
+    and those convert for themselves -- the same bits either way."""
+    from tests.plan_ops import ins
+    B, S, H, d, rank, N = 2, 128, 16, 64, 16, 768
+    M, K = B * S, H * d
+    r = rng(FAR_CASES.index(case) + 71)  # a fixed seed per case
+    rx, cs_flag = 1 << 5, 1 << 4
+    ar = Arena()
+    tab = ar.empty("tab", (S, d // 2, 2))
+    base = f32_bits(10000.0)
+    g0, g1 = (B << 32) | S, (H << 32) | d
+    prog = [ins(45, [tab], [(S << 32) | d, base])]
+    ks = ar.add("ks", r.uniform(1e-3, 5e-2, K).astype(np.float32), rodata=True)
+    Bq = ar.add("Bq", (r.standard_normal((rank, K)) * 0.02).astype(np.float32))
+    t = ar.add("t", r.standard_normal((M, rank)).astype(np.float32))
+    n_src = 5 if case == "five_pending" else 1
+    srcs, ys, ws, outs = [], [], [], []
+    for i in range(n_src):
+        srcs.append(ar.add(f"dqr{i}", r.standard_normal((M, K)).astype(np.float32)))
+        ys.append(ar.empty(f"dq{i}", (M, K)))
+        ws.append(ar.add(f"W{i}", r.integers(-127, 128, (N, K)).astype(np.int8), rodata=True))
+        outs.append(ar.empty(f"P{i}", (M, N)))
+    for i in range(n_src):
+        prog.append(ins(34, [srcs[i], ys[i], tab], [g0, g1, base]))
+    dt, dB = ar.empty("dt", (M, rank)), ar.empty("dB", (rank, K))
+    prog += [ins(2, [ys[0], Bq, dt], [M, rank, K]), ins(3, [t, ys[0], dB], [rank, K, M])]
+    if case == "copy_between":
+        prog.append(ins(20, [t, ar.empty("t2", (M, rank))], [M * rank]))
+    elif case == "writer_between":
+        prog.append(ins(5, [ys[0], srcs[0], ys[0]], [M * K]))
+    for i in range(n_src):
+        prog.append(ins(30, [ys[i], ws[i], outs[i], ks], [M, N, K], flags=rx | cs_flag))
+    if case == "writer_between":
+        prog += _readers(ar, ["dq0"])  # keeps the add's f32 store live
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    convs = backend.fused_conversions()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    sinks = {"gemms_between": 1, "copy_between": 1, "writer_between": 1, "five_pending": 5}[case]
+    assert backend.fused_conversions() - convs == sinks
+    diff = np.flatnonzero(ranged != apart)
+    assert diff.size == 0, f"{diff.size} bytes differ from byte {diff[:1]}"
+    for i in range(n_src):
+        e = maxrel(ar.get(ranged, f"P{i}"), ar.get(cpu, f"P{i}"))
+        assert e <= TOL_BF16, f"P{i}: {e:.3g}"
+
+
 RECONVERT_CASES = ["gemm_elsewhere", "gemm_into_x", "add_into_x"]
 
 
