@@ -720,6 +720,10 @@ int Attn16BwdOperands(seeai_ctx* c, const float* const src[4], uint64_t rows, ui
   return Attn16Operands(c, src, 15u, rows, cols, out);
 }
 
+bool PlanFarSink(seeai_ctx* c, uint64_t last, const float* out, uint64_t n, Bf16Sink* sink,
+                 GemmArgs* ga, int* xslot, uint64_t* key_at);
+void FarSinkDone(seeai_ctx* c, uint64_t key_at, const GemmArgs& a, int xslot);
+
 int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   if (!c->allow_fusion || !c->prog || at < c->prog || at >= c->prog + c->prog_count * 64 ||
       (at - c->prog) % 64 != 0)
@@ -765,9 +769,17 @@ int TryFuseAttnBwd(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
     const float* src[4] = {q, k, v, dout};
     uint16_t* b16[4];
     if (int rc = Attn16BwdOperands(c, src, B * S, H * d, b16)) return rc;
+    // dV's copy for the relaxed product that takes it past the adapter GEMMs.
+    Bf16Sink sink;
+    GemmArgs ga{};
+    int xslot = -1;
+    uint64_t key_at = 0;
+    if (c->cur_at) PlanFarSink(c, idx + 1, dv, B * S * H * d, &sink, &ga, &xslot, &key_at);
     SEEAI_TRY(c,
-              LaunchAttn16DKDV(b16[0], b16[1], b16[2], b16[3], stats, dk, dv, B, S, H, c->stream),
+              LaunchAttn16DKDV(b16[0], b16[1], b16[2], b16[3], stats, dk, dv, B, S, H, c->stream,
+                               sink),
               "attn.dkdv_bf16");
+    if (xslot >= 0) FarSinkDone(c, key_at, ga, xslot);
   } else {
     SEEAI_TRY(c, LaunchAttnDKDVFused(q, k, v, dout, stats, dk, dv, B, S, H, d, c->stream),
               "attn.dkdv_fused");
@@ -860,9 +872,6 @@ const char* DecodeGemm(seeai_ctx* c, const Instruction& ins, GemmArgs* out) {
 bool PlanSink(seeai_ctx* c, uint64_t last, uint64_t writer, const float* out, uint64_t n,
               Bf16Sink* sink, GemmArgs* ga, int slot = 1, int site = 0);
 void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a, int slot = 1);
-bool PlanFarSink(seeai_ctx* c, uint64_t last, const float* out, uint64_t n, Bf16Sink* sink,
-                 GemmArgs* ga, int* xslot, uint64_t* key_at);
-void FarSinkDone(seeai_ctx* c, uint64_t key_at, const GemmArgs& a, int xslot);
 // The index of the instruction being executed within its range's program
 // (c->cur_at set).
 uint64_t CurIndex(const seeai_ctx* c) { return static_cast<uint64_t>(c->cur_at - c->prog) / 64; }
@@ -1755,7 +1764,7 @@ void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a, int slot) {
 // arguments.
 bool PlanFarSink(seeai_ctx* c, uint64_t last, const float* out, uint64_t n, Bf16Sink* sink,
                  GemmArgs* ga, int* xslot, uint64_t* key_at) {
-  constexpr uint64_t kFarWindow = 16;
+  constexpr uint64_t kFarWindow = 24;
   if (!c->allow_fusion || !c->allow_sinks || !c->prog || !c->xcvt[1]) return false;
   const auto* o = reinterpret_cast<const uint8_t*>(out);
   uint64_t free_at = last;

@@ -463,7 +463,8 @@ hipError_t LaunchAttn16DQ(const uint16_t* q, const uint16_t* k, const uint16_t* 
                           size_t H, hipStream_t s);
 hipError_t LaunchAttn16DKDV(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             const uint16_t* dout, const float* stats, float* dk, float* dv,
-                            size_t B, size_t S, size_t H, hipStream_t s);
+                            size_t B, size_t S, size_t H, hipStream_t s,
+                            const Bf16Sink& sink_v = Bf16Sink{});
 bool FlashFusedDKDV(size_t d);
 hipError_t LaunchFlashFwd(const float* q, const float* k, const float* v, float* o, float* stats,
                           size_t B, size_t S, size_t H, size_t d, const int32_t* starts,

@@ -594,7 +594,7 @@ __global__ void __launch_bounds__(kBwdWaves * kWave, kMinBlocks)
 Attn16DKDV(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
            const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
            const float* __restrict__ stats, float* __restrict__ out_k,
-           float* __restrict__ out_v, int S, int H) {
+           float* __restrict__ out_v, int S, int H, Bf16Sink sink_v) {
   SEEAI_STAGE_RING(kStages);
   // Per streamed query row: -mm, -delta and the document start.  Rows are
   // contiguous, so a lane's 16 rows of a tile (8q + 4g + e) are four 16-byte
@@ -759,10 +759,12 @@ Attn16DKDV(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
         *reinterpret_cast<float4*>(out_k + at) =
             make_float4(acc_k[dt][4 * qq] * isd, acc_k[dt][4 * qq + 1] * isd,
                         acc_k[dt][4 * qq + 2] * isd, acc_k[dt][4 * qq + 3] * isd);
-      if (out_v)
-        *reinterpret_cast<float4*>(out_v + at) =
-            make_float4(acc_v[dt][4 * qq], acc_v[dt][4 * qq + 1], acc_v[dt][4 * qq + 2],
-                        acc_v[dt][4 * qq + 3]);
+      if (out_v) {
+        const float4 v4 = make_float4(acc_v[dt][4 * qq], acc_v[dt][4 * qq + 1],
+                                      acc_v[dt][4 * qq + 2], acc_v[dt][4 * qq + 3]);
+        *reinterpret_cast<float4*>(out_v + at) = v4;
+        if (sink_v.out) SinkStore4(sink_v, at, v4);  // a later product's copy of dV
+      }
     }
 }
 
@@ -798,13 +800,14 @@ hipError_t LaunchAttn16DQ(const uint16_t* q, const uint16_t* k, const uint16_t* 
 
 hipError_t LaunchAttn16DKDV(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             const uint16_t* dout, const float* stats, float* dk, float* dv,
-                            size_t B, size_t S, size_t H, hipStream_t s) {
+                            size_t B, size_t S, size_t H, hipStream_t s, const Bf16Sink& sink_v) {
   if (B * H * S == 0) return hipSuccess;
   if (!dk && !dv) return hipErrorInvalidValue;
+  if (sink_v.out && (!dv || !sink_v.store_f32)) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>((S + kBwdRows - 1) / kBwdRows * B * H));
   // Two stages, two workgroups per CU (about 200 VGPRs).
   hipLaunchKernelGGL((Attn16DKDV<2, 2>), grid, dim3(kBwdWaves * kWave), 0, s, q, k, v, dout,
-                     stats, dk, dv, static_cast<int>(S), static_cast<int>(H));
+                     stats, dk, dv, static_cast<int>(S), static_cast<int>(H), sink_v);
   return hipGetLastError();
 }
 

@@ -650,8 +650,10 @@ SINKS_PER_STEP = {"c4": 15, "c5": 17}
 # With attention on bf16 copies, per block: the attention forward writes the
 # O product's activation, the RoPE forwards of q and k write the attention's
 # own copies of them, and the V site's low-rank pass writes v's; in c5 the O
-# site's input-gradient pass also writes the attention backward's dO.
-ATTN_SINKS_PER_STEP = {"c4": 4 * 2, "c5": 5 * 2}
+# site's input-gradient pass also writes the attention backward's dO.  Per
+# step, the upper block's dK / dV pass writes dV's for its input-gradient
+# product.
+ATTN_SINKS_PER_STEP = {"c4": 4 * 2 + 1, "c5": 5 * 2 + 1}
 
 
 @pytest.mark.parametrize("attn16", [False, True])
