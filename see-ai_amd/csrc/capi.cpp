@@ -1674,24 +1674,69 @@ bool DeadFrom(seeai_ctx* c, uint64_t writer, uint64_t from, const Extent& E) {
   return true;
 }
 
-// DeadFrom, decided once per program, instruction and asking site (each
-// site asks one question of an instruction: 0 the producers' sinks and the
-// elementwise chains, 1 the low-rank fold, 2 the residual add behind a
-// GEMM, 3 the residual add behind a normalisation's gradient): the answer
-// depends on the program's words and the binding alone (dropped at bind).
-constexpr int kDeadSites = 4;
-bool DeadStore(seeai_ctx* c, uint64_t at_idx, uint64_t from, const Extent& E, int site = 0) {
-  if (!c->allow_dead_store_drop) return false;
+// Range-analysis answers, decided once per program, instruction and asking
+// site (each site asks one question of an instruction: 0 the producers'
+// sinks and the elementwise chains, 1 the low-rank fold, 2 the residual add
+// behind a GEMM, 3 the residual add behind a normalisation's gradient -- all
+// DeadFrom -- and 4 the SwiGLU backward's SiLU recompute): an answer depends
+// on the program's words and the binding alone (dropped at bind).  -1:
+// undecided.
+constexpr int kDeadSites = 5;
+int8_t& RangeMemo(seeai_ctx* c, uint64_t at_idx, int site) {
   if (c->dead_prog != c->prog || c->dead.size() != c->prog_count * kDeadSites ||
       c->dead_hash != c->prog_hash) {
     c->dead_prog = c->prog;
     c->dead_hash = c->prog_hash;
     c->dead.assign(c->prog_count * kDeadSites, -1);
   }
-  int8_t& v = c->dead[at_idx * kDeadSites + site];
+  return c->dead[at_idx * kDeadSites + site];
+}
+bool DeadStore(seeai_ctx* c, uint64_t at_idx, uint64_t from, const Extent& E, int site = 0) {
+  if (!c->allow_dead_store_drop) return false;
+  int8_t& v = RangeMemo(c, at_idx, site);
   if (v < 0) v = DeadFrom(c, at_idx, from, E) ? 1 : 0;
   if (v) ++c->dropped_stores;
   return v != 0;
+}
+
+// Which operand of the SwiGLU backward's second product (instruction
+// `at_idx`, n floats each) is y = SiLU(x) for this pass's x, by the range:
+// y's last writer before the pass is a SiLU forward (opcode 24) of exactly x
+// into exactly y, and no instruction since writes into x or y.  The pass
+// then forms y from x as that forward did (the same expression, so the same
+// bits) instead of reading it.  0: neither (y is read); 1: p0; 2: p1.
+int SiluOperand(seeai_ctx* c, uint64_t at_idx, const float* p0, const float* p1, const float* x,
+                uint64_t n) {
+  if (!c->allow_fusion || !c->prog || !c->cur_at) return 0;
+  int8_t& v = RangeMemo(c, at_idx, 4);
+  if (v >= 0) return v;
+  v = 0;
+  const auto* xb = reinterpret_cast<const uint8_t*>(x);
+  const float* cand[2] = {p0, p1};
+  bool alive[2] = {p0 != x, p1 != x};
+  for (uint64_t i = at_idx; i-- > 0;) {
+    Instruction ins;
+    std::memcpy(&ins, c->prog + i * 64, sizeof ins);
+    Touch t[16];
+    int nt = 0;
+    if (!TouchExtents(c, ins, t, &nt)) return v;
+    const Ptrs R{c};
+    for (int k = 0; k < 2; ++k) {
+      if (!alive[k]) continue;
+      const auto* yb = reinterpret_cast<const uint8_t*>(cand[k]);
+      bool hit = false;
+      for (int j = 0; j < nt; ++j)
+        if (t[j].write && Overlap(t[j].p, t[j].n, yb, n * 4)) hit = true;
+      if (!hit) continue;
+      if (ins.opcode == 24 && ins.out[0] == n && R.f(ins.in[0]) == x && R.f(ins.in[1]) == cand[k])
+        return v = static_cast<int8_t>(k + 1);
+      alive[k] = false;  // written by something else
+    }
+    for (int j = 0; j < nt; ++j)
+      if (t[j].write && Overlap(t[j].p, t[j].n, xb, n * 4)) return v;  // x changed since
+    if (!alive[0] && !alive[1]) return v;
+  }
+  return v;
 }
 
 // Conversion fused into a producer: when the instruction after index `last`
@@ -2050,6 +2095,10 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
                 *b2 = R.f(m2.in[1]), *x = R.f(n2.in[1]);
     float *o1 = R.f(m1.in[2]), *o2 = R.f(m2.in[2]), *dx = R.f(n2.in[2]);
     if (!clear({o1, o2, dx}, {a1, b1, a2, b2, x})) return -1;
+    // The second product's y = SiLU(x) formed from x where the range shows
+    // it is (x is read anyway; y then is not).
+    const int silu = SiluOperand(c, idx, a2, b2, x, n);
+    if (silu == 1) std::swap(a2, b2);  // IEEE multiplication commutes: b2 is y
     // The product SiluBwd reads is stored only where the range reads it again.
     float* o1_store = o1;
     if (DeadStore(c, idx, idx + 3, Extent{reinterpret_cast<const uint8_t*>(o1), nb}))
@@ -2063,7 +2112,7 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
     const bool sunk2 = sunk && PlanSink(c, idx + 2, idx + (first ? 1 : 0), o2, n, &sink2, &ga2, 2, 1);
     SEEAI_TRY(c,
               LaunchSwigluBwd(a1, b1, o1_store, a2, b2, o2, x, dx, n, c->stream, sink,
-                              sunk2 ? sink2 : Bf16Sink{}),
+                              sunk2 ? sink2 : Bf16Sink{}, silu != 0),
               "swiglu_bwd");
     if (sunk) SinkDone(c, idx + 2, ga);
     if (sunk2) SinkDone(c, idx + 2, ga2, 2);

@@ -392,7 +392,7 @@ hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, siz
 hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const float* a2,
                            const float* b2, float* o2, const float* x, float* dx, size_t n,
                            hipStream_t s, const Bf16Sink& sink = Bf16Sink{},
-                           const Bf16Sink& sink2 = Bf16Sink{});
+                           const Bf16Sink& sink2 = Bf16Sink{}, bool silu_b2 = false);
 bool SwigluFits(size_t n, std::initializer_list<const void*> ptrs);
 
 // W8A8 (k_gemm_i8.hip).

@@ -606,8 +606,9 @@ SiluMul4(const float4* __restrict__ x, const float4* __restrict__ u, float4* __r
 
 // kStoreO1 false: the first product is dead after the pass and is not stored.
 // `sink` takes dx's bf16 copy, `sink2` the second product's (each with its
-// f32 store kept or dropped on its own).
-template <bool kStoreO1>
+// f32 store kept or dropped on its own).  kSiluB2: b2 is SiLU(x), formed
+// here from x with the forward's expression rather than read.
+template <bool kStoreO1, bool kSiluB2>
 __global__ void __launch_bounds__(kThreads)
 SwigluBwd4(const float4* __restrict__ a1, const float4* __restrict__ b1, float4* __restrict__ o1,
            const float4* __restrict__ a2, const float4* __restrict__ b2, float4* __restrict__ o2,
@@ -615,7 +616,9 @@ SwigluBwd4(const float4* __restrict__ a1, const float4* __restrict__ b1, float4*
            Bf16Sink sink2) {
   const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
   for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
-    const float4 p = a1[i], q = b1[i], r = a2[i], t = b2[i], v = x[i];
+    const float4 p = a1[i], q = b1[i], r = a2[i], v = x[i];
+    const float4 t = kSiluB2 ? make_float4(SiluExpr(v.x), SiluExpr(v.y), SiluExpr(v.z), SiluExpr(v.w))
+                             : b2[i];
     const float4 m1 = make_float4(p.x * q.x, p.y * q.y, p.z * q.z, p.w * q.w);
     if constexpr (kStoreO1) o1[i] = m1;
     const float4 m2 = make_float4(r.x * t.x, r.y * t.y, r.z * t.z, r.w * t.w);
@@ -702,18 +705,19 @@ hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, siz
 }
 hipError_t LaunchSwigluBwd(const float* a1, const float* b1, float* o1, const float* a2,
                            const float* b2, float* o2, const float* x, float* dx, size_t n,
-                           hipStream_t s, const Bf16Sink& sink, const Bf16Sink& sink2) {
+                           hipStream_t s, const Bf16Sink& sink, const Bf16Sink& sink2,
+                           bool silu_b2) {
   if (SwigluFits(n, {a1, b1, o1, a2, b2, o2, x, dx})) {
     if (n == 0) return hipSuccess;
     const auto c4 = [](const float* p) { return reinterpret_cast<const float4*>(p); };
     const auto m4 = [](float* p) { return reinterpret_cast<float4*>(p); };
     const dim3 grid(GridFor(n / 4, kThreads, 8192));
-    if (o1)
-      hipLaunchKernelGGL(SwigluBwd4<true>, grid, dim3(kThreads), 0, s, c4(a1), c4(b1), m4(o1),
-                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4, sink, sink2);
-    else
-      hipLaunchKernelGGL(SwigluBwd4<false>, grid, dim3(kThreads), 0, s, c4(a1), c4(b1), m4(o1),
-                         c4(a2), c4(b2), m4(o2), c4(x), m4(dx), n / 4, sink, sink2);
+    auto go = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, c4(a1), c4(b1), m4(o1), c4(a2),
+                         c4(b2), m4(o2), c4(x), m4(dx), n / 4, sink, sink2);
+    };
+    if (o1) silu_b2 ? go(SwigluBwd4<true, true>) : go(SwigluBwd4<true, false>);
+    else silu_b2 ? go(SwigluBwd4<false, true>) : go(SwigluBwd4<false, false>);
     return hipGetLastError();
   }
   if (sink.out || !sink.store_f32 || sink2.out || !sink2.store_f32) return hipErrorInvalidValue;
