@@ -158,6 +158,14 @@ struct seeai_ctx {
   void* xcvt[kXSlots] = {};
   size_t xcvt_bytes = 0;
   int far_next = 0;
+  // Partial row maxima a GEMM epilogue left for the loss turn at `at`
+  // (instruction index, this epoch): of logits C [M, N].
+  float* pmax = nullptr;
+  size_t pmax_bytes = 0;
+  struct {
+    const float* C = nullptr;
+    uint64_t M = 0, N = 0, at = 0, epoch = 0;
+  } pmax_key;
   // bf16 copies of relaxed attention's operands (q, k, v, dO: four slots of
   // B·S·H·64) for the bf16-operand kernels, and what they hold: the sources
   // and the instruction that converted them.
@@ -876,6 +884,36 @@ void SinkDone(seeai_ctx* c, uint64_t last, const GemmArgs& a, int slot = 1);
 // (c->cur_at set).
 uint64_t CurIndex(const seeai_ctx* c) { return static_cast<uint64_t>(c->cur_at - c->prog) / 64; }
 
+// A relaxed product on the direct-to-LDS kernel whose C the softmax-xent
+// forward right after takes as its logits: its epilogue also leaves C's
+// partial row maxima (a->row_max_part), from which the loss turn forms the
+// row max without its own pass over the logits.
+int PlanRowMaxParts(seeai_ctx* c, GemmArgs* a) {
+  if (!c->allow_fusion || !c->cur_at || !c->prog || !a->relaxed || !c->allow_dma) return SEEAI_OK;
+  const uint64_t idx = CurIndex(c);
+  if (idx + 1 >= c->range_end) return SEEAI_OK;
+  Instruction nx;
+  std::memcpy(&nx, c->prog + (idx + 1) * 64, sizeof nx);
+  const Ptrs R{c};
+  if ((nx.opcode != 11 && nx.opcode != 51) || R.f(nx.in[0]) != a->C || nx.out[0] != a->M ||
+      nx.out[1] != a->N || XEntOneWorkgroup(a->M, a->N))
+    return SEEAI_OK;
+  a->policy = &c->policy;
+  if (!Bf16DmaRowMaxFits(*a) || !Immutable(c, a->B)) return SEEAI_OK;
+  const size_t bytes = a->M * ((a->N + 63) / 64) * 4;
+  if (bytes > c->pmax_bytes) {  // grow after draining the stream
+    DropGraphs(c);
+    SEEAI_TRY(c, hipStreamSynchronize(c->stream), "row maxima drain");
+    if (c->pmax) SEEAI_TRY(c, hipFree(c->pmax), "row maxima free");
+    c->pmax = nullptr;
+    c->pmax_bytes = 0;
+    SEEAI_TRY(c, hipMalloc(&c->pmax, bytes), "row maxima alloc");
+    c->pmax_bytes = bytes;
+  }
+  a->row_max_part = c->pmax;
+  return SEEAI_OK;
+}
+
 int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P) {
   if (!c->arena) return Fail(c, SEEAI_INVALID, "execute: no arena is bound");
   const Ptrs R{c};
@@ -898,7 +936,11 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       GemmArgs a{};
       const char* what = DecodeGemm(c, ins, &a);
       a.relaxed = Relaxed(c, ins);
-      return Gemm(c, a, what);
+      if (int rc = PlanRowMaxParts(c, &a)) return rc;
+      if (int rc = Gemm(c, a, what)) return rc;
+      if (a.row_max_part)
+        c->pmax_key = {a.C, a.M, a.N, CurIndex(c) + 1, c->a16_epoch};
+      return SEEAI_OK;
     }
     case 5: {
       Bf16Sink sink;
@@ -1351,6 +1393,7 @@ void seeai_destroy(seeai_ctx* c) {
   if (c->cvt) (void)hipFree(c->cvt);
   for (void* p : c->xcvt)
     if (p) (void)hipFree(p);
+  if (c->pmax) (void)hipFree(c->pmax);
   if (c->a16) (void)hipFree(c->a16);
   DropSavedCopies(c);
   DropShadows(c);
@@ -2295,10 +2338,17 @@ int TryFuseXEnt(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
   Bf16Sink sink;
   GemmArgs ga{};
   const bool sunk = PlanSink(c, idx + 2, idx + 2, dl, N * C, &sink, &ga);
+  // The product just before left the logits' partial row maxima.
+  const auto& pk = c->pmax_key;
+  const float* parts = pk.C == logits && pk.M == N && pk.N == C && pk.at == idx &&
+                               pk.epoch == c->a16_epoch
+                           ? c->pmax
+                           : nullptr;
+  c->pmax_key.C = nullptr;
   SEEAI_TRY(c,
             LaunchXEntFwdBwd(logits, labels, loss, keep, R.f(f.in[0]), f.out[0],
                              BitsToF32(f.in[1]), seed, dl, N, C, ins.opcode == 51, ws, c->stream,
-                             sink),
+                             sink, parts),
             "softmax_xent.fwd+bwd");
   if (sunk) SinkDone(c, idx + 2, ga);
   c->done[0] = at + 64;

@@ -249,7 +249,13 @@ bool XEntFusedFits(const float* logits, const float* probs, const float* dlogits
 hipError_t LaunchXEntFwdBwd(const float* logits, const int32_t* labels, float* loss, float* probs,
                             float* fill_dst, uint64_t fill_n, float fill_v, const float* seed,
                             float* dlogits, size_t N, size_t C, int masked, void* ws,
-                            hipStream_t s, const Bf16Sink& sink = Bf16Sink{});
+                            hipStream_t s, const Bf16Sink& sink = Bf16Sink{},
+                            const float* max_parts = nullptr);
+// Whether the fused loss turn of N rows of C runs in one workgroup (no row
+// max pass).
+bool XEntOneWorkgroup(size_t N, size_t C);
+// max_parts: the logits' partial row maxima [N, ceil(C / 64)] a GEMM
+// epilogue left (GemmArgs::row_max_part); the row max is formed from them.
 // Whether the backward's row kernel can feed a sink (float4 rows).
 bool XEntBwdSinkFits(const float* probs, const float* dlogits, size_t C);
 
@@ -353,6 +359,10 @@ struct GemmArgs {
   // lr_out's bf16 copy (round to nearest even, same [M, N] layout) for the
   // attention that reads it next; null: none.
   uint16_t* lr_sink;
+  // The relaxed direct-to-LDS kernel without a low-rank term: C's row maxima
+  // over each group of 64 columns, [M, ceil(N / 64)] (fmax: NaN ignored, a
+  // group of NaN gives NaN), for the loss turn that reads C next; null: none.
+  float* row_max_part;
 };
 constexpr int kLowRankMaxK = 16;
 // Relaxed -> MFMA (k_gemm_f32.hip); otherwise the reference's order.
@@ -367,6 +377,7 @@ size_t Bf16DmaKp(size_t K);
 bool Bf16DmaFits(const GemmArgs& a);
 // Whether the low-rank epilogue can join this product (N % 4 == 0, rank
 // operands 16-byte aligned, 1 <= lr_k <= kLowRankMaxK).
+bool Bf16DmaRowMaxFits(const GemmArgs& a);
 bool Bf16DmaLowRankFits(const GemmArgs& a);
 hipError_t LaunchConvertRowsBf16(const float* A, size_t M, size_t K, float alpha,
                                  const float* kscale, void* out, int wgs_per_cu, hipStream_t s);

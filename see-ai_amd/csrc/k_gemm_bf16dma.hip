@@ -259,21 +259,38 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
                       ((reinterpret_cast<uintptr_t>(g.C) | reinterpret_cast<uintptr_t>(g.addend) |
                         reinterpret_cast<uintptr_t>(g.b_col_scale) |
                         reinterpret_cast<uintptr_t>(g.bias)) & 15) == 0;
+    // Row m's maximum over this wave's 64 columns, from the lane's values
+    // `pm` of its half (columns 4 h + 8 q + 32 j) and the other half's, into
+    // the partials (WN = 64: the wave's columns are one group).
+    auto row_max_out = [&](int m, float pm) {
+      if constexpr (WN == 64) {
+        pm = fmaxf(pm, __shfl_xor(pm, 32));
+        // (a group wholly past the last column has no partial)
+        if (h == 0 && m < M && n0 + wn < N)
+          g.row_max_part[static_cast<size_t>(m) * ((N + 63) / 64) + (n0 + wn) / 64] = pm;
+      }
+    };
     // The plain product (the frozen projections): nothing but the stores.
     if (vec4 && !g.b_col_scale && g.alpha_dot == 1.0f && !g.addend && !g.accumulate && !g.bias &&
         !g.act) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int m = m0 + wm + i * 32 + lr;
+        float pm = __builtin_nanf("");  // fmaxf's identity
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int n = n0 + wn + j * 32 + 8 * q + 4 * h;
-            if (m < M && n < N)
+            if (m < M && n < N) {
               *reinterpret_cast<float4*>(g.C + static_cast<size_t>(m) * N + n) = make_float4(
                   acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+              if (g.row_max_part)
+                pm = fmaxf(pm, fmaxf(fmaxf(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                     fmaxf(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])));
+            }
           }
+        if (g.row_max_part) row_max_out(m, pm);
       }
       return;
     }
@@ -286,6 +303,7 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int m = m0 + wm + i * 32 + lr;
+        float pm = __builtin_nanf("");
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -312,10 +330,12 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
                 const float4 b4 = *reinterpret_cast<const float4*>(bias + n);
                 x0 = x0 + b4.x, x1 = x1 + b4.y, x2 = x2 + b4.z, x3 = x3 + b4.w;
               }
-              *reinterpret_cast<float4*>(C + o) = make_float4(ActF(g.act, x0), ActF(g.act, x1),
-                                                              ActF(g.act, x2), ActF(g.act, x3));
+              x0 = ActF(g.act, x0), x1 = ActF(g.act, x1), x2 = ActF(g.act, x2), x3 = ActF(g.act, x3);
+              *reinterpret_cast<float4*>(C + o) = make_float4(x0, x1, x2, x3);
+              if (g.row_max_part) pm = fmaxf(pm, fmaxf(fmaxf(x0, x1), fmaxf(x2, x3)));
             }
           }
+        if (g.row_max_part) row_max_out(m, pm);
       }
       return;
     }
@@ -687,6 +707,15 @@ bool Bf16DmaFits(const GemmArgs& a) {
   return ((a.M + 127) / 128) * ((a.N + 127) / 128) < (size_t{1} << 31);
 }
 
+// The partial row maxima ride the epilogue that stores from registers: no
+// low-rank term, whole 16-byte column quads.
+bool Bf16DmaRowMaxFits(const GemmArgs& a) {
+  const uintptr_t al = reinterpret_cast<uintptr_t>(a.C) | reinterpret_cast<uintptr_t>(a.addend) |
+                       reinterpret_cast<uintptr_t>(a.b_col_scale) |
+                       reinterpret_cast<uintptr_t>(a.bias);
+  return Bf16DmaFits(a) && !a.lr_out && a.N % 4 == 0 && (al & 15) == 0;
+}
+
 // The epilogue's constant-rank pass: rank 8 or 16 behind nothing but the
 // column scale and alpha.
 bool LowRankConstPass(const GemmArgs& a) {
@@ -761,6 +790,7 @@ hipError_t LaunchWeightShadow(const GemmArgs& a, void* out, hipStream_t s) {
 // 128 x 128 (four waves of 64 x 64).  Both accumulate each output over k in
 // the same 16-deep MFMA steps: the same bits.
 hipError_t LaunchGemmBf16Dma(const void* A, const void* W, const GemmArgs& a, hipStream_t s) {
+  if (a.row_max_part && !Bf16DmaRowMaxFits(a)) return hipErrorInvalidValue;
   const size_t Kp = Bf16DmaKp(a.K);
   const auto* Ab = static_cast<const __bf16*>(A);
   const auto* Wb = static_cast<const __bf16*>(W);
@@ -782,7 +812,9 @@ hipError_t LaunchGemmBf16Dma(const void* A, const void* W, const GemmArgs& a, hi
   const size_t c128 = std::max<size_t>(1, (t128 + cus - 1) / cus) * 2,
                c192 = std::max<size_t>(1, (t192 + cus - 1) / cus) * 3;  // CU-rounds x tile area / 8192
   const int mode = a.policy ? a.policy->relaxed_tile_192 : 2;
-  if (a.N >= 192 && (mode == 3 || (mode == 1 && (c192 < c128 || (c192 == c128 && r192 <= r128)))))
+  // (The partial row maxima need 64-column wave slices: not on 128 x 192.)
+  if (a.N >= 192 && !a.row_max_part &&
+      (mode == 3 || (mode == 1 && (c192 < c128 || (c192 == c128 && r192 <= r128)))))
     return Launch<128, 192, 2, 2, 3>(Ab, Wb, Kp, a, s);
   return Launch<128, 128, 2, 2, 4>(Ab, Wb, Kp, a, s);
 }

@@ -54,6 +54,19 @@ XEntRowMaxKernel(const float* __restrict__ logits, float* __restrict__ row_max, 
   if (threadIdx.x == 0) row_max[blockIdx.x] = mx;
 }
 
+// The row max from the partial maxima the producing GEMM's epilogue left
+// ([rows, parts], fmax over each group of 64 columns): fmax is exact and
+// order-free, so this is pass 1's value without a pass over the logits.
+__global__ void __launch_bounds__(kMaxThreads)
+XEntRowMaxPartsKernel(const float* __restrict__ parts, size_t P, float* __restrict__ row_max) {
+  __shared__ float red[kMaxThreads / kWave];
+  const float* p = parts + static_cast<size_t>(blockIdx.x) * P;
+  float mx = NAN;
+  for (size_t c = threadIdx.x; c < P; c += kMaxThreads) mx = fmaxf(mx, p[c]);
+  mx = BlockMaxF<kMaxThreads>(mx, red);
+  if (threadIdx.x == 0) row_max[blockIdx.x] = mx;
+}
+
 // --- pass 2: the exp-sum in the reference's order ------------------------------
 // loss.cc:24-29 sums exp(x - max) in f32, column by column, one chain per
 // row.  That association is reproduced exactly, with the chain apart from
@@ -439,6 +452,10 @@ hipError_t LaunchXEntFwd(const float* logits, const int32_t* labels, float* loss
   return hipGetLastError();
 }
 
+bool XEntOneWorkgroup(size_t N, size_t C) {
+  return N <= static_cast<size_t>(kSmallThreads) && N * C <= kSmallFloats;
+}
+
 bool XEntFusedFits(const float* logits, const float* probs, const float* dlogits, size_t C) {
   return C > 0 && Vec4Rows(logits, C) && (!probs || Vec4Rows(probs, C)) && Vec4Rows(dlogits, C);
 }
@@ -446,10 +463,10 @@ bool XEntFusedFits(const float* logits, const float* probs, const float* dlogits
 hipError_t LaunchXEntFwdBwd(const float* logits, const int32_t* labels, float* loss, float* probs,
                             float* fill_dst, uint64_t fill_n, float fill_v, const float* seed,
                             float* dlogits, size_t N, size_t C, int masked, void* ws,
-                            hipStream_t s, const Bf16Sink& sink) {
+                            hipStream_t s, const Bf16Sink& sink, const float* max_parts) {
   if (N == 0) return hipSuccess;
   if (!XEntFusedFits(logits, probs, dlogits, C)) return hipErrorInvalidValue;
-  if (N <= static_cast<size_t>(kSmallThreads) && N * C <= kSmallFloats) {
+  if (XEntOneWorkgroup(N, C)) {
     hipLaunchKernelGGL(XEntSmallKernel, dim3(1), dim3(kSmallThreads), 0, s, logits, labels, loss,
                        probs, fill_dst, fill_n, fill_v, seed, dlogits, N, C, masked, sink);
     return hipGetLastError();
@@ -461,7 +478,11 @@ hipError_t LaunchXEntFwdBwd(const float* logits, const int32_t* labels, float* l
   float* scale = row_sum + N;  // in the scratch's spare tail
   const unsigned rows = static_cast<unsigned>(N);
   hipLaunchKernelGGL(XEntScaleKernel, dim3(1), dim3(1024), 0, s, labels, seed, scale, N, masked);
-  hipLaunchKernelGGL(XEntRowMaxKernel, dim3(rows), dim3(kMaxThreads), 0, s, logits, row_max, C);
+  if (max_parts)
+    hipLaunchKernelGGL(XEntRowMaxPartsKernel, dim3(rows), dim3(kMaxThreads), 0, s, max_parts,
+                       (C + 63) / 64, row_max);
+  else
+    hipLaunchKernelGGL(XEntRowMaxKernel, dim3(rows), dim3(kMaxThreads), 0, s, logits, row_max, C);
   hipLaunchKernelGGL(XEntSerialSumKernel, dim3(static_cast<unsigned>((N + kSumRows - 1) / kSumRows)),
                      dim3(kSumThreads), 0, s, logits, row_max, row_sum, N, C);
   hipLaunchKernelGGL((XEntProbsKernel<true>), dim3(rows), dim3(kProbThreads), 0, s, logits, labels,

@@ -443,6 +443,44 @@ def test_xent_forward_fill_backward_fuse_bitwise(hip, orc, backend, masked, read
         assert e <= TOL, f"{name}: {e:.3g}"
 
 
+@pytest.mark.parametrize("head,C", [("f32", 4000), ("q8", 4000), ("f32", 4004)])
+def test_head_product_leaves_the_loss_turns_row_maxima(hip, orc, backend, head, C):
+    """A relaxed head product right before the loss turn leaves its logits'
+    row maxima over 64-column groups in its epilogue; the turn forms each
+    row's max from them instead of a pass over the logits (fmax is exact and
+    order-free).  Bitwise the instructions one by one (the probabilities
+    unstored), at a vocabulary that is and one that is not a multiple of 64."""
+    from tests.plan_ops import ins
+    N, K = 2048, 256
+    r = rng(C + len(head))
+    ar = Arena()
+    x = ar.add("x", r.standard_normal((N, K)).astype(np.float32))
+    ry = ar.add("labels", r.integers(0, C, N).astype(np.int32))
+    logits = ar.empty("logits", (N, C))
+    if head == "q8":
+        w = ar.add("W", r.integers(-127, 128, (K, C)).astype(np.int8), rodata=True)
+        ws = ar.add("Ws", r.uniform(1e-3, 3e-3, C).astype(np.float32), rodata=True)
+        prod = ins(29, [x, w, logits, ws], [N, C, K], flags=(1 << 5) | (1 << 4))
+    else:
+        w = ar.add("W", (r.standard_normal((K, C)) * 0.2).astype(np.float32), rodata=True)
+        prod = ins(1, [x, w, logits], [N, C, K], flags=1 << 5)
+    loss, probs = ar.empty("loss", (1,)), ar.empty("probs", (N, C))
+    seed, dl = ar.empty("seed", (1,)), ar.empty("dl", (N, C))
+    prog = [prod, ins(11, [logits, ry, loss, probs], [N, C]), ins(19, [seed, f32_bits(0.5)], [1]),
+            ins(12, [probs, ry, seed, dl], [N, C])]
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    diff = np.flatnonzero(ranged != _restored(apart, ar, ["probs"], arena))
+    assert diff.size == 0, f"{diff.size} bytes differ from byte {diff[:1]}"
+    for name in ["loss", "dl"]:
+        e = maxrel(ar.get(ranged, name), ar.get(cpu, name))
+        assert e <= TOL_BF16, f"{name}: {e:.3g}"
+
+
 # --- optimizer -----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("n", [1, 2048, 100003])
