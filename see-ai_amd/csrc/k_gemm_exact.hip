@@ -845,6 +845,133 @@ __global__ void __launch_bounds__(kThreads) GemmChainKernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// NT over N <= 16 outputs per row and a long K (the LoRA dt = dC B^T): the
+// reference's eight chains of an output (lane l takes every k = l mod 8, in
+// k order) sit in eight GPU lanes, each lane running its chain for eight
+// outputs of kRL rows at once, so one read of A[m][k] feeds eight products
+// and one read of B's eight values (a row of a k-major tile that every lane
+// of the same l reads together) feeds 8 kRL.  A wave holds 8 kRL rows x 8
+// chains for one group of eight outputs; a workgroup 32 kRL / kNG rows x kNG
+// groups.  A is staged row-major and B transposed (Bs[k][n]) through two LDS
+// buffers, chunk by chunk, the next chunk's loads in flight while one is
+// reduced.  At the end each
+// output's eight chain values are added in lane order (lane 0 first) and
+// multiplied by alpha, then the epilogue: the chain kernel's bits.
+// ---------------------------------------------------------------------------
+template <int kNG, int kRL, int kKLChunk>
+__global__ void __launch_bounds__(kThreads) GemmNTKLaneKernel(GemmArgs g) {
+  // kRL rows per lane: lane (r8, l) of a wave runs rows r8 + 8 r (r < kRL).
+  constexpr int kRows = 32 * kRL / kNG, kN = 8 * kNG, kKLLdA = kKLChunk + 8;
+  constexpr int kAPer = kRows * kKLChunk / 4 / kThreads;  // float4 of A per thread and chunk
+  static_assert(kAPer * 4 * kThreads == kRows * kKLChunk, "A loads cover the chunk");
+  static_assert(kKLChunk <= kThreads, "one k per thread for B");
+  __shared__ __attribute__((aligned(16))) float As[2][kRows][kKLLdA];
+  __shared__ __attribute__((aligned(16))) float Bs[2][kKLChunk][kN];
+  __shared__ __attribute__((aligned(16))) float Red[kRows][kN][8];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int l = lane % 8, ng = wave % kNG, rbase = (wave / kNG) * 8 * kRL + lane / 8;
+  const size_t M = g.M, N = g.N, K = g.K;
+  const size_t m0 = static_cast<size_t>(blockIdx.x) * kRows;
+  const float* __restrict__ A = g.A;
+  const float* __restrict__ B = static_cast<const float*>(g.B);
+  float4 ra[kAPer];
+  float rb[kN];
+  auto load = [&](size_t k0) {
+#pragma unroll
+    for (int r = 0; r < kAPer; ++r) {
+      const int f = tid + r * kThreads, row = f / (kKLChunk / 4), c4 = f % (kKLChunk / 4);
+      const size_t m = min(m0 + row, M - 1), k = min(k0 + 4 * c4, K - 4);
+      ra[r] = *reinterpret_cast<const float4*>(A + m * K + k);
+    }
+    if (tid < kKLChunk) {
+      const size_t k = min(k0 + tid, K - 1);
+#pragma unroll
+      for (int n = 0; n < kN; ++n) rb[n] = B[min(static_cast<size_t>(n), N - 1) * K + k];
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < kAPer; ++r) {
+      const int f = tid + r * kThreads, row = f / (kKLChunk / 4), c4 = f % (kKLChunk / 4);
+      float4 v = ra[r];
+      if (g.alpha_a != 1.0f)
+        v = make_float4(Mul(g.alpha_a, v.x), Mul(g.alpha_a, v.y), Mul(g.alpha_a, v.z),
+                        Mul(g.alpha_a, v.w));
+      *reinterpret_cast<float4*>(&As[buf][row][4 * c4]) = v;
+    }
+    if (tid < kKLChunk) {
+#pragma unroll
+      for (int n4 = 0; n4 < kN / 4; ++n4) {
+        float4 v = make_float4(rb[4 * n4], rb[4 * n4 + 1], rb[4 * n4 + 2], rb[4 * n4 + 3]);
+        if (static_cast<size_t>(4 * n4 + 3) >= N) {  // outputs past N: zeros
+          if (static_cast<size_t>(4 * n4) >= N) v.x = 0.0f;
+          if (static_cast<size_t>(4 * n4 + 1) >= N) v.y = 0.0f;
+          if (static_cast<size_t>(4 * n4 + 2) >= N) v.z = 0.0f;
+          v.w = 0.0f;
+        }
+        *reinterpret_cast<float4*>(&Bs[buf][tid][4 * n4]) = v;
+      }
+    }
+  };
+  float acc[kRL][8];
+#pragma unroll
+  for (int r = 0; r < kRL; ++r)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[r][j] = 0.0f;
+  auto step = [&](int buf, int k) {
+    const float4 b0 = *reinterpret_cast<const float4*>(&Bs[buf][k][8 * ng]);
+    const float4 b1 = *reinterpret_cast<const float4*>(&Bs[buf][k][8 * ng + 4]);
+    const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int r = 0; r < kRL; ++r) {
+      const float a = As[buf][rbase + 8 * r][k];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[r][j] = Add(acc[r][j], Mul(a, b[j]));
+    }
+  };
+  const size_t chunks = (K + kKLChunk - 1) / kKLChunk;
+  load(0);
+  store(0);
+  if (chunks > 1) load(kKLChunk);
+  __syncthreads();
+  for (size_t i = 0; i < chunks; ++i) {
+    const int buf = static_cast<int>(i & 1);
+    const size_t k0 = i * kKLChunk;
+    const int kn = K - k0 < static_cast<size_t>(kKLChunk) ? static_cast<int>(K - k0) : kKLChunk;
+    if (kn == kKLChunk) {
+#pragma unroll 4
+      for (int k = l; k < kKLChunk; k += 8) step(buf, k);
+    } else {
+      for (int k = l; k < kn; k += 8) step(buf, k);
+    }
+    if (i + 1 < chunks) {
+      store(buf ^ 1);
+      if (i + 2 < chunks) load(k0 + 2 * kKLChunk);
+    }
+    __syncthreads();
+  }
+  // Each output's chains in lane order: lane l of a row adds output 8 ng + l.
+#pragma unroll
+  for (int r = 0; r < kRL; ++r)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Red[rbase + 8 * r][8 * ng + j][l] = acc[r][j];
+  __builtin_amdgcn_wave_barrier();
+  const size_t n = static_cast<size_t>(8 * ng + l);
+#pragma unroll
+  for (int r = 0; r < kRL; ++r) {
+    const int mi = rbase + 8 * r;
+    const size_t m = m0 + mi;
+    const float4 c0 = *reinterpret_cast<const float4*>(&Red[mi][n][0]);
+    const float4 c1 = *reinterpret_cast<const float4*>(&Red[mi][n][4]);
+    float c = c0.x;
+    c = Add(c, c0.y), c = Add(c, c0.z), c = Add(c, c0.w);
+    c = Add(c, c1.x), c = Add(c, c1.y), c = Add(c, c1.z), c = Add(c, c1.w);
+    c = Mul(g.alpha_dot, c);
+    if (m < M && n < N) g.C[m * N + n] = Epilogue(g, m, n, c);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Long reductions over few outputs, NN / TN (the adapter gradients
 // dA = X^T dt and dB = s t^T dC over every token): the quads of a chunk are
 // independent, only their sum into the output is a chain.  A workgroup owns
@@ -1265,6 +1392,14 @@ hipError_t LaunchChain(const GemmArgs& a, hipStream_t s) {
 
 bool LongK(const GemmArgs& a) { return a.layout != 1 && a.M * a.N <= 16384 && a.K >= 1024; }
 
+// NT over at most 16 outputs per row, enough rows to fill the machine and a
+// long K, with 16-byte rows of A: the k-lane kernel.
+bool KLane(const GemmArgs& a) {
+  return a.layout == 1 && a.b_kind == 0 && !a.a_k_scale && a.N <= 16 && a.M >= 2048 &&
+         a.K >= 256 && a.K % 4 == 0 && (reinterpret_cast<uintptr_t>(a.A) & 15) == 0 &&
+         a.M * a.K < (size_t{1} << 40);
+}
+
 // Short reductions over few outputs (the small-batch plans' products, e.g.
 // 32 x 8 over K = 512): the panel kernel would give the whole GEMM a handful
 // of workgroups, each lane running its output's chain alone; the two-pass
@@ -1326,6 +1461,17 @@ hipError_t Run(const GemmArgs& a, hipStream_t s) {
   }
   if constexpr (kLayout != 1 && kBKind == 0)
     if (Fold(a)) return LaunchFold<kLayout>(a, s);
+  if constexpr (kLayout == 1 && kBKind == 0)
+    if (KLane(a)) {
+      if (a.N <= 8) {
+        hipLaunchKernelGGL((GemmNTKLaneKernel<1, 1, 128>),
+                           dim3(static_cast<unsigned>((a.M + 31) / 32)), dim3(kThreads), 0, s, a);
+      } else {  // 256-deep chunks (two rows per lane, one wave per SIMD: slower)
+        hipLaunchKernelGGL((GemmNTKLaneKernel<2, 1, 256>),
+                           dim3(static_cast<unsigned>((a.M + 15) / 16)), dim3(kThreads), 0, s, a);
+      }
+      return hipGetLastError();
+    }
   if (Chain(a) && !(kLayout != 1 && LongK(a) && a.scratch && LongKFirst(a))) {
     if (a.N <= 8) return LaunchChain<kLayout, kBKind, 32, 8>(a, s);
     if (a.M <= 8) return LaunchChain<kLayout, kBKind, 8, 32>(a, s);

@@ -44,6 +44,9 @@ GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 
                # a K % 256 tail, 4 x 8 blocks over a partial 512-deep chunk; C4's
                # 8192 x 8 x 768 on the chain kernel
                (2048, 16, 2056), (4096, 8, 1300), (8192, 8, 768),
+               # NT k-lane kernel (dt = dC B^T): C5's 8192 x 16 x 2048, twelve outputs
+               # over a partial last chunk, two output groups over a 44-deep tail
+               (8192, 16, 2048), (2048, 12, 1028), (4096, 16, 300),
                # TN over long K: quads formed by four lanes per output, folded in order
                (300, 3, 1100), (100, 1, 1030),
                # TN with the folder wave apart: 4 x 8 blocks over two chunks, 8 x 16
