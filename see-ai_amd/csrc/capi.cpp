@@ -1951,9 +1951,19 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
       const Extent out_b = GemmWrites(b);
       const Extent t_b{reinterpret_cast<const uint8_t*>(b.A), b.M * b.K * 4};
       const Extent r_b{static_cast<const uint8_t*>(b.B), b.N * b.K * 4};
+      // C' may be written over the product's own addend, exactly (the dX
+      // chains' ping-pong buffers): each element's addend is read by the
+      // lane that then writes its C', before it does.
+      const bool over_addend = a.addend &&
+                               reinterpret_cast<const uint8_t*>(a.addend) == out_b.p &&
+                               out_b.n == a.M * a.N * 4;
+      bool b_hits_reads = false;
+      for (int i = 0; i < na; ++i)
+        if (!(over_addend && reads_a[i].p == out_b.p && reads_a[i].n == out_b.n) &&
+            Overlap(out_b.p, out_b.n, reads_a[i].p, reads_a[i].n))
+          b_hits_reads = true;
       if (Overlap(out_a.p, out_a.n, out_b.p, out_b.n) || Hits(out_a, &t_b, 1) ||
-          Hits(out_a, &r_b, 1) || Hits(out_b, reads_a, na) || Hits(out_b, &t_b, 1) ||
-          Hits(out_b, &r_b, 1))
+          Hits(out_a, &r_b, 1) || b_hits_reads || Hits(out_b, &t_b, 1) || Hits(out_b, &r_b, 1))
         return -1;
       // C's store is dropped where the rest of the range overwrites C
       // before anything reads it.
@@ -1965,7 +1975,7 @@ int TryFuseLowRank(seeai_ctx* c, const Instruction& ins, const uint8_t* at,
       // itself, or C when C's store is dropped; it misses everything else
       // the pass reads.
       bool res_add = false;
-      if (j + 1 < c->range_end) {
+      if (j + 1 < c->range_end && !over_addend) {
         Instruction ad;
         std::memcpy(&ad, c->prog + (j + 1) * 64, sizeof ad);
         const Ptrs R{c};

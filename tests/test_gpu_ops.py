@@ -1230,7 +1230,8 @@ def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
     assert ranged.tobytes() == _restored(apart, ar, ["P1"], arena).tobytes()
 
 
-GAP_CASES = ["grads_between", "one_between", "mid_reads_c", "mid_writes_dc", "four_between"]
+GAP_CASES = ["grads_between", "one_between", "mid_reads_c", "mid_writes_dc", "four_between",
+             "over_addend"]
 
 
 @pytest.mark.parametrize("case", GAP_CASES)
@@ -1242,7 +1243,9 @@ def test_lora_dx_site_folds_over_the_adapter_gradients(hip, orc, backend, case):
     dispatch, P1 dropped): bitwise the instructions one by one.  Refused --
     every instruction at its place -- when an in-between GEMM reads P1 (it
     would read it before the product writes it), writes dC (the product's
-    operand), or when four GEMMs sit between."""
+    operand), or when four GEMMs sit between.  An f32 frozen product with an
+    addend whose rank-r term writes back over that addend (the dX chains'
+    ping-pong buffers) folds too."""
     from tests.plan_ops import ins
     M, D, r_ = 512, 1024, 16
     r = rng(GAP_CASES.index(case) + 61)  # a fixed seed per case
@@ -1269,6 +1272,13 @@ def test_lora_dx_site_folds_over_the_adapter_gradients(hip, orc, backend, case):
         mids.append(ins(2, [dC, B, dt2], [M, r_, D]))
     prog = ([ins(30, [dC, w, p1, ws], [M, D, D], flags=rx | cs_flag)] + mids +
             [ins(2, [dt, A, p2, p1], [M, D, r_], flags=1 << 3)])
+    out = "P2"
+    if case == "over_addend":  # P1 = dC Wf^T + Q, then Q = P1 + dt A^T
+        wf = ar.add("Wf", (r.standard_normal((D, D)) * 0.02).astype(np.float32), rodata=True)
+        q = ar.add("Q", r.standard_normal((M, D)).astype(np.float32))
+        prog = ([ins(2, [dC, wf, p1, q], [M, D, D], flags=rx | (1 << 3))] + mids +
+                [ins(2, [dt, A, q, p1], [M, D, r_], flags=1 << 3)])
+        out = "Q"
     cpu, apart = execute(hip, orc, backend, ar, prog)
     before = backend.fused_dispatches()
     arena, ro = ar.images()
@@ -1276,12 +1286,12 @@ def test_lora_dx_site_folds_over_the_adapter_gradients(hip, orc, backend, case):
     backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
     backend.Flush()
     ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
-    folds = case in ("grads_between", "one_between")
+    folds = case in ("grads_between", "one_between", "over_addend")
     assert backend.fused_dispatches() - before == int(folds)
     dead = ["P1"] if folds else []
     assert ranged.tobytes() == _restored(apart, ar, dead, arena).tobytes()
-    e = maxrel(ar.get(ranged, "P2"), ar.get(cpu, "P2"))
-    assert e <= TOL_BF16, f"P2: {e:.3g}"
+    e = maxrel(ar.get(ranged, out), ar.get(cpu, out))
+    assert e <= TOL_BF16, f"{out}: {e:.3g}"
     # the exact adapter GEMMs against the oracle (dB reads the relaxed P1
     # where the case makes it)
     for name in ("dt", "dA") + (() if case == "mid_reads_c" else ("dB",)):
