@@ -1697,6 +1697,49 @@ bool OverwritesWhatItWrites(uint16_t op) {
 // start and ends at the writer: a value that only the next step's earlier
 // instructions read keeps its store.  An instruction whose extents are not
 // modelled keeps the store.
+int SiluOperand(seeai_ctx* c, uint64_t at_idx, const float* p0, const float* p1, const float* x,
+                uint64_t n);
+
+// Whether the SwiGLU backward triple at index t (kMulEW, kMulEW, kSiluBwd)
+// runs as the fused pass that forms its y = SiLU(x) rather than reading it,
+// and E is exactly that y, read by nothing else of the triple: the same
+// checks the pass makes (TryFuseElementwise), on the same program words.
+bool SwigluBwdRecomputes(seeai_ctx* c, uint64_t t, const Extent& E) {
+  if (!c->allow_fusion || !c->prog || !c->cur_at || t + 2 >= c->range_end) return false;
+  Instruction i0, i1, i2;
+  std::memcpy(&i0, c->prog + t * 64, sizeof i0);
+  std::memcpy(&i1, c->prog + (t + 1) * 64, sizeof i1);
+  std::memcpy(&i2, c->prog + (t + 2) * 64, sizeof i2);
+  const uint64_t n = i0.out[0];
+  if (i0.opcode != 21 || i1.opcode != 21 || i2.opcode != 25 || i1.out[0] != n ||
+      i2.out[0] != n || E.n != n * 4)
+    return false;
+  const bool first = i2.in[0] == i0.in[2];
+  if (!first && i2.in[0] != i1.in[2]) return false;
+  const Instruction& m1 = first ? i0 : i1;
+  const Instruction& m2 = first ? i1 : i0;
+  const Ptrs R{c};
+  const float *a1 = R.f(m1.in[0]), *b1 = R.f(m1.in[1]), *a2 = R.f(m2.in[0]), *b2 = R.f(m2.in[1]),
+              *x = R.f(i2.in[1]);
+  float *o1 = R.f(m1.in[2]), *o2 = R.f(m2.in[2]), *dx = R.f(i2.in[2]);
+  const uint64_t nb = n * 4;
+  for (const float* o : {o1, o2, dx}) {
+    const auto* op = reinterpret_cast<const uint8_t*>(o);
+    for (const float* q : {o1, o2, dx})
+      if (q != o && Overlap(op, nb, reinterpret_cast<const uint8_t*>(q), nb)) return false;
+    for (const float* q : {a1, b1, a2, b2, x})
+      if (Overlap(op, nb, reinterpret_cast<const uint8_t*>(q), nb)) return false;
+  }
+  if (!SwigluFits(n, {a1, b1, o1, a2, b2, o2, x, dx})) return false;
+  const int silu = SiluOperand(c, t, a2, b2, x, n);
+  const float* y = silu == 1 ? a2 : silu == 2 ? b2 : nullptr;
+  if (!y || reinterpret_cast<const uint8_t*>(y) != E.p) return false;
+  const float* other = silu == 1 ? b2 : a2;
+  for (const float* q : {a1, b1, other, x})
+    if (Overlap(reinterpret_cast<const uint8_t*>(q), nb, E.p, E.n)) return false;
+  return true;
+}
+
 bool DeadFrom(seeai_ctx* c, uint64_t writer, uint64_t from, const Extent& E) {
   for (uint64_t i = from; i < c->prog_count + writer + 1; ++i) {
     const uint64_t k = i < c->prog_count ? i : i - c->prog_count;
@@ -1712,6 +1755,11 @@ bool DeadFrom(seeai_ctx* c, uint64_t writer, uint64_t from, const Extent& E) {
       if (!t[i].write) read = true;
       else if (t[i].p <= E.p && E.p + E.n <= t[i].p + t[i].n) covered = true;
     }
+    // A read that the fused SwiGLU backward replaces by forming y itself is
+    // none (the triple reads E nowhere else; scanning goes on past it).
+    if (touched && read && !covered && i < c->prog_count &&
+        (SwigluBwdRecomputes(c, k, E) || (k > 0 && SwigluBwdRecomputes(c, k - 1, E))))
+      continue;
     if (touched) return covered && !read && OverwritesWhatItWrites(ins.opcode);
   }
   return true;
@@ -2130,8 +2178,14 @@ int TryFuseElementwise(seeai_ctx* c, const Instruction& ins, const uint8_t* at) 
     if (!clear({y, h}, {x, u})) return -1;
     Bf16Sink sink;
     GemmArgs ga{};
-    const bool sunk = SwigluFits(n, {x, u, y, h}) && PlanSink(c, idx + 1, idx + 1, h, n, &sink, &ga);
-    SEEAI_TRY(c, LaunchSiluMul(x, u, y, h, n, c->stream, sink), "silu_mul");
+    const bool fits = SwigluFits(n, {x, u, y, h});
+    const bool sunk = fits && PlanSink(c, idx + 1, idx + 1, h, n, &sink, &ga);
+    // y's store is dropped where nothing reads it before it is written again
+    // -- the backward pass that forms y from x does not read it.
+    float* y_store =
+        fits && DeadStore(c, idx, idx + 2, Extent{reinterpret_cast<const uint8_t*>(y), nb}) ? nullptr
+                                                                                           : y;
+    SEEAI_TRY(c, LaunchSiluMul(x, u, y_store, h, n, c->stream, sink), "silu_mul");
     if (sunk) SinkDone(c, idx + 1, ga);
     c->done[0] = at + 64;
     c->ndone = 1;

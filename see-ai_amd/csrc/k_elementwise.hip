@@ -597,7 +597,7 @@ SiluMul4(const float4* __restrict__ x, const float4* __restrict__ u, float4* __r
   for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
     const float4 a = x[i], b = u[i];
     const float4 g = make_float4(SiluExpr(a.x), SiluExpr(a.y), SiluExpr(a.z), SiluExpr(a.w));
-    y[i] = g;
+    if (y) y[i] = g;  // null: y is dead after the pass
     const float4 hv = make_float4(g.x * b.x, g.y * b.y, g.z * b.z, g.w * b.w);
     if (sink.store_f32) h[i] = hv;
     if (sink.out) SinkStore4(sink, 4 * i, hv);
@@ -696,7 +696,7 @@ hipError_t LaunchSiluMul(const float* x, const float* u, float* y, float* h, siz
                        reinterpret_cast<float4*>(y), reinterpret_cast<float4*>(h), n / 4, sink);
     return hipGetLastError();
   }
-  if (sink.out || !sink.store_f32) return hipErrorInvalidValue;
+  if (sink.out || !sink.store_f32 || !y) return hipErrorInvalidValue;
   return Map(n, s, [=] __device__(size_t i) {
     const float g = SiluExpr(x[i]);
     y[i] = g;

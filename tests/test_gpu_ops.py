@@ -1405,7 +1405,9 @@ def test_swiglu_chains_fuse_bitwise(hip, orc, backend, n, order, read_later):
     a range: bitwise the instructions one by one (and the oracle's within
     libm), two fused dispatches.  With the two products in the other order,
     SiluBwd reads the second one: still one pass.  dsg is stored only where
-    the program reads it again (read_later); otherwise it keeps its bytes."""
+    the program reads it again (read_later); otherwise it keeps its bytes.
+    The backward forms y = SiLU(g) from g (y's writer is the SiLU forward of
+    that g), so with float4 rows the forward's y store is dropped as well."""
     from tests.plan_ops import ins
     r = rng(n)
     ar = Arena()
@@ -1425,10 +1427,11 @@ def test_swiglu_chains_fuse_bitwise(hip, orc, backend, n, order, read_later):
     backend.Flush()
     fused = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
     assert backend.fused_dispatches() - before == 2
-    dead = [] if read_later else ["dsg"]
+    dead = ([] if read_later else ["dsg"]) + (["y"] if n % 4 == 0 else [])
     assert backend.dropped_stores() - dropped_before == len(dead)
     assert fused.tobytes() == _restored(apart, ar, dead, arena).tobytes()
-    for name in ["y", "h", "dup", "dg"] + (["dsg", "dsg_read"] if read_later else []):
+    for name in [k for k in ("y", "h", "dup", "dg") if k not in dead] + (
+            ["dsg", "dsg_read"] if read_later else []):
         e = maxrel(ar.get(fused, name), ar.get(cpu, name))
         assert e <= TOL, f"{name}: {e:.3g}"
 
