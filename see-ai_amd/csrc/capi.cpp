@@ -937,9 +937,25 @@ int ExecuteOne(seeai_ctx* c, const Instruction& ins, const seeai_step_params& P)
       const char* what = DecodeGemm(c, ins, &a);
       a.relaxed = Relaxed(c, ins);
       if (int rc = PlanRowMaxParts(c, &a)) return rc;
+      // C read next by a bf16-copy attention (a backward's dO): its copy
+      // written in the epilogue.
+      int pre_slot = -1;
+      uint64_t pre_at = 0;
+      if (c->cur_at && a.relaxed && c->allow_dma && !a.row_max_part) {
+        a.policy = &c->policy;
+        GemmArgs t = a;
+        t.lr_sink = PlanAttnCopy(c, CurIndex(c), a.C, a.M * a.N, &pre_slot, &pre_at);
+        if (t.lr_sink && Bf16DmaRowMaxFits(t) && Immutable(c, t.B)) a = t;
+        else pre_slot = -1;
+      }
       if (int rc = Gemm(c, a, what)) return rc;
       if (a.row_max_part)
         c->pmax_key = {a.C, a.M, a.N, CurIndex(c) + 1, c->a16_epoch};
+      if (pre_slot >= 0) {
+        c->a16_pre[pre_slot].src = a.C;
+        c->a16_pre[pre_slot].at = pre_at;
+        c->a16_pre[pre_slot].epoch = c->a16_epoch;
+      }
       return SEEAI_OK;
     }
     case 5: {

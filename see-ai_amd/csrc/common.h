@@ -357,7 +357,8 @@ struct GemmArgs {
   // the add's operand order immaterial (IEEE addition commutes); null: none.
   const float* lr_res;
   // lr_out's bf16 copy (round to nearest even, same [M, N] layout) for the
-  // attention that reads it next; null: none.
+  // attention that reads it next -- C's, on the kernel without a low-rank
+  // term; null: none.
   uint16_t* lr_sink;
   // The relaxed direct-to-LDS kernel without a low-rank term: C's row maxima
   // over each group of 64 columns, [M, ceil(N / 64)] (fmax: NaN ignored, a

@@ -285,6 +285,11 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
             if (m < M && n < N) {
               *reinterpret_cast<float4*>(g.C + static_cast<size_t>(m) * N + n) = make_float4(
                   acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+              if (g.lr_sink) {  // C's bf16 copy for the attention that reads it next
+                const float cv[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                     acc[i][j][4 * q + 3]};
+                StoreBf16x4(g.lr_sink + static_cast<size_t>(m) * N + n, cv);
+              }
               if (g.row_max_part)
                 pm = fmaxf(pm, fmaxf(fmaxf(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
                                      fmaxf(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])));
@@ -332,6 +337,10 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
               }
               x0 = ActF(g.act, x0), x1 = ActF(g.act, x1), x2 = ActF(g.act, x2), x3 = ActF(g.act, x3);
               *reinterpret_cast<float4*>(C + o) = make_float4(x0, x1, x2, x3);
+              if (g.lr_sink) {
+                const float cv[4] = {x0, x1, x2, x3};
+                StoreBf16x4(g.lr_sink + o, cv);
+              }
               if (g.row_max_part) pm = fmaxf(pm, fmaxf(fmaxf(x0, x1), fmaxf(x2, x3)));
             }
           }
@@ -790,7 +799,10 @@ hipError_t LaunchWeightShadow(const GemmArgs& a, void* out, hipStream_t s) {
 // 128 x 128 (four waves of 64 x 64).  Both accumulate each output over k in
 // the same 16-deep MFMA steps: the same bits.
 hipError_t LaunchGemmBf16Dma(const void* A, const void* W, const GemmArgs& a, hipStream_t s) {
-  if (a.row_max_part && !Bf16DmaRowMaxFits(a)) return hipErrorInvalidValue;
+  // The partial row maxima and (with no low-rank term) C's bf16 copy ride
+  // the epilogue that stores from registers.
+  if ((a.row_max_part || (a.lr_sink && !a.lr_out)) && !Bf16DmaRowMaxFits(a))
+    return hipErrorInvalidValue;
   const size_t Kp = Bf16DmaKp(a.K);
   const auto* Ab = static_cast<const __bf16*>(A);
   const auto* Wb = static_cast<const __bf16*>(W);

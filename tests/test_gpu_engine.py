@@ -649,11 +649,11 @@ def test_c5_width_slice_step_tensors_match_the_oracle(hip, orc, torch_cuda, mode
 SINKS_PER_STEP = {"c4": 15, "c5": 17}
 # With attention on bf16 copies, per block: the attention forward writes the
 # O product's activation, the RoPE forwards of q and k write the attention's
-# own copies of them, and the V site's low-rank pass writes v's; in c5 the O
-# site's input-gradient pass also writes the attention backward's dO.  Per
-# step, the upper block's dK / dV pass writes dV's for its input-gradient
-# product.
-ATTN_SINKS_PER_STEP = {"c4": 4 * 2 + 1, "c5": 5 * 2 + 1}
+# own copies of them, the V site's low-rank pass writes v's, and the O
+# product (c4) or the O site's input-gradient pass (c5) writes the attention
+# backward's dO.  Per step, the upper block's dK / dV pass writes dV's for its
+# input-gradient product.
+ATTN_SINKS_PER_STEP = {"c4": 5 * 2 + 1, "c5": 5 * 2 + 1}
 
 
 @pytest.mark.parametrize("attn16", [False, True])
