@@ -1298,7 +1298,7 @@ def test_lora_dx_site_folds_over_the_adapter_gradients(hip, orc, backend, case):
         assert bits_equal(ar.get(ranged, name), ar.get(cpu, name)), name
 
 
-FAR_CASES = ["gemms_between", "copy_between", "writer_between", "five_pending"]
+FAR_CASES = ["gemms_between", "copy_between", "writer_between", "five_pending", "split_ranges"]
 
 
 @pytest.mark.parametrize("case", FAR_CASES)
@@ -1347,10 +1347,16 @@ def test_rope_backward_writes_a_later_products_copy(hip, orc, backend, case):
     convs = backend.fused_conversions()
     arena, ro = ar.images()
     backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
-    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    sp = hip.StepParams(*PARAMS[:5], 0, PARAMS[5])
+    if case == "split_ranges":  # the product in a range of its own: it converts
+        backend.ExecuteRange(b"".join(prog[:-1]), sp)
+        backend.ExecuteRange(prog[-1], sp)
+    else:
+        backend.ExecuteRange(b"".join(prog), sp)
     backend.Flush()
     ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
-    sinks = {"gemms_between": 1, "copy_between": 1, "writer_between": 1, "five_pending": 5}[case]
+    sinks = {"gemms_between": 1, "copy_between": 1, "writer_between": 1, "five_pending": 5,
+             "split_ranges": 0}[case]
     assert backend.fused_conversions() - convs == sinks
     diff = np.flatnonzero(ranged != apart)
     assert diff.size == 0, f"{diff.size} bytes differ from byte {diff[:1]}"
@@ -1485,6 +1491,40 @@ def test_swiglu_backward_writes_both_products_copies(hip, orc, backend, case):
     for name in ("dup" if case == "first_writes_dup" else "xg", "xu"):
         e = maxrel(ar.get(ranged, name), ar.get(cpu, name))
         assert e <= TOL_BF16, f"{name}: {e:.3g}"
+
+
+def test_swiglu_forward_keeps_y_when_the_backward_runs_in_another_range(hip, orc, backend):
+    """The forward's y store is dropped only where the backward pass that
+    forms y from g lies in the same range: with one program run as two
+    ranges, the forward's and the backward's, y is stored (the dead-store
+    scan still sees the whole program), bitwise the instructions one by one
+    apart from the unread dsg."""
+    import ctypes as C
+    from tests.plan_ops import ins
+    n = 4096
+    r = rng(77)
+    ar = Arena()
+    g, u, dh = (ar.add(k, r.standard_normal(n).astype(np.float32)) for k in ("g", "u", "dh"))
+    y, h, dsg, dup, dg = (ar.empty(k, (n,)) for k in ("y", "h", "dsg", "dup", "dg"))
+    fwd = [ins(24, [g, y], [n]), ins(21, [y, u, h], [n])]
+    bwd = [ins(21, [dh, u, dsg], [n]), ins(21, [dh, y, dup], [n]), ins(25, [dsg, g, dg], [n])]
+    cpu, apart = execute(hip, orc, backend, ar, fwd + bwd)
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    dropped_before = backend.dropped_stores()
+    sp = hip.StepParams(*PARAMS[:5], 0, PARAMS[5])
+    whole = b"".join(fwd + bwd)
+    buf = C.create_string_buffer(whole, len(whole))
+    ctx = backend.ctx
+    for lo, hi in ((0, len(fwd)), (len(fwd), len(fwd) + len(bwd))):
+        ctx.call("seeai_begin_range", buf, len(fwd) + len(bwd), lo, hi)
+        for i in range(lo, hi):
+            ctx.call("seeai_execute", C.cast(C.addressof(buf) + 64 * i, C.c_void_p), C.byref(sp))
+        ctx.call("seeai_end_range")
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.dropped_stores() - dropped_before == 1  # dsg only
+    assert ranged.tobytes() == _restored(apart, ar, ["dsg"], arena).tobytes()
 
 
 def test_swiglu_chain_refuses_to_fuse_over_an_input(hip, orc, backend):
