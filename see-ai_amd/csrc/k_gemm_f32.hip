@@ -190,6 +190,8 @@ hipError_t Dispatch(const GemmArgs& a, hipStream_t s) {
 
 hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s) {
   if (a.M == 0 || a.N == 0) return hipSuccess;
+  // The extra outputs of the direct-to-LDS kernel's epilogue exist there only.
+  if (a.lr_out || a.lr_sink || a.row_max_part) return hipErrorInvalidValue;
   // The exact family keeps the reference's reduction order (bit-exact,
   // k_gemm_exact.hip); MFMA's own summation order is the relaxed family's.
   if (!a.relaxed) return LaunchGemmExact(a, s);
