@@ -1331,6 +1331,31 @@ bool Fold(const GemmArgs& a) {
   return a.layout == 2 || (a.layout == 0 && a.M * a.N > 16384);
 }
 
+// NN with a narrow f32 B -- the LoRA products t = X A, N = 8 or 16 -- over
+// many rows and K past the panel kernel's: role-split folds of 32 x 8 or
+// 16 x 16 output blocks, four outputs per folder lane, 128-deep chunks (two
+// workgroups' LDS per CU).  C4's 8192 x 8 x 768: 17.8 us on the chain
+// kernel -> 8.0; C5's 8192 x 16 x 2048: 37.9 on the 8 x 16 fold -> 29-30
+// (one box, bitwise the same sums).
+bool FoldNarrowNN(const GemmArgs& a) {
+  const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return a.layout == 0 && a.b_kind == 0 && (a.N == 8 || a.N == 16) &&
+         a.K > static_cast<size_t>(kPanelK) && a.K % 4 == 0 && a.M % 32 == 0 && a.M >= 4096 &&
+         a.M / 16 <= 65535 && a.K * a.M < (size_t{1} << 31) && al16(a.A) && al16(a.B) &&
+         !a.a_k_scale;
+}
+
+hipError_t LaunchFoldNarrowNN(const GemmArgs& a, hipStream_t s) {
+  if (a.N == 8) {
+    hipLaunchKernelGGL((GemmFoldSplitKernel<0, 32, 8, 128, 2, 4, 4, 9, 4>),
+                       dim3(1, static_cast<unsigned>(a.M / 32)), dim3(576), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((GemmFoldSplitKernel<0, 16, 16, 128, 2, 4, 4, 9, 4>),
+                       dim3(1, static_cast<unsigned>(a.M / 16)), dim3(576), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
 template <int kLayout>
 hipError_t LaunchFold(const GemmArgs& a, hipStream_t s) {
   // BNo: N rounded up to a power of two in [2, 16] (a chunk of B then spans
@@ -1459,6 +1484,8 @@ hipError_t Run(const GemmArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((GemmPanelKernel<kLayout, kBKind>), grid, dim3(kThreads), lds, s, a);
     return hipGetLastError();
   }
+  if constexpr (kLayout == 0 && kBKind == 0)
+    if (FoldNarrowNN(a)) return LaunchFoldNarrowNN(a, s);
   if constexpr (kLayout != 1 && kBKind == 0)
     if (Fold(a)) return LaunchFold<kLayout>(a, s);
   if constexpr (kLayout == 1 && kBKind == 0)

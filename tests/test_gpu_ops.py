@@ -41,9 +41,11 @@ GEMM_SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (5, 9, 3), (67, 129, 66), (130, 
                # rank-r products: wide outputs over K <= 32 (four outputs per lane)
                (67, 1100, 16), (130, 512, 8), (100, 260, 13), (96, 256, 32), (70, 512, 21),
                # the LoRA products t = X A on the role-split fold (NN): 8 x 16 blocks over
-               # a K % 256 tail, 4 x 8 blocks over a partial 512-deep chunk; C4's
-               # 8192 x 8 x 768 on the chain kernel
-               (2048, 16, 2056), (4096, 8, 1300), (8192, 8, 768),
+               # a K % 256 tail; the narrow NN folds (32 x 8 and 16 x 16 blocks,
+               # 128-deep chunks): C4's 8192 x 8 x 768, partial last chunks, K just
+               # past the panel kernel's
+               (2048, 16, 2056), (4096, 8, 1300), (8192, 8, 768), (4096, 16, 1028),
+               (8192, 8, 516),
                # NT k-lane kernel (dt = dC B^T): C5's 8192 x 16 x 2048, twelve outputs
                # over a partial last chunk, two output groups over a 44-deep tail
                (8192, 16, 2048), (2048, 12, 1028), (4096, 16, 300),
