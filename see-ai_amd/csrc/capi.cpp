@@ -2317,6 +2317,37 @@ int TryFuseAddend(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
   return SEEAI_OK;
 }
 
+// Two adjacent exact TN products that read nothing the first writes and
+// write apart from each other and from what the first reads (a LoRA
+// site's dB = t^T dC and dA = X^T dt) run as one launch where each alone
+// would leave CUs idle (GemmExactPairFits): the same sums, bit for bit.
+int TryFuseGemmPair(seeai_ctx* c, const Instruction& ins, const uint8_t* at) {
+  if (!c->allow_fusion || !c->cur_at || !c->prog || at != c->cur_at || ins.opcode != 3) return -1;
+  const uint64_t idx = CurIndex(c);
+  if (idx + 1 >= c->range_end) return -1;
+  Instruction nx;
+  std::memcpy(&nx, c->prog + (idx + 1) * 64, sizeof nx);
+  if (nx.opcode != 3) return -1;
+  const auto relaxed = [&](const Instruction& i) {
+    return (i.flags & kFlagRelaxed) && c->allow_relaxed;
+  };
+  if (relaxed(ins) || relaxed(nx)) return -1;
+  GemmArgs a{}, b{};
+  const char* what = DecodeGemm(c, ins, &a);
+  if (!what || !DecodeGemm(c, nx, &b)) return -1;
+  a.policy = b.policy = &c->policy;
+  if (!GemmExactPairFits(a, b)) return -1;
+  Extent ra[8], rb[8];
+  const int nra = GemmReads(a, ra), nrb = GemmReads(b, rb);
+  const Extent wa = GemmWrites(a), wb = GemmWrites(b);
+  if (Hits(wa, rb, nrb) || Hits(wb, ra, nra) || Hits(wb, &wa, 1)) return -1;
+  SEEAI_TRY(c, LaunchGemmExactPair(a, b, c->stream), what);
+  c->done[0] = at + 64;
+  c->ndone = 1;
+  ++c->fused;
+  return SEEAI_OK;
+}
+
 // The residual add behind a normalisation's gradient: LayerNorm / RMSNorm
 // backward writing dx, then kAddEW of dx and a residual gradient R, runs as
 // one pass writing R + dx into the add's output (with the add's conversion
@@ -2479,6 +2510,7 @@ int seeai_execute(seeai_ctx* c, const void* instruction, const seeai_step_params
   if (rc < 0) rc = TryFuseElementwise(c, ins, at);
   if (rc < 0) rc = TryFuseNormAdd(c, ins, at);
   if (rc < 0) rc = TryFuseXEnt(c, ins, at, P);
+  if (rc < 0) rc = TryFuseGemmPair(c, ins, at);
   if (rc < 0) rc = TryFuseAddend(c, ins, at);
   if (rc < 0) rc = ExecuteOne(c, ins, P);
   c->cur_at = nullptr;

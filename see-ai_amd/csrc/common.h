@@ -369,6 +369,10 @@ constexpr int kLowRankMaxK = 16;
 // Relaxed -> MFMA (k_gemm_f32.hip); otherwise the reference's order.
 hipError_t LaunchGemm(const GemmArgs& a, hipStream_t s);
 hipError_t LaunchGemmExact(const GemmArgs& a, hipStream_t s);
+// Two independent exact TN products in one launch, where both take the
+// fold kernel and their blocks fit the CUs side by side.
+bool GemmExactPairFits(const GemmArgs& a, const GemmArgs& b);
+hipError_t LaunchGemmExactPair(const GemmArgs& a, const GemmArgs& b, hipStream_t s);
 // Workspace the exact kernels can use for this GEMM (0: none).
 size_t GemmExactScratchBytes(const GemmArgs& a);
 // Relaxed NN / NT on bf16 operands staged by direct-to-LDS loads

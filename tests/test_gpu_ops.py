@@ -1232,6 +1232,51 @@ def test_lora_site_refuses_to_fold_when_t_lands_on_c(hip, orc, backend):
     assert ranged.tobytes() == _restored(apart, ar, ["P1"], arena).tobytes()
 
 
+PAIR_CASES = ["independent", "second_reads_first", "outputs_overlap", "relaxed", "too_wide"]
+
+
+@pytest.mark.parametrize("case", PAIR_CASES)
+def test_adjacent_adapter_gradients_run_as_one_launch(hip, orc, backend, case):
+    """A LoRA site's two exact TN gradients, dB = t^T dC then dA = X^T dt
+    (rank 8, width 768, 1024 tokens), run as one launch when neither reads
+    or overwrites what the other touches and their fold blocks fit the CUs
+    side by side: bit for bit the oracle and the instructions one by one.
+    The second reading the first's output, the two writing one buffer, a
+    relaxed flag (the relaxed family's own kernels) or blocks past one per
+    CU (width 2048 at rank 16) keep them apart."""
+    from tests.plan_ops import ins
+    r, D, K = (16, 2048, 1024) if case == "too_wide" else (8, 768, 1024)
+    g = rng(PAIR_CASES.index(case) + 83)
+    ar = Arena()
+    t = ar.add("t", g.standard_normal((K, r)).astype(np.float32))
+    dC = ar.add("dC", g.standard_normal((K, D)).astype(np.float32))
+    X = ar.add("X", g.standard_normal((K, D)).astype(np.float32))
+    dt = ar.add("dt", g.standard_normal((K, r)).astype(np.float32))
+    dA = ar.empty("dA", (D, r))
+    fl = (1 << 5) if case == "relaxed" else 0
+    first = ins(3, [t, dC, ar.empty("dB", (r, D))], [r, D, K], imm=f32_bits(2.0), flags=fl)
+    second = ins(3, [X, dt, dA], [D, r, K], flags=fl)
+    if case == "second_reads_first":  # the second's B [K, r] begins with the first's D x r output
+        both = ar.empty("both", (K, r))
+        first = ins(3, [X, dt, both], [D, r, K])
+        second = ins(3, [X, both, dA], [D, r, K])
+    if case == "outputs_overlap":  # both write dA
+        first = ins(3, [X, dt, dA], [D, r, K], imm=f32_bits(2.0))
+    prog = [first, second]
+    cpu, apart = execute(hip, orc, backend, ar, prog)
+    fused = backend.fused_dispatches()
+    arena, ro = ar.images()
+    backend.Bind(arena.tobytes(), arena.nbytes, ro.tobytes())
+    backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
+    backend.Flush()
+    ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
+    assert backend.fused_dispatches() - fused == (1 if case == "independent" else 0)
+    assert ranged.tobytes() == apart.tobytes()
+    if case != "relaxed":
+        for name in ar.meta:
+            assert bits_equal(ar.get(ranged, name), ar.get(cpu, name)), name
+
+
 GAP_CASES = ["grads_between", "one_between", "mid_reads_c", "mid_writes_dc", "four_between",
              "over_addend"]
 
