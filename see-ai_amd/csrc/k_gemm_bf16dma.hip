@@ -420,10 +420,13 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
   }
   if constexpr (kLR != 0) {
     // Rank 8 or 16 with nothing but the column scale and alpha before the
-    // low-rank term: the rank is a constant, so each pass is one block of
+    // low-rank term (on 128 x 128 NT sites also an addend, which adds after
+    // alpha as in the general pass; the 256 x 256 instance has no registers
+    // to spare for it): the rank is a constant, so each pass is one block of
     // four independent chains; a residual behind the site (NN or NT) adds
     // last.
-    const bool plain = !add && !g.accumulate && !bias && !g.act;
+    constexpr bool kAddFast = kLR == 2 && BM * BN <= 128 * 128;
+    const bool plain = (!add || kAddFast) && !g.accumulate && !bias && !g.act;
     auto fast = [&](auto rq_tag) {
       constexpr int RQ = decltype(rq_tag)::value;
       float csq[4];
@@ -441,16 +444,24 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
       // lane writes it, also where the output is the residual itself).
       constexpr int kSteps = 32 / kRowsPerPass, kResAhead = kLR == 1 ? 4 : 2;
       float4 rr[kResAhead];
-      auto res_load = [&](int s) {
+      auto res_load = [&](const float* src, int s) {
         const int m = m0 + wm + (s / kSteps) * 32 + row0 + (s % kSteps) * kRowsPerPass;
         const int n = n0 + wn + c4 * 4;
         return epi_lane && m < M && n < N && s < TM * kSteps
-                   ? *reinterpret_cast<const float4*>(g.lr_res + static_cast<size_t>(m) * N + n)
+                   ? *reinterpret_cast<const float4*>(src + static_cast<size_t>(m) * N + n)
                    : make_float4(0.f, 0.f, 0.f, 0.f);
       };
       if (g.lr_res) {
 #pragma unroll
-        for (int s = 0; s < kResAhead; ++s) rr[s] = res_load(s);
+        for (int s = 0; s < kResAhead; ++s) rr[s] = res_load(g.lr_res, s);
+      }
+      // The NT site's addend, in flight the same way.
+      float4 ra[kAddFast ? kResAhead : 1];
+      if constexpr (kAddFast) {
+        if (add) {
+#pragma unroll
+          for (int s = 0; s < kResAhead; ++s) ra[s] = res_load(add, s);
+        }
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
@@ -472,6 +483,14 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
           float v[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = alpha * (v[e] * csq[e]);  // x 1.0f is exact
+          if constexpr (kAddFast) {
+            if (add) {
+              const int s = i * kSteps + tt;
+              const float4 a4 = ra[s % kResAhead];
+              if (s + kResAhead < TM * kSteps) ra[s % kResAhead] = res_load(add, s + kResAhead);
+              v[0] = a4.x + v[0], v[1] = a4.y + v[1], v[2] = a4.z + v[2], v[3] = a4.w + v[3];
+            }
+          }
           const size_t o = static_cast<size_t>(m) * N + n;
           if (g.lr_store_c) *reinterpret_cast<float4*>(C + o) = make_float4(v[0], v[1], v[2], v[3]);
           float t[kLowRankMaxK];
@@ -489,7 +508,7 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
           if (g.lr_res) {
             const int s = i * kSteps + tt;
             const float4 r4 = rr[s % kResAhead];
-            if (s + kResAhead < TM * kSteps) rr[s % kResAhead] = res_load(s + kResAhead);
+            if (s + kResAhead < TM * kSteps) rr[s % kResAhead] = res_load(g.lr_res, s + kResAhead);
             o4[0] = AddRn(r4.x, o4[0]), o4[1] = AddRn(r4.y, o4[1]);
             o4[2] = AddRn(r4.z, o4[2]), o4[3] = AddRn(r4.w, o4[3]);
           }
@@ -736,7 +755,7 @@ bool Bf16DmaLowRankFits(const GemmArgs& a) {
   return a.lr_out && a.lr_t && a.lr_b && a.lr_layout >= 0 && a.lr_layout <= 1 && a.lr_k >= 1 &&
          a.lr_k <= kLowRankMaxK && a.lr_k % 4 == 0 && a.N % 4 == 0 && !a.accumulate &&
          al16(a.lr_t) && al16(a.lr_out) && al16(a.C) && (a.lr_layout == 1 || al16(a.lr_b)) &&
-         al16(a.lr_res) && (reinterpret_cast<uintptr_t>(a.lr_sink) & 7) == 0 &&
+         al16(a.lr_res) && al16(a.addend) && (reinterpret_cast<uintptr_t>(a.lr_sink) & 7) == 0 &&
          // A residual on an NN site rides the constant-rank pass only (rank 8
          // or 16 with no addend, bias or activation), the general pass adds
          // it on NT sites alone; the bf16 copy of the output rides the
