@@ -420,13 +420,13 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
   }
   if constexpr (kLR != 0) {
     // Rank 8 or 16 with nothing but the column scale and alpha before the
-    // low-rank term (on 128 x 128 NT sites also an addend, which adds after
-    // alpha as in the general pass; the 256 x 256 instance has no registers
-    // to spare for it): the rank is a constant, so each pass is one block of
-    // four independent chains; a residual behind the site (NN or NT) adds
-    // last.
+    // low-rank term (on NT sites also an addend, which adds after alpha as
+    // in the general pass -- loaded ahead on 128 x 128 tiles, at its use on
+    // 256 x 256, which has no registers to spare for a ring): the rank is a
+    // constant, so each pass is one block of four independent chains; a
+    // residual behind the site (NN or NT) adds last.
     constexpr bool kAddFast = kLR == 2 && BM * BN <= 128 * 128;
-    const bool plain = (!add || kAddFast) && !g.accumulate && !bias && !g.act;
+    const bool plain = (!add || kLR == 2) && !g.accumulate && !bias && !g.act;
     auto fast = [&](auto rq_tag) {
       constexpr int RQ = decltype(rq_tag)::value;
       float csq[4];
@@ -483,15 +483,20 @@ GemmBf16DmaKernel(const __bf16* __restrict__ A, const __bf16* __restrict__ W, in
           float v[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = alpha * (v[e] * csq[e]);  // x 1.0f is exact
-          if constexpr (kAddFast) {
+          const size_t o = static_cast<size_t>(m) * N + n;
+          if constexpr (kLR == 2) {
             if (add) {
-              const int s = i * kSteps + tt;
-              const float4 a4 = ra[s % kResAhead];
-              if (s + kResAhead < TM * kSteps) ra[s % kResAhead] = res_load(add, s + kResAhead);
+              float4 a4;
+              if constexpr (kAddFast) {
+                const int s = i * kSteps + tt;
+                a4 = ra[s % kResAhead];
+                if (s + kResAhead < TM * kSteps) ra[s % kResAhead] = res_load(add, s + kResAhead);
+              } else {
+                a4 = *reinterpret_cast<const float4*>(add + o);
+              }
               v[0] = a4.x + v[0], v[1] = a4.y + v[1], v[2] = a4.z + v[2], v[3] = a4.w + v[3];
             }
           }
-          const size_t o = static_cast<size_t>(m) * N + n;
           if (g.lr_store_c) *reinterpret_cast<float4*>(C + o) = make_float4(v[0], v[1], v[2], v[3]);
           float t[kLowRankMaxK];
           const float* trow = tl + (m - m0) * kLowRankMaxK;

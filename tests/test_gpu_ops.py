@@ -1278,7 +1278,7 @@ def test_adjacent_adapter_gradients_run_as_one_launch(hip, orc, backend, case):
 
 
 GAP_CASES = ["grads_between", "one_between", "mid_reads_c", "mid_writes_dc", "four_between",
-             "over_addend"]
+             "over_addend", "over_addend_256"]
 
 
 @pytest.mark.parametrize("case", GAP_CASES)
@@ -1292,7 +1292,8 @@ def test_lora_dx_site_folds_over_the_adapter_gradients(hip, orc, backend, case):
     would read it before the product writes it), writes dC (the product's
     operand), or when four GEMMs sit between.  An f32 frozen product with an
     addend whose rank-r term writes back over that addend (the dX chains'
-    ping-pong buffers) folds too."""
+    ping-pong buffers) folds too, on 128 x 128 tiles and (the tile policy
+    taking 256 x 256 at this size) on 256 x 256."""
     from tests.plan_ops import ins
     M, D, r_ = 512, 1024, 16
     r = rng(GAP_CASES.index(case) + 61)  # a fixed seed per case
@@ -1320,12 +1321,22 @@ def test_lora_dx_site_folds_over_the_adapter_gradients(hip, orc, backend, case):
     prog = ([ins(30, [dC, w, p1, ws], [M, D, D], flags=rx | cs_flag)] + mids +
             [ins(2, [dt, A, p2, p1], [M, D, r_], flags=1 << 3)])
     out = "P2"
-    if case == "over_addend":  # P1 = dC Wf^T + Q, then Q = P1 + dt A^T
+    if case.startswith("over_addend"):  # P1 = dC Wf^T + Q, then Q = P1 + dt A^T
         wf = ar.add("Wf", (r.standard_normal((D, D)) * 0.02).astype(np.float32), rodata=True)
         q = ar.add("Q", r.standard_normal((M, D)).astype(np.float32))
         prog = ([ins(2, [dC, wf, p1, q], [M, D, D], flags=rx | (1 << 3))] + mids +
                 [ins(2, [dt, A, q, p1], [M, D, r_], flags=1 << 3)])
         out = "Q"
+    prev = backend.ctx.policy()
+    if case == "over_addend_256":
+        backend.ctx.configure(dict(prev, relaxed_min_tiles_256=1, relaxed_min_fill_256=1))
+    try:
+        _gap_case_run(hip, orc, backend, ar, prog, case, out)
+    finally:
+        backend.ctx.configure(prev)
+
+
+def _gap_case_run(hip, orc, backend, ar, prog, case, out):
     cpu, apart = execute(hip, orc, backend, ar, prog)
     before = backend.fused_dispatches()
     arena, ro = ar.images()
@@ -1333,7 +1344,7 @@ def test_lora_dx_site_folds_over_the_adapter_gradients(hip, orc, backend, case):
     backend.ExecuteRange(b"".join(prog), hip.StepParams(*PARAMS[:5], 0, PARAMS[5]))
     backend.Flush()
     ranged = np.frombuffer(backend.Download(0, arena.nbytes), np.uint8)
-    folds = case in ("grads_between", "one_between", "over_addend")
+    folds = case in ("grads_between", "one_between", "over_addend", "over_addend_256")
     assert backend.fused_dispatches() - before == int(folds)
     dead = ["P1"] if folds else []
     assert ranged.tobytes() == _restored(apart, ar, dead, arena).tobytes()
