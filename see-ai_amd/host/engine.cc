@@ -1,6 +1,8 @@
 // engine.cc -- the plan engine's step loop (see engine.h).
 #include "engine.h"
 
+#include <sys/mman.h>
+
 #include <cmath>
 #include <condition_variable>
 #include <cstdlib>
@@ -70,12 +72,19 @@ Result<std::unique_ptr<PlanEngine>> PlanEngine::Load(std::span<const uint8_t> bl
                 "never be validated");
 
   // plan_loader.cc:251-288: one zeroed, 16 KiB-aligned allocation holding
-  // the persistent image at offset 0.
+  // the persistent image at offset 0.  Anonymous pages read as zero until
+  // written, so the arena past the image costs no host memory or time (the
+  // mapping is over-sized by one alignment unit and the arena starts at its
+  // first 16 KiB boundary).
   e->arena_bytes_ = (h.arena_size + (kArenaAlignment - 1)) & ~(kArenaAlignment - 1);
   if (e->arena_bytes_ == 0) e->arena_bytes_ = kArenaAlignment;
-  e->arena_ = static_cast<uint8_t*>(std::aligned_alloc(kArenaAlignment, e->arena_bytes_));
-  if (!e->arena_) return Fail("arena allocation failed");
-  std::memset(e->arena_, 0, e->arena_bytes_);
+  e->map_bytes_ = e->arena_bytes_ + kArenaAlignment;
+  void* map = mmap(nullptr, e->map_bytes_, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS,
+                   -1, 0);
+  if (map == MAP_FAILED) return Fail("arena allocation failed");
+  e->map_ = map;
+  e->arena_ = reinterpret_cast<uint8_t*>(
+      (reinterpret_cast<uintptr_t>(map) + (kArenaAlignment - 1)) & ~uintptr_t{kArenaAlignment - 1});
   if (!e->plan_.persist_init.empty())
     std::memcpy(e->arena_, e->plan_.persist_init.data(), e->plan_.persist_init.size());
 
@@ -93,7 +102,7 @@ Result<std::unique_ptr<PlanEngine>> PlanEngine::Load(std::span<const uint8_t> bl
 PlanEngine::~PlanEngine() {
   seeai_feeder_destroy(feeder_);  // before the context it copies into
   backend_.reset();  // the backend's views die before the memory they view
-  std::free(arena_);
+  if (map_) munmap(map_, map_bytes_);
 }
 
 float PlanEngine::EffectiveLr() const {

@@ -101,8 +101,10 @@ class PlanEngine {
   std::vector<uint8_t> blob_;
   Plan plan_;
   std::unique_ptr<HipBackend> backend_;
-  uint8_t* arena_ = nullptr;
+  uint8_t* arena_ = nullptr;  // 16 KiB-aligned, inside the anonymous mapping map_
   uint64_t arena_bytes_ = 0;
+  void* map_ = nullptr;
+  uint64_t map_bytes_ = 0;
   uint64_t step_ = 0;
   uint64_t horizon_ = 0;
   uint64_t num_classes_ = 0;

@@ -3,6 +3,11 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
+#include <cstring>
+#include <thread>
+#include <vector>
+
 #include "seeai_hip.h"
 
 namespace seeai::host {
@@ -37,9 +42,60 @@ Result<void> HipBackend::Bind(uint8_t* arena, uint64_t arena_bytes, const uint8_
   if (auto r = Check(seeai_bind(ctx_, arena_bytes, rodata, rodata_bytes)); !r) return r;
   host_ = arena;
   host_bytes_ = arena_bytes;
-  // The engine's arena holds the persistent image (and zeros elsewhere):
-  // the device arena starts as its copy.
-  return Check(seeai_upload(ctx_, 0, arena, arena_bytes));
+  // The device arena starts as the caller's copy.  seeai_bind hands it over
+  // zeroed, so only the blocks of the caller's arena that hold a nonzero
+  // byte are uploaded (a plan's arena is its persistent image followed by
+  // zeros: C5's 23.6 GB arena uploads its few hundred MB of image).
+  return UploadNonZero(arena, arena_bytes);
+}
+
+namespace {
+bool AllZero(const uint8_t* p, uint64_t n) {
+  uint64_t i = 0;
+  for (; i < n && (reinterpret_cast<uintptr_t>(p + i) & 7) != 0; ++i)
+    if (p[i]) return false;
+  for (; i + 64 <= n; i += 64) {  // eight words per test
+    uint64_t w[8];
+    std::memcpy(w, p + i, sizeof w);
+    if ((w[0] | w[1] | w[2] | w[3] | w[4] | w[5] | w[6] | w[7]) != 0) return false;
+  }
+  for (; i < n; ++i)
+    if (p[i]) return false;
+  return true;
+}
+}  // namespace
+
+Result<void> HipBackend::UploadNonZero(const uint8_t* arena, uint64_t bytes) {
+  constexpr uint64_t kBlock = uint64_t{4} << 20;
+  const uint64_t nblocks = (bytes + kBlock - 1) / kBlock;
+  if (nblocks == 0) return {};
+  // The scan: blocks dealt round-robin to at most 16 host threads.
+  std::vector<uint8_t> nonzero(nblocks, 0);
+  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  const unsigned nt = static_cast<unsigned>(std::min<uint64_t>({hw, 16, nblocks}));
+  auto scan = [&](unsigned t) {
+    for (uint64_t b = t; b < nblocks; b += nt) {
+      const uint64_t off = b * kBlock;
+      nonzero[b] = !AllZero(arena + off, std::min(kBlock, bytes - off));
+    }
+  };
+  std::vector<std::thread> pool;
+  for (unsigned t = 1; t < nt; ++t) pool.emplace_back(scan, t);
+  scan(0);
+  for (auto& th : pool) th.join();
+  // Each run of nonzero blocks goes up as one copy.
+  for (uint64_t b = 0; b < nblocks;) {
+    if (!nonzero[b]) {
+      ++b;
+      continue;
+    }
+    uint64_t e = b;
+    while (e < nblocks && nonzero[e]) ++e;
+    const uint64_t off = b * kBlock, n = std::min(e * kBlock, bytes) - off;
+    if (auto r = Check(seeai_upload(ctx_, off, arena + off, n)); !r) return r;
+    b = e;
+  }
+  return {};
 }
 
 Result<void> HipBackend::BindSource(const uint8_t* data, uint64_t bytes) {

@@ -84,6 +84,9 @@ class HipBackend {
   seeai_ctx* context() const { return ctx_; }
 
  private:
+  // Uploads the blocks of `arena` holding a nonzero byte into the device
+  // arena seeai_bind zeroed.
+  Result<void> UploadNonZero(const uint8_t* arena, uint64_t bytes);
   explicit HipBackend(seeai_ctx* ctx) : ctx_(ctx) {}
   Result<void> Check(int status) const;
 
